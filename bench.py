@@ -1,0 +1,154 @@
+"""Benchmark of the HBF access-timing engine on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c0]
+
+A step is one pass of the timing engine over one batch of access records
+resident in HBM (one decode step of the workload); engine state carries from
+step to step and each step's issue times start at the previous step's
+makespan.  Prints one JSON line with the modeled accesses/s, the roofline of
+the dominant kernel (HIP-event timed on the engine's stream) and the CPU
+oracle's rate on a bounded sample of the same stream, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBPS = 8000.0
+ALGO_BYTES_PER_ACCESS = 40  # 32-B record in + 8-B completion out
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="c0")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="budget for the CPU-oracle baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def build_workload(name: str, steps: int):
+    """Returns (profile, ranges, list of per-step record arrays on the GPU,
+    description).  Batches are distinct where the workload defines distinct
+    steps; config 0 is a single stream replayed step after step."""
+    import torch
+    from hbfsim_amd import workloads
+
+    if name == "c0":
+        s = workloads.config0()
+        rec = torch.from_numpy(s.records.view(np.int64)).cuda()
+        desc = {"workload": "config0: 2^20 uniform 128-B reads, 1 GiB range, Poisson 2 ns",
+                "records_per_step": int(len(s.records)), "profile": s.profile.name}
+        return s.profile, s.ranges, [rec], desc, s.records
+    raise SystemExit(f"unknown config {name}")
+
+
+def cpu_baseline(profile, ranges, host_records: np.ndarray, budget_s: float) -> dict:
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_py
+
+    prof = oracle_py.load_profile(profile)
+    params = oracle_py.engine_params(prof)
+    orng, count = oracle_py.range_table(ranges, prof["page_bytes"], prof["capacity_bytes"])
+    state = oracle_py.OracleState(params)
+    done = 0
+    base = 0
+    t0 = time.perf_counter()
+    while True:
+        _, _, rep, _ = oracle_py.run(params, orng, count, host_records, base, state)
+        base = rep["makespan_ps"]
+        done += len(host_records)
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": done / dt, "unit": "accesses/s", "cores": 1, "kind": "port",
+            "sample": f"{done} records: the step-0 batch replayed {done // len(host_records)}x "
+                      f"with carried state, single-threaded oracle ({dt:.1f} s)"}
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this engine runs on one GPU; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    from hbfsim_amd import engine
+
+    profile, ranges, batches, desc, host_records = build_workload(args.config, args.steps)
+    e = engine.Engine(str(profile))
+    for base, length, perms in ranges:
+        e.register(base, length, perms)
+    n = max(int(b.shape[0]) for b in batches)
+    comp = torch.empty(n, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream()
+    base_ps = 0
+    log(f"warmup {args.warmup} steps of {n} records")
+    for k in range(args.warmup):
+        b = batches[k % len(batches)]
+        rep = e.run(b, comp, None, base_ps, stream)
+        base_ps = rep["makespan_ps"]
+    torch.cuda.synchronize()
+    kernel_ms = np.zeros(3)
+    accesses = 0
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        b = batches[k % len(batches)]
+        rep = e.run(b, comp, None, base_ps, stream)
+        base_ps = rep["makespan_ps"]
+        accesses += rep["records"]
+        kernel_ms += np.array(e.kernel_ms()[:3])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    dt = t1 - t0
+    value = accesses / dt
+    avg_ms = kernel_ms / args.steps
+    dominant = int(np.argmax(avg_ms))
+    names = ["k_summary", "k_carry", "k_apply"]
+    achieved = ALGO_BYTES_PER_ACCESS * n / (avg_ms[dominant] / 1e3) / 1e9
+    out = {
+        "metric": "modeled HBF accesses/sec on 1 MI355X",
+        "value": value,
+        "unit": "accesses/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic",
+        "config": desc,
+        "roofline": {"bound": "hbm", "kernel": names[dominant],
+                     "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBPS, "traffic": None,
+                     "kernel_ms": {nm: float(v) for nm, v in zip(names, avg_ms)},
+                     "pipeline_frac": value * ALGO_BYTES_PER_ACCESS / 1e9 / PEAK_HBM_GBPS},
+    }
+    if not args.no_cpu:
+        log("cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(profile, ranges, host_records, args.cpu_seconds)
+    e.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,186 @@
+"""ctypes binding of libhbfsim_amd.so (the C ABI in include/hbfsim_amd.h).
+
+The library is loaded from this package directory.  There is no fallback:
+when it is missing, loading raises, because every timing result must come
+from the HIP engine.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libhbfsim_amd.so"
+
+HBFSIM_OK = 0
+HBFSIM_INVALID_ARGUMENT = 1
+HBFSIM_IO_ERROR = 2
+HBFSIM_CUDA_ERROR = 3
+HBFSIM_TIMEOUT = 4
+HBFSIM_UNSUPPORTED = 5
+HBFSIM_DAEMON_LOST = 6
+
+HBFSIM_RANGE_MODE_TIMING = 1
+HBFSIM_RANGE_MODE_CAPACITY = 2
+HBFSIM_RANGE_READ = 1
+HBFSIM_RANGE_WRITE = 2
+HBFSIM_RANGE_READ_WRITE = 3
+HBFSIM_MODEL_REFERENCE = 0
+HBFSIM_MODEL_FAST = 1
+HBFSIM_MODEL_HYBRID = 2
+
+MODEL_HBF = 0
+MODEL_EMPIRICAL = 1
+
+STATUS_MODELED = 0
+STATUS_BYPASS = 1
+STATUS_UNSUPPORTED = 2
+STATUS_PAGE_HIT = 4
+STATUS_HYBRID = 8
+STATUS_PROGRAMMED = 16
+
+
+class Options(ctypes.Structure):
+    _fields_ = [("profile_path", ctypes.c_char_p), ("report_dir", ctypes.c_char_p),
+                ("mode", ctypes.c_uint32), ("ring_capacity", ctypes.c_uint32),
+                ("request_timeout_ns", ctypes.c_uint64)]
+
+
+class RangeOptions(ctypes.Structure):
+    _fields_ = [("mode", ctypes.c_uint32), ("permissions", ctypes.c_uint32),
+                ("cache_policy", ctypes.c_uint32), ("stream_id", ctypes.c_uint32)]
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [("requests_submitted", ctypes.c_uint64), ("requests_completed", ctypes.c_uint64),
+                ("fast_requests", ctypes.c_uint64), ("reference_requests", ctypes.c_uint64),
+                ("fast_modeled_ns", ctypes.c_uint64)]
+
+
+class CapacityStats(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("version", ctypes.c_uint32),
+                ("enabled", ctypes.c_uint32), ("reserved0", ctypes.c_uint32)] + [
+                   (name, ctypes.c_uint64) for name in (
+                       "page_bytes", "vmm_granularity", "pool_allocated_bytes",
+                       "logical_frame_count", "service_resolve_calls", "service_resident_hits",
+                       "service_reclaimed_hits", "service_misses",
+                       "successful_backing_read_pages", "successful_backing_read_bytes",
+                       "successful_h2d_fill_pages", "successful_h2d_fill_bytes",
+                       "successful_resolve_evictions", "service_ready_results",
+                       "successful_d2h_readback_pages", "successful_d2h_readback_bytes",
+                       "successful_backing_write_pages", "successful_backing_write_bytes")]
+
+
+class VllmOptions(ctypes.Structure):
+    _fields_ = [("profile_path", ctypes.c_char_p), ("report_dir", ctypes.c_char_p),
+                ("ring_capacity", ctypes.c_uint32), ("timing_model", ctypes.c_uint32),
+                ("request_timeout_ns", ctypes.c_uint64)]
+
+
+class EngineOptions(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("model", ctypes.c_uint32),
+                ("page_buffers", ctypes.c_uint32), ("plane_contention", ctypes.c_uint32),
+                ("transfer_page", ctypes.c_uint32), ("program_every_write", ctypes.c_uint32),
+                ("flat_geometry", ctypes.c_uint32), ("ways", ctypes.c_uint32),
+                ("xfer_quantum_ps", ctypes.c_uint64),
+                ("channel_bandwidth_bytes_per_s", ctypes.c_uint64),
+                ("tile_records", ctypes.c_uint32), ("reserved0", ctypes.c_uint32)]
+
+
+REPORT_FIELDS = ("records", "modeled", "bypass", "unsupported", "reads", "writes", "page_hits",
+                 "programs", "hybrid_sampled", "makespan_ps", "latency_sum_lo",
+                 "latency_sum_hi", "latency_max_ps", "service_sum_ps")
+
+
+class Report(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_uint64) for name in REPORT_FIELDS]
+
+    def as_dict(self) -> dict:
+        d = {name: int(getattr(self, name)) for name in REPORT_FIELDS}
+        d["latency_sum_ps"] = d["latency_sum_lo"] | (d["latency_sum_hi"] << 64)
+        return d
+
+
+_P = ctypes.c_void_p
+_U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
+_SZ = ctypes.c_size_t
+_INT = ctypes.c_int
+
+# name -> (restype, argtypes); one entry per function in include/hbfsim_amd.h
+SIGNATURES = {
+    "hbfsim_abi_version": (_U32, []),
+    "hbfsim_context_create": (_INT, [ctypes.POINTER(Options), ctypes.POINTER(_P)]),
+    "hbfsim_register_device": (_INT, [_P, _P, _SZ, ctypes.POINTER(RangeOptions)]),
+    "hbfsim_map_file": (_INT, [_P, ctypes.c_char_p, _U64, _SZ, ctypes.POINTER(RangeOptions),
+                               ctypes.POINTER(_P)]),
+    "hbfsim_flush": (_INT, [_P]),
+    "hbfsim_get_stats": (_INT, [_P, ctypes.POINTER(Stats)]),
+    "hbfsim_get_capacity_stats_v1": (_INT, [_P, ctypes.POINTER(CapacityStats)]),
+    "hbfsim_unregister": (_INT, [_P, _P]),
+    "hbfsim_context_destroy": (None, [_P]),
+    "hbfsim_vllm_abi_version": (_U32, []),
+    "hbfsim_vllm_session_create": (_INT, [ctypes.POINTER(VllmOptions), ctypes.POINTER(_P)]),
+    "hbfsim_vllm_register_storage": (_INT, [_P, _SZ, _SZ]),
+    "hbfsim_vllm_session_close": (_INT, [ctypes.POINTER(_P)]),
+    "hbfsim_vllm_status_string": (ctypes.c_char_p, [_INT]),
+    "hbfsim_vllm_session_context": (_P, [_P]),
+    "hbfsim_amd_default_engine_options": (_INT, [_P, ctypes.POINTER(EngineOptions)]),
+    "hbfsim_amd_set_engine_options": (_INT, [_P, ctypes.POINTER(EngineOptions)]),
+    "hbfsim_amd_get_engine_options": (_INT, [_P, ctypes.POINTER(EngineOptions)]),
+    "hbfsim_amd_run_device": (_INT, [_P, _P, _SZ, _P, _P, _U64, _P, ctypes.POINTER(Report)]),
+    "hbfsim_amd_run": (_INT, [_P, _P, _SZ, _P, _P, _U64, ctypes.POINTER(Report)]),
+    "hbfsim_amd_get_report": (_INT, [_P, ctypes.POINTER(Report)]),
+    "hbfsim_amd_get_geometry": (_INT, [_P, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
+    "hbfsim_amd_get_busy_totals": (_INT, [_P, _P, _SZ, _P, _SZ]),
+    "hbfsim_amd_get_state": (_INT, [_P, _P, _P, _P, _P, _P]),
+    "hbfsim_amd_set_state": (_INT, [_P, _P, _P, _P, _U64, _U64]),
+    "hbfsim_amd_reset": (_INT, [_P]),
+    "hbfsim_amd_last_kernel_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float), _INT]),
+    "hbfsim_amd_validate_profile": (_INT, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
+}
+
+_lib = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    """The HIP engine library is not built; there is no other implementation."""
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise NativeLibraryMissing(
+            f"{LIB_PATH} is missing: build it with `python -m hbfsim_amd.build` "
+            "(or __graft_entry__.build()); the timing engine has no fallback")
+    try:
+        # PyTorch bundles a HIP runtime with the same soname; loading it first
+        # keeps one runtime in the process, so tensor memory and engine
+        # kernels share a device context.
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+def status_name(code: int) -> str:
+    value = load().hbfsim_vllm_status_string(code)
+    return value.decode() if value else "unknown"
+
+
+class HbfSimError(RuntimeError):
+    def __init__(self, what: str, code: int):
+        super().__init__(f"{what}: {status_name(code)} ({code})")
+        self.code = code
+
+
+def check(code: int, what: str) -> None:
+    if code != HBFSIM_OK:
+        raise HbfSimError(what, code)

@@ -1,0 +1,58 @@
+"""Builds hbfsim_amd/libhbfsim_amd.so for gfx950 with hipcc.
+
+The library is built in-tree so it travels with the repository to the GPU
+host.  Device code is compiled without packed-FP32 instruction selection.
+"""
+from __future__ import annotations
+
+import os
+import pathlib
+import shutil
+import subprocess
+import sys
+
+HERE = pathlib.Path(__file__).resolve().parent
+ROOT = HERE.parent
+CSRC = HERE / "csrc"
+LIB = HERE / "libhbfsim_amd.so"
+
+SOURCES = [CSRC / "engine.hip", CSRC / "api.cpp", CSRC / "profile.cpp"]
+HEADERS = [CSRC / "engine.hpp", CSRC / "profile.hpp", CSRC / "json_min.hpp",
+           ROOT / "include" / "hbfsim_amd.h"]
+
+
+def hipcc() -> str:
+    for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if candidate and pathlib.Path(candidate).exists():
+            return candidate
+    raise RuntimeError("hipcc not found: the HIP engine cannot be built")
+
+
+def command(output: pathlib.Path = LIB) -> list[str]:
+    return [
+        hipcc(), "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-shared",
+        "-fvisibility=hidden", "-Wall",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", str(ROOT / "include"),
+        "-o", str(output), *[str(s) for s in SOURCES],
+    ]
+
+
+def build(verbose: bool = False) -> pathlib.Path:
+    """Compiles every source every time it is called."""
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"hipcc failed with status {proc.returncode}")
+    if verbose and proc.stderr.strip():
+        sys.stderr.write(proc.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,1274 @@
+// engine.hip -- HBF per-access timing engine for gfx950 (MI355X).
+//
+// Replaces the reference's per-access device resolver and its single global
+// busy-until tail (src/cuda_runtime/device/hbf_device.cu:765-959, 963-1344)
+// with a batch pipeline over access records resident in HBM:
+//
+//   k_summary  one wave per tile of records: classify against the range
+//              table (binary search, fences staged in LDS), stripe the media
+//              page onto channel/way/die/plane, and fold every record into a
+//              per-resource (max,+) summary of the tile.  Planes also carry
+//              their page-register tag; a tile's first record on a plane has
+//              its page-buffer hit resolved later, from the carry.
+//   k_carry    one thread per resource walks the tiles in order and turns
+//              summaries into the exact busy-until / tag state at the start
+//              of every tile (and the final state, kept for the next run).
+//   k_apply    re-reads each tile, replays it from its carry-in state and
+//              writes completion times, status bytes and accounting.
+//
+// Per resource, busy' = max(busy, issue) + service.  The map
+// b -> max(b + A, B) composes associatively,
+//   (A1, B1) then (A2, B2) = (A1 + A2, max(B1 + A2, B2)),
+// which is what lets a wave fold a group of same-resource records in
+// log2(64) shuffle rounds and lets tiles be summarised independently.
+//
+// Within a step of 64 records the wave groups lanes by resource with 64-bit
+// ballots (one per key bit), orders each group by lane, and scans it by
+// pointer jumping.  No atomics touch timing state, so results are
+// deterministic and bit-identical to the sequential CPU model.
+#include <hip/hip_runtime.h>
+
+#include "engine.hpp"
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+namespace hbfamd {
+namespace {
+
+constexpr int kWave = 64;
+constexpr std::uint32_t kMaxFences = 512;
+constexpr std::uint32_t kMaxPlanes = 1024;
+constexpr std::uint32_t kMaxChannels = 256;
+constexpr std::uint32_t kClsModeled = 0;
+constexpr std::uint32_t kClsBypass = 1;
+constexpr std::uint32_t kClsUnsupported = 2;
+constexpr std::uint32_t kClsInvalid = 3;  // lane beyond the tile
+
+struct alignas(16) PlaneSum {
+    std::uint64_t fpage1;  // page + 1 of the tile's first record (0: none)
+    std::uint64_t fissue;  // its issue time
+    std::uint64_t rA, rB;  // (max,+) map of the records after the first
+    std::uint64_t lpage1;  // page + 1 of the tile's last record
+    std::uint32_t fcls;    // first record: bit 0 op, bit 1 programs
+    std::uint32_t pad;
+};
+struct alignas(16) ChanSum {
+    std::uint64_t A, B;
+};
+struct alignas(16) PlaneCarry {
+    std::uint64_t busy, tag1;
+};
+
+struct DevReport {
+    unsigned long long v[14];
+};
+static_assert(sizeof(DevReport) == sizeof(hbfsim_amd_report), "report layout");
+enum {
+    R_RECORDS, R_MODELED, R_BYPASS, R_UNSUPPORTED, R_READS, R_WRITES, R_HITS,
+    R_PROGRAMS, R_HYBRID, R_MAKESPAN, R_LAT_LO, R_LAT_HI, R_LAT_MAX, R_SERVICE
+};
+
+// Kernel arguments, passed by value.
+struct KArgs {
+    // ranges (structure of arrays, sorted by base)
+    const std::uint64_t* r_base;
+    const std::uint64_t* r_length;
+    const std::uint64_t* r_file_offset;
+    const std::uint32_t* r_meta;  // mode | permissions << 8
+    const std::uint32_t* r_id;
+    std::uint32_t r_count, r_stride, r_nfence;
+    // geometry
+    std::uint32_t Rp, Rc;           // planes, channels (resource counts)
+    std::uint32_t W, D, P;
+    std::uint32_t pbits, cbits;     // key widths for grouping
+    std::uint32_t pow2;             // all axis sizes powers of two
+    std::uint32_t axis_size[4];     // C W D P
+    std::uint64_t axis_div[4];      // product of faster axis sizes
+    std::uint32_t axis_shift[4];    // log2 of axis_div (pow2 only)
+    std::uint32_t flat;             // one channel, one plane
+    std::uint32_t page_shift;
+    std::uint32_t slots;
+    std::uint32_t contention;
+    std::uint32_t transfer_page;
+    std::uint32_t every_write;
+    std::uint32_t hybrid;
+    std::uint32_t hybrid_warmup;
+    std::uint64_t hybrid_threshold;
+    std::uint64_t read_ps, program_ps;
+    std::uint64_t xfer_num, xfer_den, xfer_q;
+    std::uint64_t xfer_pow2[33];    // transfer ps for 2^k bytes
+    std::uint32_t tile;
+};
+
+struct Dec {
+    std::uint32_t cls;
+    std::uint32_t bits;    // bit 0 op, bit 1 programs the page
+    std::uint32_t plane, chan;
+    std::uint32_t range_id;
+    std::uint64_t page1;   // media page + 1
+    std::uint64_t issue;
+    std::uint64_t xfer;
+};
+
+__device__ __forceinline__ std::uint64_t shfl64(std::uint64_t v, int src)
+{
+    const int lo = __shfl(static_cast<int>(static_cast<std::uint32_t>(v)), src);
+    const int hi = __shfl(static_cast<int>(static_cast<std::uint32_t>(v >> 32)), src);
+    return (static_cast<std::uint64_t>(static_cast<std::uint32_t>(hi)) << 32) |
+           static_cast<std::uint32_t>(lo);
+}
+
+__device__ __forceinline__ std::uint64_t umax64(std::uint64_t a, std::uint64_t b)
+{
+    return a > b ? a : b;
+}
+
+__device__ __forceinline__ std::uint64_t lanemask_lt(int lane)
+{
+    return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// SplitMix64 finaliser, the reference's fast_hash (hbf_device.cuh:729-736).
+__device__ __forceinline__ std::uint64_t mix64(std::uint64_t v)
+{
+    v += 0x9e3779b97f4a7c15ull;
+    v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ull;
+    v = (v ^ (v >> 27)) * 0x94d049bb133111ebull;
+    return v ^ (v >> 31);
+}
+
+// Lanes whose key equals this lane's key, among `active`: one ballot per key
+// bit.  Every lane of the wave must call it (uniform control flow).
+__device__ __forceinline__ std::uint64_t match_key(std::uint32_t key, std::uint32_t bits,
+                                                   std::uint64_t active)
+{
+    std::uint64_t m = active;
+    for (std::uint32_t b = 0; b < bits; ++b) {
+        const bool bit = (key >> b) & 1u;
+        const std::uint64_t ones = __ballot(bit);
+        m &= bit ? ones : ~ones;
+    }
+    return m;
+}
+
+// Inclusive scan of (A, B) maps over each lane group, in lane order, by
+// pointer jumping along `pred` (the previous lane of the same group, or -1).
+__device__ __forceinline__ void group_scan(std::uint64_t& A, std::uint64_t& B, int pred,
+                                           int lane)
+{
+    int ptr = pred;
+    for (int s = 0; s < 6; ++s) {
+        if (__ballot(ptr >= 0) == 0) {
+            break;
+        }
+        const int src = ptr < 0 ? lane : ptr;
+        const std::uint64_t pA = shfl64(A, src);
+        const std::uint64_t pB = shfl64(B, src);
+        const int pp = __shfl(ptr, src);
+        if (ptr >= 0) {
+            B = umax64(pB + A, B);
+            A = pA + A;
+            ptr = pp;
+        }
+    }
+}
+
+// find_range_index (hbf_device.cuh:826-841): upper_bound(base) - 1 over the
+// sorted range table.  The top level runs over every `stride`-th base,
+// staged in LDS; the bottom level over at most `stride` bases in memory.
+__device__ __forceinline__ std::uint32_t find_range(const KArgs& a, const std::uint64_t* fence,
+                                                    std::uint64_t addr)
+{
+    std::uint32_t lo = 0, hi = a.r_nfence;
+    while (lo < hi) {
+        const std::uint32_t mid = (lo + hi) >> 1;
+        if (fence[mid] <= addr) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    if (lo == 0) {
+        return a.r_count;
+    }
+    const std::uint32_t start = (lo - 1) * a.r_stride;
+    std::uint32_t end = start + a.r_stride;
+    end = end < a.r_count ? end : a.r_count;
+    std::uint32_t l2 = start + 1, h2 = end;
+    while (l2 < h2) {
+        const std::uint32_t mid = (l2 + h2) >> 1;
+        if (a.r_base[mid] <= addr) {
+            l2 = mid + 1;
+        } else {
+            h2 = mid;
+        }
+    }
+    return l2 - 1;
+}
+
+// range_overlaps (hbf_device.cuh:873-884)
+__device__ __forceinline__ bool overlaps(std::uint64_t base, std::uint64_t length,
+                                         std::uint64_t addr, std::uint64_t bytes)
+{
+    if (bytes == 0 || length == 0 || base > ~0ull - length || addr > ~0ull - bytes) {
+        return false;
+    }
+    return addr < base + length && base < addr + bytes;
+}
+
+__device__ __forceinline__ std::uint64_t xfer_ps(const KArgs& a, std::uint64_t bytes)
+{
+    if ((bytes & (bytes - 1)) == 0 && bytes != 0 && bytes <= (1ull << 32)) {
+        return a.xfer_pow2[63 - __clzll(bytes)];
+    }
+    return a.xfer_q * ((bytes * a.xfer_num + a.xfer_den - 1) / a.xfer_den);
+}
+
+// Classification in the resolver's order (hbf_device.cu:1081-1165) followed
+// by striping of the media page.
+__device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence,
+                                      const hbf_record32* rec, std::size_t i,
+                                      std::uint64_t base_ps)
+{
+    const uint4* p = reinterpret_cast<const uint4*>(rec + i);
+    const uint4 x = p[0];
+    const uint4 y = p[1];
+    const std::uint64_t addr = x.x | (static_cast<std::uint64_t>(x.y) << 32);
+    const std::uint64_t bytes = x.z | (static_cast<std::uint64_t>(x.w) << 32);
+    const std::uint64_t issue_rel = y.x | (static_cast<std::uint64_t>(y.y) << 32);
+    const std::uint32_t op = y.z & 0xffu;
+    Dec d;
+    d.issue = base_ps + issue_rel;
+    d.bits = op & 1u;
+    d.plane = 0;
+    d.chan = 0;
+    d.range_id = 0;
+    d.page1 = 0;
+    d.xfer = 0;
+    const std::uint32_t idx = find_range(a, fence, addr);
+    if (idx == a.r_count || addr < a.r_base[idx] || addr - a.r_base[idx] >= a.r_length[idx]) {
+        const std::uint32_t succ = idx == a.r_count ? 0u : idx + 1u;
+        if (bytes > 0xffffffffull ||
+            (succ < a.r_count && overlaps(a.r_base[succ], a.r_length[succ], addr, bytes))) {
+            d.cls = kClsUnsupported;
+        } else {
+            d.cls = kClsBypass;
+        }
+        return d;
+    }
+    const std::uint64_t base = a.r_base[idx];
+    const std::uint64_t length = a.r_length[idx];
+    const std::uint32_t meta = a.r_meta[idx];
+    const std::uint32_t mode = meta & 0xffu;
+    const std::uint32_t perms = meta >> 8;
+    const std::uint64_t page_mask = (1ull << a.page_shift) - 1;
+    // access_supported (hbf_device.cuh:843-860); the range's own bounds and
+    // page size are validated at registration.
+    if (bytes == 0 || bytes > 0xffffffffull || op > 1 || (mode != 1 && mode != 2) ||
+        bytes > ~0ull - addr || addr + bytes > base + length || (perms & (1u << op)) == 0) {
+        d.cls = kClsUnsupported;
+        return d;
+    }
+    const std::uint64_t off = addr - base;
+    if ((off >> a.page_shift) != ((off + bytes - 1) >> a.page_shift)) {
+        d.cls = kClsUnsupported;
+        return d;
+    }
+    const std::uint64_t file_offset = a.r_file_offset[idx];
+    if ((off & ~page_mask) > ~0ull - file_offset) {
+        d.cls = kClsUnsupported;
+        return d;
+    }
+    d.cls = kClsModeled;
+    d.range_id = a.r_id[idx];
+    const std::uint64_t media = file_offset + off;
+    const std::uint64_t page = media >> a.page_shift;
+    d.page1 = page + 1;
+    const std::uint64_t page_bytes = 1ull << a.page_shift;
+    if (op == 1 && (a.every_write || (media & page_mask) + bytes == page_bytes)) {
+        d.bits |= 2u;
+    }
+    d.xfer = xfer_ps(a, a.transfer_page ? page_bytes : bytes);
+    if (!a.flat) {
+        std::uint32_t c[4];
+        if (a.pow2) {
+#pragma unroll
+            for (int ax = 0; ax < 4; ++ax) {
+                c[ax] = static_cast<std::uint32_t>((page >> a.axis_shift[ax]) &
+                                                   (a.axis_size[ax] - 1));
+            }
+        } else {
+#pragma unroll
+            for (int ax = 0; ax < 4; ++ax) {
+                c[ax] = static_cast<std::uint32_t>((page / a.axis_div[ax]) % a.axis_size[ax]);
+            }
+        }
+        d.chan = c[0];
+        d.plane = ((c[0] * a.W + c[1]) * a.D + c[2]) * a.P + c[3];
+    }
+    return d;
+}
+
+__device__ __forceinline__ std::uint64_t plane_service(const KArgs& a, std::uint32_t bits,
+                                                       bool hit)
+{
+    if ((bits & 1u) == 0) {
+        return hit ? 0ull : a.read_ps;
+    }
+    return (bits & 2u) ? a.program_ps : 0ull;
+}
+
+__device__ __forceinline__ void load_fences(const KArgs& a, std::uint64_t* fence, int lane)
+{
+    for (std::uint32_t j = lane; j < a.r_nfence; j += kWave) {
+        fence[j] = a.r_base[static_cast<std::size_t>(j) * a.r_stride];
+    }
+}
+
+__global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec, std::size_t n,
+                                                std::uint64_t base_ps, PlaneSum* psum,
+                                                ChanSum* csum, std::uint64_t* tile_count)
+{
+    extern __shared__ std::uint64_t sm[];
+    std::uint64_t* fence = sm;
+    std::uint64_t* p_f1 = fence + a.r_nfence;
+    std::uint64_t* p_fi = p_f1 + a.Rp;
+    std::uint64_t* p_rA = p_fi + a.Rp;
+    std::uint64_t* p_rB = p_rA + a.Rp;
+    std::uint64_t* p_l1 = p_rB + a.Rp;
+    std::uint64_t* c_A = p_l1 + a.Rp;
+    std::uint64_t* c_B = c_A + a.Rc;
+    std::uint32_t* p_fc = reinterpret_cast<std::uint32_t*>(c_B + a.Rc);
+    const int lane = threadIdx.x;
+    load_fences(a, fence, lane);
+    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
+        p_f1[r] = 0;
+        p_fi[r] = 0;
+        p_rA[r] = 0;
+        p_rB[r] = 0;
+        p_l1[r] = 0;
+        p_fc[r] = 0;
+    }
+    for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
+        c_A[r] = 0;
+        c_B[r] = 0;
+    }
+    __syncthreads();
+    const std::size_t tile = blockIdx.x;
+    const std::size_t begin = tile * a.tile;
+    const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
+    std::uint64_t modeled = 0;
+    for (std::size_t s = begin; s < end; s += kWave) {
+        const std::size_t i = s + lane;
+        const bool valid = i < end;
+        Dec d;
+        if (valid) {
+            d = decode(a, fence, rec, i, base_ps);
+        } else {
+            d.cls = kClsInvalid;
+            d.bits = 0;
+            d.plane = d.chan = d.range_id = 0;
+            d.page1 = d.issue = d.xfer = 0;
+        }
+        const bool m = valid && d.cls == kClsModeled;
+        const std::uint64_t active = __ballot(m);
+        modeled += __popcll(active);
+        if (active == 0) {
+            continue;
+        }
+        {  // plane stage
+            const std::uint32_t key = m ? d.plane : 0u;
+            const std::uint64_t peers = match_key(key, a.pbits, active);
+            const std::uint64_t below = peers & lanemask_lt(lane);
+            const int pred = (m && below) ? 63 - __clzll(below) : -1;
+            const int leader = m ? __ffsll(static_cast<long long>(peers)) - 1 : lane;
+            const int last = m ? 63 - __clzll(peers) : lane;
+            const std::uint64_t f1 = m ? p_f1[key] : 0ull;
+            const bool has = f1 != 0;
+            const bool tfirst = m && pred < 0 && !has;
+            std::uint64_t prev1 = shfl64(d.page1, pred < 0 ? lane : pred);
+            if (pred < 0) {
+                prev1 = m ? p_l1[key] : 0ull;
+            }
+            const bool hit = a.slots != 0 && m && prev1 == d.page1;
+            const std::uint64_t svc = plane_service(a, d.bits, hit);
+            std::uint64_t A = 0, B = 0;
+            if (m && !tfirst) {
+                A = svc;
+                B = d.issue + svc;
+            }
+            if (a.contention) {
+                group_scan(A, B, pred, lane);
+            }
+            const std::uint64_t l1 = shfl64(d.page1, leader);
+            const std::uint64_t li = shfl64(d.issue, leader);
+            const std::uint32_t lc = static_cast<std::uint32_t>(
+                __shfl(static_cast<int>(d.bits), leader));
+            if (m && lane == last) {
+                if (!has) {
+                    p_f1[key] = l1;
+                    p_fi[key] = li;
+                    p_fc[key] = lc;
+                }
+                if (a.contention) {
+                    const std::uint64_t sA = p_rA[key];
+                    const std::uint64_t sB = p_rB[key];
+                    p_rB[key] = umax64(sB + A, B);
+                    p_rA[key] = sA + A;
+                }
+                p_l1[key] = d.page1;
+            }
+        }
+        __syncthreads();
+        {  // channel stage
+            const std::uint32_t key = m ? d.chan : 0u;
+            const std::uint64_t peers = match_key(key, a.cbits, active);
+            const std::uint64_t below = peers & lanemask_lt(lane);
+            const int pred = (m && below) ? 63 - __clzll(below) : -1;
+            const int last = m ? 63 - __clzll(peers) : lane;
+            std::uint64_t A = m ? d.xfer : 0ull;
+            std::uint64_t B = m ? d.issue + d.xfer : 0ull;
+            group_scan(A, B, pred, lane);
+            if (m && lane == last) {
+                const std::uint64_t sA = c_A[key];
+                const std::uint64_t sB = c_B[key];
+                c_B[key] = umax64(sB + A, B);
+                c_A[key] = sA + A;
+            }
+        }
+        __syncthreads();
+    }
+    PlaneSum* ps = psum + tile * a.Rp;
+    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
+        PlaneSum v;
+        v.fpage1 = p_f1[r];
+        v.fissue = p_fi[r];
+        v.rA = p_rA[r];
+        v.rB = p_rB[r];
+        v.lpage1 = p_l1[r];
+        v.fcls = p_fc[r];
+        v.pad = 0;
+        ps[r] = v;
+    }
+    ChanSum* cs = csum + tile * a.Rc;
+    for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
+        ChanSum v;
+        v.A = c_A[r];
+        v.B = c_B[r];
+        cs[r] = v;
+    }
+    if (lane == 0) {
+        tile_count[tile] = modeled;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_carry(KArgs a, std::size_t ntiles, const PlaneSum* psum,
+                                              const ChanSum* csum, const std::uint64_t* tile_count,
+                                              PlaneCarry* pcarry, std::uint64_t* ccarry,
+                                              std::uint64_t* tile_seq, std::uint64_t* st_pbusy,
+                                              std::uint64_t* st_ptag, std::uint64_t* st_cbusy,
+                                              std::uint64_t* st_seq)
+{
+    const std::uint32_t t = blockIdx.x * kWave + threadIdx.x;
+    if (t < a.Rp) {
+        std::uint64_t busy = st_pbusy[t];
+        std::uint64_t tag1 = st_ptag[static_cast<std::size_t>(t) * 2];
+        for (std::size_t k = 0; k < ntiles; ++k) {
+            PlaneCarry c;
+            c.busy = busy;
+            c.tag1 = tag1;
+            pcarry[k * a.Rp + t] = c;
+            const PlaneSum S = psum[k * a.Rp + t];
+            if (S.fpage1 != 0) {
+                const bool hit = a.slots != 0 && tag1 == S.fpage1;
+                const std::uint64_t svc = plane_service(a, S.fcls, hit);
+                if (a.contention) {
+                    const std::uint64_t b = umax64(busy, S.fissue) + svc;
+                    busy = umax64(b + S.rA, S.rB);
+                }
+                tag1 = S.lpage1;
+            }
+        }
+        st_pbusy[t] = busy;
+        st_ptag[static_cast<std::size_t>(t) * 2] = tag1;
+    } else if (t < a.Rp + a.Rc) {
+        const std::uint32_t c = t - a.Rp;
+        std::uint64_t busy = st_cbusy[c];
+        for (std::size_t k = 0; k < ntiles; ++k) {
+            ccarry[k * a.Rc + c] = busy;
+            const ChanSum S = csum[k * a.Rc + c];
+            busy = umax64(busy + S.A, S.B);
+        }
+        st_cbusy[c] = busy;
+    } else if (t == a.Rp + a.Rc) {
+        std::uint64_t s = *st_seq;
+        for (std::size_t k = 0; k < ntiles; ++k) {
+            tile_seq[k] = s;
+            s += tile_count[k];
+        }
+        *st_seq = s;
+    }
+}
+
+__device__ __forceinline__ void add128(std::uint64_t& lo, std::uint64_t& hi, std::uint64_t v)
+{
+    const std::uint64_t n = lo + v;
+    hi += n < lo ? 1u : 0u;
+    lo = n;
+}
+
+__device__ __forceinline__ std::uint64_t wave_sum(std::uint64_t v)
+{
+    for (int o = 32; o > 0; o >>= 1) {
+        v += shfl64(v, threadIdx.x ^ o);
+    }
+    return v;
+}
+
+__device__ __forceinline__ std::uint64_t wave_max(std::uint64_t v)
+{
+    for (int o = 32; o > 0; o >>= 1) {
+        v = umax64(v, shfl64(v, threadIdx.x ^ o));
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, std::size_t n,
+                                              std::uint64_t base_ps, const PlaneCarry* pcarry,
+                                              const std::uint64_t* ccarry,
+                                              const std::uint64_t* tile_seq,
+                                              std::uint64_t* completion, std::uint8_t* status,
+                                              std::uint64_t* g_ptotal, std::uint64_t* g_ctotal,
+                                              DevReport* rep)
+{
+    extern __shared__ std::uint64_t sm[];
+    std::uint64_t* fence = sm;
+    std::uint64_t* p_busy = fence + a.r_nfence;
+    std::uint64_t* p_tag = p_busy + a.Rp;
+    std::uint64_t* p_tot = p_tag + a.Rp;
+    std::uint64_t* c_busy = p_tot + a.Rp;
+    std::uint64_t* c_tot = c_busy + a.Rc;
+    const int lane = threadIdx.x;
+    const std::size_t tile = blockIdx.x;
+    load_fences(a, fence, lane);
+    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
+        const PlaneCarry c = pcarry[tile * a.Rp + r];
+        p_busy[r] = c.busy;
+        p_tag[r] = c.tag1;
+        p_tot[r] = 0;
+    }
+    for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
+        c_busy[r] = ccarry[tile * a.Rc + r];
+        c_tot[r] = 0;
+    }
+    __syncthreads();
+    const std::size_t begin = tile * a.tile;
+    const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
+    std::uint64_t seq = tile_seq[tile];
+    std::uint64_t n_rec = 0, n_mod = 0, n_byp = 0, n_uns = 0, n_rd = 0, n_wr = 0;
+    std::uint64_t n_hit = 0, n_prog = 0, n_hyb = 0, mk = 0, lat_lo = 0, lat_hi = 0;
+    std::uint64_t lat_max = 0, svc_sum = 0;
+    for (std::size_t s = begin; s < end; s += kWave) {
+        const std::size_t i = s + lane;
+        const bool valid = i < end;
+        Dec d;
+        if (valid) {
+            d = decode(a, fence, rec, i, base_ps);
+        } else {
+            d.cls = kClsInvalid;
+            d.bits = 0;
+            d.plane = d.chan = d.range_id = 0;
+            d.page1 = d.issue = d.xfer = 0;
+        }
+        const bool m = valid && d.cls == kClsModeled;
+        const std::uint64_t active = __ballot(m);
+        std::uint8_t st = static_cast<std::uint8_t>(d.cls);
+        std::uint64_t done = 0;
+        if (active != 0) {
+            std::uint64_t pd, cd;
+            std::uint64_t svc;
+            bool hit;
+            {  // plane stage
+                const std::uint32_t key = m ? d.plane : 0u;
+                const std::uint64_t peers = match_key(key, a.pbits, active);
+                const std::uint64_t below = peers & lanemask_lt(lane);
+                const int pred = (m && below) ? 63 - __clzll(below) : -1;
+                const int last = m ? 63 - __clzll(peers) : lane;
+                std::uint64_t prev1 = shfl64(d.page1, pred < 0 ? lane : pred);
+                if (pred < 0) {
+                    prev1 = m ? p_tag[key] : 0ull;
+                }
+                hit = a.slots != 0 && m && prev1 == d.page1;
+                svc = plane_service(a, d.bits, hit);
+                if (a.contention) {
+                    std::uint64_t A = m ? svc : 0ull;
+                    std::uint64_t B = m ? d.issue + svc : 0ull;
+                    group_scan(A, B, pred, lane);
+                    pd = m ? umax64(p_busy[key] + A, B) : 0ull;
+                } else {
+                    pd = d.issue + svc;
+                }
+                if (m && lane == last) {
+                    if (a.contention) {
+                        p_busy[key] = pd;
+                    }
+                    p_tag[key] = d.page1;
+                }
+                if (m && svc != 0) {
+                    atomicAdd(reinterpret_cast<unsigned long long*>(&p_tot[key]),
+                              static_cast<unsigned long long>(svc));
+                }
+            }
+            __syncthreads();
+            {  // channel stage
+                const std::uint32_t key = m ? d.chan : 0u;
+                const std::uint64_t peers = match_key(key, a.cbits, active);
+                const std::uint64_t below = peers & lanemask_lt(lane);
+                const int pred = (m && below) ? 63 - __clzll(below) : -1;
+                const int last = m ? 63 - __clzll(peers) : lane;
+                std::uint64_t A = m ? d.xfer : 0ull;
+                std::uint64_t B = m ? d.issue + d.xfer : 0ull;
+                group_scan(A, B, pred, lane);
+                cd = m ? umax64(c_busy[key] + A, B) : 0ull;
+                if (m && lane == last) {
+                    c_busy[key] = cd;
+                }
+                if (m && d.xfer != 0) {
+                    atomicAdd(reinterpret_cast<unsigned long long*>(&c_tot[key]),
+                              static_cast<unsigned long long>(d.xfer));
+                }
+            }
+            __syncthreads();
+            if (m) {
+                done = umax64(pd, cd);
+                const std::uint64_t rank = __popcll(active & lanemask_lt(lane));
+                const std::uint64_t q = seq + rank;
+                if (a.hybrid) {
+                    const std::uint64_t key = ((d.page1 - 1) << a.page_shift) ^
+                                              (static_cast<std::uint64_t>(d.range_id) << 32) ^
+                                              (d.bits & 1u);
+                    if (q < a.hybrid_warmup ||
+                        (a.hybrid_threshold != 0 && mix64(q ^ key) <= a.hybrid_threshold)) {
+                        st |= 8u;
+                        ++n_hyb;
+                    }
+                }
+                ++n_mod;
+                if ((d.bits & 1u) == 0) {
+                    ++n_rd;
+                    if (hit) {
+                        st |= 4u;
+                        ++n_hit;
+                    }
+                } else {
+                    ++n_wr;
+                    if (svc != 0) {
+                        st |= 16u;
+                        ++n_prog;
+                    }
+                }
+                mk = umax64(mk, done);
+                const std::uint64_t lat = done - d.issue;
+                add128(lat_lo, lat_hi, lat);
+                lat_max = umax64(lat_max, lat);
+                svc_sum += umax64(svc, d.xfer);
+            }
+            seq += __popcll(active);
+        }
+        if (valid) {
+            ++n_rec;
+            if (d.cls == kClsBypass) {
+                done = d.issue;
+                ++n_byp;
+            } else if (d.cls == kClsUnsupported) {
+                done = ~0ull;
+                ++n_uns;
+            }
+            completion[i] = done;
+            if (status != nullptr) {
+                status[i] = st;
+            }
+        }
+    }
+    __syncthreads();
+    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
+        if (p_tot[r] != 0) {
+            atomicAdd(reinterpret_cast<unsigned long long*>(&g_ptotal[r]),
+                      static_cast<unsigned long long>(p_tot[r]));
+        }
+    }
+    for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
+        if (c_tot[r] != 0) {
+            atomicAdd(reinterpret_cast<unsigned long long*>(&g_ctotal[r]),
+                      static_cast<unsigned long long>(c_tot[r]));
+        }
+    }
+    // 128-bit latency sum: reduce the high words, then the low words with
+    // their carries.
+    std::uint64_t hi = wave_sum(lat_hi);
+    std::uint64_t lo_acc = 0, carry = 0;
+    {
+        std::uint64_t v = lat_lo;
+        for (int o = 32; o > 0; o >>= 1) {
+            const std::uint64_t other = shfl64(v, threadIdx.x ^ o);
+            const std::uint64_t oc = shfl64(carry, threadIdx.x ^ o);
+            const std::uint64_t sum = v + other;
+            carry = carry + oc + (sum < v ? 1u : 0u);
+            v = sum;
+        }
+        lo_acc = v;
+    }
+    hi += carry;
+    const std::uint64_t t_rec = wave_sum(n_rec), t_mod = wave_sum(n_mod);
+    const std::uint64_t t_byp = wave_sum(n_byp), t_uns = wave_sum(n_uns);
+    const std::uint64_t t_rd = wave_sum(n_rd), t_wr = wave_sum(n_wr);
+    const std::uint64_t t_hit = wave_sum(n_hit), t_prog = wave_sum(n_prog);
+    const std::uint64_t t_hyb = wave_sum(n_hyb), t_svc = wave_sum(svc_sum);
+    const std::uint64_t t_mk = wave_max(mk), t_lmax = wave_max(lat_max);
+    if (lane == 0) {
+        unsigned long long* v = rep->v;
+        atomicAdd(&v[R_RECORDS], t_rec);
+        atomicAdd(&v[R_MODELED], t_mod);
+        atomicAdd(&v[R_BYPASS], t_byp);
+        atomicAdd(&v[R_UNSUPPORTED], t_uns);
+        atomicAdd(&v[R_READS], t_rd);
+        atomicAdd(&v[R_WRITES], t_wr);
+        atomicAdd(&v[R_HITS], t_hit);
+        atomicAdd(&v[R_PROGRAMS], t_prog);
+        atomicAdd(&v[R_HYBRID], t_hyb);
+        atomicMax(&v[R_MAKESPAN], t_mk);
+        const unsigned long long old = atomicAdd(&v[R_LAT_LO], lo_acc);
+        const unsigned long long c = (old + lo_acc < old) ? 1ull : 0ull;
+        if (hi + c != 0) {
+            atomicAdd(&v[R_LAT_HI], hi + c);
+        }
+        atomicMax(&v[R_LAT_MAX], t_lmax);
+        atomicAdd(&v[R_SERVICE], t_svc);
+    }
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------
+// host side
+
+struct engine {
+    engine_config cfg;
+    int device{0};
+    KArgs args{};
+    // ranges
+    std::vector<range_rec> ranges;
+    bool ranges_dirty{true};
+    std::uint64_t* d_r_base{nullptr};
+    std::uint64_t* d_r_length{nullptr};
+    std::uint64_t* d_r_offset{nullptr};
+    std::uint32_t* d_r_meta{nullptr};
+    std::uint32_t* d_r_id{nullptr};
+    std::size_t range_cap{0};
+    // persistent state
+    std::uint64_t* d_pbusy{nullptr};
+    std::uint64_t* d_ptag{nullptr};
+    std::uint64_t* d_cbusy{nullptr};
+    std::uint64_t* d_ptot{nullptr};
+    std::uint64_t* d_ctot{nullptr};
+    std::uint64_t* d_seq{nullptr};
+    DevReport* d_rep{nullptr};
+    DevReport* h_rep{nullptr};  // pinned
+    // scratch
+    std::size_t tile_cap{0};
+    PlaneSum* d_psum{nullptr};
+    ChanSum* d_csum{nullptr};
+    PlaneCarry* d_pcarry{nullptr};
+    std::uint64_t* d_ccarry{nullptr};
+    std::uint64_t* d_tcount{nullptr};
+    std::uint64_t* d_tseq{nullptr};
+    hipEvent_t ev[4]{};
+    float last_ms[3]{0, 0, 0};
+    std::uint64_t burst{0};
+};
+
+namespace {
+
+int hip_status(hipError_t e) { return e == hipSuccess ? HBFSIM_OK : HBFSIM_CUDA_ERROR; }
+
+template <typename T>
+void hfree(T*& p)
+{
+    if (p != nullptr) {
+        (void)hipFree(p);
+        p = nullptr;
+    }
+}
+
+template <typename T>
+hipError_t halloc(T*& p, std::size_t count)
+{
+    return hipMalloc(reinterpret_cast<void**>(&p), sizeof(T) * (count == 0 ? 1 : count));
+}
+
+std::uint32_t bits_for(std::uint32_t n)
+{
+    std::uint32_t b = 0;
+    while ((1u << b) < n) {
+        ++b;
+    }
+    return b;
+}
+
+bool is_pow2(std::uint64_t v) { return v != 0 && (v & (v - 1)) == 0; }
+
+std::uint32_t log2u(std::uint64_t v)
+{
+    std::uint32_t b = 0;
+    while ((1ull << b) < v) {
+        ++b;
+    }
+    return b;
+}
+
+void free_scratch(engine* e)
+{
+    hfree(e->d_psum);
+    hfree(e->d_csum);
+    hfree(e->d_pcarry);
+    hfree(e->d_ccarry);
+    hfree(e->d_tcount);
+    hfree(e->d_tseq);
+    e->tile_cap = 0;
+}
+
+int ensure_scratch(engine* e, std::size_t ntiles)
+{
+    if (ntiles <= e->tile_cap) {
+        return HBFSIM_OK;
+    }
+    free_scratch(e);
+    const std::size_t cap = std::max<std::size_t>(ntiles, 16);
+    const std::size_t rp = e->args.Rp, rc = e->args.Rc;
+    if (halloc(e->d_psum, cap * rp) != hipSuccess || halloc(e->d_csum, cap * rc) != hipSuccess ||
+        halloc(e->d_pcarry, cap * rp) != hipSuccess ||
+        halloc(e->d_ccarry, cap * rc) != hipSuccess || halloc(e->d_tcount, cap) != hipSuccess ||
+        halloc(e->d_tseq, cap) != hipSuccess) {
+        free_scratch(e);
+        return HBFSIM_CUDA_ERROR;
+    }
+    e->tile_cap = cap;
+    return HBFSIM_OK;
+}
+
+int upload_ranges(engine* e, hipStream_t stream)
+{
+    const std::size_t count = e->ranges.size();
+    if (count > e->range_cap || e->d_r_base == nullptr) {
+        hfree(e->d_r_base);
+        hfree(e->d_r_length);
+        hfree(e->d_r_offset);
+        hfree(e->d_r_meta);
+        hfree(e->d_r_id);
+        const std::size_t cap = std::max<std::size_t>(count, 64);
+        if (halloc(e->d_r_base, cap) != hipSuccess || halloc(e->d_r_length, cap) != hipSuccess ||
+            halloc(e->d_r_offset, cap) != hipSuccess || halloc(e->d_r_meta, cap) != hipSuccess ||
+            halloc(e->d_r_id, cap) != hipSuccess) {
+            return HBFSIM_CUDA_ERROR;
+        }
+        e->range_cap = cap;
+    }
+    std::vector<std::uint64_t> base(count), length(count), offset(count);
+    std::vector<std::uint32_t> meta(count), id(count);
+    for (std::size_t i = 0; i < count; ++i) {
+        base[i] = e->ranges[i].base;
+        length[i] = e->ranges[i].length;
+        offset[i] = e->ranges[i].file_offset;
+        meta[i] = (e->ranges[i].mode & 0xffu) | (e->ranges[i].permissions << 8);
+        id[i] = e->ranges[i].range_id;
+    }
+    if (count != 0) {
+        hipError_t err = hipMemcpyAsync(e->d_r_base, base.data(), count * 8,
+                                        hipMemcpyHostToDevice, stream);
+        if (err == hipSuccess)
+            err = hipMemcpyAsync(e->d_r_length, length.data(), count * 8, hipMemcpyHostToDevice,
+                                 stream);
+        if (err == hipSuccess)
+            err = hipMemcpyAsync(e->d_r_offset, offset.data(), count * 8, hipMemcpyHostToDevice,
+                                 stream);
+        if (err == hipSuccess)
+            err = hipMemcpyAsync(e->d_r_meta, meta.data(), count * 4, hipMemcpyHostToDevice,
+                                 stream);
+        if (err == hipSuccess)
+            err = hipMemcpyAsync(e->d_r_id, id.data(), count * 4, hipMemcpyHostToDevice, stream);
+        if (err == hipSuccess) err = hipStreamSynchronize(stream);
+        if (err != hipSuccess) {
+            return HBFSIM_CUDA_ERROR;
+        }
+    }
+    KArgs& a = e->args;
+    a.r_base = e->d_r_base;
+    a.r_length = e->d_r_length;
+    a.r_file_offset = e->d_r_offset;
+    a.r_meta = e->d_r_meta;
+    a.r_id = e->d_r_id;
+    a.r_count = static_cast<std::uint32_t>(count);
+    a.r_stride = count <= kMaxFences ? 1u
+                                     : static_cast<std::uint32_t>((count + kMaxFences - 1) /
+                                                                  kMaxFences);
+    a.r_nfence = count == 0 ? 0u
+                            : static_cast<std::uint32_t>((count + a.r_stride - 1) / a.r_stride);
+    e->ranges_dirty = false;
+    return HBFSIM_OK;
+}
+
+std::size_t lds_summary(const KArgs& a)
+{
+    return 8ull * (a.r_nfence + 5ull * a.Rp + 2ull * a.Rc) + 4ull * a.Rp;
+}
+
+std::size_t lds_apply(const KArgs& a)
+{
+    return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc);
+}
+
+}  // namespace
+
+int engine_create(const engine_config& c, engine** out)
+{
+    *out = nullptr;
+    const std::uint32_t rp = c.n_planes(), rc = c.n_channels();
+    if (c.channels == 0 || c.ways == 0 || c.dies == 0 || c.planes == 0 || c.page_shift < 9 ||
+        c.page_shift > 31 || c.slots > 2 || c.xfer_den == 0 || c.xfer_quantum == 0 ||
+        c.tile == 0 || c.tile % kWave != 0) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    if (rp > kMaxPlanes || rc > kMaxChannels) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    // bytes * num must fit 64 bits for every transfer size up to a page.
+    const unsigned __int128 worst =
+        static_cast<unsigned __int128>(1ull << c.page_shift) * c.xfer_num + c.xfer_den;
+    if (worst > ~0ull) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    auto* e = new (std::nothrow) engine;
+    if (e == nullptr) {
+        return HBFSIM_IO_ERROR;
+    }
+    e->cfg = c;
+    if (hipGetDevice(&e->device) != hipSuccess) {
+        delete e;
+        return HBFSIM_CUDA_ERROR;
+    }
+    KArgs& a = e->args;
+    std::memset(&a, 0, sizeof(a));
+    a.Rp = rp;
+    a.Rc = rc;
+    a.W = c.ways;
+    a.D = c.dies;
+    a.P = c.planes;
+    a.pbits = bits_for(rp);
+    a.cbits = bits_for(rc);
+    a.flat = (rp == 1 && rc == 1) ? 1u : 0u;
+    const std::uint32_t size[4] = {c.channels, c.ways, c.dies, c.planes};
+    std::uint64_t div = 1;
+    bool pow2 = true;
+    for (int i = 0; i < 4; ++i) {
+        const std::uint32_t ax = c.order[i];
+        a.axis_size[ax] = size[ax];
+        a.axis_div[ax] = div;
+        pow2 = pow2 && is_pow2(size[ax]);
+        div *= size[ax];
+    }
+    for (int ax = 0; ax < 4; ++ax) {
+        a.axis_shift[ax] = log2u(a.axis_div[ax]);
+    }
+    a.pow2 = pow2 ? 1u : 0u;
+    a.page_shift = c.page_shift;
+    a.slots = c.slots;
+    a.contention = c.contention;
+    a.transfer_page = c.transfer_page;
+    a.every_write = c.every_write;
+    a.hybrid = c.hybrid;
+    a.hybrid_warmup = c.hybrid_warmup;
+    a.hybrid_threshold = c.hybrid_threshold;
+    a.read_ps = c.read_ps;
+    a.program_ps = c.program_ps;
+    a.xfer_num = c.xfer_num;
+    a.xfer_den = c.xfer_den;
+    a.xfer_q = c.xfer_quantum;
+    for (int k = 0; k <= 32; ++k) {
+        const unsigned __int128 prod = static_cast<unsigned __int128>(1ull << k) * c.xfer_num;
+        a.xfer_pow2[k] = c.xfer_quantum *
+                         static_cast<std::uint64_t>((prod + c.xfer_den - 1) / c.xfer_den);
+    }
+    a.tile = c.tile;
+    hipError_t err = halloc(e->d_pbusy, rp);
+    if (err == hipSuccess) err = halloc(e->d_ptag, 2ull * rp);
+    if (err == hipSuccess) err = halloc(e->d_cbusy, rc);
+    if (err == hipSuccess) err = halloc(e->d_ptot, rp);
+    if (err == hipSuccess) err = halloc(e->d_ctot, rc);
+    if (err == hipSuccess) err = halloc(e->d_seq, 1);
+    if (err == hipSuccess) err = halloc(e->d_rep, 1);
+    if (err == hipSuccess)
+        err = hipHostMalloc(reinterpret_cast<void**>(&e->h_rep), sizeof(DevReport));
+    for (int i = 0; i < 4 && err == hipSuccess; ++i) {
+        err = hipEventCreate(&e->ev[i]);
+    }
+    if (err != hipSuccess) {
+        engine_destroy(e);
+        return HBFSIM_CUDA_ERROR;
+    }
+    const int rs = engine_reset(e);
+    if (rs != HBFSIM_OK) {
+        engine_destroy(e);
+        return rs;
+    }
+    *out = e;
+    return HBFSIM_OK;
+}
+
+void engine_destroy(engine* e)
+{
+    if (e == nullptr) {
+        return;
+    }
+    (void)hipSetDevice(e->device);
+    (void)hipDeviceSynchronize();
+    free_scratch(e);
+    hfree(e->d_r_base);
+    hfree(e->d_r_length);
+    hfree(e->d_r_offset);
+    hfree(e->d_r_meta);
+    hfree(e->d_r_id);
+    hfree(e->d_pbusy);
+    hfree(e->d_ptag);
+    hfree(e->d_cbusy);
+    hfree(e->d_ptot);
+    hfree(e->d_ctot);
+    hfree(e->d_seq);
+    hfree(e->d_rep);
+    if (e->h_rep != nullptr) {
+        (void)hipHostFree(e->h_rep);
+    }
+    for (auto& ev : e->ev) {
+        if (ev != nullptr) {
+            (void)hipEventDestroy(ev);
+        }
+    }
+    delete e;
+}
+
+const engine_config& engine_get_config(const engine* e) { return e->cfg; }
+
+int engine_set_ranges(engine* e, const std::vector<range_rec>& ranges)
+{
+    e->ranges = ranges;
+    e->ranges_dirty = true;
+    return HBFSIM_OK;
+}
+
+int engine_reset(engine* e)
+{
+    const std::size_t rp = e->args.Rp, rc = e->args.Rc;
+    hipError_t err = hipMemset(e->d_pbusy, 0, rp * 8);
+    if (err == hipSuccess) err = hipMemset(e->d_ptag, 0, rp * 16);
+    if (err == hipSuccess) err = hipMemset(e->d_cbusy, 0, rc * 8);
+    if (err == hipSuccess) err = hipMemset(e->d_ptot, 0, rp * 8);
+    if (err == hipSuccess) err = hipMemset(e->d_ctot, 0, rc * 8);
+    if (err == hipSuccess) err = hipMemset(e->d_seq, 0, 8);
+    if (err == hipSuccess) err = hipDeviceSynchronize();
+    e->burst = 0;
+    return hip_status(err);
+}
+
+int engine_synchronize(engine* e)
+{
+    (void)e;
+    return hip_status(hipDeviceSynchronize());
+}
+
+int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_t* d_comp,
+               std::uint8_t* d_status, std::uint64_t base_ps, void* stream_ptr,
+               hbfsim_amd_report* out)
+{
+    if (out != nullptr) {
+        std::memset(out, 0, sizeof(*out));
+    }
+    if (n == 0) {
+        return HBFSIM_OK;
+    }
+    if (d_rec == nullptr || d_comp == nullptr ||
+        (reinterpret_cast<std::uintptr_t>(d_rec) & 15u) != 0 ||
+        (reinterpret_cast<std::uintptr_t>(d_comp) & 7u) != 0) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    if (e->cfg.model != HBFSIM_AMD_MODEL_HBF || e->cfg.slots > 1) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    if (hipSetDevice(e->device) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    if (e->ranges_dirty) {
+        const int st = upload_ranges(e, stream);
+        if (st != HBFSIM_OK) {
+            return st;
+        }
+    }
+    const std::size_t ntiles = (n + e->cfg.tile - 1) / e->cfg.tile;
+    if (ntiles > 0x7fffffffull) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    int st = ensure_scratch(e, ntiles);
+    if (st != HBFSIM_OK) {
+        return st;
+    }
+    const KArgs& a = e->args;
+    const std::size_t lds_a = lds_summary(a), lds_c = lds_apply(a);
+    if (lds_a > 65536 || lds_c > 65536) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    hipError_t err = hipMemsetAsync(e->d_rep, 0, sizeof(DevReport), stream);
+    if (err != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    const dim3 grid(static_cast<unsigned>(ntiles));
+    const unsigned carry_blocks = (a.Rp + a.Rc + 1 + kWave - 1) / kWave;
+    (void)hipEventRecord(e->ev[0], stream);
+    hipLaunchKernelGGL(k_summary, grid, dim3(kWave), lds_a, stream, a, d_rec, n, base_ps,
+                       e->d_psum, e->d_csum, e->d_tcount);
+    (void)hipEventRecord(e->ev[1], stream);
+    hipLaunchKernelGGL(k_carry, dim3(carry_blocks), dim3(kWave), 0, stream, a, ntiles, e->d_psum,
+                       e->d_csum, e->d_tcount, e->d_pcarry, e->d_ccarry, e->d_tseq, e->d_pbusy,
+                       e->d_ptag, e->d_cbusy, e->d_seq);
+    (void)hipEventRecord(e->ev[2], stream);
+    hipLaunchKernelGGL(k_apply, grid, dim3(kWave), lds_c, stream, a, d_rec, n, base_ps,
+                       e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status, e->d_ptot,
+                       e->d_ctot, e->d_rep);
+    (void)hipEventRecord(e->ev[3], stream);
+    err = hipGetLastError();
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(e->h_rep, e->d_rep, sizeof(DevReport), hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    for (int k = 0; k < 3; ++k) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, e->ev[k], e->ev[k + 1]) == hipSuccess) {
+            e->last_ms[k] = ms;
+        }
+    }
+    if (out != nullptr) {
+        std::memcpy(out, e->h_rep, sizeof(*out));
+    }
+    return HBFSIM_OK;
+}
+
+int engine_run_host(engine* e, const hbf_record32* records, std::size_t n,
+                    std::uint64_t* completion, std::uint8_t* status, std::uint64_t base_ps,
+                    hbfsim_amd_report* out)
+{
+    if (out != nullptr) {
+        std::memset(out, 0, sizeof(*out));
+    }
+    if (n == 0) {
+        return HBFSIM_OK;
+    }
+    if (records == nullptr || completion == nullptr) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    if (hipSetDevice(e->device) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    hbf_record32* d_rec = nullptr;
+    std::uint64_t* d_comp = nullptr;
+    std::uint8_t* d_st = nullptr;
+    hipError_t err = halloc(d_rec, n);
+    if (err == hipSuccess) err = halloc(d_comp, n);
+    if (err == hipSuccess && status != nullptr) err = halloc(d_st, n);
+    if (err == hipSuccess)
+        err = hipMemcpy(d_rec, records, n * sizeof(hbf_record32), hipMemcpyHostToDevice);
+    int st = hip_status(err);
+    if (st == HBFSIM_OK) {
+        st = engine_run(e, d_rec, n, d_comp, d_st, base_ps, nullptr, out);
+    }
+    if (st == HBFSIM_OK) {
+        err = hipMemcpy(completion, d_comp, n * 8, hipMemcpyDeviceToHost);
+        if (err == hipSuccess && status != nullptr)
+            err = hipMemcpy(status, d_st, n, hipMemcpyDeviceToHost);
+        st = hip_status(err);
+    }
+    hfree(d_rec);
+    hfree(d_comp);
+    hfree(d_st);
+    return st;
+}
+
+int engine_get_busy_totals(engine* e, std::uint64_t* plane_ps, std::size_t planes,
+                           std::uint64_t* channel_ps, std::size_t channels)
+{
+    if (hipSetDevice(e->device) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    if (plane_ps != nullptr) {
+        if (planes < e->args.Rp) return HBFSIM_INVALID_ARGUMENT;
+        if (hipMemcpy(plane_ps, e->d_ptot, e->args.Rp * 8ull, hipMemcpyDeviceToHost) != hipSuccess)
+            return HBFSIM_CUDA_ERROR;
+    }
+    if (channel_ps != nullptr) {
+        if (channels < e->args.Rc) return HBFSIM_INVALID_ARGUMENT;
+        if (hipMemcpy(channel_ps, e->d_ctot, e->args.Rc * 8ull, hipMemcpyDeviceToHost) !=
+            hipSuccess)
+            return HBFSIM_CUDA_ERROR;
+    }
+    return HBFSIM_OK;
+}
+
+int engine_get_state(engine* e, std::uint64_t* plane_busy, std::uint64_t* plane_tags,
+                     std::uint64_t* channel_cursor, std::uint64_t* sequence, std::uint64_t* burst)
+{
+    if (hipSetDevice(e->device) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    const std::size_t rp = e->args.Rp, rc = e->args.Rc;
+    hipError_t err = hipSuccess;
+    if (plane_busy) err = hipMemcpy(plane_busy, e->d_pbusy, rp * 8, hipMemcpyDeviceToHost);
+    if (err == hipSuccess && plane_tags)
+        err = hipMemcpy(plane_tags, e->d_ptag, rp * 16, hipMemcpyDeviceToHost);
+    if (err == hipSuccess && channel_cursor)
+        err = hipMemcpy(channel_cursor, e->d_cbusy, rc * 8, hipMemcpyDeviceToHost);
+    if (err == hipSuccess && sequence)
+        err = hipMemcpy(sequence, e->d_seq, 8, hipMemcpyDeviceToHost);
+    if (burst) *burst = e->burst;
+    return hip_status(err);
+}
+
+int engine_set_state(engine* e, const std::uint64_t* plane_busy, const std::uint64_t* plane_tags,
+                     const std::uint64_t* channel_cursor, std::uint64_t sequence,
+                     std::uint64_t burst)
+{
+    if (hipSetDevice(e->device) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    const std::size_t rp = e->args.Rp, rc = e->args.Rc;
+    hipError_t err = hipSuccess;
+    if (plane_busy) err = hipMemcpy(e->d_pbusy, plane_busy, rp * 8, hipMemcpyHostToDevice);
+    if (err == hipSuccess && plane_tags)
+        err = hipMemcpy(e->d_ptag, plane_tags, rp * 16, hipMemcpyHostToDevice);
+    if (err == hipSuccess && channel_cursor)
+        err = hipMemcpy(e->d_cbusy, channel_cursor, rc * 8, hipMemcpyHostToDevice);
+    if (err == hipSuccess) err = hipMemcpy(e->d_seq, &sequence, 8, hipMemcpyHostToDevice);
+    e->burst = burst;
+    return hip_status(err);
+}
+
+int engine_last_kernel_ms(const engine* e, float* ms, int max_kernels)
+{
+    const int k = std::min(3, max_kernels);
+    for (int i = 0; i < k; ++i) {
+        ms[i] = e->last_ms[i];
+    }
+    return k;
+}
+
+}  // namespace hbfamd

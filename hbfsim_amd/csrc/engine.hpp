@@ -1,0 +1,80 @@
+// engine.hpp -- host interface of the HIP timing engine (no HIP types).
+#pragma once
+
+#include "../../include/hbfsim_amd.h"
+
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+namespace hbfamd {
+
+// One registered range, the 64-byte SharedRangeRecord of the reference
+// (hbf_device.cuh:105-117).
+struct range_rec {
+    std::uint64_t base;
+    std::uint64_t length;
+    std::uint64_t file_offset;
+    std::uint32_t range_id;
+    std::uint32_t mode;
+    std::uint32_t permissions;
+    std::uint32_t cache_policy;
+    std::uint32_t stream_id;
+    std::uint32_t flags;
+    std::uint64_t page_bytes;
+    std::uint64_t reserved1;
+};
+static_assert(sizeof(range_rec) == 64, "range record layout");
+
+// Everything the kernels need, resolved from profile + engine options.
+struct engine_config {
+    std::uint32_t model{HBFSIM_AMD_MODEL_HBF};
+    std::uint32_t channels{1}, ways{1}, dies{1}, planes{1};
+    std::uint32_t order[4]{0, 1, 2, 3};  // fastest-first axis ids C W D P
+    std::uint32_t page_shift{12};
+    std::uint32_t slots{1};
+    std::uint32_t contention{1};
+    std::uint32_t transfer_page{0};
+    std::uint32_t every_write{0};
+    std::uint32_t hybrid{0};
+    std::uint32_t hybrid_warmup{0};
+    std::uint64_t hybrid_threshold{0};
+    std::uint64_t read_ps{0}, program_ps{0};
+    std::uint64_t xfer_num{1}, xfer_den{1}, xfer_quantum{1};
+    std::uint32_t tile{4096};
+    std::uint32_t emp_pages[6]{};
+    std::uint64_t emp_cum_ns[6]{};
+    std::uint64_t emp_program_ns{0};
+
+    std::uint32_t n_channels() const { return channels; }
+    std::uint32_t n_planes() const { return channels * ways * dies * planes; }
+};
+
+struct engine;
+
+// Returns HBFSIM_OK or an error; *out owns device memory on the current
+// device.
+int engine_create(const engine_config& config, engine** out);
+void engine_destroy(engine* e);
+const engine_config& engine_get_config(const engine* e);
+int engine_set_ranges(engine* e, const std::vector<range_rec>& ranges);
+int engine_run(engine* e, const hbf_record32* d_records, std::size_t n,
+               std::uint64_t* d_completion, std::uint8_t* d_status,
+               std::uint64_t base_ps, void* stream, hbfsim_amd_report* out);
+int engine_get_busy_totals(engine* e, std::uint64_t* plane_ps, std::size_t planes,
+                           std::uint64_t* channel_ps, std::size_t channels);
+int engine_get_state(engine* e, std::uint64_t* plane_busy, std::uint64_t* plane_tags,
+                     std::uint64_t* channel_cursor, std::uint64_t* sequence,
+                     std::uint64_t* burst);
+int engine_set_state(engine* e, const std::uint64_t* plane_busy,
+                     const std::uint64_t* plane_tags, const std::uint64_t* channel_cursor,
+                     std::uint64_t sequence, std::uint64_t burst);
+int engine_reset(engine* e);
+int engine_synchronize(engine* e);
+int engine_last_kernel_ms(const engine* e, float* ms, int max_kernels);
+// Host <-> device staging helpers for the host-pointer entry point.
+int engine_run_host(engine* e, const hbf_record32* records, std::size_t n,
+                    std::uint64_t* completion, std::uint8_t* status,
+                    std::uint64_t base_ps, hbfsim_amd_report* out);
+
+}  // namespace hbfamd

@@ -1,0 +1,313 @@
+/*
+ * hbfsim_amd.h -- C ABI of the MI355X (gfx950) HBF access-timing engine.
+ *
+ * One shared library, hbfsim_amd/libhbfsim_amd.so, exports three groups of
+ * entry points:
+ *
+ *   1. The reference's public C API, same names, argument meaning and error
+ *      codes (include/hbfsim/api.h:12-107 in SlugLab/HBFSim).
+ *   2. The reference's vLLM extension ABI (adapters/vllm/hbfsim_extension.h:
+ *      10-26), ABI version 2, which the loader binds through ctypes
+ *      (adapters/vllm/hbfsim_loader.py:287-385).
+ *   3. Batch entry points that replace the reference's per-access device
+ *      resolver (src/cuda_runtime/device/hbf_device.cu:765-959, 963-1344):
+ *      a stream of access records in HBM is classified, striped and timed by
+ *      HIP kernels, and completion timestamps come back in HBM.
+ *
+ * Plain C types only: no torch, no HIP types in any signature.  Device
+ * pointers are plain addresses; streams are passed as `void*` (a hipStream_t,
+ * NULL for the default stream).  Every function returns an hbfsim_error code
+ * and never throws.
+ */
+#ifndef HBFSIM_AMD_H
+#define HBFSIM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===== 1. Reference public API (include/hbfsim/api.h) ================== */
+
+typedef struct hbfsim_context hbfsim_context;
+
+/* api.h:12-20 */
+enum hbfsim_error {
+    HBFSIM_OK = 0,
+    HBFSIM_INVALID_ARGUMENT = 1,
+    HBFSIM_IO_ERROR = 2,
+    HBFSIM_CUDA_ERROR = 3, /* here: any HIP runtime failure */
+    HBFSIM_TIMEOUT = 4,
+    HBFSIM_UNSUPPORTED = 5,
+    HBFSIM_DAEMON_LOST = 6
+};
+
+/* api.h:22-40 */
+enum hbfsim_range_mode {
+    HBFSIM_RANGE_MODE_TIMING = 1,
+    HBFSIM_RANGE_MODE_CAPACITY = 2
+};
+enum hbfsim_range_permission {
+    HBFSIM_RANGE_READ = 1u << 0,
+    HBFSIM_RANGE_WRITE = 1u << 1,
+    HBFSIM_RANGE_READ_WRITE = HBFSIM_RANGE_READ | HBFSIM_RANGE_WRITE
+};
+enum hbfsim_cache_policy { HBFSIM_CACHE_POLICY_NONE = 0 };
+enum hbfsim_model_mode {
+    HBFSIM_MODEL_REFERENCE = 0,
+    HBFSIM_MODEL_FAST = 1,
+    HBFSIM_MODEL_HYBRID = 2
+};
+
+/* api.h:43-49 */
+typedef struct hbfsim_options {
+    const char* profile_path;
+    const char* report_dir;
+    uint32_t mode;
+    uint32_t ring_capacity;
+    uint64_t request_timeout_ns;
+} hbfsim_options;
+
+/* api.h:51-56 */
+typedef struct hbfsim_range_options {
+    uint32_t mode;
+    uint32_t permissions;
+    uint32_t cache_policy;
+    uint32_t stream_id;
+} hbfsim_range_options;
+
+/* api.h:58-64 */
+typedef struct hbfsim_stats {
+    uint64_t requests_submitted;
+    uint64_t requests_completed;
+    uint64_t fast_requests;
+    uint64_t reference_requests;
+    uint64_t fast_modeled_ns;
+} hbfsim_stats;
+
+/* api.h:66-90 */
+#define HBFSIM_CAPACITY_STATS_V1_VERSION 1u
+typedef struct hbfsim_capacity_stats_v1 {
+    uint32_t struct_size;
+    uint32_t version;
+    uint32_t enabled;
+    uint32_t reserved0;
+    uint64_t page_bytes;
+    uint64_t vmm_granularity;
+    uint64_t pool_allocated_bytes;
+    uint64_t logical_frame_count;
+    uint64_t service_resolve_calls;
+    uint64_t service_resident_hits;
+    uint64_t service_reclaimed_hits;
+    uint64_t service_misses;
+    uint64_t successful_backing_read_pages;
+    uint64_t successful_backing_read_bytes;
+    uint64_t successful_h2d_fill_pages;
+    uint64_t successful_h2d_fill_bytes;
+    uint64_t successful_resolve_evictions;
+    uint64_t service_ready_results;
+    uint64_t successful_d2h_readback_pages;
+    uint64_t successful_d2h_readback_bytes;
+    uint64_t successful_backing_write_pages;
+    uint64_t successful_backing_write_bytes;
+} hbfsim_capacity_stats_v1;
+
+/* api.h:92 (src/api.cpp:3-6): returns 1 */
+uint32_t hbfsim_abi_version(void);
+/* api.h:93 (context.cpp:863-1000, 424-433): loads and validates the JSON
+ * profile; ring_capacity must be a power of two in [2, 4096]; mode 0
+ * (reference, needs the MQSim daemon) returns HBFSIM_UNSUPPORTED. */
+int hbfsim_context_create(const hbfsim_options* options, hbfsim_context** out);
+/* api.h:94 (context.cpp:1658-1717, range_table.cpp:17-118): registers a
+ * TIMING range; CAPACITY ranges return HBFSIM_UNSUPPORTED. */
+int hbfsim_register_device(hbfsim_context* context, void* device_ptr,
+                           size_t length, const hbfsim_range_options* options);
+/* api.h:97 (context.cpp:1719-1760): capacity mode is not part of this
+ * engine; validates arguments, then returns HBFSIM_UNSUPPORTED. */
+int hbfsim_map_file(hbfsim_context* context, const char* path,
+                    uint64_t file_offset, size_t length,
+                    const hbfsim_range_options* options,
+                    void** logical_device_ptr_out);
+/* api.h:101: waits for all engine work issued on the context */
+int hbfsim_flush(hbfsim_context* context);
+/* api.h:102 (context.cpp:1940-2007) */
+int hbfsim_get_stats(hbfsim_context* context, hbfsim_stats* out);
+/* api.h:103: capacity mode disabled -> zeros with enabled = 0 */
+int hbfsim_get_capacity_stats_v1(hbfsim_context* context,
+                                 hbfsim_capacity_stats_v1* out);
+/* api.h:105 (context.cpp:2063-2110, range_table.cpp:120-171) */
+int hbfsim_unregister(hbfsim_context* context, void* range_base);
+/* api.h:106 */
+void hbfsim_context_destroy(hbfsim_context* context);
+
+/* ===== 2. vLLM extension ABI (adapters/vllm/hbfsim_extension.h) ======== */
+
+typedef struct hbfsim_vllm_session hbfsim_vllm_session;
+
+/* hbfsim_extension.h:12-18 */
+typedef struct hbfsim_vllm_options {
+    const char* profile_path;
+    const char* report_dir;
+    uint32_t ring_capacity;
+    uint32_t timing_model;
+    uint64_t request_timeout_ns;
+} hbfsim_vllm_options;
+
+/* hbfsim_extension.cpp:13-16: returns 2 */
+uint32_t hbfsim_vllm_abi_version(void);
+/* hbfsim_extension.cpp:18-49 */
+int hbfsim_vllm_session_create(const hbfsim_vllm_options* options,
+                               hbfsim_vllm_session** out);
+/* hbfsim_extension.cpp:51-67: TIMING range with READ permission */
+int hbfsim_vllm_register_storage(hbfsim_vllm_session* session,
+                                 uintptr_t device_address, size_t bytes);
+/* hbfsim_extension.cpp:69-81: nulls *session */
+int hbfsim_vllm_session_close(hbfsim_vllm_session** session);
+/* hbfsim_extension.cpp:83-101 */
+const char* hbfsim_vllm_status_string(int status);
+/* No counterpart in the reference: the engine context behind a session, so
+ * a vLLM worker can run the batch engine on the ranges it registered. */
+hbfsim_context* hbfsim_vllm_session_context(hbfsim_vllm_session* session);
+
+/* ===== 3. Batch timing engine ========================================== */
+
+/* One access record, 32 bytes, 16-byte aligned.  Replaces one call of the
+ * reference's per-access resolver __hbfsim_resolve(addr, bytes, op)
+ * (hbf_device.cu:963).  issue_ps is the issue time in picoseconds relative
+ * to the run's base_ps.  flags bits 0-7: operation (0 read, 1 write); other
+ * bits are ignored.  Records must be ordered by issue time; a record's
+ * service order on every resource is its position in the stream. */
+typedef struct hbf_record32 {
+    uint64_t addr;
+    uint64_t bytes;
+    uint64_t issue_ps;
+    uint64_t flags;
+} hbf_record32;
+
+/* Per-record status byte: bits 0-1 class (0 modeled, 1 bypass: outside
+ * every range, 2 unsupported: rejected by the resolver's checks), bit 2
+ * page-buffer hit, bit 3 selected by the hybrid sampler, bit 4 write that
+ * programmed the page. */
+enum hbfsim_amd_status_bits {
+    HBFSIM_AMD_MODELED = 0,
+    HBFSIM_AMD_BYPASS = 1,
+    HBFSIM_AMD_UNSUPPORTED = 2,
+    HBFSIM_AMD_PAGE_HIT = 4,
+    HBFSIM_AMD_HYBRID_SAMPLED = 8,
+    HBFSIM_AMD_PROGRAMMED = 16
+};
+
+enum hbfsim_amd_model {
+    /* planes serialise tR / tPROG with a per-plane page buffer; channels
+     * are bandwidth cursors in issue order; completion is the later of the
+     * two (the reference's latency-overlaps-transfer rule,
+     * hbf_device.cuh:797-816, per resource) */
+    HBFSIM_AMD_MODEL_HBF = 0,
+    /* the reference's empirical single-tail model, hbf_device.cu:796-881 */
+    HBFSIM_AMD_MODEL_EMPIRICAL = 1
+};
+
+/* Engine configuration beyond the reference profile.  The reference profile
+ * schema forbids extra keys, so these travel separately.  Zero-initialised
+ * fields take the documented defaults. */
+typedef struct hbfsim_amd_engine_options {
+    uint32_t struct_size;          /* sizeof(hbfsim_amd_engine_options) */
+    uint32_t model;                /* hbfsim_amd_model */
+    uint32_t page_buffers;         /* page registers per plane: 0, 1, 2 */
+    uint32_t plane_contention;     /* 1: planes serialise their service */
+    uint32_t transfer_page;        /* 1: channel moves the whole page */
+    uint32_t program_every_write;  /* 1: every write pays tPROG */
+    uint32_t flat_geometry;        /* 1: one channel, one plane */
+    uint32_t ways;                 /* chips per channel (default 1) */
+    uint64_t xfer_quantum_ps;      /* transfer rounded up to this (1) */
+    uint64_t channel_bandwidth_bytes_per_s; /* 0: aggregate / channels */
+    uint32_t tile_records;         /* records per tile, multiple of 64 */
+    uint32_t reserved0;
+} hbfsim_amd_engine_options;
+
+/* Result of one run (or, from hbfsim_amd_get_report, of all runs). */
+typedef struct hbfsim_amd_report {
+    uint64_t records;
+    uint64_t modeled;
+    uint64_t bypass;
+    uint64_t unsupported;
+    uint64_t reads;
+    uint64_t writes;
+    uint64_t page_hits;
+    uint64_t programs;
+    uint64_t hybrid_sampled;
+    uint64_t makespan_ps;      /* latest completion of a modeled record */
+    uint64_t latency_sum_lo;   /* sum of completion - issue, 128 bits */
+    uint64_t latency_sum_hi;
+    uint64_t latency_max_ps;
+    uint64_t service_sum_ps;   /* sum of uncontended service times */
+} hbfsim_amd_report;
+
+/* Defaults: HBF model (EMPIRICAL when the profile carries empirical_vmem),
+ * one page register per plane, planes serialise, access-sized transfers. */
+int hbfsim_amd_default_engine_options(const hbfsim_context* context,
+                                      hbfsim_amd_engine_options* out);
+/* Replaces the engine configuration; resets engine state. */
+int hbfsim_amd_set_engine_options(hbfsim_context* context,
+                                  const hbfsim_amd_engine_options* options);
+int hbfsim_amd_get_engine_options(const hbfsim_context* context,
+                                  hbfsim_amd_engine_options* out);
+
+/* Time n records resident in device memory (the hot path).  completion_ps
+ * [n] (device) receives completion times: issue for bypass records,
+ * UINT64_MAX for unsupported ones.  status [n] (device) may be NULL.
+ * base_ps is added to every issue_ps.  Engine state (per-plane busy and
+ * page-buffer tags, per-channel cursors) carries over from the previous run
+ * on the context.  `report` (host) may be NULL.  The call returns when the
+ * run has completed on `stream`. */
+int hbfsim_amd_run_device(hbfsim_context* context,
+                          const hbf_record32* records, size_t n,
+                          uint64_t* completion_ps, uint8_t* status,
+                          uint64_t base_ps, void* stream,
+                          hbfsim_amd_report* report);
+/* Same with host buffers: copies in, runs on the default stream, copies
+ * out. */
+int hbfsim_amd_run(hbfsim_context* context, const hbf_record32* records,
+                   size_t n, uint64_t* completion_ps, uint8_t* status,
+                   uint64_t base_ps, hbfsim_amd_report* report);
+/* Cumulative report over every run since the last reset. */
+int hbfsim_amd_get_report(const hbfsim_context* context,
+                          hbfsim_amd_report* out);
+/* Geometry the engine uses: planes = channels*ways*dies*planes_per_die. */
+int hbfsim_amd_get_geometry(const hbfsim_context* context, uint32_t* channels,
+                            uint32_t* planes);
+/* Per-resource busy totals (ps of service charged), cumulative.  Host
+ * arrays of at least `planes` and `channels` entries (either may be NULL). */
+int hbfsim_amd_get_busy_totals(hbfsim_context* context, uint64_t* plane_ps,
+                               size_t planes, uint64_t* channel_ps,
+                               size_t channels);
+/* Engine state for checkpoint / resume: plane busy [planes], plane page tags
+ * [planes * 2] (page + 1, 0 empty), channel cursors [channels], plus the
+ * modeled-request sequence and the empirical burst state.  Host arrays. */
+int hbfsim_amd_get_state(hbfsim_context* context, uint64_t* plane_busy,
+                         uint64_t* plane_tags, uint64_t* channel_cursor,
+                         uint64_t* sequence, uint64_t* burst_state);
+int hbfsim_amd_set_state(hbfsim_context* context, const uint64_t* plane_busy,
+                         const uint64_t* plane_tags,
+                         const uint64_t* channel_cursor, uint64_t sequence,
+                         uint64_t burst_state);
+/* Zeroes engine state, busy totals and the cumulative report. */
+int hbfsim_amd_reset(hbfsim_context* context);
+/* Average device time (ms) of each engine kernel over the last run,
+ * measured with HIP events on the run's stream: [0] tile summary, [1] carry
+ * chain, [2] apply.  Returns the number of kernels written. */
+int hbfsim_amd_last_kernel_ms(const hbfsim_context* context, float* ms,
+                              int max_kernels);
+
+/* Profile validation with the reference's rules and messages
+ * (src/profile/profile.cpp:238-468).  Returns HBFSIM_OK or
+ * HBFSIM_INVALID_ARGUMENT with the reference's message in `error`. */
+int hbfsim_amd_validate_profile(const char* path, char* error,
+                                size_t error_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

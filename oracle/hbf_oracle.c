@@ -1,0 +1,1101 @@
+/*
+ * hbf_oracle.c -- CPU restatement of HBFSim's per-access timing path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see hbf_oracle.h).  Plain C11, no GPU, no
+ * dependency on the product library.  Written from the behaviour of the
+ * cited reference functions; nothing here is shipped or used as a fallback.
+ */
+#include "hbf_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef unsigned __int128 u128;
+
+/* hbf_device.cuh:729-736.  SplitMix64 finaliser (public constants). */
+uint64_t orc_fast_hash(uint64_t value)
+{
+    value += 0x9e3779b97f4a7c15ULL;
+    value = (value ^ (value >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    value = (value ^ (value >> 27)) * 0x94d049bb133111ebULL;
+    return value ^ (value >> 31);
+}
+
+/* hbf_device.cuh:738-744 */
+int orc_hybrid_reference_sample(uint64_t sequence, uint32_t warmup,
+                                uint64_t threshold, uint64_t key)
+{
+    return sequence < warmup ||
+           (threshold != 0 && orc_fast_hash(sequence ^ key) <= threshold);
+}
+
+/* context.cpp:975-981: rate * UINT64_MAX in long double, saturating at 1. */
+uint64_t orc_sample_threshold(double rate)
+{
+    if (rate >= 1.0) {
+        return UINT64_MAX;
+    }
+    return (uint64_t)((long double)rate * (long double)UINT64_MAX);
+}
+
+/* hbf_device.cuh:746-756: ceil(bytes * 1e9 / bandwidth) ns, 0 if either is 0 */
+uint64_t orc_fast_transfer_ns(uint32_t bytes, uint64_t bandwidth)
+{
+    if (bytes == 0 || bandwidth == 0) {
+        return 0;
+    }
+    const uint64_t numerator = (uint64_t)bytes * 1000000000ULL;
+    return (numerator + bandwidth - 1) / bandwidth;
+}
+
+/* hbf_device.cuh:797-816: the later of latency and transfer, not the sum */
+uint64_t orc_fast_service_ns(uint64_t base_ns, uint32_t bytes,
+                             uint64_t bandwidth)
+{
+    const uint64_t transfer = orc_fast_transfer_ns(bytes, bandwidth);
+    return transfer > base_ns ? transfer : base_ns;
+}
+
+/* hbf_device.cuh:946-957 */
+uint64_t orc_saturating_add(uint64_t a, uint64_t b)
+{
+    return b > UINT64_MAX - a ? UINT64_MAX : a + b;
+}
+
+uint64_t orc_saturating_multiply(uint64_t a, uint32_t b)
+{
+    return b != 0 && a > UINT64_MAX / b ? UINT64_MAX : a * b;
+}
+
+/* hbf_device.cuh:826-841: upper_bound(base) - 1, or count when none */
+uint32_t orc_find_range_index(const orc_range* ranges, uint32_t count,
+                              uint64_t address)
+{
+    uint32_t lo = 0, hi = count;
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (ranges[mid].base <= address) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    return lo == 0 ? count : lo - 1;
+}
+
+/* hbf_device.cuh:843-860 */
+int orc_access_supported(const orc_range* r, uint64_t address, uint32_t bytes,
+                         uint32_t operation)
+{
+    if (bytes == 0 || operation > 1 || (r->mode != 1 && r->mode != 2) ||
+        r->page_bytes == 0 || r->page_bytes > UINT32_MAX ||
+        r->length > UINT64_MAX - r->base || address < r->base ||
+        address - r->base >= r->length || bytes > UINT64_MAX - address ||
+        address + bytes > r->base + r->length ||
+        (r->permissions & (1u << operation)) == 0) {
+        return 0;
+    }
+    const uint64_t offset = address - r->base;
+    const uint64_t last = offset + bytes - 1;
+    return offset / r->page_bytes == last / r->page_bytes;
+}
+
+/* hbf_device.cuh:873-884 */
+int orc_range_overlaps(const orc_range* r, uint64_t address, uint32_t bytes)
+{
+    if (bytes == 0 || r->length == 0 || r->base > UINT64_MAX - r->length ||
+        address > UINT64_MAX - bytes) {
+        return 0;
+    }
+    return address < r->base + r->length && r->base < address + bytes;
+}
+
+/* hbf_device.cuh:895-909 */
+int orc_span_touches_any_range(const orc_range* ranges, uint32_t count,
+                               uint64_t address, uint32_t bytes)
+{
+    if (ranges == NULL || count == 0 || bytes == 0) {
+        return 0;
+    }
+    const uint32_t index = orc_find_range_index(ranges, count, address);
+    if (index != count && orc_range_overlaps(&ranges[index], address, bytes)) {
+        return 1;
+    }
+    const uint32_t successor = index == count ? 0u : index + 1u;
+    return successor < count &&
+           orc_range_overlaps(&ranges[successor], address, bytes);
+}
+
+/* hbf_device.cuh:929-944 */
+orc_media orc_media_descriptor(const orc_range* r, uint64_t address,
+                               uint32_t bytes, uint32_t operation)
+{
+    orc_media m = {0, 0, 0};
+    if (!orc_access_supported(r, address, bytes, operation)) {
+        return m;
+    }
+    const uint64_t page_offset =
+        ((address - r->base) / r->page_bytes) * r->page_bytes;
+    if (page_offset > UINT64_MAX - r->file_offset) {
+        return m;
+    }
+    m.logical_address = r->file_offset + page_offset;
+    m.bytes = (uint32_t)r->page_bytes;
+    m.valid = 1;
+    return m;
+}
+
+/* The resolver's classification order, hbf_device.cu:1081-1165:
+ *   1. start-address lookup; if the start lies outside every range, the
+ *      access is rejected when its span reaches into the successor range
+ *      (:1094-1108), else it bypasses at native speed (:1128-1136);
+ *   2. inside a range, media_descriptor must be valid (:1151-1165).
+ * Record bytes wider than 32 bits cannot be described by the device ABI
+ * (u32 bytes) and are rejected. */
+uint32_t orc_classify(const orc_range* ranges, uint32_t count,
+                      uint64_t address, uint64_t bytes, uint32_t operation,
+                      uint32_t* range_index)
+{
+    const uint32_t b32 = bytes > UINT32_MAX ? 0u : (uint32_t)bytes;
+    const uint32_t index = orc_find_range_index(ranges, count, address);
+    if (index == count || address < ranges[index].base ||
+        address - ranges[index].base >= ranges[index].length) {
+        const uint32_t successor = index == count ? 0u : index + 1u;
+        if (bytes > UINT32_MAX ||
+            (successor < count &&
+             orc_range_overlaps(&ranges[successor], address, b32))) {
+            return ORC_UNSUPPORTED;
+        }
+        return ORC_BYPASS;
+    }
+    if (bytes > UINT32_MAX) {
+        return ORC_UNSUPPORTED;
+    }
+    const orc_media m = orc_media_descriptor(&ranges[index], address, b32,
+                                             operation);
+    if (!m.valid) {
+        return ORC_UNSUPPORTED;
+    }
+    *range_index = index;
+    return ORC_MODELED;
+}
+
+/* hbf_device.cuh:959-978 */
+uint64_t orc_ceiling_scaled_delta(uint64_t delta, uint32_t offset,
+                                  uint32_t span)
+{
+    if (delta == 0 || offset == 0) {
+        return 0;
+    }
+    if (span == 0) {
+        return UINT64_MAX;
+    }
+    const uint64_t quotient = delta / span;
+    const uint64_t remainder = delta % span;
+    const uint64_t integral = orc_saturating_multiply(quotient, offset);
+    const uint64_t fractional =
+        (remainder * (uint64_t)offset + span - 1) / span;
+    return orc_saturating_add(integral, fractional);
+}
+
+/* hbf_device.cuh:980-1016: piecewise-linear cumulative curve with ceiling
+ * interpolation; beyond the last point extrapolates the last segment. */
+uint64_t orc_empirical_cumulative_ns(const uint32_t* pages,
+                                     const uint64_t* cumulative,
+                                     uint32_t count, uint32_t run_pages)
+{
+    if (run_pages == 0) {
+        return 0;
+    }
+    if (pages == NULL || cumulative == NULL || count == 0) {
+        return UINT64_MAX;
+    }
+    uint32_t right = 0;
+    while (right < count && run_pages > pages[right]) {
+        ++right;
+    }
+    if (right == count) {
+        right = count - 1;
+    }
+    uint32_t left_pages = 0;
+    uint64_t left_ns = 0;
+    if (right != 0) {
+        left_pages = pages[right - 1];
+        left_ns = cumulative[right - 1];
+    }
+    if (run_pages > pages[right] && count > 1) {
+        left_pages = pages[count - 2];
+        left_ns = cumulative[count - 2];
+        right = count - 1;
+    }
+    if (pages[right] <= left_pages || cumulative[right] < left_ns ||
+        run_pages < left_pages) {
+        return UINT64_MAX;
+    }
+    const uint64_t inc = orc_ceiling_scaled_delta(
+        cumulative[right] - left_ns, run_pages - left_pages,
+        pages[right] - left_pages);
+    return orc_saturating_add(left_ns, inc);
+}
+
+/* hbf_device.cuh:1018-1029 */
+uint64_t orc_empirical_service_ns(const uint32_t* pages,
+                                  const uint64_t* cumulative, uint32_t count,
+                                  uint32_t run_pages)
+{
+    if (run_pages == 0) {
+        return 0;
+    }
+    const uint64_t cur =
+        orc_empirical_cumulative_ns(pages, cumulative, count, run_pages);
+    const uint64_t prev =
+        orc_empirical_cumulative_ns(pages, cumulative, count, run_pages - 1);
+    return cur < prev ? UINT64_MAX : cur - prev;
+}
+
+#define ORC_BURST_RUN_MASK 1023ULL
+#define ORC_MAX_EMPIRICAL_PAGE ((1ULL << 53) - 2)
+
+/* hbf_device.cuh:1031-1080: packed = (page+1) << 11 | op << 10 | run */
+int orc_update_empirical_burst(uint64_t previous, uint64_t page,
+                               uint32_t operation, uint64_t* packed,
+                               uint32_t* run_pages)
+{
+    if (page > ORC_MAX_EMPIRICAL_PAGE || operation > 1) {
+        *packed = previous;
+        *run_pages = 0;
+        return 0;
+    }
+    uint32_t run = 1;
+    const uint64_t prev_plus_one = previous >> 11;
+    const uint64_t prev_page = prev_plus_one == 0 ? UINT64_MAX
+                                                  : prev_plus_one - 1;
+    const uint32_t prev_run = (uint32_t)(previous & ORC_BURST_RUN_MASK);
+    const uint32_t prev_op = (uint32_t)((previous >> 10) & 1u);
+    if (previous != 0 && prev_run != 0 && prev_op == operation &&
+        prev_page != UINT64_MAX && prev_page + 1 == page) {
+        run = prev_run == ORC_BURST_RUN_MASK ? prev_run : prev_run + 1;
+    }
+    *packed = ((page + 1) << 11) | ((uint64_t)operation << 10) | run;
+    *run_pages = run;
+    return 1;
+}
+
+/* hbf_device.cuh:1089-1111 */
+int orc_empirical_control_valid(const orc_empirical* e)
+{
+    if (e->flags != 1 || e->point_count != 6 || e->program_latency_ns == 0) {
+        return 0;
+    }
+    for (uint32_t i = 0; i < 6; ++i) {
+        if (e->pages[i] == 0 || e->cumulative_ns[i] == 0 ||
+            (i != 0 && e->pages[i] <= e->pages[i - 1]) ||
+            (i != 0 && e->cumulative_ns[i] <= e->cumulative_ns[i - 1])) {
+            return 0;
+        }
+    }
+    return e->pages[5] <= ORC_BURST_RUN_MASK;
+}
+
+/* hbf_device.cuh:1113-1140 */
+int orc_empirical_request_service(const orc_empirical* e, uint64_t previous,
+                                  uint64_t page, uint32_t operation,
+                                  uint64_t* service_ns, uint64_t* packed,
+                                  uint32_t* run_pages)
+{
+    if (!orc_empirical_control_valid(e)) {
+        return 0;
+    }
+    if (!orc_update_empirical_burst(previous, page, operation, packed,
+                                    run_pages)) {
+        return 0;
+    }
+    *service_ns = operation == 0
+                      ? orc_empirical_service_ns(e->pages, e->cumulative_ns,
+                                                 e->point_count, *run_pages)
+                      : e->program_latency_ns;
+    return 1;
+}
+
+/* ---- range registry: range_table.cpp:17-198 ------------------------- */
+orc_range_table* orc_range_table_create(uint64_t page_bytes,
+                                        uint64_t media_capacity)
+{
+    orc_range_table* t = (orc_range_table*)calloc(1, sizeof(*t));
+    if (t == NULL) {
+        return NULL;
+    }
+    t->records = (orc_range*)calloc(ORC_RANGE_CAPACITY, sizeof(orc_range));
+    if (t->records == NULL) {
+        free(t);
+        return NULL;
+    }
+    t->next_range_id = 1;
+    t->page_bytes = page_bytes;
+    t->media_capacity = media_capacity;
+    return t;
+}
+
+void orc_range_table_destroy(orc_range_table* t)
+{
+    if (t != NULL) {
+        free(t->records);
+        free(t);
+    }
+}
+
+/* range_table.cpp:17-118: validation, media extent, overlap, publish */
+int orc_range_table_add(orc_range_table* t, uint64_t base, uint64_t length,
+                        uint32_t mode, uint32_t permissions,
+                        uint32_t cache_policy, uint32_t stream_id)
+{
+    if (base == 0 || length == 0 || t->page_bytes == 0 ||
+        length > UINT64_MAX - base || permissions == 0 ||
+        (permissions & ~3u) != 0 || cache_policy != 0) {
+        return 1;
+    }
+    if (mode != 1 && mode != 2) {
+        return 1;
+    }
+    if (t->count == ORC_RANGE_CAPACITY) {
+        return 5;
+    }
+    if (length > UINT64_MAX - (t->page_bytes - 1)) {
+        return 5;
+    }
+    const uint64_t extent =
+        ((length + t->page_bytes - 1) / t->page_bytes) * t->page_bytes;
+    if (t->next_file_offset > t->media_capacity ||
+        extent > t->media_capacity - t->next_file_offset) {
+        return 5;
+    }
+    /* lower_bound on base */
+    uint32_t lo = 0, hi = t->count;
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (t->records[mid].base < base) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    const uint32_t index = lo;
+    const uint64_t end = base + length;
+    if ((index != 0 && t->records[index - 1].base +
+                               t->records[index - 1].length > base) ||
+        (index != t->count && end > t->records[index].base)) {
+        return 1;
+    }
+    memmove(&t->records[index + 1], &t->records[index],
+            (size_t)(t->count - index) * sizeof(orc_range));
+    orc_range r;
+    memset(&r, 0, sizeof(r));
+    r.base = base;
+    r.length = length;
+    r.file_offset = t->next_file_offset;
+    r.range_id = t->next_range_id;
+    r.mode = mode;
+    r.permissions = permissions;
+    r.cache_policy = cache_policy;
+    r.stream_id = stream_id;
+    r.page_bytes = t->page_bytes;
+    t->records[index] = r;
+    t->count += 1;
+    t->next_range_id += 1;
+    t->next_file_offset += extent;
+    return 0;
+}
+
+/* range_table.cpp:120-171 */
+int orc_range_table_remove(orc_range_table* t, uint64_t base)
+{
+    if (base == 0) {
+        return 1;
+    }
+    uint32_t lo = 0, hi = t->count;
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (t->records[mid].base < base) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    if (lo == t->count || t->records[lo].base != base) {
+        return 1;
+    }
+    memmove(&t->records[lo], &t->records[lo + 1],
+            (size_t)(t->count - lo - 1) * sizeof(orc_range));
+    t->count -= 1;
+    memset(&t->records[t->count], 0, sizeof(orc_range));
+    return 0;
+}
+
+/* range_table.cpp:173-198 */
+int orc_range_table_lookup(const orc_range_table* t, uint64_t address,
+                           uint32_t bytes, uint32_t* index)
+{
+    if (bytes == 0 || t->count == 0) {
+        return 0;
+    }
+    uint32_t lo = 0, hi = t->count; /* upper_bound */
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (address < t->records[mid].base) {
+            hi = mid;
+        } else {
+            lo = mid + 1;
+        }
+    }
+    if (lo == 0) {
+        return 0;
+    }
+    const orc_range* r = &t->records[lo - 1];
+    if (address < r->base || address - r->base >= r->length) {
+        return 0;
+    }
+    *index = lo - 1;
+    if (bytes > UINT64_MAX - address || address + bytes > r->base + r->length) {
+        return 2;
+    }
+    return 1;
+}
+
+/* ---- striping ------------------------------------------------------- */
+/* MQSim's plane allocation scheme names the axis that advances fastest
+ * first (profile.hpp:51-77; the CWDP case is spelled out by
+ * bank_layout.cpp:59-72 as channel = lpa % C, chip = (lpa / C) % chips). */
+uint64_t orc_stripe(uint64_t page, const uint32_t order[4],
+                    const uint32_t sizes[4], uint32_t coords[4])
+{
+    uint64_t rem = page;
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t axis = order[i];
+        coords[axis] = (uint32_t)(rem % sizes[axis]);
+        rem /= sizes[axis];
+    }
+    return rem; /* row (page index within the plane) */
+}
+
+int orc_parse_scheme(const char* name, uint32_t order[4])
+{
+    if (name == NULL || strlen(name) != 4) {
+        return 0;
+    }
+    uint32_t seen = 0;
+    for (int i = 0; i < 4; ++i) {
+        uint32_t axis;
+        switch (name[i]) {
+        case 'C': axis = 0; break;
+        case 'W': axis = 1; break;
+        case 'D': axis = 2; break;
+        case 'P': axis = 3; break;
+        default: return 0;
+        }
+        if (seen & (1u << axis)) {
+            return 0;
+        }
+        seen |= 1u << axis;
+        order[i] = axis;
+    }
+    return 1;
+}
+
+/* bank_layout.cpp:48-57 */
+uint64_t orc_hbf_media_lpa(uint64_t q, uint32_t module, uint32_t channels)
+{
+    return q * channels + module;
+}
+
+/* bank_layout.cpp:59-72 */
+void orc_hbf_cold_read_bank(uint64_t lpa, uint32_t channels,
+                            uint32_t core_dies, uint32_t banks,
+                            uint32_t* channel, uint32_t* core_die,
+                            uint32_t* bank, uint32_t* chip)
+{
+    *channel = (uint32_t)(lpa % channels);
+    const uint32_t c = (uint32_t)((lpa / channels) % (core_dies * banks));
+    *chip = c;
+    *core_die = c / banks;
+    *bank = c % banks;
+}
+
+/* ---- multi-resource engine ----------------------------------------- */
+static uint64_t xfer_ps(const orc_engine_params* p, uint64_t bytes)
+{
+    /* q * ceil(bytes * num / den): bytes at the per-channel bandwidth,
+     * rounded up to whole quanta (q = 1000 reproduces the reference's
+     * whole-nanosecond transfer times, hbf_device.cuh:746-756). */
+    const u128 prod = (u128)bytes * p->xfer_num;
+    return p->xfer_quantum *
+           (uint64_t)((prod + p->xfer_den - 1) / p->xfer_den);
+}
+
+static uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+/* Page-buffer slot rule per plane.  slots==1: one page register.
+ * slots==2: device_coalescer.cpp:134-168 -- a miss takes the first empty
+ * slot, else the lowest-index unpinned slot (slot 0).  Nothing is pinned
+ * here because a plane finishes one sense before the next begins. */
+static int pagebuf_access(uint64_t* tags, uint32_t slots, uint64_t page)
+{
+    const uint64_t tag = page + 1;
+    for (uint32_t k = 0; k < slots; ++k) {
+        if (tags[k] == tag) {
+            return 1;
+        }
+    }
+    for (uint32_t k = 0; k < slots; ++k) {
+        if (tags[k] == 0) {
+            tags[k] = tag;
+            return 0;
+        }
+    }
+    if (slots > 0) {
+        tags[0] = tag;
+    }
+    return 0;
+}
+
+void orc_pagebuf_sequence(const uint64_t* pages, size_t n, uint32_t slots,
+                          uint8_t* hits)
+{
+    uint64_t tags[2] = {0, 0};
+    for (size_t i = 0; i < n; ++i) {
+        hits[i] = (uint8_t)pagebuf_access(tags, slots, pages[i]);
+    }
+}
+
+static void add128(orc_engine_report* r, uint64_t v)
+{
+    const uint64_t lo = r->latency_sum_lo + v;
+    r->latency_sum_hi += lo < r->latency_sum_lo;
+    r->latency_sum_lo = lo;
+}
+
+/* Per-record decode shared by the sequential and parallel oracles. */
+typedef struct decoded {
+    uint32_t cls;
+    uint32_t op;
+    uint32_t plane;   /* global plane id */
+    uint32_t channel;
+    uint64_t page;    /* media page number */
+    uint64_t issue;
+    uint64_t xfer;
+    uint64_t svc_miss;  /* plane service when the page is not buffered */
+    uint64_t svc_hit;   /* plane service when it is */
+    uint32_t range_id;
+} decoded;
+
+static void decode(const orc_engine_params* p, const orc_range* ranges,
+                   uint32_t count, const orc_record* rec, uint64_t base_ps,
+                   decoded* d)
+{
+    memset(d, 0, sizeof(*d));
+    const uint32_t op = (uint32_t)(rec->flags & 0xffu);
+    uint32_t index = 0;
+    d->issue = base_ps + rec->issue_ps;
+    d->op = op;
+    d->cls = orc_classify(ranges, count, rec->addr, rec->bytes, op, &index);
+    if (d->cls != ORC_MODELED) {
+        return;
+    }
+    const orc_range* r = &ranges[index];
+    const uint64_t media = r->file_offset + (rec->addr - r->base);
+    const uint64_t page_bytes = 1ULL << p->page_shift;
+    d->page = media >> p->page_shift;
+    d->range_id = r->range_id;
+    const uint32_t sizes[4] = {p->channels, p->ways, p->dies, p->planes};
+    uint32_t c[4];
+    orc_stripe(d->page, p->order, sizes, c);
+    d->channel = c[0];
+    d->plane = ((c[0] * p->ways + c[1]) * p->dies + c[2]) * p->planes + c[3];
+    const uint64_t xbytes = p->transfer_page ? page_bytes : rec->bytes;
+    d->xfer = xfer_ps(p, xbytes);
+    if (op == 0) {
+        d->svc_miss = p->read_ps;
+        d->svc_hit = 0;
+    } else {
+        const uint64_t off = media & (page_bytes - 1);
+        const int fill = off + rec->bytes == page_bytes;
+        d->svc_miss = d->svc_hit =
+            (fill || p->program_every_write) ? p->program_ps : 0;
+    }
+}
+
+static int engine_params_ok(const orc_engine_params* p)
+{
+    return p->channels && p->ways && p->dies && p->planes &&
+           p->page_shift >= 9 && p->page_shift < 63 && p->page_buffers <= 2 &&
+           p->xfer_den != 0 && p->xfer_quantum != 0;
+}
+
+int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
+                   uint32_t range_count, const orc_record* records, size_t n,
+                   uint64_t base_ps, orc_engine_state* s, uint64_t* completion,
+                   uint8_t* status, orc_engine_report* rep)
+{
+    if (!engine_params_ok(p)) {
+        return 1;
+    }
+    if (p->model == ORC_MODEL_FAST_EMPIRICAL &&
+        (!orc_empirical_control_valid(&p->empirical) || p->page_shift != 12)) {
+        return 5;
+    }
+    const uint32_t slots = p->page_buffers;
+    for (size_t i = 0; i < n; ++i) {
+        decoded d;
+        decode(p, ranges, range_count, &records[i], base_ps, &d);
+        rep->records += 1;
+        uint8_t st = (uint8_t)d.cls;
+        if (d.cls == ORC_BYPASS) {
+            completion[i] = d.issue;
+            rep->bypass += 1;
+        } else if (d.cls == ORC_UNSUPPORTED) {
+            completion[i] = UINT64_MAX;
+            rep->unsupported += 1;
+        } else {
+            const uint64_t seq = s->modeled_sequence++;
+            const uint64_t key = (d.page << p->page_shift) ^
+                                 ((uint64_t)d.range_id << 32) ^ d.op;
+            if (p->hybrid && orc_hybrid_reference_sample(
+                                 seq, p->hybrid_warmup, p->hybrid_threshold,
+                                 key)) {
+                rep->hybrid_sampled += 1;
+                st |= 8;
+            }
+            uint64_t done;
+            uint64_t svc_plane;
+            uint64_t xfer;
+            if (p->model == ORC_MODEL_FAST_EMPIRICAL) {
+                /* hbf_device.cu:796-881 with time_scale 1, in ps */
+                uint64_t svc_ns = 0, packed = 0;
+                uint32_t run = 0;
+                orc_empirical_request_service(&p->empirical, s->burst_state,
+                                              d.page, d.op, &svc_ns, &packed,
+                                              &run);
+                s->burst_state = packed;
+                const uint64_t svc = svc_ns * 1000u;
+                done = max_u64(s->channel_cursor[0], d.issue) + svc;
+                s->channel_cursor[0] = done;
+                s->channel_busy_total[0] += svc;
+                svc_plane = svc;
+                xfer = svc;
+            } else {
+                int hit = 0;
+                if (slots) {
+                    hit = pagebuf_access(&s->plane_tag[(size_t)d.plane * 2],
+                                         slots, d.page);
+                }
+                svc_plane = hit ? d.svc_hit : d.svc_miss;
+                uint64_t pd;
+                if (p->plane_contention) {
+                    pd = max_u64(s->plane_busy[d.plane], d.issue) + svc_plane;
+                    s->plane_busy[d.plane] = pd;
+                } else {
+                    pd = d.issue + svc_plane;
+                }
+                const uint64_t cd =
+                    max_u64(s->channel_cursor[d.channel], d.issue) + d.xfer;
+                s->channel_cursor[d.channel] = cd;
+                done = max_u64(pd, cd);
+                xfer = d.xfer;
+                s->plane_busy_total[d.plane] += svc_plane;
+                s->channel_busy_total[d.channel] += d.xfer;
+                if (d.op == 0 && hit) {
+                    rep->page_hits += 1;
+                    st |= 4;
+                }
+                if (d.op == 1 && svc_plane != 0) {
+                    rep->programs += 1;
+                    st |= 16;
+                }
+            }
+            completion[i] = done;
+            rep->modeled += 1;
+            if (d.op == 0) {
+                rep->reads += 1;
+            } else {
+                rep->writes += 1;
+            }
+            rep->makespan_ps = max_u64(rep->makespan_ps, done);
+            const uint64_t lat = done - d.issue;
+            add128(rep, lat);
+            rep->latency_max_ps = max_u64(rep->latency_max_ps, lat);
+            rep->service_sum_ps += max_u64(svc_plane, xfer);
+        }
+        if (status != NULL) {
+            status[i] = st;
+        }
+    }
+    return 0;
+}
+
+/* Parallel oracle: classification/decode in parallel over records; the plane
+ * stage in parallel over planes and the channel stage over channels, each
+ * resource's records visited in input order.  Identical results to
+ * orc_engine_run for ORC_MODEL_HBF (hybrid counting runs sequentially). */
+int orc_engine_run_parallel(const orc_engine_params* p,
+                            const orc_range* ranges, uint32_t range_count,
+                            const orc_record* records, size_t n,
+                            uint64_t base_ps, orc_engine_state* s,
+                            uint64_t* completion, uint8_t* status,
+                            orc_engine_report* rep, int threads)
+{
+    if (p->model != ORC_MODEL_HBF || threads <= 1) {
+        return orc_engine_run(p, ranges, range_count, records, n, base_ps, s,
+                              completion, status, rep);
+    }
+    if (!engine_params_ok(p)) {
+        return 1;
+    }
+    decoded* d = (decoded*)malloc(n * sizeof(decoded));
+    uint64_t* pd = (uint64_t*)malloc(n * sizeof(uint64_t));
+    uint8_t* hit = (uint8_t*)calloc(n, 1);
+    if (d == NULL || pd == NULL || hit == NULL) {
+        free(d);
+        free(pd);
+        free(hit);
+        return 2;
+    }
+    const uint32_t planes = p->channels * p->ways * p->dies * p->planes;
+    const uint32_t slots = p->page_buffers;
+#pragma omp parallel num_threads(threads)
+    {
+#pragma omp for schedule(static)
+        for (size_t i = 0; i < n; ++i) {
+            decode(p, ranges, range_count, &records[i], base_ps, &d[i]);
+        }
+        /* plane stage: thread t owns planes with id % T == t */
+#pragma omp for schedule(static, 1)
+        for (int t = 0; t < threads; ++t) {
+            for (size_t i = 0; i < n; ++i) {
+                if (d[i].cls != ORC_MODELED ||
+                    d[i].plane % (uint32_t)threads != (uint32_t)t) {
+                    continue;
+                }
+                const uint32_t pl = d[i].plane;
+                int h = 0;
+                if (slots) {
+                    h = pagebuf_access(&s->plane_tag[(size_t)pl * 2], slots,
+                                       d[i].page);
+                }
+                hit[i] = (uint8_t)h;
+                const uint64_t svc = h ? d[i].svc_hit : d[i].svc_miss;
+                if (p->plane_contention) {
+                    s->plane_busy[pl] =
+                        max_u64(s->plane_busy[pl], d[i].issue) + svc;
+                    pd[i] = s->plane_busy[pl];
+                } else {
+                    pd[i] = d[i].issue + svc;
+                }
+                s->plane_busy_total[pl] += svc;
+            }
+        }
+        /* channel stage */
+#pragma omp for schedule(static, 1)
+        for (int t = 0; t < threads; ++t) {
+            for (size_t i = 0; i < n; ++i) {
+                if (d[i].cls != ORC_MODELED ||
+                    d[i].channel % (uint32_t)threads != (uint32_t)t) {
+                    continue;
+                }
+                const uint32_t ch = d[i].channel;
+                s->channel_cursor[ch] =
+                    max_u64(s->channel_cursor[ch], d[i].issue) + d[i].xfer;
+                completion[i] = max_u64(pd[i], s->channel_cursor[ch]);
+                s->channel_busy_total[ch] += d[i].xfer;
+            }
+        }
+    }
+    (void)planes;
+    for (size_t i = 0; i < n; ++i) {
+        rep->records += 1;
+        uint8_t st = (uint8_t)d[i].cls;
+        if (d[i].cls == ORC_BYPASS) {
+            completion[i] = d[i].issue;
+            rep->bypass += 1;
+        } else if (d[i].cls == ORC_UNSUPPORTED) {
+            completion[i] = UINT64_MAX;
+            rep->unsupported += 1;
+        } else {
+            const uint64_t seq = s->modeled_sequence++;
+            const uint64_t key = (d[i].page << p->page_shift) ^
+                                 ((uint64_t)d[i].range_id << 32) ^ d[i].op;
+            if (p->hybrid && orc_hybrid_reference_sample(
+                                 seq, p->hybrid_warmup, p->hybrid_threshold,
+                                 key)) {
+                rep->hybrid_sampled += 1;
+                st |= 8;
+            }
+            const uint64_t svc = hit[i] ? d[i].svc_hit : d[i].svc_miss;
+            rep->modeled += 1;
+            if (d[i].op == 0) {
+                rep->reads += 1;
+                if (hit[i]) {
+                    rep->page_hits += 1;
+                    st |= 4;
+                }
+            } else {
+                rep->writes += 1;
+                if (svc != 0) {
+                    rep->programs += 1;
+                    st |= 16;
+                }
+            }
+            const uint64_t done = completion[i];
+            rep->makespan_ps = max_u64(rep->makespan_ps, done);
+            const uint64_t lat = done - d[i].issue;
+            add128(rep, lat);
+            rep->latency_max_ps = max_u64(rep->latency_max_ps, lat);
+            rep->service_sum_ps += max_u64(svc, d[i].xfer);
+        }
+        if (status != NULL) {
+            status[i] = st;
+        }
+    }
+    free(d);
+    free(pd);
+    free(hit);
+    return 0;
+}
+
+/* hbf_device.cu:883-958, time_scale 1: one global tail; the latency bound
+ * and the transfer tail are independent and the target is their maximum. */
+uint64_t orc_fast_model_scalar(const uint64_t* arrival_ns,
+                               const uint32_t* operation, const uint32_t* bytes,
+                               size_t n, uint64_t read_ns, uint64_t program_ns,
+                               uint64_t bandwidth, uint64_t* tail_ns,
+                               uint64_t* target_ns)
+{
+    uint64_t modeled = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const uint64_t base = operation[i] == 0 ? read_ns : program_ns;
+        const uint64_t xfer = orc_fast_transfer_ns(bytes[i], bandwidth);
+        const uint64_t start = *tail_ns > arrival_ns[i] ? *tail_ns
+                                                        : arrival_ns[i];
+        const uint64_t transfer_target = orc_saturating_add(start, xfer);
+        *tail_ns = transfer_target;
+        const uint64_t latency_target =
+            orc_saturating_add(arrival_ns[i], base);
+        target_ns[i] = latency_target > transfer_target ? latency_target
+                                                        : transfer_target;
+        modeled += orc_fast_service_ns(base, bytes[i], bandwidth);
+    }
+    return modeled;
+}
+
+/* hbf_trace_timing.cpp:92-121 (event validation) and :181-233 (fast loop):
+ * ordered blocking replay, clock += max(base, transfer) per page. */
+int orc_trace_timing_fast(const orc_trace_event* ev, size_t n,
+                          uint64_t read_ns, uint64_t program_ns,
+                          uint64_t bandwidth, uint64_t profile_page_bytes,
+                          uint64_t capacity_bytes, uint64_t* submitted,
+                          uint64_t* service_ns, uint64_t* clock_ns)
+{
+    uint64_t seq = 0, clock = 0, service = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const uint64_t bytes = ev[i].bytes;
+        const uint64_t page = ev[i].page_bytes;
+        if (bytes == 0 || page == 0 || bytes % page != 0 || page % 512 != 0 ||
+            ev[i].operation > 1 || ev[i].logical_address % page != 0 ||
+            bytes > UINT64_MAX - ev[i].logical_address) {
+            return 64;
+        }
+        if (page != profile_page_bytes ||
+            ev[i].logical_address + bytes > capacity_bytes) {
+            return 64;
+        }
+        for (uint64_t off = 0; off < bytes; off += page) {
+            ++seq;
+            const uint64_t base = ev[i].operation ? program_ns : read_ns;
+            const u128 t = ((u128)page * 1000000000ULL + bandwidth - 1) /
+                           bandwidth;
+            const uint64_t xfer = (uint64_t)t;
+            const uint64_t exposed = xfer > base ? xfer : base;
+            service = orc_saturating_add(service, exposed);
+            clock = orc_saturating_add(clock, exposed);
+        }
+    }
+    *submitted = seq;
+    *service_ns = service;
+    *clock_ns = clock;
+    return 0;
+}
+
+/* mqsim_online.cpp:321-335: bandwidth cursor lower-bounds completion */
+uint64_t orc_bandwidth_cursor(uint64_t* cursor_ns, uint64_t arrival_ns,
+                              uint64_t bytes, uint64_t bandwidth,
+                              uint64_t media_completion_ns)
+{
+    const uint64_t xfer = (uint64_t)(((u128)bytes * 1000000000ULL +
+                                      bandwidth - 1) / bandwidth);
+    *cursor_ns = max_u64(*cursor_ns, arrival_ns) + xfer;
+    return max_u64(media_completion_ns, *cursor_ns);
+}
+
+/* prefetch_model.cpp:22-50: k identical servers; a read issued at `now`
+ * takes the server that frees first and finishes one latency later. */
+void orc_media_servers(const uint64_t* now_ns, size_t n, uint32_t servers,
+                       uint64_t latency_ns, uint64_t* completion_ns)
+{
+    const uint32_t k = servers ? servers : 1;
+    uint64_t* heap = (uint64_t*)calloc(k, sizeof(uint64_t));
+    if (heap == NULL) {
+        return;
+    }
+    for (size_t i = 0; i < n; ++i) {
+        /* min over free-at times (all servers identical: ties are equal) */
+        uint32_t best = 0;
+        for (uint32_t j = 1; j < k; ++j) {
+            if (heap[j] < heap[best]) {
+                best = j;
+            }
+        }
+        const uint64_t start = max_u64(now_ns[i], heap[best]);
+        heap[best] = start + latency_ns;
+        completion_ns[i] = heap[best];
+    }
+    free(heap);
+}
+
+/* ---- thermal: thermal.cpp:172-193 (matrix), 127-160 (Cholesky), 242-311
+ * (backward-Euler step with constant segment power) -------------------- */
+int orc_thermal_dense_step(size_t n, const double* capacity,
+                           const double* boundary_g, const double* boundary_t,
+                           const double* static_power, size_t n_edges,
+                           const uint32_t* edge_a, const uint32_t* edge_b,
+                           const double* edge_g, double dt,
+                           const double* energy, double* temperature)
+{
+    double* a = (double*)calloc(n * n, sizeof(double));
+    double* l = (double*)calloc(n * n, sizeof(double));
+    double* rhs = (double*)malloc(n * sizeof(double));
+    double* y = (double*)malloc(n * sizeof(double));
+    int rc = 0;
+    if (!a || !l || !rhs || !y) {
+        rc = 2;
+        goto out;
+    }
+    for (size_t i = 0; i < n; ++i) {
+        a[i * n + i] = capacity[i] / dt + boundary_g[i];
+    }
+    for (size_t e = 0; e < n_edges; ++e) {
+        const size_t i = edge_a[e], j = edge_b[e];
+        a[i * n + i] += edge_g[e];
+        a[j * n + j] += edge_g[e];
+        a[i * n + j] -= edge_g[e];
+        a[j * n + i] -= edge_g[e];
+    }
+    for (size_t i = 0; i < n; ++i) {
+        for (size_t j = 0; j <= i; ++j) {
+            double sum = a[i * n + j];
+            for (size_t k = 0; k < j; ++k) {
+                sum -= l[i * n + k] * l[j * n + k];
+            }
+            if (i == j) {
+                if (!(sum > 0.0)) {
+                    rc = 1;
+                    goto out;
+                }
+                l[i * n + j] = sqrt(sum);
+            } else {
+                l[i * n + j] = sum / l[j * n + j];
+            }
+        }
+    }
+    for (size_t i = 0; i < n; ++i) {
+        rhs[i] = capacity[i] / dt * temperature[i] + static_power[i] +
+                 (energy ? energy[i] : 0.0) / dt +
+                 boundary_g[i] * boundary_t[i];
+    }
+    for (size_t i = 0; i < n; ++i) {
+        double sum = rhs[i];
+        for (size_t j = 0; j < i; ++j) {
+            sum -= l[i * n + j] * y[j];
+        }
+        y[i] = sum / l[i * n + i];
+    }
+    for (size_t i = n; i-- > 0;) {
+        double sum = y[i];
+        for (size_t j = i + 1; j < n; ++j) {
+            sum -= l[j * n + i] * temperature[j];
+        }
+        temperature[i] = sum / l[i * n + i];
+    }
+out:
+    free(a);
+    free(l);
+    free(rhs);
+    free(y);
+    return rc;
+}
+
+/* The same backward-Euler step on a regular grid, solved by Jacobi sweeps:
+ * T_i <- (C/dt T_i^old + P_i + sum_j g_ij T_j + gb_i tb) / (C/dt + sum_j g_ij
+ * + gb_i).  Converges because the system is strictly diagonally dominant. */
+int orc_thermal_grid_step(uint32_t nx, uint32_t ny, uint32_t nz,
+                          double capacity, double gx, double gy, double gz,
+                          double gb, double tb, double dt,
+                          const double* power, double* temperature,
+                          double tol, int max_sweeps)
+{
+    const size_t n = (size_t)nx * ny * nz;
+    double* old = (double*)malloc(n * sizeof(double));
+    double* cur = (double*)malloc(n * sizeof(double));
+    double* nxt = (double*)malloc(n * sizeof(double));
+    if (!old || !cur || !nxt) {
+        free(old);
+        free(cur);
+        free(nxt);
+        return -1;
+    }
+    memcpy(old, temperature, n * sizeof(double));
+    memcpy(cur, temperature, n * sizeof(double));
+    const double cdt = capacity / dt;
+    int sweep = 0;
+    for (; sweep < max_sweeps; ++sweep) {
+        double delta = 0.0;
+        for (uint32_t z = 0; z < nz; ++z) {
+            for (uint32_t y = 0; y < ny; ++y) {
+                for (uint32_t x = 0; x < nx; ++x) {
+                    const size_t i = ((size_t)z * ny + y) * nx + x;
+                    double num = cdt * old[i] + power[i];
+                    double den = cdt;
+                    if (x > 0) { num += gx * cur[i - 1]; den += gx; }
+                    if (x + 1 < nx) { num += gx * cur[i + 1]; den += gx; }
+                    if (y > 0) { num += gy * cur[i - nx]; den += gy; }
+                    if (y + 1 < ny) { num += gy * cur[i + nx]; den += gy; }
+                    if (z > 0) { num += gz * cur[i - (size_t)nx * ny]; den += gz; }
+                    if (z + 1 < nz) { num += gz * cur[i + (size_t)nx * ny]; den += gz; }
+                    if (z + 1 == nz) { num += gb * tb; den += gb; }
+                    nxt[i] = num / den;
+                    const double dd = fabs(nxt[i] - cur[i]);
+                    if (dd > delta) {
+                        delta = dd;
+                    }
+                }
+            }
+        }
+        double* t = cur;
+        cur = nxt;
+        nxt = t;
+        if (delta <= tol) {
+            ++sweep;
+            break;
+        }
+    }
+    memcpy(temperature, cur, n * sizeof(double));
+    free(old);
+    free(cur);
+    free(nxt);
+    return sweep;
+}
+
+/* reliability.py:17-23 */
+double orc_arrhenius(double temperature_k, double ea_ev, double tref_k)
+{
+    const double kb = 8.62e-5;
+    return exp(ea_ev / kb * (1.0 / tref_k - 1.0 / temperature_k));
+}

@@ -1,0 +1,293 @@
+/*
+ * hbf_oracle.h -- CPU restatement of HBFSim's per-access timing path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker the HIP engine is
+ * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load or call it.  The product path (hbfsim_amd/)
+ * never links, loads or falls back to it.
+ *
+ * Every function cites the reference file:line whose behaviour it restates
+ * (paths relative to the SlugLab/HBFSim tree).  Where the reference leaves a
+ * semantic open (the multi-resource engine), the restatement follows the
+ * frozen specification in the repository design notes, and the docstring says
+ * which reference special case it must reduce to.
+ *
+ * Pinning status (what checks each function; see tests/test_oracle_*.py):
+ *   fast_hash / hybrid_reference_sample  KAT (device_helper_abi_test.cpp:73-75)
+ *                                        + golden vectors from compiled cuh
+ *   fast_transfer_ns / fast_service_ns   KAT (device_helper_abi_test.cpp:79-81,
+ *                                        348-355) + golden vectors + closed form
+ *   find_range_index .. media_descriptor KAT (device_helper_abi_test.cpp:87-135,
+ *                                        371-446) + brute force + golden vectors
+ *   empirical_*                          KAT (device_helper_abi_test.cpp:137-225)
+ *                                        + golden vectors
+ *   range_table_*                        KAT (range_table_test.cpp) + invariants
+ *   stripe                               CWDP KAT (ucie_bank_layout_test.cpp:34-50)
+ *                                        + bijection invariants; other 23 orders:
+ *                                        invariants only (MQSim un-vendored)
+ *   engine_run (multi-resource)          reduces to fast_model_run and to the
+ *                                        Lindley recursion; brute-force event
+ *                                        simulation on tiny inputs
+ *   fast_model_run                       closed-form recurrence hbf_device.cu:895-910
+ *                                        and 796-881; hand-computed cases
+ *   pagebuf (K=2 lower-slot rule)        golden traces from compiled
+ *                                        device_coalescer.cpp
+ *   media_servers (k-server)             golden traces from the k-server rule
+ *   thermal_dense_step                   closed forms (thermal_tests.cpp:54-89)
+ *                                        + golden temperatures from compiled
+ *                                        thermal.cpp
+ *   arrhenius                            closed form + reliability test
+ *                                        assertion (test_system_models.py:12)
+ */
+#ifndef HBF_ORACLE_H
+#define HBF_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar helpers (hbf_device.cuh) --------------------------------- */
+uint64_t orc_fast_hash(uint64_t value);
+int orc_hybrid_reference_sample(uint64_t sequence, uint32_t warmup,
+                                uint64_t threshold, uint64_t key);
+uint64_t orc_sample_threshold(double rate);
+uint64_t orc_fast_transfer_ns(uint32_t bytes, uint64_t bandwidth);
+uint64_t orc_fast_service_ns(uint64_t base_ns, uint32_t bytes,
+                             uint64_t bandwidth);
+uint64_t orc_saturating_add(uint64_t a, uint64_t b);
+uint64_t orc_saturating_multiply(uint64_t a, uint32_t b);
+
+/* ---- range records (hbf_device.cuh:105-117) ------------------------- */
+typedef struct orc_range {
+    uint64_t base;
+    uint64_t length;
+    uint64_t file_offset;
+    uint32_t range_id;
+    uint32_t mode;
+    uint32_t permissions;
+    uint32_t cache_policy;
+    uint32_t stream_id;
+    uint32_t flags;
+    uint64_t page_bytes;
+    uint64_t reserved1;
+} orc_range;
+
+typedef struct orc_media {
+    uint64_t logical_address;
+    uint32_t bytes;
+    uint32_t valid;
+} orc_media;
+
+uint32_t orc_find_range_index(const orc_range* ranges, uint32_t count,
+                              uint64_t address);
+int orc_access_supported(const orc_range* range, uint64_t address,
+                         uint32_t bytes, uint32_t operation);
+int orc_range_overlaps(const orc_range* range, uint64_t address,
+                       uint32_t bytes);
+int orc_span_touches_any_range(const orc_range* ranges, uint32_t count,
+                               uint64_t address, uint32_t bytes);
+orc_media orc_media_descriptor(const orc_range* range, uint64_t address,
+                               uint32_t bytes, uint32_t operation);
+
+/* Classification of one access, following the resolver's order of checks
+ * (hbf_device.cu:1081-1165). */
+enum orc_status {
+    ORC_MODELED = 0,     /* timed by the engine */
+    ORC_BYPASS = 1,      /* outside every range: native address, no delay */
+    ORC_UNSUPPORTED = 2  /* straddles a range, crosses a page, no permission */
+};
+uint32_t orc_classify(const orc_range* ranges, uint32_t count,
+                      uint64_t address, uint64_t bytes, uint32_t operation,
+                      uint32_t* range_index);
+
+/* ---- empirical curve (hbf_device.cuh:959-1140) ----------------------- */
+uint64_t orc_ceiling_scaled_delta(uint64_t delta, uint32_t offset,
+                                  uint32_t span);
+uint64_t orc_empirical_cumulative_ns(const uint32_t* pages,
+                                     const uint64_t* cumulative,
+                                     uint32_t count, uint32_t run_pages);
+uint64_t orc_empirical_service_ns(const uint32_t* pages,
+                                  const uint64_t* cumulative, uint32_t count,
+                                  uint32_t run_pages);
+/* returns valid; writes packed state and run pages */
+int orc_update_empirical_burst(uint64_t previous, uint64_t page,
+                               uint32_t operation, uint64_t* packed,
+                               uint32_t* run_pages);
+typedef struct orc_empirical {
+    uint32_t flags;          /* 1 = enabled */
+    uint32_t point_count;    /* must be 6 */
+    uint32_t pages[6];
+    uint64_t cumulative_ns[6];
+    uint64_t program_latency_ns;
+} orc_empirical;
+int orc_empirical_control_valid(const orc_empirical* e);
+/* returns valid; writes service, packed state and run pages */
+int orc_empirical_request_service(const orc_empirical* e, uint64_t previous,
+                                  uint64_t page, uint32_t operation,
+                                  uint64_t* service_ns, uint64_t* packed,
+                                  uint32_t* run_pages);
+
+/* ---- host range registry (range_table.cpp:17-198) -------------------- */
+#define ORC_RANGE_CAPACITY 32768u
+typedef struct orc_range_table {
+    orc_range* records;      /* capacity ORC_RANGE_CAPACITY, sorted by base */
+    uint32_t count;
+    uint32_t next_range_id;
+    uint64_t next_file_offset;
+    uint64_t page_bytes;
+    uint64_t media_capacity;
+} orc_range_table;
+orc_range_table* orc_range_table_create(uint64_t page_bytes,
+                                        uint64_t media_capacity);
+void orc_range_table_destroy(orc_range_table* t);
+/* returns an hbfsim_error code: 0 ok, 1 invalid argument, 5 unsupported */
+int orc_range_table_add(orc_range_table* t, uint64_t base, uint64_t length,
+                        uint32_t mode, uint32_t permissions,
+                        uint32_t cache_policy, uint32_t stream_id);
+int orc_range_table_remove(orc_range_table* t, uint64_t base);
+/* 0 outside, 1 matched, 2 crosses boundary; *index set when not outside */
+int orc_range_table_lookup(const orc_range_table* t, uint64_t address,
+                           uint32_t bytes, uint32_t* index);
+
+/* ---- striping (profile.hpp:51-77; bank_layout.cpp:48-72) ------------- */
+/* axis ids: 0 channel, 1 way (chip), 2 die, 3 plane.  order[0] advances
+ * fastest.  sizes indexed by axis id.  coords indexed by axis id. */
+uint64_t orc_stripe(uint64_t page, const uint32_t order[4],
+                    const uint32_t sizes[4], uint32_t coords[4]);
+int orc_parse_scheme(const char* name, uint32_t order[4]);
+uint64_t orc_hbf_media_lpa(uint64_t q, uint32_t module, uint32_t channels);
+void orc_hbf_cold_read_bank(uint64_t lpa, uint32_t channels,
+                            uint32_t core_dies, uint32_t banks,
+                            uint32_t* channel, uint32_t* core_die,
+                            uint32_t* bank, uint32_t* chip);
+
+/* ---- multi-resource engine (frozen specification) ------------------- */
+enum orc_model {
+    ORC_MODEL_HBF = 0,             /* plane (max,+) + channel cursor */
+    ORC_MODEL_FAST_SCALAR = 1,     /* hbf_device.cu:883-958 single tail */
+    ORC_MODEL_FAST_EMPIRICAL = 2   /* hbf_device.cu:796-881 single tail */
+};
+
+typedef struct orc_engine_params {
+    uint32_t model;
+    uint32_t channels, ways, dies, planes;  /* geometry */
+    uint32_t order[4];                       /* fastest-first axis ids */
+    uint32_t page_shift;                     /* log2(page bytes) */
+    uint32_t page_buffers;                   /* K in {0,1,2} */
+    uint32_t plane_contention;               /* 1: planes serialise */
+    uint32_t transfer_page;                  /* 1: charge page bytes */
+    uint32_t program_every_write;            /* 1: tPROG on every write */
+    uint32_t hybrid;                         /* 1: count hybrid samples */
+    uint32_t hybrid_warmup;
+    uint64_t hybrid_threshold;
+    uint64_t read_ps, program_ps;            /* base latencies in ps */
+    uint64_t xfer_num, xfer_den;             /* xfer_ps =                  */
+    uint64_t xfer_quantum;                   /*   q * ceil(b*num/den)      */
+    orc_empirical empirical;                 /* MODEL_FAST_EMPIRICAL only */
+} orc_engine_params;
+
+typedef struct orc_engine_state {
+    uint64_t* plane_busy;     /* [planes_total] */
+    uint64_t* plane_tag;      /* [planes_total * 2]: page+1, 0 empty */
+    uint64_t* channel_cursor; /* [channels] (1 for fast models) */
+    uint64_t* plane_busy_total;
+    uint64_t* channel_busy_total;
+    uint64_t burst_state;     /* empirical packed burst state */
+    uint64_t modeled_sequence;/* modeled requests so far */
+} orc_engine_state;
+
+typedef struct orc_engine_report {
+    uint64_t records, modeled, bypass, unsupported;
+    uint64_t reads, writes, page_hits, programs, hybrid_sampled;
+    uint64_t makespan_ps;
+    uint64_t latency_sum_lo, latency_sum_hi;
+    uint64_t latency_max_ps;
+    uint64_t service_sum_ps;
+} orc_engine_report;
+
+typedef struct orc_record {
+    uint64_t addr, bytes, issue_ps, flags;
+} orc_record;
+
+/* Runs records in input order.  issue = base_ps + record.issue_ps.
+ * completion[i]: completion ps (bypass: issue; unsupported: UINT64_MAX).
+ * status may be NULL.  Report accumulates (caller zeroes it). */
+int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
+                   uint32_t range_count, const orc_record* records, size_t n,
+                   uint64_t base_ps, orc_engine_state* s, uint64_t* completion,
+                   uint8_t* status, orc_engine_report* report);
+/* Same, records split over `threads` OpenMP threads by plane/channel
+ * ownership (only for ORC_MODEL_HBF).  Bit-identical to orc_engine_run. */
+int orc_engine_run_parallel(const orc_engine_params* p,
+                            const orc_range* ranges, uint32_t range_count,
+                            const orc_record* records, size_t n,
+                            uint64_t base_ps, orc_engine_state* s,
+                            uint64_t* completion, uint8_t* status,
+                            orc_engine_report* report, int threads);
+
+/* ---- the reference's scalar fast model, verbatim recurrence ----------- */
+/* hbf_device.cu:883-958 with time_scale 1: for each request i (in order)
+ *   tail = max(tail, arrival) + xfer; target = max(arrival + base, tail)
+ * targets[i] written; returns fast_modeled_ns sum. */
+uint64_t orc_fast_model_scalar(const uint64_t* arrival_ns,
+                               const uint32_t* operation, const uint32_t* bytes,
+                               size_t n, uint64_t read_ns, uint64_t program_ns,
+                               uint64_t bandwidth, uint64_t* tail_ns,
+                               uint64_t* target_ns);
+
+/* ---- hbf_trace_timing fast loop (hbf_trace_timing.cpp:181-233) -------- */
+typedef struct orc_trace_event {
+    uint64_t logical_address, bytes;
+    uint32_t page_bytes, operation;
+} orc_trace_event;
+/* returns 0 ok, 64 invalid argument (bad event) */
+int orc_trace_timing_fast(const orc_trace_event* events, size_t n,
+                          uint64_t read_ns, uint64_t program_ns,
+                          uint64_t bandwidth, uint64_t profile_page_bytes,
+                          uint64_t capacity_bytes, uint64_t* submitted,
+                          uint64_t* service_ns, uint64_t* clock_ns);
+
+/* ---- MQSim adapter bandwidth cursor (mqsim_online.cpp:321-335) -------- */
+uint64_t orc_bandwidth_cursor(uint64_t* cursor_ns, uint64_t arrival_ns,
+                              uint64_t bytes, uint64_t bandwidth,
+                              uint64_t media_completion_ns);
+
+/* ---- page-buffer slot rule (device_coalescer.cpp:134-168) ------------- */
+/* Sequential accesses on one bank, each completing before the next.  K
+ * slots; hit when the page is cached; a miss fills the first empty slot,
+ * else the lowest slot.  hits[i] written. */
+void orc_pagebuf_sequence(const uint64_t* pages, size_t n, uint32_t slots,
+                          uint8_t* hits);
+
+/* ---- k-server busy-until (prefetch_model.cpp:22-50) ------------------ */
+void orc_media_servers(const uint64_t* now_ns, size_t n, uint32_t servers,
+                       uint64_t latency_ns, uint64_t* completion_ns);
+
+/* ---- thermal (thermal.cpp:127-311) ----------------------------------- */
+/* One backward-Euler step of the RC network with constant power:
+ * (C/dt + Gb + L) T' = C/dt T + Ps + E/dt + Gb Tb.  Dense Cholesky.
+ * edges: pairs (a,b) with conductance g.  Returns 0 ok, 1 not SPD. */
+int orc_thermal_dense_step(size_t n, const double* capacity,
+                           const double* boundary_g, const double* boundary_t,
+                           const double* static_power, size_t n_edges,
+                           const uint32_t* edge_a, const uint32_t* edge_b,
+                           const double* edge_g, double dt,
+                           const double* energy, double* temperature);
+/* Same step for a regular nx*ny*nz grid with 6-neighbour conductances gx,
+ * gy, gz, uniform capacity, boundary conductance gb to tb on the top layer
+ * (z = nz-1) only, power[n] watts; solved by Jacobi to |dT|<=tol or
+ * max_sweeps.  Returns sweeps used. */
+int orc_thermal_grid_step(uint32_t nx, uint32_t ny, uint32_t nz,
+                          double capacity, double gx, double gy, double gz,
+                          double gb, double tb, double dt,
+                          const double* power, double* temperature,
+                          double tol, int max_sweeps);
+double orc_arrhenius(double temperature_k, double ea_ev, double tref_k);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,272 @@
+// ref_driver.cpp -- TEST INFRASTRUCTURE ONLY.
+//
+// A thin extern "C" shim over the reference's own dependency-free sources,
+// compiled where they lie under the reference tree by oracle/Makefile's `ref`
+// target into oracle/_ref/libhbfref.so.  It is used to pin the CPU oracle and
+// to write golden vectors under tests/golden/; it is never part of the
+// product and never shipped.  Only the reference's headers are included; no
+// reference source is copied.
+#include "src/cuda_runtime/device/hbf_device.cuh"
+
+#include <hbfsim/eq3_thermal/thermal.hpp>
+#include <hbfsim/hybrid_model.hpp>
+#include <hbfsim/ucie/bank_layout.hpp>
+#include <hbfsim/ucie/device_coalescer.hpp>
+
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <string>
+#include <vector>
+
+#define REF_API extern "C" __attribute__((visibility("default")))
+
+using hbfsim::device::SharedRangeRecord;
+
+REF_API std::uint64_t ref_fast_hash(std::uint64_t v)
+{
+    return hbfsim::device::fast_hash(v);
+}
+
+REF_API int ref_hybrid_reference_sample(std::uint64_t seq, std::uint32_t warm,
+                                        std::uint64_t thr, std::uint64_t key)
+{
+    return hbfsim::device::hybrid_reference_sample(seq, warm, thr, key);
+}
+
+REF_API std::uint64_t ref_fast_transfer_ns(std::uint32_t bytes,
+                                           std::uint64_t bw)
+{
+    return hbfsim::device::fast_transfer_ns(bytes, bw);
+}
+
+REF_API std::uint64_t ref_fast_service_ns(std::uint64_t base,
+                                          std::uint32_t bytes,
+                                          std::uint64_t bw)
+{
+    return hbfsim::device::fast_service_ns(base, bytes, bw);
+}
+
+// calibrator.cpp:33-65 (host mirror)
+REF_API std::uint64_t ref_host_fast_service_ns(std::uint64_t read_ns,
+                                               std::uint64_t program_ns,
+                                               std::uint64_t bw,
+                                               std::uint32_t op,
+                                               std::uint32_t bytes)
+{
+    const hbfsim::FastModelProfile profile{read_ns, program_ns, bw};
+    const hbfsim::AccessClass access{
+        op ? hbfsim::RequestOperation::Write : hbfsim::RequestOperation::Read,
+        bytes, 0, 0};
+    return hbfsim::fast_service_ns(profile, access);
+}
+
+// Range records are passed as the 64-byte SharedRangeRecord layout.
+REF_API std::uint32_t ref_find_range_index(const SharedRangeRecord* r,
+                                           std::uint32_t count,
+                                           std::uint64_t addr)
+{
+    return hbfsim::device::find_range_index(r, count, addr);
+}
+
+REF_API int ref_access_supported(const SharedRangeRecord* r,
+                                 std::uint64_t addr, std::uint32_t bytes,
+                                 std::uint32_t op)
+{
+    return hbfsim::device::access_supported(*r, addr, bytes, op);
+}
+
+REF_API int ref_range_overlaps(const SharedRangeRecord* r, std::uint64_t addr,
+                               std::uint32_t bytes)
+{
+    return hbfsim::device::range_overlaps(*r, addr, bytes);
+}
+
+REF_API int ref_span_touches_any_range(const SharedRangeRecord* r,
+                                       std::uint32_t count,
+                                       std::uint64_t addr,
+                                       std::uint32_t bytes)
+{
+    return hbfsim::device::span_touches_any_range(r, count, addr, bytes);
+}
+
+REF_API int ref_media_descriptor(const SharedRangeRecord* r,
+                                 std::uint64_t addr, std::uint32_t bytes,
+                                 std::uint32_t op, std::uint64_t* logical,
+                                 std::uint32_t* out_bytes)
+{
+    const auto m = hbfsim::device::media_descriptor(*r, addr, bytes, op);
+    *logical = m.logical_address;
+    *out_bytes = m.bytes;
+    return m.valid;
+}
+
+REF_API std::uint64_t ref_empirical_cumulative_ns(const std::uint32_t* pages,
+                                                  const std::uint64_t* cum,
+                                                  std::uint32_t count,
+                                                  std::uint32_t run)
+{
+    return hbfsim::device::empirical_cumulative_ns(pages, cum, count, run);
+}
+
+REF_API std::uint64_t ref_empirical_service_ns(const std::uint32_t* pages,
+                                               const std::uint64_t* cum,
+                                               std::uint32_t count,
+                                               std::uint32_t run)
+{
+    return hbfsim::device::empirical_service_ns(pages, cum, count, run);
+}
+
+REF_API int ref_update_empirical_burst(std::uint64_t prev, std::uint64_t page,
+                                       std::uint32_t op, std::uint64_t* packed,
+                                       std::uint32_t* run)
+{
+    const auto u = hbfsim::device::update_empirical_burst(prev, page, op);
+    *packed = u.packed;
+    *run = u.run_pages;
+    return u.valid;
+}
+
+REF_API int ref_empirical_request_service(const std::uint32_t* pages,
+                                          const std::uint64_t* cum,
+                                          std::uint64_t program_ns,
+                                          std::uint64_t prev,
+                                          std::uint64_t page, std::uint32_t op,
+                                          std::uint64_t* service,
+                                          std::uint64_t* packed,
+                                          std::uint32_t* run)
+{
+    hbfsim::device::SharedControlHeader h{};
+    h.empirical_flags = 1;
+    h.empirical_point_count = 6;
+    h.program_latency_ns = program_ns;
+    for (int i = 0; i < 6; ++i) {
+        h.empirical_breakpoint_pages[i] = pages[i];
+        h.empirical_cumulative_ns[i] = cum[i];
+    }
+    const auto r = hbfsim::device::empirical_request_service(h, prev, page, op);
+    *service = r.service_ns;
+    *packed = r.packed_state;
+    *run = r.run_pages;
+    return r.valid;
+}
+
+// bank_layout.cpp:48-72 (scenario fixture layouts allowed)
+REF_API int ref_cold_read_bank(std::uint64_t lpa, std::uint32_t channels,
+                               std::uint32_t ncdu, std::uint32_t banks,
+                               std::uint32_t* channel, std::uint32_t* die,
+                               std::uint32_t* bank, std::uint32_t* chip)
+{
+    try {
+        const hbfsim::ucie::HbfBankLayout layout{channels, ncdu, banks, true};
+        const auto b = hbfsim::ucie::hbf_cold_read_bank(lpa, layout);
+        *channel = b.host_channel;
+        *die = b.core_die;
+        *bank = b.bank;
+        *chip = b.native_chip;
+        return 1;
+    } catch (const std::exception&) {
+        return 0;
+    }
+}
+
+REF_API int ref_hbf_media_lpa(std::uint64_t q, std::uint32_t module,
+                              std::uint32_t channels, std::uint64_t* lpa)
+{
+    try {
+        const hbfsim::ucie::HbfBankLayout layout{channels, 1, 16, true};
+        *lpa = hbfsim::ucie::hbf_media_lpa(q, module, layout);
+        return 1;
+    } catch (const std::exception&) {
+        return 0;
+    }
+}
+
+// device_coalescer.cpp:61-254 driven one access at a time on one bank with
+// the buffer cache on: arrive; a miss is submitted, completed and consumed
+// before the next access arrives.  hits[i] = buffer_hit of access i.
+REF_API int ref_pagebuf_sequence(const std::uint64_t* pages, std::size_t n,
+                                 std::uint8_t* hits)
+{
+    try {
+        hbfsim::ucie::DeviceReadCoalescer coal(4, 8, true, 1, 1);
+        for (std::size_t i = 0; i < n; ++i) {
+            const hbfsim::ucie::DevicePageKey key{1, 1, 0, 0, 7, pages[i], 0, 0};
+            const auto waiter = static_cast<std::uint64_t>(i + 1);
+            const auto a = coal.arrive(waiter, key);
+            if (!a) {
+                return 0;
+            }
+            hits[i] = a->buffer_hit ? 1 : 0;
+            if (!a->buffer_hit) {
+                const auto starts = coal.take_submittable();
+                if (starts.size() != 1) {
+                    return 0;
+                }
+                (void)coal.complete(starts[0].token, true);
+            }
+            coal.consume(waiter);
+        }
+        return 1;
+    } catch (const std::exception&) {
+        return 0;
+    }
+}
+
+// thermal.cpp: build a model from flat arrays and advance once by dt with a
+// single activity spanning [0, dt] carrying energy[i] joules on node i.
+REF_API int ref_thermal_step(std::size_t n, const double* capacity,
+                             const double* initial, const double* static_power,
+                             const double* boundary_g, const double* boundary_t,
+                             std::size_t n_edges, const std::uint32_t* ea,
+                             const std::uint32_t* eb, const double* eg,
+                             const double* energy, std::uint32_t steps,
+                             double dt, double* out)
+{
+    using namespace hbfsim::eq3_thermal;
+    try {
+        ThermalModelConfig config;
+        for (std::size_t i = 0; i < n; ++i) {
+            ThermalNode node;
+            node.id = "n" + std::to_string(i);
+            node.physical_type = PhysicalType::Hbf;
+            node.logical_role = LogicalRole::CapacityMemory;
+            node.heat_capacity_j_per_k = capacity[i];
+            node.initial_temperature_k = initial[i];
+            node.static_power_w = static_power[i];
+            node.boundary_conductance_w_per_k = boundary_g[i];
+            node.boundary_temperature_k = boundary_t[i];
+            config.nodes.push_back(node);
+        }
+        for (std::size_t e = 0; e < n_edges; ++e) {
+            config.edges.push_back({ea[e], eb[e], eg[e],
+                                    ConductanceKind::IntraComponent});
+        }
+        ThermalModel model(config);
+        for (std::uint32_t s = 0; s < steps; ++s) {
+            PhysicalActivity a;
+            a.activity_id = s + 1;
+            a.request_id = "step" + std::to_string(s);
+            a.kind = ActivityKind::Read;
+            a.start_time_s = dt * s;
+            a.end_time_s = dt * (s + 1);
+            a.completion_time_s = a.end_time_s;
+            bool any = false;
+            for (std::size_t i = 0; i < n; ++i) {
+                if (energy != nullptr && energy[i] > 0.0) {
+                    a.node_energy.push_back({i, energy[i]});
+                    any = true;
+                }
+            }
+            if (any) {
+                model.add_activity(a);
+            }
+            model.advance_to(dt * (s + 1));
+        }
+        const auto& t = model.temperatures_k();
+        std::memcpy(out, t.data(), n * sizeof(double));
+        return 1;
+    } catch (const std::exception&) {
+        return 0;
+    }
+}

@@ -1,0 +1,266 @@
+"""Test-side ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+Test infrastructure only: the oracle is the checker the HIP engine is
+compared against, never part of the product path.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import math
+import pathlib
+import subprocess
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+ORACLE_DIR = ROOT / "oracle"
+LIB = ORACLE_DIR / "liboracle.so"
+REF_LIB = ORACLE_DIR / "_ref" / "libhbfref.so"
+
+_P = ctypes.c_void_p
+_U32 = ctypes.c_uint32
+_U64 = ctypes.c_uint64
+
+
+class OrcRange(ctypes.Structure):
+    _fields_ = [("base", _U64), ("length", _U64), ("file_offset", _U64), ("range_id", _U32),
+                ("mode", _U32), ("permissions", _U32), ("cache_policy", _U32),
+                ("stream_id", _U32), ("flags", _U32), ("page_bytes", _U64),
+                ("reserved1", _U64)]
+
+
+class OrcMedia(ctypes.Structure):
+    _fields_ = [("logical_address", _U64), ("bytes", _U32), ("valid", _U32)]
+
+
+class OrcEmpirical(ctypes.Structure):
+    _fields_ = [("flags", _U32), ("point_count", _U32), ("pages", _U32 * 6),
+                ("cumulative_ns", _U64 * 6), ("program_latency_ns", _U64)]
+
+
+class OrcParams(ctypes.Structure):
+    _fields_ = [("model", _U32), ("channels", _U32), ("ways", _U32), ("dies", _U32),
+                ("planes", _U32), ("order", _U32 * 4), ("page_shift", _U32),
+                ("page_buffers", _U32), ("plane_contention", _U32), ("transfer_page", _U32),
+                ("program_every_write", _U32), ("hybrid", _U32), ("hybrid_warmup", _U32),
+                ("hybrid_threshold", _U64), ("read_ps", _U64), ("program_ps", _U64),
+                ("xfer_num", _U64), ("xfer_den", _U64), ("xfer_quantum", _U64),
+                ("empirical", OrcEmpirical)]
+
+
+class OrcState(ctypes.Structure):
+    _fields_ = [("plane_busy", _P), ("plane_tag", _P), ("channel_cursor", _P),
+                ("plane_busy_total", _P), ("channel_busy_total", _P), ("burst_state", _U64),
+                ("modeled_sequence", _U64)]
+
+
+REPORT_FIELDS = ("records", "modeled", "bypass", "unsupported", "reads", "writes", "page_hits",
+                 "programs", "hybrid_sampled", "makespan_ps", "latency_sum_lo",
+                 "latency_sum_hi", "latency_max_ps", "service_sum_ps")
+
+
+class OrcReport(ctypes.Structure):
+    _fields_ = [(name, _U64) for name in REPORT_FIELDS]
+
+    def as_dict(self) -> dict:
+        d = {name: int(getattr(self, name)) for name in REPORT_FIELDS}
+        d["latency_sum_ps"] = d["latency_sum_lo"] | (d["latency_sum_hi"] << 64)
+        return d
+
+
+class OrcTraceEvent(ctypes.Structure):
+    _fields_ = [("logical_address", _U64), ("bytes", _U64), ("page_bytes", _U32),
+                ("operation", _U32)]
+
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(ORACLE_DIR)], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = ctypes.CDLL(str(LIB))
+        sig = {
+            "orc_fast_hash": (_U64, [_U64]),
+            "orc_hybrid_reference_sample": (ctypes.c_int, [_U64, _U32, _U64, _U64]),
+            "orc_sample_threshold": (_U64, [ctypes.c_double]),
+            "orc_fast_transfer_ns": (_U64, [_U32, _U64]),
+            "orc_fast_service_ns": (_U64, [_U64, _U32, _U64]),
+            "orc_saturating_add": (_U64, [_U64, _U64]),
+            "orc_saturating_multiply": (_U64, [_U64, _U32]),
+            "orc_find_range_index": (_U32, [_P, _U32, _U64]),
+            "orc_access_supported": (ctypes.c_int, [_P, _U64, _U32, _U32]),
+            "orc_range_overlaps": (ctypes.c_int, [_P, _U64, _U32]),
+            "orc_span_touches_any_range": (ctypes.c_int, [_P, _U32, _U64, _U32]),
+            "orc_media_descriptor": (OrcMedia, [_P, _U64, _U32, _U32]),
+            "orc_classify": (_U32, [_P, _U32, _U64, _U64, _U32, _P]),
+            "orc_ceiling_scaled_delta": (_U64, [_U64, _U32, _U32]),
+            "orc_empirical_cumulative_ns": (_U64, [_P, _P, _U32, _U32]),
+            "orc_empirical_service_ns": (_U64, [_P, _P, _U32, _U32]),
+            "orc_update_empirical_burst": (ctypes.c_int, [_U64, _U64, _U32, _P, _P]),
+            "orc_empirical_control_valid": (ctypes.c_int, [_P]),
+            "orc_empirical_request_service": (ctypes.c_int, [_P, _U64, _U64, _U32, _P, _P, _P]),
+            "orc_range_table_create": (_P, [_U64, _U64]),
+            "orc_range_table_destroy": (None, [_P]),
+            "orc_range_table_add": (ctypes.c_int, [_P, _U64, _U64, _U32, _U32, _U32, _U32]),
+            "orc_range_table_remove": (ctypes.c_int, [_P, _U64]),
+            "orc_range_table_lookup": (ctypes.c_int, [_P, _U64, _U32, _P]),
+            "orc_stripe": (_U64, [_U64, _P, _P, _P]),
+            "orc_parse_scheme": (ctypes.c_int, [ctypes.c_char_p, _P]),
+            "orc_hbf_media_lpa": (_U64, [_U64, _U32, _U32]),
+            "orc_hbf_cold_read_bank": (None, [_U64, _U32, _U32, _U32, _P, _P, _P, _P]),
+            "orc_engine_run": (ctypes.c_int, [_P, _P, _U32, _P, ctypes.c_size_t, _U64, _P, _P,
+                                              _P, _P]),
+            "orc_engine_run_parallel": (ctypes.c_int, [_P, _P, _U32, _P, ctypes.c_size_t, _U64,
+                                                       _P, _P, _P, _P, ctypes.c_int]),
+            "orc_fast_model_scalar": (_U64, [_P, _P, _P, ctypes.c_size_t, _U64, _U64, _U64, _P,
+                                             _P]),
+            "orc_trace_timing_fast": (ctypes.c_int, [_P, ctypes.c_size_t, _U64, _U64, _U64, _U64,
+                                                     _U64, _P, _P, _P]),
+            "orc_bandwidth_cursor": (_U64, [_P, _U64, _U64, _U64, _U64]),
+            "orc_pagebuf_sequence": (None, [_P, ctypes.c_size_t, _U32, _P]),
+            "orc_media_servers": (None, [_P, ctypes.c_size_t, _U32, _U64, _P]),
+            "orc_thermal_dense_step": (ctypes.c_int, [ctypes.c_size_t, _P, _P, _P, _P,
+                                                      ctypes.c_size_t, _P, _P, _P,
+                                                      ctypes.c_double, _P, _P]),
+            "orc_thermal_grid_step": (ctypes.c_int, [_U32, _U32, _U32, ctypes.c_double,
+                                                     ctypes.c_double, ctypes.c_double,
+                                                     ctypes.c_double, ctypes.c_double,
+                                                     ctypes.c_double, ctypes.c_double, _P, _P,
+                                                     ctypes.c_double, ctypes.c_int]),
+            "orc_arrhenius": (ctypes.c_double, [ctypes.c_double, ctypes.c_double,
+                                                ctypes.c_double]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def ref_lib() -> ctypes.CDLL | None:
+    """The compiled reference shim, when it was built in this container."""
+    if not REF_LIB.exists():
+        return None
+    return ctypes.CDLL(str(REF_LIB))
+
+
+def addr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ---------------------------------------------------------------------------
+# engine parameters, derived independently of the product's C++ code
+
+
+def load_profile(path) -> dict:
+    return json.loads(pathlib.Path(path).read_text())
+
+
+def engine_params(profile: dict, page_buffers=1, plane_contention=1, transfer_page=0,
+                  program_every_write=0, flat_geometry=0, ways=1, xfer_quantum_ps=1,
+                  channel_bandwidth_bytes_per_s=0, hybrid=False, model=0) -> OrcParams:
+    p = OrcParams()
+    p.model = model
+    if flat_geometry:
+        p.channels = p.ways = p.dies = p.planes = 1
+    else:
+        p.channels = profile["channels"]
+        p.ways = ways
+        p.dies = profile["dies_per_channel"]
+        p.planes = profile["planes_per_die"]
+    scheme = profile.get("plane_allocation_scheme", "CWDP")
+    axis = {"C": 0, "W": 1, "D": 2, "P": 3}
+    for i, ch in enumerate(scheme):
+        p.order[i] = axis[ch]
+    p.page_shift = int(math.log2(profile["page_bytes"]))
+    p.page_buffers = page_buffers
+    p.plane_contention = plane_contention
+    p.transfer_page = transfer_page
+    p.program_every_write = program_every_write
+    p.hybrid = 1 if hybrid else 0
+    p.hybrid_warmup = profile["reference_warmup_requests"]
+    p.hybrid_threshold = lib().orc_sample_threshold(profile["reference_sample_rate"])
+    p.read_ps = profile["read_latency_ns"] * 1000
+    p.program_ps = profile["program_latency_ns"] * 1000
+    q = xfer_quantum_ps or 1
+    if channel_bandwidth_bytes_per_s:
+        num, den = 10**12, channel_bandwidth_bytes_per_s * q
+    else:
+        num, den = 10**12 * p.channels, profile["aggregate_bandwidth_bytes_per_s"] * q
+    g = math.gcd(num, den)
+    p.xfer_num, p.xfer_den, p.xfer_quantum = num // g, den // g, q
+    if "empirical_vmem" in profile:
+        e = profile["empirical_vmem"]
+        p.empirical.flags = 1
+        p.empirical.point_count = 6
+        for i, pt in enumerate(e["read_curve"]):
+            p.empirical.pages[i] = pt["pages"]
+            p.empirical.cumulative_ns[i] = pt["cumulative_ns"]
+        p.empirical.program_latency_ns = profile["program_latency_ns"]
+    return p
+
+
+class OracleState:
+    def __init__(self, params: OrcParams):
+        planes = params.channels * params.ways * params.dies * params.planes
+        self.plane_busy = np.zeros(planes, np.uint64)
+        self.plane_tag = np.zeros(planes * 2, np.uint64)
+        self.channel_cursor = np.zeros(params.channels, np.uint64)
+        self.plane_busy_total = np.zeros(planes, np.uint64)
+        self.channel_busy_total = np.zeros(params.channels, np.uint64)
+        self.s = OrcState(addr(self.plane_busy), addr(self.plane_tag),
+                          addr(self.channel_cursor), addr(self.plane_busy_total),
+                          addr(self.channel_busy_total), 0, 0)
+
+
+def range_table(ranges, page_bytes: int, capacity: int) -> list[OrcRange]:
+    """Registers (base, length, permissions) in order through the oracle's
+    restatement of RangeTable::add; returns the sorted records."""
+    L = lib()
+    t = L.orc_range_table_create(page_bytes, capacity)
+    try:
+        for base, length, perms in ranges:
+            rc = L.orc_range_table_add(t, base, length, 1, perms, 0, 0)
+            if rc != 0:
+                raise ValueError(f"oracle range add failed: {rc}")
+        class _T(ctypes.Structure):
+            _fields_ = [("records", ctypes.POINTER(OrcRange)), ("count", _U32),
+                        ("next_range_id", _U32), ("next_file_offset", _U64),
+                        ("page_bytes", _U64), ("media_capacity", _U64)]
+        tt = ctypes.cast(t, ctypes.POINTER(_T)).contents
+        out = (OrcRange * max(1, tt.count))()
+        ctypes.memmove(out, tt.records, ctypes.sizeof(OrcRange) * tt.count)
+        return out, tt.count
+    finally:
+        L.orc_range_table_destroy(t)
+
+
+def run(params: OrcParams, ranges, count: int, records: np.ndarray, base_ps: int = 0,
+        state: OracleState | None = None, threads: int = 1):
+    rec = np.ascontiguousarray(records, dtype=np.uint64).reshape(-1, 4)
+    n = rec.shape[0]
+    if state is None:
+        state = OracleState(params)
+    comp = np.zeros(n, np.uint64)
+    st = np.zeros(n, np.uint8)
+    rep = OrcReport()
+    if threads > 1:
+        rc = lib().orc_engine_run_parallel(ctypes.byref(params), ranges, count, addr(rec), n,
+                                           base_ps, ctypes.byref(state.s), addr(comp), addr(st),
+                                           ctypes.byref(rep), threads)
+    else:
+        rc = lib().orc_engine_run(ctypes.byref(params), ranges, count, addr(rec), n, base_ps,
+                                  ctypes.byref(state.s), addr(comp), addr(st),
+                                  ctypes.byref(rep))
+    if rc != 0:
+        raise RuntimeError(f"oracle engine failed: {rc}")
+    return comp, st, rep.as_dict(), state

@@ -1,0 +1,90 @@
+"""Runs one access stream through the HIP engine (C ABI) and the CPU oracle
+and compares every output bit for bit."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle_py
+from hbfsim_amd import engine as eng
+
+OPTION_KEYS = ("page_buffers", "plane_contention", "transfer_page", "program_every_write",
+               "flat_geometry", "ways", "xfer_quantum_ps", "channel_bandwidth_bytes_per_s")
+
+
+def to_device(records: np.ndarray):
+    import torch
+    rec = np.ascontiguousarray(records, dtype=np.uint64).reshape(-1, 4)
+    return torch.from_numpy(rec.view(np.int64)).cuda()
+
+
+class Pair:
+    """An engine context and an oracle state fed the same ranges and runs."""
+
+    def __init__(self, profile_path, ranges, mode="fast", tile_records=None, **options):
+        import torch  # noqa: F401  (device memory owner)
+        self.profile = oracle_py.load_profile(profile_path)
+        self.engine = eng.Engine(str(profile_path), mode=mode)
+        for base, length, perms in ranges:
+            self.engine.register(base, length, perms)
+        opts = {k: v for k, v in options.items() if k in OPTION_KEYS}
+        if tile_records is not None:
+            opts["tile_records"] = tile_records
+        if opts:
+            self.engine.set_options(**opts)
+        self.params = oracle_py.engine_params(self.profile, hybrid=(mode == "hybrid"),
+                                              **{k: v for k, v in options.items()
+                                                 if k in OPTION_KEYS})
+        self.ranges, self.count = oracle_py.range_table(ranges, self.profile["page_bytes"],
+                                                        self.profile["capacity_bytes"])
+        self.ostate = oracle_py.OracleState(self.params)
+
+    def run(self, records: np.ndarray, base_ps: int = 0):
+        import torch
+        rec = np.ascontiguousarray(records, dtype=np.uint64).reshape(-1, 4)
+        n = rec.shape[0]
+        d_rec = to_device(rec)
+        d_comp = torch.zeros(max(n, 1), dtype=torch.int64, device="cuda")
+        d_st = torch.zeros(max(n, 1), dtype=torch.uint8, device="cuda")
+        grep = self.engine.run(d_rec, d_comp, d_st, base_ps=base_ps)
+        torch.cuda.synchronize()
+        gcomp = d_comp.cpu().numpy().view(np.uint64)[:n]
+        gst = d_st.cpu().numpy()[:n]
+        ocomp, ost, orep, _ = oracle_py.run(self.params, self.ranges, self.count, rec, base_ps,
+                                            self.ostate)
+        return (gcomp, gst, grep), (ocomp, ost, orep)
+
+    def check_state(self):
+        gp, gc = self.engine.busy_totals()
+        np.testing.assert_array_equal(gp, self.ostate.plane_busy_total, "plane busy totals")
+        np.testing.assert_array_equal(gc, self.ostate.channel_busy_total, "channel busy totals")
+        st = self.engine.state()
+        np.testing.assert_array_equal(st["channel_cursor"], self.ostate.channel_cursor,
+                                      "channel cursors")
+        if self.params.plane_contention:
+            np.testing.assert_array_equal(st["plane_busy"], self.ostate.plane_busy,
+                                          "plane busy-until")
+        if self.params.page_buffers:
+            k = self.params.page_buffers
+            g = st["plane_tags"].reshape(-1, 2)[:, :k]
+            o = self.ostate.plane_tag.reshape(-1, 2)[:, :k]
+            np.testing.assert_array_equal(g, o, "page-register tags")
+        assert st["sequence"] == self.ostate.s.modeled_sequence
+
+    def close(self):
+        self.engine.close()
+
+
+def assert_same(gpu, cpu, what=""):
+    gcomp, gst, grep = gpu
+    ocomp, ost, orep = cpu
+    if not np.array_equal(gcomp, ocomp):
+        bad = np.nonzero(gcomp != ocomp)[0]
+        i = int(bad[0])
+        raise AssertionError(f"{what}: {bad.size} completion mismatches; first at {i}: "
+                             f"gpu {int(gcomp[i])} oracle {int(ocomp[i])}")
+    if not np.array_equal(gst, ost):
+        bad = np.nonzero(gst != ost)[0]
+        i = int(bad[0])
+        raise AssertionError(f"{what}: {bad.size} status mismatches; first at {i}: "
+                             f"gpu {int(gst[i])} oracle {int(ost[i])}")
+    assert grep == orep, f"{what}: report differs\n gpu {grep}\n cpu {orep}"
