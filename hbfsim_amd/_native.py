@@ -86,6 +86,13 @@ class EngineOptions(ctypes.Structure):
                 ("tile_records", ctypes.c_uint32), ("reserved0", ctypes.c_uint32)]
 
 
+class Range(ctypes.Structure):
+    _fields_ = [("base", ctypes.c_uint64), ("length", ctypes.c_uint64),
+                ("file_offset", ctypes.c_uint64), ("range_id", ctypes.c_uint32),
+                ("mode", ctypes.c_uint32), ("permissions", ctypes.c_uint32),
+                ("stream_id", ctypes.c_uint32), ("page_bytes", ctypes.c_uint64)]
+
+
 REPORT_FIELDS = ("records", "modeled", "bypass", "unsupported", "reads", "writes", "page_hits",
                  "programs", "hybrid_sampled", "makespan_ps", "latency_sum_lo",
                  "latency_sum_hi", "latency_max_ps", "service_sum_ps")
@@ -136,6 +143,8 @@ SIGNATURES = {
     "hbfsim_amd_set_state": (_INT, [_P, _P, _P, _P, _U64, _U64]),
     "hbfsim_amd_reset": (_INT, [_P]),
     "hbfsim_amd_last_kernel_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float), _INT]),
+    "hbfsim_amd_lookup_range": (_INT, [_P, _U64, _U32, ctypes.POINTER(_U32),
+                                        ctypes.POINTER(Range), ctypes.POINTER(_U32)]),
     "hbfsim_amd_validate_profile": (_INT, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
 }
 

@@ -733,6 +733,52 @@ HBF_API int hbfsim_amd_last_kernel_ms(const hbfsim_context* c, float* ms, int ma
     return hbfamd::engine_last_kernel_ms(c->eng, ms, max_kernels);
 }
 
+HBF_API int hbfsim_amd_lookup_range(hbfsim_context* c, uint64_t address, uint32_t bytes,
+                                    uint32_t* kind, hbfsim_amd_range* out, uint32_t* count)
+{
+    if (kind != nullptr) {
+        *kind = 0;
+    }
+    if (c == nullptr || kind == nullptr) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(c->mu);
+    if (count != nullptr) {
+        *count = static_cast<uint32_t>(c->ranges.size());
+    }
+    if (bytes == 0 || c->ranges.empty()) {
+        return HBFSIM_OK;
+    }
+    std::size_t lo = 0, hi = c->ranges.size();  // upper_bound on base
+    while (lo < hi) {
+        const std::size_t mid = (lo + hi) / 2;
+        if (address < c->ranges[mid].base) {
+            hi = mid;
+        } else {
+            lo = mid + 1;
+        }
+    }
+    if (lo == 0) {
+        return HBFSIM_OK;
+    }
+    const hbfamd::range_rec& r = c->ranges[lo - 1];
+    if (address < r.base || address - r.base >= r.length) {
+        return HBFSIM_OK;
+    }
+    if (out != nullptr) {
+        out->base = r.base;
+        out->length = r.length;
+        out->file_offset = r.file_offset;
+        out->range_id = r.range_id;
+        out->mode = r.mode;
+        out->permissions = r.permissions;
+        out->stream_id = r.stream_id;
+        out->page_bytes = r.page_bytes;
+    }
+    *kind = (bytes > UINT64_MAX - address || address + bytes > r.base + r.length) ? 2u : 1u;
+    return HBFSIM_OK;
+}
+
 HBF_API int hbfsim_amd_validate_profile(const char* path, char* error, size_t error_bytes)
 {
     if (error != nullptr && error_bytes != 0) {

@@ -301,6 +301,26 @@ int hbfsim_amd_reset(hbfsim_context* context);
 int hbfsim_amd_last_kernel_ms(const hbfsim_context* context, float* ms,
                               int max_kernels);
 
+/* One registered range as the registry holds it (SharedRangeRecord,
+ * hbf_device.cuh:105-117). */
+typedef struct hbfsim_amd_range {
+    uint64_t base;
+    uint64_t length;
+    uint64_t file_offset;
+    uint32_t range_id;
+    uint32_t mode;
+    uint32_t permissions;
+    uint32_t stream_id;
+    uint64_t page_bytes;
+} hbfsim_amd_range;
+
+/* RangeTable::lookup (range_table.cpp:173-198): *kind = 0 outside every
+ * range, 1 matched, 2 crosses the range end; `out` filled unless outside.
+ * Also returns the number of registered ranges in *count (may be NULL). */
+int hbfsim_amd_lookup_range(hbfsim_context* context, uint64_t address,
+                            uint32_t bytes, uint32_t* kind,
+                            hbfsim_amd_range* out, uint32_t* count);
+
 /* Profile validation with the reference's rules and messages
  * (src/profile/profile.cpp:238-468).  Returns HBFSIM_OK or
  * HBFSIM_INVALID_ARGUMENT with the reference's message in `error`. */

@@ -1,0 +1,216 @@
+"""Pins the oracle's multi-resource engine with formulas independent of its
+sequential loop:
+
+* per resource, busy-until after n accesses equals the Lindley closed form
+  S_n + max(b_0, max_k (issue_k - S_{k-1})) with S the running service sum;
+* page-register hits with one register equal "previous access on the same
+  plane was the same page";
+* the HBF model degenerated to one channel with unserialised latency is the
+  reference's single-tail recurrence (hbf_device.cu:895-910);
+* sequential, OpenMP and split runs agree; busy totals conserve work;
+* striping is a bijection for all 24 allocation orders and CWDP agrees with
+  bank_layout.cpp:59-72.
+"""
+from __future__ import annotations
+
+import ctypes
+import itertools
+import json
+
+import numpy as np
+import pytest
+
+import oracle_py
+from hbfsim_amd import workloads
+
+C0 = workloads.PROFILES / "c0.json"
+
+
+def lindley(issue: np.ndarray, svc: np.ndarray, b0: int = 0) -> np.ndarray:
+    """Busy-until after each access of one FIFO resource, closed form."""
+    issue = issue.astype(object)
+    svc = svc.astype(object)
+    out = np.empty(len(issue), dtype=object)
+    s_prev = 0
+    best = b0
+    for k in range(len(issue)):  # exact big-int arithmetic, O(n)
+        best = max(best, issue[k] - s_prev)
+        s_prev += svc[k]
+        out[k] = s_prev + best
+    return out
+
+
+def independent_engine(profile: dict, records: np.ndarray, page_buffers=1, contention=True):
+    """Re-derives completions for an all-modeled single-range stream with
+    numpy grouping and the Lindley form (no shared code with the oracle)."""
+    page = profile["page_bytes"]
+    C, D, P = profile["channels"], profile["dies_per_channel"], profile["planes_per_die"]
+    media = records[:, 0] - records[0, 0] + np.uint64(0)  # file offset 0, one range
+    media = records[:, 0] - np.uint64(workloads.RANGE_BASE)
+    pg = (media // np.uint64(page)).astype(np.int64)
+    ch = pg % C
+    die = (pg // C) % D
+    pl = (pg // (C * D)) % P
+    plane = (ch * D + die) * P + pl
+    issue = records[:, 2].astype(np.int64)
+    nbytes = records[:, 1].astype(np.int64)
+    xfer = -(-nbytes * 10**12 * C // profile["aggregate_bandwidth_bytes_per_s"])
+    op = records[:, 3].astype(np.int64)
+    off = (media % np.uint64(page)).astype(np.int64)
+    n = len(records)
+    svc = np.zeros(n, np.int64)
+    pdone = np.zeros(n, dtype=object)
+    cdone = np.zeros(n, dtype=object)
+    for p_id in np.unique(plane):
+        idx = np.nonzero(plane == p_id)[0]
+        prev_page = np.concatenate([[-1], pg[idx][:-1]])
+        hit = (prev_page == pg[idx]) if page_buffers else np.zeros(idx.size, bool)
+        s = np.where(op[idx] == 0, np.where(hit, 0, profile["read_latency_ns"] * 1000),
+                     np.where(off[idx] + nbytes[idx] == page,
+                              profile["program_latency_ns"] * 1000, 0))
+        svc[idx] = s
+        pdone[idx] = lindley(issue[idx], s) if contention else issue[idx] + s
+    for c_id in np.unique(ch):
+        idx = np.nonzero(ch == c_id)[0]
+        cdone[idx] = lindley(issue[idx], xfer[idx])
+    done = np.maximum(pdone, cdone).astype(np.uint64)
+    return done, svc, xfer, plane, ch
+
+
+def oracle_run(profile_path, s, **opts):
+    prof = oracle_py.load_profile(profile_path)
+    params = oracle_py.engine_params(prof, **opts)
+    ranges, count = oracle_py.range_table(s.ranges, prof["page_bytes"], prof["capacity_bytes"])
+    return prof, params, ranges, count
+
+
+@pytest.mark.parametrize("page_buffers,contention", [(1, 1), (0, 1), (1, 0)])
+def test_engine_equals_closed_form(page_buffers, contention):
+    s = workloads.config0(n=6000, seed=13, write_fraction_per_mille=150)
+    # concentrate on few pages so page-register hits and fills occur
+    s.records[:, 0] = np.uint64(workloads.RANGE_BASE) + (
+        s.records[:, 0] - np.uint64(workloads.RANGE_BASE)) % np.uint64(64 * 16384)
+    fill = (np.arange(len(s.records)) % 7) == 0
+    s.records[fill, 0] = s.records[fill, 0] - s.records[fill, 0] % np.uint64(16384) + \
+        np.uint64(16384 - 128)
+    s.records[fill, 3] = 1
+    prof, params, ranges, count = oracle_run(C0, s, page_buffers=page_buffers,
+                                             plane_contention=contention)
+    comp, status, rep, st = oracle_py.run(params, ranges, count, s.records)
+    done, svc, xfer, plane, ch = independent_engine(prof, s.records, page_buffers,
+                                                    bool(contention))
+    np.testing.assert_array_equal(comp, done)
+    assert rep["page_hits"] > 0 or not page_buffers
+    assert rep["programs"] > 0
+    # conservation of charged work
+    np.testing.assert_array_equal(st.channel_busy_total,
+                                  np.bincount(ch, weights=xfer, minlength=8).astype(np.uint64))
+    np.testing.assert_array_equal(st.plane_busy_total,
+                                  np.bincount(plane, weights=svc, minlength=64).astype(np.uint64))
+
+
+def test_parallel_and_split_runs_agree():
+    s = workloads.config0(n=40_000, seed=17, write_fraction_per_mille=100)
+    prof, params, ranges, count = oracle_run(C0, s)
+    c1, s1, r1, st1 = oracle_py.run(params, ranges, count, s.records)
+    c2, s2, r2, st2 = oracle_py.run(params, ranges, count, s.records, threads=6)
+    assert np.array_equal(c1, c2) and np.array_equal(s1, s2) and r1 == r2
+    st = oracle_py.OracleState(params)
+    parts = [oracle_py.run(params, ranges, count, s.records[a:b], 0, st)[0]
+             for a, b in [(0, 1), (1, 999), (999, 40_000)]]
+    assert np.array_equal(np.concatenate(parts), c1)
+    assert np.array_equal(st.plane_busy, st1.plane_busy)
+    assert np.array_equal(st.channel_cursor, st1.channel_cursor)
+
+
+def test_fast_preset_is_reference_single_tail():
+    from hbfsim_amd.engine import FAST_REFERENCE_OPTIONS
+    nominal = oracle_py.ROOT / "tests" / "golden" / "profiles" / "nominal.json"
+    prof = oracle_py.load_profile(nominal)
+    rng = np.random.default_rng(5)
+    n = 5000
+    s = workloads.Stream(nominal, [(workloads.RANGE_BASE, 1 << 28, 3)],
+                         np.zeros((n, 4), np.uint64))
+    s.records[:, 0] = np.uint64(workloads.RANGE_BASE) + \
+        rng.integers(0, (1 << 28) // 64, n).astype(np.uint64) * np.uint64(64)
+    s.records[:, 1] = 64
+    s.records[:, 3] = (rng.integers(0, 5, n) == 0).astype(np.uint64)
+    s.records[:, 2] = np.cumsum(rng.integers(0, 30, n)).astype(np.uint64) * np.uint64(1000)
+    _, params, ranges, count = oracle_run(nominal, s, **FAST_REFERENCE_OPTIONS)
+    comp, _, rep, _ = oracle_py.run(params, ranges, count, s.records)
+    arrival = s.records[:, 2] // np.uint64(1000)
+    tail = 0
+    for i in range(n):  # hbf_device.cu:895-910, written out directly
+        base = prof["program_latency_ns"] if s.records[i, 3] else prof["read_latency_ns"]
+        xfer = -(-16384 * 10**9 // prof["aggregate_bandwidth_bytes_per_s"])
+        tail = max(tail, int(arrival[i])) + xfer
+        assert int(comp[i]) == max(int(arrival[i]) + base, tail) * 1000
+
+
+def test_stripe_bijection_all_orders(oracle):
+    sizes = (ctypes.c_uint32 * 4)(3, 2, 4, 5)  # C W D P, deliberately non-power-of-two
+    total = 3 * 2 * 4 * 5
+    for perm in itertools.permutations("CWDP"):
+        name = "".join(perm).encode()
+        order = (ctypes.c_uint32 * 4)()
+        assert oracle.orc_parse_scheme(name, order)
+        seen = set()
+        coords = (ctypes.c_uint32 * 4)()
+        for page in range(total * 3):
+            row = oracle.orc_stripe(page, order, sizes, coords)
+            key = tuple(coords)
+            assert row == page // total
+            if page < total:
+                seen.add(key)
+            if page % total == 1:  # fastest axis advanced first
+                fastest = order[0]
+                prev = (ctypes.c_uint32 * 4)()
+                oracle.orc_stripe(page - 1, order, sizes, prev)
+                assert coords[fastest] == prev[fastest] + 1
+        assert len(seen) == total
+    assert not oracle.orc_parse_scheme(b"CWDD", (ctypes.c_uint32 * 4)())
+    assert not oracle.orc_parse_scheme(b"CWD", (ctypes.c_uint32 * 4)())
+
+
+def test_cwdp_agrees_with_bank_layout(oracle):
+    order = (ctypes.c_uint32 * 4)()
+    oracle.orc_parse_scheme(b"CWDP", order)
+    for channels, chips in [(16, 16), (16, 64), (4, 8)]:
+        sizes = (ctypes.c_uint32 * 4)(channels, chips, 1, 1)
+        coords = (ctypes.c_uint32 * 4)()
+        c, die, bank, chip = (ctypes.c_uint32() for _ in range(4))
+        for lpa in range(0, 5000, 7):
+            oracle.orc_stripe(lpa, order, sizes, coords)
+            oracle.orc_hbf_cold_read_bank(lpa, channels, chips // 4 or 1, 4 if chips >= 4 else 1,
+                                          ctypes.byref(c), ctypes.byref(die), ctypes.byref(bank),
+                                          ctypes.byref(chip))
+            assert coords[0] == c.value and coords[1] == chip.value
+
+
+def test_classification_counts_match_brute_force(oracle):
+    """orc_classify against a linear scan of the range table (the
+    resolver's semantics without the binary search)."""
+    rng = np.random.default_rng(9)
+    recs = (oracle_py.OrcRange * 40)()
+    base = 0x10000
+    for i in range(40):
+        recs[i].base, recs[i].length = base, int(rng.choice([0x1000, 0x3000, 0x8000]))
+        recs[i].mode, recs[i].permissions, recs[i].page_bytes = 1, int(rng.choice([1, 3])), 0x1000
+        recs[i].range_id = i + 1
+        base += recs[i].length + int(rng.choice([0, 0x800, 0x4000]))
+    idx = ctypes.c_uint32()
+    for _ in range(5000):
+        a = int(rng.integers(0x8000, base + 0x8000))
+        b = int(rng.choice([0, 1, 64, 128, 0x1000]))
+        op = int(rng.integers(0, 3))
+        got = oracle.orc_classify(recs, 40, a, b, op, ctypes.byref(idx))
+        inside = [i for i in range(40) if recs[i].base <= a < recs[i].base + recs[i].length]
+        if not inside:
+            above = [i for i in range(40) if recs[i].base > a]
+            straddle = bool(above) and b > 0 and recs[above[0]].base < a + b
+            assert got == (2 if straddle else 1)
+            continue
+        r = recs[inside[0]]
+        ok = (b > 0 and op <= 1 and (r.permissions >> op) & 1 and a + b <= r.base + r.length
+              and (a - r.base) // 0x1000 == (a - r.base + b - 1) // 0x1000)
+        assert got == (0 if ok else 2)
