@@ -779,6 +779,17 @@ HBF_API int hbfsim_amd_lookup_range(hbfsim_context* c, uint64_t address, uint32_
     return HBFSIM_OK;
 }
 
+HBF_API int hbfsim_amd_gen_segment_lines(hbf_record32* d_records, size_t capacity,
+                                         const uint64_t* d_segment_base, size_t nseg,
+                                         uint64_t lines_per_segment, uint32_t line_bytes,
+                                         uint64_t gap_ps, uint32_t issuers, uint64_t flags,
+                                         void* stream)
+{
+    return hbfamd::gen_segment_lines(d_records, capacity, d_segment_base, nseg,
+                                     lines_per_segment, line_bytes, gap_ps, issuers, flags,
+                                     stream);
+}
+
 HBF_API int hbfsim_amd_validate_profile(const char* path, char* error, size_t error_bytes)
 {
     if (error != nullptr && error_bytes != 0) {

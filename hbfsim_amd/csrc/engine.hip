@@ -10,9 +10,9 @@
 //              per-resource (max,+) summary of the tile.  Planes also carry
 //              their page-register tag; a tile's first record on a plane has
 //              its page-buffer hit resolved later, from the carry.
-//   k_carry    one thread per resource walks the tiles in order and turns
-//              summaries into the exact busy-until / tag state at the start
-//              of every tile (and the final state, kept for the next run).
+//   k_carry_*  a three-level scan over the tile summaries gives the exact
+//              busy-until / tag state at the start of every tile (and the
+//              final state, kept for the next run).
 //   k_apply    re-reads each tile, replays it from its carry-in state and
 //              writes completion times, status bytes and accounting.
 //
@@ -464,51 +464,187 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     }
 }
 
-__global__ __launch_bounds__(64) void k_carry(KArgs a, std::size_t ntiles, const PlaneSum* psum,
-                                              const ChanSum* csum, const std::uint64_t* tile_count,
-                                              PlaneCarry* pcarry, std::uint64_t* ccarry,
-                                              std::uint64_t* tile_seq, std::uint64_t* st_pbusy,
-                                              std::uint64_t* st_ptag, std::uint64_t* st_cbusy,
-                                              std::uint64_t* st_seq)
+// ---- carry chain: a three-level scan over tile summaries ---------------
+//
+// A plane summary is a (first record, (max,+) map of the rest, last page)
+// triple.  Two summaries compose associatively: the later summary's first
+// record resolves its page-register hit against the earlier one's last page,
+// then joins the map.  Level 1 folds groups of kGroup tiles, level 2 walks
+// the groups of each resource in order from the engine state, level 3 walks
+// each group's tiles from the group's carry-in.  One thread per (group,
+// resource) at levels 1 and 3, one per resource at level 2.
+
+constexpr std::uint32_t kGroup = 64;
+
+__device__ __forceinline__ PlaneSum plane_compose(const KArgs& a, const PlaneSum& s1,
+                                                  const PlaneSum& s2)
+{
+    if (s2.fpage1 == 0) {
+        return s1;
+    }
+    if (s1.fpage1 == 0) {
+        return s2;
+    }
+    PlaneSum r = s1;
+    if (a.contention) {
+        const bool hit = a.slots != 0 && s2.fpage1 == s1.lpage1;
+        const std::uint64_t svc = plane_service(a, s2.fcls, hit);
+        // rest1, then the later first record (svc, issue + svc), then rest2
+        std::uint64_t A = s1.rA + svc;
+        std::uint64_t B = umax64(s1.rB + svc, s2.fissue + svc);
+        r.rB = umax64(B + s2.rA, s2.rB);
+        r.rA = A + s2.rA;
+    }
+    r.lpage1 = s2.lpage1;
+    return r;
+}
+
+__device__ __forceinline__ void plane_apply(const KArgs& a, const PlaneSum& s, std::uint64_t& busy,
+                                            std::uint64_t& tag1)
+{
+    if (s.fpage1 == 0) {
+        return;
+    }
+    if (a.contention) {
+        const bool hit = a.slots != 0 && tag1 == s.fpage1;
+        const std::uint64_t b = umax64(busy, s.fissue) + plane_service(a, s.fcls, hit);
+        busy = umax64(b + s.rA, s.rB);
+    }
+    tag1 = s.lpage1;
+}
+
+__device__ __forceinline__ ChanSum chan_compose(const ChanSum& s1, const ChanSum& s2)
+{
+    ChanSum r;
+    r.A = s1.A + s2.A;
+    r.B = umax64(s1.B + s2.A, s2.B);
+    return r;
+}
+
+// Level 1: thread (g, r) folds the summaries of group g's tiles.
+__global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, std::size_t ngroups,
+                                                  const PlaneSum* psum, const ChanSum* csum,
+                                                  const std::uint64_t* tile_count,
+                                                  PlaneSum* gpsum, ChanSum* gcsum,
+                                                  std::uint64_t* gcount)
+{
+    const std::uint32_t rt = a.Rp + a.Rc + 1;
+    const std::size_t id = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= ngroups * rt) {
+        return;
+    }
+    const std::size_t g = id / rt;
+    const std::uint32_t r = static_cast<std::uint32_t>(id - g * rt);
+    const std::size_t t0 = g * kGroup;
+    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
+    if (r < a.Rp) {
+        PlaneSum acc = psum[t0 * a.Rp + r];
+        for (std::size_t t = t0 + 1; t < t1; ++t) {
+            acc = plane_compose(a, acc, psum[t * a.Rp + r]);
+        }
+        gpsum[g * a.Rp + r] = acc;
+    } else if (r < a.Rp + a.Rc) {
+        const std::uint32_t c = r - a.Rp;
+        ChanSum acc = csum[t0 * a.Rc + c];
+        for (std::size_t t = t0 + 1; t < t1; ++t) {
+            acc = chan_compose(acc, csum[t * a.Rc + c]);
+        }
+        gcsum[g * a.Rc + c] = acc;
+    } else {
+        std::uint64_t sum = 0;
+        for (std::size_t t = t0; t < t1; ++t) {
+            sum += tile_count[t];
+        }
+        gcount[g] = sum;
+    }
+}
+
+// Level 2: thread r walks the groups from the engine state; writes each
+// group's carry-in and the final state.
+__global__ __launch_bounds__(64) void k_carry_mid(KArgs a, std::size_t ngroups,
+                                                  const PlaneSum* gpsum, const ChanSum* gcsum,
+                                                  const std::uint64_t* gcount,
+                                                  PlaneCarry* gpcarry, std::uint64_t* gccarry,
+                                                  std::uint64_t* gseq, std::uint64_t* st_pbusy,
+                                                  std::uint64_t* st_ptag, std::uint64_t* st_cbusy,
+                                                  std::uint64_t* st_seq)
 {
     const std::uint32_t t = blockIdx.x * kWave + threadIdx.x;
     if (t < a.Rp) {
         std::uint64_t busy = st_pbusy[t];
         std::uint64_t tag1 = st_ptag[static_cast<std::size_t>(t) * 2];
-        for (std::size_t k = 0; k < ntiles; ++k) {
+        for (std::size_t g = 0; g < ngroups; ++g) {
             PlaneCarry c;
             c.busy = busy;
             c.tag1 = tag1;
-            pcarry[k * a.Rp + t] = c;
-            const PlaneSum S = psum[k * a.Rp + t];
-            if (S.fpage1 != 0) {
-                const bool hit = a.slots != 0 && tag1 == S.fpage1;
-                const std::uint64_t svc = plane_service(a, S.fcls, hit);
-                if (a.contention) {
-                    const std::uint64_t b = umax64(busy, S.fissue) + svc;
-                    busy = umax64(b + S.rA, S.rB);
-                }
-                tag1 = S.lpage1;
-            }
+            gpcarry[g * a.Rp + t] = c;
+            plane_apply(a, gpsum[g * a.Rp + t], busy, tag1);
         }
         st_pbusy[t] = busy;
         st_ptag[static_cast<std::size_t>(t) * 2] = tag1;
     } else if (t < a.Rp + a.Rc) {
         const std::uint32_t c = t - a.Rp;
         std::uint64_t busy = st_cbusy[c];
-        for (std::size_t k = 0; k < ntiles; ++k) {
-            ccarry[k * a.Rc + c] = busy;
-            const ChanSum S = csum[k * a.Rc + c];
+        for (std::size_t g = 0; g < ngroups; ++g) {
+            gccarry[g * a.Rc + c] = busy;
+            const ChanSum S = gcsum[g * a.Rc + c];
             busy = umax64(busy + S.A, S.B);
         }
         st_cbusy[c] = busy;
     } else if (t == a.Rp + a.Rc) {
         std::uint64_t s = *st_seq;
-        for (std::size_t k = 0; k < ntiles; ++k) {
-            tile_seq[k] = s;
-            s += tile_count[k];
+        for (std::size_t g = 0; g < ngroups; ++g) {
+            gseq[g] = s;
+            s += gcount[g];
         }
         *st_seq = s;
+    }
+}
+
+// Level 3: thread (g, r) walks group g's tiles from the group carry-in and
+// writes every tile's carry-in.
+__global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
+                                                    std::size_t ngroups, const PlaneSum* psum,
+                                                    const ChanSum* csum,
+                                                    const std::uint64_t* tile_count,
+                                                    const PlaneCarry* gpcarry,
+                                                    const std::uint64_t* gccarry,
+                                                    const std::uint64_t* gseq, PlaneCarry* pcarry,
+                                                    std::uint64_t* ccarry, std::uint64_t* tile_seq)
+{
+    const std::uint32_t rt = a.Rp + a.Rc + 1;
+    const std::size_t id = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (id >= ngroups * rt) {
+        return;
+    }
+    const std::size_t g = id / rt;
+    const std::uint32_t r = static_cast<std::uint32_t>(id - g * rt);
+    const std::size_t t0 = g * kGroup;
+    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
+    if (r < a.Rp) {
+        const PlaneCarry c0 = gpcarry[g * a.Rp + r];
+        std::uint64_t busy = c0.busy, tag1 = c0.tag1;
+        for (std::size_t t = t0; t < t1; ++t) {
+            PlaneCarry c;
+            c.busy = busy;
+            c.tag1 = tag1;
+            pcarry[t * a.Rp + r] = c;
+            plane_apply(a, psum[t * a.Rp + r], busy, tag1);
+        }
+    } else if (r < a.Rp + a.Rc) {
+        const std::uint32_t c = r - a.Rp;
+        std::uint64_t busy = gccarry[g * a.Rc + c];
+        for (std::size_t t = t0; t < t1; ++t) {
+            ccarry[t * a.Rc + c] = busy;
+            const ChanSum S = csum[t * a.Rc + c];
+            busy = umax64(busy + S.A, S.B);
+        }
+    } else {
+        std::uint64_t s = gseq[g];
+        for (std::size_t t = t0; t < t1; ++t) {
+            tile_seq[t] = s;
+            s += tile_count[t];
+        }
     }
 }
 
@@ -784,6 +920,12 @@ struct engine {
     std::uint64_t* d_ccarry{nullptr};
     std::uint64_t* d_tcount{nullptr};
     std::uint64_t* d_tseq{nullptr};
+    PlaneSum* d_gpsum{nullptr};
+    ChanSum* d_gcsum{nullptr};
+    PlaneCarry* d_gpcarry{nullptr};
+    std::uint64_t* d_gccarry{nullptr};
+    std::uint64_t* d_gcount{nullptr};
+    std::uint64_t* d_gseq{nullptr};
     hipEvent_t ev[4]{};
     float last_ms[3]{0, 0, 0};
     std::uint64_t burst{0};
@@ -836,6 +978,12 @@ void free_scratch(engine* e)
     hfree(e->d_ccarry);
     hfree(e->d_tcount);
     hfree(e->d_tseq);
+    hfree(e->d_gpsum);
+    hfree(e->d_gcsum);
+    hfree(e->d_gpcarry);
+    hfree(e->d_gccarry);
+    hfree(e->d_gcount);
+    hfree(e->d_gseq);
     e->tile_cap = 0;
 }
 
@@ -851,6 +999,14 @@ int ensure_scratch(engine* e, std::size_t ntiles)
         halloc(e->d_pcarry, cap * rp) != hipSuccess ||
         halloc(e->d_ccarry, cap * rc) != hipSuccess || halloc(e->d_tcount, cap) != hipSuccess ||
         halloc(e->d_tseq, cap) != hipSuccess) {
+        free_scratch(e);
+        return HBFSIM_CUDA_ERROR;
+    }
+    const std::size_t gcap = (cap + kGroup - 1) / kGroup;
+    if (halloc(e->d_gpsum, gcap * rp) != hipSuccess || halloc(e->d_gcsum, gcap * rc) != hipSuccess ||
+        halloc(e->d_gpcarry, gcap * rp) != hipSuccess ||
+        halloc(e->d_gccarry, gcap * rc) != hipSuccess || halloc(e->d_gcount, gcap) != hipSuccess ||
+        halloc(e->d_gseq, gcap) != hipSuccess) {
         free_scratch(e);
         return HBFSIM_CUDA_ERROR;
     }
@@ -1137,9 +1293,20 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
     hipLaunchKernelGGL(k_summary, grid, dim3(kWave), lds_a, stream, a, d_rec, n, base_ps,
                        e->d_psum, e->d_csum, e->d_tcount);
     (void)hipEventRecord(e->ev[1], stream);
-    hipLaunchKernelGGL(k_carry, dim3(carry_blocks), dim3(kWave), 0, stream, a, ntiles, e->d_psum,
-                       e->d_csum, e->d_tcount, e->d_pcarry, e->d_ccarry, e->d_tseq, e->d_pbusy,
-                       e->d_ptag, e->d_cbusy, e->d_seq);
+    {
+        const std::size_t ngroups = (ntiles + kGroup - 1) / kGroup;
+        const std::size_t rt = static_cast<std::size_t>(a.Rp) + a.Rc + 1;
+        const unsigned wide = static_cast<unsigned>((ngroups * rt + 255) / 256);
+        hipLaunchKernelGGL(k_carry_up, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
+                           e->d_psum, e->d_csum, e->d_tcount, e->d_gpsum, e->d_gcsum,
+                           e->d_gcount);
+        hipLaunchKernelGGL(k_carry_mid, dim3(carry_blocks), dim3(kWave), 0, stream, a, ngroups,
+                           e->d_gpsum, e->d_gcsum, e->d_gcount, e->d_gpcarry, e->d_gccarry,
+                           e->d_gseq, e->d_pbusy, e->d_ptag, e->d_cbusy, e->d_seq);
+        hipLaunchKernelGGL(k_carry_down, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
+                           e->d_psum, e->d_csum, e->d_tcount, e->d_gpcarry, e->d_gccarry,
+                           e->d_gseq, e->d_pcarry, e->d_ccarry, e->d_tseq);
+    }
     (void)hipEventRecord(e->ev[2], stream);
     hipLaunchKernelGGL(k_apply, grid, dim3(kWave), lds_c, stream, a, d_rec, n, base_ps,
                        e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status, e->d_ptot,

@@ -77,4 +77,10 @@ int engine_run_host(engine* e, const hbf_record32* records, std::size_t n,
                     std::uint64_t* completion, std::uint8_t* status,
                     std::uint64_t base_ps, hbfsim_amd_report* out);
 
+// Workload compiler (gen.hip).
+int gen_segment_lines(hbf_record32* d_records, std::size_t capacity,
+                      const std::uint64_t* d_seg_base, std::size_t nseg, std::uint64_t lines,
+                      std::uint32_t line_bytes, std::uint64_t gap_ps, std::uint32_t issuers,
+                      std::uint64_t flags, void* stream);
+
 }  // namespace hbfamd

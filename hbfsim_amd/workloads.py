@@ -96,3 +96,151 @@ def config0(n: int = 1 << 20, seed: int = 0, mean_gap_ps: int = 2000,
         w = (draws(seed, 3, 0, n) % np.uint64(1000)) < np.uint64(write_fraction_per_mille)
         rec[:, 3] = w.astype(np.uint64)
     return Stream(PROFILES / "c0.json", [(RANGE_BASE, range_bytes, 3)], rec, "config0")
+
+
+# ---------------------------------------------------------------------------
+# Config 2: Qwen3-30B-A3B-shaped MoE decode
+
+
+@dataclasses.dataclass(frozen=True)
+class MoeShape:
+    layers: int = 48
+    experts: int = 128
+    top_k: int = 8
+    hidden: int = 2048
+    intermediate: int = 768
+    tokens: int = 32
+    zipf_s: float = 1.1
+    seed: int = 1
+    line: int = 128
+    issuers: int = 256        # concurrent wavefronts issuing lines
+    gap_ps: int = 64_000      # each issues one line every 64 ns
+    base: int = 0x5000_0000_0000
+
+    @property
+    def expert_bytes(self) -> int:
+        return 3 * self.hidden * self.intermediate * 2  # gate, up, down in bf16
+
+    @property
+    def lines_per_expert(self) -> int:
+        return self.expert_bytes // self.line
+
+    def expert_base(self, layer: int, expert: int) -> int:
+        return self.base + (layer * self.experts + expert) * self.expert_bytes
+
+
+QWEN3_30B_A3B = MoeShape()
+
+
+def zipf_alias(n: int, s: float) -> tuple[np.ndarray, np.ndarray]:
+    """Walker/Vose alias table for P(k) ~ 1/(k+1)^s, k = 0..n-1, with
+    integer acceptance thresholds out of 2^32 so sampling is exact integer
+    arithmetic on the host and on the GPU."""
+    one = 1 << 32
+    w = [1.0 / math.pow(k + 1, s) for k in range(n)]
+    total = math.fsum(w)
+    q = [int(round(x / total * n * one)) for x in w]
+    q[0] += n * one - sum(q)
+    prob = [0] * n
+    alias = list(range(n))
+    small = [i for i in range(n) if q[i] < one]
+    large = [i for i in range(n) if q[i] >= one]
+    while small and large:
+        lo = small.pop()
+        hi = large.pop()
+        prob[lo] = q[lo]
+        alias[lo] = hi
+        q[hi] -= one - q[lo]
+        (small if q[hi] < one else large).append(hi)
+    for i in large + small:
+        prob[i] = one
+    return np.array(prob, np.uint64), np.array(alias, np.uint64)
+
+
+def alias_sample(u: np.ndarray, prob: np.ndarray, alias: np.ndarray) -> np.ndarray:
+    n = np.uint64(len(prob))
+    col = ((u >> np.uint64(32)) * n) >> np.uint64(32)
+    frac = u & np.uint64(0xFFFFFFFF)
+    return np.where(frac < prob[col], col, alias[col])
+
+
+def moe_selection(shape: MoeShape, steps: int, first_step: int = 0) -> list[list[np.ndarray]]:
+    """sel[s][l]: sorted union over the step's tokens of each token's top-k
+    experts, drawn without replacement from Zipf(s) (up to 64 draws per
+    token, duplicates skipped; the rare shortfall is filled by the lowest
+    unused expert ids)."""
+    prob, alias = zipf_alias(shape.experts, shape.zipf_s)
+    attempts = 64
+    out = []
+    per_step = shape.layers * shape.tokens * attempts
+    for s in range(first_step, first_step + steps):
+        u = draws(shape.seed, 100, s * per_step, per_step)
+        e = alias_sample(u, prob, alias).reshape(shape.layers, shape.tokens, attempts)
+        layers = []
+        for l_ in range(shape.layers):
+            chosen = np.zeros(shape.experts, bool)
+            for t in range(shape.tokens):
+                seen = []
+                for x in e[l_, t]:
+                    if x not in seen:
+                        seen.append(int(x))
+                        if len(seen) == shape.top_k:
+                            break
+                k = 0
+                while len(seen) < shape.top_k:
+                    if k not in seen:
+                        seen.append(k)
+                    k += 1
+                chosen[seen] = True
+            layers.append(np.nonzero(chosen)[0].astype(np.int64))
+        out.append(layers)
+    return out
+
+
+def moe_segments(shape: MoeShape, selection: list[np.ndarray]) -> np.ndarray:
+    """Expert base addresses read in one decode step, in issue order."""
+    bases = [shape.expert_base(l_, int(e)) for l_, sel in enumerate(selection) for e in sel]
+    return np.array(bases, np.uint64)
+
+
+def moe_ranges(shape: MoeShape) -> list[tuple[int, int, int]]:
+    """Every expert registered as its own read-only HBF range."""
+    return [(shape.expert_base(l_, e), shape.expert_bytes, 1)
+            for l_ in range(shape.layers) for e in range(shape.experts)]
+
+
+def segment_records(seg_base: np.ndarray, lines: int, line: int, gap_ps: int, issuers: int,
+                    start: int = 0, count: int | None = None, flags: int = 0) -> np.ndarray:
+    """Host mirror of the GPU workload compiler (hbfsim_amd_gen_segment_lines)."""
+    total = len(seg_base) * lines
+    count = total - start if count is None else count
+    j = np.arange(start, start + count, dtype=np.uint64)
+    rec = np.zeros((count, 4), np.uint64)
+    rec[:, 0] = seg_base[(j // np.uint64(lines)).astype(np.int64)] + \
+        (j % np.uint64(lines)) * np.uint64(line)
+    rec[:, 1] = line
+    rec[:, 2] = (j // np.uint64(issuers)) * np.uint64(gap_ps)
+    rec[:, 3] = flags
+    return rec
+
+
+def gpu_segment_records(seg_base: np.ndarray, lines: int, line: int, gap_ps: int, issuers: int,
+                        flags: int = 0, out=None, stream=None):
+    """Compiles one step's records on the GPU; returns an int64 [n, 4] tensor."""
+    import ctypes
+
+    import torch
+
+    from . import _native as nat
+    lib = nat.load()
+    n = len(seg_base) * lines
+    if out is None:
+        out = torch.empty((n, 4), dtype=torch.int64, device="cuda")
+    bases = torch.from_numpy(seg_base.view(np.int64)).cuda()
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    nat.check(lib.hbfsim_amd_gen_segment_lines(
+        out.data_ptr(), out.shape[0], bases.data_ptr(), len(seg_base), lines, line, gap_ps,
+        issuers, flags, ctypes.c_void_p(stream)), "generate records")
+    torch.cuda.current_stream().synchronize()
+    return out[:n]

@@ -321,6 +321,18 @@ int hbfsim_amd_lookup_range(hbfsim_context* context, uint64_t address,
                             uint32_t bytes, uint32_t* kind,
                             hbfsim_amd_range* out, uint32_t* count);
 
+/* Workload compiler, no counterpart in the reference (it generates the
+ * record streams the benchmark configurations describe).  Writes
+ * nseg * lines_per_segment records to d_records (device, capacity
+ * records): segment s, line k -> addr = d_segment_base[s] + k * line_bytes,
+ * bytes = line_bytes, issue_ps = (index / issuers) * gap_ps, flags.  The
+ * records are ordered by issue time.  Asynchronous on `stream`. */
+int hbfsim_amd_gen_segment_lines(hbf_record32* d_records, size_t capacity,
+                                 const uint64_t* d_segment_base, size_t nseg,
+                                 uint64_t lines_per_segment, uint32_t line_bytes,
+                                 uint64_t gap_ps, uint32_t issuers, uint64_t flags,
+                                 void* stream);
+
 /* Profile validation with the reference's rules and messages
  * (src/profile/profile.cpp:238-468).  Returns HBFSIM_OK or
  * HBFSIM_INVALID_ARGUMENT with the reference's message in `error`. */
