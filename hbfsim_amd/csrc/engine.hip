@@ -175,6 +175,41 @@ __device__ __forceinline__ void group_scan(std::uint64_t& A, std::uint64_t& B, i
     }
 }
 
+// Whole-wave inclusive scan of (A, B) maps in lane order, for steps where
+// every active lane belongs to one group (inactive lanes hold the identity
+// (0, 0)).  DPP row shifts build 16-lane scans, then row broadcasts join the
+// rows; no LDS traffic.  Controls are the GFX9 encodings gfx950 keeps:
+// row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ std::uint64_t dpp64(std::uint64_t v)
+{
+    const int lo = __builtin_amdgcn_update_dpp(
+        0, static_cast<int>(static_cast<std::uint32_t>(v)), Ctrl, RowMask, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(
+        0, static_cast<int>(static_cast<std::uint32_t>(v >> 32)), Ctrl, RowMask, 0xF, false);
+    return (static_cast<std::uint64_t>(static_cast<std::uint32_t>(hi)) << 32) |
+           static_cast<std::uint32_t>(lo);
+}
+
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ void dpp_scan_step(std::uint64_t& A, std::uint64_t& B)
+{
+    const std::uint64_t pA = dpp64<Ctrl, RowMask>(A);
+    const std::uint64_t pB = dpp64<Ctrl, RowMask>(B);
+    B = umax64(pB + A, B);
+    A = pA + A;
+}
+
+__device__ __forceinline__ void wave_scan(std::uint64_t& A, std::uint64_t& B)
+{
+    dpp_scan_step<0x111, 0xF>(A, B);
+    dpp_scan_step<0x112, 0xF>(A, B);
+    dpp_scan_step<0x114, 0xF>(A, B);
+    dpp_scan_step<0x118, 0xF>(A, B);
+    dpp_scan_step<0x142, 0xA>(A, B);
+    dpp_scan_step<0x143, 0xC>(A, B);
+}
+
 // find_range_index (hbf_device.cuh:826-841): upper_bound(base) - 1 over the
 // sorted range table.  The top level runs over every `stride`-th base,
 // staged in LDS; the bottom level over at most `stride` bases in memory.
@@ -226,15 +261,40 @@ __device__ __forceinline__ std::uint64_t xfer_ps(const KArgs& a, std::uint64_t b
     return a.xfer_q * ((bytes * a.xfer_num + a.xfer_den - 1) / a.xfer_den);
 }
 
-// Classification in the resolver's order (hbf_device.cu:1081-1165) followed
-// by striping of the media page.
-__device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence,
-                                      const hbf_record32* rec, std::size_t i,
-                                      std::uint64_t base_ps)
+// Range last found by this lane.  Ranges are disjoint, so an address inside
+// the cached range is inside no other one and the search can be skipped.
+struct RangeCache {
+    std::uint64_t base;
+    std::uint64_t end;
+    std::uint64_t file_offset;
+    std::uint32_t meta;
+    std::uint32_t id;
+};
+
+__device__ __forceinline__ RangeCache empty_cache()
+{
+    RangeCache c;
+    c.base = 1;
+    c.end = 0;
+    c.file_offset = 0;
+    c.meta = 0;
+    c.id = 0;
+    return c;
+}
+
+__device__ __forceinline__ void load_record(const hbf_record32* rec, std::size_t i, uint4& x,
+                                            uint4& y)
 {
     const uint4* p = reinterpret_cast<const uint4*>(rec + i);
-    const uint4 x = p[0];
-    const uint4 y = p[1];
+    x = p[0];
+    y = p[1];
+}
+
+// Classification in the resolver's order (hbf_device.cu:1081-1165) followed
+// by striping of the media page.
+__device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence, RangeCache& rc,
+                                      const uint4& x, const uint4& y, std::uint64_t base_ps)
+{
     const std::uint64_t addr = x.x | (static_cast<std::uint64_t>(x.y) << 32);
     const std::uint64_t bytes = x.z | (static_cast<std::uint64_t>(x.w) << 32);
     const std::uint64_t issue_rel = y.x | (static_cast<std::uint64_t>(y.y) << 32);
@@ -247,43 +307,47 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
     d.range_id = 0;
     d.page1 = 0;
     d.xfer = 0;
-    const std::uint32_t idx = find_range(a, fence, addr);
-    if (idx == a.r_count || addr < a.r_base[idx] || addr - a.r_base[idx] >= a.r_length[idx]) {
-        const std::uint32_t succ = idx == a.r_count ? 0u : idx + 1u;
-        if (bytes > 0xffffffffull ||
-            (succ < a.r_count && overlaps(a.r_base[succ], a.r_length[succ], addr, bytes))) {
-            d.cls = kClsUnsupported;
-        } else {
-            d.cls = kClsBypass;
+    if (!(addr >= rc.base && addr < rc.end)) {
+        const std::uint32_t idx = find_range(a, fence, addr);
+        if (idx == a.r_count || addr < a.r_base[idx] ||
+            addr - a.r_base[idx] >= a.r_length[idx]) {
+            const std::uint32_t succ = idx == a.r_count ? 0u : idx + 1u;
+            if (bytes > 0xffffffffull ||
+                (succ < a.r_count && overlaps(a.r_base[succ], a.r_length[succ], addr, bytes))) {
+                d.cls = kClsUnsupported;
+            } else {
+                d.cls = kClsBypass;
+            }
+            return d;
         }
-        return d;
+        rc.base = a.r_base[idx];
+        rc.end = rc.base + a.r_length[idx];
+        rc.file_offset = a.r_file_offset[idx];
+        rc.meta = a.r_meta[idx];
+        rc.id = a.r_id[idx];
     }
-    const std::uint64_t base = a.r_base[idx];
-    const std::uint64_t length = a.r_length[idx];
-    const std::uint32_t meta = a.r_meta[idx];
-    const std::uint32_t mode = meta & 0xffu;
-    const std::uint32_t perms = meta >> 8;
+    const std::uint32_t mode = rc.meta & 0xffu;
+    const std::uint32_t perms = rc.meta >> 8;
     const std::uint64_t page_mask = (1ull << a.page_shift) - 1;
     // access_supported (hbf_device.cuh:843-860); the range's own bounds and
     // page size are validated at registration.
     if (bytes == 0 || bytes > 0xffffffffull || op > 1 || (mode != 1 && mode != 2) ||
-        bytes > ~0ull - addr || addr + bytes > base + length || (perms & (1u << op)) == 0) {
+        bytes > ~0ull - addr || addr + bytes > rc.end || (perms & (1u << op)) == 0) {
         d.cls = kClsUnsupported;
         return d;
     }
-    const std::uint64_t off = addr - base;
+    const std::uint64_t off = addr - rc.base;
     if ((off >> a.page_shift) != ((off + bytes - 1) >> a.page_shift)) {
         d.cls = kClsUnsupported;
         return d;
     }
-    const std::uint64_t file_offset = a.r_file_offset[idx];
-    if ((off & ~page_mask) > ~0ull - file_offset) {
+    if ((off & ~page_mask) > ~0ull - rc.file_offset) {
         d.cls = kClsUnsupported;
         return d;
     }
     d.cls = kClsModeled;
-    d.range_id = a.r_id[idx];
-    const std::uint64_t media = file_offset + off;
+    d.range_id = rc.id;
+    const std::uint64_t media = rc.file_offset + off;
     const std::uint64_t page = media >> a.page_shift;
     d.page1 = page + 1;
     const std::uint64_t page_bytes = 1ull << a.page_shift;
@@ -311,6 +375,55 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
     return d;
 }
 
+__device__ __forceinline__ Dec invalid_dec()
+{
+    Dec d;
+    d.cls = kClsInvalid;
+    d.bits = 0;
+    d.plane = d.chan = d.range_id = 0;
+    d.page1 = d.issue = d.xfer = 0;
+    return d;
+}
+
+// Lane grouping by key for one step: the previous lane of the same key
+// (pred, -1 for the first), and the group's first and last lanes.  When every
+// active lane has the same key (sequential streams) the ballot match is
+// skipped.
+struct Group {
+    int pred, leader, last;
+    bool uniform;  // every active lane has the same key (wave-uniform)
+};
+
+__device__ __forceinline__ Group group_by(std::uint32_t key, std::uint32_t bits, bool m,
+                                          std::uint64_t active, int lane)
+{
+    const int first = __ffsll(static_cast<long long>(active)) - 1;
+    const std::uint32_t key0 = static_cast<std::uint32_t>(__shfl(static_cast<int>(key), first));
+    Group g;
+    std::uint64_t peers;
+    g.uniform = __ballot(m && key == key0) == active;
+    if (g.uniform) {
+        peers = active;
+    } else {
+        peers = match_key(key, bits, active);
+    }
+    const std::uint64_t below = peers & lanemask_lt(lane);
+    g.pred = (m && below) ? 63 - __clzll(below) : -1;
+    g.leader = m ? __ffsll(static_cast<long long>(peers)) - 1 : lane;
+    g.last = m ? 63 - __clzll(peers) : lane;
+    return g;
+}
+
+__device__ __forceinline__ void scan_group(const Group& g, std::uint64_t& A, std::uint64_t& B,
+                                           int lane)
+{
+    if (g.uniform) {
+        wave_scan(A, B);
+    } else {
+        group_scan(A, B, g.pred, lane);
+    }
+}
+
 __device__ __forceinline__ std::uint64_t plane_service(const KArgs& a, std::uint32_t bits,
                                                        bool hit)
 {
@@ -327,27 +440,31 @@ __device__ __forceinline__ void load_fences(const KArgs& a, std::uint64_t* fence
     }
 }
 
+// Summary pass.  Per plane the tile keeps: the first record (page, issue,
+// class), the (max,+) map of the records after it, and the last page; per
+// channel the map of all its records.  Pages are stored as page + 1 in 32
+// bits (capacity / page_bytes < 2^32 is checked on the host).
 __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
                                                 ChanSum* csum, std::uint64_t* tile_count)
 {
     extern __shared__ std::uint64_t sm[];
     std::uint64_t* fence = sm;
-    std::uint64_t* p_f1 = fence + a.r_nfence;
-    std::uint64_t* p_fi = p_f1 + a.Rp;
+    std::uint64_t* p_fi = fence + a.r_nfence;
     std::uint64_t* p_rA = p_fi + a.Rp;
     std::uint64_t* p_rB = p_rA + a.Rp;
-    std::uint64_t* p_l1 = p_rB + a.Rp;
-    std::uint64_t* c_A = p_l1 + a.Rp;
+    std::uint64_t* c_A = p_rB + a.Rp;
     std::uint64_t* c_B = c_A + a.Rc;
-    std::uint32_t* p_fc = reinterpret_cast<std::uint32_t*>(c_B + a.Rc);
+    std::uint32_t* p_f1 = reinterpret_cast<std::uint32_t*>(c_B + a.Rc);
+    std::uint32_t* p_l1 = p_f1 + a.Rp;
+    std::uint32_t* p_fc = p_l1 + a.Rp;
     const int lane = threadIdx.x;
     load_fences(a, fence, lane);
     for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
-        p_f1[r] = 0;
         p_fi[r] = 0;
         p_rA[r] = 0;
         p_rB[r] = 0;
+        p_f1[r] = 0;
         p_l1[r] = 0;
         p_fc[r] = 0;
     }
@@ -359,87 +476,78 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     const std::size_t tile = blockIdx.x;
     const std::size_t begin = tile * a.tile;
     const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
+    RangeCache rc = empty_cache();
+    uint4 x0 = make_uint4(0, 0, 0, 0), y0 = x0, x1 = x0, y1 = x0;
+    if (begin + lane < end) load_record(rec, begin + lane, x0, y0);
+    if (begin + kWave + lane < end) load_record(rec, begin + kWave + lane, x1, y1);
     std::uint64_t modeled = 0;
     for (std::size_t s = begin; s < end; s += kWave) {
+        const uint4 x = x0, y = y0;
+        x0 = x1;
+        y0 = y1;
+        if (s + 2 * kWave + lane < end) load_record(rec, s + 2 * kWave + lane, x1, y1);
         const std::size_t i = s + lane;
         const bool valid = i < end;
-        Dec d;
-        if (valid) {
-            d = decode(a, fence, rec, i, base_ps);
-        } else {
-            d.cls = kClsInvalid;
-            d.bits = 0;
-            d.plane = d.chan = d.range_id = 0;
-            d.page1 = d.issue = d.xfer = 0;
-        }
+        const Dec d = valid ? decode(a, fence, rc, x, y, base_ps) : invalid_dec();
         const bool m = valid && d.cls == kClsModeled;
         const std::uint64_t active = __ballot(m);
         modeled += __popcll(active);
         if (active == 0) {
             continue;
         }
+        const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
         {  // plane stage
             const std::uint32_t key = m ? d.plane : 0u;
-            const std::uint64_t peers = match_key(key, a.pbits, active);
-            const std::uint64_t below = peers & lanemask_lt(lane);
-            const int pred = (m && below) ? 63 - __clzll(below) : -1;
-            const int leader = m ? __ffsll(static_cast<long long>(peers)) - 1 : lane;
-            const int last = m ? 63 - __clzll(peers) : lane;
-            const std::uint64_t f1 = m ? p_f1[key] : 0ull;
+            const Group g = group_by(key, a.pbits, m, active, lane);
+            const std::uint32_t f1 = m ? p_f1[key] : 0u;
             const bool has = f1 != 0;
-            const bool tfirst = m && pred < 0 && !has;
-            std::uint64_t prev1 = shfl64(d.page1, pred < 0 ? lane : pred);
-            if (pred < 0) {
-                prev1 = m ? p_l1[key] : 0ull;
+            const bool tfirst = m && g.pred < 0 && !has;
+            std::uint32_t prev1 = static_cast<std::uint32_t>(
+                __shfl(static_cast<int>(page1), g.pred < 0 ? lane : g.pred));
+            if (g.pred < 0) {
+                prev1 = m ? p_l1[key] : 0u;
             }
-            const bool hit = a.slots != 0 && m && prev1 == d.page1;
+            const bool hit = a.slots != 0 && m && prev1 == page1;
             const std::uint64_t svc = plane_service(a, d.bits, hit);
             std::uint64_t A = 0, B = 0;
             if (m && !tfirst) {
                 A = svc;
                 B = d.issue + svc;
             }
-            if (a.contention) {
-                group_scan(A, B, pred, lane);
-            }
-            const std::uint64_t l1 = shfl64(d.page1, leader);
-            const std::uint64_t li = shfl64(d.issue, leader);
-            const std::uint32_t lc = static_cast<std::uint32_t>(
-                __shfl(static_cast<int>(d.bits), leader));
-            if (m && lane == last) {
+            scan_group(g, A, B, lane);
+            const std::uint32_t l1 =
+                static_cast<std::uint32_t>(__shfl(static_cast<int>(page1), g.leader));
+            const std::uint64_t li = shfl64(d.issue, g.leader);
+            const std::uint32_t lc =
+                static_cast<std::uint32_t>(__shfl(static_cast<int>(d.bits), g.leader));
+            if (m && lane == g.last) {
                 if (!has) {
                     p_f1[key] = l1;
                     p_fi[key] = li;
                     p_fc[key] = lc;
                 }
-                if (a.contention) {
-                    const std::uint64_t sA = p_rA[key];
-                    const std::uint64_t sB = p_rB[key];
-                    p_rB[key] = umax64(sB + A, B);
-                    p_rA[key] = sA + A;
-                }
-                p_l1[key] = d.page1;
+                const std::uint64_t sA = p_rA[key];
+                const std::uint64_t sB = p_rB[key];
+                p_rB[key] = umax64(sB + A, B);
+                p_rA[key] = sA + A;
+                p_l1[key] = page1;
             }
         }
-        __syncthreads();
         {  // channel stage
             const std::uint32_t key = m ? d.chan : 0u;
-            const std::uint64_t peers = match_key(key, a.cbits, active);
-            const std::uint64_t below = peers & lanemask_lt(lane);
-            const int pred = (m && below) ? 63 - __clzll(below) : -1;
-            const int last = m ? 63 - __clzll(peers) : lane;
+            const Group g = group_by(key, a.cbits, m, active, lane);
             std::uint64_t A = m ? d.xfer : 0ull;
             std::uint64_t B = m ? d.issue + d.xfer : 0ull;
-            group_scan(A, B, pred, lane);
-            if (m && lane == last) {
+            scan_group(g, A, B, lane);
+            if (m && lane == g.last) {
                 const std::uint64_t sA = c_A[key];
                 const std::uint64_t sB = c_B[key];
                 c_B[key] = umax64(sB + A, B);
                 c_A[key] = sA + A;
             }
         }
-        __syncthreads();
     }
+    __syncthreads();
     PlaneSum* ps = psum + tile * a.Rp;
     for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
         PlaneSum v;
@@ -486,31 +594,33 @@ __device__ __forceinline__ PlaneSum plane_compose(const KArgs& a, const PlaneSum
         return s2;
     }
     PlaneSum r = s1;
-    if (a.contention) {
-        const bool hit = a.slots != 0 && s2.fpage1 == s1.lpage1;
-        const std::uint64_t svc = plane_service(a, s2.fcls, hit);
-        // rest1, then the later first record (svc, issue + svc), then rest2
-        std::uint64_t A = s1.rA + svc;
-        std::uint64_t B = umax64(s1.rB + svc, s2.fissue + svc);
-        r.rB = umax64(B + s2.rA, s2.rB);
-        r.rA = A + s2.rA;
-    }
+    const bool hit = a.slots != 0 && s2.fpage1 == s1.lpage1;
+    const std::uint64_t svc = plane_service(a, s2.fcls, hit);
+    // rest1, then the later first record (svc, issue + svc), then rest2; A
+    // is also the service total of the records after the first
+    const std::uint64_t A = s1.rA + svc;
+    const std::uint64_t B = umax64(s1.rB + svc, s2.fissue + svc);
+    r.rB = umax64(B + s2.rA, s2.rB);
+    r.rA = A + s2.rA;
     r.lpage1 = s2.lpage1;
     return r;
 }
 
-__device__ __forceinline__ void plane_apply(const KArgs& a, const PlaneSum& s, std::uint64_t& busy,
-                                            std::uint64_t& tag1)
+// Applies a summary to a plane's state; returns the service it charged.
+__device__ __forceinline__ std::uint64_t plane_apply(const KArgs& a, const PlaneSum& s,
+                                                     std::uint64_t& busy, std::uint64_t& tag1)
 {
     if (s.fpage1 == 0) {
-        return;
+        return 0;
     }
+    const bool hit = a.slots != 0 && tag1 == s.fpage1;
+    const std::uint64_t svc = plane_service(a, s.fcls, hit);
     if (a.contention) {
-        const bool hit = a.slots != 0 && tag1 == s.fpage1;
-        const std::uint64_t b = umax64(busy, s.fissue) + plane_service(a, s.fcls, hit);
+        const std::uint64_t b = umax64(busy, s.fissue) + svc;
         busy = umax64(b + s.rA, s.rB);
     }
     tag1 = s.lpage1;
+    return svc + s.rA;
 }
 
 __device__ __forceinline__ ChanSum chan_compose(const ChanSum& s1, const ChanSum& s2)
@@ -567,30 +677,36 @@ __global__ __launch_bounds__(64) void k_carry_mid(KArgs a, std::size_t ngroups,
                                                   PlaneCarry* gpcarry, std::uint64_t* gccarry,
                                                   std::uint64_t* gseq, std::uint64_t* st_pbusy,
                                                   std::uint64_t* st_ptag, std::uint64_t* st_cbusy,
-                                                  std::uint64_t* st_seq)
+                                                  std::uint64_t* st_seq, std::uint64_t* ptotal,
+                                                  std::uint64_t* ctotal)
 {
     const std::uint32_t t = blockIdx.x * kWave + threadIdx.x;
     if (t < a.Rp) {
         std::uint64_t busy = st_pbusy[t];
         std::uint64_t tag1 = st_ptag[static_cast<std::size_t>(t) * 2];
+        std::uint64_t total = 0;
         for (std::size_t g = 0; g < ngroups; ++g) {
             PlaneCarry c;
             c.busy = busy;
             c.tag1 = tag1;
             gpcarry[g * a.Rp + t] = c;
-            plane_apply(a, gpsum[g * a.Rp + t], busy, tag1);
+            total += plane_apply(a, gpsum[g * a.Rp + t], busy, tag1);
         }
         st_pbusy[t] = busy;
         st_ptag[static_cast<std::size_t>(t) * 2] = tag1;
+        ptotal[t] += total;
     } else if (t < a.Rp + a.Rc) {
         const std::uint32_t c = t - a.Rp;
         std::uint64_t busy = st_cbusy[c];
+        std::uint64_t total = 0;
         for (std::size_t g = 0; g < ngroups; ++g) {
             gccarry[g * a.Rc + c] = busy;
             const ChanSum S = gcsum[g * a.Rc + c];
             busy = umax64(busy + S.A, S.B);
+            total += S.A;
         }
         st_cbusy[c] = busy;
+        ctotal[c] += total;
     } else if (t == a.Rp + a.Rc) {
         std::uint64_t s = *st_seq;
         for (std::size_t g = 0; g < ngroups; ++g) {
@@ -629,7 +745,7 @@ __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
             c.busy = busy;
             c.tag1 = tag1;
             pcarry[t * a.Rp + r] = c;
-            plane_apply(a, psum[t * a.Rp + r], busy, tag1);
+            (void)plane_apply(a, psum[t * a.Rp + r], busy, tag1);
         }
     } else if (r < a.Rp + a.Rc) {
         const std::uint32_t c = r - a.Rp;
@@ -676,28 +792,23 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
                                               const std::uint64_t* ccarry,
                                               const std::uint64_t* tile_seq,
                                               std::uint64_t* completion, std::uint8_t* status,
-                                              std::uint64_t* g_ptotal, std::uint64_t* g_ctotal,
-                                              DevReport* rep)
+                                              DevReport* tile_rep)
 {
     extern __shared__ std::uint64_t sm[];
     std::uint64_t* fence = sm;
     std::uint64_t* p_busy = fence + a.r_nfence;
-    std::uint64_t* p_tag = p_busy + a.Rp;
-    std::uint64_t* p_tot = p_tag + a.Rp;
-    std::uint64_t* c_busy = p_tot + a.Rp;
-    std::uint64_t* c_tot = c_busy + a.Rc;
+    std::uint64_t* c_busy = p_busy + a.Rp;
+    std::uint32_t* p_tag = reinterpret_cast<std::uint32_t*>(c_busy + a.Rc);
     const int lane = threadIdx.x;
     const std::size_t tile = blockIdx.x;
     load_fences(a, fence, lane);
     for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
         const PlaneCarry c = pcarry[tile * a.Rp + r];
         p_busy[r] = c.busy;
-        p_tag[r] = c.tag1;
-        p_tot[r] = 0;
+        p_tag[r] = static_cast<std::uint32_t>(c.tag1);
     }
     for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
         c_busy[r] = ccarry[tile * a.Rc + r];
-        c_tot[r] = 0;
     }
     __syncthreads();
     const std::size_t begin = tile * a.tile;
@@ -706,77 +817,63 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
     std::uint64_t n_rec = 0, n_mod = 0, n_byp = 0, n_uns = 0, n_rd = 0, n_wr = 0;
     std::uint64_t n_hit = 0, n_prog = 0, n_hyb = 0, mk = 0, lat_lo = 0, lat_hi = 0;
     std::uint64_t lat_max = 0, svc_sum = 0;
+    RangeCache rc = empty_cache();
+    uint4 x0 = make_uint4(0, 0, 0, 0), y0 = x0, x1 = x0, y1 = x0;
+    if (begin + lane < end) load_record(rec, begin + lane, x0, y0);
+    if (begin + kWave + lane < end) load_record(rec, begin + kWave + lane, x1, y1);
     for (std::size_t s = begin; s < end; s += kWave) {
+        const uint4 x = x0, y = y0;
+        x0 = x1;
+        y0 = y1;
+        if (s + 2 * kWave + lane < end) load_record(rec, s + 2 * kWave + lane, x1, y1);
         const std::size_t i = s + lane;
         const bool valid = i < end;
-        Dec d;
-        if (valid) {
-            d = decode(a, fence, rec, i, base_ps);
-        } else {
-            d.cls = kClsInvalid;
-            d.bits = 0;
-            d.plane = d.chan = d.range_id = 0;
-            d.page1 = d.issue = d.xfer = 0;
-        }
+        const Dec d = valid ? decode(a, fence, rc, x, y, base_ps) : invalid_dec();
         const bool m = valid && d.cls == kClsModeled;
         const std::uint64_t active = __ballot(m);
         std::uint8_t st = static_cast<std::uint8_t>(d.cls);
         std::uint64_t done = 0;
         if (active != 0) {
+            const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
             std::uint64_t pd, cd;
             std::uint64_t svc;
             bool hit;
             {  // plane stage
                 const std::uint32_t key = m ? d.plane : 0u;
-                const std::uint64_t peers = match_key(key, a.pbits, active);
-                const std::uint64_t below = peers & lanemask_lt(lane);
-                const int pred = (m && below) ? 63 - __clzll(below) : -1;
-                const int last = m ? 63 - __clzll(peers) : lane;
-                std::uint64_t prev1 = shfl64(d.page1, pred < 0 ? lane : pred);
-                if (pred < 0) {
-                    prev1 = m ? p_tag[key] : 0ull;
+                const Group g = group_by(key, a.pbits, m, active, lane);
+                std::uint32_t prev1 = static_cast<std::uint32_t>(
+                    __shfl(static_cast<int>(page1), g.pred < 0 ? lane : g.pred));
+                if (g.pred < 0) {
+                    prev1 = m ? p_tag[key] : 0u;
                 }
-                hit = a.slots != 0 && m && prev1 == d.page1;
+                hit = a.slots != 0 && m && prev1 == page1;
                 svc = plane_service(a, d.bits, hit);
                 if (a.contention) {
                     std::uint64_t A = m ? svc : 0ull;
                     std::uint64_t B = m ? d.issue + svc : 0ull;
-                    group_scan(A, B, pred, lane);
+                    scan_group(g, A, B, lane);
                     pd = m ? umax64(p_busy[key] + A, B) : 0ull;
                 } else {
                     pd = d.issue + svc;
                 }
-                if (m && lane == last) {
+                if (m && lane == g.last) {
                     if (a.contention) {
                         p_busy[key] = pd;
                     }
-                    p_tag[key] = d.page1;
-                }
-                if (m && svc != 0) {
-                    atomicAdd(reinterpret_cast<unsigned long long*>(&p_tot[key]),
-                              static_cast<unsigned long long>(svc));
+                    p_tag[key] = page1;
                 }
             }
-            __syncthreads();
             {  // channel stage
                 const std::uint32_t key = m ? d.chan : 0u;
-                const std::uint64_t peers = match_key(key, a.cbits, active);
-                const std::uint64_t below = peers & lanemask_lt(lane);
-                const int pred = (m && below) ? 63 - __clzll(below) : -1;
-                const int last = m ? 63 - __clzll(peers) : lane;
+                const Group g = group_by(key, a.cbits, m, active, lane);
                 std::uint64_t A = m ? d.xfer : 0ull;
                 std::uint64_t B = m ? d.issue + d.xfer : 0ull;
-                group_scan(A, B, pred, lane);
+                scan_group(g, A, B, lane);
                 cd = m ? umax64(c_busy[key] + A, B) : 0ull;
-                if (m && lane == last) {
+                if (m && lane == g.last) {
                     c_busy[key] = cd;
                 }
-                if (m && d.xfer != 0) {
-                    atomicAdd(reinterpret_cast<unsigned long long*>(&c_tot[key]),
-                              static_cast<unsigned long long>(d.xfer));
-                }
             }
-            __syncthreads();
             if (m) {
                 done = umax64(pd, cd);
                 const std::uint64_t rank = __popcll(active & lanemask_lt(lane));
@@ -828,60 +925,81 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
             }
         }
     }
-    __syncthreads();
-    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
-        if (p_tot[r] != 0) {
-            atomicAdd(reinterpret_cast<unsigned long long*>(&g_ptotal[r]),
-                      static_cast<unsigned long long>(p_tot[r]));
-        }
-    }
-    for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
-        if (c_tot[r] != 0) {
-            atomicAdd(reinterpret_cast<unsigned long long*>(&g_ctotal[r]),
-                      static_cast<unsigned long long>(c_tot[r]));
-        }
-    }
     // 128-bit latency sum: reduce the high words, then the low words with
     // their carries.
     std::uint64_t hi = wave_sum(lat_hi);
-    std::uint64_t lo_acc = 0, carry = 0;
-    {
-        std::uint64_t v = lat_lo;
-        for (int o = 32; o > 0; o >>= 1) {
-            const std::uint64_t other = shfl64(v, threadIdx.x ^ o);
-            const std::uint64_t oc = shfl64(carry, threadIdx.x ^ o);
-            const std::uint64_t sum = v + other;
-            carry = carry + oc + (sum < v ? 1u : 0u);
-            v = sum;
-        }
-        lo_acc = v;
+    std::uint64_t carry = 0;
+    std::uint64_t v = lat_lo;
+    for (int o = 32; o > 0; o >>= 1) {
+        const std::uint64_t other = shfl64(v, threadIdx.x ^ o);
+        const std::uint64_t oc = shfl64(carry, threadIdx.x ^ o);
+        const std::uint64_t sum = v + other;
+        carry = carry + oc + (sum < v ? 1u : 0u);
+        v = sum;
     }
     hi += carry;
-    const std::uint64_t t_rec = wave_sum(n_rec), t_mod = wave_sum(n_mod);
-    const std::uint64_t t_byp = wave_sum(n_byp), t_uns = wave_sum(n_uns);
-    const std::uint64_t t_rd = wave_sum(n_rd), t_wr = wave_sum(n_wr);
-    const std::uint64_t t_hit = wave_sum(n_hit), t_prog = wave_sum(n_prog);
-    const std::uint64_t t_hyb = wave_sum(n_hyb), t_svc = wave_sum(svc_sum);
-    const std::uint64_t t_mk = wave_max(mk), t_lmax = wave_max(lat_max);
-    if (lane == 0) {
-        unsigned long long* v = rep->v;
-        atomicAdd(&v[R_RECORDS], t_rec);
-        atomicAdd(&v[R_MODELED], t_mod);
-        atomicAdd(&v[R_BYPASS], t_byp);
-        atomicAdd(&v[R_UNSUPPORTED], t_uns);
-        atomicAdd(&v[R_READS], t_rd);
-        atomicAdd(&v[R_WRITES], t_wr);
-        atomicAdd(&v[R_HITS], t_hit);
-        atomicAdd(&v[R_PROGRAMS], t_prog);
-        atomicAdd(&v[R_HYBRID], t_hyb);
-        atomicMax(&v[R_MAKESPAN], t_mk);
-        const unsigned long long old = atomicAdd(&v[R_LAT_LO], lo_acc);
-        const unsigned long long c = (old + lo_acc < old) ? 1ull : 0ull;
-        if (hi + c != 0) {
-            atomicAdd(&v[R_LAT_HI], hi + c);
+    const std::uint64_t vals[14] = {
+        wave_sum(n_rec), wave_sum(n_mod), wave_sum(n_byp), wave_sum(n_uns), wave_sum(n_rd),
+        wave_sum(n_wr),  wave_sum(n_hit), wave_sum(n_prog), wave_sum(n_hyb), wave_max(mk),
+        v,               hi,              wave_max(lat_max), wave_sum(svc_sum)};
+    if (lane < 14) {
+        unsigned long long out = 0;
+#pragma unroll
+        for (int k = 0; k < 14; ++k) {
+            out = lane == k ? vals[k] : out;
         }
-        atomicMax(&v[R_LAT_MAX], t_lmax);
-        atomicAdd(&v[R_SERVICE], t_svc);
+        tile_rep[tile].v[lane] = out;
+    }
+}
+
+// Folds the per-tile report partials into one report (sums, maxima and the
+// 128-bit latency sum).  One block.
+__global__ __launch_bounds__(256) void k_report(const DevReport* tile_rep, std::size_t ntiles,
+                                                DevReport* rep)
+{
+    __shared__ std::uint64_t part[256][15];
+    const int t = threadIdx.x;
+    std::uint64_t acc[14] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    std::uint64_t carry = 0;
+    for (std::size_t i = t; i < ntiles; i += 256) {
+        const DevReport& r = tile_rep[i];
+        for (int k = 0; k < 14; ++k) {
+            if (k == R_MAKESPAN || k == R_LAT_MAX) {
+                acc[k] = umax64(acc[k], r.v[k]);
+            } else if (k == R_LAT_LO) {
+                const std::uint64_t s2 = acc[k] + r.v[k];
+                carry += s2 < acc[k] ? 1u : 0u;
+                acc[k] = s2;
+            } else {
+                acc[k] += r.v[k];
+            }
+        }
+    }
+    acc[R_LAT_HI] += carry;
+    for (int k = 0; k < 14; ++k) {
+        part[t][k] = acc[k];
+    }
+    __syncthreads();
+    if (t == 0) {
+        std::uint64_t out[14] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        std::uint64_t c2 = 0;
+        for (int j = 0; j < 256; ++j) {
+            for (int k = 0; k < 14; ++k) {
+                if (k == R_MAKESPAN || k == R_LAT_MAX) {
+                    out[k] = umax64(out[k], part[j][k]);
+                } else if (k == R_LAT_LO) {
+                    const std::uint64_t s2 = out[k] + part[j][k];
+                    c2 += s2 < out[k] ? 1u : 0u;
+                    out[k] = s2;
+                } else {
+                    out[k] += part[j][k];
+                }
+            }
+        }
+        out[R_LAT_HI] += c2;
+        for (int k = 0; k < 14; ++k) {
+            rep->v[k] = out[k];
+        }
     }
 }
 
@@ -926,6 +1044,7 @@ struct engine {
     std::uint64_t* d_gccarry{nullptr};
     std::uint64_t* d_gcount{nullptr};
     std::uint64_t* d_gseq{nullptr};
+    DevReport* d_tile_rep{nullptr};
     hipEvent_t ev[4]{};
     float last_ms[3]{0, 0, 0};
     std::uint64_t burst{0};
@@ -984,6 +1103,7 @@ void free_scratch(engine* e)
     hfree(e->d_gccarry);
     hfree(e->d_gcount);
     hfree(e->d_gseq);
+    hfree(e->d_tile_rep);
     e->tile_cap = 0;
 }
 
@@ -1006,7 +1126,7 @@ int ensure_scratch(engine* e, std::size_t ntiles)
     if (halloc(e->d_gpsum, gcap * rp) != hipSuccess || halloc(e->d_gcsum, gcap * rc) != hipSuccess ||
         halloc(e->d_gpcarry, gcap * rp) != hipSuccess ||
         halloc(e->d_gccarry, gcap * rc) != hipSuccess || halloc(e->d_gcount, gcap) != hipSuccess ||
-        halloc(e->d_gseq, gcap) != hipSuccess) {
+        halloc(e->d_gseq, gcap) != hipSuccess || halloc(e->d_tile_rep, cap) != hipSuccess) {
         free_scratch(e);
         return HBFSIM_CUDA_ERROR;
     }
@@ -1077,12 +1197,23 @@ int upload_ranges(engine* e, hipStream_t stream)
 
 std::size_t lds_summary(const KArgs& a)
 {
-    return 8ull * (a.r_nfence + 5ull * a.Rp + 2ull * a.Rc) + 4ull * a.Rp;
+    return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 12ull * a.Rp;
 }
 
 std::size_t lds_apply(const KArgs& a)
 {
-    return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc);
+    return 8ull * (a.r_nfence + 1ull * a.Rp + 1ull * a.Rc) + 4ull * a.Rp;
+}
+
+// Records per tile when the configuration leaves it open: the largest power
+// of two up to 16384 that still gives every CU eight tiles, at least 256.
+std::uint32_t auto_tile(std::size_t n)
+{
+    std::uint32_t t = 16384;
+    while (t > 256 && (n + t - 1) / t < 2048) {
+        t >>= 1;
+    }
+    return t;
 }
 
 }  // namespace
@@ -1093,7 +1224,7 @@ int engine_create(const engine_config& c, engine** out)
     const std::uint32_t rp = c.n_planes(), rc = c.n_channels();
     if (c.channels == 0 || c.ways == 0 || c.dies == 0 || c.planes == 0 || c.page_shift < 9 ||
         c.page_shift > 31 || c.slots > 2 || c.xfer_den == 0 || c.xfer_quantum == 0 ||
-        c.tile == 0 || c.tile % kWave != 0) {
+        c.tile % kWave != 0) {
         return HBFSIM_INVALID_ARGUMENT;
     }
     if (rp > kMaxPlanes || rc > kMaxChannels) {
@@ -1270,7 +1401,9 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
             return st;
         }
     }
-    const std::size_t ntiles = (n + e->cfg.tile - 1) / e->cfg.tile;
+    KArgs a = e->args;
+    a.tile = e->cfg.tile != 0 ? e->cfg.tile : auto_tile(n);
+    const std::size_t ntiles = (n + a.tile - 1) / a.tile;
     if (ntiles > 0x7fffffffull) {
         return HBFSIM_UNSUPPORTED;
     }
@@ -1278,15 +1411,11 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
     if (st != HBFSIM_OK) {
         return st;
     }
-    const KArgs& a = e->args;
     const std::size_t lds_a = lds_summary(a), lds_c = lds_apply(a);
     if (lds_a > 65536 || lds_c > 65536) {
         return HBFSIM_UNSUPPORTED;
     }
-    hipError_t err = hipMemsetAsync(e->d_rep, 0, sizeof(DevReport), stream);
-    if (err != hipSuccess) {
-        return HBFSIM_CUDA_ERROR;
-    }
+    hipError_t err = hipSuccess;
     const dim3 grid(static_cast<unsigned>(ntiles));
     const unsigned carry_blocks = (a.Rp + a.Rc + 1 + kWave - 1) / kWave;
     (void)hipEventRecord(e->ev[0], stream);
@@ -1302,15 +1431,16 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
                            e->d_gcount);
         hipLaunchKernelGGL(k_carry_mid, dim3(carry_blocks), dim3(kWave), 0, stream, a, ngroups,
                            e->d_gpsum, e->d_gcsum, e->d_gcount, e->d_gpcarry, e->d_gccarry,
-                           e->d_gseq, e->d_pbusy, e->d_ptag, e->d_cbusy, e->d_seq);
+                           e->d_gseq, e->d_pbusy, e->d_ptag, e->d_cbusy, e->d_seq, e->d_ptot,
+                           e->d_ctot);
         hipLaunchKernelGGL(k_carry_down, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
                            e->d_psum, e->d_csum, e->d_tcount, e->d_gpcarry, e->d_gccarry,
                            e->d_gseq, e->d_pcarry, e->d_ccarry, e->d_tseq);
     }
     (void)hipEventRecord(e->ev[2], stream);
     hipLaunchKernelGGL(k_apply, grid, dim3(kWave), lds_c, stream, a, d_rec, n, base_ps,
-                       e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status, e->d_ptot,
-                       e->d_ctot, e->d_rep);
+                       e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status, e->d_tile_rep);
+    hipLaunchKernelGGL(k_report, dim3(1), dim3(256), 0, stream, e->d_tile_rep, ntiles, e->d_rep);
     (void)hipEventRecord(e->ev[3], stream);
     err = hipGetLastError();
     if (err == hipSuccess)

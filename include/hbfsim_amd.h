@@ -223,7 +223,8 @@ typedef struct hbfsim_amd_engine_options {
     uint32_t ways;                 /* chips per channel (default 1) */
     uint64_t xfer_quantum_ps;      /* transfer rounded up to this (1) */
     uint64_t channel_bandwidth_bytes_per_s; /* 0: aggregate / channels */
-    uint32_t tile_records;         /* records per tile, multiple of 64 */
+    uint32_t tile_records;         /* records per tile, multiple of 64;
+                                      0 chooses per run (default) */
     uint32_t reserved0;
 } hbfsim_amd_engine_options;
 
