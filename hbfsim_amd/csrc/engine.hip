@@ -110,6 +110,7 @@ struct Dec {
     std::uint64_t page1;   // media page + 1
     std::uint64_t issue;
     std::uint64_t xfer;
+    std::uint64_t xbytes;  // bytes the channel moves
 };
 
 __device__ __forceinline__ std::uint64_t shfl64(std::uint64_t v, int src)
@@ -210,6 +211,36 @@ __device__ __forceinline__ void wave_scan(std::uint64_t& A, std::uint64_t& B)
     dpp_scan_step<0x143, 0xC>(A, B);
 }
 
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ void dpp_scan_step32(std::uint32_t& A, std::uint32_t& B)
+{
+    const std::uint32_t pA = static_cast<std::uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(A), Ctrl, RowMask, 0xF, false));
+    const std::uint32_t pB = static_cast<std::uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(B), Ctrl, RowMask, 0xF, false));
+    const std::uint32_t nb = pB + A;
+    B = nb > B ? nb : B;
+    A = pA + A;
+}
+
+// Two independent whole-wave scans in 32 bits, interleaved for ILP.
+__device__ __forceinline__ void wave_scan32x2(std::uint32_t& A1, std::uint32_t& B1,
+                                              std::uint32_t& A2, std::uint32_t& B2)
+{
+    dpp_scan_step32<0x111, 0xF>(A1, B1);
+    dpp_scan_step32<0x111, 0xF>(A2, B2);
+    dpp_scan_step32<0x112, 0xF>(A1, B1);
+    dpp_scan_step32<0x112, 0xF>(A2, B2);
+    dpp_scan_step32<0x114, 0xF>(A1, B1);
+    dpp_scan_step32<0x114, 0xF>(A2, B2);
+    dpp_scan_step32<0x118, 0xF>(A1, B1);
+    dpp_scan_step32<0x118, 0xF>(A2, B2);
+    dpp_scan_step32<0x142, 0xA>(A1, B1);
+    dpp_scan_step32<0x142, 0xA>(A2, B2);
+    dpp_scan_step32<0x143, 0xC>(A1, B1);
+    dpp_scan_step32<0x143, 0xC>(A2, B2);
+}
+
 // find_range_index (hbf_device.cuh:826-841): upper_bound(base) - 1 over the
 // sorted range table.  The top level runs over every `stride`-th base,
 // staged in LDS; the bottom level over at most `stride` bases in memory.
@@ -307,6 +338,7 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
     d.range_id = 0;
     d.page1 = 0;
     d.xfer = 0;
+    d.xbytes = 0;
     if (!(addr >= rc.base && addr < rc.end)) {
         const std::uint32_t idx = find_range(a, fence, addr);
         if (idx == a.r_count || addr < a.r_base[idx] ||
@@ -354,7 +386,7 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
     if (op == 1 && (a.every_write || (media & page_mask) + bytes == page_bytes)) {
         d.bits |= 2u;
     }
-    d.xfer = xfer_ps(a, a.transfer_page ? page_bytes : bytes);
+    d.xbytes = a.transfer_page ? page_bytes : bytes;
     if (!a.flat) {
         std::uint32_t c[4];
         if (a.pow2) {
@@ -381,8 +413,47 @@ __device__ __forceinline__ Dec invalid_dec()
     d.cls = kClsInvalid;
     d.bits = 0;
     d.plane = d.chan = d.range_id = 0;
-    d.page1 = d.issue = d.xfer = 0;
+    d.page1 = d.issue = d.xfer = d.xbytes = 0;
     return d;
+}
+
+// Transfer time of every lane's access.  When all modeled lanes move the same
+// byte count (the usual case) it is computed once, in scalar registers.
+__device__ __forceinline__ std::uint64_t lane_xfer(const KArgs& a, const Dec& d, bool m,
+                                                   std::uint64_t active)
+{
+    const int first = __ffsll(static_cast<long long>(active)) - 1;
+    const std::uint32_t lo = static_cast<std::uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(static_cast<std::uint32_t>(d.xbytes)), first));
+    const std::uint32_t hi = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(
+        static_cast<int>(static_cast<std::uint32_t>(d.xbytes >> 32)), first));
+    const std::uint64_t xb0 = (static_cast<std::uint64_t>(hi) << 32) | lo;
+    if (__ballot(m && d.xbytes != xb0) == 0) {
+        return xfer_ps(a, xb0);
+    }
+    return m ? xfer_ps(a, d.xbytes) : 0ull;
+}
+
+// Time origin for 32-bit scans: the first active lane's issue time.  The
+// narrow path is taken only when, for every modeled lane, issue - origin is
+// in [0, 2^30) and both services are below 2^24, so every partial sum of a
+// step fits 32 bits.  (0, 0) in relative form stands for (0, origin), which
+// acts as the identity on every state reachable in the step.
+struct Narrow {
+    std::uint64_t origin;
+    bool ok;
+};
+
+__device__ __forceinline__ Narrow narrow_check(const Dec& d, bool m, std::uint64_t active,
+                                               std::uint64_t svc1, std::uint64_t svc2)
+{
+    const int first = __ffsll(static_cast<long long>(active)) - 1;
+    Narrow n;
+    n.origin = shfl64(d.issue, first);
+    const bool bad = m && (d.issue < n.origin || d.issue - n.origin >= (1ull << 30) ||
+                           svc1 >= (1ull << 24) || svc2 >= (1ull << 24));
+    n.ok = __ballot(bad) == 0;
+    return n;
 }
 
 // Lane grouping by key for one step: the previous lane of the same key
@@ -422,6 +493,33 @@ __device__ __forceinline__ void scan_group(const Group& g, std::uint64_t& A, std
     } else {
         group_scan(A, B, g.pred, lane);
     }
+}
+
+// Scans a step's plane maps and channel maps.  When both are single-key
+// steps and the narrow check passes, both run as interleaved 32-bit DPP scans
+// relative to the time origin; otherwise each runs exactly in 64 bits.
+__device__ __forceinline__ void scan_pair(const Group& gp, std::uint64_t& Ap, std::uint64_t& Bp,
+                                          const Group& gc, std::uint64_t& Ac, std::uint64_t& Bc,
+                                          const Dec& d, bool m, std::uint64_t active,
+                                          std::uint64_t svc, std::uint64_t xfer, int lane)
+{
+    if (gp.uniform && gc.uniform) {
+        const Narrow nw = narrow_check(d, m, active, svc, xfer);
+        if (nw.ok) {
+            std::uint32_t ap = static_cast<std::uint32_t>(Ap);
+            std::uint32_t bp = Bp == 0 ? 0u : static_cast<std::uint32_t>(Bp - nw.origin);
+            std::uint32_t ac = static_cast<std::uint32_t>(Ac);
+            std::uint32_t bc = Bc == 0 ? 0u : static_cast<std::uint32_t>(Bc - nw.origin);
+            wave_scan32x2(ap, bp, ac, bc);
+            Ap = ap;
+            Bp = nw.origin + bp;
+            Ac = ac;
+            Bc = nw.origin + bc;
+            return;
+        }
+    }
+    scan_group(gp, Ap, Bp, lane);
+    scan_group(gc, Ac, Bc, lane);
 }
 
 __device__ __forceinline__ std::uint64_t plane_service(const KArgs& a, std::uint32_t bits,
@@ -495,56 +593,54 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
         if (active == 0) {
             continue;
         }
+        const std::uint64_t xfer = lane_xfer(a, d, m, active);
         const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
-        {  // plane stage
-            const std::uint32_t key = m ? d.plane : 0u;
-            const Group g = group_by(key, a.pbits, m, active, lane);
-            const std::uint32_t f1 = m ? p_f1[key] : 0u;
-            const bool has = f1 != 0;
-            const bool tfirst = m && g.pred < 0 && !has;
-            std::uint32_t prev1 = static_cast<std::uint32_t>(
-                __shfl(static_cast<int>(page1), g.pred < 0 ? lane : g.pred));
-            if (g.pred < 0) {
-                prev1 = m ? p_l1[key] : 0u;
-            }
-            const bool hit = a.slots != 0 && m && prev1 == page1;
-            const std::uint64_t svc = plane_service(a, d.bits, hit);
-            std::uint64_t A = 0, B = 0;
-            if (m && !tfirst) {
-                A = svc;
-                B = d.issue + svc;
-            }
-            scan_group(g, A, B, lane);
-            const std::uint32_t l1 =
-                static_cast<std::uint32_t>(__shfl(static_cast<int>(page1), g.leader));
-            const std::uint64_t li = shfl64(d.issue, g.leader);
-            const std::uint32_t lc =
-                static_cast<std::uint32_t>(__shfl(static_cast<int>(d.bits), g.leader));
-            if (m && lane == g.last) {
-                if (!has) {
-                    p_f1[key] = l1;
-                    p_fi[key] = li;
-                    p_fc[key] = lc;
-                }
-                const std::uint64_t sA = p_rA[key];
-                const std::uint64_t sB = p_rB[key];
-                p_rB[key] = umax64(sB + A, B);
-                p_rA[key] = sA + A;
-                p_l1[key] = page1;
-            }
+        const std::uint32_t pkey = m ? d.plane : 0u;
+        const std::uint32_t ckey = m ? d.chan : 0u;
+        const Group gp = group_by(pkey, a.pbits, m, active, lane);
+        const Group gc = group_by(ckey, a.cbits, m, active, lane);
+        // state reads come before this step's writes
+        const std::uint32_t f1 = m ? p_f1[pkey] : 0u;
+        const std::uint32_t last_page = m ? p_l1[pkey] : 0u;
+        const bool has = f1 != 0;
+        const bool tfirst = m && gp.pred < 0 && !has;
+        std::uint32_t prev1 = static_cast<std::uint32_t>(
+            __shfl(static_cast<int>(page1), gp.pred < 0 ? lane : gp.pred));
+        if (gp.pred < 0) {
+            prev1 = last_page;
         }
-        {  // channel stage
-            const std::uint32_t key = m ? d.chan : 0u;
-            const Group g = group_by(key, a.cbits, m, active, lane);
-            std::uint64_t A = m ? d.xfer : 0ull;
-            std::uint64_t B = m ? d.issue + d.xfer : 0ull;
-            scan_group(g, A, B, lane);
-            if (m && lane == g.last) {
-                const std::uint64_t sA = c_A[key];
-                const std::uint64_t sB = c_B[key];
-                c_B[key] = umax64(sB + A, B);
-                c_A[key] = sA + A;
+        const bool hit = a.slots != 0 && m && prev1 == page1;
+        const std::uint64_t svc = plane_service(a, d.bits, hit);
+        std::uint64_t Ap = 0, Bp = 0;
+        if (m && !tfirst) {
+            Ap = svc;
+            Bp = d.issue + svc;
+        }
+        std::uint64_t Ac = m ? xfer : 0ull;
+        std::uint64_t Bc = m ? d.issue + xfer : 0ull;
+        scan_pair(gp, Ap, Bp, gc, Ac, Bc, d, m, active, svc, xfer, lane);
+        const std::uint32_t l1 =
+            static_cast<std::uint32_t>(__shfl(static_cast<int>(page1), gp.leader));
+        const std::uint64_t li = shfl64(d.issue, gp.leader);
+        const std::uint32_t lc =
+            static_cast<std::uint32_t>(__shfl(static_cast<int>(d.bits), gp.leader));
+        if (m && lane == gp.last) {
+            if (!has) {
+                p_f1[pkey] = l1;
+                p_fi[pkey] = li;
+                p_fc[pkey] = lc;
             }
+            const std::uint64_t sA = p_rA[pkey];
+            const std::uint64_t sB = p_rB[pkey];
+            p_rB[pkey] = umax64(sB + Ap, Bp);
+            p_rA[pkey] = sA + Ap;
+            p_l1[pkey] = page1;
+        }
+        if (m && lane == gc.last) {
+            const std::uint64_t sA = c_A[ckey];
+            const std::uint64_t sB = c_B[ckey];
+            c_B[ckey] = umax64(sB + Ac, Bc);
+            c_A[ckey] = sA + Ac;
         }
     }
     __syncthreads();
@@ -834,45 +930,43 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
         std::uint8_t st = static_cast<std::uint8_t>(d.cls);
         std::uint64_t done = 0;
         if (active != 0) {
+            const std::uint64_t xfer = lane_xfer(a, d, m, active);
             const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
-            std::uint64_t pd, cd;
-            std::uint64_t svc;
-            bool hit;
-            {  // plane stage
-                const std::uint32_t key = m ? d.plane : 0u;
-                const Group g = group_by(key, a.pbits, m, active, lane);
-                std::uint32_t prev1 = static_cast<std::uint32_t>(
-                    __shfl(static_cast<int>(page1), g.pred < 0 ? lane : g.pred));
-                if (g.pred < 0) {
-                    prev1 = m ? p_tag[key] : 0u;
-                }
-                hit = a.slots != 0 && m && prev1 == page1;
-                svc = plane_service(a, d.bits, hit);
-                if (a.contention) {
-                    std::uint64_t A = m ? svc : 0ull;
-                    std::uint64_t B = m ? d.issue + svc : 0ull;
-                    scan_group(g, A, B, lane);
-                    pd = m ? umax64(p_busy[key] + A, B) : 0ull;
-                } else {
-                    pd = d.issue + svc;
-                }
-                if (m && lane == g.last) {
-                    if (a.contention) {
-                        p_busy[key] = pd;
-                    }
-                    p_tag[key] = page1;
-                }
+            const std::uint32_t pkey = m ? d.plane : 0u;
+            const std::uint32_t ckey = m ? d.chan : 0u;
+            const Group gp = group_by(pkey, a.pbits, m, active, lane);
+            const Group gc = group_by(ckey, a.cbits, m, active, lane);
+            // state reads come before this step's writes
+            const std::uint32_t tag = m ? p_tag[pkey] : 0u;
+            const std::uint64_t pbusy = m ? p_busy[pkey] : 0ull;
+            const std::uint64_t cbusy = m ? c_busy[ckey] : 0ull;
+            std::uint32_t prev1 = static_cast<std::uint32_t>(
+                __shfl(static_cast<int>(page1), gp.pred < 0 ? lane : gp.pred));
+            if (gp.pred < 0) {
+                prev1 = tag;
             }
-            {  // channel stage
-                const std::uint32_t key = m ? d.chan : 0u;
-                const Group g = group_by(key, a.cbits, m, active, lane);
-                std::uint64_t A = m ? d.xfer : 0ull;
-                std::uint64_t B = m ? d.issue + d.xfer : 0ull;
-                scan_group(g, A, B, lane);
-                cd = m ? umax64(c_busy[key] + A, B) : 0ull;
-                if (m && lane == g.last) {
-                    c_busy[key] = cd;
+            const bool hit = a.slots != 0 && m && prev1 == page1;
+            const std::uint64_t svc = plane_service(a, d.bits, hit);
+            std::uint64_t Ap = m ? svc : 0ull;
+            std::uint64_t Bp = m ? d.issue + svc : 0ull;
+            std::uint64_t Ac = m ? xfer : 0ull;
+            std::uint64_t Bc = m ? d.issue + xfer : 0ull;
+            if (a.contention) {
+                scan_pair(gp, Ap, Bp, gc, Ac, Bc, d, m, active, svc, xfer, lane);
+            } else {
+                scan_group(gc, Ac, Bc, lane);
+            }
+            const std::uint64_t pd =
+                a.contention ? (m ? umax64(pbusy + Ap, Bp) : 0ull) : d.issue + svc;
+            const std::uint64_t cd = m ? umax64(cbusy + Ac, Bc) : 0ull;
+            if (m && lane == gp.last) {
+                if (a.contention) {
+                    p_busy[pkey] = pd;
                 }
+                p_tag[pkey] = page1;
+            }
+            if (m && lane == gc.last) {
+                c_busy[ckey] = cd;
             }
             if (m) {
                 done = umax64(pd, cd);
@@ -906,7 +1000,7 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
                 const std::uint64_t lat = done - d.issue;
                 add128(lat_lo, lat_hi, lat);
                 lat_max = umax64(lat_max, lat);
-                svc_sum += umax64(svc, d.xfer);
+                svc_sum += umax64(svc, xfer);
             }
             seq += __popcll(active);
         }

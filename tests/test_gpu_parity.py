@@ -309,3 +309,27 @@ def test_fast_reference_preset_matches_single_tail_recurrence():
         assert grep["service_sum_ps"] == modeled * 1000
     finally:
         p.close()
+
+
+@pytest.mark.parametrize("gap_ps", [1_000, 40_000_000])
+def test_sequential_writes_and_wide_steps(gap_ps):
+    """Single-key steps whose values need 64 bits: page-filling sequential
+    writes (tPROG = 200 us) and issue gaps beyond 2^30 ps inside a step,
+    next to steps that take the 32-bit path."""
+    base = 0x6100_0000_0000
+    page = 16384
+    ranges = [(base, 64 * page, 3)]
+    n = 20_000
+    j = np.arange(n, dtype=np.uint64)
+    rec = np.zeros((n, 4), np.uint64)
+    rec[:, 0] = np.uint64(base) + (j * np.uint64(128)) % np.uint64(64 * page)
+    rec[:, 1] = 128
+    rec[:, 3] = ((j // np.uint64(2048)) % np.uint64(2)).astype(np.uint64)  # read/write phases
+    rec[:, 2] = j * np.uint64(gap_ps)
+    p = parity.Pair(C0, ranges)
+    try:
+        (_, _, grep), _ = check(p, rec, f"sequential rw gap {gap_ps}")
+        assert grep["programs"] > 0 and grep["page_hits"] > 0
+        p.check_state()
+    finally:
+        p.close()
