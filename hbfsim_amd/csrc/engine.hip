@@ -241,6 +241,48 @@ __device__ __forceinline__ void wave_scan32x2(std::uint32_t& A1, std::uint32_t& 
     dpp_scan_step32<0x143, 0xC>(A2, B2);
 }
 
+// Inclusive prefix maximum across the wave (DPP; lanes without a source take
+// 0, the identity for unsigned max).
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ std::uint32_t dpp32(std::uint32_t v)
+{
+    return static_cast<std::uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), Ctrl, RowMask, 0xF, false));
+}
+
+__device__ __forceinline__ std::uint32_t wave_prefix_max32(std::uint32_t v)
+{
+    std::uint32_t t;
+    t = dpp32<0x111, 0xF>(v); v = v > t ? v : t;
+    t = dpp32<0x112, 0xF>(v); v = v > t ? v : t;
+    t = dpp32<0x114, 0xF>(v); v = v > t ? v : t;
+    t = dpp32<0x118, 0xF>(v); v = v > t ? v : t;
+    t = dpp32<0x142, 0xA>(v); v = v > t ? v : t;
+    t = dpp32<0x143, 0xC>(v); v = v > t ? v : t;
+    return v;
+}
+
+__device__ __forceinline__ std::uint64_t wave_prefix_max64(std::uint64_t v)
+{
+    std::uint64_t t;
+    t = dpp64<0x111, 0xF>(v); v = umax64(v, t);
+    t = dpp64<0x112, 0xF>(v); v = umax64(v, t);
+    t = dpp64<0x114, 0xF>(v); v = umax64(v, t);
+    t = dpp64<0x118, 0xF>(v); v = umax64(v, t);
+    t = dpp64<0x142, 0xA>(v); v = umax64(v, t);
+    t = dpp64<0x143, 0xC>(v); v = umax64(v, t);
+    return v;
+}
+
+__device__ __forceinline__ std::uint64_t readlane64(std::uint64_t v, int lane)
+{
+    const std::uint32_t lo = static_cast<std::uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(static_cast<std::uint32_t>(v)), lane));
+    const std::uint32_t hi = static_cast<std::uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(static_cast<std::uint32_t>(v >> 32)), lane));
+    return (static_cast<std::uint64_t>(hi) << 32) | lo;
+}
+
 // find_range_index (hbf_device.cuh:826-841): upper_bound(base) - 1 over the
 // sorted range table.  The top level runs over every `stride`-th base,
 // staged in LDS; the bottom level over at most `stride` bases in memory.
@@ -456,6 +498,42 @@ __device__ __forceinline__ Narrow narrow_check(const Dec& d, bool m, std::uint64
     return n;
 }
 
+// A sequential run step: all 64 lanes are modeled reads of one media page,
+// with the same byte count, in non-decreasing issue order (weight and KV
+// streaming produce these).  With at least one page register, lanes 1..63
+// hit the page their predecessor just read (plane map (0, issue_i)), and with
+// a constant transfer x the channel maps fold to one prefix maximum:
+//   lane i's channel map = (x (i + 1), x (i + 1) + max_{k<=i} (issue_k - x k)).
+// Wave-uniform.
+__device__ __forceinline__ bool run_step(const KArgs& a, const Dec& d, std::uint64_t active,
+                                         int lane)
+{
+    if (active != ~0ull || a.slots == 0) {
+        return false;
+    }
+    const std::uint32_t page0 = static_cast<std::uint32_t>(
+        __builtin_amdgcn_readlane(static_cast<int>(static_cast<std::uint32_t>(d.page1)), 0));
+    const std::uint64_t bytes0 = readlane64(d.xbytes, 0);
+    const std::uint64_t prev = shfl64(d.issue, lane == 0 ? 0 : lane - 1);
+    const bool bad = static_cast<std::uint32_t>(d.page1) != page0 || (d.bits & 1u) != 0 ||
+                     d.xbytes != bytes0 || d.issue < prev;
+    return __ballot(bad) == 0;
+}
+
+// W_i = max_{k<=i} (issue_k + x (63 - k)) for a run step, so that the channel
+// completion of lane i is max(cursor + x (i + 1), W_i - x (62 - i)).  Runs in
+// 32 bits relative to lane 0's issue when the step's span allows.
+__device__ __forceinline__ std::uint64_t run_channel_max(const Dec& d, std::uint64_t x, int lane)
+{
+    const std::uint64_t w = d.issue + x * static_cast<std::uint64_t>(63 - lane);
+    const std::uint64_t i0 = readlane64(d.issue, 0);
+    const std::uint64_t i63 = readlane64(d.issue, 63);
+    if (i63 - i0 + 64 * x < (1ull << 31) && x < (1ull << 24)) {
+        return i0 + wave_prefix_max32(static_cast<std::uint32_t>(w - i0));
+    }
+    return wave_prefix_max64(w);
+}
+
 // Lane grouping by key for one step: the previous lane of the same key
 // (pred, -1 for the first), and the group's first and last lanes.  When every
 // active lane has the same key (sequential streams) the ballot match is
@@ -594,6 +672,37 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
             continue;
         }
         const std::uint64_t xfer = lane_xfer(a, d, m, active);
+        if (run_step(a, d, active, lane)) {
+            const std::uint64_t W = run_channel_max(d, xfer, lane);
+            if (lane == 63) {
+                const std::uint32_t pkey = d.plane;
+                const std::uint32_t ckey = d.chan;
+                const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
+                const std::uint64_t i0 = readlane64(d.issue, 0);
+                if (p_f1[pkey] == 0) {  // lane 0 is the tile's first record here
+                    p_f1[pkey] = page1;
+                    p_fi[pkey] = i0;
+                    p_fc[pkey] = 0;
+                    p_rA[pkey] = 0;
+                    p_rB[pkey] = d.issue;
+                } else {
+                    const bool lhit = p_l1[pkey] == page1;
+                    const std::uint64_t ls = lhit ? 0ull : a.read_ps;
+                    const std::uint64_t sA = p_rA[pkey] + ls;
+                    const std::uint64_t sB = umax64(p_rB[pkey] + ls, i0 + ls);
+                    p_rA[pkey] = sA;
+                    p_rB[pkey] = umax64(sB, d.issue);
+                }
+                p_l1[pkey] = page1;
+                const std::uint64_t tA = 64 * xfer;
+                const std::uint64_t tB = W + xfer;
+                const std::uint64_t sA = c_A[ckey];
+                const std::uint64_t sB = c_B[ckey];
+                c_B[ckey] = umax64(sB + tA, tB);
+                c_A[ckey] = sA + tA;
+            }
+            continue;
+        }
         const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
         const std::uint32_t pkey = m ? d.plane : 0u;
         const std::uint32_t ckey = m ? d.chan : 0u;
@@ -929,7 +1038,63 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
         const std::uint64_t active = __ballot(m);
         std::uint8_t st = static_cast<std::uint8_t>(d.cls);
         std::uint64_t done = 0;
-        if (active != 0) {
+        if (active != 0 && run_step(a, d, active, lane)) {
+            const std::uint64_t xfer = lane_xfer(a, d, m, active);
+            const std::uint64_t W = run_channel_max(d, xfer, lane);
+            const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
+            const std::uint32_t pkey = d.plane;
+            const std::uint32_t ckey = d.chan;
+            const std::uint32_t tag = p_tag[pkey];
+            const std::uint64_t pbusy = p_busy[pkey];
+            const std::uint64_t cbusy = c_busy[ckey];
+            const std::uint64_t i0 = readlane64(d.issue, 0);
+            const bool lhit = tag == page1;
+            const std::uint64_t ls = lhit ? 0ull : a.read_ps;
+            const std::uint64_t lead = a.contention ? umax64(pbusy, i0) + ls : i0 + ls;
+            std::uint64_t pd;
+            if (lane == 0) {
+                pd = lead;
+            } else {
+                pd = a.contention ? umax64(lead, d.issue) : d.issue;
+            }
+            const std::uint64_t k1 = static_cast<std::uint64_t>(lane + 1);
+            const std::uint64_t cd = umax64(cbusy + xfer * k1,
+                                            lane == 63 ? W + xfer
+                                                       : W - xfer * static_cast<std::uint64_t>(
+                                                                        62 - lane));
+            if (lane == 63) {
+                if (a.contention) {
+                    p_busy[pkey] = pd;
+                }
+                p_tag[pkey] = page1;
+                c_busy[ckey] = cd;
+            }
+            done = umax64(pd, cd);
+            const bool hit = lane == 0 ? lhit : true;
+            const std::uint64_t svc = lane == 0 ? ls : 0ull;
+            if (a.hybrid) {
+                const std::uint64_t q = seq + static_cast<std::uint64_t>(lane);
+                const std::uint64_t key = ((d.page1 - 1) << a.page_shift) ^
+                                          (static_cast<std::uint64_t>(d.range_id) << 32);
+                if (q < a.hybrid_warmup ||
+                    (a.hybrid_threshold != 0 && mix64(q ^ key) <= a.hybrid_threshold)) {
+                    st |= 8u;
+                    ++n_hyb;
+                }
+            }
+            ++n_mod;
+            ++n_rd;
+            if (hit) {
+                st |= 4u;
+                ++n_hit;
+            }
+            mk = umax64(mk, done);
+            const std::uint64_t lat = done - d.issue;
+            add128(lat_lo, lat_hi, lat);
+            lat_max = umax64(lat_max, lat);
+            svc_sum += umax64(svc, xfer);
+            seq += 64;
+        } else if (active != 0) {
             const std::uint64_t xfer = lane_xfer(a, d, m, active);
             const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
             const std::uint32_t pkey = m ? d.plane : 0u;

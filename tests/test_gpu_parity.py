@@ -333,3 +333,40 @@ def test_sequential_writes_and_wide_steps(gap_ps):
         p.check_state()
     finally:
         p.close()
+
+
+@pytest.mark.parametrize("options", [
+    dict(), dict(plane_contention=0), dict(page_buffers=0), dict(tile_records=192),
+    dict(tile_records=64, transfer_page=1),
+])
+def test_sequential_runs(tmp_path, options):
+    """Streams of whole-wave sequential runs (the fast path) interleaved with
+    steps that break the run conditions: a page boundary inside a step, a
+    write, an out-of-order issue, a bypass record; hybrid sampling on."""
+    prof = json.loads(C0.read_text())
+    prof.update(reference_sample_rate=0.02, reference_warmup_requests=7)
+    path = tmp_path / "c0-runs.json"
+    path.write_text(json.dumps(prof))
+    base = 0x6200_0000_0000
+    page = 16384
+    ranges = [(base, 256 * page, 3)]
+    n = 64 * 400 + 17
+    j = np.arange(n, dtype=np.uint64)
+    rec = np.zeros((n, 4), np.uint64)
+    rec[:, 0] = np.uint64(base) + (j * np.uint64(128) + np.uint64(64 * 128 * 3)) % \
+        np.uint64(256 * page)
+    rec[:, 1] = 128
+    rec[:, 2] = (j // np.uint64(16)) * np.uint64(3000)
+    rng = np.random.default_rng(5)
+    breaks = rng.integers(0, n, 40)
+    rec[breaks[:10], 3] = 1                          # writes
+    rec[breaks[10:20], 0] = 0x1000                   # bypass
+    rec[breaks[20:30], 2] = rec[breaks[20:30], 2] // np.uint64(2)  # issue out of order
+    p = parity.Pair(path, ranges, mode="hybrid", **options)
+    try:
+        (_, _, grep), _ = check(p, rec, f"runs {options}")
+        assert grep["hybrid_sampled"] > 0
+        assert grep["page_hits"] > 0 or options.get("page_buffers", 1) == 0
+        p.check_state()
+    finally:
+        p.close()
