@@ -107,6 +107,51 @@ class Report(ctypes.Structure):
         return d
 
 
+class ThermalGrid(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("nx", ctypes.c_uint32),
+                ("ny", ctypes.c_uint32), ("nz", ctypes.c_uint32), ("sweeps", ctypes.c_uint32),
+                ("reserved0", ctypes.c_uint32), ("capacity_j_per_k", ctypes.c_double),
+                ("gx_w_per_k", ctypes.c_double), ("gy_w_per_k", ctypes.c_double),
+                ("gz_w_per_k", ctypes.c_double), ("top_g_w_per_k", ctypes.c_double),
+                ("ambient_k", ctypes.c_double), ("dt_s", ctypes.c_double)]
+
+
+RELIABILITY_FIELDS = [("struct_size", ctypes.c_uint32), ("policy", ctypes.c_uint32),
+                      ("regions_x", ctypes.c_uint32), ("regions_y", ctypes.c_uint32),
+                      ("window_ps", ctypes.c_uint64), ("static_power_w", ctypes.c_double),
+                      ("access_energy_j", ctypes.c_double), ("refresh_energy_j", ctypes.c_double),
+                      ("activation_energy_ev", ctypes.c_double), ("reference_k", ctypes.c_double),
+                      ("retention_ps", ctypes.c_uint64), ("light_k", ctypes.c_double),
+                      ("severe_k", ctypes.c_double), ("shutdown_k", ctypes.c_double),
+                      ("hysteresis_k", ctypes.c_double), ("action_delay_ps", ctypes.c_uint64),
+                      ("min_dwell_ps", ctypes.c_uint64), ("light_gap_ps", ctypes.c_uint64)]
+
+
+class ReliabilityOptions(ctypes.Structure):
+    _fields_ = RELIABILITY_FIELDS
+
+
+COUPLED_FIELDS = ("windows", "refreshes", "deferred", "level_windows", "demand_modeled",
+                  "latency_sum_lo", "latency_sum_hi", "latency_max_ps", "makespan_ps", "peak_k")
+
+
+class CoupledReport(ctypes.Structure):
+    _fields_ = [("windows", ctypes.c_uint64), ("refreshes", ctypes.c_uint64),
+                ("deferred", ctypes.c_uint64), ("level_windows", ctypes.c_uint64 * 4),
+                ("demand_modeled", ctypes.c_uint64), ("latency_sum_lo", ctypes.c_uint64),
+                ("latency_sum_hi", ctypes.c_uint64), ("latency_max_ps", ctypes.c_uint64),
+                ("makespan_ps", ctypes.c_uint64), ("peak_k", ctypes.c_double)]
+
+    def as_dict(self) -> dict:
+        d = {}
+        for name in COUPLED_FIELDS:
+            v = getattr(self, name)
+            d[name] = [int(x) for x in v] if name == "level_windows" else (
+                float(v) if name == "peak_k" else int(v))
+        d["latency_sum_ps"] = d["latency_sum_lo"] | (d["latency_sum_hi"] << 64)
+        return d
+
+
 _P = ctypes.c_void_p
 _U32 = ctypes.c_uint32
 _U64 = ctypes.c_uint64
@@ -147,6 +192,15 @@ SIGNATURES = {
                                         ctypes.POINTER(Range), ctypes.POINTER(_U32)]),
     "hbfsim_amd_gen_segment_lines": (_INT, [_P, _SZ, _P, _SZ, _U64, _U32, _U64, _U32, _U64,
                                             _P]),
+    "hbfsim_amd_thermal_create": (_INT, [ctypes.POINTER(ThermalGrid), ctypes.POINTER(_P)]),
+    "hbfsim_amd_thermal_step": (_INT, [_P, _P, _P, _U64, _P]),
+    "hbfsim_amd_thermal_last_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float)]),
+    "hbfsim_amd_thermal_destroy": (None, [_P]),
+    "hbfsim_amd_run_coupled": (_INT, [_P, _P, ctypes.POINTER(ReliabilityOptions), _P, _SZ, _P,
+                                      _P, _P, _P, ctypes.POINTER(CoupledReport),
+                                      ctypes.POINTER(Report)]),
+    "hbfsim_amd_coupled_trace": (_INT, [_P, _P, _SZ, _P, _SZ, _P, _SZ, ctypes.POINTER(_U64),
+                                        ctypes.POINTER(_U32)]),
     "hbfsim_amd_validate_profile": (_INT, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
 }
 

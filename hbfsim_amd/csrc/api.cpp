@@ -9,6 +9,7 @@
 // and registering ranges need no GPU; the engine and its device memory are
 // created on first use.
 #include "engine.hpp"
+#include "thermal.hpp"
 #include "profile.hpp"
 
 #include <cmath>
@@ -157,6 +158,7 @@ int build_config(const hbfsim_context* c, hbfamd::engine_config* cfg)
     if ((p.capacity_bytes >> k.page_shift) >= 0xffffffffull) {
         return HBFSIM_UNSUPPORTED;
     }
+    k.media_pages = p.capacity_bytes >> k.page_shift;
     if (p.empirical.present) {
         for (int i = 0; i < 6; ++i) {
             k.emp_pages[i] = p.empirical.read_curve[i].pages;
@@ -639,6 +641,111 @@ HBF_API int hbfsim_amd_run(hbfsim_context* c, const hbf_record32* records, size_
         *report = r;
     }
     return HBFSIM_OK;
+}
+
+// ---- EQ3 thermal grid and the thermal-coupled run ----------------------
+
+struct hbfsim_amd_thermal {
+    hbfamd::thermal* impl;
+};
+
+HBF_API int hbfsim_amd_thermal_create(const hbfsim_amd_thermal_grid* grid,
+                                      hbfsim_amd_thermal** out)
+{
+    if (out != nullptr) {
+        *out = nullptr;
+    }
+    if (grid == nullptr || out == nullptr || grid->struct_size != sizeof(*grid)) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    try {
+        hbfamd::thermal* impl = nullptr;
+        const int st = hbfamd::thermal_create(*grid, &impl);
+        if (st != HBFSIM_OK) {
+            return st;
+        }
+        *out = new hbfsim_amd_thermal{impl};
+        return HBFSIM_OK;
+    } catch (...) {
+        return HBFSIM_IO_ERROR;
+    }
+}
+
+HBF_API int hbfsim_amd_thermal_step(hbfsim_amd_thermal* t, const double* d_power,
+                                    double* d_temperature, uint64_t steps, void* stream)
+{
+    if (t == nullptr || d_power == nullptr || d_temperature == nullptr) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    return hbfamd::thermal_step(t->impl, d_power, d_temperature, steps, stream);
+}
+
+HBF_API int hbfsim_amd_thermal_last_ms(const hbfsim_amd_thermal* t, float* ms)
+{
+    if (t == nullptr || ms == nullptr) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    *ms = hbfamd::thermal_last_step_ms(t->impl);
+    return HBFSIM_OK;
+}
+
+HBF_API void hbfsim_amd_thermal_destroy(hbfsim_amd_thermal* t)
+{
+    if (t == nullptr) {
+        return;
+    }
+    hbfamd::thermal_destroy(t->impl);
+    delete t;
+}
+
+HBF_API int hbfsim_amd_run_coupled(hbfsim_context* c, hbfsim_amd_thermal* t,
+                                   const hbfsim_amd_reliability_options* o,
+                                   const hbf_record32* records, size_t n,
+                                   uint64_t* completion_ps, double* d_temperature,
+                                   uint64_t* age_ps, void* stream,
+                                   hbfsim_amd_coupled_report* report,
+                                   hbfsim_amd_report* engine_report)
+{
+    if (report != nullptr) {
+        std::memset(report, 0, sizeof(*report));
+    }
+    if (engine_report != nullptr) {
+        std::memset(engine_report, 0, sizeof(*engine_report));
+    }
+    if (c == nullptr || t == nullptr || o == nullptr || o->struct_size != sizeof(*o)) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(c->mu);
+    int st = ensure_engine(c);
+    if (st != HBFSIM_OK) {
+        return st;
+    }
+    try {
+        hbfsim_amd_report r{};
+        st = hbfamd::coupled_run(c->eng, hbfamd::engine_get_config(c->eng), t->impl, *o, records,
+                                 n, completion_ps, d_temperature, age_ps, stream, report, &r);
+        if (st != HBFSIM_OK) {
+            return st;
+        }
+        account(c, r);
+        if (engine_report != nullptr) {
+            *engine_report = r;
+        }
+        return HBFSIM_OK;
+    } catch (...) {
+        return HBFSIM_IO_ERROR;
+    }
+}
+
+HBF_API int hbfsim_amd_coupled_trace(const hbfsim_amd_thermal* t, double* hot, size_t hot_count,
+                                     uint8_t* level, size_t level_count, uint8_t* refresh,
+                                     size_t refresh_count, uint64_t* windows, uint32_t* dies)
+{
+    if (t == nullptr) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    return hbfamd::coupled_trace(t->impl, hot, hot_count, level, level_count, refresh,
+                                 refresh_count, windows, dies);
 }
 
 HBF_API int hbfsim_amd_get_report(const hbfsim_context* c, hbfsim_amd_report* out)

@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include "engine.hpp"
+#include "thermal.hpp"
 
 #include <algorithm>
 #include <cstring>
@@ -99,12 +100,18 @@ struct KArgs {
     std::uint64_t read_ps, program_ps;
     std::uint64_t xfer_num, xfer_den, xfer_q;
     std::uint64_t xfer_pow2[33];    // transfer ps for 2^k bytes
+    std::uint64_t media_pages;      // device capacity in pages
     std::uint32_t tile;
 };
 
+// Record operations: 0 read, 1 write, and 2 refresh of media page `addr`
+// (read out and programmed back), valid only with kMediaFlag.
+constexpr std::uint32_t kOpRefresh = 2;
+constexpr std::uint32_t kMediaFlag = 0x100;
+
 struct Dec {
     std::uint32_t cls;
-    std::uint32_t bits;    // bit 0 op, bit 1 programs the page
+    std::uint32_t bits;    // bit 0 write or refresh, bit 1 programs, bit 2 refresh
     std::uint32_t plane, chan;
     std::uint32_t range_id;
     std::uint64_t page1;   // media page + 1
@@ -363,6 +370,36 @@ __device__ __forceinline__ void load_record(const hbf_record32* rec, std::size_t
     y = p[1];
 }
 
+// Channel and global plane id of a media page (the profile's allocation
+// scheme, fastest axis first).
+__device__ __forceinline__ void stripe(const KArgs& a, std::uint64_t page, Dec& d)
+{
+    if (a.flat) {
+        return;
+    }
+    std::uint32_t c[4];
+    if (a.pow2) {
+#pragma unroll
+        for (int ax = 0; ax < 4; ++ax) {
+            c[ax] = static_cast<std::uint32_t>((page >> a.axis_shift[ax]) &
+                                               (a.axis_size[ax] - 1));
+        }
+    } else {
+#pragma unroll
+        for (int ax = 0; ax < 4; ++ax) {
+            c[ax] = static_cast<std::uint32_t>((page / a.axis_div[ax]) % a.axis_size[ax]);
+        }
+    }
+    d.chan = c[0];
+    d.plane = ((c[0] * a.W + c[1]) * a.D + c[2]) * a.P + c[3];
+}
+
+// The operation a decoded record carries (hybrid sampler key).
+__device__ __forceinline__ std::uint32_t dec_op(std::uint32_t bits)
+{
+    return (bits & 4u) ? kOpRefresh : (bits & 1u);
+}
+
 // Classification in the resolver's order (hbf_device.cu:1081-1165) followed
 // by striping of the media page.
 __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence, RangeCache& rc,
@@ -381,6 +418,18 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
     d.page1 = 0;
     d.xfer = 0;
     d.xbytes = 0;
+    if (op == kOpRefresh && (y.z & kMediaFlag) != 0) {
+        if (bytes == 0 || bytes > 0xffffffffull || addr >= a.media_pages) {
+            d.cls = kClsUnsupported;
+            return d;
+        }
+        d.cls = kClsModeled;
+        d.bits = 7u;
+        d.page1 = addr + 1;
+        d.xbytes = bytes;
+        stripe(a, addr, d);
+        return d;
+    }
     if (!(addr >= rc.base && addr < rc.end)) {
         const std::uint32_t idx = find_range(a, fence, addr);
         if (idx == a.r_count || addr < a.r_base[idx] ||
@@ -429,23 +478,7 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
         d.bits |= 2u;
     }
     d.xbytes = a.transfer_page ? page_bytes : bytes;
-    if (!a.flat) {
-        std::uint32_t c[4];
-        if (a.pow2) {
-#pragma unroll
-            for (int ax = 0; ax < 4; ++ax) {
-                c[ax] = static_cast<std::uint32_t>((page >> a.axis_shift[ax]) &
-                                                   (a.axis_size[ax] - 1));
-            }
-        } else {
-#pragma unroll
-            for (int ax = 0; ax < 4; ++ax) {
-                c[ax] = static_cast<std::uint32_t>((page / a.axis_div[ax]) % a.axis_size[ax]);
-            }
-        }
-        d.chan = c[0];
-        d.plane = ((c[0] * a.W + c[1]) * a.D + c[2]) * a.P + c[3];
-    }
+    stripe(a, page, d);
     return d;
 }
 
@@ -605,6 +638,9 @@ __device__ __forceinline__ std::uint64_t plane_service(const KArgs& a, std::uint
 {
     if ((bits & 1u) == 0) {
         return hit ? 0ull : a.read_ps;
+    }
+    if (bits & 4u) {
+        return a.read_ps + a.program_ps;
     }
     return (bits & 2u) ? a.program_ps : 0ull;
 }
@@ -1140,7 +1176,7 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
                 if (a.hybrid) {
                     const std::uint64_t key = ((d.page1 - 1) << a.page_shift) ^
                                               (static_cast<std::uint64_t>(d.range_id) << 32) ^
-                                              (d.bits & 1u);
+                                              dec_op(d.bits);
                     if (q < a.hybrid_warmup ||
                         (a.hybrid_threshold != 0 && mix64(q ^ key) <= a.hybrid_threshold)) {
                         st |= 8u;
@@ -1155,7 +1191,7 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
                         ++n_hit;
                     }
                 } else {
-                    ++n_wr;
+                    n_wr += (d.bits & 4u) ? 0u : 1u;
                     if (svc != 0) {
                         st |= 16u;
                         ++n_prog;
@@ -1454,6 +1490,60 @@ int upload_ranges(engine* e, hipStream_t stream)
     return HBFSIM_OK;
 }
 
+// Modeled records per (window of issue time, die), for the thermal power
+// map.  Each block histograms a chunk in LDS over the windows it spans and
+// flushes the non-zero bins with global atomics.
+constexpr std::uint32_t kCountChunk = 4096;
+constexpr std::uint32_t kCountBins = 4096;
+
+__global__ __launch_bounds__(256) void k_window_counts(KArgs a, const hbf_record32* rec,
+                                                       std::size_t n, std::uint64_t window_ps,
+                                                       std::uint64_t windows,
+                                                       std::uint32_t ndie,
+                                                       std::uint32_t* counts)
+{
+    extern __shared__ std::uint64_t sm[];
+    std::uint64_t* fence = sm;
+    std::uint32_t* hist = reinterpret_cast<std::uint32_t*>(fence + a.r_nfence);
+    const int tid = threadIdx.x;
+    for (std::uint32_t j = tid; j < a.r_nfence; j += blockDim.x) {
+        fence[j] = a.r_base[static_cast<std::size_t>(j) * a.r_stride];
+    }
+    for (std::uint32_t j = tid; j < kCountBins; j += blockDim.x) {
+        hist[j] = 0;
+    }
+    __syncthreads();
+    const std::size_t begin = static_cast<std::size_t>(blockIdx.x) * kCountChunk;
+    const std::size_t end = begin + kCountChunk < n ? begin + kCountChunk : n;
+    const std::uint64_t w0 = rec[begin].issue_ps / window_ps;
+    RangeCache rc = empty_cache();
+    for (std::size_t i = begin + tid; i < end; i += blockDim.x) {
+        uint4 x, y;
+        load_record(rec, i, x, y);
+        const Dec d = decode(a, fence, rc, x, y, 0);
+        if (d.cls != kClsModeled) {
+            continue;
+        }
+        const std::uint64_t w = d.issue / window_ps;
+        if (w >= windows) {
+            continue;
+        }
+        const std::uint32_t die = d.plane / a.P;
+        const std::uint64_t bin = (w - w0) * ndie + die;
+        if (w >= w0 && bin < kCountBins) {
+            atomicAdd(&hist[bin], 1u);
+        } else {
+            atomicAdd(&counts[w * ndie + die], 1u);
+        }
+    }
+    __syncthreads();
+    for (std::uint32_t j = tid; j < kCountBins; j += blockDim.x) {
+        if (hist[j] != 0) {
+            atomicAdd(&counts[w0 * ndie + j], hist[j]);
+        }
+    }
+}
+
 std::size_t lds_summary(const KArgs& a)
 {
     return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 12ull * a.Rp;
@@ -1547,6 +1637,7 @@ int engine_create(const engine_config& c, engine** out)
                          static_cast<std::uint64_t>((prod + c.xfer_den - 1) / c.xfer_den);
     }
     a.tile = c.tile;
+    a.media_pages = c.media_pages;
     hipError_t err = halloc(e->d_pbusy, rp);
     if (err == hipSuccess) err = halloc(e->d_ptag, 2ull * rp);
     if (err == hipSuccess) err = halloc(e->d_cbusy, rc);
@@ -1825,6 +1916,37 @@ int engine_last_kernel_ms(const engine* e, float* ms, int max_kernels)
         ms[i] = e->last_ms[i];
     }
     return k;
+}
+
+
+int engine_window_counts(engine* e, const hbf_record32* d_rec, std::size_t n,
+                         std::uint64_t window_ps, std::uint64_t windows, std::uint32_t* d_counts,
+                         void* stream_ptr)
+{
+    if (n == 0) {
+        return HBFSIM_OK;
+    }
+    if (d_rec == nullptr || d_counts == nullptr || window_ps == 0 ||
+        (reinterpret_cast<std::uintptr_t>(d_rec) & 15u) != 0) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    if (hipSetDevice(e->device) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    if (e->ranges_dirty) {
+        const int st = upload_ranges(e, stream);
+        if (st != HBFSIM_OK) {
+            return st;
+        }
+    }
+    const KArgs& a = e->args;
+    const std::uint32_t ndie = a.Rp / a.P;
+    const std::size_t lds = 8ull * a.r_nfence + 4ull * kCountBins;
+    const std::size_t blocks = (n + kCountChunk - 1) / kCountChunk;
+    hipLaunchKernelGGL(k_window_counts, dim3(static_cast<unsigned>(blocks)), dim3(256), lds, stream,
+                       a, d_rec, n, window_ps, windows, ndie, d_counts);
+    return hip_status(hipGetLastError());
 }
 
 }  // namespace hbfamd

@@ -1,0 +1,1096 @@
+// thermal.hip -- EQ3 RC thermal grid and the thermal-coupled reliability
+// run for gfx950 (MI355X).
+//
+// k_thermal_window advances the grid by one backward-Euler step
+// (thermal.cpp:127-160 on a regular 6-neighbour network) with `sweeps`
+// Jacobi sweeps, temporally blocked: a workgroup stages its tile plus a halo
+// of `sweeps` cells in LDS, sweeps there, and writes only the interior, whose
+// values are exact after the last sweep.  HBM traffic per step is one read
+// and one write of the temperature (plus the power array when it is given).
+// In coupled mode the same launch first runs the window's control,
+// retention and refresh decisions (every workgroup computes them for all
+// dies, workgroup 0 stores them), builds the cell power from the window's
+// per-die access counts, and after the step folds every die's hotspot into
+// the next row of the hotspot trace with atomic maxima.
+//
+// Floating-point contraction is off in this file: every cell's update is the
+// same sequence of IEEE double operations as the CPU restatement, so
+// temperatures, hotspots and every decision derived from them are
+// bit-identical to it.
+#include <hip/hip_runtime.h>
+
+#include "thermal.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#pragma clang fp contract(off)
+
+namespace hbfamd {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kCellsPerThread = 8;
+constexpr std::uint32_t kMaxRegion = kThreads * kCellsPerThread;
+constexpr std::uint32_t kAfBins = 4096;
+constexpr double kAfT0 = 200.0;
+constexpr double kAfStepsPerK = 16.0;
+constexpr std::uint32_t kNoPending = 4;
+constexpr std::uint32_t kMaxDies = 1024;
+
+struct Ctl {
+    std::uint32_t applied;
+    std::uint32_t pending;
+    std::uint64_t pending_at;
+    std::uint64_t last_change;
+};
+
+struct TArgs {
+    std::uint32_t nx, ny, nz, sweeps;
+    std::uint32_t tx, ty, rx, ry;  // tile interior and staged region
+    std::uint32_t tiles_x;
+    std::uint32_t cells;           // rx * ry * nz
+    double cdt, gx, gy, gz, gb, tb;
+    const double* power;           // W per cell (uncoupled steps)
+    // coupled mode
+    std::uint32_t coupled;
+    std::uint32_t ndie, regions_x, rw, rh, lpd, D, policy;
+    double static_w, pa, pr;
+    const std::uint32_t* counts;   // [windows][ndie]
+    unsigned long long* hot;       // [(windows + 1)][ndie], bits of doubles
+    const std::uint64_t* af;       // retention table
+    std::uint64_t retention_ps, window_ps;
+    double light_k, severe_k, shutdown_k, hysteresis_k;
+    std::uint64_t action_delay_ps, min_dwell_ps;
+    const std::uint64_t* age_in;
+    std::uint64_t* age_out;
+    const Ctl* ctl_in;
+    Ctl* ctl_out;
+    std::uint8_t* level;
+    std::uint8_t* refresh;
+};
+
+__device__ __forceinline__ std::uint64_t sat_add(std::uint64_t a, std::uint64_t b)
+{
+    return a > ~0ull - b ? ~0ull : a + b;
+}
+
+__device__ __forceinline__ std::uint32_t af_bin(double t)
+{
+    if (!(t >= kAfT0)) {
+        return 0;
+    }
+    const double f = (t - kAfT0) * kAfStepsPerK;
+    if (!(f < static_cast<double>(kAfBins - 1))) {
+        return kAfBins - 1;
+    }
+    return static_cast<std::uint32_t>(f);
+}
+
+// cpu_service.cpp:221-255: control_sample then apply_controls.
+__device__ void control_step(const TArgs& a, Ctl& c, std::uint64_t now, double hs)
+{
+    const double thr[4] = {0.0, a.light_k, a.severe_k, a.shutdown_k};
+    std::uint32_t desired = static_cast<std::uint32_t>(hs >= a.light_k) +
+                            static_cast<std::uint32_t>(hs >= a.severe_k) +
+                            static_cast<std::uint32_t>(hs >= a.shutdown_k);
+    if (desired < c.applied && hs >= thr[c.applied] - a.hysteresis_k) {
+        desired = c.applied;
+    }
+    if (a.policy != 0) {
+        if (desired == c.applied) {
+            c.pending = kNoPending;
+        } else if (c.pending == kNoPending || c.pending != desired) {
+            const std::uint64_t x = sat_add(now, a.action_delay_ps);
+            const std::uint64_t y = sat_add(c.last_change, a.min_dwell_ps);
+            c.pending = desired;
+            c.pending_at = x > y ? x : y;
+        }
+    }
+    if (c.pending != kNoPending && c.pending_at <= now) {
+        c.applied = c.pending;
+        c.last_change = now;
+        c.pending = kNoPending;
+    }
+}
+
+// Neighbour bits of a staged cell: which neighbours exist in the grid
+// (update terms) and which of those are staged in LDS.
+enum : std::uint32_t {
+    kIn = 1u << 0,
+    kXm = 1u << 1, kXmL = 1u << 2, kXp = 1u << 3, kXpL = 1u << 4,
+    kYm = 1u << 5, kYmL = 1u << 6, kYp = 1u << 7, kYpL = 1u << 8,
+    kZm = 1u << 9, kZp = 1u << 10, kTop = 1u << 11, kInterior = 1u << 12
+};
+
+__global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const double* tin,
+                                                             double* tout, std::uint64_t w)
+{
+    extern __shared__ double lds[];
+    double* cur = lds;
+    double* nxt = lds + a.cells;
+    __shared__ double red[kThreads];
+    __shared__ std::uint8_t s_ref[kMaxDies];
+    __shared__ unsigned long long s_hot[64];
+    const int tid = threadIdx.x;
+    const std::uint32_t tile_x = blockIdx.x % a.tiles_x;
+    const std::uint32_t tile_y = blockIdx.x / a.tiles_x;
+    const int h = static_cast<int>(a.sweeps);
+    const int x0 = static_cast<int>(tile_x * a.tx) - h;
+    const int y0 = static_cast<int>(tile_y * a.ty) - h;
+    const bool leader = blockIdx.x == 0;
+
+    if (a.coupled) {
+        const double* hrow = reinterpret_cast<const double*>(a.hot + w * a.ndie);
+        double m = 0.0;
+        for (std::uint32_t d = tid; d < a.ndie; d += kThreads) {
+            m = fmax(m, hrow[d]);
+            std::uint64_t age = a.age_in[d];
+            if (w > 0) {
+                age = sat_add(age, a.af[af_bin(hrow[d])]);
+            }
+            const std::uint8_t rf = age >= a.retention_ps ? 1 : 0;
+            if (rf) {
+                age = 0;
+            }
+            s_ref[d] = rf;
+            if (leader) {
+                a.age_out[d] = age;
+                a.refresh[w * a.ndie + d] = rf;
+            }
+        }
+        red[tid] = m;
+        if (tid < 64) {
+            s_hot[tid] = 0;
+        }
+        __syncthreads();
+        for (int s = kThreads / 2; s > 0; s >>= 1) {
+            if (tid < s) {
+                red[tid] = fmax(red[tid], red[tid + s]);
+            }
+            __syncthreads();
+        }
+        if (leader && tid == 0) {
+            Ctl c = *a.ctl_in;
+            control_step(a, c, w * a.window_ps, red[0]);
+            *a.ctl_out = c;
+            a.level[w] = static_cast<std::uint8_t>(c.applied);
+        }
+    }
+
+    // Stage the region; remember each owned cell's neighbour bits and
+    // right-hand side C/dt T + P.
+    double rhs[kCellsPerThread];
+    std::uint32_t nb[kCellsPerThread];
+    const std::uint32_t plane = a.rx * a.ry;
+#pragma unroll
+    for (int k = 0; k < kCellsPerThread; ++k) {
+        const std::uint32_t c = tid + k * kThreads;
+        nb[k] = 0;
+        rhs[k] = 0.0;
+        if (c >= a.cells) {
+            continue;
+        }
+        const std::uint32_t rxi = c % a.rx;
+        const std::uint32_t t = c / a.rx;
+        const std::uint32_t ryi = t % a.ry;
+        const std::uint32_t z = t / a.ry;
+        const int gx = x0 + static_cast<int>(rxi);
+        const int gy = y0 + static_cast<int>(ryi);
+        double v = 0.0;
+        if (gx >= 0 && gx < static_cast<int>(a.nx) && gy >= 0 && gy < static_cast<int>(a.ny)) {
+            const std::size_t g = (static_cast<std::size_t>(z) * a.ny + gy) * a.nx + gx;
+            v = tin[g];
+            double p;
+            if (a.coupled) {
+                const std::uint32_t q = (static_cast<std::uint32_t>(gy) / a.rh) * a.regions_x +
+                                        static_cast<std::uint32_t>(gx) / a.rw;
+                const std::uint32_t die = q * a.D + z / a.lpd;
+                const std::uint32_t cnt = a.counts[w * a.ndie + die];
+                p = (a.static_w + static_cast<double>(cnt) * a.pa) +
+                    static_cast<double>(s_ref[die]) * a.pr;
+            } else {
+                p = a.power[g];
+            }
+            rhs[k] = a.cdt * v + p;
+            std::uint32_t b = kIn;
+            if (gx > 0) b |= kXm | (rxi > 0 ? kXmL : 0u);
+            if (gx + 1 < static_cast<int>(a.nx)) b |= kXp | (rxi + 1 < a.rx ? kXpL : 0u);
+            if (gy > 0) b |= kYm | (ryi > 0 ? kYmL : 0u);
+            if (gy + 1 < static_cast<int>(a.ny)) b |= kYp | (ryi + 1 < a.ry ? kYpL : 0u);
+            if (z > 0) b |= kZm;
+            if (z + 1 < a.nz) b |= kZp;
+            if (z + 1 == a.nz) b |= kTop;
+            if (rxi >= static_cast<std::uint32_t>(h) && rxi < h + a.tx &&
+                ryi >= static_cast<std::uint32_t>(h) && ryi < h + a.ty) {
+                b |= kInterior;
+            }
+            nb[k] = b;
+        }
+        cur[c] = v;
+    }
+    __syncthreads();
+
+    const double gbtb = a.gb * a.tb;
+    for (std::uint32_t s = 0; s < a.sweeps; ++s) {
+#pragma unroll
+        for (int k = 0; k < kCellsPerThread; ++k) {
+            const std::uint32_t c = tid + k * kThreads;
+            const std::uint32_t b = nb[k];
+            if (!(b & kIn)) {
+                continue;
+            }
+            double num = rhs[k];
+            double den = a.cdt;
+            if (b & kXm) {
+                num += a.gx * ((b & kXmL) ? cur[c - 1] : 0.0);
+                den += a.gx;
+            }
+            if (b & kXp) {
+                num += a.gx * ((b & kXpL) ? cur[c + 1] : 0.0);
+                den += a.gx;
+            }
+            if (b & kYm) {
+                num += a.gy * ((b & kYmL) ? cur[c - a.rx] : 0.0);
+                den += a.gy;
+            }
+            if (b & kYp) {
+                num += a.gy * ((b & kYpL) ? cur[c + a.rx] : 0.0);
+                den += a.gy;
+            }
+            if (b & kZm) {
+                num += a.gz * cur[c - plane];
+                den += a.gz;
+            }
+            if (b & kZp) {
+                num += a.gz * cur[c + plane];
+                den += a.gz;
+            }
+            if (b & kTop) {
+                num += gbtb;
+                den += a.gb;
+            }
+            nxt[c] = num / den;
+        }
+        __syncthreads();
+        double* t = cur;
+        cur = nxt;
+        nxt = t;
+    }
+
+#pragma unroll
+    for (int k = 0; k < kCellsPerThread; ++k) {
+        const std::uint32_t c = tid + k * kThreads;
+        if (!(nb[k] & kInterior)) {
+            continue;
+        }
+        const std::uint32_t rxi = c % a.rx;
+        const std::uint32_t t = c / a.rx;
+        const std::uint32_t ryi = t % a.ry;
+        const std::uint32_t z = t / a.ry;
+        const std::uint32_t gx = static_cast<std::uint32_t>(x0 + static_cast<int>(rxi));
+        const std::uint32_t gy = static_cast<std::uint32_t>(y0 + static_cast<int>(ryi));
+        const double v = cur[c];
+        tout[(static_cast<std::size_t>(z) * a.ny + gy) * a.nx + gx] = v;
+        if (a.coupled) {
+            atomicMax(&s_hot[z / a.lpd], static_cast<unsigned long long>(__double_as_longlong(v)));
+        }
+    }
+    if (a.coupled) {
+        __syncthreads();
+        if (tid < static_cast<int>(a.D)) {
+            const std::uint32_t gx = tile_x * a.tx, gy = tile_y * a.ty;
+            const std::uint32_t q = (gy / a.rh) * a.regions_x + gx / a.rw;
+            atomicMax(&a.hot[(w + 1) * a.ndie + q * a.D + tid], s_hot[tid]);
+        }
+    }
+}
+
+// Row 0 of the hotspot trace: every die's hottest cell of the initial grid.
+__global__ void k_die_hot(TArgs a, const double* t, unsigned long long* row)
+{
+    const std::size_t n = static_cast<std::size_t>(a.nx) * a.ny * a.nz;
+    for (std::size_t i = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
+        const std::uint32_t x = static_cast<std::uint32_t>(i % a.nx);
+        const std::uint32_t y = static_cast<std::uint32_t>((i / a.nx) % a.ny);
+        const std::uint32_t z = static_cast<std::uint32_t>(i / (static_cast<std::size_t>(a.nx) * a.ny));
+        const std::uint32_t q = (y / a.rh) * a.regions_x + x / a.rw;
+        atomicMax(&row[q * a.D + z / a.lpd],
+                  static_cast<unsigned long long>(__double_as_longlong(t[i])));
+    }
+}
+
+__global__ void k_fill_u64(unsigned long long* p, std::size_t n, unsigned long long v)
+{
+    for (std::size_t i = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x; i < n;
+         i += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
+        p[i] = v;
+    }
+}
+
+// ---- admission gate -------------------------------------------------------
+// Per demand record: e = issue deferred past severe/shutdown windows; the
+// gate is one server, a = max(e, g), g' = a + gap (gap = light_gap in light
+// windows), i.e. the (max,+) map g -> max(g + gap, e + gap).
+
+struct GArgs {
+    const hbf_record32* rec;
+    std::size_t n;
+    std::uint32_t tile;            // records per block (kThreads * per)
+    std::uint32_t per;             // records per thread
+    std::uint64_t window_ps, windows, light_gap_ps;
+    const std::uint8_t* level;     // [windows]
+    const std::uint32_t* ok2;      // [windows + 1]: first window >= w with level < 2
+};
+
+__device__ __forceinline__ void gate_record(const GArgs& g, std::size_t i, std::uint64_t& e,
+                                            std::uint64_t& gap)
+{
+    const std::uint64_t t = g.rec[i].issue_ps;
+    const std::uint64_t w = t / g.window_ps;
+    e = t;
+    if (w < g.windows && g.level[w] >= 2) {
+        e = static_cast<std::uint64_t>(g.ok2[w + 1]) * g.window_ps;
+    }
+    const std::uint64_t we = e / g.window_ps;
+    gap = (we < g.windows && g.level[we] == 1) ? g.light_gap_ps : 0ull;
+}
+
+struct MaxPlus {
+    std::uint64_t A, B;
+};
+
+__device__ __forceinline__ MaxPlus compose(MaxPlus f, MaxPlus s)
+{
+    // f first, then s
+    const std::uint64_t b = f.B + s.A;
+    return MaxPlus{f.A + s.A, b > s.B ? b : s.B};
+}
+
+__device__ MaxPlus thread_map(const GArgs& g, std::size_t begin, std::size_t end)
+{
+    MaxPlus m{0, 0};
+    for (std::size_t i = begin; i < end; ++i) {
+        std::uint64_t e, gap;
+        gate_record(g, i, e, gap);
+        m = compose(m, MaxPlus{gap, e + gap});
+    }
+    return m;
+}
+
+// Inclusive scan of per-thread maps in thread order (Hillis-Steele).
+__device__ MaxPlus block_scan(MaxPlus m, MaxPlus* sA)
+{
+    const int tid = threadIdx.x;
+    sA[tid] = m;
+    __syncthreads();
+    for (int o = 1; o < kThreads; o <<= 1) {
+        MaxPlus v = sA[tid];
+        if (tid >= o) {
+            v = compose(sA[tid - o], v);
+        }
+        __syncthreads();
+        sA[tid] = v;
+        __syncthreads();
+    }
+    return sA[tid];
+}
+
+__global__ __launch_bounds__(kThreads) void k_gate_summary(GArgs g, MaxPlus* tiles)
+{
+    __shared__ MaxPlus sA[kThreads];
+    const std::size_t base = static_cast<std::size_t>(blockIdx.x) * g.tile;
+    const std::size_t b = base + static_cast<std::size_t>(threadIdx.x) * g.per;
+    const std::size_t e = std::min(b + g.per, g.n);
+    const MaxPlus m = block_scan(b < g.n ? thread_map(g, b, e) : MaxPlus{0, 0}, sA);
+    if (threadIdx.x == kThreads - 1) {
+        tiles[blockIdx.x] = m;
+    }
+}
+
+// One block: the gate value before every tile.
+__global__ __launch_bounds__(kThreads) void k_gate_carry(const MaxPlus* tiles, std::size_t ntiles,
+                                                         std::uint64_t* carry)
+{
+    __shared__ MaxPlus sA[kThreads];
+    const std::size_t per = (ntiles + kThreads - 1) / kThreads;
+    const std::size_t b = threadIdx.x * per, e = std::min(b + per, ntiles);
+    MaxPlus m{0, 0};
+    for (std::size_t t = b; t < e; ++t) {
+        m = compose(m, tiles[t]);
+    }
+    const MaxPlus inc = block_scan(m, sA);
+    __syncthreads();
+    std::uint64_t gate = 0;
+    if (threadIdx.x > 0) {
+        const MaxPlus ex = sA[threadIdx.x - 1];
+        gate = ex.A > ex.B ? ex.A : ex.B;  // map applied to g = 0
+    }
+    (void)inc;
+    for (std::size_t t = b; t < e; ++t) {
+        carry[t] = gate;
+        const std::uint64_t x = gate + tiles[t].A;
+        gate = x > tiles[t].B ? x : tiles[t].B;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_gate_apply(GArgs g, const std::uint64_t* carry,
+                                                         std::uint64_t* admit)
+{
+    __shared__ MaxPlus sA[kThreads];
+    const std::size_t base = static_cast<std::size_t>(blockIdx.x) * g.tile;
+    const std::size_t b = base + static_cast<std::size_t>(threadIdx.x) * g.per;
+    const std::size_t e = std::min(b + g.per, g.n);
+    const MaxPlus mine = b < g.n ? thread_map(g, b, e) : MaxPlus{0, 0};
+    block_scan(mine, sA);
+    std::uint64_t gate = carry[blockIdx.x];
+    if (threadIdx.x > 0) {
+        const MaxPlus ex = sA[threadIdx.x - 1];
+        const std::uint64_t x = gate + ex.A;
+        gate = x > ex.B ? x : ex.B;
+    }
+    for (std::size_t i = b; i < e; ++i) {
+        std::uint64_t ei, gap;
+        gate_record(g, i, ei, gap);
+        const std::uint64_t ai = ei > gate ? ei : gate;
+        admit[i] = ai;
+        gate = ai + gap;
+    }
+}
+
+// Refresh j goes to j + #(demand admitted strictly before it).
+__global__ void k_refresh_place(const hbf_record32* ref, std::size_t r,
+                                const std::uint64_t* admit, std::size_t n, hbf_record32* merged)
+{
+    const std::size_t j = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x;
+    if (j >= r) {
+        return;
+    }
+    const std::uint64_t t = ref[j].issue_ps;
+    std::size_t lo = 0, hi = n;
+    while (lo < hi) {
+        const std::size_t mid = (lo + hi) >> 1;
+        if (admit[mid] < t) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    merged[j + lo] = ref[j];
+}
+
+// Demand i goes to i + #(refreshes admitted at or before it).
+__global__ void k_merge_demand(const hbf_record32* rec, std::size_t n, const std::uint64_t* admit,
+                               const std::uint64_t* ref_issue, std::size_t r,
+                               hbf_record32* merged, std::uint64_t* pos)
+{
+    const std::size_t i = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x;
+    if (i >= n) {
+        return;
+    }
+    const std::uint64_t t = admit[i];
+    std::size_t lo = 0, hi = r;
+    while (lo < hi) {
+        const std::size_t mid = (lo + hi) >> 1;
+        if (ref_issue[mid] <= t) {
+            lo = mid + 1;
+        } else {
+            hi = mid;
+        }
+    }
+    hbf_record32 v = rec[i];
+    v.issue_ps = t;
+    merged[i + lo] = v;
+    pos[i] = i + lo;
+}
+
+struct Partial {
+    unsigned long long deferred, modeled, lat_lo, lat_hi, lat_max;
+};
+
+__device__ __forceinline__ void add128(unsigned long long& lo, unsigned long long& hi,
+                                       unsigned long long v)
+{
+    const unsigned long long s = lo + v;
+    hi += s < lo ? 1ull : 0ull;
+    lo = s;
+}
+
+// Demand completions back in input order, and the demand accounting.
+__global__ __launch_bounds__(kThreads) void k_gather(const hbf_record32* rec, std::size_t n,
+                                                     const std::uint64_t* admit,
+                                                     const std::uint64_t* pos,
+                                                     const std::uint64_t* mcomp,
+                                                     const std::uint8_t* mstat,
+                                                     std::uint64_t* completion, Partial* part)
+{
+    __shared__ Partial s[kThreads];
+    Partial p{0, 0, 0, 0, 0};
+    for (std::size_t i = blockIdx.x * static_cast<std::size_t>(kThreads) + threadIdx.x; i < n;
+         i += static_cast<std::size_t>(gridDim.x) * kThreads) {
+        const std::uint64_t k = pos[i];
+        const std::uint64_t c = mcomp[k];
+        completion[i] = c;
+        const std::uint64_t t = rec[i].issue_ps;
+        p.deferred += admit[i] > t ? 1u : 0u;
+        if ((mstat[k] & 3u) == 0) {
+            const std::uint64_t lat = c - t;
+            add128(p.lat_lo, p.lat_hi, lat);
+            p.lat_max = lat > p.lat_max ? lat : p.lat_max;
+            ++p.modeled;
+        }
+    }
+    s[threadIdx.x] = p;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Partial t{0, 0, 0, 0, 0};
+        for (int k = 0; k < kThreads; ++k) {
+            t.deferred += s[k].deferred;
+            t.modeled += s[k].modeled;
+            t.lat_hi += s[k].lat_hi;
+            add128(t.lat_lo, t.lat_hi, s[k].lat_lo);
+            t.lat_max = s[k].lat_max > t.lat_max ? s[k].lat_max : t.lat_max;
+        }
+        part[blockIdx.x] = t;
+    }
+}
+
+// ---------------------------------------------------------------------------
+
+hipError_t halloc_bytes(void** p, std::size_t bytes)
+{
+    return hipMalloc(p, bytes == 0 ? 16 : bytes);
+}
+
+template <class T>
+hipError_t halloc(T*& p, std::size_t count)
+{
+    return halloc_bytes(reinterpret_cast<void**>(&p), count * sizeof(T));
+}
+
+template <class T>
+void hfree(T*& p)
+{
+    if (p != nullptr) {
+        (void)hipFree(p);
+        p = nullptr;
+    }
+}
+
+// Largest tile edge in {16, 8, 4, 2, 1} whose staged region fits.
+void choose_tile(std::uint32_t nz, std::uint32_t sweeps, std::uint32_t div_x,
+                 std::uint32_t div_y, std::uint32_t& tx, std::uint32_t& ty)
+{
+    for (std::uint32_t t = 16; t >= 1; t >>= 1) {
+        const std::uint32_t r = t + 2 * sweeps;
+        if (static_cast<std::uint64_t>(r) * r * nz <= kMaxRegion && div_x % t == 0 &&
+            div_y % t == 0) {
+            tx = ty = t;
+            return;
+        }
+        if (t == 1) {
+            break;
+        }
+    }
+    tx = ty = 0;
+}
+
+void host_retention_table(double ea, double tref, std::uint64_t window_ps, std::uint64_t* table)
+{
+    for (std::uint32_t b = 0; b < kAfBins; ++b) {
+        const double t = kAfT0 + (static_cast<double>(b) + 0.5) / kAfStepsPerK;
+        const double af = std::exp(ea / 8.62e-5 * (1.0 / tref - 1.0 / t));
+        const double v = static_cast<double>(window_ps) * af;
+        table[b] = v >= 1.8e19 ? ~0ull : static_cast<std::uint64_t>(std::llround(v));
+    }
+}
+
+}  // namespace
+
+struct thermal {
+    hbfsim_amd_thermal_grid grid{};
+    int device = 0;
+    double* d_scratch = nullptr;   // second temperature buffer
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    float last_ms = 0.0f;
+    // last coupled run
+    std::uint64_t windows = 0;
+    std::uint32_t ndie = 0;
+    std::vector<double> hot;
+    std::vector<std::uint8_t> level, refresh;
+};
+
+int thermal_create(const hbfsim_amd_thermal_grid& g, thermal** out)
+{
+    *out = nullptr;
+    if (g.nx == 0 || g.ny == 0 || g.nz == 0 || g.sweeps == 0 || g.sweeps > 8 ||
+        !(g.capacity_j_per_k > 0.0) || !(g.dt_s > 0.0) || !(g.gx_w_per_k >= 0.0) ||
+        !(g.gy_w_per_k >= 0.0) || !(g.gz_w_per_k >= 0.0) || !(g.top_g_w_per_k >= 0.0) ||
+        !std::isfinite(g.ambient_k)) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    std::uint32_t tx, ty;
+    choose_tile(g.nz, g.sweeps, 16, 16, tx, ty);
+    if (tx == 0) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    auto* th = new (std::nothrow) thermal;
+    if (th == nullptr) {
+        return HBFSIM_IO_ERROR;
+    }
+    th->grid = g;
+    hipError_t err = hipGetDevice(&th->device);
+    if (err == hipSuccess)
+        err = halloc(th->d_scratch, static_cast<std::size_t>(g.nx) * g.ny * g.nz);
+    for (int i = 0; i < 2 && err == hipSuccess; ++i) {
+        err = hipEventCreate(&th->ev[i]);
+    }
+    if (err != hipSuccess) {
+        thermal_destroy(th);
+        return HBFSIM_CUDA_ERROR;
+    }
+    *out = th;
+    return HBFSIM_OK;
+}
+
+void thermal_destroy(thermal* th)
+{
+    if (th == nullptr) {
+        return;
+    }
+    (void)hipSetDevice(th->device);
+    (void)hipDeviceSynchronize();
+    hfree(th->d_scratch);
+    for (auto& e : th->ev) {
+        if (e != nullptr) {
+            (void)hipEventDestroy(e);
+        }
+    }
+    delete th;
+}
+
+const hbfsim_amd_thermal_grid& thermal_get_grid(const thermal* th) { return th->grid; }
+
+float thermal_last_step_ms(const thermal* th) { return th->last_ms; }
+
+namespace {
+
+TArgs base_args(const hbfsim_amd_thermal_grid& g, std::uint32_t tx, std::uint32_t ty)
+{
+    TArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.nx = g.nx;
+    a.ny = g.ny;
+    a.nz = g.nz;
+    a.sweeps = g.sweeps;
+    a.tx = tx;
+    a.ty = ty;
+    a.rx = tx + 2 * g.sweeps;
+    a.ry = ty + 2 * g.sweeps;
+    a.tiles_x = (g.nx + tx - 1) / tx;
+    a.cells = a.rx * a.ry * g.nz;
+    a.cdt = g.capacity_j_per_k / g.dt_s;
+    a.gx = g.gx_w_per_k;
+    a.gy = g.gy_w_per_k;
+    a.gz = g.gz_w_per_k;
+    a.gb = g.top_g_w_per_k;
+    a.tb = g.ambient_k;
+    a.rw = a.rh = a.lpd = a.regions_x = a.D = 1;
+    return a;
+}
+
+std::uint32_t tile_blocks(const TArgs& a)
+{
+    return a.tiles_x * ((a.ny + a.ty - 1) / a.ty);
+}
+
+}  // namespace
+
+int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64_t steps,
+                 void* stream_ptr)
+{
+    if (d_power == nullptr || d_temp == nullptr) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    if (steps == 0) {
+        return HBFSIM_OK;
+    }
+    if (hipSetDevice(th->device) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    const auto& g = th->grid;
+    std::uint32_t tx, ty;
+    choose_tile(g.nz, g.sweeps, 16, 16, tx, ty);
+    TArgs a = base_args(g, tx, ty);
+    a.power = d_power;
+    const std::size_t lds = 2ull * a.cells * sizeof(double);
+    const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
+    double* buf[2] = {d_temp, th->d_scratch};
+    (void)hipEventRecord(th->ev[0], stream);
+    for (std::uint64_t s = 0; s < steps; ++s) {
+        hipLaunchKernelGGL(k_thermal_window, dim3(tile_blocks(a)), dim3(kThreads), lds, stream,
+                           a, buf[s & 1], buf[(s + 1) & 1], 0ull);
+    }
+    (void)hipEventRecord(th->ev[1], stream);
+    hipError_t err = hipGetLastError();
+    if (err == hipSuccess && (steps & 1)) {
+        err = hipMemcpyAsync(d_temp, th->d_scratch, cells * sizeof(double),
+                             hipMemcpyDeviceToDevice, stream);
+    }
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, th->ev[0], th->ev[1]) == hipSuccess) {
+        th->last_ms = ms / static_cast<float>(steps);
+    }
+    return HBFSIM_OK;
+}
+
+int coupled_run(engine* e, const engine_config& cfg, thermal* th,
+                const hbfsim_amd_reliability_options& o, const hbf_record32* d_rec,
+                std::size_t n, std::uint64_t* d_comp, double* d_temp, std::uint64_t* age,
+                void* stream_ptr, hbfsim_amd_coupled_report* out, hbfsim_amd_report* erep)
+{
+    hbfsim_amd_coupled_report rep;
+    std::memset(&rep, 0, sizeof(rep));
+    if (out != nullptr) *out = rep;
+    if (erep != nullptr) std::memset(erep, 0, sizeof(*erep));
+    const auto& g = th->grid;
+    const std::uint32_t cw = cfg.channels * cfg.ways;
+    const std::uint32_t ndie = cw * cfg.dies;
+    if (d_temp == nullptr || age == nullptr || (n != 0 && (d_rec == nullptr || d_comp == nullptr))) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    if (o.regions_x == 0 || o.regions_y == 0 || o.regions_x * o.regions_y != cw ||
+        g.nx % o.regions_x != 0 || g.ny % o.regions_y != 0 || g.nz % cfg.dies != 0 ||
+        o.window_ps == 0 || o.policy > 1) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    if (std::fabs(static_cast<double>(o.window_ps) * 1e-12 - g.dt_s) > 1e-9 * g.dt_s ||
+        cfg.dies > 64 || ndie > kMaxDies || cfg.model != HBFSIM_AMD_MODEL_HBF) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    const std::uint32_t rw = g.nx / o.regions_x, rh = g.ny / o.regions_y;
+    std::uint32_t tx, ty;
+    choose_tile(g.nz, g.sweeps, rw, rh, tx, ty);
+    if (tx == 0) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    if (hipSetDevice(th->device) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+    std::uint64_t windows = 0;
+    if (n != 0) {
+        std::uint64_t last = 0;
+        if (hipMemcpyAsync(&last, &d_rec[n - 1].issue_ps, 8, hipMemcpyDeviceToHost, stream) !=
+                hipSuccess ||
+            hipStreamSynchronize(stream) != hipSuccess) {
+            return HBFSIM_CUDA_ERROR;
+        }
+        windows = last / o.window_ps + 1;
+    }
+    rep.windows = windows;
+    if (windows > (1ull << 26)) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
+
+    std::uint32_t* d_counts = nullptr;
+    unsigned long long* d_hot = nullptr;
+    std::uint64_t* d_af = nullptr;
+    std::uint64_t* d_age = nullptr;  // [2][ndie]
+    Ctl* d_ctl = nullptr;            // [2]
+    std::uint8_t* d_level = nullptr;
+    std::uint8_t* d_refresh = nullptr;
+    std::uint32_t* d_ok2 = nullptr;
+    MaxPlus* d_gtiles = nullptr;
+    std::uint64_t* d_gcarry = nullptr;
+    std::uint64_t* d_admit = nullptr;
+    hbf_record32* d_ref = nullptr;
+    std::uint64_t* d_ref_issue = nullptr;
+    hbf_record32* d_merged = nullptr;
+    std::uint64_t* d_pos = nullptr;
+    std::uint64_t* d_mcomp = nullptr;
+    std::uint8_t* d_mstat = nullptr;
+    Partial* d_part = nullptr;
+    auto release = [&]() {
+        hfree(d_counts); hfree(d_hot); hfree(d_af); hfree(d_age); hfree(d_ctl);
+        hfree(d_level); hfree(d_refresh); hfree(d_ok2); hfree(d_gtiles); hfree(d_gcarry);
+        hfree(d_admit); hfree(d_ref); hfree(d_ref_issue); hfree(d_merged); hfree(d_pos);
+        hfree(d_mcomp); hfree(d_mstat); hfree(d_part);
+    };
+    const std::size_t wd = static_cast<std::size_t>(windows) * ndie;
+    hipError_t err = halloc(d_counts, wd + 2);
+    if (err == hipSuccess) err = halloc(d_hot, wd + ndie);
+    if (err == hipSuccess) err = halloc(d_af, kAfBins);
+    if (err == hipSuccess) err = halloc(d_age, 2ull * ndie);
+    if (err == hipSuccess) err = halloc(d_ctl, 2);
+    if (err == hipSuccess) err = halloc(d_level, windows);
+    if (err == hipSuccess) err = halloc(d_refresh, wd);
+    if (err != hipSuccess) {
+        release();
+        return HBFSIM_CUDA_ERROR;
+    }
+    // 1. per-window, per-die access counts
+    const unsigned fill_blocks = static_cast<unsigned>(std::min<std::size_t>((wd + ndie + 255) / 256, 65536));
+    hipLaunchKernelGGL(k_fill_u64, dim3(std::max(1u, fill_blocks)), dim3(256), 0, stream,
+                       d_hot, wd + ndie, 0ull);
+    int st = HBFSIM_OK;
+    if (wd != 0) {
+        hipLaunchKernelGGL(k_fill_u64, dim3(static_cast<unsigned>(std::min<std::size_t>((wd / 2 + 256) / 256, 65536))),
+                           dim3(256), 0, stream, reinterpret_cast<unsigned long long*>(d_counts),
+                           (wd * 4 + 7) / 8, 0ull);
+        st = engine_window_counts(e, d_rec, n, o.window_ps, windows, d_counts, stream_ptr);
+    }
+    if (st != HBFSIM_OK) {
+        release();
+        return st;
+    }
+    // 2. thermal / retention / throttle chain
+    std::vector<std::uint64_t> table(kAfBins);
+    host_retention_table(o.activation_energy_ev, o.reference_k, o.window_ps, table.data());
+    Ctl c0{0, kNoPending, 0, 0};
+    err = hipMemcpyAsync(d_af, table.data(), kAfBins * 8, hipMemcpyHostToDevice, stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(d_age, age, ndie * 8ull, hipMemcpyHostToDevice, stream);
+    if (err == hipSuccess) err = hipMemcpyAsync(d_ctl, &c0, sizeof(Ctl), hipMemcpyHostToDevice, stream);
+    TArgs a = base_args(g, tx, ty);
+    a.coupled = 1;
+    a.ndie = ndie;
+    a.regions_x = o.regions_x;
+    a.rw = rw;
+    a.rh = rh;
+    a.D = cfg.dies;
+    a.lpd = g.nz / cfg.dies;
+    a.policy = o.policy;
+    a.static_w = o.static_power_w;
+    const double cells_per_die = static_cast<double>(rw * rh * a.lpd);
+    a.pa = (o.access_energy_j / g.dt_s) / cells_per_die;
+    a.pr = (o.refresh_energy_j / g.dt_s) / cells_per_die;
+    a.counts = d_counts;
+    a.hot = d_hot;
+    a.af = d_af;
+    a.retention_ps = o.retention_ps;
+    a.window_ps = o.window_ps;
+    a.light_k = o.light_k;
+    a.severe_k = o.severe_k;
+    a.shutdown_k = o.shutdown_k;
+    a.hysteresis_k = o.hysteresis_k;
+    a.action_delay_ps = o.action_delay_ps;
+    a.min_dwell_ps = o.min_dwell_ps;
+    a.level = d_level;
+    a.refresh = d_refresh;
+    if (err == hipSuccess) {
+        hipLaunchKernelGGL(k_die_hot, dim3(static_cast<unsigned>(std::min<std::size_t>((cells + 255) / 256, 4096))),
+                           dim3(256), 0, stream, a, static_cast<const double*>(d_temp), d_hot);
+    }
+    const std::size_t lds = 2ull * a.cells * sizeof(double);
+    double* buf[2] = {d_temp, th->d_scratch};
+    for (std::uint64_t w = 0; w < windows && err == hipSuccess; ++w) {
+        a.age_in = d_age + (w & 1) * ndie;
+        a.age_out = d_age + ((w + 1) & 1) * ndie;
+        a.ctl_in = d_ctl + (w & 1);
+        a.ctl_out = d_ctl + ((w + 1) & 1);
+        hipLaunchKernelGGL(k_thermal_window, dim3(tile_blocks(a)), dim3(kThreads), lds, stream,
+                           a, buf[w & 1], buf[(w + 1) & 1], w);
+    }
+    if (err == hipSuccess) err = hipGetLastError();
+    if (err == hipSuccess && (windows & 1)) {
+        err = hipMemcpyAsync(d_temp, th->d_scratch, cells * sizeof(double),
+                             hipMemcpyDeviceToDevice, stream);
+    }
+    th->hot.assign(wd + ndie, 0.0);
+    th->level.assign(windows, 0);
+    th->refresh.assign(wd, 0);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(age, d_age + (windows & 1) * ndie, ndie * 8ull, hipMemcpyDeviceToHost,
+                             stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(th->hot.data(), d_hot, (wd + ndie) * 8, hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess && windows)
+        err = hipMemcpyAsync(th->level.data(), d_level, windows, hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess && wd)
+        err = hipMemcpyAsync(th->refresh.data(), d_refresh, wd, hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) {
+        release();
+        return HBFSIM_CUDA_ERROR;
+    }
+    th->windows = windows;
+    th->ndie = ndie;
+    for (std::uint64_t w = 0; w < windows; ++w) {
+        rep.level_windows[th->level[w] & 3] += 1;
+    }
+    for (double v : th->hot) {
+        rep.peak_k = v > rep.peak_k ? v : rep.peak_k;
+    }
+
+    // 3. admission, refresh records, merge
+    std::vector<std::uint32_t> ok2(windows + 1), ok3(windows + 1);
+    ok2[windows] = ok3[windows] = static_cast<std::uint32_t>(windows);
+    for (std::uint64_t w = windows; w-- > 0;) {
+        ok2[w] = th->level[w] < 2 ? static_cast<std::uint32_t>(w) : ok2[w + 1];
+        ok3[w] = th->level[w] < 3 ? static_cast<std::uint32_t>(w) : ok3[w + 1];
+    }
+    std::vector<hbf_record32> refs;
+    std::vector<std::uint64_t> ref_issue;
+    {
+        const std::uint32_t sizes[4] = {cfg.channels, cfg.ways, cfg.dies, cfg.planes};
+        std::uint64_t div[4];
+        std::uint64_t stride = 1;
+        for (int i = 0; i < 4; ++i) {
+            div[cfg.order[i]] = stride;
+            stride *= sizes[cfg.order[i]];
+        }
+        const std::uint64_t pages = cfg.media_pages == ~0ull ? 0ull : cfg.media_pages;
+        std::uint64_t rows = pages / stride;
+        if (rows == 0) rows = 1;
+        std::vector<std::uint64_t> ordinal(ndie, 0);
+        for (std::uint64_t w = 0; w < windows; ++w) {
+            for (std::uint32_t d = 0; d < ndie; ++d) {
+                if (!th->refresh[w * ndie + d]) continue;
+                const std::uint32_t q = d / cfg.dies, dd = d % cfg.dies;
+                const std::uint64_t k = ordinal[d]++;
+                const std::uint64_t coord[4] = {q / cfg.ways, q % cfg.ways, dd, k % cfg.planes};
+                std::uint64_t page = ((k / cfg.planes) % rows) * stride;
+                for (int ax = 0; ax < 4; ++ax) page += coord[ax] * div[ax];
+                hbf_record32 r;
+                r.addr = page;
+                r.bytes = 2ull << cfg.page_shift;
+                const std::uint64_t t = w * o.window_ps;
+                r.issue_ps = th->level[w] >= 3 ? static_cast<std::uint64_t>(ok3[w + 1]) * o.window_ps : t;
+                r.flags = 2u | 0x100u;
+                refs.push_back(r);
+                ref_issue.push_back(r.issue_ps);
+            }
+        }
+    }
+    const std::size_t nref = refs.size();
+    rep.refreshes = nref;
+    const std::size_t total = n + nref;
+    const std::uint32_t per = 16;
+    const std::uint32_t gtile = kThreads * per;
+    const std::size_t gtiles = (n + gtile - 1) / gtile;
+    err = halloc(d_ok2, windows + 1);
+    if (err == hipSuccess) err = halloc(d_gtiles, gtiles);
+    if (err == hipSuccess) err = halloc(d_gcarry, gtiles);
+    if (err == hipSuccess) err = halloc(d_admit, n);
+    if (err == hipSuccess) err = halloc(d_ref, nref);
+    if (err == hipSuccess) err = halloc(d_ref_issue, nref);
+    if (err == hipSuccess) err = halloc(d_merged, total);
+    if (err == hipSuccess) err = halloc(d_pos, n);
+    if (err == hipSuccess) err = halloc(d_mcomp, total);
+    if (err == hipSuccess) err = halloc(d_mstat, total);
+    const unsigned gblocks = static_cast<unsigned>(std::min<std::size_t>((n + kThreads - 1) / kThreads, 4096));
+    if (err == hipSuccess) err = halloc(d_part, std::max(1u, gblocks));
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(d_ok2, ok2.data(), ok2.size() * 4, hipMemcpyHostToDevice, stream);
+    if (err == hipSuccess && nref)
+        err = hipMemcpyAsync(d_ref, refs.data(), nref * sizeof(hbf_record32), hipMemcpyHostToDevice,
+                             stream);
+    if (err == hipSuccess && nref)
+        err = hipMemcpyAsync(d_ref_issue, ref_issue.data(), nref * 8, hipMemcpyHostToDevice, stream);
+    if (err != hipSuccess) {
+        release();
+        return HBFSIM_CUDA_ERROR;
+    }
+    if (n != 0) {
+        GArgs ga;
+        ga.rec = d_rec;
+        ga.n = n;
+        ga.tile = gtile;
+        ga.per = per;
+        ga.window_ps = o.window_ps;
+        ga.windows = windows;
+        ga.light_gap_ps = o.light_gap_ps;
+        ga.level = d_level;
+        ga.ok2 = d_ok2;
+        hipLaunchKernelGGL(k_gate_summary, dim3(static_cast<unsigned>(gtiles)), dim3(kThreads), 0,
+                           stream, ga, d_gtiles);
+        hipLaunchKernelGGL(k_gate_carry, dim3(1), dim3(kThreads), 0, stream,
+                           static_cast<const MaxPlus*>(d_gtiles), gtiles, d_gcarry);
+        hipLaunchKernelGGL(k_gate_apply, dim3(static_cast<unsigned>(gtiles)), dim3(kThreads), 0,
+                           stream, ga, static_cast<const std::uint64_t*>(d_gcarry), d_admit);
+        hipLaunchKernelGGL(k_merge_demand, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
+                           0, stream, d_rec, n, static_cast<const std::uint64_t*>(d_admit),
+                           static_cast<const std::uint64_t*>(d_ref_issue), nref, d_merged, d_pos);
+    }
+    if (nref != 0) {
+        hipLaunchKernelGGL(k_refresh_place, dim3(static_cast<unsigned>((nref + 255) / 256)),
+                           dim3(256), 0, stream, static_cast<const hbf_record32*>(d_ref), nref,
+                           static_cast<const std::uint64_t*>(d_admit), n, d_merged);
+    }
+    err = hipGetLastError();
+    if (err != hipSuccess) {
+        release();
+        return HBFSIM_CUDA_ERROR;
+    }
+    // 4. the engine on the merged stream
+    hbfsim_amd_report er;
+    st = engine_run(e, d_merged, total, d_mcomp, d_mstat, 0, stream_ptr, &er);
+    if (st != HBFSIM_OK) {
+        release();
+        return st;
+    }
+    rep.makespan_ps = er.makespan_ps;
+    if (n != 0) {
+        hipLaunchKernelGGL(k_gather, dim3(gblocks), dim3(kThreads), 0, stream, d_rec, n,
+                           static_cast<const std::uint64_t*>(d_admit),
+                           static_cast<const std::uint64_t*>(d_pos),
+                           static_cast<const std::uint64_t*>(d_mcomp),
+                           static_cast<const std::uint8_t*>(d_mstat), d_comp, d_part);
+        std::vector<Partial> parts(gblocks);
+        err = hipGetLastError();
+        if (err == hipSuccess)
+            err = hipMemcpyAsync(parts.data(), d_part, gblocks * sizeof(Partial),
+                                 hipMemcpyDeviceToHost, stream);
+        if (err == hipSuccess) err = hipStreamSynchronize(stream);
+        if (err != hipSuccess) {
+            release();
+            return HBFSIM_CUDA_ERROR;
+        }
+        for (const Partial& p : parts) {
+            rep.deferred += p.deferred;
+            rep.demand_modeled += p.modeled;
+            rep.latency_sum_hi += p.lat_hi;
+            const std::uint64_t lo = rep.latency_sum_lo + p.lat_lo;
+            rep.latency_sum_hi += lo < rep.latency_sum_lo ? 1u : 0u;
+            rep.latency_sum_lo = lo;
+            rep.latency_max_ps = std::max<std::uint64_t>(rep.latency_max_ps, p.lat_max);
+        }
+    }
+    release();
+    if (out != nullptr) *out = rep;
+    if (erep != nullptr) *erep = er;
+    return HBFSIM_OK;
+}
+
+int coupled_trace(const thermal* th, double* hot, std::size_t hot_count, std::uint8_t* level,
+                  std::size_t level_count, std::uint8_t* refresh, std::size_t refresh_count,
+                  std::uint64_t* windows, std::uint32_t* dies)
+{
+    if (windows != nullptr) *windows = th->windows;
+    if (dies != nullptr) *dies = th->ndie;
+    if ((hot != nullptr && hot_count < th->hot.size()) ||
+        (level != nullptr && level_count < th->level.size()) ||
+        (refresh != nullptr && refresh_count < th->refresh.size())) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    if (hot != nullptr && !th->hot.empty())
+        std::memcpy(hot, th->hot.data(), th->hot.size() * sizeof(double));
+    if (level != nullptr && !th->level.empty())
+        std::memcpy(level, th->level.data(), th->level.size());
+    if (refresh != nullptr && !th->refresh.empty())
+        std::memcpy(refresh, th->refresh.data(), th->refresh.size());
+    return HBFSIM_OK;
+}
+
+}  // namespace hbfamd

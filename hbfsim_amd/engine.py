@@ -212,6 +212,113 @@ class Engine:
         k = self._lib.hbfsim_amd_last_kernel_ms(self._ctx, ms, 8)
         return [float(ms[i]) for i in range(k)]
 
+    def run_coupled(self, thermal: "Thermal", options: dict, records: Any, completion: Any,
+                    temperature: Any, age_ps: np.ndarray, stream: Any = None) -> tuple[dict, dict]:
+        """Thermal-coupled run (hbfsim_amd_run_coupled): returns the coupled
+        report and the engine report of the merged stream; `temperature`
+        (device) and `age_ps` (host uint64, one per die) are updated."""
+        n = int(records.shape[0])
+        stream = _stream_handle(stream)
+        opts = reliability_options(**options)
+        rep, erep = nat.CoupledReport(), nat.Report()
+        if age_ps.dtype != np.uint64 or not age_ps.flags.c_contiguous:
+            raise ValueError("age_ps must be a contiguous uint64 array")
+        nat.check(self._lib.hbfsim_amd_run_coupled(
+            self._ctx, thermal.handle, ctypes.byref(opts), _ptr(records), n, _ptr(completion),
+            _ptr(temperature), _ptr(age_ps), ctypes.c_void_p(stream), ctypes.byref(rep),
+            ctypes.byref(erep)), "coupled run")
+        return rep.as_dict(), erep.as_dict()
+
+
+def _stream_handle(stream: Any) -> int:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if hasattr(stream, "cuda_stream"):
+        return stream.cuda_stream
+    return stream
+
+
+def reliability_options(**kw: Any) -> nat.ReliabilityOptions:
+    """hbfsim_amd_reliability_options from keyword arguments (field names of
+    include/hbfsim_amd.h); unnamed fields are zero."""
+    o = nat.ReliabilityOptions()
+    o.struct_size = ctypes.sizeof(o)
+    names = {f for f, _ in nat.RELIABILITY_FIELDS}
+    for k, v in kw.items():
+        if k not in names or k == "struct_size":
+            raise KeyError(f"unknown reliability option {k!r}")
+        setattr(o, k, v)
+    return o
+
+
+class Thermal:
+    """The EQ3 grid (hbfsim_amd_thermal_*): backward-Euler steps on device
+    temperature arrays (float64, nx*ny*nz, x fastest)."""
+
+    def __init__(self, nx: int, ny: int, nz: int, capacity_j_per_k: float, gx_w_per_k: float,
+                 gy_w_per_k: float, gz_w_per_k: float, top_g_w_per_k: float, ambient_k: float,
+                 dt_s: float, sweeps: int = 4):
+        self._lib = nat.load()
+        g = nat.ThermalGrid()
+        g.struct_size = ctypes.sizeof(g)
+        g.nx, g.ny, g.nz, g.sweeps = nx, ny, nz, sweeps
+        g.capacity_j_per_k, g.gx_w_per_k, g.gy_w_per_k = capacity_j_per_k, gx_w_per_k, gy_w_per_k
+        g.gz_w_per_k, g.top_g_w_per_k, g.ambient_k, g.dt_s = (gz_w_per_k, top_g_w_per_k,
+                                                               ambient_k, dt_s)
+        self.grid = g
+        h = ctypes.c_void_p()
+        nat.check(self._lib.hbfsim_amd_thermal_create(ctypes.byref(g), ctypes.byref(h)),
+                  "thermal create")
+        self._h = h
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        if self._h is None:
+            raise RuntimeError("thermal grid is closed")
+        return self._h
+
+    @property
+    def cells(self) -> int:
+        return self.grid.nx * self.grid.ny * self.grid.nz
+
+    def step(self, power: Any, temperature: Any, steps: int = 1, stream: Any = None) -> None:
+        nat.check(self._lib.hbfsim_amd_thermal_step(self.handle, _ptr(power), _ptr(temperature),
+                                                    steps, ctypes.c_void_p(_stream_handle(stream))),
+                  "thermal step")
+
+    def last_ms(self) -> float:
+        ms = ctypes.c_float()
+        nat.check(self._lib.hbfsim_amd_thermal_last_ms(self.handle, ctypes.byref(ms)),
+                  "thermal time")
+        return float(ms.value)
+
+    def trace(self) -> dict:
+        """Per-window trace of the last coupled run."""
+        w, d = ctypes.c_uint64(), ctypes.c_uint32()
+        nat.check(self._lib.hbfsim_amd_coupled_trace(self.handle, None, 0, None, 0, None, 0,
+                                                     ctypes.byref(w), ctypes.byref(d)), "trace")
+        windows, dies = int(w.value), int(d.value)
+        hot = np.zeros((windows + 1) * dies, dtype=np.float64)
+        level = np.zeros(windows, dtype=np.uint8)
+        refresh = np.zeros(windows * dies, dtype=np.uint8)
+        nat.check(self._lib.hbfsim_amd_coupled_trace(
+            self.handle, _ptr(hot), hot.size, _ptr(level), level.size, _ptr(refresh),
+            refresh.size, ctypes.byref(w), ctypes.byref(d)), "trace")
+        return {"windows": windows, "dies": dies, "hot": hot.reshape(windows + 1, dies),
+                "level": level, "refresh": refresh.reshape(windows, dies)}
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None:
+            self._lib.hbfsim_amd_thermal_destroy(self._h)
+            self._h = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
 
 def validate_profile(path: str) -> str | None:
     """None when the profile is valid, else the reference's error message."""

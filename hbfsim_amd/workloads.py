@@ -131,6 +131,43 @@ class MoeShape:
 
 QWEN3_30B_A3B = MoeShape()
 
+# Config 4: OLMoE-shaped trace (16 layers x 64 experts, top-8 of 32 tokens,
+# intermediate 1024) under the thermal-coupled model.
+OLMOE = MoeShape(layers=16, experts=64, intermediate=1024, seed=3, base=0x6000_0000_0000)
+C4_ACCESSES = 100_000_000
+
+# The 64 x 64 x 8 EQ3 grid of config 4: one layer per die of an 11 mm x
+# 11 mm stack of 8 dies thinned to 50 um (cell 172 um x 172 um x 50 um of
+# silicon, 1.66e6 J/(m^3 K), 150 W/(m K) laterally; 4.3e-3 W/K per cell
+# through a 10-um bond layer between dies; 2 W/K from the top die to a
+# 45 C ambient), stepped every 1 us.
+C4_GRID = dict(nx=64, ny=64, nz=8, sweeps=4, capacity_j_per_k=2.46e-6, gx_w_per_k=7.5e-3,
+               gy_w_per_k=7.5e-3, gz_w_per_k=4.3e-3, top_g_w_per_k=4.9e-4, ambient_k=318.15,
+               dt_s=1e-6)
+# Reliability inputs (the reference leaves them null: reliability.json): Ea
+# 1.04 eV at 85 C (test_system_models.py:12), a retention period of 50 us at
+# 85 C (time-compressed so refresh shows within a 25-ms trace), 20 nJ per
+# 128-B access, 10 uJ per refresh, 0.1 W static per die; throttle at 55 /
+# 60 / 70 C with 1 K hysteresis, 2-us action delay, 10-us dwell, and one
+# admission per ns while light.  Channel c occupies block (c % 4, c / 4) of
+# the x-y plane.
+C4_RELIABILITY = dict(policy=1, regions_x=4, regions_y=2, window_ps=1_000_000,
+                      static_power_w=2e-4, access_energy_j=20e-9, refresh_energy_j=10e-6,
+                      activation_energy_ev=1.04, reference_k=358.15, retention_ps=50_000_000,
+                      light_k=328.15, severe_k=333.15, shutdown_k=343.15, hysteresis_k=1.0,
+                      action_delay_ps=2_000_000, min_dwell_ps=10_000_000, light_gap_ps=1000)
+
+
+def staggered_ages(dies: int, retention_ps: int) -> np.ndarray:
+    """Initial equivalent ages: die d last refreshed d/dies of a period ago."""
+    return np.array([d * retention_ps // dies for d in range(dies)], np.uint64)
+
+
+def c4_segments(shape: MoeShape = OLMOE, steps: int = 2) -> np.ndarray:
+    """Expert bases of `steps` decode steps streamed back to back."""
+    sel = moe_selection(shape, steps)
+    return np.concatenate([moe_segments(shape, s) for s in sel])
+
 
 def zipf_alias(n: int, s: float) -> tuple[np.ndarray, np.ndarray]:
     """Walker/Vose alias table for P(k) ~ 1/(k+1)^s, k = 0..n-1, with

@@ -334,6 +334,119 @@ int hbfsim_amd_gen_segment_lines(hbf_record32* d_records, size_t capacity,
                                  uint64_t gap_ps, uint32_t issuers, uint64_t flags,
                                  void* stream);
 
+/* ===== 4. EQ3 thermal grid and thermal-coupled reliability =============
+ *
+ * The reference's RC network (src/eq3_thermal/thermal.cpp:127-311) on a
+ * regular grid: nx * ny * nz cells (x fastest, z = nz - 1 the top layer),
+ * uniform heat capacity, conductances gx / gy / gz between neighbouring
+ * cells and top_g from every top-layer cell to the ambient.  One step is
+ * ThermalModel::advance_to's backward-Euler solve,
+ *   (C/dt + G_top + L) T' = C/dt T + P + G_top T_ambient,
+ * by `sweeps` Jacobi sweeps (the system is strictly diagonally dominant;
+ * at the stiffness of a 1-us step a few sweeps reach double precision). */
+typedef struct hbfsim_amd_thermal_grid {
+    uint32_t struct_size;      /* sizeof(hbfsim_amd_thermal_grid) */
+    uint32_t nx, ny, nz;
+    uint32_t sweeps;           /* Jacobi sweeps per step, 1..8 */
+    uint32_t reserved0;
+    double capacity_j_per_k;   /* per cell */
+    double gx_w_per_k, gy_w_per_k, gz_w_per_k;
+    double top_g_w_per_k;      /* each top-layer cell to ambient */
+    double ambient_k;
+    double dt_s;               /* step length */
+} hbfsim_amd_thermal_grid;
+
+typedef struct hbfsim_amd_thermal hbfsim_amd_thermal;
+
+/* Replaces ThermalModel's constructor for a grid network
+ * (thermal.cpp:242-311).  Owns device scratch on the current device. */
+int hbfsim_amd_thermal_create(const hbfsim_amd_thermal_grid* grid,
+                              hbfsim_amd_thermal** out);
+/* ThermalModel::advance_to (thermal.cpp:127-160) with constant power:
+ * `steps` steps.  d_power: W per cell; d_temperature: K per cell, updated in
+ * place.  Device arrays of nx*ny*nz doubles.  Returns when done. */
+int hbfsim_amd_thermal_step(hbfsim_amd_thermal* thermal, const double* d_power,
+                            double* d_temperature, uint64_t steps,
+                            void* stream);
+/* Average device time (ms) of one step in the last hbfsim_amd_thermal_step
+ * call, from HIP events on its stream. */
+int hbfsim_amd_thermal_last_ms(const hbfsim_amd_thermal* thermal, float* ms);
+void hbfsim_amd_thermal_destroy(hbfsim_amd_thermal* thermal);
+
+/* Thermal-coupled refresh and throttling.  The grid is stepped once per
+ * window (window_ps = dt).  Channel-way q = c * ways + w occupies the x-y
+ * block (q % regions_x, q / regions_x) of the grid; die d of it occupies
+ * layers [d * nz / dies, (d + 1) * nz / dies).  Per window:
+ *  - control (cpu_service.cpp:221-255, policy "hysteresis"): the stack
+ *    hotspot sets the throttle level (0 none, 1 light, 2 severe,
+ *    3 shutdown) through light/severe/shutdown thresholds, hysteresis,
+ *    action delay and minimum dwell;
+ *  - retention (reliability.py:17-23, 93-108; cpu_service.cpp:169-217):
+ *    each die's equivalent age advances by window_ps times the Arrhenius
+ *    factor of its hotspot, looked up in a table of 1/16-K bins from 200 K;
+ *    at the retention period a refresh of one page of the die is issued
+ *    (plane k % P, row k / P for the die's k-th refresh) and the age
+ *    restarts;
+ *  - power: static + access_energy * (modeled accesses issued to the die in
+ *    the window) / dt + refresh_energy * refreshes / dt, spread evenly over
+ *    the die's cells (observer.cpp:42-72).
+ * Admission (cpu_service.cpp:256-285): records issued in severe or shutdown
+ * windows wait for the next window that admits demand; in light windows
+ * admissions are spaced by light_gap_ps; refreshes wait only for shutdown.
+ * Refresh records (op 2, media flag) join the stream at their admission
+ * time, before demand records admitted at the same time, and are timed by
+ * the engine like any access (plane tR + tPROG, two pages on the channel). */
+typedef struct hbfsim_amd_reliability_options {
+    uint32_t struct_size;      /* sizeof(hbfsim_amd_reliability_options) */
+    uint32_t policy;           /* 0 sample only, 1 hysteresis */
+    uint32_t regions_x, regions_y;  /* regions_x * regions_y = channels*ways */
+    uint64_t window_ps;        /* must equal the grid's dt */
+    double static_power_w;     /* per cell */
+    double access_energy_j;    /* per modeled access */
+    double refresh_energy_j;   /* per refresh */
+    double activation_energy_ev;
+    double reference_k;        /* Arrhenius reference temperature */
+    uint64_t retention_ps;     /* refresh period at reference_k */
+    double light_k, severe_k, shutdown_k, hysteresis_k;
+    uint64_t action_delay_ps, min_dwell_ps, light_gap_ps;
+} hbfsim_amd_reliability_options;
+
+typedef struct hbfsim_amd_coupled_report {
+    uint64_t windows;
+    uint64_t refreshes;
+    uint64_t deferred;           /* demand records admitted after issue */
+    uint64_t level_windows[4];   /* windows at each throttle level */
+    uint64_t demand_modeled;
+    uint64_t latency_sum_lo;     /* completion - issue over modeled demand */
+    uint64_t latency_sum_hi;
+    uint64_t latency_max_ps;
+    uint64_t makespan_ps;        /* latest completion incl. refreshes */
+    double peak_k;               /* hottest die hotspot of the run */
+} hbfsim_amd_coupled_report;
+
+/* One coupled run over n issue-ordered demand records (device), issue_ps
+ * from time 0.  d_completion_ps [n] (device) receives the demand
+ * completions; d_temperature (device, grid cells) holds the initial
+ * temperature and receives the final one; age_ps (host, channels * ways *
+ * dies entries) holds each die's equivalent age and is updated.  Engine
+ * state carries over as for hbfsim_amd_run_device.  Either report may be
+ * NULL; engine_report covers the merged stream. */
+int hbfsim_amd_run_coupled(hbfsim_context* context, hbfsim_amd_thermal* thermal,
+                           const hbfsim_amd_reliability_options* options,
+                           const hbf_record32* d_records, size_t n,
+                           uint64_t* d_completion_ps, double* d_temperature,
+                           uint64_t* age_ps, void* stream,
+                           hbfsim_amd_coupled_report* report,
+                           hbfsim_amd_report* engine_report);
+/* Per-window trace of the last coupled run: die hotspots [(windows + 1) *
+ * dies] (row 0 = the initial temperature), throttle levels [windows],
+ * refresh flags [windows * dies].  Host arrays (any may be NULL); counts are
+ * checked.  *windows and *dies receive the sizes. */
+int hbfsim_amd_coupled_trace(const hbfsim_amd_thermal* thermal, double* hot,
+                             size_t hot_count, uint8_t* level, size_t level_count,
+                             uint8_t* refresh, size_t refresh_count,
+                             uint64_t* windows, uint32_t* dies);
+
 /* Profile validation with the reference's rules and messages
  * (src/profile/profile.cpp:238-468).  Returns HBFSIM_OK or
  * HBFSIM_INVALID_ARGUMENT with the reference's message in `error`. */

@@ -597,6 +597,27 @@ static void decode(const orc_engine_params* p, const orc_range* ranges,
     uint32_t index = 0;
     d->issue = base_ps + rec->issue_ps;
     d->op = op;
+    if (op == ORC_OP_REFRESH && (rec->flags & ORC_FLAG_MEDIA) != 0) {
+        /* refresh of media page `addr`: read it out and program it back
+         * (cpu_service.cpp:181-212's read -> program pair as one job) */
+        const uint64_t page = rec->addr;
+        if (rec->bytes == 0 || rec->bytes > 0xffffffffULL ||
+            (p->media_pages != 0 && page >= p->media_pages) ||
+            page >= (UINT64_MAX >> p->page_shift)) {
+            d->cls = ORC_UNSUPPORTED;
+            return;
+        }
+        d->cls = ORC_MODELED;
+        d->page = page;
+        const uint32_t sz[4] = {p->channels, p->ways, p->dies, p->planes};
+        uint32_t cc[4];
+        orc_stripe(page, p->order, sz, cc);
+        d->channel = cc[0];
+        d->plane = ((cc[0] * p->ways + cc[1]) * p->dies + cc[2]) * p->planes + cc[3];
+        d->xfer = xfer_ps(p, rec->bytes);
+        d->svc_miss = d->svc_hit = p->read_ps + p->program_ps;
+        return;
+    }
     d->cls = orc_classify(ranges, count, rec->addr, rec->bytes, op, &index);
     if (d->cls != ORC_MODELED) {
         return;
@@ -707,7 +728,7 @@ int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
                     rep->page_hits += 1;
                     st |= 4;
                 }
-                if (d.op == 1 && svc_plane != 0) {
+                if (d.op != 0 && svc_plane != 0) {
                     rep->programs += 1;
                     st |= 16;
                 }
@@ -716,7 +737,7 @@ int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
             rep->modeled += 1;
             if (d.op == 0) {
                 rep->reads += 1;
-            } else {
+            } else if (d.op == 1) {
                 rep->writes += 1;
             }
             rep->makespan_ps = max_u64(rep->makespan_ps, done);
@@ -838,7 +859,9 @@ int orc_engine_run_parallel(const orc_engine_params* p,
                     st |= 4;
                 }
             } else {
-                rep->writes += 1;
+                if (d[i].op == 1) {
+                    rep->writes += 1;
+                }
                 if (svc != 0) {
                     rep->programs += 1;
                     st |= 16;
@@ -1035,25 +1058,17 @@ out:
 /* The same backward-Euler step on a regular grid, solved by Jacobi sweeps:
  * T_i <- (C/dt T_i^old + P_i + sum_j g_ij T_j + gb_i tb) / (C/dt + sum_j g_ij
  * + gb_i).  Converges because the system is strictly diagonally dominant. */
-int orc_thermal_grid_step(uint32_t nx, uint32_t ny, uint32_t nz,
-                          double capacity, double gx, double gy, double gz,
-                          double gb, double tb, double dt,
-                          const double* power, double* temperature,
-                          double tol, int max_sweeps)
+/* Jacobi sweeps over caller-provided buffers (old = T at the start of the
+ * step, cur = current iterate, nxt = scratch).  Each cell's numerator and
+ * denominator are accumulated in a fixed order -- x-1, x+1, y-1, y+1, z-1,
+ * z+1, ambient -- which the GPU stencil follows operation for operation. */
+static int grid_jacobi(uint32_t nx, uint32_t ny, uint32_t nz, double cdt,
+                       double gx, double gy, double gz, double gb, double tb,
+                       const double* power, const double* old, double** curp,
+                       double** nxtp, double tol, int max_sweeps)
 {
-    const size_t n = (size_t)nx * ny * nz;
-    double* old = (double*)malloc(n * sizeof(double));
-    double* cur = (double*)malloc(n * sizeof(double));
-    double* nxt = (double*)malloc(n * sizeof(double));
-    if (!old || !cur || !nxt) {
-        free(old);
-        free(cur);
-        free(nxt);
-        return -1;
-    }
-    memcpy(old, temperature, n * sizeof(double));
-    memcpy(cur, temperature, n * sizeof(double));
-    const double cdt = capacity / dt;
+    double* cur = *curp;
+    double* nxt = *nxtp;
     int sweep = 0;
     for (; sweep < max_sweeps; ++sweep) {
         double delta = 0.0;
@@ -1086,11 +1101,36 @@ int orc_thermal_grid_step(uint32_t nx, uint32_t ny, uint32_t nz,
             break;
         }
     }
+    *curp = cur;
+    *nxtp = nxt;
+    return sweep;
+}
+
+int orc_thermal_grid_step(uint32_t nx, uint32_t ny, uint32_t nz,
+                          double capacity, double gx, double gy, double gz,
+                          double gb, double tb, double dt,
+                          const double* power, double* temperature,
+                          double tol, int max_sweeps)
+{
+    const size_t n = (size_t)nx * ny * nz;
+    double* old = (double*)malloc(n * sizeof(double));
+    double* cur = (double*)malloc(n * sizeof(double));
+    double* nxt = (double*)malloc(n * sizeof(double));
+    if (!old || !cur || !nxt) {
+        free(old);
+        free(cur);
+        free(nxt);
+        return -1;
+    }
+    memcpy(old, temperature, n * sizeof(double));
+    memcpy(cur, temperature, n * sizeof(double));
+    const int sweeps = grid_jacobi(nx, ny, nz, capacity / dt, gx, gy, gz, gb,
+                                   tb, power, old, &cur, &nxt, tol, max_sweeps);
     memcpy(temperature, cur, n * sizeof(double));
     free(old);
     free(cur);
     free(nxt);
-    return sweep;
+    return sweeps;
 }
 
 /* reliability.py:17-23 */
@@ -1098,4 +1138,379 @@ double orc_arrhenius(double temperature_k, double ea_ev, double tref_k)
 {
     const double kb = 8.62e-5;
     return exp(ea_ev / kb * (1.0 / tref_k - 1.0 / temperature_k));
+}
+
+/* ---- thermal-coupled reliability ------------------------------------ */
+
+void orc_retention_table(double ea_ev, double tref_k, uint64_t window_ps,
+                         uint64_t* table)
+{
+    for (uint32_t b = 0; b < ORC_AF_BINS; ++b) {
+        const double t = ORC_AF_T0 + ((double)b + 0.5) / ORC_AF_STEPS_PER_K;
+        const double v = (double)window_ps * orc_arrhenius(t, ea_ev, tref_k);
+        table[b] = v >= 1.8e19 ? UINT64_MAX : (uint64_t)llround(v);
+    }
+}
+
+uint32_t orc_retention_bin(double t)
+{
+    if (!(t >= ORC_AF_T0)) {
+        return 0;
+    }
+    const double f = (t - ORC_AF_T0) * ORC_AF_STEPS_PER_K;
+    if (!(f < (double)(ORC_AF_BINS - 1))) {
+        return ORC_AF_BINS - 1;
+    }
+    return (uint32_t)f;
+}
+
+static int reliability_ok(const orc_reliability* r)
+{
+    return r->nx && r->ny && r->nz && r->sweeps && r->regions_x &&
+           r->regions_y && r->dies && r->nx % r->regions_x == 0 &&
+           r->ny % r->regions_y == 0 && r->nz % r->dies == 0 &&
+           r->window_ps != 0 && r->dt_s > 0.0 && r->capacity > 0.0;
+}
+
+static uint32_t die_of_cell(const orc_reliability* r, uint32_t x, uint32_t y,
+                            uint32_t z)
+{
+    const uint32_t rw = r->nx / r->regions_x, rh = r->ny / r->regions_y;
+    const uint32_t lpd = r->nz / r->dies;
+    const uint32_t q = (y / rh) * r->regions_x + x / rw;
+    return q * r->dies + z / lpd;
+}
+
+static void die_hotspots(const orc_reliability* r, const double* t,
+                         double* hot)
+{
+    const uint32_t ndie = r->regions_x * r->regions_y * r->dies;
+    for (uint32_t d = 0; d < ndie; ++d) {
+        hot[d] = 0.0;
+    }
+    for (uint32_t z = 0; z < r->nz; ++z) {
+        for (uint32_t y = 0; y < r->ny; ++y) {
+            for (uint32_t x = 0; x < r->nx; ++x) {
+                const double v = t[((size_t)z * r->ny + y) * r->nx + x];
+                const uint32_t d = die_of_cell(r, x, y, z);
+                if (v > hot[d]) {
+                    hot[d] = v;
+                }
+            }
+        }
+    }
+}
+
+/* cpu_service.cpp:221-255 (control_sample then apply_controls, policy
+ * "hysteresis") for one sample at `now` with stack hotspot `hs`. */
+uint32_t orc_control_step(const orc_reliability* r, orc_control* c,
+                          uint64_t now, double hs)
+{
+    const double thr[4] = {0.0, r->light_k, r->severe_k, r->shutdown_k};
+    uint32_t desired = (uint32_t)(hs >= r->light_k) +
+                       (uint32_t)(hs >= r->severe_k) +
+                       (uint32_t)(hs >= r->shutdown_k);
+    if (desired < c->applied && hs >= thr[c->applied] - r->hysteresis_k) {
+        desired = c->applied;
+    }
+    if (r->policy != 0) {
+        if (desired == c->applied) {
+            c->pending = ORC_NO_PENDING;
+        } else if (c->pending == ORC_NO_PENDING || c->pending != desired) {
+            const uint64_t a = orc_saturating_add(now, r->action_delay_ps);
+            const uint64_t b = orc_saturating_add(c->last_change_ps, r->min_dwell_ps);
+            c->pending = desired;
+            c->pending_at_ps = a > b ? a : b;
+        }
+    }
+    if (c->pending != ORC_NO_PENDING && c->pending_at_ps <= now) {
+        c->applied = c->pending;
+        c->last_change_ps = now;
+        c->pending = ORC_NO_PENDING;
+    }
+    return c->applied;
+}
+
+int orc_reliability_chain(const orc_reliability* r, const uint32_t* counts,
+                          uint64_t windows, double* temperature, uint64_t* age,
+                          orc_control* ctl, double* hot, uint8_t* level,
+                          uint8_t* refresh)
+{
+    if (!reliability_ok(r)) {
+        return 1;
+    }
+    const uint32_t ndie = r->regions_x * r->regions_y * r->dies;
+    const size_t n = (size_t)r->nx * r->ny * r->nz;
+    const double cells =
+        (double)((r->nx / r->regions_x) * (r->ny / r->regions_y) *
+                 (r->nz / r->dies));
+    const double pa = (r->access_energy_j / r->dt_s) / cells;
+    const double pr = (r->refresh_energy_j / r->dt_s) / cells;
+    const double cdt = r->capacity / r->dt_s;
+    uint64_t* table = (uint64_t*)malloc(ORC_AF_BINS * sizeof(uint64_t));
+    double* power = (double*)malloc(n * sizeof(double));
+    double* old = (double*)malloc(n * sizeof(double));
+    double* cur = (double*)malloc(n * sizeof(double));
+    double* nxt = (double*)malloc(n * sizeof(double));
+    if (!table || !power || !old || !cur || !nxt) {
+        free(table);
+        free(power);
+        free(old);
+        free(cur);
+        free(nxt);
+        return 2;
+    }
+    orc_retention_table(r->activation_ev, r->reference_k, r->window_ps, table);
+    die_hotspots(r, temperature, hot);
+    for (uint64_t w = 0; w < windows; ++w) {
+        const uint64_t now = w * r->window_ps;
+        const double* hp = hot + w * ndie;
+        double hs = hp[0];
+        for (uint32_t d = 1; d < ndie; ++d) {
+            if (hp[d] > hs) {
+                hs = hp[d];
+            }
+        }
+        level[w] = (uint8_t)orc_control_step(r, ctl, now, hs);
+        uint8_t* rf = refresh + w * ndie;
+        for (uint32_t d = 0; d < ndie; ++d) {
+            if (w > 0) {
+                age[d] = orc_saturating_add(age[d], table[orc_retention_bin(hp[d])]);
+            }
+            rf[d] = age[d] >= r->retention_ps;
+            if (rf[d]) {
+                age[d] = 0;
+            }
+        }
+        const uint32_t* cw = counts + w * ndie;
+        for (uint32_t z = 0; z < r->nz; ++z) {
+            for (uint32_t y = 0; y < r->ny; ++y) {
+                for (uint32_t x = 0; x < r->nx; ++x) {
+                    const uint32_t d = die_of_cell(r, x, y, z);
+                    power[((size_t)z * r->ny + y) * r->nx + x] =
+                        (r->static_w + (double)cw[d] * pa) + (double)rf[d] * pr;
+                }
+            }
+        }
+        memcpy(old, temperature, n * sizeof(double));
+        memcpy(cur, temperature, n * sizeof(double));
+        (void)grid_jacobi(r->nx, r->ny, r->nz, cdt, r->gx, r->gy, r->gz, r->gb,
+                          r->ambient_k, power, old, &cur, &nxt, -1.0,
+                          (int)r->sweeps);
+        memcpy(temperature, cur, n * sizeof(double));
+        die_hotspots(r, temperature, hot + (w + 1) * ndie);
+    }
+    free(table);
+    free(power);
+    free(old);
+    free(cur);
+    free(nxt);
+    return 0;
+}
+
+uint64_t orc_defer(const uint8_t* level, uint64_t windows, uint64_t window_ps,
+                   uint64_t t, uint32_t limit)
+{
+    uint64_t w = t / window_ps;
+    if (w >= windows || level[w] < limit) {
+        return t;
+    }
+    ++w;
+    while (w < windows && level[w] >= limit) {
+        ++w;
+    }
+    return w * window_ps;
+}
+
+void orc_admit(const uint8_t* level, uint64_t windows, uint64_t window_ps,
+               uint64_t light_gap_ps, const orc_record* rec, size_t n,
+               uint64_t* admit)
+{
+    uint64_t gate = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const uint64_t e = orc_defer(level, windows, window_ps, rec[i].issue_ps, 2);
+        const uint64_t we = e / window_ps;
+        const uint64_t gap = (we < windows && level[we] == 1) ? light_gap_ps : 0;
+        const uint64_t a = e > gate ? e : gate;
+        admit[i] = a;
+        gate = a + gap;
+    }
+}
+
+size_t orc_refresh_records(const orc_engine_params* p, const uint8_t* refresh,
+                           const uint8_t* level, uint64_t windows,
+                           uint64_t window_ps, uint64_t* ordinal,
+                           orc_record* out)
+{
+    const uint32_t sizes[4] = {p->channels, p->ways, p->dies, p->planes};
+    uint64_t div[4];
+    uint64_t stride = 1;
+    for (int i = 0; i < 4; ++i) {
+        div[p->order[i]] = stride;
+        stride *= sizes[p->order[i]];
+    }
+    uint64_t rows = p->media_pages / stride;
+    if (rows == 0) {
+        rows = 1;
+    }
+    const uint32_t ndie = p->channels * p->ways * p->dies;
+    size_t r = 0;
+    for (uint64_t w = 0; w < windows; ++w) {
+        for (uint32_t d = 0; d < ndie; ++d) {
+            if (!refresh[w * ndie + d]) {
+                continue;
+            }
+            const uint32_t q = d / p->dies, dd = d % p->dies;
+            const uint64_t k = ordinal[d]++;
+            const uint32_t coord[4] = {q / p->ways, q % p->ways, dd,
+                                       (uint32_t)(k % p->planes)};
+            uint64_t page = ((k / p->planes) % rows) * stride;
+            for (int ax = 0; ax < 4; ++ax) {
+                page += coord[ax] * div[ax];
+            }
+            out[r].addr = page;
+            out[r].bytes = 2ULL << p->page_shift;
+            out[r].issue_ps = orc_defer(level, windows, window_ps, w * window_ps, 3);
+            out[r].flags = ORC_OP_REFRESH | ORC_FLAG_MEDIA;
+            ++r;
+        }
+    }
+    return r;
+}
+
+void orc_merge_records(const orc_record* demand, const uint64_t* admit,
+                       size_t n, const orc_record* extra, size_t r,
+                       orc_record* out, uint64_t* demand_pos)
+{
+    size_t i = 0, j = 0, k = 0;
+    while (i < n || j < r) {
+        if (j < r && (i == n || extra[j].issue_ps <= admit[i])) {
+            out[k++] = extra[j++];
+        } else {
+            out[k] = demand[i];
+            out[k].issue_ps = admit[i];
+            demand_pos[i++] = k++;
+        }
+    }
+}
+
+int orc_window_counts(const orc_engine_params* p, const orc_range* ranges,
+                      uint32_t range_count, const orc_record* rec, size_t n,
+                      uint64_t window_ps, uint64_t windows, uint32_t* counts)
+{
+    if (!engine_params_ok(p) || window_ps == 0) {
+        return 1;
+    }
+    for (size_t i = 0; i < n; ++i) {
+        decoded d;
+        decode(p, ranges, range_count, &rec[i], 0, &d);
+        const uint64_t w = rec[i].issue_ps / window_ps;
+        if (d.cls != ORC_MODELED || w >= windows) {
+            continue;
+        }
+        counts[w * (p->channels * p->ways * p->dies) + d.plane / p->planes] += 1;
+    }
+    return 0;
+}
+
+int orc_coupled_run(const orc_engine_params* p, const orc_range* ranges,
+                    uint32_t range_count, const orc_reliability* r,
+                    const orc_record* rec, size_t n, double* temperature,
+                    uint64_t* age, orc_engine_state* s, uint64_t* completion,
+                    orc_coupled_report* rep, double* hot, uint8_t* level,
+                    uint8_t* refresh, uint64_t windows_cap)
+{
+    memset(rep, 0, sizeof(*rep));
+    const uint32_t ndie = p->channels * p->ways * p->dies;
+    if (!reliability_ok(r) || r->regions_x * r->regions_y != p->channels * p->ways ||
+        r->dies != p->dies || p->model != ORC_MODEL_HBF) {
+        return 1;
+    }
+    uint64_t last = 0;
+    for (size_t i = 0; i < n; ++i) {
+        if (rec[i].issue_ps > last) {
+            last = rec[i].issue_ps;
+        }
+    }
+    const uint64_t windows = n ? last / r->window_ps + 1 : 0;
+    rep->windows = windows;
+    if (windows > windows_cap) {
+        return 3;
+    }
+    uint32_t* counts = (uint32_t*)calloc(windows * ndie + 1, sizeof(uint32_t));
+    uint64_t* admit = (uint64_t*)malloc((n + 1) * sizeof(uint64_t));
+    if (!counts || !admit) {
+        free(counts);
+        free(admit);
+        return 2;
+    }
+    int rc = orc_window_counts(p, ranges, range_count, rec, n, r->window_ps, windows, counts);
+    orc_control ctl = {0, ORC_NO_PENDING, 0, 0};
+    if (rc == 0) {
+        rc = orc_reliability_chain(r, counts, windows, temperature, age, &ctl, hot,
+                                   level, refresh);
+    }
+    free(counts);
+    if (rc != 0) {
+        free(admit);
+        return rc;
+    }
+    size_t nref = 0;
+    for (uint64_t k = 0; k < windows * ndie; ++k) {
+        nref += refresh[k];
+    }
+    for (uint64_t w = 0; w < windows; ++w) {
+        rep->level_windows[level[w]] += 1;
+    }
+    for (uint64_t k = 0; k < (windows + 1) * ndie; ++k) {
+        if (hot[k] > rep->peak_k) {
+            rep->peak_k = hot[k];
+        }
+    }
+    orc_admit(level, windows, r->window_ps, r->light_gap_ps, rec, n, admit);
+    orc_record* extra = (orc_record*)malloc((nref + 1) * sizeof(orc_record));
+    uint64_t* ordinal = (uint64_t*)calloc(ndie, sizeof(uint64_t));
+    orc_record* merged = (orc_record*)malloc((n + nref + 1) * sizeof(orc_record));
+    uint64_t* pos = (uint64_t*)malloc((n + 1) * sizeof(uint64_t));
+    uint64_t* mcomp = (uint64_t*)malloc((n + nref + 1) * sizeof(uint64_t));
+    uint8_t* mstat = (uint8_t*)malloc(n + nref + 1);
+    if (!extra || !ordinal || !merged || !pos || !mcomp || !mstat) {
+        rc = 2;
+    } else {
+        const size_t got = orc_refresh_records(p, refresh, level, windows, r->window_ps,
+                                               ordinal, extra);
+        (void)got;
+        orc_merge_records(rec, admit, n, extra, nref, merged, pos);
+        orc_engine_report er;
+        memset(&er, 0, sizeof(er));
+        rc = orc_engine_run(p, ranges, range_count, merged, n + nref, 0, s, mcomp, mstat,
+                            &er);
+        rep->refreshes = nref;
+        rep->makespan_ps = er.makespan_ps;
+        for (size_t i = 0; rc == 0 && i < n; ++i) {
+            const uint64_t c = mcomp[pos[i]];
+            completion[i] = c;
+            if (admit[i] > rec[i].issue_ps) {
+                rep->deferred += 1;
+            }
+            if ((mstat[pos[i]] & 3u) == ORC_MODELED) {
+                const uint64_t lat = c - rec[i].issue_ps;
+                const uint64_t lo = rep->latency_sum_lo + lat;
+                rep->latency_sum_hi += lo < rep->latency_sum_lo;
+                rep->latency_sum_lo = lo;
+                if (lat > rep->latency_max_ps) {
+                    rep->latency_max_ps = lat;
+                }
+                rep->demand_modeled += 1;
+            }
+        }
+    }
+    free(admit);
+    free(extra);
+    free(ordinal);
+    free(merged);
+    free(pos);
+    free(mcomp);
+    free(mstat);
+    return rc;
 }

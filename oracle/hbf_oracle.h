@@ -99,6 +99,11 @@ enum orc_status {
     ORC_BYPASS = 1,      /* outside every range: native address, no delay */
     ORC_UNSUPPORTED = 2  /* straddles a range, crosses a page, no permission */
 };
+/* Record operations beyond read (0) and write (1): a refresh of media page
+ * `addr` (read out and programmed back; plane tR + tPROG, channel `bytes`),
+ * valid only with the media flag.  Injected by the reliability model. */
+#define ORC_OP_REFRESH 2u
+#define ORC_FLAG_MEDIA 0x100u
 uint32_t orc_classify(const orc_range* ranges, uint32_t count,
                       uint64_t address, uint64_t bytes, uint32_t operation,
                       uint32_t* range_index);
@@ -187,6 +192,7 @@ typedef struct orc_engine_params {
     uint64_t xfer_num, xfer_den;             /* xfer_ps =                  */
     uint64_t xfer_quantum;                   /*   q * ceil(b*num/den)      */
     orc_empirical empirical;                 /* MODEL_FAST_EMPIRICAL only */
+    uint64_t media_pages;                    /* device pages; 0 = no limit */
 } orc_engine_params;
 
 typedef struct orc_engine_state {
@@ -286,6 +292,100 @@ int orc_thermal_grid_step(uint32_t nx, uint32_t ny, uint32_t nz,
                           const double* power, double* temperature,
                           double tol, int max_sweeps);
 double orc_arrhenius(double temperature_k, double ea_ev, double tref_k);
+
+/* ---- thermal-coupled reliability ------------------------------------ */
+/* The EQ3 grid of orc_thermal_grid_step stepped once per window of
+ * `window_ps` with a fixed number of Jacobi sweeps; power per cell from the
+ * per-die access counts of the window (observer.cpp:42-72's energy per
+ * window); per-die equivalent age advanced with the Arrhenius factor of the
+ * die's hotspot (reliability.py:17-23, 93-108) through an integer lookup
+ * table; refresh due when the age reaches the retention period
+ * (cpu_service.cpp:169-217, the fixed period replaced by the derated one);
+ * throttle level from the stack hotspot with hysteresis
+ * (cpu_service.cpp:221-255).  Dies sit on the grid as follows: channel-way
+ * q = c*W + w covers the x-y block (q % regions_x, q / regions_x); die d of
+ * it covers layers [d*nz/D, (d+1)*nz/D). */
+typedef struct orc_reliability {
+    uint32_t nx, ny, nz, sweeps;
+    double capacity, gx, gy, gz, gb, ambient_k, dt_s;
+    uint64_t window_ps;
+    uint32_t regions_x, regions_y, dies, policy; /* policy 1: hysteresis */
+    double static_w;              /* W per cell */
+    double access_energy_j, refresh_energy_j;
+    double activation_ev, reference_k;
+    uint64_t retention_ps;        /* refresh period at reference_k */
+    double light_k, severe_k, shutdown_k, hysteresis_k;
+    uint64_t action_delay_ps, min_dwell_ps, light_gap_ps;
+} orc_reliability;
+
+#define ORC_NO_PENDING 4u
+typedef struct orc_control {
+    uint32_t applied;  /* 0 none, 1 light, 2 severe, 3 shutdown */
+    uint32_t pending;  /* ORC_NO_PENDING or the level waiting to apply */
+    uint64_t pending_at_ps, last_change_ps;
+} orc_control;
+
+typedef struct orc_coupled_report {
+    uint64_t windows, refreshes, deferred;
+    uint64_t level_windows[4];
+    uint64_t demand_modeled;
+    uint64_t latency_sum_lo, latency_sum_hi, latency_max_ps;
+    uint64_t makespan_ps;
+    double peak_k;
+} orc_coupled_report;
+
+/* Retention lookup: table[b] = llround(window_ps * AF(T_b)), T_b = T0 +
+ * (b + 1/2) / 16 K; bin(T) = floor((T - T0) * 16) clamped. */
+#define ORC_AF_BINS 4096u
+#define ORC_AF_T0 200.0
+#define ORC_AF_STEPS_PER_K 16.0
+void orc_retention_table(double ea_ev, double tref_k, uint64_t window_ps,
+                         uint64_t* table);
+uint32_t orc_retention_bin(double t);
+/* One control sample at `now` with stack hotspot hs (cpu_service.cpp:
+ * 221-255: control_sample, then apply_controls); returns the applied level. */
+uint32_t orc_control_step(const orc_reliability* r, orc_control* c,
+                          uint64_t now, double hs);
+/* counts [windows][dies]; hot [(windows+1)][dies] (row 0 = initial);
+ * level [windows]; refresh [windows][dies].  temperature, age and ctl are
+ * updated in place. */
+int orc_reliability_chain(const orc_reliability* r, const uint32_t* counts,
+                          uint64_t windows, double* temperature, uint64_t* age,
+                          orc_control* ctl, double* hot, uint8_t* level,
+                          uint8_t* refresh);
+/* First time >= t whose window's level is below `limit` (t itself when
+ * its window allows; window starts otherwise). */
+uint64_t orc_defer(const uint8_t* level, uint64_t windows, uint64_t window_ps,
+                   uint64_t t, uint32_t limit);
+/* Admission (cpu_service.cpp:256-285 for record streams): severe and
+ * shutdown windows defer a request to the next window that admits demand;
+ * light windows space admissions by light_gap_ps. */
+void orc_admit(const uint8_t* level, uint64_t windows, uint64_t window_ps,
+               uint64_t light_gap_ps, const orc_record* rec, size_t n,
+               uint64_t* admit);
+/* Refresh records (op 2, media flag) in (window, die) order; ordinal[die]
+ * counts each die's refreshes and picks plane k % P and row k / P. */
+size_t orc_refresh_records(const orc_engine_params* p, const uint8_t* refresh,
+                           const uint8_t* level, uint64_t windows,
+                           uint64_t window_ps, uint64_t* ordinal,
+                           orc_record* out);
+/* Merge by admission time, refresh records first on ties. */
+void orc_merge_records(const orc_record* demand, const uint64_t* admit,
+                       size_t n, const orc_record* extra, size_t r,
+                       orc_record* out, uint64_t* demand_pos);
+/* Modeled accesses per (window of issue_ps, die). */
+int orc_window_counts(const orc_engine_params* p, const orc_range* ranges,
+                      uint32_t range_count, const orc_record* rec, size_t n,
+                      uint64_t window_ps, uint64_t windows, uint32_t* counts);
+/* The whole coupled run: counts -> chain -> admission -> refresh records ->
+ * merge -> engine; completion[n] of the demand records.  hot, level and
+ * refresh are sized for windows_cap windows. */
+int orc_coupled_run(const orc_engine_params* p, const orc_range* ranges,
+                    uint32_t range_count, const orc_reliability* r,
+                    const orc_record* rec, size_t n, double* temperature,
+                    uint64_t* age, orc_engine_state* s, uint64_t* completion,
+                    orc_coupled_report* rep, double* hot, uint8_t* level,
+                    uint8_t* refresh, uint64_t windows_cap);
 
 #ifdef __cplusplus
 }

@@ -46,7 +46,7 @@ class OrcParams(ctypes.Structure):
                 ("program_every_write", _U32), ("hybrid", _U32), ("hybrid_warmup", _U32),
                 ("hybrid_threshold", _U64), ("read_ps", _U64), ("program_ps", _U64),
                 ("xfer_num", _U64), ("xfer_den", _U64), ("xfer_quantum", _U64),
-                ("empirical", OrcEmpirical)]
+                ("empirical", OrcEmpirical), ("media_pages", _U64)]
 
 
 class OrcState(ctypes.Structure):
@@ -73,6 +73,46 @@ class OrcTraceEvent(ctypes.Structure):
     _fields_ = [("logical_address", _U64), ("bytes", _U64), ("page_bytes", _U32),
                 ("operation", _U32)]
 
+
+_D = ctypes.c_double
+
+
+class OrcReliability(ctypes.Structure):
+    _fields_ = [("nx", _U32), ("ny", _U32), ("nz", _U32), ("sweeps", _U32), ("capacity", _D),
+                ("gx", _D), ("gy", _D), ("gz", _D), ("gb", _D), ("ambient_k", _D), ("dt_s", _D),
+                ("window_ps", _U64), ("regions_x", _U32), ("regions_y", _U32), ("dies", _U32),
+                ("policy", _U32), ("static_w", _D), ("access_energy_j", _D),
+                ("refresh_energy_j", _D), ("activation_ev", _D), ("reference_k", _D),
+                ("retention_ps", _U64), ("light_k", _D), ("severe_k", _D), ("shutdown_k", _D),
+                ("hysteresis_k", _D), ("action_delay_ps", _U64), ("min_dwell_ps", _U64),
+                ("light_gap_ps", _U64)]
+
+
+class OrcControl(ctypes.Structure):
+    _fields_ = [("applied", _U32), ("pending", _U32), ("pending_at_ps", _U64),
+                ("last_change_ps", _U64)]
+
+
+NO_PENDING = 4
+
+
+class OrcCoupledReport(ctypes.Structure):
+    _fields_ = [("windows", _U64), ("refreshes", _U64), ("deferred", _U64),
+                ("level_windows", _U64 * 4), ("demand_modeled", _U64), ("latency_sum_lo", _U64),
+                ("latency_sum_hi", _U64), ("latency_max_ps", _U64), ("makespan_ps", _U64),
+                ("peak_k", _D)]
+
+    def as_dict(self) -> dict:
+        d = {}
+        for name, _ in self._fields_:
+            v = getattr(self, name)
+            d[name] = [int(x) for x in v] if name == "level_windows" else (
+                float(v) if name == "peak_k" else int(v))
+        d["latency_sum_ps"] = d["latency_sum_lo"] | (d["latency_sum_hi"] << 64)
+        return d
+
+
+AF_BINS = 4096
 
 _lib = None
 
@@ -137,6 +177,18 @@ def lib() -> ctypes.CDLL:
                                                      ctypes.c_double, ctypes.c_int]),
             "orc_arrhenius": (ctypes.c_double, [ctypes.c_double, ctypes.c_double,
                                                 ctypes.c_double]),
+            "orc_retention_table": (None, [_D, _D, _U64, _P]),
+            "orc_retention_bin": (_U32, [_D]),
+            "orc_control_step": (_U32, [_P, _P, _U64, _D]),
+            "orc_reliability_chain": (ctypes.c_int, [_P, _P, _U64, _P, _P, _P, _P, _P, _P]),
+            "orc_defer": (_U64, [_P, _U64, _U64, _U64, _U32]),
+            "orc_admit": (None, [_P, _U64, _U64, _U64, _P, ctypes.c_size_t, _P]),
+            "orc_refresh_records": (ctypes.c_size_t, [_P, _P, _P, _U64, _U64, _P, _P]),
+            "orc_merge_records": (None, [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, _P]),
+            "orc_window_counts": (ctypes.c_int, [_P, _P, _U32, _P, ctypes.c_size_t, _U64, _U64,
+                                                 _P]),
+            "orc_coupled_run": (ctypes.c_int, [_P, _P, _U32, _P, _P, ctypes.c_size_t, _P, _P, _P,
+                                               _P, _P, _P, _P, _P, _U64]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -198,6 +250,7 @@ def engine_params(profile: dict, page_buffers=1, plane_contention=1, transfer_pa
         num, den = 10**12 * p.channels, profile["aggregate_bandwidth_bytes_per_s"] * q
     g = math.gcd(num, den)
     p.xfer_num, p.xfer_den, p.xfer_quantum = num // g, den // g, q
+    p.media_pages = profile["capacity_bytes"] // profile["page_bytes"]
     if "empirical_vmem" in profile:
         e = profile["empirical_vmem"]
         p.empirical.flags = 1
@@ -264,3 +317,62 @@ def run(params: OrcParams, ranges, count: int, records: np.ndarray, base_ps: int
     if rc != 0:
         raise RuntimeError(f"oracle engine failed: {rc}")
     return comp, st, rep.as_dict(), state
+
+
+# ---------------------------------------------------------------------------
+# thermal-coupled reliability
+
+
+def reliability(grid: dict, options: dict, dies: int) -> OrcReliability:
+    """orc_reliability from the keyword sets the product API takes (grid:
+    nx, ny, nz, sweeps, capacity_j_per_k, g*_w_per_k, top_g_w_per_k,
+    ambient_k, dt_s; options: the hbfsim_amd_reliability_options fields)."""
+    r = OrcReliability()
+    r.nx, r.ny, r.nz = grid["nx"], grid["ny"], grid["nz"]
+    r.sweeps = grid.get("sweeps", 4)
+    r.capacity = grid["capacity_j_per_k"]
+    r.gx, r.gy, r.gz = grid["gx_w_per_k"], grid["gy_w_per_k"], grid["gz_w_per_k"]
+    r.gb, r.ambient_k, r.dt_s = grid["top_g_w_per_k"], grid["ambient_k"], grid["dt_s"]
+    r.window_ps = options["window_ps"]
+    r.regions_x, r.regions_y, r.dies = options["regions_x"], options["regions_y"], dies
+    r.policy = options.get("policy", 1)
+    r.static_w = options.get("static_power_w", 0.0)
+    r.access_energy_j = options.get("access_energy_j", 0.0)
+    r.refresh_energy_j = options.get("refresh_energy_j", 0.0)
+    r.activation_ev = options.get("activation_energy_ev", 0.0)
+    r.reference_k = options.get("reference_k", 358.15)
+    r.retention_ps = options.get("retention_ps", 0)
+    r.light_k, r.severe_k = options.get("light_k", 0.0), options.get("severe_k", 0.0)
+    r.shutdown_k, r.hysteresis_k = options.get("shutdown_k", 0.0), options.get("hysteresis_k", 0.0)
+    r.action_delay_ps = options.get("action_delay_ps", 0)
+    r.min_dwell_ps = options.get("min_dwell_ps", 0)
+    r.light_gap_ps = options.get("light_gap_ps", 0)
+    return r
+
+
+def coupled_run(params: OrcParams, ranges, count: int, rel: OrcReliability,
+                records: np.ndarray, temperature: np.ndarray, age: np.ndarray,
+                state: OracleState | None = None):
+    """orc_coupled_run; temperature and age are updated in place.  Returns
+    (completion, report, trace dict, state)."""
+    rec = np.ascontiguousarray(records, dtype=np.uint64).reshape(-1, 4)
+    n = rec.shape[0]
+    if state is None:
+        state = OracleState(params)
+    windows = int(rec[:, 2].max()) // rel.window_ps + 1 if n else 0
+    dies = params.channels * params.ways * params.dies
+    comp = np.zeros(max(n, 1), np.uint64)
+    hot = np.zeros((windows + 1) * dies, np.float64)
+    level = np.zeros(max(windows, 1), np.uint8)
+    refresh = np.zeros(max(windows * dies, 1), np.uint8)
+    rep = OrcCoupledReport()
+    assert temperature.dtype == np.float64 and age.dtype == np.uint64
+    rc = lib().orc_coupled_run(ctypes.byref(params), ranges, count, ctypes.byref(rel), addr(rec),
+                               n, addr(temperature), addr(age), ctypes.byref(state.s),
+                               addr(comp), ctypes.byref(rep), addr(hot), addr(level),
+                               addr(refresh), windows)
+    if rc != 0:
+        raise RuntimeError(f"oracle coupled run failed: {rc}")
+    trace = {"windows": windows, "dies": dies, "hot": hot.reshape(windows + 1, dies),
+             "level": level[:windows], "refresh": refresh[: windows * dies].reshape(windows, dies)}
+    return comp[:n], rep.as_dict(), trace, state
