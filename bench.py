@@ -1,6 +1,6 @@
 """Benchmark of the HBF access-timing engine on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c0]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c0|c4|thermal]
 
 A step is one pass of the timing engine over one batch of access records
 resident in HBM (one decode step of the workload); engine state carries from
@@ -105,6 +105,172 @@ def cpu_baseline(profile, ranges, host_records: np.ndarray, budget_s: float) -> 
                       f"single-threaded oracle ({dt:.1f} s)"}
 
 
+def bench_c4(args) -> dict:
+    """Config 4: the OLMoE trace (1e8 accesses) through the thermal-coupled
+    run.  A step is one whole coupled run from the initial state: access
+    counts, the 64x64x8 grid stepped every simulated microsecond with
+    refresh and throttle decisions, admission, refresh merge, engine."""
+    import torch
+    from hbfsim_amd import engine, workloads as w
+
+    shape = w.OLMOE
+    seg = w.c4_segments(shape, 2)
+    rec = w.gpu_segment_records(seg, shape.lines_per_expert, shape.line, shape.gap_ps,
+                                shape.issuers)[: w.C4_ACCESSES]
+    ranges = w.moe_ranges(shape)
+    e = engine.Engine(str(w.PROFILES / "c4.json"))
+    for base, length, perms in ranges:
+        e.register(base, length, perms)
+    th = engine.Thermal(**w.C4_GRID)
+    cells = th.cells
+    comp = torch.empty(rec.shape[0], dtype=torch.int64, device="cuda")
+    temp = torch.empty(cells, dtype=torch.float64, device="cuda")
+    age0 = w.staggered_ages(64, w.C4_RELIABILITY["retention_ps"])
+    stream = torch.cuda.current_stream()
+
+    def step():
+        e.reset()
+        temp.fill_(w.C4_GRID["ambient_k"])
+        age = age0.copy()
+        return e.run_coupled(th, w.C4_RELIABILITY, rec, comp, temp, age, stream)
+
+    log(f"c4: {rec.shape[0]} records, warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    phases = {}
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        rep, erep = step()
+        for k, v in th.coupled_ms().items():
+            phases[k] = phases.get(k, 0.0) + v / args.steps
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    windows = rep["windows"]
+    per_window_ms = phases["thermal_chain"] / max(1, windows)
+    cell_sweeps = cells * w.C4_GRID["sweeps"]
+    thermal_gbps = 16 * cell_sweeps / (per_window_ms / 1e3) / 1e9
+    n = int(rec.shape[0])
+    engine_gbps = ALGO_BYTES_PER_ACCESS * (n + rep["refreshes"]) / (phases["engine"] / 1e3) / 1e9
+    dominant = max(("thermal_chain", "engine"), key=lambda k: phases[k])
+    roof = ({"bound": "hbm", "kernel": "k_thermal_window", "achieved": thermal_gbps,
+             "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": thermal_gbps / PEAK_HBM_GBPS,
+             "traffic": None, "algorithmic": "16 B per cell-sweep, 32768 cells x 4 sweeps "
+                                             "per launch (one launch per window)",
+             "kernel_ms": per_window_ms}
+            if dominant == "thermal_chain" else
+            {"bound": "hbm", "kernel": "engine (k_summary + k_carry + k_apply)",
+             "achieved": engine_gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+             "frac": engine_gbps / PEAK_HBM_GBPS, "traffic": None})
+    roof["phases_ms"] = phases
+    out = {
+        "metric": "modeled HBF accesses/sec on 1 MI355X", "value": n * args.steps / dt,
+        "unit": "accesses/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": dt / args.steps * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u64+f64", "data": "synthetic",
+        "config": {"workload": "config4: OLMoE-shaped decode trace (16 layers x 64 experts, "
+                               "top-8 of 32 tokens, Zipf(1.1) seed 3) truncated at 1e8 "
+                               "accesses, thermal-coupled: 64x64x8 EQ3 grid stepped every "
+                               "1 us, Arrhenius-derated refresh, hysteresis throttling",
+                   "records_per_step": n, "profile": "c4.json (8 ch x 8 die x 2 plane)",
+                   "windows": windows, "refreshes": rep["refreshes"],
+                   "level_windows": rep["level_windows"], "deferred": rep["deferred"],
+                   "peak_k": rep["peak_k"], "makespan_ps": rep["makespan_ps"]},
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        log("cpu baseline (coupled oracle)")
+        out["cpu_baseline"] = cpu_baseline_c4(rec, ranges, args.cpu_seconds)
+    th.close()
+    e.close()
+    return out
+
+
+def cpu_baseline_c4(rec, ranges, budget_s: float) -> dict:
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_py
+    from hbfsim_amd import workloads as w
+
+    prof = oracle_py.load_profile(w.PROFILES / "c4.json")
+    params = oracle_py.engine_params(prof)
+    orng, count = oracle_py.range_table(ranges, prof["page_bytes"], prof["capacity_bytes"])
+    rel = oracle_py.reliability(w.C4_GRID, w.C4_RELIABILITY, params.dies)
+    sample = rec[: 1_000_000].cpu().numpy().view(np.uint64)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        temp = np.full(64 * 64 * 8, w.C4_GRID["ambient_k"])
+        age = w.staggered_ages(64, w.C4_RELIABILITY["retention_ps"])
+        oracle_py.coupled_run(params, orng, count, rel, sample, temp, age)
+        done += len(sample)
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": done / dt, "unit": "accesses/s", "cores": 1, "kind": "port",
+            "sample": f"the first {len(sample)} records of the config-4 trace (250 windows of "
+                      f"the 64x64x8 grid), coupled run from the initial state, repeated "
+                      f"{done // len(sample)}x, single-threaded oracle ({dt:.1f} s)"}
+
+
+def bench_thermal(args) -> dict:
+    """The EQ3 stencil alone on a large grid (2048 x 2048 x 8 cells, 4 sweeps
+    per step, constant power): cell-sweeps per second."""
+    import torch
+    from hbfsim_amd import engine, workloads as w
+
+    g = dict(w.C4_GRID, nx=2048, ny=2048)
+    th = engine.Thermal(**g)
+    cells = th.cells
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    power = torch.rand(cells, dtype=torch.float64, device="cuda", generator=gen) * 0.01
+    temp = torch.full((cells,), g["ambient_k"], dtype=torch.float64, device="cuda")
+    steps_per_call = 10
+    th.step(power, temp, steps_per_call * max(1, args.warmup))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    kms = 0.0
+    for _ in range(args.steps):
+        th.step(power, temp, steps_per_call)
+        kms += th.last_ms() / args.steps
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    sweeps = cells * g["sweeps"]
+    value = sweeps * steps_per_call * args.steps / dt
+    achieved = 16 * sweeps / (kms / 1e3) / 1e9
+    out = {
+        "metric": "EQ3 thermal grid cell-sweeps/sec on 1 MI355X", "value": value,
+        "unit": "cell-sweeps/s", "n_gpus": 1, "steps": args.steps * steps_per_call,
+        "warmup": args.warmup * steps_per_call, "ms_per_step": dt / args.steps / steps_per_call * 1e3,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": "EQ3 grid 2048 x 2048 x 8 cells, 4 Jacobi sweeps per backward-"
+                               "Euler step, config-4 conductances, random power"},
+        "roofline": {"bound": "hbm", "kernel": "k_thermal_window", "achieved": achieved,
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBPS,
+                     "traffic": None, "kernel_ms": kms,
+                     "algorithmic": "16 B per cell-sweep (8 B read + 8 B write)"},
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "tests"))
+        import oracle_py
+        L = oracle_py.lib()
+        nx, ny, nz = 256, 256, 8
+        p = np.random.default_rng(7).uniform(0, 0.01, nx * ny * nz)
+        t = np.full(nx * ny * nz, g["ambient_k"])
+        done, c0 = 0, time.perf_counter()
+        while time.perf_counter() - c0 < args.cpu_seconds:
+            L.orc_thermal_grid_step(nx, ny, nz, g["capacity_j_per_k"], g["gx_w_per_k"],
+                                    g["gy_w_per_k"], g["gz_w_per_k"], g["top_g_w_per_k"],
+                                    g["ambient_k"], g["dt_s"], p.ctypes.data, t.ctypes.data,
+                                    -1.0, 4)
+            done += nx * ny * nz * 4
+        out["cpu_baseline"] = {"value": done / (time.perf_counter() - c0),
+                               "unit": "cell-sweeps/s", "cores": 1, "kind": "port",
+                               "sample": "256 x 256 x 8 grid, 4 sweeps per step, "
+                                         "single-threaded oracle"}
+    th.close()
+    return out
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -113,6 +279,11 @@ def main() -> None:
         sys.exit(2)
     import torch
     from hbfsim_amd import engine
+
+    if args.config in ("c4", "thermal"):
+        out = bench_c4(args) if args.config == "c4" else bench_thermal(args)
+        print(json.dumps(out), flush=True)
+        return
 
     profile, ranges, batches, desc, host_records = build_workload(args.config, args.steps,
                                                                   args.batches)

@@ -199,6 +199,7 @@ SIGNATURES = {
     "hbfsim_amd_run_coupled": (_INT, [_P, _P, ctypes.POINTER(ReliabilityOptions), _P, _SZ, _P,
                                       _P, _P, _P, ctypes.POINTER(CoupledReport),
                                       ctypes.POINTER(Report)]),
+    "hbfsim_amd_coupled_last_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float), _INT]),
     "hbfsim_amd_coupled_trace": (_INT, [_P, _P, _SZ, _P, _SZ, _P, _SZ, ctypes.POINTER(_U64),
                                         ctypes.POINTER(_U32)]),
     "hbfsim_amd_validate_profile": (_INT, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),

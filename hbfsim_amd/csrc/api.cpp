@@ -737,6 +737,14 @@ HBF_API int hbfsim_amd_run_coupled(hbfsim_context* c, hbfsim_amd_thermal* t,
     }
 }
 
+HBF_API int hbfsim_amd_coupled_last_ms(const hbfsim_amd_thermal* t, float* ms, int max_phases)
+{
+    if (t == nullptr || ms == nullptr || max_phases < 0) {
+        return -1;
+    }
+    return hbfamd::coupled_last_ms(t->impl, ms, max_phases);
+}
+
 HBF_API int hbfsim_amd_coupled_trace(const hbfsim_amd_thermal* t, double* hot, size_t hot_count,
                                      uint8_t* level, size_t level_count, uint8_t* refresh,
                                      size_t refresh_count, uint64_t* windows, uint32_t* dies)

@@ -401,7 +401,10 @@ __device__ __forceinline__ std::uint32_t dec_op(std::uint32_t bits)
 }
 
 // Classification in the resolver's order (hbf_device.cu:1081-1165) followed
-// by striping of the media page.
+// by striping of the media page.  Refresh records are recognised only in
+// the kRefresh instantiation (streams the thermal-coupled run merged them
+// into); the other streams keep the branch out of the hot loop.
+template <bool kRefresh>
 __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence, RangeCache& rc,
                                       const uint4& x, const uint4& y, std::uint64_t base_ps)
 {
@@ -418,7 +421,7 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
     d.page1 = 0;
     d.xfer = 0;
     d.xbytes = 0;
-    if (op == kOpRefresh && (y.z & kMediaFlag) != 0) {
+    if (kRefresh && op == kOpRefresh && (y.z & kMediaFlag) != 0) {
         if (bytes == 0 || bytes > 0xffffffffull || addr >= a.media_pages) {
             d.cls = kClsUnsupported;
             return d;
@@ -478,7 +481,25 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
         d.bits |= 2u;
     }
     d.xbytes = a.transfer_page ? page_bytes : bytes;
-    stripe(a, page, d);
+    // (striping written out here rather than through stripe(): the helper
+    // costs the summary kernel a quarter of its speed)
+    if (!a.flat) {
+        std::uint32_t c[4];
+        if (a.pow2) {
+#pragma unroll
+            for (int ax = 0; ax < 4; ++ax) {
+                c[ax] = static_cast<std::uint32_t>((page >> a.axis_shift[ax]) &
+                                                   (a.axis_size[ax] - 1));
+            }
+        } else {
+#pragma unroll
+            for (int ax = 0; ax < 4; ++ax) {
+                c[ax] = static_cast<std::uint32_t>((page / a.axis_div[ax]) % a.axis_size[ax]);
+            }
+        }
+        d.chan = c[0];
+        d.plane = ((c[0] * a.W + c[1]) * a.D + c[2]) * a.P + c[3];
+    }
     return d;
 }
 
@@ -656,6 +677,7 @@ __device__ __forceinline__ void load_fences(const KArgs& a, std::uint64_t* fence
 // class), the (max,+) map of the records after it, and the last page; per
 // channel the map of all its records.  Pages are stored as page + 1 in 32
 // bits (capacity / page_bytes < 2^32 is checked on the host).
+template <bool kRefresh>
 __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
                                                 ChanSum* csum, std::uint64_t* tile_count)
@@ -700,7 +722,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
         if (s + 2 * kWave + lane < end) load_record(rec, s + 2 * kWave + lane, x1, y1);
         const std::size_t i = s + lane;
         const bool valid = i < end;
-        const Dec d = valid ? decode(a, fence, rc, x, y, base_ps) : invalid_dec();
+        const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
         const bool m = valid && d.cls == kClsModeled;
         const std::uint64_t active = __ballot(m);
         modeled += __popcll(active);
@@ -1028,6 +1050,7 @@ __device__ __forceinline__ std::uint64_t wave_max(std::uint64_t v)
     return v;
 }
 
+template <bool kRefresh>
 __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, std::size_t n,
                                               std::uint64_t base_ps, const PlaneCarry* pcarry,
                                               const std::uint64_t* ccarry,
@@ -1069,7 +1092,7 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
         if (s + 2 * kWave + lane < end) load_record(rec, s + 2 * kWave + lane, x1, y1);
         const std::size_t i = s + lane;
         const bool valid = i < end;
-        const Dec d = valid ? decode(a, fence, rc, x, y, base_ps) : invalid_dec();
+        const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
         const bool m = valid && d.cls == kClsModeled;
         const std::uint64_t active = __ballot(m);
         std::uint8_t st = static_cast<std::uint8_t>(d.cls);
@@ -1520,7 +1543,7 @@ __global__ __launch_bounds__(256) void k_window_counts(KArgs a, const hbf_record
     for (std::size_t i = begin + tid; i < end; i += blockDim.x) {
         uint4 x, y;
         load_record(rec, i, x, y);
-        const Dec d = decode(a, fence, rc, x, y, 0);
+        const Dec d = decode<false>(a, fence, rc, x, y, 0);
         if (d.cls != kClsModeled) {
             continue;
         }
@@ -1725,7 +1748,7 @@ int engine_synchronize(engine* e)
 
 int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_t* d_comp,
                std::uint8_t* d_status, std::uint64_t base_ps, void* stream_ptr,
-               hbfsim_amd_report* out)
+               hbfsim_amd_report* out, bool refresh_records)
 {
     if (out != nullptr) {
         std::memset(out, 0, sizeof(*out));
@@ -1769,8 +1792,13 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
     const dim3 grid(static_cast<unsigned>(ntiles));
     const unsigned carry_blocks = (a.Rp + a.Rc + 1 + kWave - 1) / kWave;
     (void)hipEventRecord(e->ev[0], stream);
-    hipLaunchKernelGGL(k_summary, grid, dim3(kWave), lds_a, stream, a, d_rec, n, base_ps,
-                       e->d_psum, e->d_csum, e->d_tcount);
+    if (refresh_records) {
+        hipLaunchKernelGGL(k_summary<true>, grid, dim3(kWave), lds_a, stream, a, d_rec, n,
+                           base_ps, e->d_psum, e->d_csum, e->d_tcount);
+    } else {
+        hipLaunchKernelGGL(k_summary<false>, grid, dim3(kWave), lds_a, stream, a, d_rec, n,
+                           base_ps, e->d_psum, e->d_csum, e->d_tcount);
+    }
     (void)hipEventRecord(e->ev[1], stream);
     {
         const std::size_t ngroups = (ntiles + kGroup - 1) / kGroup;
@@ -1788,8 +1816,13 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
                            e->d_gseq, e->d_pcarry, e->d_ccarry, e->d_tseq);
     }
     (void)hipEventRecord(e->ev[2], stream);
-    hipLaunchKernelGGL(k_apply, grid, dim3(kWave), lds_c, stream, a, d_rec, n, base_ps,
-                       e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status, e->d_tile_rep);
+    if (refresh_records) {
+        hipLaunchKernelGGL(k_apply<true>, grid, dim3(kWave), lds_c, stream, a, d_rec, n, base_ps,
+                           e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status, e->d_tile_rep);
+    } else {
+        hipLaunchKernelGGL(k_apply<false>, grid, dim3(kWave), lds_c, stream, a, d_rec, n, base_ps,
+                           e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status, e->d_tile_rep);
+    }
     hipLaunchKernelGGL(k_report, dim3(1), dim3(256), 0, stream, e->d_tile_rep, ntiles, e->d_rep);
     (void)hipEventRecord(e->ev[3], stream);
     err = hipGetLastError();

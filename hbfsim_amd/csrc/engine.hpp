@@ -59,9 +59,12 @@ int engine_create(const engine_config& config, engine** out);
 void engine_destroy(engine* e);
 const engine_config& engine_get_config(const engine* e);
 int engine_set_ranges(engine* e, const std::vector<range_rec>& ranges);
+// refresh_records: the stream may hold refresh records (op 2 with the media
+// flag); without it they are classified like any other operation > 1.
 int engine_run(engine* e, const hbf_record32* d_records, std::size_t n,
                std::uint64_t* d_completion, std::uint8_t* d_status,
-               std::uint64_t base_ps, void* stream, hbfsim_amd_report* out);
+               std::uint64_t base_ps, void* stream, hbfsim_amd_report* out,
+               bool refresh_records = false);
 int engine_get_busy_totals(engine* e, std::uint64_t* plane_ps, std::size_t planes,
                            std::uint64_t* channel_ps, std::size_t channels);
 int engine_get_state(engine* e, std::uint64_t* plane_busy, std::uint64_t* plane_tags,

@@ -53,23 +53,19 @@ struct TArgs {
     std::uint32_t tx, ty, rx, ry;  // tile interior and staged region
     std::uint32_t tiles_x;
     std::uint32_t cells;           // rx * ry * nz
+    std::uint32_t step_x, step_y, step_z;  // 256 in the region's mixed radix
     double cdt, gx, gy, gz, gb, tb;
     const double* power;           // W per cell (uncoupled steps)
     // coupled mode
     std::uint32_t coupled;
-    std::uint32_t ndie, regions_x, rw, rh, lpd, D, policy;
+    std::uint32_t ndie, regions_x, rw, rh, lpd, D;
     double static_w, pa, pr;
     const std::uint32_t* counts;   // [windows][ndie]
     unsigned long long* hot;       // [(windows + 1)][ndie], bits of doubles
     const std::uint64_t* af;       // retention table
     std::uint64_t retention_ps, window_ps;
-    double light_k, severe_k, shutdown_k, hysteresis_k;
-    std::uint64_t action_delay_ps, min_dwell_ps;
     const std::uint64_t* age_in;
     std::uint64_t* age_out;
-    const Ctl* ctl_in;
-    Ctl* ctl_out;
-    std::uint8_t* level;
     std::uint8_t* refresh;
 };
 
@@ -90,33 +86,6 @@ __device__ __forceinline__ std::uint32_t af_bin(double t)
     return static_cast<std::uint32_t>(f);
 }
 
-// cpu_service.cpp:221-255: control_sample then apply_controls.
-__device__ void control_step(const TArgs& a, Ctl& c, std::uint64_t now, double hs)
-{
-    const double thr[4] = {0.0, a.light_k, a.severe_k, a.shutdown_k};
-    std::uint32_t desired = static_cast<std::uint32_t>(hs >= a.light_k) +
-                            static_cast<std::uint32_t>(hs >= a.severe_k) +
-                            static_cast<std::uint32_t>(hs >= a.shutdown_k);
-    if (desired < c.applied && hs >= thr[c.applied] - a.hysteresis_k) {
-        desired = c.applied;
-    }
-    if (a.policy != 0) {
-        if (desired == c.applied) {
-            c.pending = kNoPending;
-        } else if (c.pending == kNoPending || c.pending != desired) {
-            const std::uint64_t x = sat_add(now, a.action_delay_ps);
-            const std::uint64_t y = sat_add(c.last_change, a.min_dwell_ps);
-            c.pending = desired;
-            c.pending_at = x > y ? x : y;
-        }
-    }
-    if (c.pending != kNoPending && c.pending_at <= now) {
-        c.applied = c.pending;
-        c.last_change = now;
-        c.pending = kNoPending;
-    }
-}
-
 // Neighbour bits of a staged cell: which neighbours exist in the grid
 // (update terms) and which of those are staged in LDS.
 enum : std::uint32_t {
@@ -126,28 +95,121 @@ enum : std::uint32_t {
     kZm = 1u << 9, kZp = 1u << 10, kTop = 1u << 11, kInterior = 1u << 12
 };
 
+template <bool kCoupled, int kCells>
 __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const double* tin,
                                                              double* tout, std::uint64_t w)
 {
+    // LDS: cur[cells + 1] and nxt[cells + 1]; slot `cells` of both holds
+    // 0.0 and stands for every neighbour outside the grid.
     extern __shared__ double lds[];
+    __shared__ std::uint8_t s_ref[kCoupled ? kMaxDies : 1];
+    __shared__ unsigned long long s_hot[kCoupled ? 64 : 1];
+    const std::uint32_t rx = a.rx, ry = a.ry, nz = a.nz, nx = a.nx, ny = a.ny;
+    const std::uint32_t cells = a.cells, plane = rx * ry, sweeps = a.sweeps;
+    const std::uint32_t tx = a.tx, ty = a.ty, h = sweeps;
+    const std::uint32_t zero = cells;
     double* cur = lds;
-    double* nxt = lds + a.cells;
-    __shared__ double red[kThreads];
-    __shared__ std::uint8_t s_ref[kMaxDies];
-    __shared__ unsigned long long s_hot[64];
+    double* nxt = lds + cells + 1;
     const int tid = threadIdx.x;
     const std::uint32_t tile_x = blockIdx.x % a.tiles_x;
     const std::uint32_t tile_y = blockIdx.x / a.tiles_x;
-    const int h = static_cast<int>(a.sweeps);
-    const int x0 = static_cast<int>(tile_x * a.tx) - h;
-    const int y0 = static_cast<int>(tile_y * a.ty) - h;
-    const bool leader = blockIdx.x == 0;
+    const int x0 = static_cast<int>(tile_x * tx) - static_cast<int>(h);
+    const int y0 = static_cast<int>(tile_y * ty) - static_cast<int>(h);
+    const double cdt = a.cdt, gx = a.gx, gy = a.gy, gz = a.gz, gb = a.gb;
+    const double gbtb = gb * a.tb;
 
-    if (a.coupled) {
+    // 1. Owned cells c = tid + 256 k.  Per cell, once: its grid index, die,
+    //    the LDS slots of its six neighbours (`zero` outside the grid; the
+    //    cell itself outside the staged region, which disturbs only cells
+    //    within `sweeps` of the region edge), 1 / den with den summed in the
+    //    CPU restatement's order, and its ambient term.
+    std::uint32_t gidx[kCells], die[kCells], fl[kCells];
+    std::uint32_t nbr[kCells][6];
+    double rden[kCells], topv[kCells];
+    std::uint32_t safe_die = 0;
+    {
+        std::uint32_t xi = static_cast<std::uint32_t>(tid) % rx;
+        std::uint32_t t0 = static_cast<std::uint32_t>(tid) / rx;
+        std::uint32_t yi = t0 % ry;
+        std::uint32_t zi = t0 / ry;
+        // The tile lies inside one channel-way region; its halo reaches at
+        // most one region further (sweeps <= region size, checked on the
+        // host), so a cell's region differs from the tile's by -1, 0 or 1.
+        int qx0 = 0, qy0 = 0, rx0 = 0, ry0 = 0;
+        if (kCoupled) {
+            qx0 = static_cast<int>((tile_x * tx) / a.rw);
+            qy0 = static_cast<int>((tile_y * ty) / a.rh);
+            rx0 = qx0 * static_cast<int>(a.rw);
+            ry0 = qy0 * static_cast<int>(a.rh);
+            safe_die = (static_cast<std::uint32_t>(qy0) * a.regions_x +
+                        static_cast<std::uint32_t>(qx0)) * a.D;
+        }
+#pragma unroll
+        for (int k = 0; k < kCells; ++k) {
+            const std::uint32_t c = tid + k * kThreads;
+            const int gxx = x0 + static_cast<int>(xi);
+            const int gyy = y0 + static_cast<int>(yi);
+            std::uint32_t f = 0, g = 0, d = safe_die;
+            std::uint32_t n0 = zero, n1 = zero, n2 = zero, n3 = zero, n4 = zero, n5 = zero;
+            double den = cdt, top = 0.0;
+            if (c < cells && gxx >= 0 && gxx < static_cast<int>(nx) && gyy >= 0 &&
+                gyy < static_cast<int>(ny)) {
+                g = (zi * ny + static_cast<std::uint32_t>(gyy)) * nx + static_cast<std::uint32_t>(gxx);
+                f = kIn;
+                if (xi >= h && xi < h + tx && yi >= h && yi < h + ty) f |= kInterior;
+                if (gxx > 0) { n0 = xi > 0 ? c - 1 : c; den += gx; }
+                if (gxx + 1 < static_cast<int>(nx)) { n1 = xi + 1 < rx ? c + 1 : c; den += gx; }
+                if (gyy > 0) { n2 = yi > 0 ? c - rx : c; den += gy; }
+                if (gyy + 1 < static_cast<int>(ny)) { n3 = yi + 1 < ry ? c + rx : c; den += gy; }
+                if (zi > 0) { n4 = c - plane; den += gz; }
+                if (zi + 1 < nz) {
+                    n5 = c + plane;
+                    den += gz;
+                } else {
+                    den += gb;
+                    top = gbtb;
+                }
+                if (kCoupled) {
+                    const int qx = qx0 + (gxx < rx0 ? -1 : (gxx >= rx0 + static_cast<int>(a.rw) ? 1 : 0));
+                    const int qy = qy0 + (gyy < ry0 ? -1 : (gyy >= ry0 + static_cast<int>(a.rh) ? 1 : 0));
+                    d = (static_cast<std::uint32_t>(qy) * a.regions_x +
+                         static_cast<std::uint32_t>(qx)) * a.D + zi / a.lpd;
+                }
+            }
+            fl[k] = f;
+            gidx[k] = g;
+            die[k] = d;
+            nbr[k][0] = n0; nbr[k][1] = n1; nbr[k][2] = n2;
+            nbr[k][3] = n3; nbr[k][4] = n4; nbr[k][5] = n5;
+            rden[k] = (f & kIn) ? 1.0 / den : 0.0;
+            topv[k] = top;
+            xi += a.step_x;
+            const std::uint32_t cx = xi >= rx ? 1u : 0u;
+            xi -= cx * rx;
+            yi += a.step_y + cx;
+            const std::uint32_t cy = yi >= ry ? 1u : 0u;
+            yi -= cy * ry;
+            zi += a.step_z + cy;
+        }
+    }
+    // 2. Every independent global load at once (cells outside the grid load
+    //    index 0 and are masked).
+    double v[kCells], pin[kCells];
+    std::uint32_t cnt[kCells];
+#pragma unroll
+    for (int k = 0; k < kCells; ++k) {
+        v[k] = tin[gidx[k]];
+        if (kCoupled) {
+            cnt[k] = a.counts[w * a.ndie + die[k]];
+        } else {
+            pin[k] = a.power[gidx[k]];
+        }
+    }
+    if (kCoupled) {
+        // this window's retention and refresh decisions for every die (all
+        // blocks; block 0 stores them)
         const double* hrow = reinterpret_cast<const double*>(a.hot + w * a.ndie);
-        double m = 0.0;
         for (std::uint32_t d = tid; d < a.ndie; d += kThreads) {
-            m = fmax(m, hrow[d]);
             std::uint64_t age = a.age_in[d];
             if (w > 0) {
                 age = sat_add(age, a.af[af_bin(hrow[d])]);
@@ -157,123 +219,64 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
                 age = 0;
             }
             s_ref[d] = rf;
-            if (leader) {
+            if (blockIdx.x == 0) {
                 a.age_out[d] = age;
                 a.refresh[w * a.ndie + d] = rf;
             }
         }
-        red[tid] = m;
         if (tid < 64) {
             s_hot[tid] = 0;
         }
         __syncthreads();
-        for (int s = kThreads / 2; s > 0; s >>= 1) {
-            if (tid < s) {
-                red[tid] = fmax(red[tid], red[tid + s]);
-            }
-            __syncthreads();
-        }
-        if (leader && tid == 0) {
-            Ctl c = *a.ctl_in;
-            control_step(a, c, w * a.window_ps, red[0]);
-            *a.ctl_out = c;
-            a.level[w] = static_cast<std::uint8_t>(c.applied);
-        }
     }
 
-    // Stage the region; remember each owned cell's neighbour bits and
-    // right-hand side C/dt T + P.
-    double rhs[kCellsPerThread];
-    std::uint32_t nb[kCellsPerThread];
-    const std::uint32_t plane = a.rx * a.ry;
+    // 3. Right-hand sides C/dt T + P and the staged temperatures.
+    double rhs[kCells];
 #pragma unroll
-    for (int k = 0; k < kCellsPerThread; ++k) {
+    for (int k = 0; k < kCells; ++k) {
         const std::uint32_t c = tid + k * kThreads;
-        nb[k] = 0;
-        rhs[k] = 0.0;
-        if (c >= a.cells) {
-            continue;
+        double p;
+        if (kCoupled) {
+            p = (a.static_w + static_cast<double>(cnt[k]) * a.pa) +
+                static_cast<double>(s_ref[die[k]]) * a.pr;
+        } else {
+            p = pin[k];
         }
-        const std::uint32_t rxi = c % a.rx;
-        const std::uint32_t t = c / a.rx;
-        const std::uint32_t ryi = t % a.ry;
-        const std::uint32_t z = t / a.ry;
-        const int gx = x0 + static_cast<int>(rxi);
-        const int gy = y0 + static_cast<int>(ryi);
-        double v = 0.0;
-        if (gx >= 0 && gx < static_cast<int>(a.nx) && gy >= 0 && gy < static_cast<int>(a.ny)) {
-            const std::size_t g = (static_cast<std::size_t>(z) * a.ny + gy) * a.nx + gx;
-            v = tin[g];
-            double p;
-            if (a.coupled) {
-                const std::uint32_t q = (static_cast<std::uint32_t>(gy) / a.rh) * a.regions_x +
-                                        static_cast<std::uint32_t>(gx) / a.rw;
-                const std::uint32_t die = q * a.D + z / a.lpd;
-                const std::uint32_t cnt = a.counts[w * a.ndie + die];
-                p = (a.static_w + static_cast<double>(cnt) * a.pa) +
-                    static_cast<double>(s_ref[die]) * a.pr;
-            } else {
-                p = a.power[g];
-            }
-            rhs[k] = a.cdt * v + p;
-            std::uint32_t b = kIn;
-            if (gx > 0) b |= kXm | (rxi > 0 ? kXmL : 0u);
-            if (gx + 1 < static_cast<int>(a.nx)) b |= kXp | (rxi + 1 < a.rx ? kXpL : 0u);
-            if (gy > 0) b |= kYm | (ryi > 0 ? kYmL : 0u);
-            if (gy + 1 < static_cast<int>(a.ny)) b |= kYp | (ryi + 1 < a.ry ? kYpL : 0u);
-            if (z > 0) b |= kZm;
-            if (z + 1 < a.nz) b |= kZp;
-            if (z + 1 == a.nz) b |= kTop;
-            if (rxi >= static_cast<std::uint32_t>(h) && rxi < h + a.tx &&
-                ryi >= static_cast<std::uint32_t>(h) && ryi < h + a.ty) {
-                b |= kInterior;
-            }
-            nb[k] = b;
+        const bool in = (fl[k] & kIn) != 0;
+        rhs[k] = in ? cdt * v[k] + p : 0.0;
+        if (c < cells) {
+            cur[c] = in ? v[k] : 0.0;
         }
-        cur[c] = v;
+    }
+    if (tid == 0) {
+        cur[zero] = 0.0;
+        nxt[zero] = 0.0;
     }
     __syncthreads();
 
-    const double gbtb = a.gb * a.tb;
-    for (std::uint32_t s = 0; s < a.sweeps; ++s) {
+    // 4. Jacobi sweeps in LDS: num accumulates the six neighbour terms in
+    //    order (a neighbour outside the grid adds gx * 0.0 = +0.0, exact)
+    //    and the ambient term; the update is num * (1 / den).
+    for (std::uint32_t s = 0; s < sweeps; ++s) {
+        double out[kCells];
 #pragma unroll
-        for (int k = 0; k < kCellsPerThread; ++k) {
-            const std::uint32_t c = tid + k * kThreads;
-            const std::uint32_t b = nb[k];
-            if (!(b & kIn)) {
-                continue;
-            }
+        for (int k = 0; k < kCells; ++k) {
             double num = rhs[k];
-            double den = a.cdt;
-            if (b & kXm) {
-                num += a.gx * ((b & kXmL) ? cur[c - 1] : 0.0);
-                den += a.gx;
+            num += gx * cur[nbr[k][0]];
+            num += gx * cur[nbr[k][1]];
+            num += gy * cur[nbr[k][2]];
+            num += gy * cur[nbr[k][3]];
+            num += gz * cur[nbr[k][4]];
+            num += gz * cur[nbr[k][5]];
+            num += topv[k];
+            out[k] = num * rden[k];
+        }
+#pragma unroll
+        for (int k = 0; k < kCells; ++k) {
+            const std::uint32_t c = tid + k * kThreads;
+            if (c < cells) {
+                nxt[c] = out[k];
             }
-            if (b & kXp) {
-                num += a.gx * ((b & kXpL) ? cur[c + 1] : 0.0);
-                den += a.gx;
-            }
-            if (b & kYm) {
-                num += a.gy * ((b & kYmL) ? cur[c - a.rx] : 0.0);
-                den += a.gy;
-            }
-            if (b & kYp) {
-                num += a.gy * ((b & kYpL) ? cur[c + a.rx] : 0.0);
-                den += a.gy;
-            }
-            if (b & kZm) {
-                num += a.gz * cur[c - plane];
-                den += a.gz;
-            }
-            if (b & kZp) {
-                num += a.gz * cur[c + plane];
-                den += a.gz;
-            }
-            if (b & kTop) {
-                num += gbtb;
-                den += a.gb;
-            }
-            nxt[c] = num / den;
         }
         __syncthreads();
         double* t = cur;
@@ -281,31 +284,43 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
         nxt = t;
     }
 
+    // 5. Interior write-back and per-die hotspots.
 #pragma unroll
-    for (int k = 0; k < kCellsPerThread; ++k) {
-        const std::uint32_t c = tid + k * kThreads;
-        if (!(nb[k] & kInterior)) {
-            continue;
-        }
-        const std::uint32_t rxi = c % a.rx;
-        const std::uint32_t t = c / a.rx;
-        const std::uint32_t ryi = t % a.ry;
-        const std::uint32_t z = t / a.ry;
-        const std::uint32_t gx = static_cast<std::uint32_t>(x0 + static_cast<int>(rxi));
-        const std::uint32_t gy = static_cast<std::uint32_t>(y0 + static_cast<int>(ryi));
-        const double v = cur[c];
-        tout[(static_cast<std::size_t>(z) * a.ny + gy) * a.nx + gx] = v;
-        if (a.coupled) {
-            atomicMax(&s_hot[z / a.lpd], static_cast<unsigned long long>(__double_as_longlong(v)));
+    for (int k = 0; k < kCells; ++k) {
+        if (fl[k] & kInterior) {
+            const double val = cur[tid + k * kThreads];
+            tout[gidx[k]] = val;
+            if (kCoupled) {
+                atomicMax(&s_hot[die[k] - safe_die],
+                          static_cast<unsigned long long>(__double_as_longlong(val)));
+            }
         }
     }
-    if (a.coupled) {
+    if (kCoupled) {
         __syncthreads();
         if (tid < static_cast<int>(a.D)) {
-            const std::uint32_t gx = tile_x * a.tx, gy = tile_y * a.ty;
-            const std::uint32_t q = (gy / a.rh) * a.regions_x + gx / a.rw;
-            atomicMax(&a.hot[(w + 1) * a.ndie + q * a.D + tid], s_hot[tid]);
+            atomicMax(&a.hot[(w + 1) * a.ndie + safe_die + tid], s_hot[tid]);
         }
+    }
+}
+
+template <bool kCoupled>
+void launch_window(const TArgs& a, std::uint32_t blocks, std::size_t lds, hipStream_t stream,
+                   const double* tin, double* tout, std::uint64_t w)
+{
+    const std::uint32_t per = (a.cells + kThreads - 1) / kThreads;
+    if (per <= 2) {
+        hipLaunchKernelGGL((k_thermal_window<kCoupled, 2>), dim3(blocks), dim3(kThreads), lds,
+                           stream, a, tin, tout, w);
+    } else if (per <= 4) {
+        hipLaunchKernelGGL((k_thermal_window<kCoupled, 4>), dim3(blocks), dim3(kThreads), lds,
+                           stream, a, tin, tout, w);
+    } else if (per <= 5) {
+        hipLaunchKernelGGL((k_thermal_window<kCoupled, 5>), dim3(blocks), dim3(kThreads), lds,
+                           stream, a, tin, tout, w);
+    } else {
+        hipLaunchKernelGGL((k_thermal_window<kCoupled, 8>), dim3(blocks), dim3(kThreads), lds,
+                           stream, a, tin, tout, w);
     }
 }
 
@@ -581,22 +596,60 @@ void hfree(T*& p)
     }
 }
 
-// Largest tile edge in {16, 8, 4, 2, 1} whose staged region fits.
-void choose_tile(std::uint32_t nz, std::uint32_t sweeps, std::uint32_t div_x,
-                 std::uint32_t div_y, std::uint32_t& tx, std::uint32_t& ty)
+// Tile edge in {16, 8, 4, 2, 1}: of those whose staged region fits in one
+// workgroup and that divide div_x and div_y, the largest that still gives
+// every CU a tile (256 tiles), else the smallest.
+void choose_tile(std::uint32_t nx, std::uint32_t ny, std::uint32_t nz, std::uint32_t sweeps,
+                 std::uint32_t div_x, std::uint32_t div_y, std::uint32_t& tx, std::uint32_t& ty)
 {
+    tx = ty = 0;
     for (std::uint32_t t = 16; t >= 1; t >>= 1) {
         const std::uint32_t r = t + 2 * sweeps;
         if (static_cast<std::uint64_t>(r) * r * nz <= kMaxRegion && div_x % t == 0 &&
             div_y % t == 0) {
             tx = ty = t;
-            return;
-        }
-        if (t == 1) {
-            break;
+            const std::uint64_t tiles = static_cast<std::uint64_t>((nx + t - 1) / t) *
+                                        ((ny + t - 1) / t);
+            if (tiles >= 256) {
+                return;
+            }
         }
     }
-    tx = ty = 0;
+}
+
+std::uint64_t host_sat_add(std::uint64_t a, std::uint64_t b)
+{
+    return a > ~0ull - b ? ~0ull : a + b;
+}
+
+// cpu_service.cpp:221-255: control_sample, then apply_controls, at `now`
+// with stack hotspot hs; returns the applied level.
+std::uint32_t control_step(const hbfsim_amd_reliability_options& o, Ctl& c, std::uint64_t now,
+                           double hs)
+{
+    const double thr[4] = {0.0, o.light_k, o.severe_k, o.shutdown_k};
+    std::uint32_t desired = static_cast<std::uint32_t>(hs >= o.light_k) +
+                            static_cast<std::uint32_t>(hs >= o.severe_k) +
+                            static_cast<std::uint32_t>(hs >= o.shutdown_k);
+    if (desired < c.applied && hs >= thr[c.applied] - o.hysteresis_k) {
+        desired = c.applied;
+    }
+    if (o.policy != 0) {
+        if (desired == c.applied) {
+            c.pending = kNoPending;
+        } else if (c.pending == kNoPending || c.pending != desired) {
+            const std::uint64_t x = host_sat_add(now, o.action_delay_ps);
+            const std::uint64_t y = host_sat_add(c.last_change, o.min_dwell_ps);
+            c.pending = desired;
+            c.pending_at = x > y ? x : y;
+        }
+    }
+    if (c.pending != kNoPending && c.pending_at <= now) {
+        c.applied = c.pending;
+        c.last_change = now;
+        c.pending = kNoPending;
+    }
+    return c.applied;
 }
 
 void host_retention_table(double ea, double tref, std::uint64_t window_ps, std::uint64_t* table)
@@ -616,7 +669,9 @@ struct thermal {
     int device = 0;
     double* d_scratch = nullptr;   // second temperature buffer
     hipEvent_t ev[2] = {nullptr, nullptr};
+    hipEvent_t cev[8] = {};        // coupled-run phase boundaries
     float last_ms = 0.0f;
+    float phase_ms[5] = {};        // counts, thermal chain, admission, engine, gather
     // last coupled run
     std::uint64_t windows = 0;
     std::uint32_t ndie = 0;
@@ -634,7 +689,7 @@ int thermal_create(const hbfsim_amd_thermal_grid& g, thermal** out)
         return HBFSIM_INVALID_ARGUMENT;
     }
     std::uint32_t tx, ty;
-    choose_tile(g.nz, g.sweeps, 16, 16, tx, ty);
+    choose_tile(g.nx, g.ny, g.nz, g.sweeps, 16, 16, tx, ty);
     if (tx == 0) {
         return HBFSIM_UNSUPPORTED;
     }
@@ -648,6 +703,9 @@ int thermal_create(const hbfsim_amd_thermal_grid& g, thermal** out)
         err = halloc(th->d_scratch, static_cast<std::size_t>(g.nx) * g.ny * g.nz);
     for (int i = 0; i < 2 && err == hipSuccess; ++i) {
         err = hipEventCreate(&th->ev[i]);
+    }
+    for (int i = 0; i < 8 && err == hipSuccess; ++i) {
+        err = hipEventCreate(&th->cev[i]);
     }
     if (err != hipSuccess) {
         thermal_destroy(th);
@@ -670,12 +728,26 @@ void thermal_destroy(thermal* th)
             (void)hipEventDestroy(e);
         }
     }
+    for (auto& e : th->cev) {
+        if (e != nullptr) {
+            (void)hipEventDestroy(e);
+        }
+    }
     delete th;
 }
 
 const hbfsim_amd_thermal_grid& thermal_get_grid(const thermal* th) { return th->grid; }
 
 float thermal_last_step_ms(const thermal* th) { return th->last_ms; }
+
+int coupled_last_ms(const thermal* th, float* ms, int max)
+{
+    const int k = max < 5 ? max : 5;
+    for (int i = 0; i < k; ++i) {
+        ms[i] = th->phase_ms[i];
+    }
+    return k;
+}
 
 namespace {
 
@@ -693,6 +765,9 @@ TArgs base_args(const hbfsim_amd_thermal_grid& g, std::uint32_t tx, std::uint32_
     a.ry = ty + 2 * g.sweeps;
     a.tiles_x = (g.nx + tx - 1) / tx;
     a.cells = a.rx * a.ry * g.nz;
+    a.step_x = kThreads % a.rx;
+    a.step_y = (kThreads / a.rx) % a.ry;
+    a.step_z = kThreads / (a.rx * a.ry);
     a.cdt = g.capacity_j_per_k / g.dt_s;
     a.gx = g.gx_w_per_k;
     a.gy = g.gy_w_per_k;
@@ -725,16 +800,15 @@ int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     const auto& g = th->grid;
     std::uint32_t tx, ty;
-    choose_tile(g.nz, g.sweeps, 16, 16, tx, ty);
+    choose_tile(g.nx, g.ny, g.nz, g.sweeps, 16, 16, tx, ty);
     TArgs a = base_args(g, tx, ty);
     a.power = d_power;
-    const std::size_t lds = 2ull * a.cells * sizeof(double);
+    const std::size_t lds = 2ull * (a.cells + 1) * sizeof(double);
     const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
     double* buf[2] = {d_temp, th->d_scratch};
     (void)hipEventRecord(th->ev[0], stream);
     for (std::uint64_t s = 0; s < steps; ++s) {
-        hipLaunchKernelGGL(k_thermal_window, dim3(tile_blocks(a)), dim3(kThreads), lds, stream,
-                           a, buf[s & 1], buf[(s + 1) & 1], 0ull);
+        launch_window<false>(a, tile_blocks(a), lds, stream, buf[s & 1], buf[(s + 1) & 1], 0ull);
     }
     (void)hipEventRecord(th->ev[1], stream);
     hipError_t err = hipGetLastError();
@@ -779,8 +853,8 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     }
     const std::uint32_t rw = g.nx / o.regions_x, rh = g.ny / o.regions_y;
     std::uint32_t tx, ty;
-    choose_tile(g.nz, g.sweeps, rw, rh, tx, ty);
-    if (tx == 0) {
+    choose_tile(g.nx, g.ny, g.nz, g.sweeps, rw, rh, tx, ty);
+    if (tx == 0 || g.sweeps > rw || g.sweeps > rh) {
         return HBFSIM_UNSUPPORTED;
     }
     if (hipSetDevice(th->device) != hipSuccess) {
@@ -807,7 +881,6 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     unsigned long long* d_hot = nullptr;
     std::uint64_t* d_af = nullptr;
     std::uint64_t* d_age = nullptr;  // [2][ndie]
-    Ctl* d_ctl = nullptr;            // [2]
     std::uint8_t* d_level = nullptr;
     std::uint8_t* d_refresh = nullptr;
     std::uint32_t* d_ok2 = nullptr;
@@ -822,7 +895,7 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     std::uint8_t* d_mstat = nullptr;
     Partial* d_part = nullptr;
     auto release = [&]() {
-        hfree(d_counts); hfree(d_hot); hfree(d_af); hfree(d_age); hfree(d_ctl);
+        hfree(d_counts); hfree(d_hot); hfree(d_af); hfree(d_age);
         hfree(d_level); hfree(d_refresh); hfree(d_ok2); hfree(d_gtiles); hfree(d_gcarry);
         hfree(d_admit); hfree(d_ref); hfree(d_ref_issue); hfree(d_merged); hfree(d_pos);
         hfree(d_mcomp); hfree(d_mstat); hfree(d_part);
@@ -832,7 +905,6 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     if (err == hipSuccess) err = halloc(d_hot, wd + ndie);
     if (err == hipSuccess) err = halloc(d_af, kAfBins);
     if (err == hipSuccess) err = halloc(d_age, 2ull * ndie);
-    if (err == hipSuccess) err = halloc(d_ctl, 2);
     if (err == hipSuccess) err = halloc(d_level, windows);
     if (err == hipSuccess) err = halloc(d_refresh, wd);
     if (err != hipSuccess) {
@@ -840,6 +912,7 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
         return HBFSIM_CUDA_ERROR;
     }
     // 1. per-window, per-die access counts
+    (void)hipEventRecord(th->cev[0], stream);
     const unsigned fill_blocks = static_cast<unsigned>(std::min<std::size_t>((wd + ndie + 255) / 256, 65536));
     hipLaunchKernelGGL(k_fill_u64, dim3(std::max(1u, fill_blocks)), dim3(256), 0, stream,
                        d_hot, wd + ndie, 0ull);
@@ -855,13 +928,12 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
         return st;
     }
     // 2. thermal / retention / throttle chain
+    (void)hipEventRecord(th->cev[1], stream);
     std::vector<std::uint64_t> table(kAfBins);
     host_retention_table(o.activation_energy_ev, o.reference_k, o.window_ps, table.data());
-    Ctl c0{0, kNoPending, 0, 0};
     err = hipMemcpyAsync(d_af, table.data(), kAfBins * 8, hipMemcpyHostToDevice, stream);
     if (err == hipSuccess)
         err = hipMemcpyAsync(d_age, age, ndie * 8ull, hipMemcpyHostToDevice, stream);
-    if (err == hipSuccess) err = hipMemcpyAsync(d_ctl, &c0, sizeof(Ctl), hipMemcpyHostToDevice, stream);
     TArgs a = base_args(g, tx, ty);
     a.coupled = 1;
     a.ndie = ndie;
@@ -870,7 +942,6 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     a.rh = rh;
     a.D = cfg.dies;
     a.lpd = g.nz / cfg.dies;
-    a.policy = o.policy;
     a.static_w = o.static_power_w;
     const double cells_per_die = static_cast<double>(rw * rh * a.lpd);
     a.pa = (o.access_energy_j / g.dt_s) / cells_per_die;
@@ -880,29 +951,20 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     a.af = d_af;
     a.retention_ps = o.retention_ps;
     a.window_ps = o.window_ps;
-    a.light_k = o.light_k;
-    a.severe_k = o.severe_k;
-    a.shutdown_k = o.shutdown_k;
-    a.hysteresis_k = o.hysteresis_k;
-    a.action_delay_ps = o.action_delay_ps;
-    a.min_dwell_ps = o.min_dwell_ps;
-    a.level = d_level;
     a.refresh = d_refresh;
     if (err == hipSuccess) {
         hipLaunchKernelGGL(k_die_hot, dim3(static_cast<unsigned>(std::min<std::size_t>((cells + 255) / 256, 4096))),
                            dim3(256), 0, stream, a, static_cast<const double*>(d_temp), d_hot);
     }
-    const std::size_t lds = 2ull * a.cells * sizeof(double);
+    const std::size_t lds = 2ull * (a.cells + 1) * sizeof(double);
     double* buf[2] = {d_temp, th->d_scratch};
     for (std::uint64_t w = 0; w < windows && err == hipSuccess; ++w) {
         a.age_in = d_age + (w & 1) * ndie;
         a.age_out = d_age + ((w + 1) & 1) * ndie;
-        a.ctl_in = d_ctl + (w & 1);
-        a.ctl_out = d_ctl + ((w + 1) & 1);
-        hipLaunchKernelGGL(k_thermal_window, dim3(tile_blocks(a)), dim3(kThreads), lds, stream,
-                           a, buf[w & 1], buf[(w + 1) & 1], w);
+        launch_window<true>(a, tile_blocks(a), lds, stream, buf[w & 1], buf[(w + 1) & 1], w);
     }
     if (err == hipSuccess) err = hipGetLastError();
+    (void)hipEventRecord(th->cev[2], stream);
     if (err == hipSuccess && (windows & 1)) {
         err = hipMemcpyAsync(d_temp, th->d_scratch, cells * sizeof(double),
                              hipMemcpyDeviceToDevice, stream);
@@ -915,8 +977,6 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
                              stream);
     if (err == hipSuccess)
         err = hipMemcpyAsync(th->hot.data(), d_hot, (wd + ndie) * 8, hipMemcpyDeviceToHost, stream);
-    if (err == hipSuccess && windows)
-        err = hipMemcpyAsync(th->level.data(), d_level, windows, hipMemcpyDeviceToHost, stream);
     if (err == hipSuccess && wd)
         err = hipMemcpyAsync(th->refresh.data(), d_refresh, wd, hipMemcpyDeviceToHost, stream);
     if (err == hipSuccess) err = hipStreamSynchronize(stream);
@@ -926,8 +986,18 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     }
     th->windows = windows;
     th->ndie = ndie;
-    for (std::uint64_t w = 0; w < windows; ++w) {
-        rep.level_windows[th->level[w] & 3] += 1;
+    // throttle levels from the stack hotspot of each window's start
+    {
+        Ctl c{0, kNoPending, 0, 0};
+        for (std::uint64_t w = 0; w < windows; ++w) {
+            const double* row = th->hot.data() + w * ndie;
+            double hs = row[0];
+            for (std::uint32_t d = 1; d < ndie; ++d) {
+                hs = row[d] > hs ? row[d] : hs;
+            }
+            th->level[w] = static_cast<std::uint8_t>(control_step(o, c, w * o.window_ps, hs));
+            rep.level_windows[th->level[w]] += 1;
+        }
     }
     for (double v : th->hot) {
         rep.peak_k = v > rep.peak_k ? v : rep.peak_k;
@@ -993,6 +1063,8 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     if (err == hipSuccess) err = halloc(d_part, std::max(1u, gblocks));
     if (err == hipSuccess)
         err = hipMemcpyAsync(d_ok2, ok2.data(), ok2.size() * 4, hipMemcpyHostToDevice, stream);
+    if (err == hipSuccess && windows)
+        err = hipMemcpyAsync(d_level, th->level.data(), windows, hipMemcpyHostToDevice, stream);
     if (err == hipSuccess && nref)
         err = hipMemcpyAsync(d_ref, refs.data(), nref * sizeof(hbf_record32), hipMemcpyHostToDevice,
                              stream);
@@ -1002,6 +1074,7 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
         release();
         return HBFSIM_CUDA_ERROR;
     }
+    (void)hipEventRecord(th->cev[3], stream);
     if (n != 0) {
         GArgs ga;
         ga.rec = d_rec;
@@ -1033,14 +1106,16 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
         release();
         return HBFSIM_CUDA_ERROR;
     }
+    (void)hipEventRecord(th->cev[4], stream);
     // 4. the engine on the merged stream
     hbfsim_amd_report er;
-    st = engine_run(e, d_merged, total, d_mcomp, d_mstat, 0, stream_ptr, &er);
+    st = engine_run(e, d_merged, total, d_mcomp, d_mstat, 0, stream_ptr, &er, nref != 0);
     if (st != HBFSIM_OK) {
         release();
         return st;
     }
     rep.makespan_ps = er.makespan_ps;
+    (void)hipEventRecord(th->cev[5], stream);
     if (n != 0) {
         hipLaunchKernelGGL(k_gather, dim3(gblocks), dim3(kThreads), 0, stream, d_rec, n,
                            static_cast<const std::uint64_t*>(d_admit),
@@ -1048,6 +1123,7 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
                            static_cast<const std::uint64_t*>(d_mcomp),
                            static_cast<const std::uint8_t*>(d_mstat), d_comp, d_part);
         std::vector<Partial> parts(gblocks);
+        (void)hipEventRecord(th->cev[6], stream);
         err = hipGetLastError();
         if (err == hipSuccess)
             err = hipMemcpyAsync(parts.data(), d_part, gblocks * sizeof(Partial),
@@ -1068,6 +1144,14 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
         }
     }
     release();
+    const int pairs[5][2] = {{0, 1}, {1, 2}, {3, 4}, {4, 5}, {5, 6}};
+    for (int k = 0; k < 5; ++k) {
+        float ms = 0.0f;
+        th->phase_ms[k] = (n != 0 && hipEventElapsedTime(&ms, th->cev[pairs[k][0]],
+                                                         th->cev[pairs[k][1]]) == hipSuccess)
+                              ? ms
+                              : 0.0f;
+    }
     if (out != nullptr) *out = rep;
     if (erep != nullptr) *erep = er;
     return HBFSIM_OK;

@@ -29,6 +29,9 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
                 std::size_t n, std::uint64_t* d_completion, double* d_temperature,
                 std::uint64_t* age_ps, void* stream, hbfsim_amd_coupled_report* out,
                 hbfsim_amd_report* engine_report);
+// Device time (ms) of the last coupled run's phases: [0] access counts,
+// [1] thermal chain, [2] admission and merge, [3] engine, [4] gather.
+int coupled_last_ms(const thermal* th, float* ms, int max);
 // Per-window trace of the last coupled run (host arrays).
 int coupled_trace(const thermal* th, double* hot, std::size_t hot_count, std::uint8_t* level,
                   std::size_t level_count, std::uint8_t* refresh, std::size_t refresh_count,

@@ -293,6 +293,13 @@ class Thermal:
                   "thermal time")
         return float(ms.value)
 
+    def coupled_ms(self) -> dict:
+        """Device time of the last coupled run's phases."""
+        ms = (ctypes.c_float * 5)()
+        k = self._lib.hbfsim_amd_coupled_last_ms(self.handle, ms, 5)
+        names = ("counts", "thermal_chain", "admission", "engine", "gather")
+        return {names[i]: float(ms[i]) for i in range(k)}
+
     def trace(self) -> dict:
         """Per-window trace of the last coupled run."""
         w, d = ctypes.c_uint64(), ctypes.c_uint32()

@@ -178,7 +178,11 @@ hbfsim_context* hbfsim_vllm_session_context(hbfsim_vllm_session* session);
  * (hbf_device.cu:963).  issue_ps is the issue time in picoseconds relative
  * to the run's base_ps.  flags bits 0-7: operation (0 read, 1 write); other
  * bits are ignored.  Records must be ordered by issue time; a record's
- * service order on every resource is its position in the stream. */
+ * service order on every resource is its position in the stream.  The
+ * thermal-coupled run also merges refresh records into the stream it times:
+ * operation 2 with flag bit 8 set, addr = media page, bytes moved on the
+ * channel (read out and written back); elsewhere operation 2 is
+ * unsupported like any operation above 1. */
 typedef struct hbf_record32 {
     uint64_t addr;
     uint64_t bytes;
@@ -438,6 +442,12 @@ int hbfsim_amd_run_coupled(hbfsim_context* context, hbfsim_amd_thermal* thermal,
                            uint64_t* age_ps, void* stream,
                            hbfsim_amd_coupled_report* report,
                            hbfsim_amd_report* engine_report);
+/* Device time (ms) of the last coupled run's phases, from HIP events on its
+ * stream: [0] access counts, [1] thermal chain (all windows), [2] admission
+ * and merge, [3] engine on the merged stream, [4] gather.  Returns the
+ * number written (-1 on a NULL argument). */
+int hbfsim_amd_coupled_last_ms(const hbfsim_amd_thermal* thermal, float* ms,
+                               int max_phases);
 /* Per-window trace of the last coupled run: die hotspots [(windows + 1) *
  * dies] (row 0 = the initial temperature), throttle levels [windows],
  * refresh flags [windows * dies].  Host arrays (any may be NULL); counts are

@@ -597,7 +597,7 @@ static void decode(const orc_engine_params* p, const orc_range* ranges,
     uint32_t index = 0;
     d->issue = base_ps + rec->issue_ps;
     d->op = op;
-    if (op == ORC_OP_REFRESH && (rec->flags & ORC_FLAG_MEDIA) != 0) {
+    if (p->media_records && op == ORC_OP_REFRESH && (rec->flags & ORC_FLAG_MEDIA) != 0) {
         /* refresh of media page `addr`: read it out and program it back
          * (cpu_service.cpp:181-212's read -> program pair as one job) */
         const uint64_t page = rec->addr;
@@ -1061,7 +1061,8 @@ out:
 /* Jacobi sweeps over caller-provided buffers (old = T at the start of the
  * step, cur = current iterate, nxt = scratch).  Each cell's numerator and
  * denominator are accumulated in a fixed order -- x-1, x+1, y-1, y+1, z-1,
- * z+1, ambient -- which the GPU stencil follows operation for operation. */
+ * z+1, ambient -- and the update is num * (1 / den); the GPU stencil
+ * follows this operation for operation. */
 static int grid_jacobi(uint32_t nx, uint32_t ny, uint32_t nz, double cdt,
                        double gx, double gy, double gz, double gb, double tb,
                        const double* power, const double* old, double** curp,
@@ -1085,7 +1086,7 @@ static int grid_jacobi(uint32_t nx, uint32_t ny, uint32_t nz, double cdt,
                     if (z > 0) { num += gz * cur[i - (size_t)nx * ny]; den += gz; }
                     if (z + 1 < nz) { num += gz * cur[i + (size_t)nx * ny]; den += gz; }
                     if (z + 1 == nz) { num += gb * tb; den += gb; }
-                    nxt[i] = num / den;
+                    nxt[i] = num * (1.0 / den);
                     const double dd = fabs(nxt[i] - cur[i]);
                     if (dd > delta) {
                         delta = dd;
@@ -1483,7 +1484,9 @@ int orc_coupled_run(const orc_engine_params* p, const orc_range* ranges,
         orc_merge_records(rec, admit, n, extra, nref, merged, pos);
         orc_engine_report er;
         memset(&er, 0, sizeof(er));
-        rc = orc_engine_run(p, ranges, range_count, merged, n + nref, 0, s, mcomp, mstat,
+        orc_engine_params q = *p;
+        q.media_records = nref != 0;
+        rc = orc_engine_run(&q, ranges, range_count, merged, n + nref, 0, s, mcomp, mstat,
                             &er);
         rep->refreshes = nref;
         rep->makespan_ps = er.makespan_ps;

@@ -101,7 +101,9 @@ enum orc_status {
 };
 /* Record operations beyond read (0) and write (1): a refresh of media page
  * `addr` (read out and programmed back; plane tR + tPROG, channel `bytes`),
- * valid only with the media flag.  Injected by the reliability model. */
+ * valid only with the media flag and only in streams whose parameters set
+ * media_records (the coupled run's merged stream); elsewhere an operation
+ * above 1 is unsupported, as the resolver has it. */
 #define ORC_OP_REFRESH 2u
 #define ORC_FLAG_MEDIA 0x100u
 uint32_t orc_classify(const orc_range* ranges, uint32_t count,
@@ -193,6 +195,8 @@ typedef struct orc_engine_params {
     uint64_t xfer_quantum;                   /*   q * ceil(b*num/den)      */
     orc_empirical empirical;                 /* MODEL_FAST_EMPIRICAL only */
     uint64_t media_pages;                    /* device pages; 0 = no limit */
+    uint32_t media_records;                  /* 1: accept refresh records */
+    uint32_t reserved;
 } orc_engine_params;
 
 typedef struct orc_engine_state {

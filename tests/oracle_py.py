@@ -46,7 +46,8 @@ class OrcParams(ctypes.Structure):
                 ("program_every_write", _U32), ("hybrid", _U32), ("hybrid_warmup", _U32),
                 ("hybrid_threshold", _U64), ("read_ps", _U64), ("program_ps", _U64),
                 ("xfer_num", _U64), ("xfer_den", _U64), ("xfer_quantum", _U64),
-                ("empirical", OrcEmpirical), ("media_pages", _U64)]
+                ("empirical", OrcEmpirical), ("media_pages", _U64), ("media_records", _U32),
+                ("reserved", _U32)]
 
 
 class OrcState(ctypes.Structure):
