@@ -38,11 +38,44 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="budget for the CPU-oracle baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="first fill and copy 2 GiB (known HBM bytes) so that counter runs "
+                         "can calibrate FETCH_SIZE / WRITE_SIZE")
     return ap.parse_args()
+
+
+def copy_probe() -> None:
+    """A plain fill (2 GiB written) and copy (2 GiB read + 2 GiB written)
+    outside the timed region: the reference kernels for HBM counters."""
+    import torch
+    n = (1 << 31) // 4
+    src = torch.empty(n, dtype=torch.float32, device="cuda")
+    src.fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def committed_traffic(summary: str, kernel: str, units: int) -> tuple[float | None, str | None]:
+    """HBM bytes per launch of `kernel` for `units` records (or cells), from
+    a committed counter summary under profiles/ (two rocprofv3 passes,
+    FETCH_SIZE and WRITE_SIZE, each calibrated against a 2 GiB copy).
+    Counters cannot be read from inside the timed run, so the figure is the
+    measured bytes per unit of that profile scaled to this launch."""
+    path = ROOT / "profiles" / summary
+    if not path.exists():
+        return None, None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if parts and parts[0] == kernel and not line.startswith("#"):
+            return float(parts[-1]) * units, f"profiles/{summary}"
+    return None, None
 
 
 def build_workload(name: str, steps: int, batches: int = 6):
@@ -246,7 +279,9 @@ def bench_thermal(args) -> dict:
                                "Euler step, config-4 conductances, random power"},
         "roofline": {"bound": "hbm", "kernel": "k_thermal_window", "achieved": achieved,
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBPS,
-                     "traffic": None, "kernel_ms": kms,
+                     "traffic": committed_traffic("thermal_traffic_grid2048.txt",
+                                                  "k_thermal_window", cells)[0],
+                     "traffic_source": "profiles/thermal_traffic_grid2048.txt", "kernel_ms": kms,
                      "algorithmic": "16 B per cell-sweep (8 B read + 8 B write)"},
     }
     if not args.no_cpu:
@@ -280,6 +315,8 @@ def main() -> None:
     import torch
     from hbfsim_amd import engine
 
+    if args.copy_probe:
+        copy_probe()
     if args.config in ("c4", "thermal"):
         out = bench_c4(args) if args.config == "c4" else bench_thermal(args)
         print(json.dumps(out), flush=True)
@@ -319,6 +356,9 @@ def main() -> None:
     names = ["k_summary", "k_carry", "k_apply"]
     per_launch = accesses / args.steps
     achieved = ALGO_BYTES_PER_ACCESS * per_launch / (avg_ms[dominant] / 1e3) / 1e9
+    traffic, traffic_src = (committed_traffic("engine_traffic_config2.txt", names[dominant],
+                                              int(per_launch))
+                            if args.config == "c2" else (None, None))
     out = {
         "metric": "modeled HBF accesses/sec on 1 MI355X",
         "value": value,
@@ -335,7 +375,8 @@ def main() -> None:
         "config": desc,
         "roofline": {"bound": "hbm", "kernel": names[dominant],
                      "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBPS, "traffic": None,
+                     "frac": achieved / PEAK_HBM_GBPS, "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "kernel_ms": {nm: float(v) for nm, v in zip(names, avg_ms)},
                      "pipeline_frac": value * ALGO_BYTES_PER_ACCESS / 1e9 / PEAK_HBM_GBPS},
     }
