@@ -39,6 +39,29 @@ def command(output: pathlib.Path = LIB) -> list[str]:
     ]
 
 
+CLI = HERE / "hbf_trace_timing"
+CLI_SOURCES = [CSRC / "trace_timing.cpp", CSRC / "profile.cpp"]
+
+
+def cli_command(output: pathlib.Path = CLI) -> list[str]:
+    """The hbf_trace_timing drop-in: host C++ only."""
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+    return [cxx, "-O2", "-std=c++17", "-Wall", "-o", str(output), *[str(s) for s in CLI_SOURCES]]
+
+
+def build_cli(verbose: bool = False) -> pathlib.Path:
+    tmp = CLI.with_suffix(".tmp")
+    cmd = cli_command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"c++ failed with status {proc.returncode}")
+    os.replace(tmp, CLI)
+    return CLI
+
+
 def build(verbose: bool = False) -> pathlib.Path:
     """Compiles every source every time it is called."""
     tmp = LIB.with_suffix(".so.tmp")
@@ -52,6 +75,7 @@ def build(verbose: bool = False) -> pathlib.Path:
     if verbose and proc.stderr.strip():
         sys.stderr.write(proc.stderr)
     os.replace(tmp, LIB)
+    build_cli(verbose)
     return LIB
 
 
