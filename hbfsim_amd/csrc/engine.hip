@@ -1567,6 +1567,441 @@ __global__ __launch_bounds__(256) void k_window_counts(KArgs a, const hbf_record
     }
 }
 
+// ---- empirical single-tail model (hbf_device.cu:796-881) -----------------
+// One busy-until tail; a read's service is the cumulative curve's increment
+// at its burst run (streak of consecutive ascending pages with one
+// operation, capped at 1023, hbf_device.cuh:1031-1080), a write's is tPROG.
+// Three scans over tiles of 4096 records (256 threads x 16 consecutive
+// records): the streak summaries (associative, below) give every tile its
+// incoming burst state; with services known, the tail's (max,+) maps give
+// every tile its incoming busy time; the apply pass replays each thread's
+// records from both.  Services per run come from a 1024-entry table.
+constexpr int kEmpThreads = 256;
+constexpr std::uint32_t kEmpPer = 16;
+constexpr std::uint32_t kEmpTile = kEmpThreads * kEmpPer;
+constexpr std::uint64_t kRunCap = 1023;
+constexpr std::uint64_t kMaxEmpPage = (1ull << 53) - 2;
+
+struct alignas(16) Burst {
+    std::uint64_t fpage, lpage;  // first / last page of the streak records
+    std::uint64_t lead, tail;    // lengths of the first and last streaks
+    std::uint64_t nburst;        // records taking part in streaks
+    std::uint64_t nmod;          // modeled records
+    std::uint32_t fop, lop, all, pad;
+};
+struct alignas(16) BState {
+    std::uint64_t page, run;
+    std::uint32_t op, valid;
+};
+struct alignas(16) TailMap {
+    std::uint64_t A, B;  // b -> max(b + A, B)
+};
+
+__device__ __forceinline__ Burst burst_zero()
+{
+    Burst b;
+    b.fpage = b.lpage = b.lead = b.tail = b.nburst = b.nmod = 0;
+    b.fop = b.lop = b.all = b.pad = 0;
+    return b;
+}
+
+// a then b
+__device__ __forceinline__ Burst burst_combine(const Burst& a, const Burst& b)
+{
+    if (b.nburst == 0) {
+        Burst r = a;
+        r.nmod = a.nmod + b.nmod;
+        return r;
+    }
+    if (a.nburst == 0) {
+        Burst r = b;
+        r.nmod = a.nmod + b.nmod;
+        return r;
+    }
+    const bool cont = a.lop == b.fop && a.lpage + 1 == b.fpage;
+    Burst r;
+    r.fpage = a.fpage;
+    r.fop = a.fop;
+    r.lpage = b.lpage;
+    r.lop = b.lop;
+    r.lead = (a.all && cont) ? a.lead + b.lead : a.lead;
+    r.tail = (b.all && cont) ? a.tail + b.tail : b.tail;
+    r.all = (a.all && b.all && cont) ? 1u : 0u;
+    r.nburst = a.nburst + b.nburst;
+    r.nmod = a.nmod + b.nmod;
+    r.pad = 0;
+    return r;
+}
+
+__device__ __forceinline__ BState burst_apply(const BState& st, const Burst& s)
+{
+    if (s.nburst == 0) {
+        return st;
+    }
+    const bool cont = st.valid && st.op == s.fop && st.page + 1 == s.fpage;
+    BState r;
+    r.page = s.lpage;
+    r.op = s.lop;
+    r.valid = 1;
+    const std::uint64_t len = (s.all && cont) ? st.run + s.tail : s.tail;
+    r.run = len < kRunCap ? len : kRunCap;
+    return r;
+}
+
+__device__ __forceinline__ void burst_add(Burst& b, std::uint64_t page, std::uint32_t op)
+{
+    if (b.nburst == 0) {
+        b.fpage = b.lpage = page;
+        b.fop = b.lop = op;
+        b.lead = b.tail = 1;
+        b.all = 1;
+    } else {
+        const bool cont = b.lop == op && b.lpage + 1 == page;
+        if (cont) {
+            ++b.tail;
+            if (b.all) {
+                ++b.lead;
+            }
+        } else {
+            b.all = 0;
+            b.tail = 1;
+        }
+        b.lpage = page;
+        b.lop = op;
+    }
+    ++b.nburst;
+}
+
+// One modeled record through the burst state (orc_update_empirical_burst):
+// its service in ps.
+__device__ __forceinline__ std::uint64_t emp_step(BState& st, std::uint64_t page,
+                                                  std::uint32_t op, const std::uint64_t* svc_ps,
+                                                  std::uint64_t program_ps)
+{
+    if (page > kMaxEmpPage) {
+        return 0;
+    }
+    const bool cont = st.valid && st.op == op && st.page + 1 == page;
+    const std::uint64_t run = cont ? (st.run < kRunCap ? st.run + 1 : kRunCap) : 1;
+    st.page = page;
+    st.op = op;
+    st.run = run;
+    st.valid = 1;
+    return op == 0 ? svc_ps[run] : program_ps;
+}
+
+__device__ __forceinline__ TailMap tail_compose(const TailMap& f, const TailMap& s)
+{
+    const std::uint64_t b = f.B + s.A;
+    return TailMap{f.A + s.A, b > s.B ? b : s.B};
+}
+
+// Inclusive scan over the block's threads, in thread order.
+template <class T, class F>
+__device__ T block_scan_incl(T v, T* buf, F op)
+{
+    const int t = threadIdx.x;
+    buf[t] = v;
+    __syncthreads();
+    for (int o = 1; o < kEmpThreads; o <<= 1) {
+        T x = buf[t];
+        if (t >= o) {
+            x = op(buf[t - o], x);
+        }
+        __syncthreads();
+        buf[t] = x;
+        __syncthreads();
+    }
+    return buf[t];
+}
+
+struct EmpRec {
+    Dec d;
+    bool valid, modeled;
+};
+
+__device__ __forceinline__ EmpRec emp_decode(const KArgs& a, const std::uint64_t* fence,
+                                             RangeCache& rc, const hbf_record32* rec,
+                                             std::size_t n, std::size_t i, std::uint64_t base_ps)
+{
+    EmpRec r;
+    r.valid = i < n;
+    if (r.valid) {
+        uint4 x, y;
+        load_record(rec, i, x, y);
+        r.d = decode<false>(a, fence, rc, x, y, base_ps);
+    } else {
+        r.d = invalid_dec();
+    }
+    r.modeled = r.valid && r.d.cls == kClsModeled;
+    return r;
+}
+
+__device__ __forceinline__ void emp_load_fences(const KArgs& a, std::uint64_t* fence)
+{
+    for (std::uint32_t j = threadIdx.x; j < a.r_nfence; j += kEmpThreads) {
+        fence[j] = a.r_base[static_cast<std::size_t>(j) * a.r_stride];
+    }
+}
+
+// The burst summary of this thread's records, and the block's.
+__device__ Burst emp_thread_burst(const KArgs& a, const std::uint64_t* fence,
+                                  const hbf_record32* rec, std::size_t n, std::size_t begin,
+                                  std::uint64_t base_ps)
+{
+    RangeCache rc = empty_cache();
+    Burst b = burst_zero();
+    for (std::uint32_t k = 0; k < kEmpPer; ++k) {
+        const EmpRec r = emp_decode(a, fence, rc, rec, n, begin + k, base_ps);
+        if (r.modeled) {
+            ++b.nmod;
+            const std::uint64_t page = r.d.page1 - 1;
+            if (page <= kMaxEmpPage) {
+                burst_add(b, page, dec_op(r.d.bits));
+            }
+        }
+    }
+    return b;
+}
+
+__global__ __launch_bounds__(kEmpThreads) void k_emp_burst(KArgs a, const hbf_record32* rec,
+                                                           std::size_t n, std::uint64_t base_ps,
+                                                           Burst* tiles)
+{
+    extern __shared__ std::uint64_t fence[];
+    __shared__ Burst buf[kEmpThreads];
+    emp_load_fences(a, fence);
+    __syncthreads();
+    const std::size_t begin = static_cast<std::size_t>(blockIdx.x) * kEmpTile + threadIdx.x * kEmpPer;
+    const Burst b = emp_thread_burst(a, fence, rec, n, begin, base_ps);
+    const Burst incl = block_scan_incl(b, buf, burst_combine);
+    if (threadIdx.x == kEmpThreads - 1) {
+        tiles[blockIdx.x] = incl;
+    }
+}
+
+// One block: the burst state and modeled-request sequence before every
+// tile, and after the last.
+__global__ __launch_bounds__(kEmpThreads) void k_emp_burst_carry(const Burst* tiles,
+                                                                 std::size_t ntiles, BState init,
+                                                                 std::uint64_t seq0,
+                                                                 BState* tile_in,
+                                                                 std::uint64_t* tile_seq,
+                                                                 BState* final_state,
+                                                                 std::uint64_t* final_seq)
+{
+    __shared__ Burst buf[kEmpThreads];
+    const std::size_t per = (ntiles + kEmpThreads - 1) / kEmpThreads;
+    const std::size_t b = threadIdx.x * per;
+    const std::size_t e = b + per < ntiles ? b + per : ntiles;
+    Burst m = burst_zero();
+    for (std::size_t t = b; t < e; ++t) {
+        m = burst_combine(m, tiles[t]);
+    }
+    const Burst incl = block_scan_incl(m, buf, burst_combine);
+    Burst ex = burst_zero();
+    if (threadIdx.x > 0) {
+        ex = buf[threadIdx.x - 1];
+    }
+    BState st = burst_apply(init, ex);
+    std::uint64_t seq = seq0 + ex.nmod;
+    for (std::size_t t = b; t < e; ++t) {
+        tile_in[t] = st;
+        tile_seq[t] = seq;
+        st = burst_apply(st, tiles[t]);
+        seq += tiles[t].nmod;
+    }
+    if (threadIdx.x == kEmpThreads - 1) {
+        *final_state = burst_apply(init, incl);
+        *final_seq = seq0 + incl.nmod;
+    }
+}
+
+// Per thread: burst state at its first record (block scan of the thread
+// summaries from the tile's incoming state); returns it and the number of
+// modeled records before the thread within the tile.
+__device__ BState emp_thread_state(const KArgs& a, const std::uint64_t* fence,
+                                   const hbf_record32* rec, std::size_t n, std::size_t begin,
+                                   std::uint64_t base_ps, const BState& tile_state, Burst* buf,
+                                   std::uint64_t& nmod_before)
+{
+    const Burst mine = emp_thread_burst(a, fence, rec, n, begin, base_ps);
+    block_scan_incl(mine, buf, burst_combine);
+    Burst ex = burst_zero();
+    if (threadIdx.x > 0) {
+        ex = buf[threadIdx.x - 1];
+    }
+    nmod_before = ex.nmod;
+    return burst_apply(tile_state, ex);
+}
+
+__device__ TailMap emp_thread_map(const KArgs& a, const std::uint64_t* fence,
+                                  const hbf_record32* rec, std::size_t n, std::size_t begin,
+                                  std::uint64_t base_ps, BState st, const std::uint64_t* svc_ps,
+                                  std::uint64_t program_ps)
+{
+    RangeCache rc = empty_cache();
+    TailMap m{0, 0};
+    for (std::uint32_t k = 0; k < kEmpPer; ++k) {
+        const EmpRec r = emp_decode(a, fence, rc, rec, n, begin + k, base_ps);
+        if (r.modeled) {
+            const std::uint64_t svc =
+                emp_step(st, r.d.page1 - 1, dec_op(r.d.bits), svc_ps, program_ps);
+            m = tail_compose(m, TailMap{svc, r.d.issue + svc});
+        }
+    }
+    return m;
+}
+
+__global__ __launch_bounds__(kEmpThreads) void k_emp_map(KArgs a, const hbf_record32* rec,
+                                                         std::size_t n, std::uint64_t base_ps,
+                                                         const BState* tile_in,
+                                                         const std::uint64_t* svc_ps,
+                                                         std::uint64_t program_ps,
+                                                         TailMap* tiles)
+{
+    extern __shared__ std::uint64_t fence[];
+    __shared__ Burst buf[kEmpThreads];
+    __shared__ TailMap mbuf[kEmpThreads];
+    emp_load_fences(a, fence);
+    __syncthreads();
+    const std::size_t begin = static_cast<std::size_t>(blockIdx.x) * kEmpTile + threadIdx.x * kEmpPer;
+    std::uint64_t before = 0;
+    const BState st = emp_thread_state(a, fence, rec, n, begin, base_ps, tile_in[blockIdx.x], buf,
+                                       before);
+    const TailMap m = emp_thread_map(a, fence, rec, n, begin, base_ps, st, svc_ps, program_ps);
+    const TailMap incl = block_scan_incl(m, mbuf, tail_compose);
+    if (threadIdx.x == kEmpThreads - 1) {
+        tiles[blockIdx.x] = incl;
+    }
+}
+
+// One block: the tail before every tile and after the last.
+__global__ __launch_bounds__(kEmpThreads) void k_emp_tail_carry(const TailMap* tiles,
+                                                                std::size_t ntiles,
+                                                                std::uint64_t tail0,
+                                                                std::uint64_t* tile_tail,
+                                                                std::uint64_t* final_tail)
+{
+    __shared__ TailMap buf[kEmpThreads];
+    const std::size_t per = (ntiles + kEmpThreads - 1) / kEmpThreads;
+    const std::size_t b = threadIdx.x * per;
+    const std::size_t e = b + per < ntiles ? b + per : ntiles;
+    TailMap m{0, 0};
+    for (std::size_t t = b; t < e; ++t) {
+        m = tail_compose(m, tiles[t]);
+    }
+    const TailMap incl = block_scan_incl(m, buf, tail_compose);
+    std::uint64_t g = tail0;
+    if (threadIdx.x > 0) {
+        const TailMap ex = buf[threadIdx.x - 1];
+        g = umax64(tail0 + ex.A, ex.B);
+    }
+    for (std::size_t t = b; t < e; ++t) {
+        tile_tail[t] = g;
+        g = umax64(g + tiles[t].A, tiles[t].B);
+    }
+    if (threadIdx.x == kEmpThreads - 1) {
+        *final_tail = umax64(tail0 + incl.A, incl.B);
+    }
+}
+
+__global__ __launch_bounds__(kEmpThreads) void k_emp_apply(
+    KArgs a, const hbf_record32* rec, std::size_t n, std::uint64_t base_ps, const BState* tile_in,
+    const std::uint64_t* tile_seq, const std::uint64_t* tile_tail, const std::uint64_t* svc_ps,
+    std::uint64_t program_ps, std::uint64_t* completion, std::uint8_t* status, DevReport* tile_rep)
+{
+    extern __shared__ std::uint64_t fence[];
+    __shared__ Burst buf[kEmpThreads];
+    __shared__ TailMap mbuf[kEmpThreads];
+    emp_load_fences(a, fence);
+    __syncthreads();
+    const std::size_t begin = static_cast<std::size_t>(blockIdx.x) * kEmpTile + threadIdx.x * kEmpPer;
+    std::uint64_t before = 0;
+    BState st = emp_thread_state(a, fence, rec, n, begin, base_ps, tile_in[blockIdx.x], buf,
+                                 before);
+    const TailMap mine = emp_thread_map(a, fence, rec, n, begin, base_ps, st, svc_ps, program_ps);
+    block_scan_incl(mine, mbuf, tail_compose);
+    std::uint64_t tail = tile_tail[blockIdx.x];
+    if (threadIdx.x > 0) {
+        const TailMap ex = mbuf[threadIdx.x - 1];
+        tail = umax64(tail + ex.A, ex.B);
+    }
+    std::uint64_t seq = tile_seq[blockIdx.x] + before;
+    unsigned long long v[14] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    RangeCache rc = empty_cache();
+    for (std::uint32_t k = 0; k < kEmpPer; ++k) {
+        const std::size_t i = begin + k;
+        const EmpRec r = emp_decode(a, fence, rc, rec, n, i, base_ps);
+        if (!r.valid) {
+            break;
+        }
+        ++v[R_RECORDS];
+        std::uint8_t sb = static_cast<std::uint8_t>(r.d.cls);
+        std::uint64_t done;
+        if (r.d.cls == kClsBypass) {
+            done = r.d.issue;
+            ++v[R_BYPASS];
+        } else if (r.d.cls == kClsUnsupported) {
+            done = ~0ull;
+            ++v[R_UNSUPPORTED];
+        } else {
+            const std::uint32_t op = dec_op(r.d.bits);
+            const std::uint64_t page = r.d.page1 - 1;
+            if (a.hybrid) {
+                const std::uint64_t key = (page << a.page_shift) ^
+                                          (static_cast<std::uint64_t>(r.d.range_id) << 32) ^ op;
+                if (seq < a.hybrid_warmup ||
+                    (a.hybrid_threshold != 0 && mix64(seq ^ key) <= a.hybrid_threshold)) {
+                    sb |= 8u;
+                    ++v[R_HYBRID];
+                }
+            }
+            ++seq;
+            const std::uint64_t svc = emp_step(st, page, op, svc_ps, program_ps);
+            done = umax64(tail, r.d.issue) + svc;
+            tail = done;
+            ++v[R_MODELED];
+            ++v[op == 0 ? R_READS : R_WRITES];
+            v[R_MAKESPAN] = umax64(v[R_MAKESPAN], done);
+            const std::uint64_t lat = done - r.d.issue;
+            const unsigned long long lo = v[R_LAT_LO] + lat;
+            v[R_LAT_HI] += lo < v[R_LAT_LO] ? 1u : 0u;
+            v[R_LAT_LO] = lo;
+            v[R_LAT_MAX] = umax64(v[R_LAT_MAX], lat);
+            v[R_SERVICE] += svc;
+        }
+        completion[i] = done;
+        if (status != nullptr) {
+            status[i] = sb;
+        }
+    }
+    // block report
+    __shared__ unsigned long long part[kEmpThreads * 14];
+    for (int k = 0; k < 14; ++k) {
+        part[threadIdx.x * 14 + k] = v[k];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        DevReport out{};
+        for (int t = 0; t < kEmpThreads; ++t) {
+            const unsigned long long* q = part + t * 14;
+            for (int k = 0; k < 14; ++k) {
+                if (k == R_MAKESPAN || k == R_LAT_MAX) {
+                    out.v[k] = umax64(out.v[k], q[k]);
+                } else if (k == R_LAT_LO) {
+                    const unsigned long long s2 = out.v[k] + q[k];
+                    out.v[R_LAT_HI] += s2 < out.v[k] ? 1u : 0u;
+                    out.v[k] = s2;
+                } else {
+                    out.v[k] += q[k];
+                }
+            }
+        }
+        tile_rep[blockIdx.x] = out;
+    }
+}
+
 std::size_t lds_summary(const KArgs& a)
 {
     return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 12ull * a.Rp;
@@ -1586,6 +2021,208 @@ std::uint32_t auto_tile(std::size_t n)
         t >>= 1;
     }
     return t;
+}
+
+// Empirical curve on the host (hbf_device.cuh:959-1029), for the per-run
+// service table.
+std::uint64_t sat_mul(std::uint64_t a, std::uint32_t b)
+{
+    return b != 0 && a > ~0ull / b ? ~0ull : a * b;
+}
+
+std::uint64_t sat_add_host(std::uint64_t a, std::uint64_t b)
+{
+    return b > ~0ull - a ? ~0ull : a + b;
+}
+
+std::uint64_t ceiling_scaled_delta(std::uint64_t delta, std::uint32_t offset, std::uint32_t span)
+{
+    if (delta == 0 || offset == 0) {
+        return 0;
+    }
+    if (span == 0) {
+        return ~0ull;
+    }
+    const std::uint64_t q = delta / span, r = delta % span;
+    return sat_add_host(sat_mul(q, offset), (r * offset + span - 1) / span);
+}
+
+std::uint64_t emp_cumulative(const engine_config& c, std::uint32_t run)
+{
+    if (run == 0) {
+        return 0;
+    }
+    const std::uint32_t count = 6;
+    std::uint32_t right = 0;
+    while (right < count && run > c.emp_pages[right]) {
+        ++right;
+    }
+    if (right == count) {
+        right = count - 1;
+    }
+    std::uint32_t left_pages = 0;
+    std::uint64_t left_ns = 0;
+    if (right != 0) {
+        left_pages = c.emp_pages[right - 1];
+        left_ns = c.emp_cum_ns[right - 1];
+    }
+    if (run > c.emp_pages[right]) {
+        left_pages = c.emp_pages[count - 2];
+        left_ns = c.emp_cum_ns[count - 2];
+        right = count - 1;
+    }
+    if (c.emp_pages[right] <= left_pages || c.emp_cum_ns[right] < left_ns || run < left_pages) {
+        return ~0ull;
+    }
+    return sat_add_host(left_ns, ceiling_scaled_delta(c.emp_cum_ns[right] - left_ns,
+                                                      run - left_pages,
+                                                      c.emp_pages[right] - left_pages));
+}
+
+bool emp_control_valid(const engine_config& c)
+{
+    if (c.emp_program_ns == 0) {
+        return false;
+    }
+    for (int i = 0; i < 6; ++i) {
+        if (c.emp_pages[i] == 0 || c.emp_cum_ns[i] == 0 ||
+            (i != 0 && (c.emp_pages[i] <= c.emp_pages[i - 1] ||
+                        c.emp_cum_ns[i] <= c.emp_cum_ns[i - 1]))) {
+            return false;
+        }
+    }
+    return c.emp_pages[5] <= kRunCap;
+}
+
+// Service (ps) of a read at burst run 0..1023; products wrap like the CPU
+// restatement's.
+std::vector<std::uint64_t> emp_service_table(const engine_config& c)
+{
+    std::vector<std::uint64_t> t(kRunCap + 1, 0);
+    for (std::uint32_t run = 1; run <= kRunCap; ++run) {
+        const std::uint64_t cur = emp_cumulative(c, run), prev = emp_cumulative(c, run - 1);
+        const std::uint64_t ns = cur < prev ? ~0ull : cur - prev;
+        t[run] = ns * 1000ull;
+    }
+    return t;
+}
+
+int run_empirical(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_t* d_comp,
+                  std::uint8_t* d_status, std::uint64_t base_ps, hipStream_t stream,
+                  hbfsim_amd_report* out)
+{
+    const engine_config& c = e->cfg;
+    if (c.page_shift != 12 || !emp_control_valid(c)) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    const KArgs& a = e->args;
+    const std::size_t ntiles = (n + kEmpTile - 1) / kEmpTile;
+    const std::vector<std::uint64_t> table = emp_service_table(c);
+    std::uint64_t* d_svc = nullptr;
+    Burst* d_bt = nullptr;
+    BState* d_in = nullptr;
+    std::uint64_t* d_tseq = nullptr;
+    TailMap* d_maps = nullptr;
+    std::uint64_t* d_tail = nullptr;
+    DevReport* d_trep = nullptr;
+    BState* d_final = nullptr;
+    std::uint64_t* d_fin = nullptr;  // [0] sequence, [1] tail
+    auto release = [&]() {
+        hfree(d_svc); hfree(d_bt); hfree(d_in); hfree(d_tseq); hfree(d_maps); hfree(d_tail);
+        hfree(d_trep); hfree(d_final); hfree(d_fin);
+    };
+    hipError_t err = halloc(d_svc, table.size());
+    if (err == hipSuccess) err = halloc(d_bt, ntiles);
+    if (err == hipSuccess) err = halloc(d_in, ntiles);
+    if (err == hipSuccess) err = halloc(d_tseq, ntiles);
+    if (err == hipSuccess) err = halloc(d_maps, ntiles);
+    if (err == hipSuccess) err = halloc(d_tail, ntiles);
+    if (err == hipSuccess) err = halloc(d_trep, ntiles);
+    if (err == hipSuccess) err = halloc(d_final, 1);
+    if (err == hipSuccess) err = halloc(d_fin, 2);
+    std::uint64_t seq0 = 0, tail0 = 0;
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(d_svc, table.data(), table.size() * 8, hipMemcpyHostToDevice, stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(&seq0, e->d_seq, 8, hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(&tail0, e->d_cbusy, 8, hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) {
+        release();
+        return HBFSIM_CUDA_ERROR;
+    }
+    BState init{};
+    {
+        const std::uint64_t packed = e->burst;
+        const std::uint64_t p1 = packed >> 11;
+        init.valid = (packed != 0 && (packed & kRunCap) != 0 && p1 != 0) ? 1u : 0u;
+        init.page = p1 == 0 ? 0 : p1 - 1;
+        init.op = static_cast<std::uint32_t>((packed >> 10) & 1u);
+        init.run = packed & kRunCap;
+    }
+    const std::size_t lds = 8ull * a.r_nfence;
+    const dim3 grid(static_cast<unsigned>(ntiles));
+    (void)hipEventRecord(e->ev[0], stream);
+    hipLaunchKernelGGL(k_emp_burst, grid, dim3(kEmpThreads), lds, stream, a, d_rec, n, base_ps,
+                       d_bt);
+    hipLaunchKernelGGL(k_emp_burst_carry, dim3(1), dim3(kEmpThreads), 0, stream,
+                       static_cast<const Burst*>(d_bt), ntiles, init, seq0, d_in, d_tseq, d_final,
+                       d_fin);
+    (void)hipEventRecord(e->ev[1], stream);
+    hipLaunchKernelGGL(k_emp_map, grid, dim3(kEmpThreads), lds, stream, a, d_rec, n, base_ps,
+                       static_cast<const BState*>(d_in), static_cast<const std::uint64_t*>(d_svc),
+                       c.emp_program_ns * 1000ull, d_maps);
+    hipLaunchKernelGGL(k_emp_tail_carry, dim3(1), dim3(kEmpThreads), 0, stream,
+                       static_cast<const TailMap*>(d_maps), ntiles, tail0, d_tail, d_fin + 1);
+    (void)hipEventRecord(e->ev[2], stream);
+    hipLaunchKernelGGL(k_emp_apply, grid, dim3(kEmpThreads), lds, stream, a, d_rec, n, base_ps,
+                       static_cast<const BState*>(d_in), static_cast<const std::uint64_t*>(d_tseq),
+                       static_cast<const std::uint64_t*>(d_tail),
+                       static_cast<const std::uint64_t*>(d_svc), c.emp_program_ns * 1000ull,
+                       d_comp, d_status, d_trep);
+    hipLaunchKernelGGL(k_report, dim3(1), dim3(256), 0, stream,
+                       static_cast<const DevReport*>(d_trep), ntiles, e->d_rep);
+    (void)hipEventRecord(e->ev[3], stream);
+    BState fin{};
+    std::uint64_t fin2[2] = {0, 0};
+    err = hipGetLastError();
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(e->h_rep, e->d_rep, sizeof(DevReport), hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(&fin, d_final, sizeof(BState), hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(fin2, d_fin, 16, hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(e->d_seq, d_fin, 8, hipMemcpyDeviceToDevice, stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(e->d_cbusy, d_fin + 1, 8, hipMemcpyDeviceToDevice, stream);
+    std::uint64_t tot = 0;
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(&tot, e->d_ctot, 8, hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err == hipSuccess) {
+        tot += e->h_rep->v[R_SERVICE];
+        err = hipMemcpyAsync(e->d_ctot, &tot, 8, hipMemcpyHostToDevice, stream);
+    }
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    release();
+    if (err != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    if (fin.valid) {
+        e->burst = ((fin.page + 1) << 11) | (static_cast<std::uint64_t>(fin.op) << 10) | fin.run;
+    }
+    for (int k = 0; k < 3; ++k) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, e->ev[k], e->ev[k + 1]) == hipSuccess) {
+            e->last_ms[k] = ms;
+        }
+    }
+    if (out != nullptr) {
+        std::memcpy(out, e->h_rep, sizeof(*out));
+    }
+    return HBFSIM_OK;
 }
 
 }  // namespace
@@ -1761,7 +2398,10 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         (reinterpret_cast<std::uintptr_t>(d_comp) & 7u) != 0) {
         return HBFSIM_INVALID_ARGUMENT;
     }
-    if (e->cfg.model != HBFSIM_AMD_MODEL_HBF || e->cfg.slots > 1) {
+    if (e->cfg.model != HBFSIM_AMD_MODEL_HBF && e->cfg.model != HBFSIM_AMD_MODEL_EMPIRICAL) {
+        return HBFSIM_UNSUPPORTED;
+    }
+    if (e->cfg.model == HBFSIM_AMD_MODEL_HBF && e->cfg.slots > 1) {
         return HBFSIM_UNSUPPORTED;
     }
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
@@ -1773,6 +2413,12 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         if (st != HBFSIM_OK) {
             return st;
         }
+    }
+    if (e->cfg.model == HBFSIM_AMD_MODEL_EMPIRICAL) {
+        if (refresh_records) {
+            return HBFSIM_UNSUPPORTED;
+        }
+        return run_empirical(e, d_rec, n, d_comp, d_status, base_ps, stream, out);
     }
     KArgs a = e->args;
     a.tile = e->cfg.tile != 0 ? e->cfg.tile : auto_tile(n);
