@@ -102,6 +102,7 @@ struct KArgs {
     std::uint64_t xfer_pow2[33];    // transfer ps for 2^k bytes
     std::uint64_t media_pages;      // device capacity in pages
     std::uint32_t tile;
+    std::uint32_t ext_hits;         // page-buffer hits given per record (K = 2)
 };
 
 // Record operations: 0 read, 1 write, and 2 refresh of media page `addr`
@@ -677,10 +678,11 @@ __device__ __forceinline__ void load_fences(const KArgs& a, std::uint64_t* fence
 // class), the (max,+) map of the records after it, and the last page; per
 // channel the map of all its records.  Pages are stored as page + 1 in 32
 // bits (capacity / page_bytes < 2^32 is checked on the host).
-template <bool kRefresh>
+template <bool kRefresh, bool kHits>
 __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
-                                                ChanSum* csum, std::uint64_t* tile_count)
+                                                ChanSum* csum, std::uint64_t* tile_count,
+                                                const std::uint8_t* hits)
 {
     extern __shared__ std::uint64_t sm[];
     std::uint64_t* fence = sm;
@@ -724,13 +726,14 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
         const bool valid = i < end;
         const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
         const bool m = valid && d.cls == kClsModeled;
+        const bool hbit = kHits && valid && hits[i] != 0;
         const std::uint64_t active = __ballot(m);
         modeled += __popcll(active);
         if (active == 0) {
             continue;
         }
         const std::uint64_t xfer = lane_xfer(a, d, m, active);
-        if (run_step(a, d, active, lane)) {
+        if (!kHits && run_step(a, d, active, lane)) {
             const std::uint64_t W = run_channel_max(d, xfer, lane);
             if (lane == 63) {
                 const std::uint32_t pkey = d.plane;
@@ -776,7 +779,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
         if (gp.pred < 0) {
             prev1 = last_page;
         }
-        const bool hit = a.slots != 0 && m && prev1 == page1;
+        const bool hit = kHits ? (m && hbit) : (a.slots != 0 && m && prev1 == page1);
         const std::uint64_t svc = plane_service(a, d.bits, hit);
         std::uint64_t Ap = 0, Bp = 0;
         if (m && !tfirst) {
@@ -789,8 +792,10 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
         const std::uint32_t l1 =
             static_cast<std::uint32_t>(__shfl(static_cast<int>(page1), gp.leader));
         const std::uint64_t li = shfl64(d.issue, gp.leader);
+        // the leader's class; with given hits, bit 3 carries its hit
+        const std::uint32_t lbits = kHits && hit ? (d.bits | 8u) : d.bits;
         const std::uint32_t lc =
-            static_cast<std::uint32_t>(__shfl(static_cast<int>(d.bits), gp.leader));
+            static_cast<std::uint32_t>(__shfl(static_cast<int>(lbits), gp.leader));
         if (m && lane == gp.last) {
             if (!has) {
                 p_f1[pkey] = l1;
@@ -857,7 +862,7 @@ __device__ __forceinline__ PlaneSum plane_compose(const KArgs& a, const PlaneSum
         return s2;
     }
     PlaneSum r = s1;
-    const bool hit = a.slots != 0 && s2.fpage1 == s1.lpage1;
+    const bool hit = a.ext_hits ? (s2.fcls & 8u) != 0 : (a.slots != 0 && s2.fpage1 == s1.lpage1);
     const std::uint64_t svc = plane_service(a, s2.fcls, hit);
     // rest1, then the later first record (svc, issue + svc), then rest2; A
     // is also the service total of the records after the first
@@ -876,7 +881,7 @@ __device__ __forceinline__ std::uint64_t plane_apply(const KArgs& a, const Plane
     if (s.fpage1 == 0) {
         return 0;
     }
-    const bool hit = a.slots != 0 && tag1 == s.fpage1;
+    const bool hit = a.ext_hits ? (s.fcls & 8u) != 0 : (a.slots != 0 && tag1 == s.fpage1);
     const std::uint64_t svc = plane_service(a, s.fcls, hit);
     if (a.contention) {
         const std::uint64_t b = umax64(busy, s.fissue) + svc;
@@ -1050,13 +1055,13 @@ __device__ __forceinline__ std::uint64_t wave_max(std::uint64_t v)
     return v;
 }
 
-template <bool kRefresh>
+template <bool kRefresh, bool kHits>
 __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, std::size_t n,
                                               std::uint64_t base_ps, const PlaneCarry* pcarry,
                                               const std::uint64_t* ccarry,
                                               const std::uint64_t* tile_seq,
                                               std::uint64_t* completion, std::uint8_t* status,
-                                              DevReport* tile_rep)
+                                              DevReport* tile_rep, const std::uint8_t* hits)
 {
     extern __shared__ std::uint64_t sm[];
     std::uint64_t* fence = sm;
@@ -1094,10 +1099,11 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
         const bool valid = i < end;
         const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
         const bool m = valid && d.cls == kClsModeled;
+        const bool hbit = kHits && valid && hits[i] != 0;
         const std::uint64_t active = __ballot(m);
         std::uint8_t st = static_cast<std::uint8_t>(d.cls);
         std::uint64_t done = 0;
-        if (active != 0 && run_step(a, d, active, lane)) {
+        if (!kHits && active != 0 && run_step(a, d, active, lane)) {
             const std::uint64_t xfer = lane_xfer(a, d, m, active);
             const std::uint64_t W = run_channel_max(d, xfer, lane);
             const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
@@ -1169,7 +1175,7 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
             if (gp.pred < 0) {
                 prev1 = tag;
             }
-            const bool hit = a.slots != 0 && m && prev1 == page1;
+            const bool hit = kHits ? (m && hbit) : (a.slots != 0 && m && prev1 == page1);
             const std::uint64_t svc = plane_service(a, d.bits, hit);
             std::uint64_t Ap = m ? svc : 0ull;
             std::uint64_t Bp = m ? d.issue + svc : 0ull;
@@ -2002,6 +2008,254 @@ __global__ __launch_bounds__(kEmpThreads) void k_emp_apply(
     }
 }
 
+// ---- two page registers per plane (device_coalescer.cpp:134-168) ---------
+// A miss fills the first empty slot, else slot 0.  Slot 1 is therefore
+// written once and then kept, and from then on a read hits when its page is
+// slot 1's or the last page other than slot 1's seen on the plane.  Hits do
+// not depend on timing, so they come from their own scans and the timing
+// pipeline consumes them (kHits):
+//   k_k2_first   per plane, the first record (optionally: whose page differs
+//                from a given one) -- the fill events before both slots hold
+//                a page; only run while some plane has an empty slot;
+//   k_k2_last    per tile and plane, the last page other than slot 1's;
+//   k_k2_up/mid/down  the carry of that page across tiles;
+//   k_k2_hits    one hit byte per record.
+struct K2Plane {
+    std::uint64_t start3;  // first record index with both slots held
+    std::uint64_t miss1, miss2;  // fill events before that (or ~0)
+    std::uint32_t t1;      // slot 1's page + 1 from start3 on (0: never)
+    std::uint32_t l_init;  // last page other than t1 before the run
+};
+
+constexpr std::uint32_t kK2Chunk = 16384;
+
+__global__ __launch_bounds__(256) void k_k2_first(KArgs a, const hbf_record32* rec,
+                                                  std::size_t n, std::uint64_t base_ps,
+                                                  const std::uint32_t* want,
+                                                  const std::uint32_t* differ,
+                                                  unsigned long long* first)
+{
+    extern __shared__ std::uint64_t sm[];
+    std::uint64_t* fence = sm;
+    unsigned long long* lmin = reinterpret_cast<unsigned long long*>(fence + a.r_nfence);
+    for (std::uint32_t j = threadIdx.x; j < a.r_nfence; j += blockDim.x) {
+        fence[j] = a.r_base[static_cast<std::size_t>(j) * a.r_stride];
+    }
+    for (std::uint32_t r = threadIdx.x; r < a.Rp; r += blockDim.x) {
+        lmin[r] = ~0ull;
+    }
+    __syncthreads();
+    const std::size_t begin = static_cast<std::size_t>(blockIdx.x) * kK2Chunk;
+    const std::size_t end = begin + kK2Chunk < n ? begin + kK2Chunk : n;
+    RangeCache rc = empty_cache();
+    for (std::size_t i = begin + threadIdx.x; i < end; i += blockDim.x) {
+        uint4 x, y;
+        load_record(rec, i, x, y);
+        const Dec d = decode<false>(a, fence, rc, x, y, base_ps);
+        if (d.cls != kClsModeled || !want[d.plane]) {
+            continue;
+        }
+        const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
+        if (differ[d.plane] != 0 && page1 == differ[d.plane]) {
+            continue;
+        }
+        atomicMin(&lmin[d.plane], static_cast<unsigned long long>(i));
+    }
+    __syncthreads();
+    for (std::uint32_t r = threadIdx.x; r < a.Rp; r += blockDim.x) {
+        if (lmin[r] != ~0ull) {
+            atomicMin(&first[r], lmin[r]);
+        }
+    }
+}
+
+// Page + 1 of record idx[r] for every plane r (0 when none).
+__global__ __launch_bounds__(256) void k_k2_page(KArgs a, const hbf_record32* rec, std::size_t n,
+                                                 std::uint64_t base_ps,
+                                                 const unsigned long long* idx,
+                                                 std::uint32_t* page1)
+{
+    extern __shared__ std::uint64_t fence[];
+    for (std::uint32_t j = threadIdx.x; j < a.r_nfence; j += blockDim.x) {
+        fence[j] = a.r_base[static_cast<std::size_t>(j) * a.r_stride];
+    }
+    __syncthreads();
+    for (std::uint32_t r = threadIdx.x; r < a.Rp; r += blockDim.x) {
+        std::uint32_t v = 0;
+        if (idx[r] < n) {
+            RangeCache rc = empty_cache();
+            uint4 x, y;
+            load_record(rec, idx[r], x, y);
+            v = static_cast<std::uint32_t>(decode<false>(a, fence, rc, x, y, base_ps).page1);
+        }
+        page1[r] = v;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_k2_last(KArgs a, const hbf_record32* rec, std::size_t n,
+                                                std::uint64_t base_ps, const K2Plane* kp,
+                                                std::uint32_t* tile_last)
+{
+    extern __shared__ std::uint64_t sm[];
+    std::uint64_t* fence = sm;
+    std::uint32_t* t1 = reinterpret_cast<std::uint32_t*>(fence + a.r_nfence);
+    std::uint32_t* last = t1 + a.Rp;
+    const int lane = threadIdx.x;
+    load_fences(a, fence, lane);
+    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
+        t1[r] = kp[r].t1;
+        last[r] = 0;
+    }
+    __syncthreads();
+    const std::size_t tile = blockIdx.x;
+    const std::size_t begin = tile * a.tile;
+    const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
+    RangeCache rc = empty_cache();
+    for (std::size_t s = begin; s < end; s += kWave) {
+        const std::size_t i = s + lane;
+        const bool valid = i < end;
+        Dec d = invalid_dec();
+        if (valid) {
+            uint4 x, y;
+            load_record(rec, i, x, y);
+            d = decode<false>(a, fence, rc, x, y, base_ps);
+        }
+        const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
+        const bool nt = valid && d.cls == kClsModeled && page1 != t1[d.plane];
+        const std::uint64_t active = __ballot(nt);
+        if (active == 0) {
+            continue;
+        }
+        const Group g = group_by(nt ? d.plane : 0u, a.pbits, nt, active, lane);
+        if (nt && lane == g.last) {
+            last[d.plane] = page1;
+        }
+    }
+    __syncthreads();
+    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
+        tile_last[tile * a.Rp + r] = last[r];
+    }
+}
+
+// Level 1: the last nonzero page of each (group of kGroup tiles, plane).
+__global__ __launch_bounds__(256) void k_k2_up(KArgs a, std::size_t ntiles, std::size_t ngroups,
+                                               const std::uint32_t* tile_last,
+                                               std::uint32_t* group_last)
+{
+    const std::size_t t = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x;
+    if (t >= ngroups * a.Rp) {
+        return;
+    }
+    const std::size_t g = t / a.Rp, r = t % a.Rp;
+    std::uint32_t v = 0;
+    const std::size_t e = (g + 1) * kGroup < ntiles ? (g + 1) * kGroup : ntiles;
+    for (std::size_t k = g * kGroup; k < e; ++k) {
+        const std::uint32_t x = tile_last[k * a.Rp + r];
+        v = x != 0 ? x : v;
+    }
+    group_last[g * a.Rp + r] = v;
+}
+
+// Level 2: per plane, the page before each group, and after the last.
+__global__ __launch_bounds__(256) void k_k2_mid(KArgs a, std::size_t ngroups, const K2Plane* kp,
+                                                const std::uint32_t* group_last,
+                                                std::uint32_t* group_in, std::uint32_t* final_last)
+{
+    const std::uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= a.Rp) {
+        return;
+    }
+    std::uint32_t v = kp[r].l_init;
+    for (std::size_t g = 0; g < ngroups; ++g) {
+        group_in[g * a.Rp + r] = v;
+        const std::uint32_t x = group_last[g * a.Rp + r];
+        v = x != 0 ? x : v;
+    }
+    final_last[r] = v;
+}
+
+// Level 3: the page before each tile.
+__global__ __launch_bounds__(256) void k_k2_down(KArgs a, std::size_t ntiles, std::size_t ngroups,
+                                                 const std::uint32_t* tile_last,
+                                                 const std::uint32_t* group_in,
+                                                 std::uint32_t* tile_in)
+{
+    const std::size_t t = blockIdx.x * static_cast<std::size_t>(blockDim.x) + threadIdx.x;
+    if (t >= ngroups * a.Rp) {
+        return;
+    }
+    const std::size_t g = t / a.Rp, r = t % a.Rp;
+    std::uint32_t v = group_in[g * a.Rp + r];
+    const std::size_t e = (g + 1) * kGroup < ntiles ? (g + 1) * kGroup : ntiles;
+    for (std::size_t k = g * kGroup; k < e; ++k) {
+        tile_in[k * a.Rp + r] = v;
+        const std::uint32_t x = tile_last[k * a.Rp + r];
+        v = x != 0 ? x : v;
+    }
+}
+
+__global__ __launch_bounds__(64) void k_k2_hits(KArgs a, const hbf_record32* rec, std::size_t n,
+                                                std::uint64_t base_ps, const K2Plane* kp,
+                                                const std::uint32_t* tile_in, std::uint8_t* hits)
+{
+    extern __shared__ std::uint64_t sm[];
+    std::uint64_t* fence = sm;
+    std::uint32_t* t1 = reinterpret_cast<std::uint32_t*>(fence + a.r_nfence);
+    std::uint32_t* last = t1 + a.Rp;
+    const int lane = threadIdx.x;
+    const std::size_t tile = blockIdx.x;
+    load_fences(a, fence, lane);
+    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
+        t1[r] = kp[r].t1;
+        last[r] = tile_in[tile * a.Rp + r];
+    }
+    __syncthreads();
+    const std::size_t begin = tile * a.tile;
+    const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
+    RangeCache rc = empty_cache();
+    for (std::size_t s = begin; s < end; s += kWave) {
+        const std::size_t i = s + lane;
+        const bool valid = i < end;
+        Dec d = invalid_dec();
+        if (valid) {
+            uint4 x, y;
+            load_record(rec, i, x, y);
+            d = decode<false>(a, fence, rc, x, y, base_ps);
+        }
+        const bool m = valid && d.cls == kClsModeled;
+        const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
+        const std::uint32_t pt1 = m ? t1[d.plane] : 0u;
+        const bool nt = m && page1 != pt1;
+        const std::uint64_t active = __ballot(nt);
+        bool hit = false;
+        if (active != 0) {
+            const Group g = group_by(nt ? d.plane : 0u, a.pbits, nt, active, lane);
+            std::uint32_t prev1 = static_cast<std::uint32_t>(
+                __shfl(static_cast<int>(page1), g.pred < 0 ? lane : g.pred));
+            if (g.pred < 0) {
+                prev1 = nt ? last[d.plane] : 0u;
+            }
+            hit = nt && prev1 == page1;
+            __syncthreads();  // every lane has read `last` before it changes
+            if (nt && lane == g.last) {
+                last[d.plane] = page1;
+            }
+            __syncthreads();
+        }
+        if (m) {
+            const K2Plane& k = kp[d.plane];
+            if (i < k.start3) {
+                hit = i != k.miss1 && i != k.miss2;
+            } else if (!nt) {
+                hit = true;  // slot 1's page
+            }
+            hits[i] = hit ? 1u : 0u;
+        } else if (valid) {
+            hits[i] = 0;
+        }
+    }
+}
+
 std::size_t lds_summary(const KArgs& a)
 {
     return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 12ull * a.Rp;
@@ -2225,6 +2479,188 @@ int run_empirical(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint
     return HBFSIM_OK;
 }
 
+// Per-record page-buffer hits for two registers per plane, and the tags the
+// run leaves behind (host array [2 * planes]).  d_hits: n bytes.
+int k2_hits(engine* e, const KArgs& a, const hbf_record32* d_rec, std::size_t n,
+            std::uint64_t base_ps, std::size_t ntiles, hipStream_t stream, std::uint8_t* d_hits,
+            std::vector<std::uint64_t>& tags_out)
+{
+    const std::uint32_t rp = a.Rp;
+    std::vector<std::uint64_t> tags(2ull * rp);
+    hipError_t err = hipMemcpyAsync(tags.data(), e->d_ptag, tags.size() * 8,
+                                    hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    std::vector<K2Plane> kp(rp);
+    std::vector<std::uint32_t> want(rp, 0), differ(rp, 0);
+    std::vector<unsigned long long> idx_a(rp, ~0ull), idx_b(rp, ~0ull);
+    std::vector<std::uint32_t> page_a(rp, 0), page_b(rp, 0);
+    bool need_a = false;
+    for (std::uint32_t r = 0; r < rp; ++r) {
+        const std::uint64_t t0 = tags[2 * r], t1 = tags[2 * r + 1];
+        need_a = need_a || (t0 == 0 && t1 == 0);
+    }
+    std::uint32_t* d_want = nullptr;
+    std::uint32_t* d_differ = nullptr;
+    unsigned long long* d_first = nullptr;
+    std::uint32_t* d_page = nullptr;
+    K2Plane* d_kp = nullptr;
+    const std::size_t ngroups = (ntiles + kGroup - 1) / kGroup;
+    std::uint32_t* d_tlast = nullptr;
+    std::uint32_t* d_tin = nullptr;
+    std::uint32_t* d_glast = nullptr;
+    std::uint32_t* d_gin = nullptr;
+    std::uint32_t* d_final = nullptr;
+    auto release = [&]() {
+        hfree(d_want); hfree(d_differ); hfree(d_first); hfree(d_page); hfree(d_kp);
+        hfree(d_tlast); hfree(d_tin); hfree(d_glast); hfree(d_gin); hfree(d_final);
+    };
+    err = halloc(d_want, rp);
+    if (err == hipSuccess) err = halloc(d_differ, rp);
+    if (err == hipSuccess) err = halloc(d_first, rp);
+    if (err == hipSuccess) err = halloc(d_page, rp);
+    if (err == hipSuccess) err = halloc(d_kp, rp);
+    if (err == hipSuccess) err = halloc(d_tlast, ntiles * rp);
+    if (err == hipSuccess) err = halloc(d_tin, ntiles * rp);
+    if (err == hipSuccess) err = halloc(d_glast, ngroups * rp);
+    if (err == hipSuccess) err = halloc(d_gin, ngroups * rp);
+    if (err == hipSuccess) err = halloc(d_final, rp);
+    if (err != hipSuccess) {
+        release();
+        return HBFSIM_CUDA_ERROR;
+    }
+    const unsigned first_blocks = static_cast<unsigned>((n + kK2Chunk - 1) / kK2Chunk);
+    const std::size_t lds_first = 8ull * a.r_nfence + 8ull * rp;
+    // pass A: the first record of every plane with both slots empty
+    auto first_pass = [&](std::vector<unsigned long long>& idx,
+                          std::vector<std::uint32_t>& page) -> hipError_t {
+        std::vector<unsigned long long> init(rp, ~0ull);
+        hipError_t e2 = hipMemcpyAsync(d_want, want.data(), rp * 4, hipMemcpyHostToDevice, stream);
+        if (e2 == hipSuccess)
+            e2 = hipMemcpyAsync(d_differ, differ.data(), rp * 4, hipMemcpyHostToDevice, stream);
+        if (e2 == hipSuccess)
+            e2 = hipMemcpyAsync(d_first, init.data(), rp * 8, hipMemcpyHostToDevice, stream);
+        if (e2 != hipSuccess) return e2;
+        hipLaunchKernelGGL(k_k2_first, dim3(first_blocks), dim3(256), lds_first, stream, a, d_rec,
+                           n, base_ps, static_cast<const std::uint32_t*>(d_want),
+                           static_cast<const std::uint32_t*>(d_differ), d_first);
+        hipLaunchKernelGGL(k_k2_page, dim3(1), dim3(256), 8ull * a.r_nfence, stream, a, d_rec, n,
+                           base_ps, static_cast<const unsigned long long*>(d_first), d_page);
+        e2 = hipGetLastError();
+        if (e2 == hipSuccess)
+            e2 = hipMemcpyAsync(idx.data(), d_first, rp * 8, hipMemcpyDeviceToHost, stream);
+        if (e2 == hipSuccess)
+            e2 = hipMemcpyAsync(page.data(), d_page, rp * 4, hipMemcpyDeviceToHost, stream);
+        if (e2 == hipSuccess) e2 = hipStreamSynchronize(stream);
+        return e2;
+    };
+    if (need_a) {
+        for (std::uint32_t r = 0; r < rp; ++r) {
+            want[r] = tags[2 * r] == 0 && tags[2 * r + 1] == 0;
+            differ[r] = 0;
+        }
+        err = first_pass(idx_a, page_a);
+    }
+    // pass B: the first record whose page differs from the one slot held
+    if (err == hipSuccess) {
+        bool any = false;
+        for (std::uint32_t r = 0; r < rp; ++r) {
+            const std::uint64_t t0 = tags[2 * r], t1 = tags[2 * r + 1];
+            want[r] = 0;
+            differ[r] = 0;
+            if (t0 != 0 && t1 == 0) {
+                want[r] = 1;
+                differ[r] = static_cast<std::uint32_t>(t0);
+            } else if (t0 == 0 && t1 != 0) {
+                want[r] = 1;
+                differ[r] = static_cast<std::uint32_t>(t1);
+            } else if (t0 == 0 && t1 == 0 && idx_a[r] < n) {
+                want[r] = 1;
+                differ[r] = page_a[r];
+            }
+            any = any || want[r];
+        }
+        if (any) {
+            err = first_pass(idx_b, page_b);
+        }
+    }
+    if (err != hipSuccess) {
+        release();
+        return HBFSIM_CUDA_ERROR;
+    }
+    for (std::uint32_t r = 0; r < rp; ++r) {
+        const std::uint64_t t0 = tags[2 * r], t1 = tags[2 * r + 1];
+        K2Plane& k = kp[r];
+        k.start3 = ~0ull;
+        k.miss1 = k.miss2 = ~0ull;
+        k.t1 = 0;
+        k.l_init = 0;
+        const bool b = idx_b[r] < n;
+        if (t0 != 0 && t1 != 0) {
+            k.start3 = 0;
+            k.t1 = static_cast<std::uint32_t>(t1);
+            k.l_init = static_cast<std::uint32_t>(t0);
+        } else if (t0 != 0) {
+            k.l_init = static_cast<std::uint32_t>(t0);
+            if (b) {
+                k.miss2 = idx_b[r];
+                k.start3 = idx_b[r] + 1;
+                k.t1 = page_b[r];
+            }
+        } else if (t1 != 0) {
+            k.t1 = static_cast<std::uint32_t>(t1);
+            if (b) {
+                k.miss1 = idx_b[r];
+                k.start3 = idx_b[r] + 1;
+            }
+        } else if (idx_a[r] < n) {
+            k.miss1 = idx_a[r];
+            if (b) {
+                k.miss2 = idx_b[r];
+                k.start3 = idx_b[r] + 1;
+                k.t1 = page_b[r];
+            }
+        }
+    }
+    err = hipMemcpyAsync(d_kp, kp.data(), rp * sizeof(K2Plane), hipMemcpyHostToDevice, stream);
+    if (err != hipSuccess) {
+        release();
+        return HBFSIM_CUDA_ERROR;
+    }
+    const std::size_t lds = 8ull * a.r_nfence + 8ull * rp;
+    const unsigned wide = static_cast<unsigned>((ngroups * rp + 255) / 256);
+    hipLaunchKernelGGL(k_k2_last, dim3(static_cast<unsigned>(ntiles)), dim3(kWave), lds, stream, a,
+                       d_rec, n, base_ps, static_cast<const K2Plane*>(d_kp), d_tlast);
+    hipLaunchKernelGGL(k_k2_up, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
+                       static_cast<const std::uint32_t*>(d_tlast), d_glast);
+    hipLaunchKernelGGL(k_k2_mid, dim3((rp + 255) / 256), dim3(256), 0, stream, a, ngroups,
+                       static_cast<const K2Plane*>(d_kp), static_cast<const std::uint32_t*>(d_glast),
+                       d_gin, d_final);
+    hipLaunchKernelGGL(k_k2_down, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
+                       static_cast<const std::uint32_t*>(d_tlast),
+                       static_cast<const std::uint32_t*>(d_gin), d_tin);
+    hipLaunchKernelGGL(k_k2_hits, dim3(static_cast<unsigned>(ntiles)), dim3(kWave), lds, stream, a,
+                       d_rec, n, base_ps, static_cast<const K2Plane*>(d_kp),
+                       static_cast<const std::uint32_t*>(d_tin), d_hits);
+    std::vector<std::uint32_t> fin(rp);
+    err = hipGetLastError();
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(fin.data(), d_final, rp * 4, hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    release();
+    if (err != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    tags_out.assign(2ull * rp, 0);
+    for (std::uint32_t r = 0; r < rp; ++r) {
+        tags_out[2 * r] = fin[r];
+        tags_out[2 * r + 1] = kp[r].t1;
+    }
+    return HBFSIM_OK;
+}
+
 }  // namespace
 
 int engine_create(const engine_config& c, engine** out)
@@ -2401,7 +2837,7 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
     if (e->cfg.model != HBFSIM_AMD_MODEL_HBF && e->cfg.model != HBFSIM_AMD_MODEL_EMPIRICAL) {
         return HBFSIM_UNSUPPORTED;
     }
-    if (e->cfg.model == HBFSIM_AMD_MODEL_HBF && e->cfg.slots > 1) {
+    if (e->cfg.model == HBFSIM_AMD_MODEL_HBF && e->cfg.slots == 2 && refresh_records) {
         return HBFSIM_UNSUPPORTED;
     }
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
@@ -2435,15 +2871,34 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         return HBFSIM_UNSUPPORTED;
     }
     hipError_t err = hipSuccess;
+    // two page registers: hits first, from their own scans
+    const bool k2 = e->cfg.slots == 2;
+    std::uint8_t* d_hits = nullptr;
+    std::vector<std::uint64_t> k2_tags;
+    if (k2) {
+        if (halloc(d_hits, n) != hipSuccess) {
+            return HBFSIM_CUDA_ERROR;
+        }
+        st = k2_hits(e, a, d_rec, n, base_ps, ntiles, stream, d_hits, k2_tags);
+        if (st != HBFSIM_OK) {
+            hfree(d_hits);
+            return st;
+        }
+        a.ext_hits = 1;
+    }
     const dim3 grid(static_cast<unsigned>(ntiles));
     const unsigned carry_blocks = (a.Rp + a.Rc + 1 + kWave - 1) / kWave;
     (void)hipEventRecord(e->ev[0], stream);
-    if (refresh_records) {
-        hipLaunchKernelGGL(k_summary<true>, grid, dim3(kWave), lds_a, stream, a, d_rec, n,
-                           base_ps, e->d_psum, e->d_csum, e->d_tcount);
+    const std::uint8_t* hits = d_hits;
+    if (k2) {
+        hipLaunchKernelGGL((k_summary<false, true>), grid, dim3(kWave), lds_a, stream, a, d_rec,
+                           n, base_ps, e->d_psum, e->d_csum, e->d_tcount, hits);
+    } else if (refresh_records) {
+        hipLaunchKernelGGL((k_summary<true, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
+                           n, base_ps, e->d_psum, e->d_csum, e->d_tcount, hits);
     } else {
-        hipLaunchKernelGGL(k_summary<false>, grid, dim3(kWave), lds_a, stream, a, d_rec, n,
-                           base_ps, e->d_psum, e->d_csum, e->d_tcount);
+        hipLaunchKernelGGL((k_summary<false, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
+                           n, base_ps, e->d_psum, e->d_csum, e->d_tcount, hits);
     }
     (void)hipEventRecord(e->ev[1], stream);
     {
@@ -2462,19 +2917,29 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
                            e->d_gseq, e->d_pcarry, e->d_ccarry, e->d_tseq);
     }
     (void)hipEventRecord(e->ev[2], stream);
-    if (refresh_records) {
-        hipLaunchKernelGGL(k_apply<true>, grid, dim3(kWave), lds_c, stream, a, d_rec, n, base_ps,
-                           e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status, e->d_tile_rep);
+    if (k2) {
+        hipLaunchKernelGGL((k_apply<false, true>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
+                           base_ps, e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status,
+                           e->d_tile_rep, hits);
+    } else if (refresh_records) {
+        hipLaunchKernelGGL((k_apply<true, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
+                           base_ps, e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status,
+                           e->d_tile_rep, hits);
     } else {
-        hipLaunchKernelGGL(k_apply<false>, grid, dim3(kWave), lds_c, stream, a, d_rec, n, base_ps,
-                           e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status, e->d_tile_rep);
+        hipLaunchKernelGGL((k_apply<false, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
+                           base_ps, e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status,
+                           e->d_tile_rep, hits);
     }
     hipLaunchKernelGGL(k_report, dim3(1), dim3(256), 0, stream, e->d_tile_rep, ntiles, e->d_rep);
     (void)hipEventRecord(e->ev[3], stream);
     err = hipGetLastError();
     if (err == hipSuccess)
         err = hipMemcpyAsync(e->h_rep, e->d_rep, sizeof(DevReport), hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess && k2)
+        err = hipMemcpyAsync(e->d_ptag, k2_tags.data(), k2_tags.size() * 8, hipMemcpyHostToDevice,
+                             stream);
     if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    hfree(d_hits);
     if (err != hipSuccess) {
         return HBFSIM_CUDA_ERROR;
     }
