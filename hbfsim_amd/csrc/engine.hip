@@ -405,7 +405,7 @@ __device__ __forceinline__ std::uint32_t dec_op(std::uint32_t bits)
 // by striping of the media page.  Refresh records are recognised only in
 // the kRefresh instantiation (streams the thermal-coupled run merged them
 // into); the other streams keep the branch out of the hot loop.
-template <bool kRefresh>
+template <bool kRefresh, bool kUniform = false>
 __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence, RangeCache& rc,
                                       const uint4& x, const uint4& y, std::uint64_t base_ps)
 {
@@ -435,7 +435,11 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
         return d;
     }
     if (!(addr >= rc.base && addr < rc.end)) {
-        const std::uint32_t idx = find_range(a, fence, addr);
+        std::uint32_t idx = find_range(a, fence, addr);
+        if (kUniform) {
+            // wave-uniform record: keep the range in scalar registers
+            idx = static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(idx)));
+        }
         if (idx == a.r_count || addr < a.r_base[idx] ||
             addr - a.r_base[idx] >= a.r_length[idx]) {
             const std::uint32_t succ = idx == a.r_count ? 0u : idx + 1u;
@@ -589,6 +593,64 @@ __device__ __forceinline__ std::uint64_t run_channel_max(const Dec& d, std::uint
     return wave_prefix_max64(w);
 }
 
+__device__ __forceinline__ std::uint32_t rfl32(std::uint32_t v)
+{
+    return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
+// A linear step: 64 reads addr_0 + k * bytes_0, one issue time, one page of
+// one range (weight streaming issues whole page-halves in one slot).  Lane
+// 0's record is decoded once in scalar registers; every lane then shares
+// its classification, page, plane, channel and transfer time, and the
+// step's effect on its plane and channel has a closed form.  Anything else
+// (and any step with fewer than 64 records) takes the general paths.
+struct Linear {
+    bool ok;
+    Dec d;
+    std::uint64_t xfer;
+};
+
+template <bool kRefresh>
+__device__ __forceinline__ Linear linear_step(const KArgs& a, const std::uint64_t* fence,
+                                              RangeCache& rcu, const uint4& x, const uint4& y,
+                                              std::uint64_t base_ps, bool full, int lane)
+{
+    Linear L;
+    L.ok = false;
+    if (!full) {
+        return L;
+    }
+    const std::uint64_t addr = x.x | (static_cast<std::uint64_t>(x.y) << 32);
+    const std::uint64_t bytes = x.z | (static_cast<std::uint64_t>(x.w) << 32);
+    const std::uint64_t issue = y.x | (static_cast<std::uint64_t>(y.y) << 32);
+    const uint4 xu = make_uint4(rfl32(x.x), rfl32(x.y), rfl32(x.z), rfl32(x.w));
+    const uint4 yu = make_uint4(rfl32(y.x), rfl32(y.y), rfl32(y.z), rfl32(y.w));
+    const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
+    const std::uint64_t b0 = xu.z | (static_cast<std::uint64_t>(xu.w) << 32);
+    const std::uint64_t i0 = yu.x | (static_cast<std::uint64_t>(yu.y) << 32);
+    if ((yu.z & 0xffu) != 0 || b0 == 0 || b0 > 0xffffffffull) {
+        return L;  // reads of 1..2^32 bytes only
+    }
+    const bool lin = addr == a0 + static_cast<std::uint64_t>(lane) * b0 && bytes == b0 &&
+                     issue == i0 && y.z == yu.z;
+    if (__ballot(!lin) != 0) {
+        return L;
+    }
+    const Dec d = decode<kRefresh, true>(a, fence, rcu, xu, yu, base_ps);
+    if (d.cls != kClsModeled) {
+        return L;
+    }
+    const std::uint64_t span = 64 * b0;
+    const std::uint64_t off0 = a0 - rcu.base;
+    if (span > rcu.end - a0 || (off0 >> a.page_shift) != ((off0 + span - 1) >> a.page_shift)) {
+        return L;
+    }
+    L.ok = true;
+    L.d = d;
+    L.xfer = xfer_ps(a, d.xbytes);
+    return L;
+}
+
 // Lane grouping by key for one step: the previous lane of the same key
 // (pred, -1 for the first), and the group's first and last lanes.  When every
 // active lane has the same key (sequential streams) the ballot match is
@@ -713,6 +775,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     const std::size_t begin = tile * a.tile;
     const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
     RangeCache rc = empty_cache();
+    RangeCache rcu = empty_cache();  // wave-uniform copy for linear steps
     uint4 x0 = make_uint4(0, 0, 0, 0), y0 = x0, x1 = x0, y1 = x0;
     if (begin + lane < end) load_record(rec, begin + lane, x0, y0);
     if (begin + kWave + lane < end) load_record(rec, begin + kWave + lane, x1, y1);
@@ -724,6 +787,38 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
         if (s + 2 * kWave + lane < end) load_record(rec, s + 2 * kWave + lane, x1, y1);
         const std::size_t i = s + lane;
         const bool valid = i < end;
+        if (!kHits && a.slots == 1) {
+            const Linear L = linear_step<kRefresh>(a, fence, rcu, x, y, base_ps,
+                                                   s + kWave <= end, lane);
+            if (L.ok) {
+                const std::uint32_t pkey = L.d.plane;
+                const std::uint32_t ckey = L.d.chan;
+                const std::uint32_t page1 = static_cast<std::uint32_t>(L.d.page1);
+                const std::uint64_t i0 = L.d.issue;
+                const std::uint64_t xf = L.xfer;
+                if (lane == 0) {
+                    if (p_f1[pkey] == 0) {  // the tile's first record, then 63 hits
+                        p_f1[pkey] = page1;
+                        p_fi[pkey] = i0;
+                        p_fc[pkey] = 0;
+                        p_rA[pkey] = 0;
+                        p_rB[pkey] = i0;
+                    } else {
+                        const std::uint64_t ls = p_l1[pkey] == page1 ? 0ull : a.read_ps;
+                        const std::uint64_t sA = p_rA[pkey] + ls;
+                        const std::uint64_t sB = umax64(p_rB[pkey] + ls, i0 + ls);
+                        p_rA[pkey] = sA;
+                        p_rB[pkey] = umax64(sB, i0);
+                    }
+                    p_l1[pkey] = page1;
+                    const std::uint64_t tA = 64 * xf;
+                    c_B[ckey] = umax64(c_B[ckey] + tA, i0 + tA);
+                    c_A[ckey] = c_A[ckey] + tA;
+                }
+                modeled += kWave;
+                continue;
+            }
+        }
         const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
         const bool m = valid && d.cls == kClsModeled;
         const bool hbit = kHits && valid && hits[i] != 0;
@@ -1087,6 +1182,7 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
     std::uint64_t n_hit = 0, n_prog = 0, n_hyb = 0, mk = 0, lat_lo = 0, lat_hi = 0;
     std::uint64_t lat_max = 0, svc_sum = 0;
     RangeCache rc = empty_cache();
+    RangeCache rcu = empty_cache();  // wave-uniform copy for linear steps
     uint4 x0 = make_uint4(0, 0, 0, 0), y0 = x0, x1 = x0, y1 = x0;
     if (begin + lane < end) load_record(rec, begin + lane, x0, y0);
     if (begin + kWave + lane < end) load_record(rec, begin + kWave + lane, x1, y1);
@@ -1097,6 +1193,53 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
         if (s + 2 * kWave + lane < end) load_record(rec, s + 2 * kWave + lane, x1, y1);
         const std::size_t i = s + lane;
         const bool valid = i < end;
+        if (!kHits && a.slots == 1 && !a.hybrid) {
+            const Linear L = linear_step<kRefresh>(a, fence, rcu, x, y, base_ps,
+                                                   s + kWave <= end, lane);
+            if (L.ok) {
+                const std::uint32_t pkey = L.d.plane;
+                const std::uint32_t ckey = L.d.chan;
+                const std::uint32_t page1 = static_cast<std::uint32_t>(L.d.page1);
+                const std::uint64_t i0 = L.d.issue;
+                const std::uint64_t xf = L.xfer;
+                const std::uint32_t tag = p_tag[pkey];
+                const std::uint64_t pbusy = p_busy[pkey];
+                const std::uint64_t cbusy = c_busy[ckey];
+                const bool lhit = tag == page1;
+                const std::uint64_t ls = lhit ? 0ull : a.read_ps;
+                // lane 0 pays the sense; the rest hit.  With contention the
+                // plane is busy until `lead` (>= i0) for every lane.
+                const std::uint64_t lead = a.contention ? umax64(pbusy, i0) + ls : i0 + ls;
+                const std::uint64_t pd = (lane == 0 || a.contention) ? lead : i0;
+                const std::uint64_t cd =
+                    umax64(cbusy, i0) + xf * static_cast<std::uint64_t>(lane + 1);
+                if (lane == 63) {
+                    if (a.contention) {
+                        p_busy[pkey] = pd;
+                    }
+                    p_tag[pkey] = page1;
+                    c_busy[ckey] = cd;
+                }
+                const std::uint64_t done = umax64(pd, cd);
+                const bool hit = lane == 0 ? lhit : true;
+                const std::uint64_t svc = lane == 0 ? ls : 0ull;
+                ++n_rec;
+                ++n_mod;
+                ++n_rd;
+                n_hit += hit ? 1u : 0u;
+                mk = umax64(mk, done);
+                const std::uint64_t lat = done - i0;
+                add128(lat_lo, lat_hi, lat);
+                lat_max = umax64(lat_max, lat);
+                svc_sum += umax64(svc, xf);
+                seq += kWave;
+                completion[i] = done;
+                if (status != nullptr) {
+                    status[i] = static_cast<std::uint8_t>(hit ? 4u : 0u);
+                }
+                continue;
+            }
+        }
         const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
         const bool m = valid && d.cls == kClsModeled;
         const bool hbit = kHits && valid && hits[i] != 0;
