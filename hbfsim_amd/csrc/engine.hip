@@ -342,6 +342,35 @@ __device__ __forceinline__ std::uint64_t xfer_ps(const KArgs& a, std::uint64_t b
     return a.xfer_q * ((bytes * a.xfer_num + a.xfer_den - 1) / a.xfer_den);
 }
 
+// The same with the power-of-two table in LDS, for per-lane byte counts: a
+// lane-indexed read of the kernel arguments would be a vector memory load,
+// and the record pipeline keeps those out of the step loop.
+__device__ __forceinline__ std::uint64_t xfer_ps_lds(const KArgs& a, const std::uint64_t* xp,
+                                                     std::uint64_t bytes)
+{
+    if ((bytes & (bytes - 1)) == 0 && bytes != 0 && bytes <= (1ull << 32)) {
+        return xp[63 - __clzll(bytes)];
+    }
+    return a.xfer_q * ((bytes * a.xfer_num + a.xfer_den - 1) / a.xfer_den);
+}
+
+// Copies the power-of-two transfer table into LDS (`xp`, 33 entries).
+__device__ __forceinline__ void load_xfer_table(const KArgs& a, std::uint64_t* xp, int lane)
+{
+    if (lane < 33) {
+        xp[lane] = a.xfer_pow2[lane];
+    }
+}
+
+// Waits for every outstanding vector memory operation (s_waitcnt vmcnt(0)).
+// Called where a step has just made its own per-lane loads, so that none of
+// them is still outstanding when the next step starts: the record pipeline's
+// group in flight is then waited on only when the wave needs it.
+__device__ __forceinline__ void wait_vector_loads()
+{
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt 0, expcnt 7, lgkmcnt 15: vmcnt only
+}
+
 // Range last found by this lane.  Ranges are disjoint, so an address inside
 // the cached range is inside no other one and the search can be skipped.
 struct RangeCache {
@@ -369,6 +398,89 @@ __device__ __forceinline__ void load_record(const hbf_record32* rec, std::size_t
     const uint4* p = reinterpret_cast<const uint4*>(rec + i);
     x = p[0];
     y = p[1];
+}
+
+// Records reach a wave in groups of kPipe steps: while the wave works through
+// one group (held in registers), the next group's loads are in flight, so
+// each wave keeps kPipe * 2 KiB of reads outstanding for kPipe steps of
+// work.  (A load queue rotated one step at a time would wait on the newest
+// load at every step, since the rotation copies it.)  A step's 2 KiB arrive
+// coalesced, 16 B per lane: half A holds records 0..31 and half B records
+// 32..63, lane l holding word pair l & 1 of record l >> 1 (even lanes address
+// and bytes, odd lanes issue time and operation).  Loading record-per-lane
+// instead (32 B stride) caps the read rate at ~4.8 TB/s; the coalesced form
+// streams at ~6.3 TB/s.  Within the current group the next step is always
+// slot 0: taking a step shifts the group down by one slot, register moves
+// with constant indices that wait on nothing in flight (a selection by step
+// index would put the group in scratch memory).
+constexpr int kPipe = 4;
+constexpr std::size_t kGroupSpan = static_cast<std::size_t>(kPipe) * kWave;
+
+struct RecordPipe {
+    uint4 ca[kPipe], cb[kPipe];  // the group being worked through
+    uint4 na[kPipe], nb[kPipe];  // the next group, in flight
+
+    __device__ __forceinline__ void issue(const hbf_record32* rec, std::size_t g,
+                                          std::size_t end, int lane)
+    {
+        const uint4* p = reinterpret_cast<const uint4*>(rec);
+        const std::size_t words = 2 * end;  // 16-byte words in the tile's records
+#pragma unroll
+        for (int j = 0; j < kPipe; ++j) {
+            const std::size_t w = 2 * (g + static_cast<std::size_t>(j) * kWave) + lane;
+            na[j] = make_uint4(0, 0, 0, 0);
+            nb[j] = na[j];
+            if (w < words) {
+                na[j] = p[w];
+            }
+            if (w + kWave < words) {
+                nb[j] = p[w + kWave];
+            }
+        }
+    }
+    // Makes the group in flight current and issues the one after it.
+    __device__ __forceinline__ void advance(const hbf_record32* rec, std::size_t next,
+                                            std::size_t end, int lane)
+    {
+#pragma unroll
+        for (int j = 0; j < kPipe; ++j) {
+            ca[j] = na[j];
+            cb[j] = nb[j];
+        }
+        if (next < end) {
+            issue(rec, next, end, lane);
+        }
+    }
+    // The current group's next step, in the coalesced halves.
+    __device__ __forceinline__ void take(uint4& A, uint4& B)
+    {
+        A = ca[0];
+        B = cb[0];
+#pragma unroll
+        for (int j = 0; j + 1 < kPipe; ++j) {
+            ca[j] = ca[j + 1];
+            cb[j] = cb[j + 1];
+        }
+    }
+};
+
+// Record-per-lane form of a step (lane r gets record r's two word pairs).
+__device__ __forceinline__ void to_records(const uint4& A, const uint4& B, int lane, uint4& x,
+                                           uint4& y)
+{
+    const int sx = ((2 * lane) & 63) << 2;  // bpermute byte addresses
+    const int sy = ((2 * lane + 1) & 63) << 2;
+    const bool lo = lane < 32;
+    const auto pick = [&](std::uint32_t a, std::uint32_t b, int src) {
+        const std::uint32_t ta =
+            static_cast<std::uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(a)));
+        const std::uint32_t tb =
+            static_cast<std::uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(b)));
+        return lo ? ta : tb;
+    };
+    x = make_uint4(pick(A.x, B.x, sx), pick(A.y, B.y, sx), pick(A.z, B.z, sx),
+                   pick(A.w, B.w, sx));
+    y = make_uint4(pick(A.x, B.x, sy), pick(A.y, B.y, sy), pick(A.z, B.z, sy), 0);
 }
 
 // Channel and global plane id of a media page (the profile's allocation
@@ -456,6 +568,9 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
         rc.file_offset = a.r_file_offset[idx];
         rc.meta = a.r_meta[idx];
         rc.id = a.r_id[idx];
+        if (!kUniform) {
+            wait_vector_loads();
+        }
     }
     const std::uint32_t mode = rc.meta & 0xffu;
     const std::uint32_t perms = rc.meta >> 8;
@@ -520,8 +635,8 @@ __device__ __forceinline__ Dec invalid_dec()
 
 // Transfer time of every lane's access.  When all modeled lanes move the same
 // byte count (the usual case) it is computed once, in scalar registers.
-__device__ __forceinline__ std::uint64_t lane_xfer(const KArgs& a, const Dec& d, bool m,
-                                                   std::uint64_t active)
+__device__ __forceinline__ std::uint64_t lane_xfer(const KArgs& a, const std::uint64_t* xp,
+                                                   const Dec& d, bool m, std::uint64_t active)
 {
     const int first = __ffsll(static_cast<long long>(active)) - 1;
     const std::uint32_t lo = static_cast<std::uint32_t>(
@@ -532,7 +647,7 @@ __device__ __forceinline__ std::uint64_t lane_xfer(const KArgs& a, const Dec& d,
     if (__ballot(m && d.xbytes != xb0) == 0) {
         return xfer_ps(a, xb0);
     }
-    return m ? xfer_ps(a, d.xbytes) : 0ull;
+    return m ? xfer_ps_lds(a, xp, d.xbytes) : 0ull;
 }
 
 // Time origin for 32-bit scans: the first active lane's issue time.  The
@@ -598,57 +713,119 @@ __device__ __forceinline__ std::uint32_t rfl32(std::uint32_t v)
     return static_cast<std::uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
 }
 
-// A linear step: 64 reads addr_0 + k * bytes_0, one issue time, one page of
-// one range (weight streaming issues whole page-halves in one slot).  Lane
-// 0's record is decoded once in scalar registers; every lane then shares
-// its classification, page, plane, channel and transfer time, and the
-// step's effect on its plane and channel has a closed form.  Anything else
-// (and any step with fewer than 64 records) takes the general paths.
-struct Linear {
-    bool ok;
-    Dec d;
-    std::uint64_t xfer;
-};
+// A linear step: 64 reads addr_0 + k * bytes_0 with one issue time, inside
+// one page of one range (weight streaming issues whole page-halves in one
+// slot).  Such a step touches one plane and one channel; lanes 1..63 hit the
+// page lane 0 opened, so its effect has a closed form given lane 0's record.
+// linear_detect checks a step in scalar registers against the wave-uniform
+// range cache (the full decode runs only when the cache misses) and returns
+// the step's media page + 1, issue time and byte count.  Anything else (and
+// any step with fewer than 64 records) takes the general paths.
+__device__ __forceinline__ std::uint32_t rl32(std::uint32_t v, int k)
+{
+    return static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), k));
+}
 
 template <bool kRefresh>
-__device__ __forceinline__ Linear linear_step(const KArgs& a, const std::uint64_t* fence,
-                                              RangeCache& rcu, const uint4& x, const uint4& y,
-                                              std::uint64_t base_ps, bool full, int lane)
+__device__ __forceinline__ bool linear_detect(const KArgs& a, const std::uint64_t* fence,
+                                              RangeCache& rcu, const uint4& A, const uint4& B,
+                                              std::uint64_t base_ps, bool full, int lane,
+                                              std::uint32_t& page1, std::uint64_t& issue0,
+                                              std::uint32_t& bytes0)
 {
-    Linear L;
-    L.ok = false;
     if (!full) {
-        return L;
+        return false;
     }
-    const std::uint64_t addr = x.x | (static_cast<std::uint64_t>(x.y) << 32);
-    const std::uint64_t bytes = x.z | (static_cast<std::uint64_t>(x.w) << 32);
-    const std::uint64_t issue = y.x | (static_cast<std::uint64_t>(y.y) << 32);
-    const uint4 xu = make_uint4(rfl32(x.x), rfl32(x.y), rfl32(x.z), rfl32(x.w));
-    const uint4 yu = make_uint4(rfl32(y.x), rfl32(y.y), rfl32(y.z), rfl32(y.w));
+    // record 0: address and bytes in lane 0, issue and operation in lane 1
+    const uint4 xu = make_uint4(rfl32(A.x), rfl32(A.y), rfl32(A.z), rfl32(A.w));
+    const uint4 yu = make_uint4(rl32(A.x, 1), rl32(A.y, 1), rl32(A.z, 1), 0);
+    if ((yu.z & 0xffu) != 0 || xu.w != 0 || xu.z == 0) {
+        return false;  // reads of 1 .. 2^32 - 1 bytes only
+    }
     const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
-    const std::uint64_t b0 = xu.z | (static_cast<std::uint64_t>(xu.w) << 32);
-    const std::uint64_t i0 = yu.x | (static_cast<std::uint64_t>(yu.y) << 32);
-    if ((yu.z & 0xffu) != 0 || b0 == 0 || b0 > 0xffffffffull) {
-        return L;  // reads of 1..2^32 bytes only
+    // lane l checks word pair l & 1 of records l >> 1 (half A) and 32 + (l >> 1) (half B)
+    const std::uint64_t ea = a0 + static_cast<std::uint64_t>(lane >> 1) * xu.z;
+    const std::uint64_t eb = ea + 32ull * xu.z;
+    const std::uint64_t wa = A.x | (static_cast<std::uint64_t>(A.y) << 32);
+    const std::uint64_t wb = B.x | (static_cast<std::uint64_t>(B.y) << 32);
+    const bool odd = (lane & 1) != 0;
+    const bool ok_even = wa == ea && A.z == xu.z && A.w == 0 && wb == eb && B.z == xu.z &&
+                         B.w == 0;
+    const bool ok_odd = A.x == yu.x && A.y == yu.y && A.z == yu.z && B.x == yu.x &&
+                        B.y == yu.y && B.z == yu.z;
+    if (__ballot(odd ? !ok_odd : !ok_even) != 0) {
+        return false;
     }
-    const bool lin = addr == a0 + static_cast<std::uint64_t>(lane) * b0 && bytes == b0 &&
-                     issue == i0 && y.z == yu.z;
-    if (__ballot(!lin) != 0) {
-        return L;
+    if (!(a0 >= rcu.base && a0 < rcu.end)) {
+        // refill the cache through the full classification
+        const Dec d = decode<kRefresh, true>(a, fence, rcu, xu, yu, base_ps);
+        if (d.cls != kClsModeled) {
+            return false;
+        }
     }
-    const Dec d = decode<kRefresh, true>(a, fence, rcu, xu, yu, base_ps);
-    if (d.cls != kClsModeled) {
-        return L;
+    // every record inside the cached range, which admits reads, and in one
+    // page whose media offset does not wrap (access_supported,
+    // hbf_device.cuh:843-860, for all 64 records at once)
+    const std::uint32_t mode = rcu.meta & 0xffu;
+    const std::uint64_t span = 64ull * xu.z;
+    if ((mode != 1 && mode != 2) || (rcu.meta & (1u << 8)) == 0 || span > rcu.end - a0) {
+        return false;
     }
-    const std::uint64_t span = 64 * b0;
     const std::uint64_t off0 = a0 - rcu.base;
-    if (span > rcu.end - a0 || (off0 >> a.page_shift) != ((off0 + span - 1) >> a.page_shift)) {
-        return L;
+    const std::uint64_t page_mask = (1ull << a.page_shift) - 1;
+    if ((off0 >> a.page_shift) != ((off0 + span - 1) >> a.page_shift) ||
+        (off0 & ~page_mask) > ~0ull - rcu.file_offset) {
+        return false;
     }
-    L.ok = true;
-    L.d = d;
-    L.xfer = xfer_ps(a, d.xbytes);
-    return L;
+    page1 = static_cast<std::uint32_t>(((rcu.file_offset + off0) >> a.page_shift) + 1);
+    issue0 = base_ps + (yu.x | (static_cast<std::uint64_t>(yu.y) << 32));
+    bytes0 = xu.z;
+    return true;
+}
+
+// What the summary pass learned about a step, for the apply pass: a linear
+// step's media page + 1, byte count and issue time (bytes == 0: any other
+// step).  Indexed by record index / 64.
+struct alignas(16) StepDesc {
+    std::uint32_t page1;
+    std::uint32_t bytes;
+    std::uint64_t issue;
+};
+
+// Linear steps waiting to be folded: lane k holds step k (k < n) -- its media
+// page + 1, issue time and byte count.  Pending steps are always consecutive
+// steps of the tile, the first starting at record `first`.
+struct LinBatch {
+    std::uint32_t page1;
+    std::uint32_t bytes;
+    std::uint64_t issue;
+    std::size_t first;
+    int n;
+
+    __device__ __forceinline__ void push(std::uint32_t p1, std::uint64_t i0, std::uint32_t b0,
+                                         std::size_t s)
+    {
+        if (n == 0) {
+            first = s;
+        }
+        if (static_cast<int>(threadIdx.x) == n) {
+            page1 = p1;
+            bytes = b0;
+            issue = i0;
+        }
+        ++n;
+    }
+};
+
+__device__ __forceinline__ LinBatch empty_batch()
+{
+    LinBatch b;
+    b.page1 = 0;
+    b.bytes = 0;
+    b.issue = 0;
+    b.first = 0;
+    b.n = 0;
+    return b;
 }
 
 // Lane grouping by key for one step: the previous lane of the same key
@@ -736,6 +913,119 @@ __device__ __forceinline__ void load_fences(const KArgs& a, std::uint64_t* fence
     }
 }
 
+// Step view of a batch of linear steps: lane k < n stands for step k, with
+// lane 0's record of that step (plane and channel from the media page, the
+// byte count the channel moves per record and its transfer time).
+struct StepView {
+    Dec d;
+    bool m;
+    std::uint64_t active;
+    std::uint64_t x;  // transfer of one record
+};
+
+__device__ __forceinline__ StepView step_view(const KArgs& a, const std::uint64_t* xp,
+                                              const LinBatch& q, int lane)
+{
+    StepView v;
+    v.m = lane < q.n;
+    v.active = q.n == kWave ? ~0ull : ((1ull << q.n) - 1);
+    v.d.cls = v.m ? kClsModeled : kClsInvalid;
+    v.d.bits = 0;
+    v.d.plane = 0;
+    v.d.chan = 0;
+    v.d.range_id = 0;
+    v.d.page1 = q.page1;
+    v.d.issue = q.issue;
+    v.d.xbytes = a.transfer_page ? (1ull << a.page_shift) : q.bytes;
+    v.d.xfer = 0;
+    if (v.m) {
+        stripe(a, static_cast<std::uint64_t>(q.page1) - 1, v.d);
+    }
+    v.x = v.m ? xfer_ps_lds(a, xp, v.d.xbytes) : 0ull;
+    return v;
+}
+
+// Folds a batch of linear steps into the tile summary: the per-record fold
+// of the general path applied to whole steps.  A step after another record of
+// its plane has plane map (sense, issue + sense) -- lane 0 senses unless its
+// page is the one the plane last read, lanes 1..63 hit; a step that is the
+// tile's first record on its plane records lane 0 as that first record and
+// folds the 63 hits after it, map (0, issue).  The channel map of a step is
+// (64 x, issue + 64 x).
+__device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t* xp,
+                                             const LinBatch& q, int lane, std::uint64_t* p_fi,
+                                             std::uint64_t* p_rA, std::uint64_t* p_rB,
+                                             std::uint64_t* c_A, std::uint64_t* c_B,
+                                             std::uint32_t* p_f1, std::uint32_t* p_l1,
+                                             std::uint32_t* p_fc, StepDesc* desc)
+{
+    if (desc != nullptr && lane < q.n) {
+        StepDesc sd;
+        sd.page1 = q.page1;
+        sd.bytes = q.bytes;
+        sd.issue = q.issue;
+        desc[q.first / kWave + lane] = sd;
+    }
+    const StepView v = step_view(a, xp, q, lane);
+    const bool m = v.m;
+    const std::uint32_t pkey = m ? v.d.plane : 0u;
+    const std::uint32_t ckey = m ? v.d.chan : 0u;
+    const Group gp = group_by(pkey, a.pbits, m, v.active, lane);
+    const Group gc = group_by(ckey, a.cbits, m, v.active, lane);
+    const std::uint32_t f1 = m ? p_f1[pkey] : 0u;
+    const std::uint32_t last_page = m ? p_l1[pkey] : 0u;
+    const bool has = f1 != 0;
+    const bool tfirst = m && gp.pred < 0 && !has;
+    std::uint32_t prev1 = static_cast<std::uint32_t>(
+        __shfl(static_cast<int>(q.page1), gp.pred < 0 ? lane : gp.pred));
+    if (gp.pred < 0) {
+        prev1 = last_page;
+    }
+    const std::uint64_t ls = prev1 == q.page1 ? 0ull : a.read_ps;
+    const std::uint64_t cx = 64 * v.x;
+    std::uint64_t Ap = 0, Bp = 0, Ac = 0, Bc = 0;
+    if (m) {
+        Ap = tfirst ? 0ull : ls;
+        Bp = q.issue + Ap;
+        Ac = cx;
+        Bc = q.issue + cx;
+    }
+    scan_pair(gp, Ap, Bp, gc, Ac, Bc, v.d, m, v.active, ls, cx, lane);
+    const std::uint32_t l1 =
+        static_cast<std::uint32_t>(__shfl(static_cast<int>(q.page1), gp.leader));
+    const std::uint64_t li = shfl64(q.issue, gp.leader);
+    if (m && lane == gp.last) {
+        if (!has) {
+            p_f1[pkey] = l1;
+            p_fi[pkey] = li;
+            p_fc[pkey] = 0;  // a read
+        }
+        const std::uint64_t sA = p_rA[pkey];
+        const std::uint64_t sB = p_rB[pkey];
+        p_rB[pkey] = umax64(sB + Ap, Bp);
+        p_rA[pkey] = sA + Ap;
+        p_l1[pkey] = q.page1;
+    }
+    if (m && lane == gc.last) {
+        const std::uint64_t sA = c_A[ckey];
+        const std::uint64_t sB = c_B[ckey];
+        c_B[ckey] = umax64(sB + Ac, Bc);
+        c_A[ckey] = sA + Ac;
+    }
+}
+
+// 64-bit words of a tile's touched-plane mask.
+__host__ __device__ __forceinline__ std::uint32_t mask_words(const KArgs& a)
+{
+    return (a.Rp + 63) / 64;
+}
+
+__device__ __forceinline__ bool touched(const std::uint64_t* tmask, std::uint32_t words,
+                                        std::size_t tile, std::uint32_t r)
+{
+    return ((tmask[tile * words + r / 64] >> (r % 64)) & 1u) != 0;
+}
+
 // Summary pass.  Per plane the tile keeps: the first record (page, issue,
 // class), the (max,+) map of the records after it, and the last page; per
 // channel the map of all its records.  Pages are stored as page + 1 in 32
@@ -743,8 +1033,9 @@ __device__ __forceinline__ void load_fences(const KArgs& a, std::uint64_t* fence
 template <bool kRefresh, bool kHits>
 __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
-                                                ChanSum* csum, std::uint64_t* tile_count,
-                                                const std::uint8_t* hits)
+                                                std::uint64_t* tmask, ChanSum* csum,
+                                                std::uint64_t* tile_count,
+                                                const std::uint8_t* hits, StepDesc* desc)
 {
     extern __shared__ std::uint64_t sm[];
     std::uint64_t* fence = sm;
@@ -756,8 +1047,10 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     std::uint32_t* p_f1 = reinterpret_cast<std::uint32_t*>(c_B + a.Rc);
     std::uint32_t* p_l1 = p_f1 + a.Rp;
     std::uint32_t* p_fc = p_l1 + a.Rp;
+    __shared__ std::uint64_t xp[33];
     const int lane = threadIdx.x;
     load_fences(a, fence, lane);
+    load_xfer_table(a, xp, lane);
     for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
         p_fi[r] = 0;
         p_rA[r] = 0;
@@ -776,152 +1069,158 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
     RangeCache rc = empty_cache();
     RangeCache rcu = empty_cache();  // wave-uniform copy for linear steps
-    uint4 x0 = make_uint4(0, 0, 0, 0), y0 = x0, x1 = x0, y1 = x0;
-    if (begin + lane < end) load_record(rec, begin + lane, x0, y0);
-    if (begin + kWave + lane < end) load_record(rec, begin + kWave + lane, x1, y1);
+    RecordPipe pipe;
+    pipe.issue(rec, begin, end, lane);
+    LinBatch q = empty_batch();
     std::uint64_t modeled = 0;
-    for (std::size_t s = begin; s < end; s += kWave) {
-        const uint4 x = x0, y = y0;
-        x0 = x1;
-        y0 = y1;
-        if (s + 2 * kWave + lane < end) load_record(rec, s + 2 * kWave + lane, x1, y1);
-        const std::size_t i = s + lane;
-        const bool valid = i < end;
-        if (!kHits && a.slots == 1) {
-            const Linear L = linear_step<kRefresh>(a, fence, rcu, x, y, base_ps,
-                                                   s + kWave <= end, lane);
-            if (L.ok) {
-                const std::uint32_t pkey = L.d.plane;
-                const std::uint32_t ckey = L.d.chan;
-                const std::uint32_t page1 = static_cast<std::uint32_t>(L.d.page1);
-                const std::uint64_t i0 = L.d.issue;
-                const std::uint64_t xf = L.xfer;
-                if (lane == 0) {
-                    if (p_f1[pkey] == 0) {  // the tile's first record, then 63 hits
+    for (std::size_t g = begin; g < end; g += kGroupSpan) {
+        pipe.advance(rec, g + kGroupSpan, end, lane);
+        const std::size_t gend = g + kGroupSpan < end ? g + kGroupSpan : end;
+        for (std::size_t s = g; s < gend; s += kWave) {
+            uint4 A, B;
+            pipe.take(A, B);
+            const std::size_t i = s + lane;
+            const bool valid = i < end;
+            if (!kHits && a.slots == 1) {
+                // linear steps wait in a batch; the batch is folded when full, at
+                // the tile's last step, and before any other step (order matters)
+                std::uint32_t lp, lb;
+                std::uint64_t li;
+                const bool lin = linear_detect<kRefresh>(a, fence, rcu, A, B, base_ps,
+                                                         s + kWave <= end, lane, lp, li, lb);
+                if (lin) {
+                    q.push(lp, li, lb, s);
+                }
+                if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= end)) {
+                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
+                                 desc);
+                    modeled += static_cast<std::uint64_t>(q.n) * kWave;
+                    q.n = 0;
+                }
+                if (lin) {
+                    continue;
+                }
+                if (desc != nullptr && lane == 0) {
+                    desc[s / kWave] = StepDesc{0, 0, 0};  // replayed from its records
+                }
+            }
+            uint4 x, y;
+            to_records(A, B, lane, x, y);
+            const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
+            const bool m = valid && d.cls == kClsModeled;
+            const bool hbit = kHits && valid && hits[i] != 0;
+            const std::uint64_t active = __ballot(m);
+            modeled += __popcll(active);
+            if (active == 0) {
+                continue;
+            }
+            const std::uint64_t xfer = lane_xfer(a, xp, d, m, active);
+            if (!kHits && run_step(a, d, active, lane)) {
+                const std::uint64_t W = run_channel_max(d, xfer, lane);
+                if (lane == 63) {
+                    const std::uint32_t pkey = d.plane;
+                    const std::uint32_t ckey = d.chan;
+                    const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
+                    const std::uint64_t i0 = readlane64(d.issue, 0);
+                    if (p_f1[pkey] == 0) {  // lane 0 is the tile's first record here
                         p_f1[pkey] = page1;
                         p_fi[pkey] = i0;
                         p_fc[pkey] = 0;
                         p_rA[pkey] = 0;
-                        p_rB[pkey] = i0;
+                        p_rB[pkey] = d.issue;
                     } else {
-                        const std::uint64_t ls = p_l1[pkey] == page1 ? 0ull : a.read_ps;
+                        const bool lhit = p_l1[pkey] == page1;
+                        const std::uint64_t ls = lhit ? 0ull : a.read_ps;
                         const std::uint64_t sA = p_rA[pkey] + ls;
                         const std::uint64_t sB = umax64(p_rB[pkey] + ls, i0 + ls);
                         p_rA[pkey] = sA;
-                        p_rB[pkey] = umax64(sB, i0);
+                        p_rB[pkey] = umax64(sB, d.issue);
                     }
                     p_l1[pkey] = page1;
-                    const std::uint64_t tA = 64 * xf;
-                    c_B[ckey] = umax64(c_B[ckey] + tA, i0 + tA);
-                    c_A[ckey] = c_A[ckey] + tA;
+                    const std::uint64_t tA = 64 * xfer;
+                    const std::uint64_t tB = W + xfer;
+                    const std::uint64_t sA = c_A[ckey];
+                    const std::uint64_t sB = c_B[ckey];
+                    c_B[ckey] = umax64(sB + tA, tB);
+                    c_A[ckey] = sA + tA;
                 }
-                modeled += kWave;
                 continue;
             }
-        }
-        const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
-        const bool m = valid && d.cls == kClsModeled;
-        const bool hbit = kHits && valid && hits[i] != 0;
-        const std::uint64_t active = __ballot(m);
-        modeled += __popcll(active);
-        if (active == 0) {
-            continue;
-        }
-        const std::uint64_t xfer = lane_xfer(a, d, m, active);
-        if (!kHits && run_step(a, d, active, lane)) {
-            const std::uint64_t W = run_channel_max(d, xfer, lane);
-            if (lane == 63) {
-                const std::uint32_t pkey = d.plane;
-                const std::uint32_t ckey = d.chan;
-                const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
-                const std::uint64_t i0 = readlane64(d.issue, 0);
-                if (p_f1[pkey] == 0) {  // lane 0 is the tile's first record here
-                    p_f1[pkey] = page1;
-                    p_fi[pkey] = i0;
-                    p_fc[pkey] = 0;
-                    p_rA[pkey] = 0;
-                    p_rB[pkey] = d.issue;
-                } else {
-                    const bool lhit = p_l1[pkey] == page1;
-                    const std::uint64_t ls = lhit ? 0ull : a.read_ps;
-                    const std::uint64_t sA = p_rA[pkey] + ls;
-                    const std::uint64_t sB = umax64(p_rB[pkey] + ls, i0 + ls);
-                    p_rA[pkey] = sA;
-                    p_rB[pkey] = umax64(sB, d.issue);
+            const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
+            const std::uint32_t pkey = m ? d.plane : 0u;
+            const std::uint32_t ckey = m ? d.chan : 0u;
+            const Group gp = group_by(pkey, a.pbits, m, active, lane);
+            const Group gc = group_by(ckey, a.cbits, m, active, lane);
+            // state reads come before this step's writes
+            const std::uint32_t f1 = m ? p_f1[pkey] : 0u;
+            const std::uint32_t last_page = m ? p_l1[pkey] : 0u;
+            const bool has = f1 != 0;
+            const bool tfirst = m && gp.pred < 0 && !has;
+            std::uint32_t prev1 = static_cast<std::uint32_t>(
+                __shfl(static_cast<int>(page1), gp.pred < 0 ? lane : gp.pred));
+            if (gp.pred < 0) {
+                prev1 = last_page;
+            }
+            const bool hit = kHits ? (m && hbit) : (a.slots != 0 && m && prev1 == page1);
+            const std::uint64_t svc = plane_service(a, d.bits, hit);
+            std::uint64_t Ap = 0, Bp = 0;
+            if (m && !tfirst) {
+                Ap = svc;
+                Bp = d.issue + svc;
+            }
+            std::uint64_t Ac = m ? xfer : 0ull;
+            std::uint64_t Bc = m ? d.issue + xfer : 0ull;
+            scan_pair(gp, Ap, Bp, gc, Ac, Bc, d, m, active, svc, xfer, lane);
+            const std::uint32_t l1 =
+                static_cast<std::uint32_t>(__shfl(static_cast<int>(page1), gp.leader));
+            const std::uint64_t li = shfl64(d.issue, gp.leader);
+            // the leader's class; with given hits, bit 3 carries its hit
+            const std::uint32_t lbits = kHits && hit ? (d.bits | 8u) : d.bits;
+            const std::uint32_t lc =
+                static_cast<std::uint32_t>(__shfl(static_cast<int>(lbits), gp.leader));
+            if (m && lane == gp.last) {
+                if (!has) {
+                    p_f1[pkey] = l1;
+                    p_fi[pkey] = li;
+                    p_fc[pkey] = lc;
                 }
+                const std::uint64_t sA = p_rA[pkey];
+                const std::uint64_t sB = p_rB[pkey];
+                p_rB[pkey] = umax64(sB + Ap, Bp);
+                p_rA[pkey] = sA + Ap;
                 p_l1[pkey] = page1;
-                const std::uint64_t tA = 64 * xfer;
-                const std::uint64_t tB = W + xfer;
+            }
+            if (m && lane == gc.last) {
                 const std::uint64_t sA = c_A[ckey];
                 const std::uint64_t sB = c_B[ckey];
-                c_B[ckey] = umax64(sB + tA, tB);
-                c_A[ckey] = sA + tA;
+                c_B[ckey] = umax64(sB + Ac, Bc);
+                c_A[ckey] = sA + Ac;
             }
-            continue;
-        }
-        const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
-        const std::uint32_t pkey = m ? d.plane : 0u;
-        const std::uint32_t ckey = m ? d.chan : 0u;
-        const Group gp = group_by(pkey, a.pbits, m, active, lane);
-        const Group gc = group_by(ckey, a.cbits, m, active, lane);
-        // state reads come before this step's writes
-        const std::uint32_t f1 = m ? p_f1[pkey] : 0u;
-        const std::uint32_t last_page = m ? p_l1[pkey] : 0u;
-        const bool has = f1 != 0;
-        const bool tfirst = m && gp.pred < 0 && !has;
-        std::uint32_t prev1 = static_cast<std::uint32_t>(
-            __shfl(static_cast<int>(page1), gp.pred < 0 ? lane : gp.pred));
-        if (gp.pred < 0) {
-            prev1 = last_page;
-        }
-        const bool hit = kHits ? (m && hbit) : (a.slots != 0 && m && prev1 == page1);
-        const std::uint64_t svc = plane_service(a, d.bits, hit);
-        std::uint64_t Ap = 0, Bp = 0;
-        if (m && !tfirst) {
-            Ap = svc;
-            Bp = d.issue + svc;
-        }
-        std::uint64_t Ac = m ? xfer : 0ull;
-        std::uint64_t Bc = m ? d.issue + xfer : 0ull;
-        scan_pair(gp, Ap, Bp, gc, Ac, Bc, d, m, active, svc, xfer, lane);
-        const std::uint32_t l1 =
-            static_cast<std::uint32_t>(__shfl(static_cast<int>(page1), gp.leader));
-        const std::uint64_t li = shfl64(d.issue, gp.leader);
-        // the leader's class; with given hits, bit 3 carries its hit
-        const std::uint32_t lbits = kHits && hit ? (d.bits | 8u) : d.bits;
-        const std::uint32_t lc =
-            static_cast<std::uint32_t>(__shfl(static_cast<int>(lbits), gp.leader));
-        if (m && lane == gp.last) {
-            if (!has) {
-                p_f1[pkey] = l1;
-                p_fi[pkey] = li;
-                p_fc[pkey] = lc;
-            }
-            const std::uint64_t sA = p_rA[pkey];
-            const std::uint64_t sB = p_rB[pkey];
-            p_rB[pkey] = umax64(sB + Ap, Bp);
-            p_rA[pkey] = sA + Ap;
-            p_l1[pkey] = page1;
-        }
-        if (m && lane == gc.last) {
-            const std::uint64_t sA = c_A[ckey];
-            const std::uint64_t sB = c_B[ckey];
-            c_B[ckey] = umax64(sB + Ac, Bc);
-            c_A[ckey] = sA + Ac;
         }
     }
     __syncthreads();
+    // Only planes the tile touched get a summary; a bit mask per tile says
+    // which (the others are identities, and the carry chain skips them).
     PlaneSum* ps = psum + tile * a.Rp;
-    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
-        PlaneSum v;
-        v.fpage1 = p_f1[r];
-        v.fissue = p_fi[r];
-        v.rA = p_rA[r];
-        v.rB = p_rB[r];
-        v.lpage1 = p_l1[r];
-        v.fcls = p_fc[r];
-        v.pad = 0;
-        ps[r] = v;
+    std::uint64_t* tm = tmask + tile * mask_words(a);
+    for (std::uint32_t r0 = 0; r0 < a.Rp; r0 += kWave) {
+        const std::uint32_t r = r0 + lane;
+        const bool touched = r < a.Rp && p_f1[r] != 0;
+        const std::uint64_t bits = __ballot(touched);
+        if (lane == 0) {
+            tm[r0 / kWave] = bits;
+        }
+        if (touched) {
+            PlaneSum v;
+            v.fpage1 = p_f1[r];
+            v.fissue = p_fi[r];
+            v.rA = p_rA[r];
+            v.rB = p_rB[r];
+            v.lpage1 = p_l1[r];
+            v.fcls = p_fc[r];
+            v.pad = 0;
+            ps[r] = v;
+        }
     }
     ChanSum* cs = csum + tile * a.Rc;
     for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
@@ -996,7 +1295,8 @@ __device__ __forceinline__ ChanSum chan_compose(const ChanSum& s1, const ChanSum
 
 // Level 1: thread (g, r) folds the summaries of group g's tiles.
 __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, std::size_t ngroups,
-                                                  const PlaneSum* psum, const ChanSum* csum,
+                                                  const PlaneSum* psum,
+                                                  const std::uint64_t* tmask, const ChanSum* csum,
                                                   const std::uint64_t* tile_count,
                                                   PlaneSum* gpsum, ChanSum* gcsum,
                                                   std::uint64_t* gcount)
@@ -1011,9 +1311,12 @@ __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, s
     const std::size_t t0 = g * kGroup;
     const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
     if (r < a.Rp) {
-        PlaneSum acc = psum[t0 * a.Rp + r];
-        for (std::size_t t = t0 + 1; t < t1; ++t) {
-            acc = plane_compose(a, acc, psum[t * a.Rp + r]);
+        const std::uint32_t words = mask_words(a);
+        PlaneSum acc{};  // the identity: no first record
+        for (std::size_t t = t0; t < t1; ++t) {
+            if (touched(tmask, words, t, r)) {
+                acc = plane_compose(a, acc, psum[t * a.Rp + r]);
+            }
         }
         gpsum[g * a.Rp + r] = acc;
     } else if (r < a.Rp + a.Rc) {
@@ -1084,6 +1387,7 @@ __global__ __launch_bounds__(64) void k_carry_mid(KArgs a, std::size_t ngroups,
 // writes every tile's carry-in.
 __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
                                                     std::size_t ngroups, const PlaneSum* psum,
+                                                    const std::uint64_t* tmask,
                                                     const ChanSum* csum,
                                                     const std::uint64_t* tile_count,
                                                     const PlaneCarry* gpcarry,
@@ -1102,8 +1406,12 @@ __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
     const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
     if (r < a.Rp) {
         const PlaneCarry c0 = gpcarry[g * a.Rp + r];
+        const std::uint32_t words = mask_words(a);
         std::uint64_t busy = c0.busy, tag1 = c0.tag1;
         for (std::size_t t = t0; t < t1; ++t) {
+            if (!touched(tmask, words, t, r)) {
+                continue;  // the tile neither reads nor changes this plane
+            }
             PlaneCarry c;
             c.busy = busy;
             c.tag1 = tag1;
@@ -1150,26 +1458,127 @@ __device__ __forceinline__ std::uint64_t wave_max(std::uint64_t v)
     return v;
 }
 
+// Replays a batch of linear steps from the plane and channel state and writes
+// their completions.  Per step, lane 0 senses unless its page is the one the
+// plane last read (with contention the plane is busy from max(busy, issue)
+// for the sense, and the hits after it end at the same time); the channel
+// moves the 64 records back to back from max(channel busy, issue).  The
+// step-level maps are scanned across the batch exactly as records are in the
+// general path; then every step's 64 completions follow in closed form:
+//   plane  lane 0: lead = max(busy, issue) + sense (busy ignored without
+//          contention); lanes 1..63: lead with contention, else issue;
+//   channel lane j: top - x (63 - j), top = max(busy, issue) + 64 x.
+struct ApplySums {
+    std::uint64_t n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq;
+};
+
+__device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* xp,
+                                           const LinBatch& q, int lane, std::uint64_t* p_busy,
+                                           std::uint64_t* c_busy, std::uint32_t* p_tag,
+                                           std::uint64_t* completion, std::uint8_t* status,
+                                           ApplySums& t)
+{
+    const StepView v = step_view(a, xp, q, lane);
+    const bool m = v.m;
+    const std::uint32_t pkey = m ? v.d.plane : 0u;
+    const std::uint32_t ckey = m ? v.d.chan : 0u;
+    const Group gp = group_by(pkey, a.pbits, m, v.active, lane);
+    const Group gc = group_by(ckey, a.cbits, m, v.active, lane);
+    const std::uint32_t tag = m ? p_tag[pkey] : 0u;
+    const std::uint64_t pbusy = m ? p_busy[pkey] : 0ull;
+    const std::uint64_t cbusy = m ? c_busy[ckey] : 0ull;
+    std::uint32_t prev1 = static_cast<std::uint32_t>(
+        __shfl(static_cast<int>(q.page1), gp.pred < 0 ? lane : gp.pred));
+    if (gp.pred < 0) {
+        prev1 = tag;
+    }
+    const bool lhit = m && prev1 == q.page1;
+    const std::uint64_t ls = lhit ? 0ull : a.read_ps;
+    const std::uint64_t cx = 64 * v.x;
+    std::uint64_t Ap = 0, Bp = 0, Ac = 0, Bc = 0;
+    if (m) {
+        Ap = ls;
+        Bp = q.issue + ls;
+        Ac = cx;
+        Bc = q.issue + cx;
+    }
+    if (a.contention) {
+        scan_pair(gp, Ap, Bp, gc, Ac, Bc, v.d, m, v.active, ls, cx, lane);
+    } else {
+        scan_group(gc, Ac, Bc, lane);
+    }
+    const std::uint64_t lead = a.contention ? umax64(pbusy + Ap, Bp) : q.issue + ls;
+    const std::uint64_t top = umax64(cbusy + Ac, Bc);
+    if (m && lane == gp.last) {
+        if (a.contention) {
+            p_busy[pkey] = lead;
+        }
+        p_tag[pkey] = q.page1;
+    }
+    if (m && lane == gc.last) {
+        c_busy[ckey] = top;
+    }
+    // accounting: every lane gets one record of each step; all are modeled
+    // reads, lanes 1..63 hit, lane 0 hits when its page was buffered
+    const std::uint64_t nq = static_cast<std::uint64_t>(q.n);
+    const std::uint64_t hits = __ballot(lhit);  // (every lane takes part)
+    t.n_rec += nq;
+    t.n_mod += nq;
+    t.n_rd += nq;
+    t.n_hit += lane == 0 ? static_cast<std::uint64_t>(__popcll(hits)) : nq;
+    const std::uint64_t sx = wave_sum(v.x);                        // lanes 1..63: service x
+    const std::uint64_t s0 = wave_sum(m ? umax64(ls, v.x) : 0ull);  // lane 0: max(sense, x)
+    t.svc_sum += lane == 0 ? s0 : sx;
+    t.seq += 64 * nq;
+    const std::uint64_t back = static_cast<std::uint64_t>(63 - lane);
+    for (int k = 0; k < q.n; ++k) {
+        const std::uint64_t lead_k = readlane64(lead, k);
+        const std::uint64_t top_k = readlane64(top, k);
+        const std::uint64_t i0 = readlane64(q.issue, k);
+        const std::uint64_t x = readlane64(v.x, k);
+        const std::uint64_t pd = (lane == 0 || a.contention) ? lead_k : i0;
+        const std::uint64_t done = umax64(pd, top_k - x * back);
+        t.mk = umax64(t.mk, done);
+        const std::uint64_t lat = done - i0;
+        add128(t.lat_lo, t.lat_hi, lat);
+        t.lat_max = umax64(t.lat_max, lat);
+        const std::size_t i = q.first + static_cast<std::size_t>(k) * kWave + lane;
+        completion[i] = done;
+        if (status != nullptr) {
+            const bool hit = lane != 0 || ((hits >> k) & 1u) != 0;
+            status[i] = static_cast<std::uint8_t>(hit ? 4u : 0u);
+        }
+    }
+}
+
 template <bool kRefresh, bool kHits>
 __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, std::size_t n,
                                               std::uint64_t base_ps, const PlaneCarry* pcarry,
+                                              const std::uint64_t* tmask,
                                               const std::uint64_t* ccarry,
                                               const std::uint64_t* tile_seq,
                                               std::uint64_t* completion, std::uint8_t* status,
-                                              DevReport* tile_rep, const std::uint8_t* hits)
+                                              DevReport* tile_rep, const std::uint8_t* hits,
+                                              const StepDesc* desc)
 {
     extern __shared__ std::uint64_t sm[];
     std::uint64_t* fence = sm;
     std::uint64_t* p_busy = fence + a.r_nfence;
     std::uint64_t* c_busy = p_busy + a.Rp;
     std::uint32_t* p_tag = reinterpret_cast<std::uint32_t*>(c_busy + a.Rc);
+    __shared__ std::uint64_t xp[33];
     const int lane = threadIdx.x;
     const std::size_t tile = blockIdx.x;
     load_fences(a, fence, lane);
+    load_xfer_table(a, xp, lane);
+    // carry-ins exist for the planes the tile touches, the only ones it reads
+    const std::uint32_t words = mask_words(a);
     for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
-        const PlaneCarry c = pcarry[tile * a.Rp + r];
-        p_busy[r] = c.busy;
-        p_tag[r] = static_cast<std::uint32_t>(c.tag1);
+        if (touched(tmask, words, tile, r)) {
+            const PlaneCarry c = pcarry[tile * a.Rp + r];
+            p_busy[r] = c.busy;
+            p_tag[r] = static_cast<std::uint32_t>(c.tag1);
+        }
     }
     for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
         c_busy[r] = ccarry[tile * a.Rc + r];
@@ -1183,212 +1592,224 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
     std::uint64_t lat_max = 0, svc_sum = 0;
     RangeCache rc = empty_cache();
     RangeCache rcu = empty_cache();  // wave-uniform copy for linear steps
-    uint4 x0 = make_uint4(0, 0, 0, 0), y0 = x0, x1 = x0, y1 = x0;
-    if (begin + lane < end) load_record(rec, begin + lane, x0, y0);
-    if (begin + kWave + lane < end) load_record(rec, begin + kWave + lane, x1, y1);
-    for (std::size_t s = begin; s < end; s += kWave) {
-        const uint4 x = x0, y = y0;
-        x0 = x1;
-        y0 = y1;
-        if (s + 2 * kWave + lane < end) load_record(rec, s + 2 * kWave + lane, x1, y1);
-        const std::size_t i = s + lane;
-        const bool valid = i < end;
-        if (!kHits && a.slots == 1 && !a.hybrid) {
-            const Linear L = linear_step<kRefresh>(a, fence, rcu, x, y, base_ps,
-                                                   s + kWave <= end, lane);
-            if (L.ok) {
-                const std::uint32_t pkey = L.d.plane;
-                const std::uint32_t ckey = L.d.chan;
-                const std::uint32_t page1 = static_cast<std::uint32_t>(L.d.page1);
-                const std::uint64_t i0 = L.d.issue;
-                const std::uint64_t xf = L.xfer;
-                const std::uint32_t tag = p_tag[pkey];
-                const std::uint64_t pbusy = p_busy[pkey];
-                const std::uint64_t cbusy = c_busy[ckey];
-                const bool lhit = tag == page1;
-                const std::uint64_t ls = lhit ? 0ull : a.read_ps;
-                // lane 0 pays the sense; the rest hit.  With contention the
-                // plane is busy until `lead` (>= i0) for every lane.
-                const std::uint64_t lead = a.contention ? umax64(pbusy, i0) + ls : i0 + ls;
-                const std::uint64_t pd = (lane == 0 || a.contention) ? lead : i0;
-                const std::uint64_t cd =
-                    umax64(cbusy, i0) + xf * static_cast<std::uint64_t>(lane + 1);
-                if (lane == 63) {
-                    if (a.contention) {
-                        p_busy[pkey] = pd;
-                    }
-                    p_tag[pkey] = page1;
-                    c_busy[ckey] = cd;
-                }
-                const std::uint64_t done = umax64(pd, cd);
-                const bool hit = lane == 0 ? lhit : true;
-                const std::uint64_t svc = lane == 0 ? ls : 0ull;
-                ++n_rec;
-                ++n_mod;
-                ++n_rd;
-                n_hit += hit ? 1u : 0u;
-                mk = umax64(mk, done);
-                const std::uint64_t lat = done - i0;
-                add128(lat_lo, lat_hi, lat);
-                lat_max = umax64(lat_max, lat);
-                svc_sum += umax64(svc, xf);
-                seq += kWave;
-                completion[i] = done;
-                if (status != nullptr) {
-                    status[i] = static_cast<std::uint8_t>(hit ? 4u : 0u);
-                }
+    LinBatch q = empty_batch();
+    const auto fold = [&]() {
+        ApplySums t{n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq};
+        fold_apply(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t);
+        n_rec = t.n_rec;
+        n_mod = t.n_mod;
+        n_rd = t.n_rd;
+        n_hit = t.n_hit;
+        mk = t.mk;
+        lat_lo = t.lat_lo;
+        lat_hi = t.lat_hi;
+        lat_max = t.lat_max;
+        svc_sum = t.svc_sum;
+        seq = t.seq;
+        q.n = 0;
+    };
+    // Windows of 64 steps.  A window whose steps the summary pass found all
+    // linear is replayed from their descriptors alone, without reading its
+    // records; any other window streams its records through the pipeline.
+    for (std::size_t w0 = begin; w0 < end; w0 += kWave * kWave) {
+        const std::size_t wend = w0 + kWave * kWave < end ? w0 + kWave * kWave : end;
+        if (desc != nullptr) {
+            const int nst = static_cast<int>((wend - w0 + kWave - 1) / kWave);
+            StepDesc sd{0, 0, 0};
+            if (lane < nst) {
+                sd = desc[w0 / kWave + lane];
+            }
+            const std::uint64_t all = nst == kWave ? ~0ull : ((1ull << nst) - 1);
+            if (__ballot(lane < nst && sd.bytes != 0) == all) {
+                q.page1 = sd.page1;
+                q.bytes = sd.bytes;
+                q.issue = sd.issue;
+                q.first = w0;
+                q.n = nst;
+                fold();
                 continue;
             }
         }
-        const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
-        const bool m = valid && d.cls == kClsModeled;
-        const bool hbit = kHits && valid && hits[i] != 0;
-        const std::uint64_t active = __ballot(m);
-        std::uint8_t st = static_cast<std::uint8_t>(d.cls);
-        std::uint64_t done = 0;
-        if (!kHits && active != 0 && run_step(a, d, active, lane)) {
-            const std::uint64_t xfer = lane_xfer(a, d, m, active);
-            const std::uint64_t W = run_channel_max(d, xfer, lane);
-            const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
-            const std::uint32_t pkey = d.plane;
-            const std::uint32_t ckey = d.chan;
-            const std::uint32_t tag = p_tag[pkey];
-            const std::uint64_t pbusy = p_busy[pkey];
-            const std::uint64_t cbusy = c_busy[ckey];
-            const std::uint64_t i0 = readlane64(d.issue, 0);
-            const bool lhit = tag == page1;
-            const std::uint64_t ls = lhit ? 0ull : a.read_ps;
-            const std::uint64_t lead = a.contention ? umax64(pbusy, i0) + ls : i0 + ls;
-            std::uint64_t pd;
-            if (lane == 0) {
-                pd = lead;
-            } else {
-                pd = a.contention ? umax64(lead, d.issue) : d.issue;
-            }
-            const std::uint64_t k1 = static_cast<std::uint64_t>(lane + 1);
-            const std::uint64_t cd = umax64(cbusy + xfer * k1,
-                                            lane == 63 ? W + xfer
-                                                       : W - xfer * static_cast<std::uint64_t>(
-                                                                        62 - lane));
-            if (lane == 63) {
-                if (a.contention) {
-                    p_busy[pkey] = pd;
-                }
-                p_tag[pkey] = page1;
-                c_busy[ckey] = cd;
-            }
-            done = umax64(pd, cd);
-            const bool hit = lane == 0 ? lhit : true;
-            const std::uint64_t svc = lane == 0 ? ls : 0ull;
-            if (a.hybrid) {
-                const std::uint64_t q = seq + static_cast<std::uint64_t>(lane);
-                const std::uint64_t key = ((d.page1 - 1) << a.page_shift) ^
-                                          (static_cast<std::uint64_t>(d.range_id) << 32);
-                if (q < a.hybrid_warmup ||
-                    (a.hybrid_threshold != 0 && mix64(q ^ key) <= a.hybrid_threshold)) {
-                    st |= 8u;
-                    ++n_hyb;
-                }
-            }
-            ++n_mod;
-            ++n_rd;
-            if (hit) {
-                st |= 4u;
-                ++n_hit;
-            }
-            mk = umax64(mk, done);
-            const std::uint64_t lat = done - d.issue;
-            add128(lat_lo, lat_hi, lat);
-            lat_max = umax64(lat_max, lat);
-            svc_sum += umax64(svc, xfer);
-            seq += 64;
-        } else if (active != 0) {
-            const std::uint64_t xfer = lane_xfer(a, d, m, active);
-            const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
-            const std::uint32_t pkey = m ? d.plane : 0u;
-            const std::uint32_t ckey = m ? d.chan : 0u;
-            const Group gp = group_by(pkey, a.pbits, m, active, lane);
-            const Group gc = group_by(ckey, a.cbits, m, active, lane);
-            // state reads come before this step's writes
-            const std::uint32_t tag = m ? p_tag[pkey] : 0u;
-            const std::uint64_t pbusy = m ? p_busy[pkey] : 0ull;
-            const std::uint64_t cbusy = m ? c_busy[ckey] : 0ull;
-            std::uint32_t prev1 = static_cast<std::uint32_t>(
-                __shfl(static_cast<int>(page1), gp.pred < 0 ? lane : gp.pred));
-            if (gp.pred < 0) {
-                prev1 = tag;
-            }
-            const bool hit = kHits ? (m && hbit) : (a.slots != 0 && m && prev1 == page1);
-            const std::uint64_t svc = plane_service(a, d.bits, hit);
-            std::uint64_t Ap = m ? svc : 0ull;
-            std::uint64_t Bp = m ? d.issue + svc : 0ull;
-            std::uint64_t Ac = m ? xfer : 0ull;
-            std::uint64_t Bc = m ? d.issue + xfer : 0ull;
-            if (a.contention) {
-                scan_pair(gp, Ap, Bp, gc, Ac, Bc, d, m, active, svc, xfer, lane);
-            } else {
-                scan_group(gc, Ac, Bc, lane);
-            }
-            const std::uint64_t pd =
-                a.contention ? (m ? umax64(pbusy + Ap, Bp) : 0ull) : d.issue + svc;
-            const std::uint64_t cd = m ? umax64(cbusy + Ac, Bc) : 0ull;
-            if (m && lane == gp.last) {
-                if (a.contention) {
-                    p_busy[pkey] = pd;
-                }
-                p_tag[pkey] = page1;
-            }
-            if (m && lane == gc.last) {
-                c_busy[ckey] = cd;
-            }
-            if (m) {
-                done = umax64(pd, cd);
-                const std::uint64_t rank = __popcll(active & lanemask_lt(lane));
-                const std::uint64_t q = seq + rank;
-                if (a.hybrid) {
-                    const std::uint64_t key = ((d.page1 - 1) << a.page_shift) ^
-                                              (static_cast<std::uint64_t>(d.range_id) << 32) ^
-                                              dec_op(d.bits);
-                    if (q < a.hybrid_warmup ||
-                        (a.hybrid_threshold != 0 && mix64(q ^ key) <= a.hybrid_threshold)) {
-                        st |= 8u;
-                        ++n_hyb;
+        RecordPipe pipe;
+        pipe.issue(rec, w0, wend, lane);
+        for (std::size_t g = w0; g < wend; g += kGroupSpan) {
+            pipe.advance(rec, g + kGroupSpan, wend, lane);
+            const std::size_t gend = g + kGroupSpan < wend ? g + kGroupSpan : wend;
+            for (std::size_t s = g; s < gend; s += kWave) {
+                uint4 A, B;
+                pipe.take(A, B);
+                const std::size_t i = s + lane;
+                const bool valid = i < end;
+                if (!kHits && a.slots == 1 && !a.hybrid) {
+                    // batched as in the summary pass
+                    std::uint32_t lp, lb;
+                    std::uint64_t li;
+                    const bool lin = linear_detect<kRefresh>(a, fence, rcu, A, B, base_ps,
+                                                             s + kWave <= end, lane, lp, li, lb);
+                    if (lin) {
+                        q.push(lp, li, lb, s);
+                    }
+                    if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= wend)) {
+                        fold();
+                    }
+                    if (lin) {
+                        continue;
                     }
                 }
-                ++n_mod;
-                if ((d.bits & 1u) == 0) {
+                uint4 x, y;
+                to_records(A, B, lane, x, y);
+                const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
+                const bool m = valid && d.cls == kClsModeled;
+                const bool hbit = kHits && valid && hits[i] != 0;
+                const std::uint64_t active = __ballot(m);
+                std::uint8_t st = static_cast<std::uint8_t>(d.cls);
+                std::uint64_t done = 0;
+                if (!kHits && active != 0 && run_step(a, d, active, lane)) {
+                    const std::uint64_t xfer = lane_xfer(a, xp, d, m, active);
+                    const std::uint64_t W = run_channel_max(d, xfer, lane);
+                    const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
+                    const std::uint32_t pkey = d.plane;
+                    const std::uint32_t ckey = d.chan;
+                    const std::uint32_t tag = p_tag[pkey];
+                    const std::uint64_t pbusy = p_busy[pkey];
+                    const std::uint64_t cbusy = c_busy[ckey];
+                    const std::uint64_t i0 = readlane64(d.issue, 0);
+                    const bool lhit = tag == page1;
+                    const std::uint64_t ls = lhit ? 0ull : a.read_ps;
+                    const std::uint64_t lead = a.contention ? umax64(pbusy, i0) + ls : i0 + ls;
+                    std::uint64_t pd;
+                    if (lane == 0) {
+                        pd = lead;
+                    } else {
+                        pd = a.contention ? umax64(lead, d.issue) : d.issue;
+                    }
+                    const std::uint64_t k1 = static_cast<std::uint64_t>(lane + 1);
+                    const std::uint64_t back = static_cast<std::uint64_t>(62 - lane);
+                    const std::uint64_t cd =
+                        umax64(cbusy + xfer * k1, lane == 63 ? W + xfer : W - xfer * back);
+                    if (lane == 63) {
+                        if (a.contention) {
+                            p_busy[pkey] = pd;
+                        }
+                        p_tag[pkey] = page1;
+                        c_busy[ckey] = cd;
+                    }
+                    done = umax64(pd, cd);
+                    const bool hit = lane == 0 ? lhit : true;
+                    const std::uint64_t svc = lane == 0 ? ls : 0ull;
+                    if (a.hybrid) {
+                        const std::uint64_t qn = seq + static_cast<std::uint64_t>(lane);
+                        const std::uint64_t key = ((d.page1 - 1) << a.page_shift) ^
+                                                  (static_cast<std::uint64_t>(d.range_id) << 32);
+                        if (qn < a.hybrid_warmup ||
+                            (a.hybrid_threshold != 0 && mix64(qn ^ key) <= a.hybrid_threshold)) {
+                            st |= 8u;
+                            ++n_hyb;
+                        }
+                    }
+                    ++n_mod;
                     ++n_rd;
                     if (hit) {
                         st |= 4u;
                         ++n_hit;
                     }
-                } else {
-                    n_wr += (d.bits & 4u) ? 0u : 1u;
-                    if (svc != 0) {
-                        st |= 16u;
-                        ++n_prog;
+                    mk = umax64(mk, done);
+                    const std::uint64_t lat = done - d.issue;
+                    add128(lat_lo, lat_hi, lat);
+                    lat_max = umax64(lat_max, lat);
+                    svc_sum += umax64(svc, xfer);
+                    seq += 64;
+                } else if (active != 0) {
+                    const std::uint64_t xfer = lane_xfer(a, xp, d, m, active);
+                    const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
+                    const std::uint32_t pkey = m ? d.plane : 0u;
+                    const std::uint32_t ckey = m ? d.chan : 0u;
+                    const Group gp = group_by(pkey, a.pbits, m, active, lane);
+                    const Group gc = group_by(ckey, a.cbits, m, active, lane);
+                    // state reads come before this step's writes
+                    const std::uint32_t tag = m ? p_tag[pkey] : 0u;
+                    const std::uint64_t pbusy = m ? p_busy[pkey] : 0ull;
+                    const std::uint64_t cbusy = m ? c_busy[ckey] : 0ull;
+                    std::uint32_t prev1 = static_cast<std::uint32_t>(
+                        __shfl(static_cast<int>(page1), gp.pred < 0 ? lane : gp.pred));
+                    if (gp.pred < 0) {
+                        prev1 = tag;
+                    }
+                    const bool hit = kHits ? (m && hbit) : (a.slots != 0 && m && prev1 == page1);
+                    const std::uint64_t svc = plane_service(a, d.bits, hit);
+                    std::uint64_t Ap = m ? svc : 0ull;
+                    std::uint64_t Bp = m ? d.issue + svc : 0ull;
+                    std::uint64_t Ac = m ? xfer : 0ull;
+                    std::uint64_t Bc = m ? d.issue + xfer : 0ull;
+                    if (a.contention) {
+                        scan_pair(gp, Ap, Bp, gc, Ac, Bc, d, m, active, svc, xfer, lane);
+                    } else {
+                        scan_group(gc, Ac, Bc, lane);
+                    }
+                    const std::uint64_t pd =
+                        a.contention ? (m ? umax64(pbusy + Ap, Bp) : 0ull) : d.issue + svc;
+                    const std::uint64_t cd = m ? umax64(cbusy + Ac, Bc) : 0ull;
+                    if (m && lane == gp.last) {
+                        if (a.contention) {
+                            p_busy[pkey] = pd;
+                        }
+                        p_tag[pkey] = page1;
+                    }
+                    if (m && lane == gc.last) {
+                        c_busy[ckey] = cd;
+                    }
+                    if (m) {
+                        done = umax64(pd, cd);
+                        const std::uint64_t rank = __popcll(active & lanemask_lt(lane));
+                        const std::uint64_t qn = seq + rank;
+                        if (a.hybrid) {
+                            const std::uint64_t key =
+                                ((d.page1 - 1) << a.page_shift) ^
+                                (static_cast<std::uint64_t>(d.range_id) << 32) ^ dec_op(d.bits);
+                            const bool sampled =
+                                qn < a.hybrid_warmup ||
+                                (a.hybrid_threshold != 0 && mix64(qn ^ key) <= a.hybrid_threshold);
+                            if (sampled) {
+                                st |= 8u;
+                                ++n_hyb;
+                            }
+                        }
+                        ++n_mod;
+                        if ((d.bits & 1u) == 0) {
+                            ++n_rd;
+                            if (hit) {
+                                st |= 4u;
+                                ++n_hit;
+                            }
+                        } else {
+                            n_wr += (d.bits & 4u) ? 0u : 1u;
+                            if (svc != 0) {
+                                st |= 16u;
+                                ++n_prog;
+                            }
+                        }
+                        mk = umax64(mk, done);
+                        const std::uint64_t lat = done - d.issue;
+                        add128(lat_lo, lat_hi, lat);
+                        lat_max = umax64(lat_max, lat);
+                        svc_sum += umax64(svc, xfer);
+                    }
+                    seq += __popcll(active);
+                }
+                if (valid) {
+                    ++n_rec;
+                    if (d.cls == kClsBypass) {
+                        done = d.issue;
+                        ++n_byp;
+                    } else if (d.cls == kClsUnsupported) {
+                        done = ~0ull;
+                        ++n_uns;
+                    }
+                    completion[i] = done;
+                    if (status != nullptr) {
+                        status[i] = st;
                     }
                 }
-                mk = umax64(mk, done);
-                const std::uint64_t lat = done - d.issue;
-                add128(lat_lo, lat_hi, lat);
-                lat_max = umax64(lat_max, lat);
-                svc_sum += umax64(svc, xfer);
-            }
-            seq += __popcll(active);
-        }
-        if (valid) {
-            ++n_rec;
-            if (d.cls == kClsBypass) {
-                done = d.issue;
-                ++n_byp;
-            } else if (d.cls == kClsUnsupported) {
-                done = ~0ull;
-                ++n_uns;
-            }
-            completion[i] = done;
-            if (status != nullptr) {
-                status[i] = st;
             }
         }
     }
@@ -1500,6 +1921,7 @@ struct engine {
     // scratch
     std::size_t tile_cap{0};
     PlaneSum* d_psum{nullptr};
+    std::uint64_t* d_tmask{nullptr};  // touched planes per tile
     ChanSum* d_csum{nullptr};
     PlaneCarry* d_pcarry{nullptr};
     std::uint64_t* d_ccarry{nullptr};
@@ -1512,6 +1934,8 @@ struct engine {
     std::uint64_t* d_gcount{nullptr};
     std::uint64_t* d_gseq{nullptr};
     DevReport* d_tile_rep{nullptr};
+    StepDesc* d_desc{nullptr};  // per-step descriptors (records / 64)
+    std::size_t desc_cap{0};
     hipEvent_t ev[4]{};
     float last_ms[3]{0, 0, 0};
     std::uint64_t burst{0};
@@ -1559,6 +1983,7 @@ std::uint32_t log2u(std::uint64_t v)
 void free_scratch(engine* e)
 {
     hfree(e->d_psum);
+    hfree(e->d_tmask);
     hfree(e->d_csum);
     hfree(e->d_pcarry);
     hfree(e->d_ccarry);
@@ -1571,6 +1996,8 @@ void free_scratch(engine* e)
     hfree(e->d_gcount);
     hfree(e->d_gseq);
     hfree(e->d_tile_rep);
+    hfree(e->d_desc);
+    e->desc_cap = 0;
     e->tile_cap = 0;
 }
 
@@ -1582,7 +2009,9 @@ int ensure_scratch(engine* e, std::size_t ntiles)
     free_scratch(e);
     const std::size_t cap = std::max<std::size_t>(ntiles, 16);
     const std::size_t rp = e->args.Rp, rc = e->args.Rc;
-    if (halloc(e->d_psum, cap * rp) != hipSuccess || halloc(e->d_csum, cap * rc) != hipSuccess ||
+    if (halloc(e->d_psum, cap * rp) != hipSuccess ||
+        halloc(e->d_tmask, cap * mask_words(e->args)) != hipSuccess ||
+        halloc(e->d_csum, cap * rc) != hipSuccess ||
         halloc(e->d_pcarry, cap * rp) != hipSuccess ||
         halloc(e->d_ccarry, cap * rc) != hipSuccess || halloc(e->d_tcount, cap) != hipSuccess ||
         halloc(e->d_tseq, cap) != hipSuccess) {
@@ -3029,19 +3458,36 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         }
         a.ext_hits = 1;
     }
+    // step descriptors, where the apply pass replays linear steps from them
+    StepDesc* desc = nullptr;
+    if (!k2 && a.slots == 1 && a.hybrid == 0) {
+        const std::size_t nsteps = (n + kWave - 1) / kWave;
+        if (nsteps > e->desc_cap) {
+            hfree(e->d_desc);
+            e->desc_cap = 0;
+            if (halloc(e->d_desc, nsteps) != hipSuccess) {
+                return HBFSIM_CUDA_ERROR;
+            }
+            e->desc_cap = nsteps;
+        }
+        desc = e->d_desc;
+    }
     const dim3 grid(static_cast<unsigned>(ntiles));
     const unsigned carry_blocks = (a.Rp + a.Rc + 1 + kWave - 1) / kWave;
     (void)hipEventRecord(e->ev[0], stream);
     const std::uint8_t* hits = d_hits;
     if (k2) {
         hipLaunchKernelGGL((k_summary<false, true>), grid, dim3(kWave), lds_a, stream, a, d_rec,
-                           n, base_ps, e->d_psum, e->d_csum, e->d_tcount, hits);
+                           n, base_ps, e->d_psum, e->d_tmask, e->d_csum, e->d_tcount,
+                           hits, desc);
     } else if (refresh_records) {
         hipLaunchKernelGGL((k_summary<true, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
-                           n, base_ps, e->d_psum, e->d_csum, e->d_tcount, hits);
+                           n, base_ps, e->d_psum, e->d_tmask, e->d_csum, e->d_tcount,
+                           hits, desc);
     } else {
         hipLaunchKernelGGL((k_summary<false, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
-                           n, base_ps, e->d_psum, e->d_csum, e->d_tcount, hits);
+                           n, base_ps, e->d_psum, e->d_tmask, e->d_csum, e->d_tcount,
+                           hits, desc);
     }
     (void)hipEventRecord(e->ev[1], stream);
     {
@@ -3049,29 +3495,29 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         const std::size_t rt = static_cast<std::size_t>(a.Rp) + a.Rc + 1;
         const unsigned wide = static_cast<unsigned>((ngroups * rt + 255) / 256);
         hipLaunchKernelGGL(k_carry_up, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
-                           e->d_psum, e->d_csum, e->d_tcount, e->d_gpsum, e->d_gcsum,
-                           e->d_gcount);
+                           e->d_psum, e->d_tmask, e->d_csum, e->d_tcount, e->d_gpsum,
+                           e->d_gcsum, e->d_gcount);
         hipLaunchKernelGGL(k_carry_mid, dim3(carry_blocks), dim3(kWave), 0, stream, a, ngroups,
                            e->d_gpsum, e->d_gcsum, e->d_gcount, e->d_gpcarry, e->d_gccarry,
                            e->d_gseq, e->d_pbusy, e->d_ptag, e->d_cbusy, e->d_seq, e->d_ptot,
                            e->d_ctot);
         hipLaunchKernelGGL(k_carry_down, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
-                           e->d_psum, e->d_csum, e->d_tcount, e->d_gpcarry, e->d_gccarry,
-                           e->d_gseq, e->d_pcarry, e->d_ccarry, e->d_tseq);
+                           e->d_psum, e->d_tmask, e->d_csum, e->d_tcount, e->d_gpcarry,
+                           e->d_gccarry, e->d_gseq, e->d_pcarry, e->d_ccarry, e->d_tseq);
     }
     (void)hipEventRecord(e->ev[2], stream);
     if (k2) {
         hipLaunchKernelGGL((k_apply<false, true>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
-                           base_ps, e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status,
-                           e->d_tile_rep, hits);
+                           base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
+                           d_status, e->d_tile_rep, hits, desc);
     } else if (refresh_records) {
         hipLaunchKernelGGL((k_apply<true, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
-                           base_ps, e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status,
-                           e->d_tile_rep, hits);
+                           base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
+                           d_status, e->d_tile_rep, hits, desc);
     } else {
         hipLaunchKernelGGL((k_apply<false, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
-                           base_ps, e->d_pcarry, e->d_ccarry, e->d_tseq, d_comp, d_status,
-                           e->d_tile_rep, hits);
+                           base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
+                           d_status, e->d_tile_rep, hits, desc);
     }
     hipLaunchKernelGGL(k_report, dim3(1), dim3(256), 0, stream, e->d_tile_rep, ntiles, e->d_rep);
     (void)hipEventRecord(e->ev[3], stream);

@@ -1,0 +1,163 @@
+"""Linear steps (64 reads addr_0 + k * bytes_0 with one issue time, inside one
+page) take a batched path on the GPU: they wait in a batch of up to 64 steps
+that is folded with one lane per step.  These streams mix such steps with
+steps that end a batch early (writes, page crossings, bypass and unreadable
+ranges, short or out-of-order steps), revisit planes and pages inside one
+batch, jump between ranges (the uniform range cache refills) and let issue
+times fall back, under every plane/transfer option; results must match the
+CPU oracle bit for bit."""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+import parity
+from test_gpu_parity import C0, C2, check
+
+pytestmark = pytest.mark.gpu
+
+PAGE = 16384
+BASE = 0x6400_0000_0000
+
+
+def ranges_for(count=6, pages=96):
+    """Readable ranges, plus a write-only one (range index `count`)."""
+    out = [(BASE + r * (pages + 8) * PAGE, pages * PAGE, 3 if r % 2 else 1) for r in range(count)]
+    out.append((BASE + count * (pages + 8) * PAGE, pages * PAGE, 2))
+    return out
+
+
+def linear_stream(seed, steps, ranges, kinds=None):
+    """One step at a time: mostly linear steps on a few hot pages (so later
+    steps of a batch hit pages earlier ones opened, on the same and other
+    planes), with breaking steps in between."""
+    rng = np.random.default_rng(seed)
+    kinds = kinds or {"lin": 0.80, "write": 0.03, "cross": 0.03, "bypass": 0.03,
+                      "wo": 0.02, "ragged": 0.03, "late": 0.03, "mixed_issue": 0.03}
+    names = list(kinds)
+    probs = np.array([kinds[k] for k in names], float)
+    probs /= probs.sum()
+    readable = [r for r in ranges if r[2] & 1]
+    wo = [r for r in ranges if not r[2] & 1]
+    hot = [(int(rng.integers(0, len(readable))), int(rng.integers(0, 96))) for _ in range(12)]
+    out = []
+    t = 10_000_000
+    lanes = np.arange(64, dtype=np.uint64)
+    for _ in range(steps):
+        kind = names[int(rng.choice(len(names), p=probs))]
+        b = int(rng.choice([64, 128, 256]))
+        ri, pg = hot[int(rng.integers(0, len(hot)))] if rng.random() < 0.7 else \
+            (int(rng.integers(0, len(readable))), int(rng.integers(0, 96)))
+        base, length, _ = readable[ri]
+        slot = int(rng.integers(0, PAGE // (64 * b)))
+        a0 = base + pg * PAGE + slot * 64 * b
+        t += int(rng.choice([0, 0, 500, 4000, 70_000]))
+        issue = t
+        step = np.zeros((64, 4), np.uint64)
+        step[:, 0] = np.uint64(a0) + lanes * np.uint64(b)
+        step[:, 1] = b
+        step[:, 2] = issue
+        if kind == "write":
+            step[int(rng.integers(0, 64)), 3] = 1
+        elif kind == "cross":  # the step runs over the page end
+            step[:, 0] = np.uint64(base + pg * PAGE + PAGE - 32 * b) + lanes * np.uint64(b)
+            if pg == length // PAGE - 1:
+                step[:, 0] -= np.uint64(PAGE)
+        elif kind == "bypass":
+            step[:, 0] = np.uint64(0x1000) + lanes * np.uint64(b)
+        elif kind == "wo":
+            wb = wo[0][0]
+            step[:, 0] = np.uint64(wb + pg * PAGE) + lanes * np.uint64(b)
+        elif kind == "ragged":  # one lane's byte count differs
+            step[int(rng.integers(0, 64)), 1] = b // 2
+        elif kind == "late":  # issue time falls back far
+            step[:, 2] = max(0, issue - 9_000_000)
+        elif kind == "mixed_issue":
+            step[int(rng.integers(1, 64)):, 2] = issue + 1
+        out.append(step)
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("profile", [C0, C2], ids=["c0", "c2"])
+@pytest.mark.parametrize("options", [
+    dict(), dict(plane_contention=0), dict(transfer_page=1), dict(tile_records=64 * 64),
+    dict(tile_records=64 * 70),
+])
+def test_linear_batches_bit_exact(profile, options):
+    ranges = ranges_for()
+    rec = linear_stream(11, 1500, ranges)
+    p = parity.Pair(profile, ranges, **options)
+    try:
+        (_, _, grep), _ = check(p, rec, f"linear batches {profile.name} {options}")
+        assert grep["page_hits"] > 0 and grep["bypass"] > 0 and grep["unsupported"] > 0
+        p.check_state()
+    finally:
+        p.close()
+
+
+@pytest.mark.parametrize("n_linear", [1, 2, 63, 64, 65, 127, 128, 129, 4095, 4097])
+def test_linear_batch_lengths(n_linear):
+    """Runs of exactly n linear steps, then a breaking step, a tail of fewer
+    than 64 records, and runs that end exactly at the tile end."""
+    ranges = ranges_for()
+    rec = linear_stream(n_linear, n_linear, ranges, kinds={"lin": 1.0})
+    brk = linear_stream(n_linear + 1, 3, ranges, kinds={"write": 1.0})
+    tail = linear_stream(n_linear + 2, 1, ranges, kinds={"lin": 1.0})[:37]
+    stream = np.concatenate([rec, brk, rec, tail])
+    for tile in (None, 64 * 64, 64 * n_linear):
+        p = parity.Pair(C2, ranges, tile_records=tile)
+        try:
+            check(p, stream, f"{n_linear} linear steps, tile {tile}")
+            p.check_state()
+        finally:
+            p.close()
+
+
+@pytest.mark.parametrize("wide", ["issue", "sense", "transfer"])
+def test_linear_wide_times_take_64_bit_scans(tmp_path, wide):
+    """Values past the 32-bit relative scans inside one batch: issue gaps
+    beyond 2^30 ps between steps, a sense time of 4e7 ps (> 2^24), or a
+    transfer quantum that makes a step's channel time 2^26 ps."""
+    ranges = ranges_for()
+    rec = linear_stream(5, 600, ranges, kinds={"lin": 1.0})
+    profile, opts = C2, {}
+    if wide == "issue":
+        steps = rec.reshape(-1, 64, 4)
+        steps[:, :, 2] = (np.arange(steps.shape[0], dtype=np.uint64) *
+                          np.uint64(1_500_000_000))[:, None]
+    elif wide == "sense":
+        prof = json.loads(C2.read_text())
+        prof["read_latency_ns"] = 40_000
+        profile = tmp_path / "c2-slow-sense.json"
+        profile.write_text(json.dumps(prof))
+    else:
+        opts = dict(xfer_quantum_ps=1 << 20)
+    p = parity.Pair(profile, ranges, **opts)
+    try:
+        check(p, rec, f"wide linear steps ({wide})")
+        p.check_state()
+    finally:
+        p.close()
+
+
+def test_linear_split_runs_resume():
+    """A stream cut inside batches: the carried state after each run must let
+    the next run continue exactly."""
+    ranges = ranges_for()
+    rec = linear_stream(17, 900, ranges)
+    whole = parity.Pair(C2, ranges)
+    split = parity.Pair(C2, ranges)
+    try:
+        (gw, _, _), _ = check(whole, rec, "whole")
+        parts = []
+        for lo, hi in [(0, 64 * 10), (64 * 10, 64 * 10 + 5), (64 * 10 + 5, 64 * 500),
+                       (64 * 500, len(rec))]:
+            (g, _, _), _ = check(split, rec[lo:hi], f"part {lo}:{hi}")
+            parts.append(g)
+            split.check_state()
+        np.testing.assert_array_equal(np.concatenate(parts), gw)
+    finally:
+        whole.close()
+        split.close()
