@@ -783,6 +783,83 @@ __device__ __forceinline__ bool linear_detect(const KArgs& a, const std::uint64_
     return true;
 }
 
+// A linear group: kPipe consecutive linear steps continuing one another
+// (record r of the group at address a0 + r * bytes0), each step with its own
+// issue time, all inside the cached range.  Checked at once on the group's
+// registers: lane l looks at word pair l & 1 of records 64 j + 32 h + (l >> 1)
+// for every step j and half h.
+struct GroupLin {
+    std::uint32_t page1[kPipe];
+    std::uint64_t issue[kPipe];
+    std::uint32_t bytes;
+};
+
+template <bool kRefresh>
+__device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t* fence,
+                                             RangeCache& rcu, const RecordPipe& pipe,
+                                             std::uint64_t base_ps, int lane, GroupLin& gl)
+{
+    const uint4 xu = make_uint4(rfl32(pipe.ca[0].x), rfl32(pipe.ca[0].y), rfl32(pipe.ca[0].z),
+                                rfl32(pipe.ca[0].w));
+    const std::uint32_t op0 = rl32(pipe.ca[0].z, 1);
+    if ((op0 & 0xffu) != 0 || xu.w != 0 || xu.z == 0) {
+        return false;  // reads of 1 .. 2^32 - 1 bytes only
+    }
+    const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
+    const std::uint64_t b0 = xu.z;
+    const std::uint64_t half = 32ull * b0;  // bytes between the two halves of a step
+    const std::uint64_t mine = a0 + static_cast<std::uint64_t>(lane >> 1) * b0;
+    const bool odd = (lane & 1) != 0;
+    std::uint32_t ilo[kPipe], ihi[kPipe];
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < kPipe; ++j) {
+        ilo[j] = rl32(pipe.ca[j].x, 1);
+        ihi[j] = rl32(pipe.ca[j].y, 1);
+        const uint4& A = pipe.ca[j];
+        const uint4& B = pipe.cb[j];
+        const std::uint64_t ea = mine + static_cast<std::uint64_t>(2 * j) * half;
+        const std::uint64_t eb = ea + half;
+        const std::uint64_t wa = A.x | (static_cast<std::uint64_t>(A.y) << 32);
+        const std::uint64_t wb = B.x | (static_cast<std::uint64_t>(B.y) << 32);
+        const bool ev = wa == ea && A.z == xu.z && A.w == 0 && wb == eb && B.z == xu.z &&
+                        B.w == 0;
+        const bool od = A.x == ilo[j] && A.y == ihi[j] && A.z == op0 && B.x == ilo[j] &&
+                        B.y == ihi[j] && B.z == op0;
+        ok = ok && (odd ? od : ev);
+    }
+    if (__ballot(!ok) != 0) {
+        return false;
+    }
+    if (!(a0 >= rcu.base && a0 < rcu.end)) {
+        const uint4 yu = make_uint4(ilo[0], ihi[0], op0, 0);
+        const Dec d = decode<kRefresh, true>(a, fence, rcu, xu, yu, base_ps);
+        if (d.cls != kClsModeled) {
+            return false;
+        }
+    }
+    const std::uint32_t mode = rcu.meta & 0xffu;
+    const std::uint64_t step = 64ull * b0;
+    const std::uint64_t span = kPipe * step;
+    if ((mode != 1 && mode != 2) || (rcu.meta & (1u << 8)) == 0 || span > rcu.end - a0) {
+        return false;
+    }
+    const std::uint64_t page_mask = (1ull << a.page_shift) - 1;
+    const std::uint64_t off0 = a0 - rcu.base;
+#pragma unroll
+    for (int j = 0; j < kPipe; ++j) {
+        const std::uint64_t off = off0 + static_cast<std::uint64_t>(j) * step;
+        if ((off >> a.page_shift) != ((off + step - 1) >> a.page_shift) ||
+            (off & ~page_mask) > ~0ull - rcu.file_offset) {
+            return false;
+        }
+        gl.page1[j] = static_cast<std::uint32_t>(((rcu.file_offset + off) >> a.page_shift) + 1);
+        gl.issue[j] = base_ps + (ilo[j] | (static_cast<std::uint64_t>(ihi[j]) << 32));
+    }
+    gl.bytes = xu.z;
+    return true;
+}
+
 // What the summary pass learned about a step, for the apply pass: a linear
 // step's media page + 1, byte count and issue time (bytes == 0: any other
 // step).  Indexed by record index / 64.
@@ -814,6 +891,27 @@ struct LinBatch {
             issue = i0;
         }
         ++n;
+    }
+    // Appends a linear group's kPipe steps (needs n <= 64 - kPipe).
+    __device__ __forceinline__ void push_group(const GroupLin& gl, std::size_t s)
+    {
+        if (n == 0) {
+            first = s;
+        }
+        const int j = static_cast<int>(threadIdx.x) - n;
+        if (j >= 0 && j < kPipe) {
+            std::uint32_t p1 = gl.page1[0];
+            std::uint64_t i0 = gl.issue[0];
+#pragma unroll
+            for (int k = 1; k < kPipe; ++k) {
+                p1 = j == k ? gl.page1[k] : p1;
+                i0 = j == k ? gl.issue[k] : i0;
+            }
+            page1 = p1;
+            issue = i0;
+            bytes = gl.bytes;
+        }
+        n += kPipe;
     }
 };
 
@@ -1076,6 +1174,20 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     for (std::size_t g = begin; g < end; g += kGroupSpan) {
         pipe.advance(rec, g + kGroupSpan, end, lane);
         const std::size_t gend = g + kGroupSpan < end ? g + kGroupSpan : end;
+        if (!kHits && a.slots == 1 && g + kGroupSpan <= end && q.n <= kWave - kPipe) {
+            // a whole group of linear steps joins the batch at once
+            GroupLin gl;
+            if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
+                q.push_group(gl, g);
+                if (q.n == kWave || gend >= end) {
+                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
+                                 desc);
+                    modeled += static_cast<std::uint64_t>(q.n) * kWave;
+                    q.n = 0;
+                }
+                continue;
+            }
+        }
         for (std::size_t s = g; s < gend; s += kWave) {
             uint4 A, B;
             pipe.take(A, B);

@@ -161,3 +161,55 @@ def test_linear_split_runs_resume():
     finally:
         whole.close()
         split.close()
+
+
+def contiguous_stream(seed, runs, ranges):
+    """Runs of steps that continue one another in address (groups of four
+    such steps take the group path), started at arbitrary step offsets so
+    groups straddle pages, range ends and batch boundaries; issue times per
+    step or per run; occasional breaking records inside a run."""
+    rng = np.random.default_rng(seed)
+    readable = [r for r in ranges if r[2] & 1]
+    lanes = np.arange(64, dtype=np.uint64)
+    out = []
+    t = 5_000_000
+    for _ in range(runs):
+        base, length, _ = readable[int(rng.integers(0, len(readable)))]
+        b = int(rng.choice([64, 128, 256]))
+        steps = int(rng.integers(1, 41))
+        start = int(rng.integers(0, length // (64 * b))) * 64 * b
+        per_step_issue = rng.random() < 0.5
+        for k in range(steps):
+            a0 = base + start + k * 64 * b
+            if a0 + 64 * b > base + length:
+                a0 = base + length - 32 * b  # runs over the range end
+            if not per_step_issue and k % 4 == 0 or per_step_issue:
+                t += int(rng.choice([0, 300, 2000, 90_000]))
+            step = np.zeros((64, 4), np.uint64)
+            step[:, 0] = np.uint64(a0) + lanes * np.uint64(b)
+            step[:, 1] = b
+            step[:, 2] = t
+            r = rng.random()
+            if r < 0.02:
+                step[int(rng.integers(0, 64)), 3] = 1        # a write
+            elif r < 0.04:
+                step[int(rng.integers(0, 64)), 2] += 1       # one late record
+            elif r < 0.05:
+                step[int(rng.integers(0, 64)), 0] += 1       # one address off the line
+            out.append(step)
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("options", [dict(), dict(plane_contention=0), dict(transfer_page=1),
+                                     dict(tile_records=64 * 24)])
+def test_linear_groups_bit_exact(options):
+    ranges = ranges_for()
+    rec = contiguous_stream(23, 400, ranges)
+    for profile in (C0, C2):
+        p = parity.Pair(profile, ranges, **options)
+        try:
+            (_, _, grep), _ = check(p, rec, f"linear groups {profile.name} {options}")
+            assert grep["page_hits"] > 0
+            p.check_state()
+        finally:
+            p.close()
