@@ -1357,6 +1357,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
 // resource) at levels 1 and 3, one per resource at level 2.
 
 constexpr std::uint32_t kGroup = 64;
+constexpr int kChunk = 8;  // loads a carry thread keeps in flight
 
 __device__ __forceinline__ PlaneSum plane_compose(const KArgs& a, const PlaneSum& s1,
                                                   const PlaneSum& s2)
@@ -1422,20 +1423,45 @@ __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, s
     const std::uint32_t r = static_cast<std::uint32_t>(id - g * rt);
     const std::size_t t0 = g * kGroup;
     const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
+    // Loads go out kChunk at a time ahead of the (serial) composition, so a
+    // thread waits once per chunk rather than once per tile.
     if (r < a.Rp) {
         const std::uint32_t words = mask_words(a);
         PlaneSum acc{};  // the identity: no first record
-        for (std::size_t t = t0; t < t1; ++t) {
-            if (touched(tmask, words, t, r)) {
-                acc = plane_compose(a, acc, psum[t * a.Rp + r]);
+        for (std::size_t t = t0; t < t1; t += kChunk) {
+            bool hit[kChunk];
+            PlaneSum buf[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                hit[k] = t + k < t1 && touched(tmask, words, t + k, r);
+            }
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                if (hit[k]) {
+                    buf[k] = psum[(t + k) * a.Rp + r];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                if (hit[k]) {
+                    acc = plane_compose(a, acc, buf[k]);
+                }
             }
         }
         gpsum[g * a.Rp + r] = acc;
     } else if (r < a.Rp + a.Rc) {
         const std::uint32_t c = r - a.Rp;
-        ChanSum acc = csum[t0 * a.Rc + c];
-        for (std::size_t t = t0 + 1; t < t1; ++t) {
-            acc = chan_compose(acc, csum[t * a.Rc + c]);
+        ChanSum acc{0, 0};  // the identity
+        for (std::size_t t = t0; t < t1; t += kChunk) {
+            ChanSum buf[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                buf[k] = t + k < t1 ? csum[(t + k) * a.Rc + c] : ChanSum{0, 0};
+            }
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                acc = chan_compose(acc, buf[k]);
+            }
         }
         gcsum[g * a.Rc + c] = acc;
     } else {
@@ -1463,12 +1489,22 @@ __global__ __launch_bounds__(64) void k_carry_mid(KArgs a, std::size_t ngroups,
         std::uint64_t busy = st_pbusy[t];
         std::uint64_t tag1 = st_ptag[static_cast<std::size_t>(t) * 2];
         std::uint64_t total = 0;
-        for (std::size_t g = 0; g < ngroups; ++g) {
-            PlaneCarry c;
-            c.busy = busy;
-            c.tag1 = tag1;
-            gpcarry[g * a.Rp + t] = c;
-            total += plane_apply(a, gpsum[g * a.Rp + t], busy, tag1);
+        for (std::size_t g0 = 0; g0 < ngroups; g0 += kChunk) {
+            PlaneSum buf[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                buf[k] = g0 + k < ngroups ? gpsum[(g0 + k) * a.Rp + t] : PlaneSum{};
+            }
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                if (g0 + k < ngroups) {
+                    PlaneCarry c;
+                    c.busy = busy;
+                    c.tag1 = tag1;
+                    gpcarry[(g0 + k) * a.Rp + t] = c;
+                    total += plane_apply(a, buf[k], busy, tag1);
+                }
+            }
         }
         st_pbusy[t] = busy;
         st_ptag[static_cast<std::size_t>(t) * 2] = tag1;
@@ -1477,11 +1513,20 @@ __global__ __launch_bounds__(64) void k_carry_mid(KArgs a, std::size_t ngroups,
         const std::uint32_t c = t - a.Rp;
         std::uint64_t busy = st_cbusy[c];
         std::uint64_t total = 0;
-        for (std::size_t g = 0; g < ngroups; ++g) {
-            gccarry[g * a.Rc + c] = busy;
-            const ChanSum S = gcsum[g * a.Rc + c];
-            busy = umax64(busy + S.A, S.B);
-            total += S.A;
+        for (std::size_t g0 = 0; g0 < ngroups; g0 += kChunk) {
+            ChanSum buf[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                buf[k] = g0 + k < ngroups ? gcsum[(g0 + k) * a.Rc + c] : ChanSum{0, 0};
+            }
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                if (g0 + k < ngroups) {
+                    gccarry[(g0 + k) * a.Rc + c] = busy;
+                    busy = umax64(busy + buf[k].A, buf[k].B);
+                    total += buf[k].A;
+                }
+            }
         }
         st_cbusy[c] = busy;
         ctotal[c] += total;
@@ -1520,23 +1565,47 @@ __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
         const PlaneCarry c0 = gpcarry[g * a.Rp + r];
         const std::uint32_t words = mask_words(a);
         std::uint64_t busy = c0.busy, tag1 = c0.tag1;
-        for (std::size_t t = t0; t < t1; ++t) {
-            if (!touched(tmask, words, t, r)) {
-                continue;  // the tile neither reads nor changes this plane
+        for (std::size_t t = t0; t < t1; t += kChunk) {
+            bool hit[kChunk];
+            PlaneSum buf[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                hit[k] = t + k < t1 && touched(tmask, words, t + k, r);
             }
-            PlaneCarry c;
-            c.busy = busy;
-            c.tag1 = tag1;
-            pcarry[t * a.Rp + r] = c;
-            (void)plane_apply(a, psum[t * a.Rp + r], busy, tag1);
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                if (hit[k]) {
+                    buf[k] = psum[(t + k) * a.Rp + r];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                // an untouched tile neither reads nor changes this plane
+                if (hit[k]) {
+                    PlaneCarry c;
+                    c.busy = busy;
+                    c.tag1 = tag1;
+                    pcarry[(t + k) * a.Rp + r] = c;
+                    (void)plane_apply(a, buf[k], busy, tag1);
+                }
+            }
         }
     } else if (r < a.Rp + a.Rc) {
         const std::uint32_t c = r - a.Rp;
         std::uint64_t busy = gccarry[g * a.Rc + c];
-        for (std::size_t t = t0; t < t1; ++t) {
-            ccarry[t * a.Rc + c] = busy;
-            const ChanSum S = csum[t * a.Rc + c];
-            busy = umax64(busy + S.A, S.B);
+        for (std::size_t t = t0; t < t1; t += kChunk) {
+            ChanSum buf[kChunk];
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                buf[k] = t + k < t1 ? csum[(t + k) * a.Rc + c] : ChanSum{0, 0};
+            }
+#pragma unroll
+            for (int k = 0; k < kChunk; ++k) {
+                if (t + k < t1) {
+                    ccarry[(t + k) * a.Rc + c] = busy;
+                    busy = umax64(busy + buf[k].A, buf[k].B);
+                }
+            }
         }
     } else {
         std::uint64_t s = gseq[g];
@@ -2119,7 +2188,9 @@ int ensure_scratch(engine* e, std::size_t ntiles)
         return HBFSIM_OK;
     }
     free_scratch(e);
-    const std::size_t cap = std::max<std::size_t>(ntiles, 16);
+    // an eighth of headroom, so that batches a little larger than the last
+    // do not reallocate (freeing device memory synchronises the device)
+    const std::size_t cap = std::max<std::size_t>(ntiles + ntiles / 8, 16);
     const std::size_t rp = e->args.Rp, rc = e->args.Rc;
     if (halloc(e->d_psum, cap * rp) != hipSuccess ||
         halloc(e->d_tmask, cap * mask_words(e->args)) != hipSuccess ||
@@ -3577,10 +3648,11 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         if (nsteps > e->desc_cap) {
             hfree(e->d_desc);
             e->desc_cap = 0;
-            if (halloc(e->d_desc, nsteps) != hipSuccess) {
+            const std::size_t cap = nsteps + nsteps / 8;  // headroom, as for the tiles
+            if (halloc(e->d_desc, cap) != hipSuccess) {
                 return HBFSIM_CUDA_ERROR;
             }
-            e->desc_cap = nsteps;
+            e->desc_cap = cap;
         }
         desc = e->d_desc;
     }
