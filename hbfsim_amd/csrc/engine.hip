@@ -1346,6 +1346,21 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     }
 }
 
+__device__ __forceinline__ void add128(std::uint64_t& lo, std::uint64_t& hi, std::uint64_t v)
+{
+    const std::uint64_t n = lo + v;
+    hi += n < lo ? 1u : 0u;
+    lo = n;
+}
+
+__device__ __forceinline__ std::uint64_t wave_sum(std::uint64_t v)
+{
+    for (int o = 32; o > 0; o >>= 1) {
+        v += shfl64(v, threadIdx.x ^ o);
+    }
+    return v;
+}
+
 // ---- carry chain: a three-level scan over tile summaries ---------------
 //
 // A plane summary is a (first record, (max,+) map of the rest, last page)
@@ -1356,7 +1371,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
 // each group's tiles from the group's carry-in.  One thread per (group,
 // resource) at levels 1 and 3, one per resource at level 2.
 
-constexpr std::uint32_t kGroup = 64;
+constexpr std::uint32_t kGroup = 16;
 constexpr int kChunk = 8;  // loads a carry thread keeps in flight
 
 __device__ __forceinline__ PlaneSum plane_compose(const KArgs& a, const PlaneSum& s1,
@@ -1473,70 +1488,161 @@ __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, s
     }
 }
 
-// Level 2: thread r walks the groups from the engine state; writes each
-// group's carry-in and the final state.
-__global__ __launch_bounds__(64) void k_carry_mid(KArgs a, std::size_t ngroups,
-                                                  const PlaneSum* gpsum, const ChanSum* gcsum,
-                                                  const std::uint64_t* gcount,
-                                                  PlaneCarry* gpcarry, std::uint64_t* gccarry,
-                                                  std::uint64_t* gseq, std::uint64_t* st_pbusy,
-                                                  std::uint64_t* st_ptag, std::uint64_t* st_cbusy,
-                                                  std::uint64_t* st_seq, std::uint64_t* ptotal,
-                                                  std::uint64_t* ctotal)
+// Level 2: block r scans resource r's group summaries (an exclusive scan by
+// composition, kMidBlock groups per pass with a running carry) and applies
+// each prefix to the engine state: every group's carry-in, the final state,
+// and the service total.
+constexpr int kMidBlock = 512;
+
+union MidShared {
+    PlaneSum p[kMidBlock];
+    ChanSum c[kMidBlock];
+    std::uint64_t s[kMidBlock];
+};
+
+// Inclusive scan of x over the block (Hillis-Steele, earlier elements first).
+template <typename T, typename F>
+__device__ __forceinline__ T block_scan(T x, T* sh, T identity, F compose)
 {
-    const std::uint32_t t = blockIdx.x * kWave + threadIdx.x;
-    if (t < a.Rp) {
-        std::uint64_t busy = st_pbusy[t];
-        std::uint64_t tag1 = st_ptag[static_cast<std::size_t>(t) * 2];
-        std::uint64_t total = 0;
-        for (std::size_t g0 = 0; g0 < ngroups; g0 += kChunk) {
-            PlaneSum buf[kChunk];
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                buf[k] = g0 + k < ngroups ? gpsum[(g0 + k) * a.Rp + t] : PlaneSum{};
-            }
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if (g0 + k < ngroups) {
-                    PlaneCarry c;
-                    c.busy = busy;
-                    c.tag1 = tag1;
-                    gpcarry[(g0 + k) * a.Rp + t] = c;
-                    total += plane_apply(a, buf[k], busy, tag1);
-                }
-            }
+    const int tid = threadIdx.x;
+    sh[tid] = x;
+    __syncthreads();
+    for (int off = 1; off < kMidBlock; off <<= 1) {
+        T y = identity;
+        if (tid >= off) {
+            y = sh[tid - off];
         }
-        st_pbusy[t] = busy;
-        st_ptag[static_cast<std::size_t>(t) * 2] = tag1;
-        ptotal[t] += total;
-    } else if (t < a.Rp + a.Rc) {
-        const std::uint32_t c = t - a.Rp;
+        __syncthreads();
+        x = compose(y, x);
+        sh[tid] = x;
+        __syncthreads();
+    }
+    return x;
+}
+
+__device__ __forceinline__ std::uint64_t block_sum(std::uint64_t v, std::uint64_t* sh)
+{
+    const std::uint64_t w = wave_sum(v);
+    const int tid = threadIdx.x;
+    if ((tid & (kWave - 1)) == 0) {
+        sh[tid / kWave] = w;
+    }
+    __syncthreads();
+    std::uint64_t total = 0;
+    for (int k = 0; k < kMidBlock / kWave; ++k) {
+        total += sh[k];
+    }
+    __syncthreads();
+    return total;
+}
+
+__global__ __launch_bounds__(kMidBlock) void k_carry_mid(
+    KArgs a, std::size_t ngroups, const PlaneSum* gpsum, const ChanSum* gcsum,
+    const std::uint64_t* gcount, PlaneCarry* gpcarry, std::uint64_t* gccarry,
+    std::uint64_t* gseq, std::uint64_t* st_pbusy, std::uint64_t* st_ptag,
+    std::uint64_t* st_cbusy, std::uint64_t* st_seq, std::uint64_t* ptotal, std::uint64_t* ctotal)
+{
+    __shared__ MidShared sh;
+    __shared__ std::uint64_t red[kMidBlock / kWave];
+    __shared__ std::uint64_t next[2];
+    const std::uint32_t r = blockIdx.x;
+    const int tid = threadIdx.x;
+    if (r < a.Rp) {
+        std::uint64_t busy = st_pbusy[r];
+        std::uint64_t tag1 = st_ptag[static_cast<std::size_t>(r) * 2];
+        std::uint64_t total = 0;
+        const PlaneSum id{};
+        const auto compose = [&](const PlaneSum& s1, const PlaneSum& s2) {
+            return plane_compose(a, s1, s2);
+        };
+        for (std::size_t g0 = 0; g0 < ngroups; g0 += kMidBlock) {
+            const std::size_t g = g0 + tid;
+            PlaneSum own = id;
+            if (g < ngroups) {
+                own = gpsum[g * a.Rp + r];
+            }
+            (void)block_scan(own, sh.p, id, compose);
+            PlaneSum before = id;
+            if (tid > 0) {
+                before = sh.p[tid - 1];
+            }
+            std::uint64_t b = busy, t1 = tag1;
+            (void)plane_apply(a, before, b, t1);  // the state this group starts from
+            std::uint64_t svc = 0;
+            if (g < ngroups) {
+                PlaneCarry c;
+                c.busy = b;
+                c.tag1 = t1;
+                gpcarry[g * a.Rp + r] = c;
+                svc = plane_apply(a, own, b, t1);
+            }
+            const std::size_t last = (ngroups - g0 < kMidBlock ? ngroups - g0 : kMidBlock) - 1;
+            if (static_cast<std::size_t>(tid) == last) {
+                next[0] = b;
+                next[1] = t1;
+            }
+            total += block_sum(svc, red);
+            busy = next[0];
+            tag1 = next[1];
+            __syncthreads();
+        }
+        if (tid == 0) {
+            st_pbusy[r] = busy;
+            st_ptag[static_cast<std::size_t>(r) * 2] = tag1;
+            ptotal[r] += total;
+        }
+    } else if (r < a.Rp + a.Rc) {
+        const std::uint32_t c = r - a.Rp;
         std::uint64_t busy = st_cbusy[c];
         std::uint64_t total = 0;
-        for (std::size_t g0 = 0; g0 < ngroups; g0 += kChunk) {
-            ChanSum buf[kChunk];
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                buf[k] = g0 + k < ngroups ? gcsum[(g0 + k) * a.Rc + c] : ChanSum{0, 0};
+        const ChanSum id{0, 0};
+        for (std::size_t g0 = 0; g0 < ngroups; g0 += kMidBlock) {
+            const std::size_t g = g0 + tid;
+            ChanSum own = id;
+            if (g < ngroups) {
+                own = gcsum[g * a.Rc + c];
             }
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if (g0 + k < ngroups) {
-                    gccarry[(g0 + k) * a.Rc + c] = busy;
-                    busy = umax64(busy + buf[k].A, buf[k].B);
-                    total += buf[k].A;
-                }
+            const ChanSum inc = block_scan(own, sh.c, id, chan_compose);
+            ChanSum before = id;
+            if (tid > 0) {
+                before = sh.c[tid - 1];
             }
+            if (g < ngroups) {
+                gccarry[g * a.Rc + c] = umax64(busy + before.A, before.B);
+            }
+            const std::size_t last = (ngroups - g0 < kMidBlock ? ngroups - g0 : kMidBlock) - 1;
+            if (static_cast<std::size_t>(tid) == last) {
+                next[0] = umax64(busy + inc.A, inc.B);
+            }
+            total += block_sum(g < ngroups ? own.A : 0ull, red);
+            busy = next[0];
+            __syncthreads();
         }
-        st_cbusy[c] = busy;
-        ctotal[c] += total;
-    } else if (t == a.Rp + a.Rc) {
-        std::uint64_t s = *st_seq;
-        for (std::size_t g = 0; g < ngroups; ++g) {
-            gseq[g] = s;
-            s += gcount[g];
+        if (tid == 0) {
+            st_cbusy[c] = busy;
+            ctotal[c] += total;
         }
-        *st_seq = s;
+    } else if (r == a.Rp + a.Rc) {
+        std::uint64_t seq = *st_seq;
+        const auto add = [](std::uint64_t x, std::uint64_t y) { return x + y; };
+        for (std::size_t g0 = 0; g0 < ngroups; g0 += kMidBlock) {
+            const std::size_t g = g0 + tid;
+            const std::uint64_t own = g < ngroups ? gcount[g] : 0ull;
+            const std::uint64_t inc = block_scan(own, sh.s, std::uint64_t{0}, add);
+            if (g < ngroups) {
+                gseq[g] = seq + inc - own;
+            }
+            const std::size_t last = (ngroups - g0 < kMidBlock ? ngroups - g0 : kMidBlock) - 1;
+            if (static_cast<std::size_t>(tid) == last) {
+                next[0] = seq + inc;
+            }
+            __syncthreads();
+            seq = next[0];
+            __syncthreads();
+        }
+        if (tid == 0) {
+            *st_seq = seq;
+        }
     }
 }
 
@@ -1616,20 +1722,6 @@ __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
     }
 }
 
-__device__ __forceinline__ void add128(std::uint64_t& lo, std::uint64_t& hi, std::uint64_t v)
-{
-    const std::uint64_t n = lo + v;
-    hi += n < lo ? 1u : 0u;
-    lo = n;
-}
-
-__device__ __forceinline__ std::uint64_t wave_sum(std::uint64_t v)
-{
-    for (int o = 32; o > 0; o >>= 1) {
-        v += shfl64(v, threadIdx.x ^ o);
-    }
-    return v;
-}
 
 __device__ __forceinline__ std::uint64_t wave_max(std::uint64_t v)
 {
@@ -1711,23 +1803,55 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
     const std::uint64_t s0 = wave_sum(m ? umax64(ls, v.x) : 0ull);  // lane 0: max(sense, x)
     t.svc_sum += lane == 0 ? s0 : sx;
     t.seq += 64 * nq;
-    const std::uint64_t back = static_cast<std::uint64_t>(63 - lane);
-    for (int k = 0; k < q.n; ++k) {
-        const std::uint64_t lead_k = readlane64(lead, k);
-        const std::uint64_t top_k = readlane64(top, k);
-        const std::uint64_t i0 = readlane64(q.issue, k);
-        const std::uint64_t x = readlane64(v.x, k);
-        const std::uint64_t pd = (lane == 0 || a.contention) ? lead_k : i0;
-        const std::uint64_t done = umax64(pd, top_k - x * back);
-        t.mk = umax64(t.mk, done);
-        const std::uint64_t lat = done - i0;
-        add128(t.lat_lo, t.lat_hi, lat);
-        t.lat_max = umax64(t.lat_max, lat);
-        const std::size_t i = q.first + static_cast<std::size_t>(k) * kWave + lane;
-        completion[i] = done;
-        if (status != nullptr) {
-            const bool hit = lane != 0 || ((hits >> k) & 1u) != 0;
-            status[i] = static_cast<std::uint8_t>(hit ? 4u : 0u);
+    // Completions two steps at a time: lane l writes records 2 (l & 31) and
+    // 2 (l & 31) + 1 of step k + (l >> 5), 16 bytes per lane.
+    const int sub = lane >> 5;
+    const std::uint64_t j0 = 2u * static_cast<std::uint64_t>(lane & 31);
+    const bool wide = (reinterpret_cast<std::uintptr_t>(completion) & 15u) == 0;
+    for (int k = 0; k < q.n; k += 2) {
+        const int ks = k + sub;
+        const std::uint64_t lead_k = shfl64(lead, ks);
+        const std::uint64_t top_k = shfl64(top, ks);
+        const std::uint64_t i0 = shfl64(q.issue, ks);
+        const std::uint64_t x = shfl64(v.x, ks);
+        if (ks < q.n) {
+            const std::uint64_t pd0 = (j0 == 0 || a.contention) ? lead_k : i0;
+            const std::uint64_t pd1 = a.contention ? lead_k : i0;
+            const std::uint64_t done0 = umax64(pd0, top_k - x * (63 - j0));
+            const std::uint64_t done1 = umax64(pd1, top_k - x * (62 - j0));
+            t.mk = umax64(t.mk, umax64(done0, done1));
+            const std::uint64_t lat0 = done0 - i0, lat1 = done1 - i0;
+            add128(t.lat_lo, t.lat_hi, lat0);
+            add128(t.lat_lo, t.lat_hi, lat1);
+            t.lat_max = umax64(t.lat_max, umax64(lat0, lat1));
+            std::uint64_t* out = completion + q.first + static_cast<std::size_t>(ks) * kWave + j0;
+            if (wide) {
+                *reinterpret_cast<ulonglong2*>(out) = make_ulonglong2(done0, done1);
+            } else {
+                out[0] = done0;
+                out[1] = done1;
+            }
+        }
+    }
+    // Status bytes four steps at a time: 4 for a page-register hit (every
+    // record but a sensing lane 0), 0 otherwise.
+    if (status != nullptr) {
+        const bool words = (reinterpret_cast<std::uintptr_t>(status) & 3u) == 0;
+        for (int k = 0; k < q.n; k += 4) {
+            const int ks = k + (lane >> 4);
+            if (ks < q.n) {
+                const std::uint32_t r0 = 4u * static_cast<std::uint32_t>(lane & 15);
+                const bool sense = r0 == 0 && ((hits >> ks) & 1u) == 0;
+                std::uint8_t* out = status + q.first + static_cast<std::size_t>(ks) * kWave + r0;
+                if (words) {
+                    *reinterpret_cast<std::uint32_t*>(out) = sense ? 0x04040400u : 0x04040404u;
+                } else {
+                    out[0] = sense ? 0u : 4u;
+                    out[1] = 4u;
+                    out[2] = 4u;
+                    out[3] = 4u;
+                }
+            }
         }
     }
 }
@@ -3657,7 +3781,6 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         desc = e->d_desc;
     }
     const dim3 grid(static_cast<unsigned>(ntiles));
-    const unsigned carry_blocks = (a.Rp + a.Rc + 1 + kWave - 1) / kWave;
     (void)hipEventRecord(e->ev[0], stream);
     const std::uint8_t* hits = d_hits;
     if (k2) {
@@ -3681,7 +3804,8 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         hipLaunchKernelGGL(k_carry_up, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
                            e->d_psum, e->d_tmask, e->d_csum, e->d_tcount, e->d_gpsum,
                            e->d_gcsum, e->d_gcount);
-        hipLaunchKernelGGL(k_carry_mid, dim3(carry_blocks), dim3(kWave), 0, stream, a, ngroups,
+        hipLaunchKernelGGL(k_carry_mid, dim3(a.Rp + a.Rc + 1), dim3(kMidBlock), 0, stream, a,
+                           ngroups,
                            e->d_gpsum, e->d_gcsum, e->d_gcount, e->d_gpcarry, e->d_gccarry,
                            e->d_gseq, e->d_pbusy, e->d_ptag, e->d_cbusy, e->d_seq, e->d_ptot,
                            e->d_ctot);
