@@ -1118,10 +1118,25 @@ __host__ __device__ __forceinline__ std::uint32_t mask_words(const KArgs& a)
     return (a.Rp + 63) / 64;
 }
 
-__device__ __forceinline__ bool touched(const std::uint64_t* tmask, std::uint32_t words,
-                                        std::size_t tile, std::uint32_t r)
+// A tile's plane summaries are packed: word w of its mask holds the touched
+// planes r in [64 w, 64 w + 64) and how many touched planes come before them.
+struct alignas(16) MaskWord {
+    std::uint64_t bits;
+    std::uint32_t base;
+    std::uint32_t pad;
+};
+
+// Where plane r's entry sits among tile `tile`'s packed summaries (and carry-
+// ins), or -1 when the tile does not touch the plane.
+__device__ __forceinline__ int slot(const MaskWord* tmask, std::uint32_t words, std::size_t tile,
+                                    std::uint32_t r)
 {
-    return ((tmask[tile * words + r / 64] >> (r % 64)) & 1u) != 0;
+    const MaskWord m = tmask[tile * words + r / 64];
+    const std::uint32_t bit = r % 64;
+    if (((m.bits >> bit) & 1u) == 0) {
+        return -1;
+    }
+    return static_cast<int>(m.base) + __popcll(m.bits & ((1ull << bit) - 1));
 }
 
 // Summary pass.  Per plane the tile keeps: the first record (page, issue,
@@ -1131,7 +1146,7 @@ __device__ __forceinline__ bool touched(const std::uint64_t* tmask, std::uint32_
 template <bool kRefresh, bool kHits>
 __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
-                                                std::uint64_t* tmask, ChanSum* csum,
+                                                MaskWord* tmask, ChanSum* csum,
                                                 std::uint64_t* tile_count,
                                                 const std::uint8_t* hits, StepDesc* desc)
 {
@@ -1311,16 +1326,22 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
         }
     }
     __syncthreads();
-    // Only planes the tile touched get a summary; a bit mask per tile says
-    // which (the others are identities, and the carry chain skips them).
+    // Only planes the tile touched get a summary, packed in plane order; the
+    // tile's mask words say which (the others are identities, and the carry
+    // chain skips them).
     PlaneSum* ps = psum + tile * a.Rp;
-    std::uint64_t* tm = tmask + tile * mask_words(a);
+    MaskWord* tm = tmask + tile * mask_words(a);
+    std::uint32_t count = 0;
     for (std::uint32_t r0 = 0; r0 < a.Rp; r0 += kWave) {
         const std::uint32_t r = r0 + lane;
         const bool touched = r < a.Rp && p_f1[r] != 0;
         const std::uint64_t bits = __ballot(touched);
         if (lane == 0) {
-            tm[r0 / kWave] = bits;
+            MaskWord m;
+            m.bits = bits;
+            m.base = count;
+            m.pad = 0;
+            tm[r0 / kWave] = m;
         }
         if (touched) {
             PlaneSum v;
@@ -1331,8 +1352,9 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
             v.lpage1 = p_l1[r];
             v.fcls = p_fc[r];
             v.pad = 0;
-            ps[r] = v;
+            ps[count + __popcll(bits & lanemask_lt(lane))] = v;
         }
+        count += static_cast<std::uint32_t>(__popcll(bits));
     }
     ChanSum* cs = csum + tile * a.Rc;
     for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
@@ -1424,7 +1446,7 @@ __device__ __forceinline__ ChanSum chan_compose(const ChanSum& s1, const ChanSum
 // Level 1: thread (g, r) folds the summaries of group g's tiles.
 __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, std::size_t ngroups,
                                                   const PlaneSum* psum,
-                                                  const std::uint64_t* tmask, const ChanSum* csum,
+                                                  const MaskWord* tmask, const ChanSum* csum,
                                                   const std::uint64_t* tile_count,
                                                   PlaneSum* gpsum, ChanSum* gcsum,
                                                   std::uint64_t* gcount)
@@ -1444,21 +1466,21 @@ __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, s
         const std::uint32_t words = mask_words(a);
         PlaneSum acc{};  // the identity: no first record
         for (std::size_t t = t0; t < t1; t += kChunk) {
-            bool hit[kChunk];
+            int at[kChunk];
             PlaneSum buf[kChunk];
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
-                hit[k] = t + k < t1 && touched(tmask, words, t + k, r);
+                at[k] = t + k < t1 ? slot(tmask, words, t + k, r) : -1;
             }
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
-                if (hit[k]) {
-                    buf[k] = psum[(t + k) * a.Rp + r];
+                if (at[k] >= 0) {
+                    buf[k] = psum[(t + k) * a.Rp + at[k]];
                 }
             }
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
-                if (hit[k]) {
+                if (at[k] >= 0) {
                     acc = plane_compose(a, acc, buf[k]);
                 }
             }
@@ -1650,7 +1672,7 @@ __global__ __launch_bounds__(kMidBlock) void k_carry_mid(
 // writes every tile's carry-in.
 __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
                                                     std::size_t ngroups, const PlaneSum* psum,
-                                                    const std::uint64_t* tmask,
+                                                    const MaskWord* tmask,
                                                     const ChanSum* csum,
                                                     const std::uint64_t* tile_count,
                                                     const PlaneCarry* gpcarry,
@@ -1672,26 +1694,26 @@ __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
         const std::uint32_t words = mask_words(a);
         std::uint64_t busy = c0.busy, tag1 = c0.tag1;
         for (std::size_t t = t0; t < t1; t += kChunk) {
-            bool hit[kChunk];
+            int at[kChunk];
             PlaneSum buf[kChunk];
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
-                hit[k] = t + k < t1 && touched(tmask, words, t + k, r);
+                at[k] = t + k < t1 ? slot(tmask, words, t + k, r) : -1;
             }
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
-                if (hit[k]) {
-                    buf[k] = psum[(t + k) * a.Rp + r];
+                if (at[k] >= 0) {
+                    buf[k] = psum[(t + k) * a.Rp + at[k]];
                 }
             }
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
                 // an untouched tile neither reads nor changes this plane
-                if (hit[k]) {
+                if (at[k] >= 0) {
                     PlaneCarry c;
                     c.busy = busy;
                     c.tag1 = tag1;
-                    pcarry[(t + k) * a.Rp + r] = c;
+                    pcarry[(t + k) * a.Rp + at[k]] = c;  // packed like the summaries
                     (void)plane_apply(a, buf[k], busy, tag1);
                 }
             }
@@ -1859,7 +1881,7 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
 template <bool kRefresh, bool kHits>
 __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, std::size_t n,
                                               std::uint64_t base_ps, const PlaneCarry* pcarry,
-                                              const std::uint64_t* tmask,
+                                              const MaskWord* tmask,
                                               const std::uint64_t* ccarry,
                                               const std::uint64_t* tile_seq,
                                               std::uint64_t* completion, std::uint8_t* status,
@@ -1879,8 +1901,9 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
     // carry-ins exist for the planes the tile touches, the only ones it reads
     const std::uint32_t words = mask_words(a);
     for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
-        if (touched(tmask, words, tile, r)) {
-            const PlaneCarry c = pcarry[tile * a.Rp + r];
+        const int at = slot(tmask, words, tile, r);
+        if (at >= 0) {
+            const PlaneCarry c = pcarry[tile * a.Rp + at];
             p_busy[r] = c.busy;
             p_tag[r] = static_cast<std::uint32_t>(c.tag1);
         }
@@ -2147,53 +2170,97 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
 
 // Folds the per-tile report partials into one report (sums, maxima and the
 // 128-bit latency sum).  One block.
-__global__ __launch_bounds__(256) void k_report(const DevReport* tile_rep, std::size_t ntiles,
-                                                DevReport* rep)
+// Report reduction in two launches: blocks fold runs of tile reports into
+// partials, then one block folds the partials.  A block's 256 threads are 16
+// streams x 16 words (the 14 report words, the carry out of the 128-bit
+// latency sum, padding); sums and maxima are exact in any order.
+constexpr int kRepWords = 16;
+constexpr int kRepCarry = 14;
+constexpr int kRepParts = 256;
+
+__device__ __forceinline__ void rep_join(int f, std::uint64_t& acc, std::uint64_t& carry,
+                                         std::uint64_t v, std::uint64_t vcarry)
 {
-    __shared__ std::uint64_t part[256][15];
-    const int t = threadIdx.x;
-    std::uint64_t acc[14] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    std::uint64_t carry = 0;
-    for (std::size_t i = t; i < ntiles; i += 256) {
-        const DevReport& r = tile_rep[i];
-        for (int k = 0; k < 14; ++k) {
-            if (k == R_MAKESPAN || k == R_LAT_MAX) {
-                acc[k] = umax64(acc[k], r.v[k]);
-            } else if (k == R_LAT_LO) {
-                const std::uint64_t s2 = acc[k] + r.v[k];
-                carry += s2 < acc[k] ? 1u : 0u;
-                acc[k] = s2;
-            } else {
-                acc[k] += r.v[k];
-            }
-        }
+    if (f == R_MAKESPAN || f == R_LAT_MAX) {
+        acc = umax64(acc, v);
+    } else if (f == R_LAT_LO) {
+        const std::uint64_t s2 = acc + v;
+        carry += vcarry + (s2 < acc ? 1u : 0u);
+        acc = s2;
+    } else {
+        acc += v;
     }
-    acc[R_LAT_HI] += carry;
-    for (int k = 0; k < 14; ++k) {
-        part[t][k] = acc[k];
+}
+
+// in: `count` entries of kIn words (14: tile reports, kRepWords: partials);
+// block b folds entries [b * per, (b + 1) * per).  With kFinal the single
+// block writes the report (carry added into the high latency word), else a
+// kRepWords partial per block.
+template <int kIn, bool kFinal>
+__global__ __launch_bounds__(256) void k_report(const std::uint64_t* in, std::size_t count,
+                                                std::size_t per, std::uint64_t* out)
+{
+    __shared__ std::uint64_t acc_sh[16][kRepWords];
+    __shared__ std::uint64_t carry_sh[16];
+    const int t = threadIdx.x;
+    const int f = t % kRepWords;
+    const int stream = t / kRepWords;
+    const std::size_t lo = static_cast<std::size_t>(blockIdx.x) * per;
+    const std::size_t hi = lo + per < count ? lo + per : count;
+    std::uint64_t acc = 0, carry = 0;
+    for (std::size_t i = lo + stream; i < hi; i += 16) {
+        const std::uint64_t v = f < kIn ? in[i * kIn + f] : 0ull;
+        // a partial's carry word travels with its latency word
+        const std::uint64_t vc = (kIn == kRepWords && f == R_LAT_LO) ? in[i * kIn + kRepCarry]
+                                                                       : 0ull;
+        rep_join(f, acc, carry, f == kRepCarry ? 0ull : v, vc);
+    }
+    acc_sh[stream][f] = acc;
+    if (f == R_LAT_LO) {
+        carry_sh[stream] = carry;
     }
     __syncthreads();
-    if (t == 0) {
-        std::uint64_t out[14] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        std::uint64_t c2 = 0;
-        for (int j = 0; j < 256; ++j) {
-            for (int k = 0; k < 14; ++k) {
-                if (k == R_MAKESPAN || k == R_LAT_MAX) {
-                    out[k] = umax64(out[k], part[j][k]);
-                } else if (k == R_LAT_LO) {
-                    const std::uint64_t s2 = out[k] + part[j][k];
-                    c2 += s2 < out[k] ? 1u : 0u;
-                    out[k] = s2;
-                } else {
-                    out[k] += part[j][k];
-                }
+    for (int half = 8; half > 0; half >>= 1) {
+        if (stream < half) {
+            std::uint64_t a0 = acc_sh[stream][f];
+            std::uint64_t c0 = f == R_LAT_LO ? carry_sh[stream] : 0ull;
+            rep_join(f, a0, c0, acc_sh[stream + half][f],
+                     f == R_LAT_LO ? carry_sh[stream + half] : 0ull);
+            acc_sh[stream][f] = a0;
+            if (f == R_LAT_LO) {
+                carry_sh[stream] = c0;
             }
         }
-        out[R_LAT_HI] += c2;
-        for (int k = 0; k < 14; ++k) {
-            rep->v[k] = out[k];
+        __syncthreads();
+    }
+    if (stream == 0) {
+        if (kFinal) {
+            if (f < 14) {
+                out[f] = f == R_LAT_HI ? acc_sh[0][f] + carry_sh[0] : acc_sh[0][f];
+            }
+        } else {
+            out[static_cast<std::size_t>(blockIdx.x) * kRepWords + f] =
+                f == kRepCarry ? carry_sh[0] : acc_sh[0][f];
         }
     }
+}
+
+// Folds `ntiles` tile reports into `rep` (parts: kRepParts * kRepWords words).
+void launch_report(hipStream_t stream, const DevReport* tile_rep, std::size_t ntiles,
+                   DevReport* rep, std::uint64_t* parts)
+{
+    const std::size_t per = (ntiles + kRepParts - 1) / kRepParts;
+    const std::size_t nparts = per == 0 ? 0 : (ntiles + per - 1) / per;
+    if (nparts == 0) {
+        hipLaunchKernelGGL((k_report<kRepWords, true>), dim3(1), dim3(256), 0, stream, parts,
+                           std::size_t{0}, std::size_t{1}, reinterpret_cast<std::uint64_t*>(rep));
+        return;
+    }
+    hipLaunchKernelGGL((k_report<14, false>), dim3(static_cast<unsigned>(nparts)), dim3(256), 0,
+                       stream, reinterpret_cast<const std::uint64_t*>(tile_rep), ntiles, per,
+                       parts);
+    hipLaunchKernelGGL((k_report<kRepWords, true>), dim3(1), dim3(256), 0, stream, parts, nparts,
+                       nparts, reinterpret_cast<std::uint64_t*>(rep));
 }
 
 }  // namespace
@@ -2223,10 +2290,11 @@ struct engine {
     std::uint64_t* d_seq{nullptr};
     DevReport* d_rep{nullptr};
     DevReport* h_rep{nullptr};  // pinned
+    std::uint64_t* d_rep_parts{nullptr};  // report partials
     // scratch
     std::size_t tile_cap{0};
     PlaneSum* d_psum{nullptr};
-    std::uint64_t* d_tmask{nullptr};  // touched planes per tile
+    MaskWord* d_tmask{nullptr};  // touched planes per tile
     ChanSum* d_csum{nullptr};
     PlaneCarry* d_pcarry{nullptr};
     std::uint64_t* d_ccarry{nullptr};
@@ -3314,8 +3382,8 @@ int run_empirical(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint
                        static_cast<const std::uint64_t*>(d_tail),
                        static_cast<const std::uint64_t*>(d_svc), c.emp_program_ns * 1000ull,
                        d_comp, d_status, d_trep);
-    hipLaunchKernelGGL(k_report, dim3(1), dim3(256), 0, stream,
-                       static_cast<const DevReport*>(d_trep), ntiles, e->d_rep);
+    launch_report(stream, static_cast<const DevReport*>(d_trep), ntiles, e->d_rep,
+                  e->d_rep_parts);
     (void)hipEventRecord(e->ev[3], stream);
     BState fin{};
     std::uint64_t fin2[2] = {0, 0};
@@ -3620,6 +3688,7 @@ int engine_create(const engine_config& c, engine** out)
     if (err == hipSuccess) err = halloc(e->d_ctot, rc);
     if (err == hipSuccess) err = halloc(e->d_seq, 1);
     if (err == hipSuccess) err = halloc(e->d_rep, 1);
+    if (err == hipSuccess) err = halloc(e->d_rep_parts, kRepParts * kRepWords);
     if (err == hipSuccess)
         err = hipHostMalloc(reinterpret_cast<void**>(&e->h_rep), sizeof(DevReport));
     for (int i = 0; i < 4 && err == hipSuccess; ++i) {
@@ -3658,6 +3727,7 @@ void engine_destroy(engine* e)
     hfree(e->d_ctot);
     hfree(e->d_seq);
     hfree(e->d_rep);
+    hfree(e->d_rep_parts);
     if (e->h_rep != nullptr) {
         (void)hipHostFree(e->h_rep);
     }
@@ -3827,7 +3897,7 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
                            base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
                            d_status, e->d_tile_rep, hits, desc);
     }
-    hipLaunchKernelGGL(k_report, dim3(1), dim3(256), 0, stream, e->d_tile_rep, ntiles, e->d_rep);
+    launch_report(stream, e->d_tile_rep, ntiles, e->d_rep, e->d_rep_parts);
     (void)hipEventRecord(e->ev[3], stream);
     err = hipGetLastError();
     if (err == hipSuccess)
