@@ -438,15 +438,20 @@ struct RecordPipe {
             }
         }
     }
-    // Makes the group in flight current and issues the one after it.
-    __device__ __forceinline__ void advance(const hbf_record32* rec, std::size_t next,
-                                            std::size_t end, int lane)
+    // Makes the group in flight current (waiting for it).
+    __device__ __forceinline__ void promote()
     {
 #pragma unroll
         for (int j = 0; j < kPipe; ++j) {
             ca[j] = na[j];
             cb[j] = nb[j];
         }
+    }
+    // Makes the group in flight current and issues the one after it.
+    __device__ __forceinline__ void advance(const hbf_record32* rec, std::size_t next,
+                                            std::size_t end, int lane)
+    {
+        promote();
         if (next < end) {
             issue(rec, next, end, lane);
         }
@@ -1055,15 +1060,8 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
                                              std::uint64_t* p_rA, std::uint64_t* p_rB,
                                              std::uint64_t* c_A, std::uint64_t* c_B,
                                              std::uint32_t* p_f1, std::uint32_t* p_l1,
-                                             std::uint32_t* p_fc, StepDesc* desc)
+                                             std::uint32_t* p_fc)
 {
-    if (desc != nullptr && lane < q.n) {
-        StepDesc sd;
-        sd.page1 = q.page1;
-        sd.bytes = q.bytes;
-        sd.issue = q.issue;
-        desc[q.first / kWave + lane] = sd;
-    }
     const StepView v = step_view(a, xp, q, lane);
     const bool m = v.m;
     const std::uint32_t pkey = m ? v.d.plane : 0u;
@@ -1110,6 +1108,22 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
         c_B[ckey] = umax64(sB + Ac, Bc);
         c_A[ckey] = sA + Ac;
     }
+}
+
+// Writes a folded batch's step descriptors.  The summary pass calls it just
+// before issuing a group's loads: vector memory operations complete in
+// issue order, so a store placed after a group's loads would hold up the
+// wait for that group.
+__device__ __forceinline__ void write_descs(StepDesc* desc, LinBatch& dq, int lane)
+{
+    if (dq.n != 0 && desc != nullptr && lane < dq.n) {
+        StepDesc sd;
+        sd.page1 = dq.page1;
+        sd.bytes = dq.bytes;
+        sd.issue = dq.issue;
+        desc[dq.first / kWave + lane] = sd;
+    }
+    dq.n = 0;
 }
 
 // 64-bit words of a tile's touched-plane mask.
@@ -1185,9 +1199,14 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     RecordPipe pipe;
     pipe.issue(rec, begin, end, lane);
     LinBatch q = empty_batch();
+    LinBatch dq = empty_batch();  // a folded batch whose descriptors are not written yet
     std::uint64_t modeled = 0;
     for (std::size_t g = begin; g < end; g += kGroupSpan) {
-        pipe.advance(rec, g + kGroupSpan, end, lane);
+        pipe.promote();
+        write_descs(desc, dq, lane);
+        if (g + kGroupSpan < end) {
+            pipe.issue(rec, g + kGroupSpan, end, lane);
+        }
         const std::size_t gend = g + kGroupSpan < end ? g + kGroupSpan : end;
         if (!kHits && a.slots == 1 && g + kGroupSpan <= end && q.n <= kWave - kPipe) {
             // a whole group of linear steps joins the batch at once
@@ -1195,9 +1214,9 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
             if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
                 q.push_group(gl, g);
                 if (q.n == kWave || gend >= end) {
-                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
-                                 desc);
+                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
+                    dq = q;
                     q.n = 0;
                 }
                 continue;
@@ -1219,9 +1238,10 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
                     q.push(lp, li, lb, s);
                 }
                 if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= end)) {
-                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
-                                 desc);
+                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
+                    write_descs(desc, dq, lane);  // at most one batch waits
+                    dq = q;
                     q.n = 0;
                 }
                 if (lin) {
@@ -1325,6 +1345,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
             }
         }
     }
+    write_descs(desc, dq, lane);
     __syncthreads();
     // Only planes the tile touched get a summary, packed in plane order; the
     // tile's mask words say which (the others are identities, and the carry
