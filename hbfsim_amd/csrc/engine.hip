@@ -1846,35 +1846,68 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
     const std::uint64_t s0 = wave_sum(m ? umax64(ls, v.x) : 0ull);  // lane 0: max(sense, x)
     t.svc_sum += lane == 0 ? s0 : sx;
     t.seq += 64 * nq;
-    // Completions two steps at a time: lane l writes records 2 (l & 31) and
-    // 2 (l & 31) + 1 of step k + (l >> 5), 16 bytes per lane.
-    const int sub = lane >> 5;
-    const std::uint64_t j0 = 2u * static_cast<std::uint64_t>(lane & 31);
-    const bool wide = (reinterpret_cast<std::uintptr_t>(completion) & 15u) == 0;
-    for (int k = 0; k < q.n; k += 2) {
-        const int ks = k + sub;
-        const std::uint64_t lead_k = shfl64(lead, ks);
-        const std::uint64_t top_k = shfl64(top, ks);
-        const std::uint64_t i0 = shfl64(q.issue, ks);
-        const std::uint64_t x = shfl64(v.x, ks);
-        if (ks < q.n) {
-            const std::uint64_t pd0 = (j0 == 0 || a.contention) ? lead_k : i0;
-            const std::uint64_t pd1 = a.contention ? lead_k : i0;
-            const std::uint64_t done0 = umax64(pd0, top_k - x * (63 - j0));
-            const std::uint64_t done1 = umax64(pd1, top_k - x * (62 - j0));
-            t.mk = umax64(t.mk, umax64(done0, done1));
-            const std::uint64_t lat0 = done0 - i0, lat1 = done1 - i0;
-            add128(t.lat_lo, t.lat_hi, lat0);
-            add128(t.lat_lo, t.lat_hi, lat1);
-            t.lat_max = umax64(t.lat_max, umax64(lat0, lat1));
-            std::uint64_t* out = completion + q.first + static_cast<std::size_t>(ks) * kWave + j0;
-            if (wide) {
-                *reinterpret_cast<ulonglong2*>(out) = make_ulonglong2(done0, done1);
-            } else {
-                out[0] = done0;
-                out[1] = done1;
+    // Per-step totals of the 64 records, in closed form (lane k: step k).
+    // Record j completes at done_j = max(pd_j, top - x (63 - j)), with pd_0 =
+    // lead and pd_j = P for j >= 1 (P = lead with contention, else the issue
+    // time).  The channel term grows with j, so among j = 1..63 the last cnt
+    // records follow it and the others wait for P; the largest such record is
+    // max(lead, top).
+    if (m) {
+        const std::uint64_t x = v.x;
+        const std::uint64_t P = a.contention ? lead : q.issue;
+        const std::uint64_t d0 = umax64(lead, top - 63 * x);
+        std::uint64_t cnt = 0;  // records 1..63 on the channel side
+        if (top >= P) {
+            const std::uint64_t D = top - P;
+            std::uint64_t tmax = 0;  // largest t <= 62 with x t <= D (x t <= 64 x <= top)
+            for (std::uint64_t stp = 32; stp != 0; stp >>= 1) {
+                if (tmax + stp <= 62 && x * (tmax + stp) <= D) {
+                    tmax += stp;
+                }
             }
+            cnt = tmax + 1;
         }
+        // sum_j done_j - 64 issue, exactly in 128 bits
+        std::uint64_t lo = d0, hi = 0;
+        const auto add = [&](std::uint64_t f, std::uint64_t w) {  // += f * w
+            const std::uint64_t pl = f * w;
+            const std::uint64_t ph = __umul64hi(f, w);
+            const std::uint64_t n2 = lo + pl;
+            hi += ph + (n2 < lo ? 1u : 0u);
+            lo = n2;
+        };
+        const auto sub = [&](std::uint64_t f, std::uint64_t w) {  // -= f * w
+            const std::uint64_t pl = f * w;
+            const std::uint64_t ph = __umul64hi(f, w);
+            hi -= ph + (lo < pl ? 1u : 0u);
+            lo -= pl;
+        };
+        add(63 - cnt, P);
+        add(cnt, top);
+        sub(x, cnt * (cnt - (cnt != 0 ? 1 : 0)) / 2);
+        sub(64, q.issue);
+        const std::uint64_t n2 = t.lat_lo + lo;
+        t.lat_hi += hi + (n2 < t.lat_lo ? 1u : 0u);
+        t.lat_lo = n2;
+        const std::uint64_t most = umax64(lead, top);
+        t.mk = umax64(t.mk, most);
+        t.lat_max = umax64(t.lat_max, most - q.issue);
+    }
+    // Completions, one step at a time: lane j writes record j.  Step values
+    // come in scalar registers; with one transfer time for the whole batch
+    // the channel offset x (63 - j) is a per-lane constant.
+    const std::uint64_t x0 = readlane64(v.x, 0);
+    const bool xuni = __ballot(m && v.x != x0) == 0;
+    const std::uint64_t back = static_cast<std::uint64_t>(63 - lane);
+    const std::uint64_t xm0 = x0 * back;
+    const bool lead_lane = lane == 0 || a.contention != 0;
+    for (int k = 0; k < q.n; ++k) {
+        const std::uint64_t lead_k = readlane64(lead, k);
+        const std::uint64_t top_k = readlane64(top, k);
+        const std::uint64_t i0 = readlane64(q.issue, k);
+        const std::uint64_t xm = xuni ? xm0 : readlane64(v.x, k) * back;
+        const std::uint64_t done = umax64(lead_lane ? lead_k : i0, top_k - xm);
+        completion[q.first + static_cast<std::size_t>(k) * kWave + lane] = done;
     }
     // Status bytes four steps at a time: 4 for a page-register hit (every
     // record but a sensing lane 0), 0 otherwise.
