@@ -16,8 +16,8 @@ ROOT = HERE.parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libhbfsim_amd.so"
 
-SOURCES = [CSRC / "engine.hip", CSRC / "gen.hip", CSRC / "thermal.hip", CSRC / "api.cpp",
-           CSRC / "profile.cpp"]
+SOURCES = [CSRC / "engine.hip", CSRC / "gen.hip", CSRC / "thermal.hip", CSRC / "servers.hip",
+           CSRC / "api.cpp", CSRC / "profile.cpp"]
 HEADERS = [CSRC / "engine.hpp", CSRC / "thermal.hpp", CSRC / "profile.hpp", CSRC / "json_min.hpp",
            ROOT / "include" / "hbfsim_amd.h"]
 

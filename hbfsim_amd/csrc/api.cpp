@@ -909,6 +909,13 @@ HBF_API int hbfsim_amd_gen_segment_lines(hbf_record32* d_records, size_t capacit
                                      stream);
 }
 
+HBF_API int hbfsim_amd_media_servers(const uint64_t* d_now_ns, size_t n, uint32_t servers,
+                                     uint64_t latency_ns, uint64_t* d_completion_ns,
+                                     void* stream)
+{
+    return hbfamd::media_servers(d_now_ns, n, servers, latency_ns, d_completion_ns, stream);
+}
+
 HBF_API int hbfsim_amd_validate_profile(const char* path, char* error, size_t error_bytes)
 {
     if (error != nullptr && error_bytes != 0) {

@@ -87,4 +87,8 @@ int gen_segment_lines(hbf_record32* d_records, std::size_t capacity,
                       std::uint32_t line_bytes, std::uint64_t gap_ps, std::uint32_t issuers,
                       std::uint64_t flags, void* stream);
 
+// k identical media servers (servers.hip).
+int media_servers(const std::uint64_t* d_now, std::size_t n, std::uint32_t servers,
+                  std::uint64_t latency_ns, std::uint64_t* d_completion, void* stream);
+
 }  // namespace hbfamd

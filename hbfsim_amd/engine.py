@@ -327,6 +327,24 @@ class Thermal:
             pass
 
 
+def media_servers(now_ns: Any, servers: int, latency_ns: int, stream: Any = None) -> Any:
+    """MediaServers::issue (prefetch_model.cpp:22-50) over a batch of reads
+    issued at non-decreasing times `now_ns` (torch int64 on the GPU): returns
+    their completion times.  Raises ValueError for issue times that decrease
+    or reach 2^63 ns."""
+    import torch
+
+    n = int(now_ns.shape[0])
+    out = torch.empty(max(n, 1), dtype=torch.int64, device=now_ns.device)
+    lib = nat.load()
+    rc = lib.hbfsim_amd_media_servers(_ptr(now_ns), n, servers, latency_ns, _ptr(out),
+                                      ctypes.c_void_p(_stream_handle(stream)))
+    if rc == nat.HBFSIM_INVALID_ARGUMENT:
+        raise ValueError("issue times must not decrease and must stay below 2^63 ns")
+    nat.check(rc, "media servers")
+    return out[:n]
+
+
 def validate_profile(path: str) -> str | None:
     """None when the profile is valid, else the reference's error message."""
     buf = ctypes.create_string_buffer(512)

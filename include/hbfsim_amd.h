@@ -341,6 +341,18 @@ int hbfsim_amd_gen_segment_lines(hbf_record32* d_records, size_t capacity,
                                  uint64_t gap_ps, uint32_t issuers, uint64_t flags,
                                  void* stream);
 
+/* MediaServers::issue (src/prefetch/prefetch_model.cpp:22-50) for a batch:
+ * `servers` identical servers (0 counts as 1), all free at time 0, each read
+ * taking latency_ns; read i, issued at d_now_ns[i], starts when the
+ * earliest-free server frees (or at its issue time) and completes
+ * latency_ns later, in d_completion_ns[i].  Device arrays of n entries.
+ * Issue times must not decrease (simulate_prefetch's clock never runs
+ * backwards, prefetch_model.cpp:124-186) and must stay below 2^63 ns:
+ * HBFSIM_INVALID_ARGUMENT otherwise (completions are then unspecified).
+ * Synchronises `stream`. */
+int hbfsim_amd_media_servers(const uint64_t* d_now_ns, size_t n, uint32_t servers,
+                             uint64_t latency_ns, uint64_t* d_completion_ns, void* stream);
+
 /* ===== 4. EQ3 thermal grid and thermal-coupled reliability =============
  *
  * The reference's RC network (src/eq3_thermal/thermal.cpp:127-311) on a
