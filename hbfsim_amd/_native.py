@@ -193,6 +193,7 @@ SIGNATURES = {
     "hbfsim_amd_gen_segment_lines": (_INT, [_P, _SZ, _P, _SZ, _U64, _U32, _U64, _U32, _U64,
                                             _P]),
     "hbfsim_amd_media_servers": (_INT, [_P, _SZ, _U32, _U64, _P, _P]),
+    "hbfsim_amd_gen_spans": (_INT, [_P, _SZ, _P, _P, _P, _SZ, _U64, _U32, _U64, _U32, _P]),
     "hbfsim_amd_thermal_create": (_INT, [ctypes.POINTER(ThermalGrid), ctypes.POINTER(_P)]),
     "hbfsim_amd_thermal_step": (_INT, [_P, _P, _P, _U64, _P]),
     "hbfsim_amd_thermal_last_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float)]),

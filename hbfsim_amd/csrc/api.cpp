@@ -909,6 +909,16 @@ HBF_API int hbfsim_amd_gen_segment_lines(hbf_record32* d_records, size_t capacit
                                      stream);
 }
 
+HBF_API int hbfsim_amd_gen_spans(hbf_record32* d_records, size_t capacity,
+                                 const uint64_t* d_span_base, const uint64_t* d_span_first,
+                                 const uint32_t* d_span_op, size_t nspan, uint64_t total,
+                                 uint32_t line_bytes, uint64_t gap_ps, uint32_t issuers,
+                                 void* stream)
+{
+    return hbfamd::gen_spans(d_records, capacity, d_span_base, d_span_first, d_span_op, nspan,
+                             total, line_bytes, gap_ps, issuers, stream);
+}
+
 HBF_API int hbfsim_amd_media_servers(const uint64_t* d_now_ns, size_t n, uint32_t servers,
                                      uint64_t latency_ns, uint64_t* d_completion_ns,
                                      void* stream)

@@ -87,6 +87,13 @@ int gen_segment_lines(hbf_record32* d_records, std::size_t capacity,
                       std::uint32_t line_bytes, std::uint64_t gap_ps, std::uint32_t issuers,
                       std::uint64_t flags, void* stream);
 
+// Variable-length spans of lines (gen.hip): d_first has nspan + 1 entries,
+// d_first[0] = 0 and d_first[nspan] = total <= capacity (checked on the host).
+int gen_spans(hbf_record32* d_records, std::size_t capacity, const std::uint64_t* d_base,
+              const std::uint64_t* d_first, const std::uint32_t* d_op, std::size_t nspan,
+              std::uint64_t total, std::uint32_t line_bytes, std::uint64_t gap_ps,
+              std::uint32_t issuers, void* stream);
+
 // k identical media servers (servers.hip).
 int media_servers(const std::uint64_t* d_now, std::size_t n, std::uint32_t servers,
                   std::uint64_t latency_ns, std::uint64_t* d_completion, void* stream);

@@ -281,3 +281,226 @@ def gpu_segment_records(seg_base: np.ndarray, lines: int, line: int, gap_ps: int
         issuers, flags, ctypes.c_void_p(stream)), "generate records")
     torch.cuda.current_stream().synchronize()
     return out[:n]
+
+
+# ---------------------------------------------------------------------------
+# Spans: runs of consecutive lines, each with its own length and operation
+# (the GPU compiler is hbfsim_amd_gen_spans).
+
+
+def span_records(base: np.ndarray, first: np.ndarray, op: np.ndarray, line: int, gap_ps: int,
+                 issuers: int, start: int = 0, count: int | None = None) -> np.ndarray:
+    """Host mirror of the GPU span compiler: records [start, start + count)."""
+    total = int(first[-1])
+    count = total - start if count is None else count
+    j = np.arange(start, start + count, dtype=np.uint64)
+    s = np.searchsorted(first[:-1].astype(np.uint64), j, side="right") - 1
+    rec = np.zeros((count, 4), np.uint64)
+    rec[:, 0] = base[s] + (j - first[s].astype(np.uint64)) * np.uint64(line)
+    rec[:, 1] = line
+    rec[:, 2] = (j // np.uint64(issuers)) * np.uint64(gap_ps)
+    rec[:, 3] = op[s].astype(np.uint64)
+    return rec
+
+
+def gpu_span_records(base: np.ndarray, first: np.ndarray, op: np.ndarray, line: int,
+                     gap_ps: int, issuers: int, out=None, stream=None):
+    """Compiles spans' records on the GPU; returns an int64 [n, 4] tensor."""
+    import ctypes
+
+    import torch
+
+    from . import _native as nat
+    lib = nat.load()
+    n = int(first[-1])
+    if out is None:
+        out = torch.empty((max(n, 1), 4), dtype=torch.int64, device="cuda")
+    d_base = torch.from_numpy(np.ascontiguousarray(base, np.uint64).view(np.int64)).cuda()
+    d_first = torch.from_numpy(np.ascontiguousarray(first, np.uint64).view(np.int64)).cuda()
+    d_op = torch.from_numpy(np.ascontiguousarray(op, np.uint32).view(np.int32)).cuda()
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    nat.check(lib.hbfsim_amd_gen_spans(
+        out.data_ptr(), out.shape[0], d_base.data_ptr(), d_first.data_ptr(), d_op.data_ptr(),
+        len(base), n, line, gap_ps, issuers, ctypes.c_void_p(stream)), "generate span records")
+    torch.cuda.current_stream().synchronize()
+    return out[:n]
+
+
+def _spans(parts: list[tuple[int, int, int]]) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """(base, lines, op) triples -> (base, first, op) arrays."""
+    base = np.array([p[0] for p in parts], np.uint64)
+    lines = np.array([p[1] for p in parts], np.uint64)
+    op = np.array([p[2] for p in parts], np.uint32)
+    first = np.zeros(len(parts) + 1, np.uint64)
+    np.cumsum(lines, out=first[1:])
+    return base, first, op
+
+
+# ---------------------------------------------------------------------------
+# Config 1: TinyLlama-1.1B-shaped decode weight streaming.  Every step reads
+# every weight tensor front to back in 128-B lines, 256 wavefronts issuing a
+# line each every 64 ns; each tensor is its own read-only range.  Profile c0.
+
+
+@dataclasses.dataclass(frozen=True)
+class DenseShape:
+    layers: int = 22
+    hidden: int = 2048
+    intermediate: int = 5632
+    heads: int = 32
+    kv_heads: int = 4
+    vocab: int = 32000
+    dtype_bytes: int = 2
+    line: int = 128
+    issuers: int = 256
+    gap_ps: int = 64_000
+    page: int = 16384
+    base: int = 0x4000_0000_0000
+
+    def tensors(self) -> list[tuple[str, int]]:
+        """(name, bytes) in the order a decode step reads them."""
+        h, i, d = self.hidden, self.intermediate, self.dtype_bytes
+        kv = self.kv_heads * (h // self.heads)
+        out = [("embed_tokens", self.vocab * h * d)]
+        for l_ in range(self.layers):
+            out += [(f"{l_}.input_layernorm", h * d), (f"{l_}.q_proj", h * h * d),
+                    (f"{l_}.k_proj", kv * h * d), (f"{l_}.v_proj", kv * h * d),
+                    (f"{l_}.o_proj", h * h * d), (f"{l_}.post_attention_layernorm", h * d),
+                    (f"{l_}.gate_proj", i * h * d), (f"{l_}.up_proj", i * h * d),
+                    (f"{l_}.down_proj", h * i * d)]
+        out += [("norm", h * d), ("lm_head", self.vocab * h * d)]
+        return out
+
+    def layout(self) -> list[tuple[int, int]]:
+        """(base, bytes) per tensor, packed on page boundaries."""
+        out, at = [], self.base
+        for _, nbytes in self.tensors():
+            out.append((at, nbytes))
+            at += -(-nbytes // self.page) * self.page
+        return out
+
+
+TINYLLAMA = DenseShape()
+
+
+def dense_ranges(shape: DenseShape) -> list[tuple[int, int, int]]:
+    return [(b, n, 1) for b, n in shape.layout()]
+
+
+def dense_spans(shape: DenseShape) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """One decode step's spans: every tensor, whole lines."""
+    return _spans([(b, -(-n // shape.line), 0) for b, n in shape.layout()])
+
+
+# ---------------------------------------------------------------------------
+# Config 3: paged KV cache.  K and V of every layer live in pools of 16-token
+# blocks (kv_heads * head_dim values per token, bf16); each sequence's blocks
+# are scattered over its pools by a seeded permutation, with room for the
+# steps' appends.  A decode step, layer by layer: every sequence appends its
+# new token (K, then V: token_bytes of writes each, which end on a 16-KiB page
+# boundary every 8 tokens and then program), then every sequence's K and V
+# blocks are read up to the current length.  Profile c3 (256 GiB).
+
+
+@dataclasses.dataclass(frozen=True)
+class PagedKvShape:
+    layers: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    dtype_bytes: int = 2
+    block_tokens: int = 16
+    seqs: int = 64
+    min_len: int = 1024
+    max_len: int = 32768
+    seed: int = 2
+    steps: int = 32
+    line: int = 128
+    issuers: int = 256
+    gap_ps: int = 64_000
+    page: int = 16384
+    base: int = 0x3000_0000_0000
+
+    @property
+    def token_bytes(self) -> int:
+        return self.kv_heads * self.head_dim * self.dtype_bytes
+
+    @property
+    def block_bytes(self) -> int:
+        return self.block_tokens * self.token_bytes
+
+    def lengths(self) -> np.ndarray:
+        rng = np.random.default_rng(self.seed)
+        return rng.integers(self.min_len, self.max_len + 1, self.seqs).astype(np.int64)
+
+    def blocks_per_seq(self) -> np.ndarray:
+        return -(-(self.lengths() + self.steps) // self.block_tokens)
+
+    def pool_bytes(self) -> int:
+        return int(self.blocks_per_seq().sum()) * self.block_bytes
+
+    def pool_base(self, layer: int, kind: int) -> int:
+        span = -(-self.pool_bytes() // self.page) * self.page
+        return self.base + (2 * layer + kind) * span
+
+    def tables(self) -> list[list[np.ndarray]]:
+        """tables[layer][kind] -> physical block of (seq, logical block), flattened
+        by sequence (offsets from blocks_per_seq)."""
+        rng = np.random.default_rng(self.seed + 1)
+        nblk = int(self.blocks_per_seq().sum())
+        return [[rng.permutation(nblk) for _ in range(2)] for _ in range(self.layers)]
+
+
+PAGED_KV = PagedKvShape()
+
+
+def kv_ranges(shape: PagedKvShape) -> list[tuple[int, int, int]]:
+    return [(shape.pool_base(l_, k), shape.pool_bytes(), 3)
+            for l_ in range(shape.layers) for k in range(2)]
+
+
+def kv_spans(shape: PagedKvShape, step: int,
+             tables=None) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Decode step `step` (0-based) of the paged-KV configuration."""
+    tables = shape.tables() if tables is None else tables
+    lens = shape.lengths() + step                  # tokens before this step's append
+    bps = shape.blocks_per_seq()
+    off = np.concatenate([[0], np.cumsum(bps)[:-1]])
+    tb, bt, line = shape.token_bytes, shape.block_bytes, shape.line
+    wlines = tb // line
+    nread = -(-(lens + 1) // shape.block_tokens)   # blocks read, the new token included
+    seq_of = np.repeat(np.arange(shape.seqs), nread)
+    blk_of = np.arange(int(nread.sum())) - np.repeat(np.cumsum(nread) - nread, nread)
+    valid = np.minimum(shape.block_tokens, lens[seq_of] + 1 - blk_of * shape.block_tokens)
+    rlines = (valid * tb // line).astype(np.uint64)
+    bases, lines, ops = [], [], []
+    for l_ in range(shape.layers):
+        pk, pv = shape.pool_base(l_, 0), shape.pool_base(l_, 1)
+        tk, tv = tables[l_]
+        # appends: K then V of every sequence
+        blk = off + lens // shape.block_tokens
+        at = (lens % shape.block_tokens) * tb
+        wb = np.empty(2 * shape.seqs, np.uint64)
+        wb[0::2] = np.uint64(pk) + tk[blk].astype(np.uint64) * np.uint64(bt) + at.astype(np.uint64)
+        wb[1::2] = np.uint64(pv) + tv[blk].astype(np.uint64) * np.uint64(bt) + at.astype(np.uint64)
+        bases.append(wb)
+        lines.append(np.full(2 * shape.seqs, wlines, np.uint64))
+        ops.append(np.ones(2 * shape.seqs, np.uint32))
+        # reads: every sequence's K blocks, then its V blocks
+        phys = off[seq_of] + blk_of
+        kb = np.uint64(pk) + tk[phys].astype(np.uint64) * np.uint64(bt)
+        vb = np.uint64(pv) + tv[phys].astype(np.uint64) * np.uint64(bt)
+        starts = np.concatenate([[0], np.cumsum(nread)[:-1]])
+        order_b, order_l = [], []
+        for s in range(shape.seqs):
+            a, z = starts[s], starts[s] + nread[s]
+            order_b += [kb[a:z], vb[a:z]]
+            order_l += [rlines[a:z], rlines[a:z]]
+        bases.append(np.concatenate(order_b))
+        lines.append(np.concatenate(order_l))
+        ops.append(np.zeros(sum(len(x) for x in order_b), np.uint32))
+    base = np.concatenate(bases)
+    nl = np.concatenate(lines)
+    first = np.zeros(len(base) + 1, np.uint64)
+    np.cumsum(nl, out=first[1:])
+    return base, first, np.concatenate(ops)

@@ -341,6 +341,18 @@ int hbfsim_amd_gen_segment_lines(hbf_record32* d_records, size_t capacity,
                                  uint64_t gap_ps, uint32_t issuers, uint64_t flags,
                                  void* stream);
 
+/* Workload compiler for spans of different lengths, no counterpart in the
+ * reference (it generates the TinyLlama weight-streaming and paged-KV
+ * configurations).  Span s covers records [d_span_first[s],
+ * d_span_first[s + 1]) (nspan + 1 device entries, starting at 0 and ending
+ * at total <= capacity, non-decreasing): line k of the span reads (op 0) or
+ * writes (op 1) line_bytes at d_span_base[s] + k * line_bytes; record j is
+ * issued at (j / issuers) * gap_ps.  Asynchronous on `stream`. */
+int hbfsim_amd_gen_spans(hbf_record32* d_records, size_t capacity,
+                         const uint64_t* d_span_base, const uint64_t* d_span_first,
+                         const uint32_t* d_span_op, size_t nspan, uint64_t total,
+                         uint32_t line_bytes, uint64_t gap_ps, uint32_t issuers, void* stream);
+
 /* MediaServers::issue (src/prefetch/prefetch_model.cpp:22-50) for a batch:
  * `servers` identical servers (0 counts as 1), all free at time 0, each read
  * taking latency_ns; read i, issued at d_now_ns[i], starts when the

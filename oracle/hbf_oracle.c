@@ -960,27 +960,129 @@ uint64_t orc_bandwidth_cursor(uint64_t* cursor_ns, uint64_t arrival_ns,
 
 /* prefetch_model.cpp:22-50: k identical servers; a read issued at `now`
  * takes the server that frees first and finishes one latency later. */
+/* MediaServers::issue (prefetch_model.cpp:37-46): the server that frees
+ * first takes the read.  The servers are identical, so a scan for the
+ * minimum free-at time serves as the heap. */
+static uint64_t servers_issue(uint64_t* free_at, uint32_t k, uint64_t now, uint64_t latency)
+{
+    uint32_t best = 0;
+    for (uint32_t j = 1; j < k; ++j) {
+        if (free_at[j] < free_at[best]) {
+            best = j;
+        }
+    }
+    const uint64_t start = max_u64(now, free_at[best]);
+    free_at[best] = start + latency;
+    return free_at[best];
+}
+
 void orc_media_servers(const uint64_t* now_ns, size_t n, uint32_t servers,
                        uint64_t latency_ns, uint64_t* completion_ns)
 {
     const uint32_t k = servers ? servers : 1;
-    uint64_t* heap = (uint64_t*)calloc(k, sizeof(uint64_t));
-    if (heap == NULL) {
+    uint64_t* free_at = (uint64_t*)calloc(k, sizeof(uint64_t));
+    if (free_at == NULL) {
         return;
     }
     for (size_t i = 0; i < n; ++i) {
-        /* min over free-at times (all servers identical: ties are equal) */
-        uint32_t best = 0;
-        for (uint32_t j = 1; j < k; ++j) {
-            if (heap[j] < heap[best]) {
-                best = j;
+        completion_ns[i] = servers_issue(free_at, k, now_ns[i], latency_ns);
+    }
+    free(free_at);
+}
+
+/* StagingBuffer (prefetch_model.cpp:55-103): pages in insertion order with
+ * their arrival times; inserting past the capacity drops the oldest. */
+typedef struct {
+    uint64_t* page;
+    uint64_t* arrival;
+    size_t size, capacity;
+} staging;
+
+static long staging_find(const staging* b, uint64_t page)
+{
+    for (size_t i = 0; i < b->size; ++i) {
+        if (b->page[i] == page) {
+            return (long)i;
+        }
+    }
+    return -1;
+}
+
+static void staging_remove(staging* b, size_t at)
+{
+    for (size_t i = at + 1; i < b->size; ++i) {
+        b->page[i - 1] = b->page[i];
+        b->arrival[i - 1] = b->arrival[i];
+    }
+    --b->size;
+}
+
+int orc_simulate_prefetch(const uint64_t* pages, size_t n, uint32_t policy,
+                          uint32_t lead_distance, uint32_t buffer_pages,
+                          uint32_t max_in_flight, uint64_t read_latency_ns,
+                          uint64_t compute_ns_per_access, uint64_t* stats)
+{
+    memset(stats, 0, 7 * sizeof(uint64_t));
+    if (policy > 1) {
+        return 1;
+    }
+    stats[2] = n;
+    if (n == 0) {
+        return 0;
+    }
+    const uint32_t k = max_in_flight ? max_in_flight : 1;
+    staging b;
+    b.capacity = buffer_pages ? buffer_pages : 1;
+    b.size = 0;
+    uint64_t* free_at = (uint64_t*)calloc(k, sizeof(uint64_t));
+    b.page = (uint64_t*)malloc((b.capacity + 1) * sizeof(uint64_t));
+    b.arrival = (uint64_t*)malloc((b.capacity + 1) * sizeof(uint64_t));
+    if (!free_at || !b.page || !b.arrival) {
+        free(free_at);
+        free(b.page);
+        free(b.arrival);
+        return 1;
+    }
+    uint64_t clock = 0;
+    for (size_t i = 0; i < n; ++i) {
+        clock += compute_ns_per_access;
+        /* NextPage predicts the page after this one (no workload model) */
+        if (policy == 1 && lead_distance > 0) {
+            const uint64_t predicted = pages[i] + 1;
+            if (staging_find(&b, predicted) < 0) {
+                const uint64_t arrival = servers_issue(free_at, k, clock, read_latency_ns);
+                b.page[b.size] = predicted;
+                b.arrival[b.size] = arrival;
+                ++b.size;
+                while (b.size > b.capacity) {
+                    staging_remove(&b, 0);
+                    ++stats[6];
+                }
+                ++stats[5];
             }
         }
-        const uint64_t start = max_u64(now_ns[i], heap[best]);
-        heap[best] = start + latency_ns;
-        completion_ns[i] = heap[best];
+        const long at = staging_find(&b, pages[i]);
+        if (at >= 0) {
+            const uint64_t arrival = b.arrival[at];
+            staging_remove(&b, (size_t)at);
+            ++stats[4];
+            if (arrival > clock) {
+                stats[1] += arrival - clock;
+                clock = arrival;
+            }
+        } else {
+            const uint64_t arrival = servers_issue(free_at, k, clock, read_latency_ns);
+            ++stats[3];
+            stats[1] += arrival - clock;
+            clock = arrival;
+        }
     }
-    free(heap);
+    stats[6] += b.size;
+    stats[0] = clock;
+    free(free_at);
+    free(b.page);
+    free(b.arrival);
+    return 0;
 }
 
 /* ---- thermal: thermal.cpp:172-193 (matrix), 127-160 (Cholesky), 242-311

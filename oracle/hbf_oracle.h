@@ -276,6 +276,16 @@ void orc_pagebuf_sequence(const uint64_t* pages, size_t n, uint32_t slots,
 void orc_media_servers(const uint64_t* now_ns, size_t n, uint32_t servers,
                        uint64_t latency_ns, uint64_t* completion_ns);
 
+/* simulate_prefetch (prefetch_model.cpp:116-186), MediaServers and
+ * StagingBuffer (:22-100) for the policies without a random predictor:
+ * policy 0 None, 1 NextPage.  stats[7] = total_ns, stall_ns,
+ * demand_accesses, demand_misses, prefetch_hits, prefetch_issued,
+ * prefetch_wasted.  Returns 0, or 1 for another policy / no memory. */
+int orc_simulate_prefetch(const uint64_t* pages, size_t n, uint32_t policy,
+                          uint32_t lead_distance, uint32_t buffer_pages,
+                          uint32_t max_in_flight, uint64_t read_latency_ns,
+                          uint64_t compute_ns_per_access, uint64_t* stats);
+
 /* ---- thermal (thermal.cpp:127-311) ----------------------------------- */
 /* One backward-Euler step of the RC network with constant power:
  * (C/dt + Gb + L) T' = C/dt T + Ps + E/dt + Gb Tb.  Dense Cholesky.

@@ -10,6 +10,7 @@
 
 #include <hbfsim/eq3_thermal/thermal.hpp>
 #include <hbfsim/hybrid_model.hpp>
+#include <hbfsim/prefetch_model.hpp>
 #include <hbfsim/ucie/bank_layout.hpp>
 #include <hbfsim/ucie/device_coalescer.hpp>
 
@@ -265,6 +266,40 @@ REF_API int ref_thermal_step(std::size_t n, const double* capacity,
         }
         const auto& t = model.temperatures_k();
         std::memcpy(out, t.data(), n * sizeof(double));
+        return 1;
+    } catch (const std::exception&) {
+        return 0;
+    }
+}
+
+// simulate_prefetch (src/prefetch/prefetch_model.cpp:116-186): stats[7] =
+// total_ns, stall_ns, demand_accesses, demand_misses, prefetch_hits,
+// prefetch_issued, prefetch_wasted.
+REF_API int ref_simulate_prefetch(const std::uint64_t* pages, std::size_t n, std::uint32_t policy,
+                                  double accuracy, std::uint32_t lead_distance,
+                                  std::uint32_t buffer_pages, std::uint32_t max_in_flight,
+                                  std::uint64_t read_latency_ns, std::uint64_t compute_ns,
+                                  std::uint64_t seed, std::uint64_t* stats)
+{
+    try {
+        hbfsim::PrefetchConfig c;
+        c.policy = static_cast<hbfsim::PrefetchPolicy>(policy);
+        c.accuracy = accuracy;
+        c.lead_distance = lead_distance;
+        c.buffer_pages = buffer_pages;
+        c.max_in_flight = max_in_flight;
+        c.read_latency_ns = read_latency_ns;
+        c.compute_ns_per_access = compute_ns;
+        c.seed = seed;
+        const std::vector<std::uint64_t> stream(pages, pages + n);
+        const hbfsim::PrefetchStats r = hbfsim::simulate_prefetch(stream, c);
+        stats[0] = r.total_ns;
+        stats[1] = r.stall_ns;
+        stats[2] = r.demand_accesses;
+        stats[3] = r.demand_misses;
+        stats[4] = r.prefetch_hits;
+        stats[5] = r.prefetch_issued;
+        stats[6] = r.prefetch_wasted;
         return 1;
     } catch (const std::exception&) {
         return 0;

@@ -46,6 +46,8 @@ def bind(ref):
         "ref_pagebuf_sequence": (ctypes.c_int, [P, ctypes.c_size_t, P]),
         "ref_thermal_step": (ctypes.c_int, [ctypes.c_size_t, P, P, P, P, P, ctypes.c_size_t, P,
                                             P, P, P, U32, ctypes.c_double, P]),
+        "ref_simulate_prefetch": (ctypes.c_int, [P, ctypes.c_size_t, U32, ctypes.c_double, U32,
+                                                 U32, U32, U64, U64, U64, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(ref, name)
@@ -83,6 +85,40 @@ def table_json(recs, count):
     return [{"base": r.base, "length": r.length, "file_offset": r.file_offset,
              "range_id": r.range_id, "mode": r.mode, "permissions": r.permissions,
              "page_bytes": r.page_bytes} for r in recs[:count]]
+
+
+def prefetch_stream(rng, n):
+    kind = int(rng.integers(0, 4))
+    if kind == 0:                                   # sequential
+        return np.arange(n, dtype=np.uint64) + np.uint64(rng.integers(0, 1000))
+    if kind == 1:                                   # few pages, repeats
+        return rng.integers(0, 6, n).astype(np.uint64)
+    if kind == 2:                                   # random over many pages
+        return rng.integers(0, 10**6, n).astype(np.uint64)
+    runs = []                                       # runs of consecutive pages
+    while sum(len(r) for r in runs) < n:
+        start = int(rng.integers(0, 500))
+        runs.append(np.arange(start, start + int(rng.integers(1, 30)), dtype=np.uint64))
+    return np.concatenate(runs)[:n]
+
+
+def prefetch_cases(ref):
+    """simulate_prefetch with the policies that draw no random numbers (the
+    Accuracy policy's draws come from the C++ library's distribution)."""
+    rng = np.random.default_rng(20261201)  # its own stream: earlier vectors stay as they are
+    cases = []
+    for _ in range(80):
+        n = int(rng.integers(0, 400))
+        pages = prefetch_stream(rng, n) if n else np.zeros(0, np.uint64)
+        cfg = [int(rng.integers(0, 2)), int(rng.choice([0, 1, 3])),
+               int(rng.choice([0, 1, 2, 8, 64])), int(rng.choice([0, 1, 2, 4, 32])),
+               int(rng.choice([0, 1, 1000, 10_000])), int(rng.choice([0, 5, 3000]))]
+        stats = np.zeros(7, np.uint64)
+        ok = ref.ref_simulate_prefetch(pages.ctypes.data, n, cfg[0], 1.0, cfg[1], cfg[2], cfg[3],
+                                       cfg[4], cfg[5], 1, stats.ctypes.data)
+        cases.append({"pages": pages.tolist(), "config": cfg, "ok": ok,
+                      "stats": stats.tolist()})
+    return cases
 
 
 def main() -> None:
@@ -239,6 +275,7 @@ def main() -> None:
                    "energy": energy.tolist(), "steps": steps, "dt": dt, "ok": ok,
                    "temperature": outv.tolist()})
     out["thermal"] = th
+    out["prefetch"] = prefetch_cases(ref)
 
     path = HERE / "ref_vectors.json"
     path.write_text(json.dumps(out, separators=(",", ":")) + "\n")

@@ -168,6 +168,8 @@ def lib() -> ctypes.CDLL:
             "orc_bandwidth_cursor": (_U64, [_P, _U64, _U64, _U64, _U64]),
             "orc_pagebuf_sequence": (None, [_P, ctypes.c_size_t, _U32, _P]),
             "orc_media_servers": (None, [_P, ctypes.c_size_t, _U32, _U64, _P]),
+            "orc_simulate_prefetch": (ctypes.c_int, [_P, ctypes.c_size_t, _U32, _U32, _U32,
+                                                     _U32, _U64, _U64, _P]),
             "orc_thermal_dense_step": (ctypes.c_int, [ctypes.c_size_t, _P, _P, _P, _P,
                                                       ctypes.c_size_t, _P, _P, _P,
                                                       ctypes.c_double, _P, _P]),
