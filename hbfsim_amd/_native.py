@@ -194,6 +194,11 @@ SIGNATURES = {
                                             _P]),
     "hbfsim_amd_media_servers": (_INT, [_P, _SZ, _U32, _U64, _P, _P]),
     "hbfsim_amd_gen_spans": (_INT, [_P, _SZ, _P, _P, _P, _SZ, _U64, _U32, _U64, _U32, _P]),
+    "hbfsim_amd_sampler_create": (_INT, [_U32, ctypes.c_double, _U64, ctypes.POINTER(_P)]),
+    "hbfsim_amd_sampler_destroy": (None, [_P]),
+    "hbfsim_amd_sampler_reference": (_INT, [_P, _P, _P, _U64, _SZ, _P,
+                                            ctypes.POINTER(_U64), _P]),
+    "hbfsim_amd_calibrate": (_INT, [_P, _P, _SZ, _P, _SZ, ctypes.POINTER(_SZ), _P]),
     "hbfsim_amd_thermal_create": (_INT, [ctypes.POINTER(ThermalGrid), ctypes.POINTER(_P)]),
     "hbfsim_amd_thermal_step": (_INT, [_P, _P, _P, _U64, _P]),
     "hbfsim_amd_thermal_last_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float)]),

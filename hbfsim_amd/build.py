@@ -17,7 +17,7 @@ CSRC = HERE / "csrc"
 LIB = HERE / "libhbfsim_amd.so"
 
 SOURCES = [CSRC / "engine.hip", CSRC / "gen.hip", CSRC / "thermal.hip", CSRC / "servers.hip",
-           CSRC / "api.cpp", CSRC / "profile.cpp"]
+           CSRC / "hybrid.hip", CSRC / "api.cpp", CSRC / "profile.cpp"]
 HEADERS = [CSRC / "engine.hpp", CSRC / "thermal.hpp", CSRC / "profile.hpp", CSRC / "json_min.hpp",
            ROOT / "include" / "hbfsim_amd.h"]
 

@@ -926,6 +926,59 @@ HBF_API int hbfsim_amd_media_servers(const uint64_t* d_now_ns, size_t n, uint32_
     return hbfamd::media_servers(d_now_ns, n, servers, latency_ns, d_completion_ns, stream);
 }
 
+struct hbfsim_amd_sampler {
+    hbfamd::sampler_state* state;
+};
+
+HBF_API int hbfsim_amd_sampler_create(uint32_t warmup_requests, double sample_rate,
+                                      uint64_t seed, hbfsim_amd_sampler** out)
+{
+    if (out == nullptr) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    *out = nullptr;
+    hbfamd::sampler_state* st = nullptr;
+    const int rc = hbfamd::sampler_create(warmup_requests, sample_rate, seed, &st);
+    if (rc != HBFSIM_OK) {
+        return rc;
+    }
+    *out = new (std::nothrow) hbfsim_amd_sampler{st};
+    if (*out == nullptr) {
+        hbfamd::sampler_destroy(st);
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    return HBFSIM_OK;
+}
+
+HBF_API void hbfsim_amd_sampler_destroy(hbfsim_amd_sampler* sampler)
+{
+    if (sampler != nullptr) {
+        hbfamd::sampler_destroy(sampler->state);
+        delete sampler;
+    }
+}
+
+HBF_API int hbfsim_amd_sampler_reference(hbfsim_amd_sampler* sampler,
+                                         const hbfsim_amd_access_class* d_access,
+                                         const uint64_t* d_sequence, uint64_t first_sequence,
+                                         size_t n, uint8_t* d_flags, uint64_t* references,
+                                         void* stream)
+{
+    if (sampler == nullptr) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    return hbfamd::sampler_reference(sampler->state, d_access, d_sequence, first_sequence, n,
+                                     d_flags, references, stream);
+}
+
+HBF_API int hbfsim_amd_calibrate(const hbfsim_amd_access_class* d_access,
+                                 const uint64_t* d_latency_ns, size_t n,
+                                 hbfsim_amd_calibration* d_rows, size_t max_rows, size_t* rows,
+                                 void* stream)
+{
+    return hbfamd::calibrate(d_access, d_latency_ns, n, d_rows, max_rows, rows, stream);
+}
+
 HBF_API int hbfsim_amd_validate_profile(const char* path, char* error, size_t error_bytes)
 {
     if (error != nullptr && error_bytes != 0) {

@@ -98,4 +98,17 @@ int gen_spans(hbf_record32* d_records, std::size_t capacity, const std::uint64_t
 int media_servers(const std::uint64_t* d_now, std::size_t n, std::uint32_t servers,
                   std::uint64_t latency_ns, std::uint64_t* d_completion, void* stream);
 
+// Hybrid model's sampler and calibrator (hybrid.hip).
+struct sampler_state;
+int sampler_create(std::uint32_t warmup, double sample_rate, std::uint64_t seed,
+                   sampler_state** out);
+void sampler_destroy(sampler_state* s);
+int sampler_reference(sampler_state* s, const hbfsim_amd_access_class* d_access,
+                      const std::uint64_t* d_sequence, std::uint64_t first_sequence,
+                      std::size_t n, std::uint8_t* d_flags, std::uint64_t* references,
+                      void* stream);
+int calibrate(const hbfsim_amd_access_class* d_access, const std::uint64_t* d_latency,
+              std::size_t n, hbfsim_amd_calibration* d_rows, std::size_t max_rows,
+              std::size_t* rows_out, void* stream);
+
 }  // namespace hbfamd

@@ -365,6 +365,65 @@ int hbfsim_amd_gen_spans(hbf_record32* d_records, size_t capacity,
 int hbfsim_amd_media_servers(const uint64_t* d_now_ns, size_t n, uint32_t servers,
                              uint64_t latency_ns, uint64_t* d_completion_ns, void* stream);
 
+/* ----- Hybrid model: request sampler and calibrator -------------------
+ * The host-side HybridSampler and Calibrator of src/hybrid/calibrator.cpp
+ * (include/hbfsim/hybrid_model.hpp:13-60) for batches of requests held in
+ * device memory.  hbfsim_amd_access_class is AccessClass (operation 0 read,
+ * 1 write) and orders like its defaulted operator<=>: operation, bytes,
+ * queue_bucket, locality_bucket. */
+typedef struct hbfsim_amd_access_class {
+    uint32_t operation;
+    uint32_t bytes;
+    uint32_t queue_bucket;
+    uint32_t locality_bucket;
+} hbfsim_amd_access_class;
+
+/* CalibrationEstimate (hybrid_model.hpp:28-36) with its class. */
+typedef struct hbfsim_amd_calibration {
+    hbfsim_amd_access_class access;
+    uint64_t count;
+    uint64_t mean_ns;
+    uint64_t p50_ns;
+    uint64_t p95_ns;
+    uint64_t p99_ns;
+    double log_mean;
+    double log_sigma;
+} hbfsim_amd_calibration;
+
+typedef struct hbfsim_amd_sampler hbfsim_amd_sampler;
+
+/* HybridSampler(warmup_requests, sample_rate, seed) (calibrator.cpp:67-81):
+ * HBFSIM_INVALID_ARGUMENT for a rate outside [0, 1] or not finite (the
+ * constructor's std::invalid_argument). */
+int hbfsim_amd_sampler_create(uint32_t warmup_requests, double sample_rate, uint64_t seed,
+                              hbfsim_amd_sampler** out);
+void hbfsim_amd_sampler_destroy(hbfsim_amd_sampler* sampler);
+
+/* HybridSampler::reference (calibrator.cpp:83-96) for n requests in order:
+ * d_flags[i] = reference(sequence_i, d_access[i]), with sequence_i =
+ * d_sequence[i], or first_sequence + i when d_sequence is NULL (the
+ * consecutive sequences of hbf_trace_timing.cpp:181-206).  The sampler keeps
+ * the classes it has seen across calls, as the reference's seen set does.
+ * *references (if not NULL) receives the number of flags set.  Device
+ * arrays; synchronises `stream`.  n must be below 2^32. */
+int hbfsim_amd_sampler_reference(hbfsim_amd_sampler* sampler,
+                                 const hbfsim_amd_access_class* d_access,
+                                 const uint64_t* d_sequence, uint64_t first_sequence, size_t n,
+                                 uint8_t* d_flags, uint64_t* references, void* stream);
+
+/* Calibrator::observe(d_access[i], d_latency_ns[i]) for every i, then
+ * estimate() of every class observed (calibrator.cpp:98-136), one row per
+ * class in class order into d_rows.  count, mean_ns (floor of the 128-bit
+ * sum / count) and the percentiles equal the reference's; log_mean and
+ * log_sigma are computed in double on the GPU (the reference sums in long
+ * double) and agree to 1e-12 relative.  *rows receives the class count;
+ * HBFSIM_INVALID_ARGUMENT when it exceeds max_rows (nothing written) or
+ * when a latency is 0 (observe's "latency_ns must be positive").  Device
+ * arrays; synchronises `stream`.  n must be below 2^32. */
+int hbfsim_amd_calibrate(const hbfsim_amd_access_class* d_access, const uint64_t* d_latency_ns,
+                         size_t n, hbfsim_amd_calibration* d_rows, size_t max_rows,
+                         size_t* rows, void* stream);
+
 /* ===== 4. EQ3 thermal grid and thermal-coupled reliability =============
  *
  * The reference's RC network (src/eq3_thermal/thermal.cpp:127-311) on a

@@ -1619,3 +1619,153 @@ int orc_coupled_run(const orc_engine_params* p, const orc_range* ranges,
     free(mstat);
     return rc;
 }
+
+/* ---- hybrid sampler and calibrator (src/hybrid/calibrator.cpp:67-138) -- */
+
+typedef struct orc_class_item {
+    orc_access_class key;
+    uint64_t second;  /* index (sampler) or latency (calibrator) */
+    size_t index;
+} orc_class_item;
+
+/* AccessClass's defaulted operator<=> (hybrid_model.hpp:13-20): operation,
+ * bytes, queue_bucket, locality_bucket, in that order. */
+static int class_cmp(const orc_access_class* a, const orc_access_class* b)
+{
+    if (a->operation != b->operation) return a->operation < b->operation ? -1 : 1;
+    if (a->bytes != b->bytes) return a->bytes < b->bytes ? -1 : 1;
+    if (a->queue_bucket != b->queue_bucket) return a->queue_bucket < b->queue_bucket ? -1 : 1;
+    if (a->locality_bucket != b->locality_bucket)
+        return a->locality_bucket < b->locality_bucket ? -1 : 1;
+    return 0;
+}
+
+static int class_item_cmp(const void* pa, const void* pb)
+{
+    const orc_class_item* a = (const orc_class_item*)pa;
+    const orc_class_item* b = (const orc_class_item*)pb;
+    const int c = class_cmp(&a->key, &b->key);
+    if (c != 0) return c;
+    if (a->second != b->second) return a->second < b->second ? -1 : 1;
+    return a->index < b->index ? -1 : (a->index > b->index ? 1 : 0);
+}
+
+/* HybridSampler (calibrator.cpp:67-96).  The constructor rejects a rate
+ * outside [0, 1] or not finite and sets threshold = max for rate >= 1, else
+ * rate * (long double)UINT64_MAX truncated.  reference(sequence, access)
+ * inserts the class into the seen set and returns true for a warm-up
+ * sequence, a class not seen before, or when the SplitMix64 finaliser of
+ * sequence ^ seed ^ bytes<<17 ^ queue<<33 ^ locality<<49 ^ operation<<61 is
+ * at most the threshold.  Over a stream the "not seen before" requests are
+ * the first occurrence of each class, found here by sorting (class, index). */
+int orc_sampler_run(uint32_t warmup, double sample_rate, uint64_t seed,
+                    const orc_access_class* access, const uint64_t* sequence,
+                    size_t n, uint8_t* flags)
+{
+    if (!isfinite(sample_rate) || sample_rate < 0.0 || sample_rate > 1.0) {
+        return 1;
+    }
+    const uint64_t threshold = orc_sample_threshold(sample_rate);
+    orc_class_item* items = (orc_class_item*)malloc((n ? n : 1) * sizeof(*items));
+    if (items == NULL) {
+        return 2;
+    }
+    for (size_t i = 0; i < n; ++i) {
+        items[i].key = access[i];
+        items[i].second = i;
+        items[i].index = i;
+        flags[i] = 0;
+    }
+    qsort(items, n, sizeof(*items), class_item_cmp);
+    for (size_t j = 0; j < n; ++j) {
+        if (j == 0 || class_cmp(&items[j].key, &items[j - 1].key) != 0) {
+            flags[items[j].index] = 1;  /* unseen */
+        }
+    }
+    free(items);
+    for (size_t i = 0; i < n; ++i) {
+        const orc_access_class* a = &access[i];
+        uint64_t value = sequence[i] ^ seed;
+        value ^= (uint64_t)a->bytes << 17;
+        value ^= (uint64_t)a->queue_bucket << 33;
+        value ^= (uint64_t)a->locality_bucket << 49;
+        value ^= (uint64_t)a->operation << 61;
+        if (sequence[i] < warmup || orc_fast_hash(value) <= threshold) {
+            flags[i] = 1;
+        }
+    }
+    return 0;
+}
+
+/* calibrator.cpp:20-30: the sample of rank ceil(size * num / den) (1-based),
+ * clamped to the sorted range. */
+static uint64_t class_percentile(const orc_class_item* sorted, size_t size,
+                                 uint32_t num, uint32_t den)
+{
+    const unsigned __int128 rank =
+        ((unsigned __int128)size * num + den - 1) / den;
+    size_t index = rank == 0 ? 0 : (size_t)(rank - 1);
+    if (index > size - 1) {
+        index = size - 1;
+    }
+    return sorted[index].second;
+}
+
+/* Calibrator::observe then estimate for each class (calibrator.cpp:98-136):
+ * samples of a class sorted ascending; count; mean = 128-bit sum / count;
+ * p50, p95, p99 by class_percentile; log_mean = sum of log(sample) in long
+ * double, in sorted order, / count; log_sigma = sqrt(sum (log - log_mean)^2
+ * / count) in long double; both returned as double. */
+long orc_calibrate(const orc_access_class* access, const uint64_t* latency,
+                   size_t n, orc_calibration* rows)
+{
+    for (size_t i = 0; i < n; ++i) {
+        if (latency[i] == 0) {
+            return -1;
+        }
+    }
+    orc_class_item* items = (orc_class_item*)malloc((n ? n : 1) * sizeof(*items));
+    if (items == NULL) {
+        return -1;
+    }
+    for (size_t i = 0; i < n; ++i) {
+        items[i].key = access[i];
+        items[i].second = latency[i];
+        items[i].index = i;
+    }
+    qsort(items, n, sizeof(*items), class_item_cmp);
+    long count = 0;
+    size_t begin = 0;
+    while (begin < n) {
+        size_t end = begin + 1;
+        while (end < n && class_cmp(&items[end].key, &items[begin].key) == 0) {
+            ++end;
+        }
+        const orc_class_item* s = items + begin;
+        const size_t size = end - begin;
+        unsigned __int128 sum = 0;
+        long double log_sum = 0.0L;
+        for (size_t k = 0; k < size; ++k) {
+            sum += s[k].second;
+            log_sum += logl((long double)s[k].second);
+        }
+        const long double log_mean = log_sum / size;
+        long double squared = 0.0L;
+        for (size_t k = 0; k < size; ++k) {
+            const long double delta = logl((long double)s[k].second) - log_mean;
+            squared += delta * delta;
+        }
+        orc_calibration* r = &rows[count++];
+        r->access = s[0].key;
+        r->count = size;
+        r->mean_ns = (uint64_t)(sum / size);
+        r->p50_ns = class_percentile(s, size, 50, 100);
+        r->p95_ns = class_percentile(s, size, 95, 100);
+        r->p99_ns = class_percentile(s, size, 99, 100);
+        r->log_mean = (double)log_mean;
+        r->log_sigma = (double)sqrtl(squared / size);
+        begin = end;
+    }
+    free(items);
+    return count;
+}

@@ -33,6 +33,9 @@
  *   pagebuf (K=2 lower-slot rule)        golden traces from compiled
  *                                        device_coalescer.cpp
  *   media_servers (k-server)             golden traces from the k-server rule
+ *   sampler_run / calibrate              KAT (calibrator_test.cpp:18-26, 92-105)
+ *                                        + compiled calibrator.cpp on random
+ *                                        streams (flags and estimates equal)
  *   thermal_dense_step                   closed forms (thermal_tests.cpp:54-89)
  *                                        + golden temperatures from compiled
  *                                        thermal.cpp
@@ -285,6 +288,33 @@ int orc_simulate_prefetch(const uint64_t* pages, size_t n, uint32_t policy,
                           uint32_t lead_distance, uint32_t buffer_pages,
                           uint32_t max_in_flight, uint64_t read_latency_ns,
                           uint64_t compute_ns_per_access, uint64_t* stats);
+
+/* ---- hybrid sampler and calibrator (calibrator.cpp:67-138) ----------- */
+typedef struct orc_access_class {
+    uint32_t operation;
+    uint32_t bytes;
+    uint32_t queue_bucket;
+    uint32_t locality_bucket;
+} orc_access_class;
+
+/* HybridSampler(warmup, rate, seed) then flags[i] = reference(sequence[i],
+ * access[i]) for i in order, from an empty seen set.  Returns 0, 1 for a
+ * rate the constructor rejects, 2 when memory runs out. */
+int orc_sampler_run(uint32_t warmup, double sample_rate, uint64_t seed,
+                    const orc_access_class* access, const uint64_t* sequence,
+                    size_t n, uint8_t* flags);
+
+typedef struct orc_calibration {
+    orc_access_class access;
+    uint64_t count, mean_ns, p50_ns, p95_ns, p99_ns;
+    double log_mean, log_sigma;
+} orc_calibration;
+
+/* Calibrator::observe(access[i], latency[i]) for all i, then estimate() of
+ * every class observed, in the class order (std::map's).  Returns the row
+ * count, or -1 for a zero latency (observe rejects it) or no memory. */
+long orc_calibrate(const orc_access_class* access, const uint64_t* latency,
+                   size_t n, orc_calibration* rows);
 
 /* ---- thermal (thermal.cpp:127-311) ----------------------------------- */
 /* One backward-Euler step of the RC network with constant power:

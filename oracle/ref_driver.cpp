@@ -305,3 +305,58 @@ REF_API int ref_simulate_prefetch(const std::uint64_t* pages, std::size_t n, std
         return 0;
     }
 }
+
+// HybridSampler (calibrator.cpp:67-96) over a stream: flags[i] =
+// reference(sequence[i], access[i]) in order.  access holds n x 4 u32
+// (operation, bytes, queue_bucket, locality_bucket).  Returns 1, or 0 when
+// the constructor throws.
+REF_API int ref_sampler_run(std::uint32_t warmup, double rate, std::uint64_t seed,
+                            const std::uint32_t* access, const std::uint64_t* sequence,
+                            std::size_t n, std::uint8_t* flags)
+{
+    try {
+        hbfsim::HybridSampler sampler(warmup, rate, seed);
+        for (std::size_t i = 0; i < n; ++i) {
+            const hbfsim::AccessClass c{static_cast<hbfsim::RequestOperation>(access[4 * i]),
+                                        access[4 * i + 1], access[4 * i + 2], access[4 * i + 3]};
+            flags[i] = sampler.reference(sequence[i], c) ? 1 : 0;
+        }
+        return 1;
+    } catch (const std::exception&) {
+        return 0;
+    }
+}
+
+// Calibrator (calibrator.cpp:98-136): observe every (access[i], latency[i]),
+// then estimate(query).  out_u64 = count, mean, p50, p95, p99; out_f64 =
+// log_mean, log_sigma.  Returns 1 with an estimate, 0 without one, -1 when
+// observe throws.
+REF_API int ref_calibrate(const std::uint32_t* access, const std::uint64_t* latency,
+                          std::size_t n, const std::uint32_t* query, std::uint64_t* out_u64,
+                          double* out_f64)
+{
+    try {
+        hbfsim::Calibrator cal;
+        for (std::size_t i = 0; i < n; ++i) {
+            const hbfsim::AccessClass c{static_cast<hbfsim::RequestOperation>(access[4 * i]),
+                                        access[4 * i + 1], access[4 * i + 2], access[4 * i + 3]};
+            cal.observe(c, latency[i]);
+        }
+        const hbfsim::AccessClass q{static_cast<hbfsim::RequestOperation>(query[0]), query[1],
+                                    query[2], query[3]};
+        const auto e = cal.estimate(q);
+        if (!e) {
+            return 0;
+        }
+        out_u64[0] = e->count;
+        out_u64[1] = e->mean_ns;
+        out_u64[2] = e->p50_ns;
+        out_u64[3] = e->p95_ns;
+        out_u64[4] = e->p99_ns;
+        out_f64[0] = e->log_mean;
+        out_f64[1] = e->log_sigma;
+        return 1;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}

@@ -48,6 +48,9 @@ def bind(ref):
                                             P, P, P, U32, ctypes.c_double, P]),
         "ref_simulate_prefetch": (ctypes.c_int, [P, ctypes.c_size_t, U32, ctypes.c_double, U32,
                                                  U32, U32, U64, U64, U64, P]),
+        "ref_sampler_run": (ctypes.c_int, [U32, ctypes.c_double, U64, P, P, ctypes.c_size_t,
+                                           P]),
+        "ref_calibrate": (ctypes.c_int, [P, P, ctypes.c_size_t, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(ref, name)
@@ -119,6 +122,55 @@ def prefetch_cases(ref):
         cases.append({"pages": pages.tolist(), "config": cfg, "ok": ok,
                       "stats": stats.tolist()})
     return cases
+
+
+def class_stream(rng, n, classes):
+    """n access classes (n x 4 u32) drawn from `classes` distinct ones, the
+    fields mixing small values, both operations and 32-bit extremes."""
+    pool = np.stack([rng.integers(0, 2, classes),
+                     rng.choice([0, 1, 4096, 16384, 65536, 2**31, 2**32 - 1], classes),
+                     rng.choice([0, 1, 7, 2**32 - 1], classes),
+                     rng.choice([0, 3, 2**16, 2**32 - 1], classes)], axis=1).astype(np.uint32)
+    return np.ascontiguousarray(pool[rng.integers(0, classes, n)])
+
+
+def hybrid_cases(ref):
+    """HybridSampler flags and Calibrator estimates from the compiled
+    calibrator.cpp: streams with few and many classes, warm-up and rate
+    edges (0, 1, in between), sequences from 0 and from far out."""
+    rng = np.random.default_rng(20261202)
+    sampler = []
+    for _ in range(40):
+        n = int(rng.integers(0, 300))
+        acc = class_stream(rng, n, int(rng.integers(1, 12)))
+        first = int(rng.choice([0, 1, 1000, 2**40]))
+        seq = np.arange(first, first + n, dtype=np.uint64)
+        warm = int(rng.choice([0, 4, 64, 2**32 - 1]))
+        rate = float(rng.choice([0.0, 0.01, 0.25, 0.5, 1.0]))
+        seed = int(rng.choice([0, 7, 2**63 + 5]))
+        flags = np.zeros(max(n, 1), np.uint8)
+        ok = ref.ref_sampler_run(warm, rate, seed, acc.ctypes.data, seq.ctypes.data, n,
+                                 flags.ctypes.data)
+        sampler.append({"access": acc.tolist(), "first": first, "warmup": warm, "rate": rate,
+                        "seed": seed, "ok": ok, "flags": flags[:n].tolist()})
+    calib = []
+    for _ in range(30):
+        n = int(rng.integers(1, 400))
+        acc = class_stream(rng, n, int(rng.integers(1, 8)))
+        edge = np.array([1, 2, 999, 10_000, 123_456, 2**40, 2**63, 2**64 - 1], np.uint64)
+        lat = edge[rng.integers(0, len(edge), n)] if rng.random() < 0.3 else \
+            rng.integers(1, 200_000, n).astype(np.uint64)
+        lat = np.ascontiguousarray(lat, np.uint64)
+        rows = []
+        for q in np.unique(acc, axis=0):
+            q = np.ascontiguousarray(q, np.uint32)
+            u = np.zeros(5, np.uint64)
+            f = np.zeros(2, np.float64)
+            ok = ref.ref_calibrate(acc.ctypes.data, lat.ctypes.data, n, q.ctypes.data,
+                                   u.ctypes.data, f.ctypes.data)
+            rows.append({"class": q.tolist(), "ok": ok, "u64": u.tolist(), "f64": f.tolist()})
+        calib.append({"access": acc.tolist(), "latency": lat.tolist(), "rows": rows})
+    return {"sampler": sampler, "calibrate": calib}
 
 
 def main() -> None:
@@ -276,6 +328,7 @@ def main() -> None:
                    "temperature": outv.tolist()})
     out["thermal"] = th
     out["prefetch"] = prefetch_cases(ref)
+    out["hybrid"] = hybrid_cases(ref)
 
     path = HERE / "ref_vectors.json"
     path.write_text(json.dumps(out, separators=(",", ":")) + "\n")

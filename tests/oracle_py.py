@@ -170,6 +170,9 @@ def lib() -> ctypes.CDLL:
             "orc_media_servers": (None, [_P, ctypes.c_size_t, _U32, _U64, _P]),
             "orc_simulate_prefetch": (ctypes.c_int, [_P, ctypes.c_size_t, _U32, _U32, _U32,
                                                      _U32, _U64, _U64, _P]),
+            "orc_sampler_run": (ctypes.c_int, [_U32, ctypes.c_double, _U64, _P, _P,
+                                               ctypes.c_size_t, _P]),
+            "orc_calibrate": (ctypes.c_long, [_P, _P, ctypes.c_size_t, _P]),
             "orc_thermal_dense_step": (ctypes.c_int, [ctypes.c_size_t, _P, _P, _P, _P,
                                                       ctypes.c_size_t, _P, _P, _P,
                                                       ctypes.c_double, _P, _P]),
@@ -210,6 +213,40 @@ def ref_lib() -> ctypes.CDLL | None:
 
 def addr(a: np.ndarray) -> int:
     return a.ctypes.data
+
+
+# ---------------------------------------------------------------------------
+# hybrid sampler and calibrator (calibrator.cpp:67-138)
+
+CALIBRATION_DTYPE = np.dtype([("operation", "<u4"), ("bytes", "<u4"), ("queue_bucket", "<u4"),
+                              ("locality_bucket", "<u4"), ("count", "<u8"), ("mean_ns", "<u8"),
+                              ("p50_ns", "<u8"), ("p95_ns", "<u8"), ("p99_ns", "<u8"),
+                              ("log_mean", "<f8"), ("log_sigma", "<f8")])
+
+
+def sampler_run(warmup, rate, seed, access, sequence) -> np.ndarray:
+    """flags[i] = HybridSampler(warmup, rate, seed).reference(sequence[i],
+    access[i]) in order; access is (n, 4) u32.  ValueError for a bad rate."""
+    access = np.ascontiguousarray(access, np.uint32).reshape(-1, 4)
+    sequence = np.ascontiguousarray(sequence, np.uint64)
+    flags = np.zeros(len(access), np.uint8)
+    rc = lib().orc_sampler_run(warmup, rate, seed, addr(access), addr(sequence), len(access),
+                               addr(flags))
+    if rc == 1:
+        raise ValueError("sample_rate must be in [0, 1]")
+    assert rc == 0
+    return flags
+
+
+def calibrate(access, latency) -> np.ndarray:
+    """Calibrator estimates of every observed class, in class order."""
+    access = np.ascontiguousarray(access, np.uint32).reshape(-1, 4)
+    latency = np.ascontiguousarray(latency, np.uint64)
+    rows = np.zeros(max(len(access), 1), CALIBRATION_DTYPE)
+    n = lib().orc_calibrate(addr(access), addr(latency), len(access), addr(rows))
+    if n < 0:
+        raise ValueError("latency_ns must be positive")
+    return rows[:n]
 
 
 # ---------------------------------------------------------------------------
