@@ -415,10 +415,14 @@ __device__ __forceinline__ void load_record(const hbf_record32* rec, std::size_t
 // index would put the group in scratch memory).
 constexpr int kPipe = 4;
 constexpr std::size_t kGroupSpan = static_cast<std::size_t>(kPipe) * kWave;
+// The summary pass, whose occupancy its per-plane LDS state limits (not its
+// registers), keeps twice as many steps in flight per wave.
+constexpr int kSumPipe = 8;
 
-struct RecordPipe {
-    uint4 ca[kPipe], cb[kPipe];  // the group being worked through
-    uint4 na[kPipe], nb[kPipe];  // the next group, in flight
+template <int D>
+struct RecordPipeT {
+    uint4 ca[D], cb[D];  // the group being worked through
+    uint4 na[D], nb[D];  // the next group, in flight
 
     __device__ __forceinline__ void issue(const hbf_record32* rec, std::size_t g,
                                           std::size_t end, int lane)
@@ -426,7 +430,7 @@ struct RecordPipe {
         const uint4* p = reinterpret_cast<const uint4*>(rec);
         const std::size_t words = 2 * end;  // 16-byte words in the tile's records
 #pragma unroll
-        for (int j = 0; j < kPipe; ++j) {
+        for (int j = 0; j < D; ++j) {
             const std::size_t w = 2 * (g + static_cast<std::size_t>(j) * kWave) + lane;
             na[j] = make_uint4(0, 0, 0, 0);
             nb[j] = na[j];
@@ -442,7 +446,7 @@ struct RecordPipe {
     __device__ __forceinline__ void promote()
     {
 #pragma unroll
-        for (int j = 0; j < kPipe; ++j) {
+        for (int j = 0; j < D; ++j) {
             ca[j] = na[j];
             cb[j] = nb[j];
         }
@@ -462,12 +466,14 @@ struct RecordPipe {
         A = ca[0];
         B = cb[0];
 #pragma unroll
-        for (int j = 0; j + 1 < kPipe; ++j) {
+        for (int j = 0; j + 1 < D; ++j) {
             ca[j] = ca[j + 1];
             cb[j] = cb[j + 1];
         }
     }
 };
+
+using RecordPipe = RecordPipeT<kPipe>;
 
 // Record-per-lane form of a step (lane r gets record r's two word pairs).
 __device__ __forceinline__ void to_records(const uint4& A, const uint4& B, int lane, uint4& x,
@@ -788,21 +794,22 @@ __device__ __forceinline__ bool linear_detect(const KArgs& a, const std::uint64_
     return true;
 }
 
-// A linear group: kPipe consecutive linear steps continuing one another
+// A linear group: D consecutive linear steps continuing one another
 // (record r of the group at address a0 + r * bytes0), each step with its own
 // issue time, all inside the cached range.  Checked at once on the group's
 // registers: lane l looks at word pair l & 1 of records 64 j + 32 h + (l >> 1)
 // for every step j and half h.
+template <int D>
 struct GroupLin {
-    std::uint32_t page1[kPipe];
-    std::uint64_t issue[kPipe];
+    std::uint32_t page1[D];
+    std::uint64_t issue[D];
     std::uint32_t bytes;
 };
 
-template <bool kRefresh>
+template <bool kRefresh, int D>
 __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t* fence,
-                                             RangeCache& rcu, const RecordPipe& pipe,
-                                             std::uint64_t base_ps, int lane, GroupLin& gl)
+                                             RangeCache& rcu, const RecordPipeT<D>& pipe,
+                                             std::uint64_t base_ps, int lane, GroupLin<D>& gl)
 {
     const uint4 xu = make_uint4(rfl32(pipe.ca[0].x), rfl32(pipe.ca[0].y), rfl32(pipe.ca[0].z),
                                 rfl32(pipe.ca[0].w));
@@ -815,10 +822,10 @@ __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t
     const std::uint64_t half = 32ull * b0;  // bytes between the two halves of a step
     const std::uint64_t mine = a0 + static_cast<std::uint64_t>(lane >> 1) * b0;
     const bool odd = (lane & 1) != 0;
-    std::uint32_t ilo[kPipe], ihi[kPipe];
+    std::uint32_t ilo[D], ihi[D];
     bool ok = true;
 #pragma unroll
-    for (int j = 0; j < kPipe; ++j) {
+    for (int j = 0; j < D; ++j) {
         ilo[j] = rl32(pipe.ca[j].x, 1);
         ihi[j] = rl32(pipe.ca[j].y, 1);
         const uint4& A = pipe.ca[j];
@@ -845,14 +852,14 @@ __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t
     }
     const std::uint32_t mode = rcu.meta & 0xffu;
     const std::uint64_t step = 64ull * b0;
-    const std::uint64_t span = kPipe * step;
+    const std::uint64_t span = D * step;
     if ((mode != 1 && mode != 2) || (rcu.meta & (1u << 8)) == 0 || span > rcu.end - a0) {
         return false;
     }
     const std::uint64_t page_mask = (1ull << a.page_shift) - 1;
     const std::uint64_t off0 = a0 - rcu.base;
 #pragma unroll
-    for (int j = 0; j < kPipe; ++j) {
+    for (int j = 0; j < D; ++j) {
         const std::uint64_t off = off0 + static_cast<std::uint64_t>(j) * step;
         if ((off >> a.page_shift) != ((off + step - 1) >> a.page_shift) ||
             (off & ~page_mask) > ~0ull - rcu.file_offset) {
@@ -897,18 +904,19 @@ struct LinBatch {
         }
         ++n;
     }
-    // Appends a linear group's kPipe steps (needs n <= 64 - kPipe).
-    __device__ __forceinline__ void push_group(const GroupLin& gl, std::size_t s)
+    // Appends a linear group's D steps (needs n <= 64 - D).
+    template <int D>
+    __device__ __forceinline__ void push_group(const GroupLin<D>& gl, std::size_t s)
     {
         if (n == 0) {
             first = s;
         }
         const int j = static_cast<int>(threadIdx.x) - n;
-        if (j >= 0 && j < kPipe) {
+        if (j >= 0 && j < D) {
             std::uint32_t p1 = gl.page1[0];
             std::uint64_t i0 = gl.issue[0];
 #pragma unroll
-            for (int k = 1; k < kPipe; ++k) {
+            for (int k = 1; k < D; ++k) {
                 p1 = j == k ? gl.page1[k] : p1;
                 i0 = j == k ? gl.issue[k] : i0;
             }
@@ -916,7 +924,7 @@ struct LinBatch {
             issue = i0;
             bytes = gl.bytes;
         }
-        n += kPipe;
+        n += D;
     }
 };
 
@@ -1009,11 +1017,41 @@ __device__ __forceinline__ std::uint64_t plane_service(const KArgs& a, std::uint
     return (bits & 2u) ? a.program_ps : 0ull;
 }
 
+// The range fences (r_nfence <= kMaxFences), a lane's share in registers:
+// fetch_fences issues every load before store_fences writes any of them, so
+// a tile's set-up waits for memory once rather than once per 64 fences.
+constexpr int kFencesPerLane = static_cast<int>(kMaxFences) / kWave;
+
+struct FenceRegs {
+    std::uint64_t v[kFencesPerLane];
+};
+
+__device__ __forceinline__ FenceRegs fetch_fences(const KArgs& a, int lane)
+{
+    FenceRegs f;
+#pragma unroll
+    for (int k = 0; k < kFencesPerLane; ++k) {
+        const std::uint32_t j = static_cast<std::uint32_t>(lane + k * kWave);
+        f.v[k] = j < a.r_nfence ? a.r_base[static_cast<std::size_t>(j) * a.r_stride] : 0ull;
+    }
+    return f;
+}
+
+__device__ __forceinline__ void store_fences(const KArgs& a, const FenceRegs& f,
+                                             std::uint64_t* fence, int lane)
+{
+#pragma unroll
+    for (int k = 0; k < kFencesPerLane; ++k) {
+        const std::uint32_t j = static_cast<std::uint32_t>(lane + k * kWave);
+        if (j < a.r_nfence) {
+            fence[j] = f.v[k];
+        }
+    }
+}
+
 __device__ __forceinline__ void load_fences(const KArgs& a, std::uint64_t* fence, int lane)
 {
-    for (std::uint32_t j = lane; j < a.r_nfence; j += kWave) {
-        fence[j] = a.r_base[static_cast<std::size_t>(j) * a.r_stride];
-    }
+    store_fences(a, fetch_fences(a, lane), fence, lane);
 }
 
 // Step view of a batch of linear steps: lane k < n stands for step k, with
@@ -1176,8 +1214,18 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     std::uint32_t* p_fc = p_l1 + a.Rp;
     __shared__ std::uint64_t xp[33];
     const int lane = threadIdx.x;
-    load_fences(a, fence, lane);
+    const std::size_t tile = blockIdx.x;
+    const std::size_t begin = tile * a.tile;
+    const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
+    // set-up loads and the first group of records are in flight together
+    const FenceRegs fr = fetch_fences(a, lane);
+    // (the page-register variant takes no linear groups and keeps 4 deep)
+    constexpr int kDepth = kHits ? kPipe : kSumPipe;
+    constexpr std::size_t kSpan = static_cast<std::size_t>(kDepth) * kWave;
+    RecordPipeT<kDepth> pipe;
+    pipe.issue(rec, begin, end, lane);
     load_xfer_table(a, xp, lane);
+    store_fences(a, fr, fence, lane);
     for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
         p_fi[r] = 0;
         p_rA[r] = 0;
@@ -1191,26 +1239,21 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
         c_B[r] = 0;
     }
     __syncthreads();
-    const std::size_t tile = blockIdx.x;
-    const std::size_t begin = tile * a.tile;
-    const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
     RangeCache rc = empty_cache();
     RangeCache rcu = empty_cache();  // wave-uniform copy for linear steps
-    RecordPipe pipe;
-    pipe.issue(rec, begin, end, lane);
     LinBatch q = empty_batch();
     LinBatch dq = empty_batch();  // a folded batch whose descriptors are not written yet
     std::uint64_t modeled = 0;
-    for (std::size_t g = begin; g < end; g += kGroupSpan) {
+    for (std::size_t g = begin; g < end; g += kSpan) {
         pipe.promote();
         write_descs(desc, dq, lane);
-        if (g + kGroupSpan < end) {
-            pipe.issue(rec, g + kGroupSpan, end, lane);
+        if (g + kSpan < end) {
+            pipe.issue(rec, g + kSpan, end, lane);
         }
-        const std::size_t gend = g + kGroupSpan < end ? g + kGroupSpan : end;
-        if (!kHits && a.slots == 1 && g + kGroupSpan <= end && q.n <= kWave - kPipe) {
+        const std::size_t gend = g + kSpan < end ? g + kSpan : end;
+        if (!kHits && a.slots == 1 && g + kSpan <= end && q.n <= kWave - kDepth) {
             // a whole group of linear steps joins the batch at once
-            GroupLin gl;
+            GroupLin<kDepth> gl;
             if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
                 q.push_group(gl, g);
                 if (q.n == kWave || gend >= end) {
@@ -1893,21 +1936,51 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
         t.mk = umax64(t.mk, most);
         t.lat_max = umax64(t.lat_max, most - q.issue);
     }
-    // Completions, one step at a time: lane j writes record j.  Step values
-    // come in scalar registers; with one transfer time for the whole batch
-    // the channel offset x (63 - j) is a per-lane constant.
+    // Completions.  Record j >= 1 of step k completes at max(P_k, top_k -
+    // x_k (63 - j)) and record 0 at D0_k.  Lane j writes record j of every
+    // step (whole 512-B rows: a row left partly written for a later store
+    // costs more than the selects), taking P_k, top_k and D0_k from lane k by
+    // shuffles; with one transfer time for the whole batch x (63 - j) is a
+    // per-lane constant.  Nothing is outstanding here (the batch's values
+    // were read above); saying so keeps a conservative wait for vector
+    // memory out of the store loop, which would drain the stores.
     const std::uint64_t x0 = readlane64(v.x, 0);
     const bool xuni = __ballot(m && v.x != x0) == 0;
     const std::uint64_t back = static_cast<std::uint64_t>(63 - lane);
-    const std::uint64_t xm0 = x0 * back;
-    const bool lead_lane = lane == 0 || a.contention != 0;
-    for (int k = 0; k < q.n; ++k) {
-        const std::uint64_t lead_k = readlane64(lead, k);
-        const std::uint64_t top_k = readlane64(top, k);
-        const std::uint64_t i0 = readlane64(q.issue, k);
-        const std::uint64_t xm = xuni ? xm0 : readlane64(v.x, k) * back;
-        const std::uint64_t done = umax64(lead_lane ? lead_k : i0, top_k - xm);
-        completion[q.first + static_cast<std::size_t>(k) * kWave + lane] = done;
+    const std::uint64_t P = a.contention ? lead : q.issue;
+    const std::uint64_t D0 = umax64(lead, top - 63 * v.x);
+    std::uint64_t* out = completion + q.first + lane;
+    wait_vector_loads();
+    const bool z = lane == 0;
+    if (xuni) {
+        const std::uint64_t xm = x0 * back;
+        int k = 0;
+        for (; k + 4 <= q.n; k += 4) {
+            std::uint64_t pk[4], tk[4], dk[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                pk[u] = shfl64(P, k + u);
+                tk[u] = shfl64(top, k + u);
+                dk[u] = shfl64(D0, k + u);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const std::uint64_t done = umax64(pk[u], tk[u] - xm);
+                out[static_cast<std::size_t>(k + u) * kWave] = z ? dk[u] : done;
+            }
+        }
+        for (; k < q.n; ++k) {
+            const std::uint64_t done = umax64(shfl64(P, k), shfl64(top, k) - xm);
+            const std::uint64_t d = shfl64(D0, k);
+            out[static_cast<std::size_t>(k) * kWave] = z ? d : done;
+        }
+    } else {
+        for (int k = 0; k < q.n; ++k) {
+            const std::uint64_t xm = shfl64(v.x, k) * back;
+            const std::uint64_t done = umax64(shfl64(P, k), shfl64(top, k) - xm);
+            const std::uint64_t d = shfl64(D0, k);
+            out[static_cast<std::size_t>(k) * kWave] = z ? d : done;
+        }
     }
     // Status bytes four steps at a time: 4 for a page-register hit (every
     // record but a sensing lane 0), 0 otherwise.
@@ -1932,6 +2005,66 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
     }
 }
 
+// A tile's plane carry-ins are packed like its summaries: word w of the
+// mask covers planes [64 w, 64 w + 64), so lane l reads bit l of each word.
+// Eight words' carries are in flight before any is written.
+__device__ __forceinline__ void load_plane_carry(const KArgs& a, const MaskWord* tmask,
+                                                 const PlaneCarry* pcarry, std::size_t tile,
+                                                 std::uint64_t* p_busy, std::uint32_t* p_tag,
+                                                 int lane)
+{
+    constexpr int kWords = 8;
+    const std::uint32_t words = mask_words(a);
+    const MaskWord* tm = tmask + tile * words;
+    const PlaneCarry* pc = pcarry + tile * a.Rp;
+    const std::uint64_t below = lanemask_lt(lane);
+    for (std::uint32_t w0 = 0; w0 < words; w0 += kWords) {
+        PlaneCarry c[kWords];
+        bool has[kWords];
+#pragma unroll
+        for (int k = 0; k < kWords; ++k) {
+            has[k] = false;
+            if (w0 + k < words) {
+                const MaskWord mw = tm[w0 + k];
+                if ((mw.bits >> lane) & 1ull) {
+                    has[k] = true;
+                    c[k] = pc[mw.base + static_cast<std::uint32_t>(__popcll(mw.bits & below))];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kWords; ++k) {
+            if (has[k]) {
+                const std::uint32_t r = (w0 + k) * kWave + static_cast<std::uint32_t>(lane);
+                p_busy[r] = c[k].busy;
+                p_tag[r] = static_cast<std::uint32_t>(c[k].tag1);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void load_chan_carry(const KArgs& a, const std::uint64_t* ccarry,
+                                                std::size_t tile, std::uint64_t* c_busy, int lane)
+{
+    constexpr int kPer = 4;
+    const std::uint64_t* cc = ccarry + tile * a.Rc;
+    for (std::uint32_t r0 = 0; r0 < a.Rc; r0 += kPer * kWave) {
+        std::uint64_t v[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const std::uint32_t r = r0 + k * kWave + static_cast<std::uint32_t>(lane);
+            v[k] = r < a.Rc ? cc[r] : 0ull;
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const std::uint32_t r = r0 + k * kWave + static_cast<std::uint32_t>(lane);
+            if (r < a.Rc) {
+                c_busy[r] = v[k];
+            }
+        }
+    }
+}
+
 template <bool kRefresh, bool kHits>
 __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, std::size_t n,
                                               std::uint64_t base_ps, const PlaneCarry* pcarry,
@@ -1950,21 +2083,13 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
     __shared__ std::uint64_t xp[33];
     const int lane = threadIdx.x;
     const std::size_t tile = blockIdx.x;
-    load_fences(a, fence, lane);
+    // set-up loads in flight together: the fences, then the carry-ins, which
+    // exist for the planes the tile touches (the only ones it reads)
+    const FenceRegs fr = fetch_fences(a, lane);
     load_xfer_table(a, xp, lane);
-    // carry-ins exist for the planes the tile touches, the only ones it reads
-    const std::uint32_t words = mask_words(a);
-    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
-        const int at = slot(tmask, words, tile, r);
-        if (at >= 0) {
-            const PlaneCarry c = pcarry[tile * a.Rp + at];
-            p_busy[r] = c.busy;
-            p_tag[r] = static_cast<std::uint32_t>(c.tag1);
-        }
-    }
-    for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
-        c_busy[r] = ccarry[tile * a.Rc + r];
-    }
+    load_plane_carry(a, tmask, pcarry, tile, p_busy, p_tag, lane);
+    load_chan_carry(a, ccarry, tile, c_busy, lane);
+    store_fences(a, fr, fence, lane);
     __syncthreads();
     const std::size_t begin = tile * a.tile;
     const std::size_t end = begin + a.tile < n ? begin + a.tile : n;

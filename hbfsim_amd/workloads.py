@@ -504,3 +504,78 @@ def kv_spans(shape: PagedKvShape, step: int,
     first = np.zeros(len(base) + 1, np.uint64)
     np.cumsum(nl, out=first[1:])
     return base, first, np.concatenate(ops)
+
+
+# ---------------------------------------------------------------------------
+# Routed-expert trace events (adapters/vllm_capacity/trace_schema.json,
+# written by trace_collector.py:163-199) compiled into record streams.  An
+# event is one (token, layer) of a request: its top-k experts and the
+# compact list of their tensor accesses, each a byte range
+# [source_offset_begin, source_offset_end) of a checkpoint shard with the
+# pages it touches and a stream-wide access_order_sequence.  Each tensor
+# access becomes one span of line reads at the shard's base address, in
+# access order.
+
+
+def _event_int(event: dict, key: str) -> int:
+    value = event[key]
+    if isinstance(value, bool) or not isinstance(value, int) or value < 0:
+        raise ValueError(f"trace event field {key} must be a non-negative integer")
+    return value
+
+
+def trace_event_spans(events, shard_base: dict[str, int], page_bytes: int, line_bytes: int,
+                      whole_pages: bool = False) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Spans (base, first, op) for the tensor accesses of schema-1 trace
+    events, in access order.  A span reads the lines covering the tensor's
+    byte range (with whole_pages, its pages [page_begin, page_end)) at
+    shard_base[source_shard] + offset.  Raises ValueError where the
+    reference's readers reject an event (trace_replay.py:100-108 and
+    trace_collector.py:154-160: schema version, empty or repeated top-k ids)
+    and where an event disagrees with how the collector wrote it (page
+    bounds from the offsets, access sequences consecutive from one event to
+    the next, an expert tensor of an expert outside the top-k)."""
+    if page_bytes <= 0 or line_bytes <= 0 or page_bytes % line_bytes:
+        raise ValueError("page_bytes must be a positive multiple of line_bytes")
+    parts: list[tuple[int, int, int]] = []
+    next_seq = None
+    for event in events:
+        if isinstance(event, (str, bytes)):
+            import json
+            event = json.loads(event)
+        if event.get("schema_version") != 1:
+            raise ValueError("unsupported trace schema")
+        ids = [int(v) for v in event["topk_expert_ids"]]
+        if not ids or len(set(ids)) != len(ids) or min(ids) < 0:
+            raise ValueError("invalid top-k expert list")
+        begin = _event_int(event, "access_order_sequence_begin")
+        end = _event_int(event, "access_order_sequence_end")
+        if next_seq is not None and begin != next_seq:
+            raise ValueError("access order sequences are not consecutive across events")
+        tensors = sorted(event["expert_tensors"], key=lambda t: _event_int(t, "access_order_sequence"))
+        if [int(t["access_order_sequence"]) for t in tensors] != list(range(begin, end)):
+            raise ValueError("tensor access sequences do not fill the event's range")
+        next_seq = end
+        for t in tensors:
+            if int(t["expert_id"]) not in ids:
+                raise ValueError("tensor access of an expert outside the top-k")
+            lo = _event_int(t, "source_offset_begin")
+            hi = _event_int(t, "source_offset_end")
+            if hi <= lo:
+                raise ValueError("empty tensor byte range")
+            pb, pe = _event_int(t, "page_begin"), _event_int(t, "page_end")
+            if pb != lo // page_bytes or pe != (hi + page_bytes - 1) // page_bytes:
+                raise ValueError("page bounds differ from the byte range")
+            shard = t["source_shard"]
+            if shard not in shard_base:
+                raise ValueError(f"no base address for shard {shard!r}")
+            if int(shard_base[shard]) % line_bytes:
+                raise ValueError("shard base addresses must be line-aligned")
+            if whole_pages:
+                lo, hi = pb * page_bytes, pe * page_bytes
+            first_line = lo // line_bytes
+            lines = (hi + line_bytes - 1) // line_bytes - first_line
+            parts.append((int(shard_base[shard]) + first_line * line_bytes, lines, 0))
+    if not parts:
+        raise ValueError("trace contains no expert accesses")
+    return _spans(parts)
