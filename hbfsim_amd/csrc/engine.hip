@@ -1098,7 +1098,7 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
                                              std::uint64_t* p_rA, std::uint64_t* p_rB,
                                              std::uint64_t* c_A, std::uint64_t* c_B,
                                              std::uint32_t* p_f1, std::uint32_t* p_l1,
-                                             std::uint32_t* p_fc)
+                                             std::uint8_t* p_fc)
 {
     const StepView v = step_view(a, xp, q, lane);
     const bool m = v.m;
@@ -1211,7 +1211,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     std::uint64_t* c_B = c_A + a.Rc;
     std::uint32_t* p_f1 = reinterpret_cast<std::uint32_t*>(c_B + a.Rc);
     std::uint32_t* p_l1 = p_f1 + a.Rp;
-    std::uint32_t* p_fc = p_l1 + a.Rp;
+    std::uint8_t* p_fc = reinterpret_cast<std::uint8_t*>(p_l1 + a.Rp);  // class bits < 16
     __shared__ std::uint64_t xp[33];
     const int lane = threadIdx.x;
     const std::size_t tile = blockIdx.x;
@@ -1372,7 +1372,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
                 if (!has) {
                     p_f1[pkey] = l1;
                     p_fi[pkey] = li;
-                    p_fc[pkey] = lc;
+                    p_fc[pkey] = static_cast<std::uint8_t>(lc);
                 }
                 const std::uint64_t sA = p_rA[pkey];
                 const std::uint64_t sB = p_rB[pkey];
@@ -3384,7 +3384,7 @@ __global__ __launch_bounds__(64) void k_k2_hits(KArgs a, const hbf_record32* rec
 
 std::size_t lds_summary(const KArgs& a)
 {
-    return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 12ull * a.Rp;
+    return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 8ull * a.Rp + ((a.Rp + 7ull) & ~7ull);
 }
 
 std::size_t lds_apply(const KArgs& a)
