@@ -428,6 +428,17 @@ struct RecordPipeT {
                                           std::size_t end, int lane)
     {
         const uint4* p = reinterpret_cast<const uint4*>(rec);
+        if (g + static_cast<std::size_t>(D) * kWave <= end) {
+            // the whole group lies inside the tile (every group but a tile's
+            // last): plain loads, no per-load bounds or zero fill
+            const uint4* q = p + 2 * g + static_cast<std::size_t>(lane);
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                na[j] = q[static_cast<std::size_t>(2 * j) * kWave];
+                nb[j] = q[static_cast<std::size_t>(2 * j + 1) * kWave];
+            }
+            return;
+        }
         const std::size_t words = 2 * end;  // 16-byte words in the tile's records
 #pragma unroll
         for (int j = 0; j < D; ++j) {

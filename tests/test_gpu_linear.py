@@ -213,3 +213,52 @@ def test_linear_groups_bit_exact(options):
             p.check_state()
         finally:
             p.close()
+
+
+def striding_stream(pages, b, seed, reps=2):
+    """Linear steps, one per listed page (offset 0 of the page), one batch
+    of 64 steps per list; each step with its own issue time."""
+    rng = np.random.default_rng(seed)
+    lanes = np.arange(64, dtype=np.uint64)
+    out, t = [], 1_000_000
+    base = BASE
+    for _ in range(reps):
+        for pg in pages:
+            t += int(rng.choice([0, 700, 30_000]))
+            step = np.zeros((64, 4), np.uint64)
+            step[:, 0] = np.uint64(base + pg * PAGE) + lanes * np.uint64(b)
+            step[:, 1] = b
+            step[:, 2] = t
+            out.append(step)
+    return np.concatenate(out)
+
+
+@pytest.mark.parametrize("profile,planes", [(C0, 64), (C2, 512)], ids=["c0", "c2"])
+@pytest.mark.parametrize("shape", ["stride1", "span_below", "span_equal", "stride_over",
+                                   "pairs"])
+def test_linear_batches_rising_pages_across_one_stripe_period(profile, planes, shape):
+    """Batches whose pages rise from step to step: within one striping period
+    (span below the plane count) the runs of equal page are the plane groups;
+    from a span of one period on, two pages of a batch may share a plane and
+    grouping goes by key.  Both must agree with the oracle."""
+    if shape == "stride1":
+        pages = list(range(64))
+    elif shape == "span_below":
+        pages = sorted(set(np.linspace(0, planes - 1, 64).astype(int).tolist()))
+    elif shape == "span_equal":  # the first and last page share a plane
+        pages = sorted(set(np.linspace(0, planes, 64).astype(int).tolist()))
+    elif shape == "stride_over":
+        pages = [k * (planes // 32 + 1) for k in range(64)]
+    else:  # two steps per page, as weight streaming has them
+        pages = [k // 2 for k in range(64)]
+    pages = [p % 1100 for p in pages]
+    assert pages == sorted(pages)
+    ranges = [(BASE, 1200 * PAGE, 1)]
+    rec = striding_stream(pages, 128 if shape == "pairs" else 256, len(pages) + planes)
+    p = parity.Pair(profile, ranges)
+    try:
+        (_, _, grep), _ = check(p, rec, f"rising pages {shape} on {planes} planes")
+        assert grep["modeled"] == len(rec)
+        p.check_state()
+    finally:
+        p.close()
