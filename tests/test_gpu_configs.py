@@ -3,6 +3,8 @@
 oracle.  Config 3 (paged KV cache) runs every step of a reduced shape
 bit-exact, and one full-size step (1.17e9 records, 150 GB of KV) whose prefix
 matches the oracle and whose totals match the configuration's arithmetic.
+One full config-2 step (2.7e8 records) is checked the same way, and against
+itself run as two runs with carried state.
 The GPU record compiler is checked against its host mirror on the way."""
 from __future__ import annotations
 
@@ -131,3 +133,54 @@ def test_kv_full_size_step():
         np.testing.assert_array_equal(d_st[:prefix].cpu().numpy(), ost)
     finally:
         pair.close()
+
+
+def test_config2_full_size_step():
+    """One whole config-2 decode step (the bench's step 0: 2.7e8 records of
+    48 x 128 Qwen3-30B-A3B experts on the 512-plane profile).  Its record
+    prefix equals the host mirror of the compiler; its first 6M completions
+    and statuses equal the oracle's (a completion depends only on earlier
+    records); every record is a modeled read, no completion precedes its
+    issue and the makespan is the last completion; and the same step run as
+    two runs with carried state gives the same completions bit for bit."""
+    import torch
+    shape = w.QWEN3_30B_A3B
+    seg = w.moe_segments(shape, w.moe_selection(shape, 1)[0])
+    d_rec = w.gpu_segment_records(seg, shape.lines_per_expert, shape.line, shape.gap_ps,
+                                  shape.issuers)
+    n = int(d_rec.shape[0])
+    assert n > 2.5e8
+    prefix = 6_000_000
+    rec = d_rec[:prefix].cpu().numpy().view(np.uint64)
+    np.testing.assert_array_equal(
+        rec, w.segment_records(seg, shape.lines_per_expert, shape.line, shape.gap_ps,
+                               shape.issuers, 0, prefix))
+    c2 = w.PROFILES / "c2.json"
+    whole = parity.Pair(c2, w.moe_ranges(shape))
+    split = parity.Pair(c2, w.moe_ranges(shape))
+    try:
+        d_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+        d_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+        rep = whole.engine.run(d_rec, d_comp, d_st)
+        torch.cuda.synchronize()
+        assert rep["records"] == rep["modeled"] == rep["reads"] == n
+        assert rep["writes"] == 0 and rep["bypass"] == 0 and rep["unsupported"] == 0
+        assert n - n // 64 <= rep["page_hits"] < n
+        assert bool((d_comp >= d_rec[:, 2]).all())
+        assert int(d_comp.max()) == rep["makespan_ps"]
+        ocomp, ost, _, _ = oracle_py.run(whole.params, whole.ranges, whole.count, rec, 0,
+                                         oracle_py.OracleState(whole.params), threads=8)
+        np.testing.assert_array_equal(d_comp[:prefix].cpu().numpy().view(np.uint64), ocomp)
+        np.testing.assert_array_equal(d_st[:prefix].cpu().numpy(), ost)
+        cut = (n // 3) | 37  # inside a step and a tile
+        s_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+        s_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+        r1 = split.engine.run(d_rec[:cut], s_comp[:cut], s_st[:cut])
+        r2 = split.engine.run(d_rec[cut:], s_comp[cut:], s_st[cut:])
+        torch.cuda.synchronize()
+        assert torch.equal(s_comp, d_comp) and torch.equal(s_st, d_st)
+        assert r1["page_hits"] + r2["page_hits"] == rep["page_hits"]
+        assert max(r1["makespan_ps"], r2["makespan_ps"]) == rep["makespan_ps"]
+    finally:
+        whole.close()
+        split.close()
