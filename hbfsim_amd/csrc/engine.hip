@@ -362,6 +362,19 @@ __device__ __forceinline__ void load_xfer_table(const KArgs& a, std::uint64_t* x
     }
 }
 
+// The same in two halves, so that later loads can be issued in between.
+__device__ __forceinline__ std::uint64_t fetch_xfer(const KArgs& a, int lane)
+{
+    return lane < 33 ? a.xfer_pow2[lane] : 0ull;
+}
+
+__device__ __forceinline__ void store_xfer(std::uint64_t* xp, std::uint64_t v, int lane)
+{
+    if (lane < 33) {
+        xp[lane] = v;
+    }
+}
+
 // Waits for every outstanding vector memory operation (s_waitcnt vmcnt(0)).
 // Called where a step has just made its own per-lane loads, so that none of
 // them is still outstanding when the next step starts: the record pipeline's
@@ -1230,13 +1243,14 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
     // set-up loads and the first group of records are in flight together
     const FenceRegs fr = fetch_fences(a, lane);
+    const std::uint64_t xv = fetch_xfer(a, lane);
     // (the page-register variant takes no linear groups and keeps 4 deep)
     constexpr int kDepth = kHits ? kPipe : kSumPipe;
     constexpr std::size_t kSpan = static_cast<std::size_t>(kDepth) * kWave;
     RecordPipeT<kDepth> pipe;
     pipe.issue(rec, begin, end, lane);
-    load_xfer_table(a, xp, lane);
     store_fences(a, fr, fence, lane);
+    store_xfer(xp, xv, lane);
     for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
         p_fi[r] = 0;
         p_rA[r] = 0;
@@ -2029,18 +2043,27 @@ __device__ __forceinline__ void load_plane_carry(const KArgs& a, const MaskWord*
     const MaskWord* tm = tmask + tile * words;
     const PlaneCarry* pc = pcarry + tile * a.Rp;
     const std::uint64_t below = lanemask_lt(lane);
-    for (std::uint32_t w0 = 0; w0 < words; w0 += kWords) {
+    // (unrolled over the at most kMaxPlanes / 64 words: a loop back edge
+    // would make the compiler wait for every carry load before the next)
+#pragma unroll
+    for (std::uint32_t w0 = 0; w0 < kMaxPlanes / kWave; w0 += kWords) {
+        if (w0 >= words) {
+            break;
+        }
+        // the mask words first, then the carries: vector loads complete in
+        // issue order, so a word loaded after a carry would wait for it
+        MaskWord mw[kWords];
+#pragma unroll
+        for (int k = 0; k < kWords; ++k) {
+            mw[k] = w0 + k < words ? tm[w0 + k] : MaskWord{0, 0, 0};
+        }
         PlaneCarry c[kWords];
         bool has[kWords];
 #pragma unroll
         for (int k = 0; k < kWords; ++k) {
-            has[k] = false;
-            if (w0 + k < words) {
-                const MaskWord mw = tm[w0 + k];
-                if ((mw.bits >> lane) & 1ull) {
-                    has[k] = true;
-                    c[k] = pc[mw.base + static_cast<std::uint32_t>(__popcll(mw.bits & below))];
-                }
+            has[k] = ((mw[k].bits >> lane) & 1ull) != 0;
+            if (has[k]) {
+                c[k] = pc[mw[k].base + static_cast<std::uint32_t>(__popcll(mw[k].bits & below))];
             }
         }
 #pragma unroll
@@ -2097,10 +2120,11 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
     // set-up loads in flight together: the fences, then the carry-ins, which
     // exist for the planes the tile touches (the only ones it reads)
     const FenceRegs fr = fetch_fences(a, lane);
-    load_xfer_table(a, xp, lane);
+    const std::uint64_t xv = fetch_xfer(a, lane);
     load_plane_carry(a, tmask, pcarry, tile, p_busy, p_tag, lane);
     load_chan_carry(a, ccarry, tile, c_busy, lane);
     store_fences(a, fr, fence, lane);
+    store_xfer(xp, xv, lane);
     __syncthreads();
     const std::size_t begin = tile * a.tile;
     const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
