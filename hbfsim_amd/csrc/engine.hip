@@ -1533,6 +1533,29 @@ __device__ __forceinline__ ChanSum chan_compose(const ChanSum& s1, const ChanSum
 }
 
 // Level 1: thread (g, r) folds the summaries of group g's tiles.
+// Slots of plane r in tiles t .. t + kChunk - 1 (those below t1; -1 where
+// a tile did not touch r).  The chunk's mask words are loaded whole and
+// together before any is decoded: decoding each word as it arrives would
+// put a memory round trip per tile in front of the summaries' loads.
+__device__ __forceinline__ void chunk_slots(const MaskWord* tmask, std::uint32_t words,
+                                            std::size_t t, std::size_t t1, std::uint32_t r,
+                                            int (&at)[kChunk])
+{
+    MaskWord mw[kChunk];
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+        mw[k] = t + k < t1 ? tmask[(t + k) * words + r / 64] : MaskWord{0, 0, 0};
+    }
+    const std::uint32_t bit = r % 64;
+    const std::uint64_t below = (1ull << bit) - 1;
+#pragma unroll
+    for (int k = 0; k < kChunk; ++k) {
+        at[k] = ((mw[k].bits >> bit) & 1u) != 0
+                    ? static_cast<int>(mw[k].base) + __popcll(mw[k].bits & below)
+                    : -1;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, std::size_t ngroups,
                                                   const PlaneSum* psum,
                                                   const MaskWord* tmask, const ChanSum* csum,
@@ -1554,13 +1577,15 @@ __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, s
     if (r < a.Rp) {
         const std::uint32_t words = mask_words(a);
         PlaneSum acc{};  // the identity: no first record
-        for (std::size_t t = t0; t < t1; t += kChunk) {
+#pragma unroll
+        for (std::uint32_t c = 0; c < kGroup / kChunk; ++c) {
+            const std::size_t t = t0 + static_cast<std::size_t>(c) * kChunk;
+            if (t >= t1) {
+                break;
+            }
             int at[kChunk];
             PlaneSum buf[kChunk];
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                at[k] = t + k < t1 ? slot(tmask, words, t + k, r) : -1;
-            }
+            chunk_slots(tmask, words, t, t1, r, at);
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
                 if (at[k] >= 0) {
@@ -1782,13 +1807,15 @@ __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
         const PlaneCarry c0 = gpcarry[g * a.Rp + r];
         const std::uint32_t words = mask_words(a);
         std::uint64_t busy = c0.busy, tag1 = c0.tag1;
-        for (std::size_t t = t0; t < t1; t += kChunk) {
+#pragma unroll
+        for (std::uint32_t c = 0; c < kGroup / kChunk; ++c) {
+            const std::size_t t = t0 + static_cast<std::size_t>(c) * kChunk;
+            if (t >= t1) {
+                break;
+            }
             int at[kChunk];
             PlaneSum buf[kChunk];
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                at[k] = t + k < t1 ? slot(tmask, words, t + k, r) : -1;
-            }
+            chunk_slots(tmask, words, t, t1, r, at);
 #pragma unroll
             for (int k = 0; k < kChunk; ++k) {
                 if (at[k] >= 0) {
