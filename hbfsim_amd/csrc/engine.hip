@@ -2057,6 +2057,24 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
     }
 }
 
+// The apply pass copies a tile's step descriptors into LDS with its other
+// set-up loads (tiles of up to kStageSteps steps, 4 KiB): read per window
+// from memory instead, each read would wait for the previous window's
+// completion stores, vector memory completing in issue order.
+constexpr std::uint32_t kStageSteps = 256;
+
+__host__ __device__ __forceinline__ std::uint32_t staged_steps(const KArgs& a)
+{
+    return a.tile <= kStageSteps * kWave ? a.tile / kWave : 0u;
+}
+
+// Byte offset of the staged descriptors in the apply pass's LDS (after the
+// fences, plane busy, channel busy and plane tags; 16-byte aligned).
+__host__ __device__ __forceinline__ std::size_t apply_desc_offset(const KArgs& a)
+{
+    return (8ull * (a.r_nfence + a.Rp + a.Rc) + 4ull * a.Rp + 15ull) & ~15ull;
+}
+
 // A tile's plane carry-ins are packed like its summaries: word w of the
 // mask covers planes [64 w, 64 w + 64), so lane l reads bit l of each word.
 // Eight words' carries are in flight before any is written.
@@ -2126,7 +2144,7 @@ __device__ __forceinline__ void load_chan_carry(const KArgs& a, const std::uint6
     }
 }
 
-template <bool kRefresh, bool kHits>
+template <bool kRefresh, bool kHits, bool kStaged = false>
 __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, std::size_t n,
                                               std::uint64_t base_ps, const PlaneCarry* pcarry,
                                               const MaskWord* tmask,
@@ -2146,15 +2164,40 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
     const std::size_t tile = blockIdx.x;
     // set-up loads in flight together: the fences, then the carry-ins, which
     // exist for the planes the tile touches (the only ones it reads)
+    const std::size_t begin = tile * a.tile;
+    const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
+    // kStaged: the launch found descriptors and a tile of at most kStageSteps
+    // steps (a template parameter: as a run-time flag it costs registers)
+    constexpr bool stage = kStaged;
+    StepDesc* sdesc = reinterpret_cast<StepDesc*>(reinterpret_cast<unsigned char*>(sm) +
+                                                  apply_desc_offset(a));
+    const std::size_t tsteps = (end - begin + kWave - 1) / kWave;
     const FenceRegs fr = fetch_fences(a, lane);
     const std::uint64_t xv = fetch_xfer(a, lane);
+    constexpr int kDescPerLane = static_cast<int>(kStageSteps) / kWave;
+    StepDesc dv[kDescPerLane];
+#pragma unroll
+    for (int k = 0; k < kDescPerLane; ++k) {
+        const std::size_t j = static_cast<std::size_t>(k * kWave + lane);
+        dv[k] = StepDesc{0, 0, 0};
+        if (stage && j < tsteps) {
+            dv[k] = desc[begin / kWave + j];
+        }
+    }
     load_plane_carry(a, tmask, pcarry, tile, p_busy, p_tag, lane);
     load_chan_carry(a, ccarry, tile, c_busy, lane);
     store_fences(a, fr, fence, lane);
     store_xfer(xp, xv, lane);
+    if (stage) {
+#pragma unroll
+        for (int k = 0; k < kDescPerLane; ++k) {
+            const std::size_t j = static_cast<std::size_t>(k * kWave + lane);
+            if (j < tsteps) {
+                sdesc[j] = dv[k];
+            }
+        }
+    }
     __syncthreads();
-    const std::size_t begin = tile * a.tile;
-    const std::size_t end = begin + a.tile < n ? begin + a.tile : n;
     std::uint64_t seq = tile_seq[tile];
     std::uint64_t n_rec = 0, n_mod = 0, n_byp = 0, n_uns = 0, n_rd = 0, n_wr = 0;
     std::uint64_t n_hit = 0, n_prog = 0, n_hyb = 0, mk = 0, lat_lo = 0, lat_hi = 0;
@@ -2186,7 +2229,11 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
             const int nst = static_cast<int>((wend - w0 + kWave - 1) / kWave);
             StepDesc sd{0, 0, 0};
             if (lane < nst) {
-                sd = desc[w0 / kWave + lane];
+                if (stage) {
+                    sd = sdesc[(w0 - begin) / kWave + lane];
+                } else {
+                    sd = desc[w0 / kWave + lane];
+                }
             }
             const std::uint64_t all = nst == kWave ? ~0ull : ((1ull << nst) - 1);
             if (__ballot(lane < nst && sd.bytes != 0) == all) {
@@ -3451,7 +3498,7 @@ std::size_t lds_summary(const KArgs& a)
 
 std::size_t lds_apply(const KArgs& a)
 {
-    return 8ull * (a.r_nfence + 1ull * a.Rp + 1ull * a.Rc) + 4ull * a.Rp;
+    return apply_desc_offset(a) + 16ull * staged_steps(a);
 }
 
 // Records per tile when the configuration leaves it open: the largest power
@@ -4125,14 +4172,23 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
                            e->d_gccarry, e->d_gseq, e->d_pcarry, e->d_ccarry, e->d_tseq);
     }
     (void)hipEventRecord(e->ev[2], stream);
+    const bool staged = desc != nullptr && staged_steps(a) != 0;
     if (k2) {
         hipLaunchKernelGGL((k_apply<false, true>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
                            base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
                            d_status, e->d_tile_rep, hits, desc);
+    } else if (refresh_records && staged) {
+        hipLaunchKernelGGL((k_apply<true, false, true>), grid, dim3(kWave), lds_c, stream, a,
+                           d_rec, n, base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq,
+                           d_comp, d_status, e->d_tile_rep, hits, desc);
     } else if (refresh_records) {
         hipLaunchKernelGGL((k_apply<true, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
                            base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
                            d_status, e->d_tile_rep, hits, desc);
+    } else if (staged) {
+        hipLaunchKernelGGL((k_apply<false, false, true>), grid, dim3(kWave), lds_c, stream, a,
+                           d_rec, n, base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq,
+                           d_comp, d_status, e->d_tile_rep, hits, desc);
     } else {
         hipLaunchKernelGGL((k_apply<false, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
                            base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
