@@ -122,8 +122,11 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
     //    the LDS slots of its six neighbours (`zero` outside the grid; the
     //    cell itself outside the staged region, which disturbs only cells
     //    within `sweeps` of the region edge), 1 / den with den summed in the
-    //    CPU restatement's order, and its ambient term.
+    //    CPU restatement's order, and its ambient term.  The grid index and
+    //    die come first (1a), so that the window's global loads (2) are in
+    //    flight while the rest (1b, with its divisions) is computed.
     std::uint32_t gidx[kCells], die[kCells], fl[kCells];
+    std::uint32_t cx[kCells], cy[kCells], cz[kCells];
     std::uint32_t nbr[kCells][6];
     double rden[kCells], topv[kCells];
     std::uint32_t safe_die = 0;
@@ -150,25 +153,11 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
             const int gxx = x0 + static_cast<int>(xi);
             const int gyy = y0 + static_cast<int>(yi);
             std::uint32_t f = 0, g = 0, d = safe_die;
-            std::uint32_t n0 = zero, n1 = zero, n2 = zero, n3 = zero, n4 = zero, n5 = zero;
-            double den = cdt, top = 0.0;
             if (c < cells && gxx >= 0 && gxx < static_cast<int>(nx) && gyy >= 0 &&
                 gyy < static_cast<int>(ny)) {
                 g = (zi * ny + static_cast<std::uint32_t>(gyy)) * nx + static_cast<std::uint32_t>(gxx);
                 f = kIn;
                 if (xi >= h && xi < h + tx && yi >= h && yi < h + ty) f |= kInterior;
-                if (gxx > 0) { n0 = xi > 0 ? c - 1 : c; den += gx; }
-                if (gxx + 1 < static_cast<int>(nx)) { n1 = xi + 1 < rx ? c + 1 : c; den += gx; }
-                if (gyy > 0) { n2 = yi > 0 ? c - rx : c; den += gy; }
-                if (gyy + 1 < static_cast<int>(ny)) { n3 = yi + 1 < ry ? c + rx : c; den += gy; }
-                if (zi > 0) { n4 = c - plane; den += gz; }
-                if (zi + 1 < nz) {
-                    n5 = c + plane;
-                    den += gz;
-                } else {
-                    den += gb;
-                    top = gbtb;
-                }
                 if (kCoupled) {
                     const int qx = qx0 + (gxx < rx0 ? -1 : (gxx >= rx0 + static_cast<int>(a.rw) ? 1 : 0));
                     const int qy = qy0 + (gyy < ry0 ? -1 : (gyy >= ry0 + static_cast<int>(a.rh) ? 1 : 0));
@@ -179,17 +168,16 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
             fl[k] = f;
             gidx[k] = g;
             die[k] = d;
-            nbr[k][0] = n0; nbr[k][1] = n1; nbr[k][2] = n2;
-            nbr[k][3] = n3; nbr[k][4] = n4; nbr[k][5] = n5;
-            rden[k] = (f & kIn) ? 1.0 / den : 0.0;
-            topv[k] = top;
+            cx[k] = xi;
+            cy[k] = yi;
+            cz[k] = zi;
             xi += a.step_x;
-            const std::uint32_t cx = xi >= rx ? 1u : 0u;
-            xi -= cx * rx;
-            yi += a.step_y + cx;
-            const std::uint32_t cy = yi >= ry ? 1u : 0u;
-            yi -= cy * ry;
-            zi += a.step_z + cy;
+            const std::uint32_t carry_x = xi >= rx ? 1u : 0u;
+            xi -= carry_x * rx;
+            yi += a.step_y + carry_x;
+            const std::uint32_t carry_y = yi >= ry ? 1u : 0u;
+            yi -= carry_y * ry;
+            zi += a.step_z + carry_y;
         }
     }
     // 2. Every independent global load at once (cells outside the grid load
@@ -204,6 +192,34 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
         } else {
             pin[k] = a.power[gidx[k]];
         }
+    }
+    // 1b. Neighbour slots, 1 / den and the ambient term.
+#pragma unroll
+    for (int k = 0; k < kCells; ++k) {
+        const std::uint32_t c = tid + k * kThreads;
+        const std::uint32_t xi = cx[k], yi = cy[k], zi = cz[k];
+        const int gxx = x0 + static_cast<int>(xi);
+        const int gyy = y0 + static_cast<int>(yi);
+        std::uint32_t n0 = zero, n1 = zero, n2 = zero, n3 = zero, n4 = zero, n5 = zero;
+        double den = cdt, top = 0.0;
+        if (fl[k] & kIn) {
+            if (gxx > 0) { n0 = xi > 0 ? c - 1 : c; den += gx; }
+            if (gxx + 1 < static_cast<int>(nx)) { n1 = xi + 1 < rx ? c + 1 : c; den += gx; }
+            if (gyy > 0) { n2 = yi > 0 ? c - rx : c; den += gy; }
+            if (gyy + 1 < static_cast<int>(ny)) { n3 = yi + 1 < ry ? c + rx : c; den += gy; }
+            if (zi > 0) { n4 = c - plane; den += gz; }
+            if (zi + 1 < nz) {
+                n5 = c + plane;
+                den += gz;
+            } else {
+                den += gb;
+                top = gbtb;
+            }
+        }
+        nbr[k][0] = n0; nbr[k][1] = n1; nbr[k][2] = n2;
+        nbr[k][3] = n3; nbr[k][4] = n4; nbr[k][5] = n5;
+        rden[k] = (fl[k] & kIn) ? 1.0 / den : 0.0;
+        topv[k] = top;
     }
     if (kCoupled) {
         // this window's retention and refresh decisions for every die (all
