@@ -24,11 +24,17 @@ ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0
-ALGO_BYTES_PER_ACCESS = 40  # 32-B record in + 8-B completion out
-# The same 40 B split over the two per-record kernels: the summary pass reads
-# each record, the apply pass writes each completion (linear steps replay from
-# the summary pass's step descriptors, not from the records).
-KERNEL_BYTES_PER_ACCESS = {"k_summary": 32, "k_apply": 8}
+# Algorithmic bytes per access: the record in + the 8-B completion out, 40 B
+# with 32-byte records and 24 B with packed 16-byte ones (the roofline of
+# each form is its own; the two are never mixed).  The same bytes split over
+# the two per-record kernels: the summary pass reads each record, the apply
+# pass writes each completion (linear steps replay from the summary pass's
+# step descriptors, not from the records).
+RECORD_BYTES = {"packed": 16, "32": 32}
+
+
+def kernel_bytes(records: str) -> dict:
+    return {"k_summary": RECORD_BYTES[records], "k_apply": 8}
 
 
 def parse() -> argparse.Namespace:
@@ -42,6 +48,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="budget for the CPU-oracle baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--records", choices=("packed", "32"), default="packed",
+                    help="record form in HBM: packed 16-byte records (hbf_record16) or "
+                         "32-byte ones (hbf_record32); packing runs before the timed region")
+    ap.add_argument("--no-compare", action="store_true",
+                    help="with packed records, skip timing the same steps from 32-byte ones")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first fill and copy 2 GiB (known HBM bytes) so that counter runs "
                          "can calibrate FETCH_SIZE / WRITE_SIZE")
@@ -188,7 +199,7 @@ def bench_c4(args) -> dict:
     cell_sweeps = cells * w.C4_GRID["sweeps"]
     thermal_gbps = 16 * cell_sweeps / (per_window_ms / 1e3) / 1e9
     n = int(rec.shape[0])
-    engine_gbps = ALGO_BYTES_PER_ACCESS * (n + rep["refreshes"]) / (phases["engine"] / 1e3) / 1e9
+    engine_gbps = (RECORD_BYTES["32"] + 8) * (n + rep["refreshes"]) / (phases["engine"] / 1e3) / 1e9
     dominant = max(("thermal_chain", "engine"), key=lambda k: phases[k])
     roof = ({"bound": "hbm", "kernel": "k_thermal_window", "achieved": thermal_gbps,
              "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": thermal_gbps / PEAK_HBM_GBPS,
@@ -328,42 +339,36 @@ def main() -> None:
 
     profile, ranges, batches, desc, host_records = build_workload(args.config, args.steps,
                                                                   args.batches)
-    e = engine.Engine(str(profile))
-    for base, length, perms in ranges:
-        e.register(base, length, perms)
-    n = max(int(b.shape[0]) for b in batches)
-    comp = torch.empty(n, dtype=torch.int64, device="cuda")
-    stream = torch.cuda.current_stream()
-    base_ps = 0
-    log(f"warmup {args.warmup} steps of {n} records")
-    for k in range(args.warmup):
-        b = batches[k % len(batches)]
-        rep = e.run(b, comp, None, base_ps, stream)
-        base_ps = rep["makespan_ps"]
-    torch.cuda.synchronize()
-    kernel_ms = np.zeros(3)
-    accesses = 0
-    log(f"timing {args.steps} steps")
-    t0 = time.perf_counter()
-    for k in range(args.steps):
-        b = batches[k % len(batches)]
-        rep = e.run(b, comp, None, base_ps, stream)
-        base_ps = rep["makespan_ps"]
-        accesses += rep["records"]
-        kernel_ms += np.array(e.kernel_ms()[:3])
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    dt = t1 - t0
-    value = accesses / dt
-    avg_ms = kernel_ms / args.steps
+    records = args.records
+    timed = batches
+    if records == "packed":
+        try:
+            timed = [engine.pack_records(b) for b in batches]
+        except ValueError as err:
+            log(f"{err}: timing 32-byte records")
+            records = "32"
+    desc = dict(desc, records=("packed 16-byte records (hbf_record16)" if records == "packed"
+                               else "32-byte records (hbf_record32)"))
+    value, dt, avg_ms, accesses = time_steps(engine, profile, ranges, timed, records, args)
+    other = None
+    if records == "packed" and not args.no_compare:
+        # the same steps from 32-byte records, for comparison (its own roofline)
+        v32, dt32, ms32, _ = time_steps(engine, profile, ranges, batches, "32", args)
+        other = {"records": "32-byte records (hbf_record32)", "value": v32,
+                 "ms_per_step": dt32 / args.steps * 1e3, "algorithmic_bytes_per_access": 40,
+                 "pipeline_frac": v32 * 40 / 1e9 / PEAK_HBM_GBPS,
+                 "kernel_ms": {nm: float(v) for nm, v in
+                               zip(["k_summary", "k_carry", "k_apply"], ms32)}}
+    algo = RECORD_BYTES[records] + 8
+    kb = kernel_bytes(records)
     names = ["k_summary", "k_carry", "k_apply"]
     # the dominant per-record kernel (the carry chain works per tile and resource)
     dominant = 0 if avg_ms[0] >= avg_ms[2] else 2
     per_launch = accesses / args.steps
-    achieved = (KERNEL_BYTES_PER_ACCESS[names[dominant]] * per_launch /
-                (avg_ms[dominant] / 1e3) / 1e9)
-    traffic, traffic_src = (committed_traffic("engine_traffic_config2.txt", names[dominant],
-                                              int(per_launch))
+    achieved = kb[names[dominant]] * per_launch / (avg_ms[dominant] / 1e3) / 1e9
+    summary = ("engine_traffic_config2_packed.txt" if records == "packed"
+               else "engine_traffic_config2.txt")
+    traffic, traffic_src = (committed_traffic(summary, names[dominant], int(per_launch))
                             if args.config == "c2" else (None, None))
     out = {
         "metric": "modeled HBF accesses/sec on 1 MI355X",
@@ -380,19 +385,54 @@ def main() -> None:
         "data": "synthetic",
         "config": desc,
         "roofline": {"bound": "hbm", "kernel": names[dominant],
-                     "algorithmic": f"{KERNEL_BYTES_PER_ACCESS[names[dominant]]} B per access x "
+                     "algorithmic": f"{kb[names[dominant]]} B per access x "
                                     f"{int(per_launch)} accesses per launch",
                      "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBPS, "traffic": traffic,
                      "traffic_source": traffic_src,
                      "kernel_ms": {nm: float(v) for nm, v in zip(names, avg_ms)},
-                     "pipeline_frac": value * ALGO_BYTES_PER_ACCESS / 1e9 / PEAK_HBM_GBPS},
+                     "algorithmic_bytes_per_access": algo,
+                     "pipeline_frac": value * algo / 1e9 / PEAK_HBM_GBPS},
     }
+    if other is not None:
+        out["records32"] = other
     if not args.no_cpu:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline(profile, ranges, host_records, args.cpu_seconds)
-    e.close()
     print(json.dumps(out), flush=True)
+
+
+def time_steps(engine, profile, ranges, batches, records, args):
+    """Warm-up steps, then exactly `args.steps` timed steps of one engine
+    (bracketed by device synchronisation); returns (accesses/s, seconds,
+    average per-kernel ms, accesses)."""
+    import torch
+    e = engine.Engine(str(profile))
+    for base, length, perms in ranges:
+        e.register(base, length, perms)
+    run = e.run_packed if records == "packed" else e.run
+    n = max(int(b.shape[0]) for b in batches)
+    comp = torch.empty(n, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream()
+    base_ps = 0
+    log(f"warmup {args.warmup} steps of {n} records ({records})")
+    for k in range(args.warmup):
+        rep = run(batches[k % len(batches)], comp, None, base_ps, stream)
+        base_ps = rep["makespan_ps"]
+    torch.cuda.synchronize()
+    kernel_ms = np.zeros(3)
+    accesses = 0
+    log(f"timing {args.steps} steps ({records})")
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        rep = run(batches[k % len(batches)], comp, None, base_ps, stream)
+        base_ps = rep["makespan_ps"]
+        accesses += rep["records"]
+        kernel_ms += np.array(e.kernel_ms()[:3])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    e.close()
+    return accesses / dt, dt, kernel_ms / args.steps, accesses
 
 
 if __name__ == "__main__":

@@ -616,6 +616,35 @@ HBF_API int hbfsim_amd_run_device(hbfsim_context* c, const hbf_record32* records
     return HBFSIM_OK;
 }
 
+HBF_API int hbfsim_amd_run_device_packed(hbfsim_context* c, const hbf_record16* records,
+                                         size_t n, uint64_t* completion_ps, uint8_t* status,
+                                         uint64_t base_ps, void* stream,
+                                         hbfsim_amd_report* report)
+{
+    if (report != nullptr) {
+        std::memset(report, 0, sizeof(*report));
+    }
+    if (c == nullptr || (n != 0 && (records == nullptr || completion_ps == nullptr))) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(c->mu);
+    int st = ensure_engine(c);
+    if (st != HBFSIM_OK) {
+        return st;
+    }
+    hbfsim_amd_report r{};
+    st = hbfamd::engine_run_packed(c->eng, records, n, completion_ps, status, base_ps, stream,
+                                   &r);
+    if (st != HBFSIM_OK) {
+        return st;
+    }
+    account(c, r);
+    if (report != nullptr) {
+        *report = r;
+    }
+    return HBFSIM_OK;
+}
+
 HBF_API int hbfsim_amd_run(hbfsim_context* c, const hbf_record32* records, size_t n,
                            uint64_t* completion_ps, uint8_t* status, uint64_t base_ps,
                            hbfsim_amd_report* report)

@@ -33,6 +33,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 namespace hbfamd {
@@ -432,13 +433,23 @@ constexpr std::size_t kGroupSpan = static_cast<std::size_t>(kPipe) * kWave;
 // registers), keeps twice as many steps in flight per wave.
 constexpr int kSumPipe = 8;
 
+// A step in the registers of one lane: the coalesced halves of 32-byte
+// records, or one packed 16-byte record.
+struct Step32 {
+    uint4 A, B;
+};
+struct Step16 {
+    uint4 R;
+};
+
 template <int D>
 struct RecordPipeT {
+    using Step = Step32;
     uint4 ca[D], cb[D];  // the group being worked through
     uint4 na[D], nb[D];  // the next group, in flight
 
-    __device__ __forceinline__ void issue(const hbf_record32* rec, std::size_t g,
-                                          std::size_t end, int lane)
+    __device__ __forceinline__ void issue(const void* rec, std::size_t g, std::size_t end,
+                                          int lane)
     {
         const uint4* p = reinterpret_cast<const uint4*>(rec);
         if (g + static_cast<std::size_t>(D) * kWave <= end) {
@@ -476,8 +487,8 @@ struct RecordPipeT {
         }
     }
     // Makes the group in flight current and issues the one after it.
-    __device__ __forceinline__ void advance(const hbf_record32* rec, std::size_t next,
-                                            std::size_t end, int lane)
+    __device__ __forceinline__ void advance(const void* rec, std::size_t next, std::size_t end,
+                                            int lane)
     {
         promote();
         if (next < end) {
@@ -485,10 +496,10 @@ struct RecordPipeT {
         }
     }
     // The current group's next step, in the coalesced halves.
-    __device__ __forceinline__ void take(uint4& A, uint4& B)
+    __device__ __forceinline__ void take(Step32& st)
     {
-        A = ca[0];
-        B = cb[0];
+        st.A = ca[0];
+        st.B = cb[0];
 #pragma unroll
         for (int j = 0; j + 1 < D; ++j) {
             ca[j] = ca[j + 1];
@@ -496,6 +507,70 @@ struct RecordPipeT {
         }
     }
 };
+
+// Packed records (hbf_record16, 16 B): word 0 holds the address (bits 0-47)
+// and byte count (bits 48-63), word 1 the issue time (bits 0-55) and the
+// operation (bits 56-63).  A step is 1 KiB and lane r loads record r whole,
+// so no transpose is needed, and a group holds one register quad per step.
+template <int D>
+struct PackedPipeT {
+    using Step = Step16;
+    uint4 c[D];   // the group being worked through
+    uint4 nx[D];  // the next group, in flight
+
+    __device__ __forceinline__ void issue(const void* rec, std::size_t g, std::size_t end,
+                                          int lane)
+    {
+        const uint4* p = reinterpret_cast<const uint4*>(rec);
+        if (g + static_cast<std::size_t>(D) * kWave <= end) {
+            const uint4* q = p + g + static_cast<std::size_t>(lane);
+#pragma unroll
+            for (int j = 0; j < D; ++j) {
+                nx[j] = q[static_cast<std::size_t>(j) * kWave];
+            }
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            const std::size_t i = g + static_cast<std::size_t>(j) * kWave + lane;
+            nx[j] = make_uint4(0, 0, 0, 0);
+            if (i < end) {
+                nx[j] = p[i];
+            }
+        }
+    }
+    __device__ __forceinline__ void promote()
+    {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+            c[j] = nx[j];
+        }
+    }
+    __device__ __forceinline__ void advance(const void* rec, std::size_t next, std::size_t end,
+                                            int lane)
+    {
+        promote();
+        if (next < end) {
+            issue(rec, next, end, lane);
+        }
+    }
+    __device__ __forceinline__ void take(Step16& st)
+    {
+        st.R = c[0];
+#pragma unroll
+        for (int j = 0; j + 1 < D; ++j) {
+            c[j] = c[j + 1];
+        }
+    }
+};
+
+// A packed record in the two word quads the decoder takes (x: address,
+// bytes; y: issue time, operation).
+__device__ __forceinline__ void unpack16(const uint4& r, uint4& x, uint4& y)
+{
+    x = make_uint4(r.x, r.y & 0xffffu, r.y >> 16, 0u);
+    y = make_uint4(r.z, r.w & 0xffffffu, r.w >> 24, 0u);
+}
 
 using RecordPipe = RecordPipeT<kPipe>;
 
@@ -516,6 +591,16 @@ __device__ __forceinline__ void to_records(const uint4& A, const uint4& B, int l
     x = make_uint4(pick(A.x, B.x, sx), pick(A.y, B.y, sx), pick(A.z, B.z, sx),
                    pick(A.w, B.w, sx));
     y = make_uint4(pick(A.x, B.x, sy), pick(A.y, B.y, sy), pick(A.z, B.z, sy), 0);
+}
+
+__device__ __forceinline__ void step_records(const Step32& st, int lane, uint4& x, uint4& y)
+{
+    to_records(st.A, st.B, lane, x, y);
+}
+
+__device__ __forceinline__ void step_records(const Step16& st, int, uint4& x, uint4& y)
+{
+    unpack16(st.R, x, y);
 }
 
 // Channel and global plane id of a media page (the profile's allocation
@@ -761,9 +846,17 @@ __device__ __forceinline__ std::uint32_t rl32(std::uint32_t v, int k)
     return static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), k));
 }
 
+// The range and page checks of a step whose 64 records already follow
+// record 0 (xu: its address and bytes, yu: its issue time and operation).
+template <bool kRefresh>
+__device__ __forceinline__ bool linear_tail(const KArgs& a, const std::uint64_t* fence,
+                                            RangeCache& rcu, const uint4& xu, const uint4& yu,
+                                            std::uint64_t base_ps, std::uint32_t& page1,
+                                            std::uint64_t& issue0, std::uint32_t& bytes0);
+
 template <bool kRefresh>
 __device__ __forceinline__ bool linear_detect(const KArgs& a, const std::uint64_t* fence,
-                                              RangeCache& rcu, const uint4& A, const uint4& B,
+                                              RangeCache& rcu, const Step32& st,
                                               std::uint64_t base_ps, bool full, int lane,
                                               std::uint32_t& page1, std::uint64_t& issue0,
                                               std::uint32_t& bytes0)
@@ -771,6 +864,8 @@ __device__ __forceinline__ bool linear_detect(const KArgs& a, const std::uint64_
     if (!full) {
         return false;
     }
+    const uint4& A = st.A;
+    const uint4& B = st.B;
     // record 0: address and bytes in lane 0, issue and operation in lane 1
     const uint4 xu = make_uint4(rfl32(A.x), rfl32(A.y), rfl32(A.z), rfl32(A.w));
     const uint4 yu = make_uint4(rl32(A.x, 1), rl32(A.y, 1), rl32(A.z, 1), 0);
@@ -791,6 +886,45 @@ __device__ __forceinline__ bool linear_detect(const KArgs& a, const std::uint64_
     if (__ballot(odd ? !ok_odd : !ok_even) != 0) {
         return false;
     }
+    return linear_tail<kRefresh>(a, fence, rcu, xu, yu, base_ps, page1, issue0, bytes0);
+}
+
+// A packed step: lane l checks its own record against record 0.
+template <bool kRefresh>
+__device__ __forceinline__ bool linear_detect(const KArgs& a, const std::uint64_t* fence,
+                                              RangeCache& rcu, const Step16& st,
+                                              std::uint64_t base_ps, bool full, int lane,
+                                              std::uint32_t& page1, std::uint64_t& issue0,
+                                              std::uint32_t& bytes0)
+{
+    if (!full) {
+        return false;
+    }
+    const uint4& R = st.R;
+    const uint4 r0 = make_uint4(rfl32(R.x), rfl32(R.y), rfl32(R.z), rfl32(R.w));
+    uint4 xu, yu;
+    unpack16(r0, xu, yu);
+    if (yu.z != 0 || xu.z == 0) {
+        return false;  // reads of at least one byte only
+    }
+    const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
+    const std::uint64_t mine = a0 + static_cast<std::uint64_t>(lane) * xu.z;
+    const bool ok = R.x == static_cast<std::uint32_t>(mine) &&
+                    (R.y & 0xffffu) == (mine >> 32) && (R.y >> 16) == xu.z && R.z == r0.z &&
+                    R.w == r0.w;
+    if (__ballot(!ok) != 0) {
+        return false;
+    }
+    return linear_tail<kRefresh>(a, fence, rcu, xu, yu, base_ps, page1, issue0, bytes0);
+}
+
+template <bool kRefresh>
+__device__ __forceinline__ bool linear_tail(const KArgs& a, const std::uint64_t* fence,
+                                            RangeCache& rcu, const uint4& xu, const uint4& yu,
+                                            std::uint64_t base_ps, std::uint32_t& page1,
+                                            std::uint64_t& issue0, std::uint32_t& bytes0)
+{
+    const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
     if (!(a0 >= rcu.base && a0 < rcu.end)) {
         // refill the cache through the full classification
         const Dec d = decode<kRefresh, true>(a, fence, rcu, xu, yu, base_ps);
@@ -831,6 +965,13 @@ struct GroupLin {
 };
 
 template <bool kRefresh, int D>
+__device__ __forceinline__ bool group_tail(const KArgs& a, const std::uint64_t* fence,
+                                           RangeCache& rcu, std::uint64_t base_ps,
+                                           const uint4& xu, std::uint32_t op0,
+                                           const std::uint32_t (&ilo)[D],
+                                           const std::uint32_t (&ihi)[D], GroupLin<D>& gl);
+
+template <bool kRefresh, int D>
 __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t* fence,
                                              RangeCache& rcu, const RecordPipeT<D>& pipe,
                                              std::uint64_t base_ps, int lane, GroupLin<D>& gl)
@@ -867,6 +1008,55 @@ __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t
     if (__ballot(!ok) != 0) {
         return false;
     }
+    return group_tail<kRefresh, D>(a, fence, rcu, base_ps, xu, op0, ilo, ihi, gl);
+}
+
+// A packed group: lane l checks its own record of every step.
+template <bool kRefresh, int D>
+__device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t* fence,
+                                             RangeCache& rcu, const PackedPipeT<D>& pipe,
+                                             std::uint64_t base_ps, int lane, GroupLin<D>& gl)
+{
+    const uint4 r0 = make_uint4(rfl32(pipe.c[0].x), rfl32(pipe.c[0].y), rfl32(pipe.c[0].z),
+                                rfl32(pipe.c[0].w));
+    uint4 xu, yu;
+    unpack16(r0, xu, yu);
+    if (yu.z != 0 || xu.z == 0) {
+        return false;  // reads of at least one byte only
+    }
+    const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
+    const std::uint64_t b0 = xu.z;
+    const std::uint64_t mine = a0 + static_cast<std::uint64_t>(lane) * b0;
+    std::uint32_t ilo[D], ihi[D];
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+        const uint4& R = pipe.c[j];
+        const std::uint32_t w = rfl32(R.w);  // record 0 of step j: issue high, operation
+        ilo[j] = rfl32(R.z);
+        ihi[j] = w & 0xffffffu;
+        const std::uint64_t e = mine + static_cast<std::uint64_t>(j) * 64ull * b0;
+        ok = ok && (w >> 24) == 0 && R.x == static_cast<std::uint32_t>(e) &&
+             (R.y & 0xffffu) == (e >> 32) && (R.y >> 16) == b0 && R.z == ilo[j] && R.w == w;
+    }
+    if (__ballot(!ok) != 0) {
+        return false;
+    }
+    return group_tail<kRefresh, D>(a, fence, rcu, base_ps, xu, 0u, ilo, ihi, gl);
+}
+
+// The range and page checks of a group whose records already continue one
+// another from record 0 (xu: its address and bytes; op0, ilo, ihi: its
+// operation and every step's issue time), and the group's step values.
+template <bool kRefresh, int D>
+__device__ __forceinline__ bool group_tail(const KArgs& a, const std::uint64_t* fence,
+                                           RangeCache& rcu, std::uint64_t base_ps,
+                                           const uint4& xu, std::uint32_t op0,
+                                           const std::uint32_t (&ilo)[D],
+                                           const std::uint32_t (&ihi)[D], GroupLin<D>& gl)
+{
+    const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
+    const std::uint64_t b0 = xu.z;
     if (!(a0 >= rcu.base && a0 < rcu.end)) {
         const uint4 yu = make_uint4(ilo[0], ihi[0], op0, 0);
         const Dec d = decode<kRefresh, true>(a, fence, rcu, xu, yu, base_ps);
@@ -1219,8 +1409,8 @@ __device__ __forceinline__ int slot(const MaskWord* tmask, std::uint32_t words, 
 // class), the (max,+) map of the records after it, and the last page; per
 // channel the map of all its records.  Pages are stored as page + 1 in 32
 // bits (capacity / page_bytes < 2^32 is checked on the host).
-template <bool kRefresh, bool kHits>
-__global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec, std::size_t n,
+template <bool kRefresh, bool kHits, bool kPacked = false>
+__global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
                                                 MaskWord* tmask, ChanSum* csum,
                                                 std::uint64_t* tile_count,
@@ -1244,10 +1434,12 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
     // set-up loads and the first group of records are in flight together
     const FenceRegs fr = fetch_fences(a, lane);
     const std::uint64_t xv = fetch_xfer(a, lane);
-    // (the page-register variant takes no linear groups and keeps 4 deep)
-    constexpr int kDepth = kHits ? kPipe : kSumPipe;
+    // (the page-register variant takes no linear groups and keeps 4 deep;
+    // packed records take half the registers per step and go twice as deep)
+    constexpr int kDepth = kHits ? kPipe : (kPacked ? 2 * kSumPipe : kSumPipe);
     constexpr std::size_t kSpan = static_cast<std::size_t>(kDepth) * kWave;
-    RecordPipeT<kDepth> pipe;
+    using Pipe = std::conditional_t<kPacked, PackedPipeT<kDepth>, RecordPipeT<kDepth>>;
+    Pipe pipe;
     pipe.issue(rec, begin, end, lane);
     store_fences(a, fr, fence, lane);
     store_xfer(xp, xv, lane);
@@ -1291,8 +1483,8 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
             }
         }
         for (std::size_t s = g; s < gend; s += kWave) {
-            uint4 A, B;
-            pipe.take(A, B);
+            typename Pipe::Step st;
+            pipe.take(st);
             const std::size_t i = s + lane;
             const bool valid = i < end;
             if (!kHits && a.slots == 1) {
@@ -1300,7 +1492,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
                 // the tile's last step, and before any other step (order matters)
                 std::uint32_t lp, lb;
                 std::uint64_t li;
-                const bool lin = linear_detect<kRefresh>(a, fence, rcu, A, B, base_ps,
+                const bool lin = linear_detect<kRefresh>(a, fence, rcu, st, base_ps,
                                                          s + kWave <= end, lane, lp, li, lb);
                 if (lin) {
                     q.push(lp, li, lb, s);
@@ -1320,7 +1512,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const hbf_record32* rec
                 }
             }
             uint4 x, y;
-            to_records(A, B, lane, x, y);
+            step_records(st, lane, x, y);
             const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
             const bool m = valid && d.cls == kClsModeled;
             const bool hbit = kHits && valid && hits[i] != 0;
@@ -2144,8 +2336,8 @@ __device__ __forceinline__ void load_chan_carry(const KArgs& a, const std::uint6
     }
 }
 
-template <bool kRefresh, bool kHits, bool kStaged = false>
-__global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, std::size_t n,
+template <bool kRefresh, bool kHits, bool kStaged = false, bool kPacked = false>
+__global__ __launch_bounds__(64) void k_apply(KArgs a, const void* rec, std::size_t n,
                                               std::uint64_t base_ps, const PlaneCarry* pcarry,
                                               const MaskWord* tmask,
                                               const std::uint64_t* ccarry,
@@ -2246,21 +2438,22 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
                 continue;
             }
         }
-        RecordPipe pipe;
+        using Pipe = std::conditional_t<kPacked, PackedPipeT<kPipe>, RecordPipe>;
+        Pipe pipe;
         pipe.issue(rec, w0, wend, lane);
         for (std::size_t g = w0; g < wend; g += kGroupSpan) {
             pipe.advance(rec, g + kGroupSpan, wend, lane);
             const std::size_t gend = g + kGroupSpan < wend ? g + kGroupSpan : wend;
             for (std::size_t s = g; s < gend; s += kWave) {
-                uint4 A, B;
-                pipe.take(A, B);
+                typename Pipe::Step sr;
+                pipe.take(sr);
                 const std::size_t i = s + lane;
                 const bool valid = i < end;
                 if (!kHits && a.slots == 1 && !a.hybrid) {
                     // batched as in the summary pass
                     std::uint32_t lp, lb;
                     std::uint64_t li;
-                    const bool lin = linear_detect<kRefresh>(a, fence, rcu, A, B, base_ps,
+                    const bool lin = linear_detect<kRefresh>(a, fence, rcu, sr, base_ps,
                                                              s + kWave <= end, lane, lp, li, lb);
                     if (lin) {
                         q.push(lp, li, lb, s);
@@ -2273,7 +2466,7 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const hbf_record32* rec, 
                     }
                 }
                 uint4 x, y;
-                to_records(A, B, lane, x, y);
+                step_records(sr, lane, x, y);
                 const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
                 const bool m = valid && d.cls == kClsModeled;
                 const bool hbit = kHits && valid && hits[i] != 0;
@@ -4056,9 +4249,28 @@ int engine_synchronize(engine* e)
     return hip_status(hipDeviceSynchronize());
 }
 
+int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
+                   std::uint64_t* d_comp, std::uint8_t* d_status, std::uint64_t base_ps,
+                   void* stream_ptr, hbfsim_amd_report* out, bool refresh_records);
+
 int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_t* d_comp,
                std::uint8_t* d_status, std::uint64_t base_ps, void* stream_ptr,
                hbfsim_amd_report* out, bool refresh_records)
+{
+    return engine_run_any(e, d_rec, false, n, d_comp, d_status, base_ps, stream_ptr, out,
+                          refresh_records);
+}
+
+int engine_run_packed(engine* e, const hbf_record16* d_rec, std::size_t n,
+                      std::uint64_t* d_comp, std::uint8_t* d_status, std::uint64_t base_ps,
+                      void* stream_ptr, hbfsim_amd_report* out)
+{
+    return engine_run_any(e, d_rec, true, n, d_comp, d_status, base_ps, stream_ptr, out, false);
+}
+
+int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
+                   std::uint64_t* d_comp, std::uint8_t* d_status, std::uint64_t base_ps,
+                   void* stream_ptr, hbfsim_amd_report* out, bool refresh_records)
 {
     if (out != nullptr) {
         std::memset(out, 0, sizeof(*out));
@@ -4070,6 +4282,12 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         (reinterpret_cast<std::uintptr_t>(d_rec) & 15u) != 0 ||
         (reinterpret_cast<std::uintptr_t>(d_comp) & 7u) != 0) {
         return HBFSIM_INVALID_ARGUMENT;
+    }
+    // packed records take the main pipeline only: one page register, no
+    // hybrid sampling, the HBF model (no refresh records: they need flags)
+    if (packed && (e->cfg.model != HBFSIM_AMD_MODEL_HBF || e->cfg.slots != 1 ||
+                   e->cfg.hybrid != 0)) {
+        return HBFSIM_UNSUPPORTED;
     }
     if (e->cfg.model != HBFSIM_AMD_MODEL_HBF && e->cfg.model != HBFSIM_AMD_MODEL_EMPIRICAL) {
         return HBFSIM_UNSUPPORTED;
@@ -4091,7 +4309,8 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         if (refresh_records) {
             return HBFSIM_UNSUPPORTED;
         }
-        return run_empirical(e, d_rec, n, d_comp, d_status, base_ps, stream, out);
+        return run_empirical(e, static_cast<const hbf_record32*>(d_rec), n, d_comp, d_status,
+                             base_ps, stream, out);
     }
     KArgs a = e->args;
     a.tile = e->cfg.tile != 0 ? e->cfg.tile : auto_tile(n);
@@ -4116,7 +4335,8 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         if (halloc(d_hits, n) != hipSuccess) {
             return HBFSIM_CUDA_ERROR;
         }
-        st = k2_hits(e, a, d_rec, n, base_ps, ntiles, stream, d_hits, k2_tags);
+        st = k2_hits(e, a, static_cast<const hbf_record32*>(d_rec), n, base_ps, ntiles, stream,
+                     d_hits, k2_tags);
         if (st != HBFSIM_OK) {
             hfree(d_hits);
             return st;
@@ -4148,6 +4368,10 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
     } else if (refresh_records) {
         hipLaunchKernelGGL((k_summary<true, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
                            n, base_ps, e->d_psum, e->d_tmask, e->d_csum, e->d_tcount,
+                           hits, desc);
+    } else if (packed) {
+        hipLaunchKernelGGL((k_summary<false, false, true>), grid, dim3(kWave), lds_a, stream, a,
+                           d_rec, n, base_ps, e->d_psum, e->d_tmask, e->d_csum, e->d_tcount,
                            hits, desc);
     } else {
         hipLaunchKernelGGL((k_summary<false, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
@@ -4185,6 +4409,14 @@ int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_
         hipLaunchKernelGGL((k_apply<true, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
                            base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
                            d_status, e->d_tile_rep, hits, desc);
+    } else if (packed && staged) {
+        hipLaunchKernelGGL((k_apply<false, false, true, true>), grid, dim3(kWave), lds_c, stream,
+                           a, d_rec, n, base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry,
+                           e->d_tseq, d_comp, d_status, e->d_tile_rep, hits, desc);
+    } else if (packed) {
+        hipLaunchKernelGGL((k_apply<false, false, false, true>), grid, dim3(kWave), lds_c, stream,
+                           a, d_rec, n, base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry,
+                           e->d_tseq, d_comp, d_status, e->d_tile_rep, hits, desc);
     } else if (staged) {
         hipLaunchKernelGGL((k_apply<false, false, true>), grid, dim3(kWave), lds_c, stream, a,
                            d_rec, n, base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq,

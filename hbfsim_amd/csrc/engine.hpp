@@ -65,6 +65,11 @@ int engine_run(engine* e, const hbf_record32* d_records, std::size_t n,
                std::uint64_t* d_completion, std::uint8_t* d_status,
                std::uint64_t base_ps, void* stream, hbfsim_amd_report* out,
                bool refresh_records = false);
+// The same for packed 16-byte records (main pipeline only: one page
+// register, no hybrid sampling, HBF model; else HBFSIM_UNSUPPORTED).
+int engine_run_packed(engine* e, const hbf_record16* d_records, std::size_t n,
+                      std::uint64_t* d_completion, std::uint8_t* d_status,
+                      std::uint64_t base_ps, void* stream, hbfsim_amd_report* out);
 int engine_get_busy_totals(engine* e, std::uint64_t* plane_ps, std::size_t planes,
                            std::uint64_t* channel_ps, std::size_t channels);
 int engine_get_state(engine* e, std::uint64_t* plane_busy, std::uint64_t* plane_tags,

@@ -149,6 +149,22 @@ class Engine:
             ctypes.c_void_p(stream), ctypes.byref(rep)), "run")
         return rep.as_dict()
 
+    def run_packed(self, records: Any, completion: Any, status: Any = None, base_ps: int = 0,
+                   stream: Any = None) -> dict:
+        """Times device-resident packed records (torch int64 [n, 2] on the GPU,
+        hbf_record16, see pack_records)."""
+        n = int(records.shape[0])
+        if stream is None:
+            import torch
+            stream = torch.cuda.current_stream().cuda_stream
+        elif hasattr(stream, "cuda_stream"):
+            stream = stream.cuda_stream
+        rep = nat.Report()
+        nat.check(self._lib.hbfsim_amd_run_device_packed(
+            self._ctx, _ptr(records), n, _ptr(completion), _ptr(status), base_ps,
+            ctypes.c_void_p(stream), ctypes.byref(rep)), "run (packed)")
+        return rep.as_dict()
+
     def run_host(self, records: np.ndarray, base_ps: int = 0,
                  want_status: bool = True) -> tuple[np.ndarray, np.ndarray | None, dict]:
         """Copies host records in, runs on the GPU, copies completions out."""
@@ -325,6 +341,19 @@ class Thermal:
             self.close()
         except Exception:
             pass
+
+
+def pack_records(records: Any) -> Any:
+    """32-byte records (torch int64 [n, 4] on the GPU: addr, bytes, issue_ps,
+    flags) packed into 16-byte ones (int64 [n, 2]: addr | bytes << 48,
+    issue_ps | flags << 56).  ValueError when a record does not fit: address
+    from 2^48, byte count from 2^16, issue time from 2^56 ps, flags from 256."""
+    addr, nbytes, issue, flags = (records[:, k] for k in range(4))
+    if bool(((addr >> 48) != 0).any() | ((nbytes >> 16) != 0).any() |
+            ((issue >> 56) != 0).any() | ((flags >> 8) != 0).any()):
+        raise ValueError("records do not fit the packed 16-byte form")
+    import torch
+    return torch.stack([addr | (nbytes << 48), issue | (flags << 56)], dim=1).contiguous()
 
 
 def media_servers(now_ns: Any, servers: int, latency_ns: int, stream: Any = None) -> Any:

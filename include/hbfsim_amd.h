@@ -190,6 +190,18 @@ typedef struct hbf_record32 {
     uint64_t flags;
 } hbf_record32;
 
+/* Packed 16-byte record, an input format of this engine with no
+ * counterpart in the reference: half the bytes of hbf_record32 per access
+ * for the hot path.  addr_bytes holds the address in bits 0-47 and the byte
+ * count in bits 48-63; issue_op holds issue_ps in bits 0-55 and the
+ * operation (0 read, 1 write) in bits 56-63.  It carries every record whose
+ * address is below 2^48, byte count below 2^16, issue time below 2^56 ps and
+ * flags below 256 (no refresh records). */
+typedef struct hbf_record16 {
+    uint64_t addr_bytes;
+    uint64_t issue_op;
+} hbf_record16;
+
 /* Per-record status byte: bits 0-1 class (0 modeled, 1 bypass: outside
  * every range, 2 unsupported: rejected by the resolver's checks), bit 2
  * page-buffer hit, bit 3 selected by the hybrid sampler, bit 4 write that
@@ -275,6 +287,14 @@ int hbfsim_amd_run_device(hbfsim_context* context,
                           uint64_t* completion_ps, uint8_t* status,
                           uint64_t base_ps, void* stream,
                           hbfsim_amd_report* report);
+/* hbfsim_amd_run_device for packed records: the same results as the
+ * 32-byte records they pack.  Contexts with two page registers, hybrid
+ * sampling or the empirical model return HBFSIM_UNSUPPORTED. */
+int hbfsim_amd_run_device_packed(hbfsim_context* context,
+                                 const hbf_record16* records, size_t n,
+                                 uint64_t* completion_ps, uint8_t* status,
+                                 uint64_t base_ps, void* stream,
+                                 hbfsim_amd_report* report);
 /* Same with host buffers: copies in, runs on the default stream, copies
  * out. */
 int hbfsim_amd_run(hbfsim_context* context, const hbf_record32* records,

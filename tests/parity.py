@@ -53,6 +53,24 @@ class Pair:
                                             self.ostate)
         return (gcomp, gst, grep), (ocomp, ost, orep)
 
+    def run_packed(self, records: np.ndarray, base_ps: int = 0):
+        """run() through the packed 16-byte records; the oracle takes the
+        32-byte records they pack."""
+        import torch
+        from hbfsim_amd.engine import pack_records
+        rec = np.ascontiguousarray(records, dtype=np.uint64).reshape(-1, 4)
+        n = rec.shape[0]
+        d_rec = pack_records(to_device(rec))
+        d_comp = torch.zeros(max(n, 1), dtype=torch.int64, device="cuda")
+        d_st = torch.zeros(max(n, 1), dtype=torch.uint8, device="cuda")
+        grep = self.engine.run_packed(d_rec, d_comp, d_st, base_ps=base_ps)
+        torch.cuda.synchronize()
+        gcomp = d_comp.cpu().numpy().view(np.uint64)[:n]
+        gst = d_st.cpu().numpy()[:n]
+        ocomp, ost, orep, _ = oracle_py.run(self.params, self.ranges, self.count, rec, base_ps,
+                                            self.ostate)
+        return (gcomp, gst, grep), (ocomp, ost, orep)
+
     def check_state(self):
         gp, gc = self.engine.busy_totals()
         np.testing.assert_array_equal(gp, self.ostate.plane_busy_total, "plane busy totals")
