@@ -136,21 +136,45 @@ def cpu_baseline(profile, ranges, host_records: np.ndarray, budget_s: float) -> 
     prof = oracle_py.load_profile(profile)
     params = oracle_py.engine_params(prof)
     orng, count = oracle_py.range_table(ranges, prof["page_bytes"], prof["capacity_bytes"])
-    state = oracle_py.OracleState(params)
-    done = 0
-    base = 0
-    t0 = time.perf_counter()
-    while True:
-        _, _, rep, _ = oracle_py.run(params, orng, count, host_records, base, state)
-        base = rep["makespan_ps"]
-        done += len(host_records)
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": done / dt, "unit": "accesses/s", "cores": 1, "kind": "port",
-            "sample": f"{done} records: the first {len(host_records)} records of step 0, "
-                      f"replayed {done // len(host_records)}x with carried state, "
-                      f"single-threaded oracle ({dt:.1f} s)"}
+
+    def timed(threads: int, seconds: float) -> tuple[float, int, float]:
+        state = oracle_py.OracleState(params)
+        done, base = 0, 0
+        t0 = time.perf_counter()
+        while True:
+            _, _, rep, _ = oracle_py.run(params, orng, count, host_records, base, state,
+                                         threads=threads)
+            base = rep["makespan_ps"]
+            done += len(host_records)
+            if time.perf_counter() - t0 >= seconds:
+                break
+        dt = time.perf_counter() - t0
+        return done / dt, done, dt
+
+    value, done, dt = timed(1, budget_s)
+    out = {"value": value, "unit": "accesses/s", "cores": 1, "kind": "port",
+           "sample": f"{done} records: the first {len(host_records)} records of step 0, "
+                     f"replayed {done // len(host_records)}x with carried state, "
+                     f"single-threaded oracle ({dt:.1f} s)"}
+    # the same sample on the host's cores (the oracle's OpenMP split: tiles
+    # summarised in parallel, composed in order), at most the box's share of 16
+    threads = max(1, min(16, os.cpu_count() or 1))
+    if threads > 1:
+        pv, pdone, pdt = timed(threads, budget_s / 2)
+        out["parallel"] = {"value": pv, "unit": "accesses/s", "cores": threads,
+                           "sample": f"{pdone} records, the same sample ({pdt:.1f} s)"}
+    out["host"] = {"nproc": os.cpu_count(), "cpu": host_cpu()}
+    return out
+
+
+def host_cpu() -> str:
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def bench_c4(args) -> dict:
