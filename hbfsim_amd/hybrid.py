@@ -148,11 +148,19 @@ class Calibrator:
         acc = torch.cat(self._access)
         lat = torch.cat(self._latency)
         n = int(acc.shape[0])
-        rows = torch.empty((n, 9), dtype=torch.int64, device=acc.device)  # 72-byte rows
-        count = ctypes.c_size_t()
-        rc = self._lib.hbfsim_amd_calibrate(_ptr(acc), _ptr(lat), n, _ptr(rows), n,
-                                            ctypes.byref(count),
-                                            ctypes.c_void_p(_stream_handle(stream)))
+        # one 72-byte row per class: start small, and size exactly once the
+        # library has said how many classes there are
+        cap = min(n, 1 << 16)
+        while True:
+            rows = torch.empty((cap, 9), dtype=torch.int64, device=acc.device)
+            count = ctypes.c_size_t()
+            rc = self._lib.hbfsim_amd_calibrate(_ptr(acc), _ptr(lat), n, _ptr(rows), cap,
+                                                ctypes.byref(count),
+                                                ctypes.c_void_p(_stream_handle(stream)))
+            if rc == nat.HBFSIM_INVALID_ARGUMENT and count.value > cap:
+                cap = count.value
+                continue
+            break
         if rc == nat.HBFSIM_INVALID_ARGUMENT:
             raise ValueError("latency_ns must be positive")
         nat.check(rc, "calibrate")
