@@ -1182,6 +1182,37 @@ __device__ __forceinline__ Group group_by(std::uint32_t key, std::uint32_t bits,
     return g;
 }
 
+// Plane grouping of a batch of linear steps (lane k: step k, active lanes a
+// prefix).  Steps on one media page share a plane.  Striping maps the page
+// modulo C W D P = Rp one-to-one onto the planes (mixed-radix digits), so
+// when the batch's pages never fall from lane to lane and span fewer than Rp
+// pages, the runs of equal page are exactly the plane groups: one shuffle and
+// two ballots instead of a ballot per key bit.  Otherwise, by key.
+__device__ __forceinline__ Group group_plane_runs(const KArgs& a, std::uint32_t page1,
+                                                  std::uint32_t key, bool m,
+                                                  std::uint64_t active, int lane)
+{
+    const std::uint32_t prev =
+        static_cast<std::uint32_t>(__shfl(static_cast<int>(page1), lane > 0 ? lane - 1 : 0));
+    const int last_lane = 63 - __clzll(active);
+    const std::uint32_t p0 = rfl32(page1);
+    const std::uint32_t pl = rl32(page1, last_lane);
+    const bool falls = m && lane > 0 && prev > page1;
+    if (__ballot(falls) != 0 || pl - p0 >= a.Rp) {
+        return group_by(key, a.pbits, m, active, lane);
+    }
+    const bool head = m && (lane == 0 || prev != page1);
+    const std::uint64_t heads = __ballot(head);
+    const std::uint64_t upto = lane == 63 ? ~0ull : ((2ull << lane) - 1);
+    const std::uint64_t later = heads & ~upto;
+    Group g;
+    g.uniform = heads == 1ull;
+    g.pred = (m && !head) ? lane - 1 : -1;
+    g.leader = m ? 63 - __clzll(heads & upto) : lane;
+    g.last = m ? (later != 0 ? __ffsll(static_cast<long long>(later)) - 2 : last_lane) : lane;
+    return g;
+}
+
 __device__ __forceinline__ void scan_group(const Group& g, std::uint64_t& A, std::uint64_t& B,
                                            int lane)
 {
@@ -1318,7 +1349,7 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
     const bool m = v.m;
     const std::uint32_t pkey = m ? v.d.plane : 0u;
     const std::uint32_t ckey = m ? v.d.chan : 0u;
-    const Group gp = group_by(pkey, a.pbits, m, v.active, lane);
+    const Group gp = group_plane_runs(a, q.page1, pkey, m, v.active, lane);
     const Group gc = group_by(ckey, a.cbits, m, v.active, lane);
     const std::uint32_t f1 = m ? p_f1[pkey] : 0u;
     const std::uint32_t last_page = m ? p_l1[pkey] : 0u;
@@ -2085,7 +2116,7 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
     const bool m = v.m;
     const std::uint32_t pkey = m ? v.d.plane : 0u;
     const std::uint32_t ckey = m ? v.d.chan : 0u;
-    const Group gp = group_by(pkey, a.pbits, m, v.active, lane);
+    const Group gp = group_plane_runs(a, q.page1, pkey, m, v.active, lane);
     const Group gc = group_by(ckey, a.cbits, m, v.active, lane);
     const std::uint32_t tag = m ? p_tag[pkey] : 0u;
     const std::uint64_t pbusy = m ? p_busy[pkey] : 0ull;
