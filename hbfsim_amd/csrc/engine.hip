@@ -1011,29 +1011,11 @@ __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t
     return group_tail<kRefresh, D>(a, fence, rcu, base_ps, xu, op0, ilo, ihi, gl);
 }
 
-// A packed group of linear steps, as far as it is wave-uniform: the file
-// offset of record 0, the step in bytes and the byte count.  Every record of
-// a step carries the step's issue time, so each lane takes its step's issue
-// time from its own registers when the group joins a batch, and its page from
-// file0 + step index x step (LinBatch::push_packed).
-struct GroupLin16 {
-    std::uint64_t file0;
-    std::uint64_t step;
-    std::uint32_t bytes;
-};
-
-template <bool kRefresh, int D>
-__device__ __forceinline__ bool group_tail16(const KArgs& a, const std::uint64_t* fence,
-                                             RangeCache& rcu, std::uint64_t base_ps,
-                                             const uint4& xu, const uint4& yu, int lane,
-                                             GroupLin16& gl);
-
-// A packed group: lane l checks its own record of every step, with no branch
-// per step (the checks of all steps are and-ed, then one ballot).
+// A packed group: lane l checks its own record of every step.
 template <bool kRefresh, int D>
 __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t* fence,
                                              RangeCache& rcu, const PackedPipeT<D>& pipe,
-                                             std::uint64_t base_ps, int lane, GroupLin16& gl)
+                                             std::uint64_t base_ps, int lane, GroupLin<D>& gl)
 {
     const uint4 r0 = make_uint4(rfl32(pipe.c[0].x), rfl32(pipe.c[0].y), rfl32(pipe.c[0].z),
                                 rfl32(pipe.c[0].w));
@@ -1045,59 +1027,22 @@ __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t
     const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
     const std::uint64_t b0 = xu.z;
     const std::uint64_t mine = a0 + static_cast<std::uint64_t>(lane) * b0;
+    std::uint32_t ilo[D], ihi[D];
     bool ok = true;
-    std::uint32_t hi_or = 0;  // operation bits of every step's record 0
 #pragma unroll
     for (int j = 0; j < D; ++j) {
         const uint4& R = pipe.c[j];
         const std::uint32_t w = rfl32(R.w);  // record 0 of step j: issue high, operation
-        const std::uint32_t lo = rfl32(R.z);
-        hi_or |= w;
+        ilo[j] = rfl32(R.z);
+        ihi[j] = w & 0xffffffu;
         const std::uint64_t e = mine + static_cast<std::uint64_t>(j) * 64ull * b0;
-        ok = ok & (R.x == static_cast<std::uint32_t>(e)) & ((R.y & 0xffffu) == (e >> 32)) &
-             ((R.y >> 16) == b0) & (R.z == lo) & (R.w == w);
+        ok = ok && (w >> 24) == 0 && R.x == static_cast<std::uint32_t>(e) &&
+             (R.y & 0xffffu) == (e >> 32) && (R.y >> 16) == b0 && R.z == ilo[j] && R.w == w;
     }
-    if ((hi_or >> 24) != 0 || __ballot(!ok) != 0) {
+    if (__ballot(!ok) != 0) {
         return false;
     }
-    return group_tail16<kRefresh, D>(a, fence, rcu, base_ps, xu, yu, lane, gl);
-}
-
-// The range and page checks of a packed group whose records already continue
-// one another from record 0 (xu, yu: record 0 unpacked).  Lane j < D checks
-// step j; the checks are those of group_tail.
-template <bool kRefresh, int D>
-__device__ __forceinline__ bool group_tail16(const KArgs& a, const std::uint64_t* fence,
-                                             RangeCache& rcu, std::uint64_t base_ps,
-                                             const uint4& xu, const uint4& yu, int lane,
-                                             GroupLin16& gl)
-{
-    const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
-    const std::uint64_t b0 = xu.z;
-    if (!(a0 >= rcu.base && a0 < rcu.end)) {
-        const Dec d = decode<kRefresh, true>(a, fence, rcu, xu, yu, base_ps);
-        if (d.cls != kClsModeled) {
-            return false;
-        }
-    }
-    const std::uint32_t mode = rcu.meta & 0xffu;
-    const std::uint64_t step = 64ull * b0;
-    const std::uint64_t span = D * step;
-    if ((mode != 1 && mode != 2) || (rcu.meta & (1u << 8)) == 0 || span > rcu.end - a0) {
-        return false;
-    }
-    const std::uint64_t page_mask = (1ull << a.page_shift) - 1;
-    const std::uint64_t off0 = a0 - rcu.base;
-    const std::uint64_t off = off0 + static_cast<std::uint64_t>(lane < D ? lane : 0) * step;
-    const bool bad = ((off >> a.page_shift) != ((off + step - 1) >> a.page_shift)) ||
-                     (off & ~page_mask) > ~0ull - rcu.file_offset;
-    if (__ballot(bad) != 0) {
-        return false;
-    }
-    gl.file0 = rcu.file_offset + off0;
-    gl.step = step;
-    gl.bytes = xu.z;
-    return true;
+    return group_tail<kRefresh, D>(a, fence, rcu, base_ps, xu, 0u, ilo, ihi, gl);
 }
 
 // The range and page checks of a group whose records already continue one
@@ -1191,34 +1136,6 @@ struct LinBatch {
             }
             page1 = p1;
             issue = i0;
-            bytes = gl.bytes;
-        }
-        n += D;
-    }
-
-    // A packed group's steps join at lanes n .. n + D - 1: lane n + j takes
-    // step j's issue time from its own record of step j (every record of a
-    // linear step carries it) and its page from gl.file0 + j * gl.step.
-    template <int D>
-    __device__ __forceinline__ void push_packed(const PackedPipeT<D>& pipe, const GroupLin16& gl,
-                                                std::uint32_t page_shift, std::uint64_t base_ps,
-                                                std::size_t s)
-    {
-        if (n == 0) {
-            first = s;
-        }
-        const int j = static_cast<int>(threadIdx.x) - n;
-        std::uint32_t lo = pipe.c[0].z;
-        std::uint32_t hi = pipe.c[0].w;
-#pragma unroll
-        for (int k = 1; k < D; ++k) {
-            lo = j == k ? pipe.c[k].z : lo;
-            hi = j == k ? pipe.c[k].w : hi;
-        }
-        if (j >= 0 && j < D) {
-            const std::uint64_t f = gl.file0 + static_cast<std::uint64_t>(j) * gl.step;
-            page1 = static_cast<std::uint32_t>((f >> page_shift) + 1);
-            issue = base_ps + (lo | (static_cast<std::uint64_t>(hi) << 32));
             bytes = gl.bytes;
         }
         n += D;
@@ -1584,21 +1501,9 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::s
         const std::size_t gend = g + kSpan < end ? g + kSpan : end;
         if (!kHits && a.slots == 1 && g + kSpan <= end && q.n <= kWave - kDepth) {
             // a whole group of linear steps joins the batch at once
-            bool joined;
-            if constexpr (kPacked) {
-                GroupLin16 gl;
-                joined = group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl);
-                if (joined) {
-                    q.push_packed(pipe, gl, a.page_shift, base_ps, g);
-                }
-            } else {
-                GroupLin<kDepth> gl;
-                joined = group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl);
-                if (joined) {
-                    q.push_group(gl, g);
-                }
-            }
-            if (joined) {
+            GroupLin<kDepth> gl;
+            if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
+                q.push_group(gl, g);
                 if (q.n == kWave || gend >= end) {
                     fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
