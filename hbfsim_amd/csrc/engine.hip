@@ -40,7 +40,10 @@ namespace hbfamd {
 namespace {
 
 constexpr int kWave = 64;
-constexpr std::uint32_t kMaxFences = 512;
+// Top level of the two-level range lookup (find_range), staged in LDS by
+// every per-record kernel.  256 fences (2 KiB) rather than 512 let the
+// summary pass hold 8 waves per CU instead of 7 at 512 planes.
+constexpr std::uint32_t kMaxFences = 256;
 constexpr std::uint32_t kMaxPlanes = 1024;
 constexpr std::uint32_t kMaxChannels = 256;
 constexpr std::uint32_t kClsModeled = 0;
