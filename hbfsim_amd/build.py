@@ -29,14 +29,24 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP engine cannot be built")
 
 
+FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-fvisibility=hidden", "-Wall",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
 def command(output: pathlib.Path = LIB) -> list[str]:
-    return [
-        hipcc(), "-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-shared",
-        "-fvisibility=hidden", "-Wall",
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        "-I", str(ROOT / "include"),
-        "-o", str(output), *[str(s) for s in SOURCES],
-    ]
+    """The whole library in one hipcc call (kept for reference; build() runs
+    the same flags per source in parallel, then links)."""
+    return [hipcc(), *FLAGS, "-shared", "-I", str(ROOT / "include"), "-o", str(output),
+            *[str(s) for s in SOURCES]]
+
+
+def object_command(source: pathlib.Path, output: pathlib.Path) -> list[str]:
+    return [hipcc(), *FLAGS, "-I", str(ROOT / "include"), "-c", "-o", str(output), str(source)]
+
+
+def link_command(objects: list[pathlib.Path], output: pathlib.Path) -> list[str]:
+    return [hipcc(), "--offload-arch=gfx950", "-fPIC", "-shared", "-o", str(output),
+            *[str(o) for o in objects]]
 
 
 CLI = HERE / "hbf_trace_timing"
@@ -62,18 +72,30 @@ def build_cli(verbose: bool = False) -> pathlib.Path:
     return CLI
 
 
-def build(verbose: bool = False) -> pathlib.Path:
-    """Compiles every source every time it is called."""
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = command(tmp)
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True)
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
-        raise RuntimeError(f"hipcc failed with status {proc.returncode}")
+        raise RuntimeError(f"hipcc failed with status {proc.returncode}: {cmd[-1]}")
     if verbose and proc.stderr.strip():
         sys.stderr.write(proc.stderr)
+
+
+def build(verbose: bool = False) -> pathlib.Path:
+    """Compiles every source every time it is called: one object per source
+    (in parallel, at most 8 at a time), then one link."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    objects = [objdir / (src.name + ".o") for src in SOURCES]
+    jobs = max(1, min(8, os.cpu_count() or 1, len(SOURCES)))
+    with ThreadPoolExecutor(jobs) as pool:
+        list(pool.map(lambda so: _run(object_command(*so), verbose), zip(SOURCES, objects)))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run(link_command(objects, tmp), verbose)
     os.replace(tmp, LIB)
     build_cli(verbose)
     return LIB

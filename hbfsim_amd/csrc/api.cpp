@@ -206,11 +206,17 @@ void add_report(hbfsim_amd_report& t, const hbfsim_amd_report& r)
     t.service_sum_ps += r.service_sum_ps;
 }
 
+// hbfsim_stats as the reference fills it (context.cpp:1983-2004): the request
+// counters count ring requests, i.e. the requests the hybrid sampler sends to
+// the detailed model (hbf_device.cu:782-787 -> resolve_leader), so they stay 0
+// in fast mode; fast_requests counts the fast-model resolutions
+// (hbf_device.cu:951).  A sampled request is submitted and completed in the
+// same run here.
 void account(hbfsim_context* c, const hbfsim_amd_report& r)
 {
     add_report(c->total, r);
-    c->stats.requests_submitted += r.records;
-    c->stats.requests_completed += r.modeled;
+    c->stats.requests_submitted += r.hybrid_sampled;
+    c->stats.requests_completed += r.hybrid_sampled;
     c->stats.fast_requests += r.modeled - r.hybrid_sampled;
     c->stats.reference_requests += r.hybrid_sampled;
     c->stats.fast_modeled_ns += r.service_sum_ps / 1000u;

@@ -204,9 +204,15 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+def ref_available() -> bool:
+    """Whether the compiled reference shim was built here.  Checks the file
+    only, so collecting tests never loads the shim."""
+    return REF_LIB.exists()
+
+
 def ref_lib() -> ctypes.CDLL | None:
     """The compiled reference shim, when it was built in this container."""
-    if not REF_LIB.exists():
+    if not ref_available():
         return None
     return ctypes.CDLL(str(REF_LIB))
 

@@ -271,7 +271,13 @@ def test_hybrid_sampling_counts(tmp_path):
         assert grep["hybrid_sampled"] > 100
         (_, _, grep2), _ = check(p, rec, "hybrid second run")
         stats = p.engine.stats()
-        assert stats["reference_requests"] == grep["hybrid_sampled"] + grep2["hybrid_sampled"]
+        sampled = grep["hybrid_sampled"] + grep2["hybrid_sampled"]
+        modeled = grep["modeled"] + grep2["modeled"]
+        # context.cpp:1983-2004: the request counters count ring requests
+        # (the sampled ones), fast_requests the fast-model resolutions
+        assert stats["reference_requests"] == sampled
+        assert stats["requests_submitted"] == stats["requests_completed"] == sampled
+        assert stats["fast_requests"] == modeled - sampled
     finally:
         p.close()
 

@@ -99,7 +99,7 @@ def test_prefetch_simulation_matches_reference_vectors():
         assert rc == 0 and stats == c["stats"], c["config"]
 
 
-@pytest.mark.skipif(oracle_py.ref_lib() is None, reason="reference shim not built here")
+@pytest.mark.skipif(not oracle_py.ref_available(), reason="reference shim not built here")
 def test_prefetch_simulation_live_against_reference():
     import sys
     import pathlib
