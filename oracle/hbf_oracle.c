@@ -7,6 +7,8 @@
  */
 #include "hbf_oracle.h"
 
+#include <omp.h>
+
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -753,10 +755,80 @@ int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
     return 0;
 }
 
-/* Parallel oracle: classification/decode in parallel over records; the plane
- * stage in parallel over planes and the channel stage over channels, each
- * resource's records visited in input order.  Identical results to
- * orc_engine_run for ORC_MODEL_HBF (hybrid counting runs sequentially). */
+/* Stable bucket of a chunk's modeled records by resource (plane or channel):
+ * after the call, order[start[r] .. start[r + 1]) lists the records of
+ * resource r in input order.  Counting sort, one histogram per thread over
+ * a contiguous part of the chunk. */
+static void bucket_by_resource(const decoded* d, size_t m, uint32_t resources,
+                               int by_plane, int threads, size_t* hist,
+                               size_t* start, uint32_t* order)
+{
+    int nt_shared = 1;
+#pragma omp parallel num_threads(threads)
+    {
+        const int nt = omp_get_num_threads();
+        const int t = omp_get_thread_num();
+#pragma omp single
+        nt_shared = nt;
+        const size_t lo = m * (size_t)t / (size_t)nt;
+        const size_t hi = m * (size_t)(t + 1) / (size_t)nt;
+        size_t* h = hist + (size_t)t * resources;
+        memset(h, 0, resources * sizeof(size_t));
+        for (size_t i = lo; i < hi; ++i) {
+            if (d[i].cls == ORC_MODELED) {
+                h[by_plane ? d[i].plane : d[i].channel] += 1;
+            }
+        }
+#pragma omp barrier
+#pragma omp single
+        {
+            size_t acc = 0;
+            for (uint32_t r = 0; r < resources; ++r) {
+                start[r] = acc;
+                for (int u = 0; u < nt_shared; ++u) {
+                    const size_t c = hist[(size_t)u * resources + r];
+                    hist[(size_t)u * resources + r] = acc;
+                    acc += c;
+                }
+            }
+            start[resources] = acc;
+        }
+        for (size_t i = lo; i < hi; ++i) {
+            if (d[i].cls == ORC_MODELED) {
+                order[h[by_plane ? d[i].plane : d[i].channel]++] = (uint32_t)i;
+            }
+        }
+    }
+}
+
+static void merge_report(orc_engine_report* t, const orc_engine_report* r)
+{
+    t->records += r->records;
+    t->modeled += r->modeled;
+    t->bypass += r->bypass;
+    t->unsupported += r->unsupported;
+    t->reads += r->reads;
+    t->writes += r->writes;
+    t->page_hits += r->page_hits;
+    t->programs += r->programs;
+    t->hybrid_sampled += r->hybrid_sampled;
+    t->makespan_ps = max_u64(t->makespan_ps, r->makespan_ps);
+    const uint64_t lo = t->latency_sum_lo + r->latency_sum_lo;
+    t->latency_sum_hi += r->latency_sum_hi + (lo < t->latency_sum_lo);
+    t->latency_sum_lo = lo;
+    t->latency_max_ps = max_u64(t->latency_max_ps, r->latency_max_ps);
+    t->service_sum_ps += r->service_sum_ps;
+}
+
+/* Parallel oracle, identical results to orc_engine_run for ORC_MODEL_HBF.
+ * The stream is taken in chunks of 2^24 records, with engine state carried
+ * from chunk to chunk exactly as from record to record.  Per chunk:
+ * classification/decode in parallel over records; the records bucketed by
+ * plane (stable), the plane stage in parallel over planes, each plane's
+ * records in input order; the same by channel for the channel stage; then
+ * status, report and the hybrid sequence in parallel over parts of the
+ * chunk, each part's sequence numbers offset by the modeled records before
+ * it. */
 int orc_engine_run_parallel(const orc_engine_params* p,
                             const orc_range* ranges, uint32_t range_count,
                             const orc_record* records, size_t n,
@@ -771,116 +843,169 @@ int orc_engine_run_parallel(const orc_engine_params* p,
     if (!engine_params_ok(p)) {
         return 1;
     }
-    decoded* d = (decoded*)malloc(n * sizeof(decoded));
-    uint64_t* pd = (uint64_t*)malloc(n * sizeof(uint64_t));
-    uint8_t* hit = (uint8_t*)calloc(n, 1);
-    if (d == NULL || pd == NULL || hit == NULL) {
-        free(d);
-        free(pd);
-        free(hit);
+    const uint32_t planes = p->channels * p->ways * p->dies * p->planes;
+    const uint32_t resources = planes > p->channels ? planes : p->channels;
+    const uint32_t slots = p->page_buffers;
+    const size_t chunk = (size_t)1 << 24;
+    const size_t cap = n < chunk ? (n ? n : 1) : chunk;
+    decoded* d = (decoded*)malloc(cap * sizeof(decoded));
+    uint64_t* pd = (uint64_t*)malloc(cap * sizeof(uint64_t));
+    uint8_t* hit = (uint8_t*)malloc(cap);
+    uint32_t* order = (uint32_t*)malloc(cap * sizeof(uint32_t));
+    size_t* hist = (size_t*)malloc((size_t)threads * resources * sizeof(size_t));
+    size_t* start = (size_t*)malloc(((size_t)resources + 1) * sizeof(size_t));
+    size_t* part_modeled = (size_t*)calloc((size_t)threads + 1, sizeof(size_t));
+    orc_engine_report* part = (orc_engine_report*)calloc((size_t)threads, sizeof(orc_engine_report));
+    if (!d || !pd || !hit || !order || !hist || !start || !part_modeled || !part) {
+        free(d); free(pd); free(hit); free(order); free(hist); free(start);
+        free(part_modeled); free(part);
         return 2;
     }
-    const uint32_t planes = p->channels * p->ways * p->dies * p->planes;
-    const uint32_t slots = p->page_buffers;
-#pragma omp parallel num_threads(threads)
-    {
-#pragma omp for schedule(static)
-        for (size_t i = 0; i < n; ++i) {
-            decode(p, ranges, range_count, &records[i], base_ps, &d[i]);
+    for (size_t c0 = 0; c0 < n; c0 += cap) {
+        const size_t m = n - c0 < cap ? n - c0 : cap;
+        const orc_record* rec = records + c0;
+        uint64_t* comp = completion + c0;
+        uint8_t* stat = status != NULL ? status + c0 : NULL;
+#pragma omp parallel for num_threads(threads) schedule(static)
+        for (size_t i = 0; i < m; ++i) {
+            decode(p, ranges, range_count, &rec[i], base_ps, &d[i]);
+            hit[i] = 0;
         }
-        /* plane stage: thread t owns planes with id % T == t */
-#pragma omp for schedule(static, 1)
-        for (int t = 0; t < threads; ++t) {
-            for (size_t i = 0; i < n; ++i) {
-                if (d[i].cls != ORC_MODELED ||
-                    d[i].plane % (uint32_t)threads != (uint32_t)t) {
-                    continue;
-                }
-                const uint32_t pl = d[i].plane;
+        /* plane stage */
+        bucket_by_resource(d, m, planes, 1, threads, hist, start, order);
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+        for (uint32_t pl = 0; pl < planes; ++pl) {
+            /* the plane's state in locals: neighbouring planes share cache
+             * lines and belong to other threads */
+            uint64_t tags[2] = {s->plane_tag[(size_t)pl * 2],
+                                s->plane_tag[(size_t)pl * 2 + 1]};
+            uint64_t busy = s->plane_busy[pl];
+            uint64_t total = 0;
+            for (size_t k = start[pl]; k < start[pl + 1]; ++k) {
+                const size_t i = order[k];
                 int h = 0;
                 if (slots) {
-                    h = pagebuf_access(&s->plane_tag[(size_t)pl * 2], slots,
-                                       d[i].page);
+                    h = pagebuf_access(tags, slots, d[i].page);
                 }
                 hit[i] = (uint8_t)h;
                 const uint64_t svc = h ? d[i].svc_hit : d[i].svc_miss;
                 if (p->plane_contention) {
-                    s->plane_busy[pl] =
-                        max_u64(s->plane_busy[pl], d[i].issue) + svc;
-                    pd[i] = s->plane_busy[pl];
+                    busy = max_u64(busy, d[i].issue) + svc;
+                    pd[i] = busy;
                 } else {
                     pd[i] = d[i].issue + svc;
                 }
-                s->plane_busy_total[pl] += svc;
+                total += svc;
+            }
+            if (start[pl] != start[pl + 1]) {
+                s->plane_tag[(size_t)pl * 2] = tags[0];
+                s->plane_tag[(size_t)pl * 2 + 1] = tags[1];
+                s->plane_busy[pl] = busy;
+                s->plane_busy_total[pl] += total;
             }
         }
         /* channel stage */
-#pragma omp for schedule(static, 1)
-        for (int t = 0; t < threads; ++t) {
-            for (size_t i = 0; i < n; ++i) {
-                if (d[i].cls != ORC_MODELED ||
-                    d[i].channel % (uint32_t)threads != (uint32_t)t) {
-                    continue;
-                }
-                const uint32_t ch = d[i].channel;
-                s->channel_cursor[ch] =
-                    max_u64(s->channel_cursor[ch], d[i].issue) + d[i].xfer;
-                completion[i] = max_u64(pd[i], s->channel_cursor[ch]);
-                s->channel_busy_total[ch] += d[i].xfer;
+        bucket_by_resource(d, m, p->channels, 0, threads, hist, start, order);
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+        for (uint32_t ch = 0; ch < p->channels; ++ch) {
+            uint64_t cursor = s->channel_cursor[ch];
+            uint64_t total = 0;
+            for (size_t k = start[ch]; k < start[ch + 1]; ++k) {
+                const size_t i = order[k];
+                cursor = max_u64(cursor, d[i].issue) + d[i].xfer;
+                comp[i] = max_u64(pd[i], cursor);
+                total += d[i].xfer;
             }
+            s->channel_cursor[ch] = cursor;
+            s->channel_busy_total[ch] += total;
         }
-    }
-    (void)planes;
-    for (size_t i = 0; i < n; ++i) {
-        rep->records += 1;
-        uint8_t st = (uint8_t)d[i].cls;
-        if (d[i].cls == ORC_BYPASS) {
-            completion[i] = d[i].issue;
-            rep->bypass += 1;
-        } else if (d[i].cls == ORC_UNSUPPORTED) {
-            completion[i] = UINT64_MAX;
-            rep->unsupported += 1;
-        } else {
-            const uint64_t seq = s->modeled_sequence++;
-            const uint64_t key = (d[i].page << p->page_shift) ^
-                                 ((uint64_t)d[i].range_id << 32) ^ d[i].op;
-            if (p->hybrid && orc_hybrid_reference_sample(
-                                 seq, p->hybrid_warmup, p->hybrid_threshold,
-                                 key)) {
-                rep->hybrid_sampled += 1;
-                st |= 8;
+        /* status and report: modeled counts per part, then the parts */
+        int nparts = 1;
+#pragma omp parallel num_threads(threads)
+        {
+            const int nt = omp_get_num_threads();
+            const int t = omp_get_thread_num();
+#pragma omp single
+            nparts = nt;
+            const size_t lo = m * (size_t)t / (size_t)nt;
+            const size_t hi = m * (size_t)(t + 1) / (size_t)nt;
+            size_t cnt = 0;
+            for (size_t i = lo; i < hi; ++i) {
+                cnt += d[i].cls == ORC_MODELED;
             }
-            const uint64_t svc = hit[i] ? d[i].svc_hit : d[i].svc_miss;
-            rep->modeled += 1;
-            if (d[i].op == 0) {
-                rep->reads += 1;
-                if (hit[i]) {
-                    rep->page_hits += 1;
-                    st |= 4;
-                }
-            } else {
-                if (d[i].op == 1) {
-                    rep->writes += 1;
-                }
-                if (svc != 0) {
-                    rep->programs += 1;
-                    st |= 16;
+            part_modeled[t + 1] = cnt;
+#pragma omp barrier
+#pragma omp single
+            {
+                part_modeled[0] = 0;
+                for (int u = 0; u < nparts; ++u) {
+                    part_modeled[u + 1] += part_modeled[u];
                 }
             }
-            const uint64_t done = completion[i];
-            rep->makespan_ps = max_u64(rep->makespan_ps, done);
-            const uint64_t lat = done - d[i].issue;
-            add128(rep, lat);
-            rep->latency_max_ps = max_u64(rep->latency_max_ps, lat);
-            rep->service_sum_ps += max_u64(svc, d[i].xfer);
+            orc_engine_report* r = &part[t];
+            memset(r, 0, sizeof(*r));
+            uint64_t seq = s->modeled_sequence + part_modeled[t];
+            for (size_t i = lo; i < hi; ++i) {
+                r->records += 1;
+                uint8_t st = (uint8_t)d[i].cls;
+                if (d[i].cls == ORC_BYPASS) {
+                    comp[i] = d[i].issue;
+                    r->bypass += 1;
+                } else if (d[i].cls == ORC_UNSUPPORTED) {
+                    comp[i] = UINT64_MAX;
+                    r->unsupported += 1;
+                } else {
+                    const uint64_t key = (d[i].page << p->page_shift) ^
+                                         ((uint64_t)d[i].range_id << 32) ^ d[i].op;
+                    if (p->hybrid && orc_hybrid_reference_sample(
+                                         seq, p->hybrid_warmup, p->hybrid_threshold,
+                                         key)) {
+                        r->hybrid_sampled += 1;
+                        st |= 8;
+                    }
+                    ++seq;
+                    const uint64_t svc = hit[i] ? d[i].svc_hit : d[i].svc_miss;
+                    r->modeled += 1;
+                    if (d[i].op == 0) {
+                        r->reads += 1;
+                        if (hit[i]) {
+                            r->page_hits += 1;
+                            st |= 4;
+                        }
+                    } else {
+                        if (d[i].op == 1) {
+                            r->writes += 1;
+                        }
+                        if (svc != 0) {
+                            r->programs += 1;
+                            st |= 16;
+                        }
+                    }
+                    const uint64_t done = comp[i];
+                    r->makespan_ps = max_u64(r->makespan_ps, done);
+                    const uint64_t lat = done - d[i].issue;
+                    add128(r, lat);
+                    r->latency_max_ps = max_u64(r->latency_max_ps, lat);
+                    r->service_sum_ps += max_u64(svc, d[i].xfer);
+                }
+                if (stat != NULL) {
+                    stat[i] = st;
+                }
+            }
         }
-        if (status != NULL) {
-            status[i] = st;
+        for (int u = 0; u < nparts; ++u) {
+            merge_report(rep, &part[u]);
         }
+        s->modeled_sequence += part_modeled[nparts];
     }
     free(d);
     free(pd);
     free(hit);
+    free(order);
+    free(hist);
+    free(start);
+    free(part_modeled);
+    free(part);
     return 0;
 }
 
@@ -1175,6 +1300,10 @@ static int grid_jacobi(uint32_t nx, uint32_t ny, uint32_t nz, double cdt,
     int sweep = 0;
     for (; sweep < max_sweeps; ++sweep) {
         double delta = 0.0;
+        /* every cell is computed on its own, so rows run in parallel with
+         * the same results */
+#pragma omp parallel for collapse(2) reduction(max : delta) schedule(static) \
+    if ((size_t)nx * ny * nz >= 16384)
         for (uint32_t z = 0; z < nz; ++z) {
             for (uint32_t y = 0; y < ny; ++y) {
                 for (uint32_t x = 0; x < nx; ++x) {
@@ -1284,23 +1413,30 @@ static uint32_t die_of_cell(const orc_reliability* r, uint32_t x, uint32_t y,
     return q * r->dies + z / lpd;
 }
 
+/* hot[d] = the hottest cell of die d (0 if none is above 0 K).  Dies are
+ * disjoint blocks of cells (die_of_cell), visited in parallel. */
 static void die_hotspots(const orc_reliability* r, const double* t,
                          double* hot)
 {
     const uint32_t ndie = r->regions_x * r->regions_y * r->dies;
+    const uint32_t rw = r->nx / r->regions_x, rh = r->ny / r->regions_y;
+    const uint32_t lpd = r->nz / r->dies;
+#pragma omp parallel for schedule(static) if ((size_t)r->nx * r->ny * r->nz >= 16384)
     for (uint32_t d = 0; d < ndie; ++d) {
-        hot[d] = 0.0;
-    }
-    for (uint32_t z = 0; z < r->nz; ++z) {
-        for (uint32_t y = 0; y < r->ny; ++y) {
-            for (uint32_t x = 0; x < r->nx; ++x) {
-                const double v = t[((size_t)z * r->ny + y) * r->nx + x];
-                const uint32_t d = die_of_cell(r, x, y, z);
-                if (v > hot[d]) {
-                    hot[d] = v;
+        const uint32_t q = d / r->dies, dz = d % r->dies;
+        const uint32_t x0 = (q % r->regions_x) * rw, y0 = (q / r->regions_x) * rh;
+        double m = 0.0;
+        for (uint32_t z = dz * lpd; z < (dz + 1) * lpd; ++z) {
+            for (uint32_t y = y0; y < y0 + rh; ++y) {
+                for (uint32_t x = x0; x < x0 + rw; ++x) {
+                    const double v = t[((size_t)z * r->ny + y) * r->nx + x];
+                    if (v > m) {
+                        m = v;
+                    }
                 }
             }
         }
+        hot[d] = m;
     }
 }
 
@@ -1504,6 +1640,7 @@ int orc_window_counts(const orc_engine_params* p, const orc_range* ranges,
     if (!engine_params_ok(p) || window_ps == 0) {
         return 1;
     }
+#pragma omp parallel for schedule(static) if (n >= 65536)
     for (size_t i = 0; i < n; ++i) {
         decoded d;
         decode(p, ranges, range_count, &rec[i], 0, &d);
@@ -1511,9 +1648,20 @@ int orc_window_counts(const orc_engine_params* p, const orc_range* ranges,
         if (d.cls != ORC_MODELED || w >= windows) {
             continue;
         }
+#pragma omp atomic
         counts[w * (p->channels * p->ways * p->dies) + d.plane / p->planes] += 1;
     }
     return 0;
+}
+
+void orc_set_threads(int threads)
+{
+    omp_set_num_threads(threads > 0 ? threads : 1);
+}
+
+int orc_get_threads(void)
+{
+    return omp_get_max_threads();
 }
 
 int orc_coupled_run(const orc_engine_params* p, const orc_range* ranges,
@@ -1588,8 +1736,8 @@ int orc_coupled_run(const orc_engine_params* p, const orc_range* ranges,
         memset(&er, 0, sizeof(er));
         orc_engine_params q = *p;
         q.media_records = nref != 0;
-        rc = orc_engine_run(&q, ranges, range_count, merged, n + nref, 0, s, mcomp, mstat,
-                            &er);
+        rc = orc_engine_run_parallel(&q, ranges, range_count, merged, n + nref, 0, s, mcomp,
+                                     mstat, &er, omp_get_max_threads());
         rep->refreshes = nref;
         rep->makespan_ps = er.makespan_ps;
         for (size_t i = 0; rc == 0 && i < n; ++i) {

@@ -421,6 +421,12 @@ void orc_merge_records(const orc_record* demand, const uint64_t* admit,
 int orc_window_counts(const orc_engine_params* p, const orc_range* ranges,
                       uint32_t range_count, const orc_record* rec, size_t n,
                       uint64_t window_ps, uint64_t windows, uint32_t* counts);
+/* Thread count of the oracle's OpenMP parts (omp_set_num_threads): the
+ * parallel engine's callers pass their own count; the Jacobi sweeps, the
+ * hotspot reduction, the window counts and the coupled run's engine use
+ * this one.  Results do not depend on it. */
+void orc_set_threads(int threads);
+int orc_get_threads(void);
 /* The whole coupled run: counts -> chain -> admission -> refresh records ->
  * merge -> engine; completion[n] of the demand records.  hot, level and
  * refresh are sized for windows_cap windows. */

@@ -193,6 +193,8 @@ def lib() -> ctypes.CDLL:
             "orc_merge_records": (None, [_P, _P, ctypes.c_size_t, _P, ctypes.c_size_t, _P, _P]),
             "orc_window_counts": (ctypes.c_int, [_P, _P, _U32, _P, ctypes.c_size_t, _U64, _U64,
                                                  _P]),
+            "orc_set_threads": (None, [ctypes.c_int]),
+            "orc_get_threads": (ctypes.c_int, []),
             "orc_coupled_run": (ctypes.c_int, [_P, _P, _U32, _P, _P, ctypes.c_size_t, _P, _P, _P,
                                                _P, _P, _P, _P, _P, _U64]),
         }

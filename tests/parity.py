@@ -106,3 +106,54 @@ def assert_same(gpu, cpu, what=""):
         raise AssertionError(f"{what}: {bad.size} status mismatches; first at {i}: "
                              f"gpu {int(gst[i])} oracle {int(ost[i])}")
     assert grep == orep, f"{what}: report differs\n gpu {grep}\n cpu {orep}"
+
+
+ORACLE_THREADS = max(1, min(16, __import__("os").cpu_count() or 1))
+CHUNK = 1 << 26
+
+
+def merge_reports(a: dict | None, b: dict) -> dict:
+    """Report of two consecutive runs (counts add, extremes take the max)."""
+    if a is None:
+        return dict(b)
+    out = {k: a[k] + b[k] for k in a if k not in ("makespan_ps", "latency_max_ps",
+                                                  "latency_sum_lo", "latency_sum_hi",
+                                                  "latency_sum_ps")}
+    out["makespan_ps"] = max(a["makespan_ps"], b["makespan_ps"])
+    out["latency_max_ps"] = max(a["latency_max_ps"], b["latency_max_ps"])
+    total = a["latency_sum_ps"] + b["latency_sum_ps"]
+    out["latency_sum_ps"] = total
+    out["latency_sum_lo"] = total & ((1 << 64) - 1)
+    out["latency_sum_hi"] = total >> 64
+    return out
+
+
+def compare_whole(pair: "Pair", d_rec, d_comp, d_st, base_ps: int, what: str,
+                  chunk: int = CHUNK) -> dict:
+    """Every completion and status byte of a GPU run of the 32-byte records
+    d_rec (int64 [n, 4] on the GPU) against the OpenMP oracle run over the
+    same records, taken in chunks with the oracle's state carried (the same
+    as one run).  Returns the oracle's report of the whole run."""
+    n = int(d_rec.shape[0])
+    rep = None
+    for a in range(0, n, chunk):
+        b = min(n, a + chunk)
+        rec = d_rec[a:b].cpu().numpy().view(np.uint64)
+        ocomp, ost, orep, _ = oracle_py.run(pair.params, pair.ranges, pair.count, rec, base_ps,
+                                            pair.ostate, threads=ORACLE_THREADS)
+        gcomp = d_comp[a:b].cpu().numpy().view(np.uint64)
+        gst = d_st[a:b].cpu().numpy()
+        if not np.array_equal(gcomp, ocomp):
+            bad = np.nonzero(gcomp != ocomp)[0]
+            i = int(bad[0])
+            raise AssertionError(f"{what}: {bad.size} completion mismatches in records "
+                                 f"[{a}, {b}); first at {a + i}: gpu {int(gcomp[i])} "
+                                 f"oracle {int(ocomp[i])}")
+        if not np.array_equal(gst, ost):
+            bad = np.nonzero(gst != ost)[0]
+            i = int(bad[0])
+            raise AssertionError(f"{what}: {bad.size} status mismatches in records "
+                                 f"[{a}, {b}); first at {a + i}: gpu {int(gst[i])} "
+                                 f"oracle {int(ost[i])}")
+        rep = merge_reports(rep, orep)
+    return rep

@@ -1,11 +1,12 @@
-"""Configs 1 and 3 on the GPU.  Config 1 (TinyLlama-1.1B weight streaming,
-17.2M records a step) runs two whole decode steps bit-exact against the CPU
-oracle.  Config 3 (paged KV cache) runs every step of a reduced shape
-bit-exact, and one full-size step (1.17e9 records, 150 GB of KV) whose prefix
-matches the oracle and whose totals match the configuration's arithmetic.
-One full config-2 step (2.7e8 records) is checked the same way, and against
-itself run as two runs with carried state.
-The GPU record compiler is checked against its host mirror on the way."""
+"""Configs 1, 2 and 3 on the GPU, every completion against the CPU oracle.
+Config 1 (TinyLlama-1.1B weight streaming, 17.2M records a step): two whole
+decode steps.  Config 2 (the benchmarked Qwen3-30B-A3B MoE decode, 2.7e8
+records a step): the bench's first two steps, chained with the makespan
+carried as the next base as bench.py does, in both record forms.  Config 3
+(paged KV cache): every step of a reduced shape, and one whole full-size step
+(1.17e9 records over 150 GB of KV).  The oracle runs over each whole step in
+chunks with its state carried.  The GPU record compiler is checked against
+its host mirror on the way."""
 from __future__ import annotations
 
 import numpy as np
@@ -14,6 +15,7 @@ import pytest
 import oracle_py
 import parity
 from hbfsim_amd import workloads as w
+from hbfsim_amd.engine import pack_records
 
 pytestmark = pytest.mark.gpu
 
@@ -99,15 +101,20 @@ def test_kv_reduced_all_steps_bit_exact():
 
 
 def test_kv_full_size_step():
+    """One whole full-size paged-KV step: 1.17e9 records (reads of every page
+    of 64 sequences x 32 layers, one appended token per sequence and layer),
+    every completion and status equal to the oracle's, in both record forms;
+    the totals also match the configuration's arithmetic."""
     import torch
     shape = w.PAGED_KV
     spans = w.kv_spans(shape, 0)
     n = int(spans[1][-1])
     d_rec = gpu_records(spans, shape)
-    prefix = 6_000_000
+    prefix = 1 << 20
     np.testing.assert_array_equal(d_rec[:prefix].cpu().numpy().view(np.uint64),
                                   host_records(spans, shape, 0, prefix))
     pair = parity.Pair(C3, w.kv_ranges(shape))
+    packed = parity.Pair(C3, w.kv_ranges(shape))
     try:
         d_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
         d_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
@@ -121,66 +128,89 @@ def test_kv_full_size_step():
         assert rep["writes"] == writes and rep["reads"] == n - writes
         assert rep["programs"] == fills
         assert rep["bypass"] == 0 and rep["unsupported"] == 0
-        # completions never precede their issue, and the makespan is the last one
-        issue = d_rec[:, 2]
-        assert bool((d_comp >= issue).all())
-        assert int(d_comp.max()) == rep["makespan_ps"]
-        # the prefix is what the oracle computes for it
-        rec = d_rec[:prefix].cpu().numpy().view(np.uint64)
-        ocomp, ost, _, _ = oracle_py.run(pair.params, pair.ranges, pair.count, rec, 0,
-                                         oracle_py.OracleState(pair.params), threads=8)
-        np.testing.assert_array_equal(d_comp[:prefix].cpu().numpy().view(np.uint64), ocomp)
-        np.testing.assert_array_equal(d_st[:prefix].cpu().numpy(), ost)
+        # the packed form of the same step gives the same results
+        d_pk = pack_records(d_rec)
+        p_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+        p_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+        prep = packed.engine.run_packed(d_pk, p_comp, p_st)
+        torch.cuda.synchronize()
+        del d_pk
+        assert prep == rep
+        assert torch.equal(p_comp, d_comp) and torch.equal(p_st, d_st)
+        del p_comp, p_st
+        orep = parity.compare_whole(pair, d_rec, d_comp, d_st, 0, "paged KV full step")
+        assert orep == rep
+        pair.check_state()
     finally:
         pair.close()
+        packed.close()
 
 
-def test_config2_full_size_step():
-    """One whole config-2 decode step (the bench's step 0: 2.7e8 records of
-    48 x 128 Qwen3-30B-A3B experts on the 512-plane profile).  Its record
-    prefix equals the host mirror of the compiler; its first 6M completions
-    and statuses equal the oracle's (a completion depends only on earlier
-    records); every record is a modeled read, no completion precedes its
-    issue and the makespan is the last completion; and the same step run as
-    two runs with carried state gives the same completions bit for bit."""
+def test_config2_bench_steps_whole():
+    """The benchmark's first two config-2 steps (2.7e8 records each, 48 x 128
+    Qwen3-30B-A3B experts on the 512-plane profile), timed from packed
+    records with the first step's makespan carried as the second's base, as
+    bench.py chains them: every completion and status byte, both reports,
+    the per-resource busy totals and the engine state equal the oracle's.
+    The second step's issue times lie beyond 2^32 ps.  The same steps from
+    32-byte records give the same results, and step 0 cut into two runs at an
+    arbitrary record gives them too."""
     import torch
     shape = w.QWEN3_30B_A3B
-    seg = w.moe_segments(shape, w.moe_selection(shape, 1)[0])
-    d_rec = w.gpu_segment_records(seg, shape.lines_per_expert, shape.line, shape.gap_ps,
-                                  shape.issuers)
-    n = int(d_rec.shape[0])
-    assert n > 2.5e8
-    prefix = 6_000_000
-    rec = d_rec[:prefix].cpu().numpy().view(np.uint64)
-    np.testing.assert_array_equal(
-        rec, w.segment_records(seg, shape.lines_per_expert, shape.line, shape.gap_ps,
-                               shape.issuers, 0, prefix))
+    sel = w.moe_selection(shape, 2)
     c2 = w.PROFILES / "c2.json"
-    whole = parity.Pair(c2, w.moe_ranges(shape))
+    pair = parity.Pair(c2, w.moe_ranges(shape))
+    wide = parity.Pair(c2, w.moe_ranges(shape))
     split = parity.Pair(c2, w.moe_ranges(shape))
     try:
-        d_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
-        d_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
-        rep = whole.engine.run(d_rec, d_comp, d_st)
-        torch.cuda.synchronize()
-        assert rep["records"] == rep["modeled"] == rep["reads"] == n
-        assert rep["writes"] == 0 and rep["bypass"] == 0 and rep["unsupported"] == 0
-        assert n - n // 64 <= rep["page_hits"] < n
-        assert bool((d_comp >= d_rec[:, 2]).all())
-        assert int(d_comp.max()) == rep["makespan_ps"]
-        ocomp, ost, _, _ = oracle_py.run(whole.params, whole.ranges, whole.count, rec, 0,
-                                         oracle_py.OracleState(whole.params), threads=8)
-        np.testing.assert_array_equal(d_comp[:prefix].cpu().numpy().view(np.uint64), ocomp)
-        np.testing.assert_array_equal(d_st[:prefix].cpu().numpy(), ost)
-        cut = (n // 3) | 37  # inside a step and a tile
-        s_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
-        s_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
-        r1 = split.engine.run(d_rec[:cut], s_comp[:cut], s_st[:cut])
-        r2 = split.engine.run(d_rec[cut:], s_comp[cut:], s_st[cut:])
-        torch.cuda.synchronize()
-        assert torch.equal(s_comp, d_comp) and torch.equal(s_st, d_st)
-        assert r1["page_hits"] + r2["page_hits"] == rep["page_hits"]
-        assert max(r1["makespan_ps"], r2["makespan_ps"]) == rep["makespan_ps"]
+        base = 0
+        for k in range(2):
+            seg = w.moe_segments(shape, sel[k])
+            d_rec = w.gpu_segment_records(seg, shape.lines_per_expert, shape.line,
+                                          shape.gap_ps, shape.issuers)
+            n = int(d_rec.shape[0])
+            assert n > 2.5e8
+            if k == 0:
+                np.testing.assert_array_equal(
+                    d_rec[:1 << 20].cpu().numpy().view(np.uint64),
+                    w.segment_records(seg, shape.lines_per_expert, shape.line, shape.gap_ps,
+                                      shape.issuers, 0, 1 << 20))
+            d_pk = pack_records(d_rec)
+            d_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+            d_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+            rep = pair.engine.run_packed(d_pk, d_comp, d_st, base_ps=base)
+            torch.cuda.synchronize()
+            del d_pk
+            assert rep["records"] == rep["modeled"] == rep["reads"] == n
+            assert n - n // 64 <= rep["page_hits"] < n
+            w_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+            w_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+            wrep = wide.engine.run(d_rec, w_comp, w_st, base_ps=base)
+            torch.cuda.synchronize()
+            assert wrep == rep
+            assert torch.equal(w_comp, d_comp) and torch.equal(w_st, d_st)
+            del w_comp, w_st
+            if k == 0:
+                cut = (n // 3) | 37  # inside a step and a tile
+                s_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+                s_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+                r1 = split.engine.run(d_rec[:cut], s_comp[:cut], s_st[:cut])
+                r2 = split.engine.run(d_rec[cut:], s_comp[cut:], s_st[cut:])
+                torch.cuda.synchronize()
+                assert torch.equal(s_comp, d_comp) and torch.equal(s_st, d_st)
+                assert r1["page_hits"] + r2["page_hits"] == rep["page_hits"]
+                del s_comp, s_st
+            else:
+                assert base + int(d_rec[0, 2]) > 1 << 32
+            orep = parity.compare_whole(pair, d_rec, d_comp, d_st, base, f"config-2 step {k}")
+            assert orep == rep
+            base = rep["makespan_ps"]
+            del d_rec, d_comp, d_st
+        pair.check_state()
+        # the 32-byte context charged the same busy time to every resource
+        for got, want in zip(wide.engine.busy_totals(), pair.engine.busy_totals()):
+            np.testing.assert_array_equal(got, want)
     finally:
-        whole.close()
+        pair.close()
+        wide.close()
         split.close()

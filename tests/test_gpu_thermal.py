@@ -176,6 +176,30 @@ def test_coupled_run_full_grid_prefix():
     assert_coupled_equal(got, want)
 
 
+def test_coupled_run_whole_config4():
+    """The benchmarked config-4 run in full: the first 1e8 records of the
+    OLMoE trace on all 1,024 expert ranges, the 64x64x8 grid stepped through
+    all 25,000 windows with the config-4 reliability parameters from the
+    ambient grid and staggered ages.  Every window's hotspots, levels and
+    refresh flags, the final grid and ages, every demand completion, the
+    report and the engine state equal the oracle's."""
+    shape = w.OLMOE
+    seg = w.c4_segments(shape, 2)
+    d_rec = w.gpu_segment_records(seg, shape.lines_per_expert, shape.line, shape.gap_ps,
+                                  shape.issuers)[: w.C4_ACCESSES]
+    rec = d_rec.cpu().numpy().view(np.uint64)
+    del d_rec
+    opts = dict(w.C4_RELIABILITY)
+    age0 = w.staggered_ages(64, opts["retention_ps"])
+    t0 = np.full(64 * 64 * 8, w.C4_GRID["ambient_k"])
+    got, want = run_pair(rec, w.moe_ranges(shape), dict(w.C4_GRID), opts, age0, t0)
+    rep = want["rep"]
+    assert rep["windows"] == 25_000 and rep["demand_modeled"] == w.C4_ACCESSES
+    assert rep["refreshes"] > 1000 and rep["deferred"] > 0
+    assert rep["level_windows"][1] > 0 and rep["level_windows"][2] > 0
+    assert_coupled_equal(got, want)
+
+
 def test_coupled_without_events_is_the_plain_run():
     import torch
     rec, ranges = c4_case(100_000)

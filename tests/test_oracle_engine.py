@@ -214,3 +214,33 @@ def test_classification_counts_match_brute_force(oracle):
         ok = (b > 0 and op <= 1 and (r.permissions >> op) & 1 and a + b <= r.base + r.length
               and (a - r.base) // 0x1000 == (a - r.base + b - 1) // 0x1000)
         assert got == (0 if ok else 2)
+
+
+def test_parallel_run_across_chunks_with_every_class():
+    """The OpenMP oracle works in chunks of 2^24 records with state carried;
+    over 2^24 + 54,321 records of mixed classes (bypass below the range,
+    unsupported page-crossing lines, writes) in hybrid mode with two page
+    registers, it equals the sequential oracle bit for bit."""
+    import json
+    n = (1 << 24) + 54_321
+    s = workloads.config0(n=n, seed=23, write_fraction_per_mille=80)
+    rec = s.records
+    rec[::97, 0] -= np.uint64(1 << 20)          # below the range: bypass
+    rec[5::89, 0] += np.uint64(16384 - 64)      # some cross their page end: unsupported
+    prof = oracle_py.load_profile(C0)
+    prof.update(reference_sample_rate=0.01, reference_warmup_requests=1000)
+    for page_buffers in (1, 2):
+        params = oracle_py.engine_params(prof, page_buffers=page_buffers, hybrid=True)
+        ranges, count = oracle_py.range_table(s.ranges, prof["page_bytes"],
+                                              prof["capacity_bytes"])
+        st1 = oracle_py.OracleState(params)
+        c1, s1, r1, _ = oracle_py.run(params, ranges, count, rec, 7, st1)
+        st2 = oracle_py.OracleState(params)
+        c2, s2, r2, _ = oracle_py.run(params, ranges, count, rec, 7, st2, threads=8)
+        assert r1 == r2, json.dumps([r1, r2])
+        assert r1["bypass"] > 0 and r1["unsupported"] > 0 and r1["hybrid_sampled"] > 0
+        assert np.array_equal(c1, c2) and np.array_equal(s1, s2)
+        for name in ("plane_busy", "plane_tag", "channel_cursor", "plane_busy_total",
+                     "channel_busy_total"):
+            assert np.array_equal(getattr(st1, name), getattr(st2, name)), name
+        assert st1.s.modeled_sequence == st2.s.modeled_sequence
