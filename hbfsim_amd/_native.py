@@ -182,6 +182,8 @@ SIGNATURES = {
     "hbfsim_amd_run_device": (_INT, [_P, _P, _SZ, _P, _P, _U64, _P, ctypes.POINTER(Report)]),
     "hbfsim_amd_run_device_packed": (_INT, [_P, _P, _SZ, _P, _P, _U64, _P,
                                             ctypes.POINTER(Report)]),
+    "hbfsim_amd_run_device_packed_noalloc": (_INT, [_P, _P, _SZ, _P, _P, _U64, _P,
+                                                    ctypes.POINTER(Report)]),
     "hbfsim_amd_run": (_INT, [_P, _P, _SZ, _P, _P, _U64, ctypes.POINTER(Report)]),
     "hbfsim_amd_get_report": (_INT, [_P, ctypes.POINTER(Report)]),
     "hbfsim_amd_get_geometry": (_INT, [_P, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),

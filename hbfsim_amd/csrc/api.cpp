@@ -651,6 +651,34 @@ HBF_API int hbfsim_amd_run_device_packed(hbfsim_context* c, const hbf_record16* 
     return HBFSIM_OK;
 }
 
+HBF_API int hbfsim_amd_run_device_packed_noalloc(hbfsim_context* c, const hbf_record16* records,
+                                                 size_t n, uint64_t* completion_ps,
+                                                 uint8_t* status, uint64_t base_ps, void* stream,
+                                                 hbfsim_amd_report* report)
+{
+    if (report != nullptr) {
+        std::memset(report, 0, sizeof(*report));
+    }
+    if (c == nullptr || (n != 0 && (records == nullptr || completion_ps == nullptr))) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    std::lock_guard<std::mutex> lock(c->mu);
+    if (c->eng == nullptr) {
+        return HBFSIM_UNSUPPORTED;  // creating the engine allocates
+    }
+    hbfsim_amd_report r{};
+    const int st = hbfamd::engine_run_packed_noalloc(c->eng, records, n, completion_ps, status,
+                                                     base_ps, stream, &r);
+    if (st != HBFSIM_OK) {
+        return st;
+    }
+    account(c, r);
+    if (report != nullptr) {
+        *report = r;
+    }
+    return HBFSIM_OK;
+}
+
 HBF_API int hbfsim_amd_run(hbfsim_context* c, const hbf_record32* records, size_t n,
                            uint64_t* completion_ps, uint8_t* status, uint64_t base_ps,
                            hbfsim_amd_report* report)

@@ -33,6 +33,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -2781,6 +2782,47 @@ void launch_report(hipStream_t stream, const DevReport* tile_rep, std::size_t nt
 }  // namespace
 
 // ------------------------------------------------------------------------
+// Scratch of the entry point that allocates nothing
+// (hbfsim_amd_run_device_packed_noalloc): one array per device, part of the
+// code object, so the entry point never calls an allocator.  Host code uses
+// only the device address hipGetSymbolAddress returns for it (kept per device
+// in noalloc_scratch below), never the array's name.  Every call on a device
+// shares it; calls that overlap on one device race.  Nothing in it needs to
+// start at zero: each kernel of a run writes every scratch word it reads
+// before reading it, as with the engine's own reused scratch.
+
+}  // namespace hbfamd
+
+static __device__ __align__(256) unsigned char scratch[hbfamd::kNoAllocScratchBytes];
+
+namespace hbfamd {
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
+
+// Looks the array's device address up once per device; `device` must be
+// current.  Returns nullptr when the lookup fails.
+void* noalloc_scratch(int device)
+{
+    if (device < 0 || device >= kMaxDevices) {
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (g_noalloc_ptr[device] == nullptr) {
+        void* ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) == hipSuccess) {
+            g_noalloc_ptr[device] = ptr;
+        }
+    }
+    return g_noalloc_ptr[device];
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------------
 // host side
 
 struct engine {
@@ -2828,6 +2870,70 @@ struct engine {
     float last_ms[3]{0, 0, 0};
     std::uint64_t burst{0};
 };
+
+// Where one run of the main pipeline keeps its per-tile and per-group
+// summaries, carries, tile reports and step descriptors.
+struct RunScratch {
+    PlaneSum* psum;
+    MaskWord* tmask;
+    ChanSum* csum;
+    PlaneCarry* pcarry;
+    std::uint64_t* ccarry;
+    std::uint64_t* tcount;
+    std::uint64_t* tseq;
+    PlaneSum* gpsum;
+    ChanSum* gcsum;
+    PlaneCarry* gpcarry;
+    std::uint64_t* gccarry;
+    std::uint64_t* gcount;
+    std::uint64_t* gseq;
+    DevReport* tile_rep;
+    StepDesc* desc;
+};
+
+namespace {
+
+// Lays a run's scratch out in one buffer from `base`, each piece 256-byte
+// aligned: per tile the plane summaries and carries (64 B per plane), the
+// mask words (16 B per 64 planes), the channel summaries and carries (24 B
+// per channel), two counters and a tile report (128 B); per group of kGroup
+// tiles the same summaries and carries; and 16 B of step descriptor per 64
+// records.  Returns the bytes needed; with base == nullptr it only counts.
+std::size_t carve_scratch(const KArgs& a, std::size_t ntiles, std::size_t nsteps,
+                          unsigned char* base, RunScratch* s)
+{
+    std::size_t off = 0;
+    auto take = [&](auto*& ptr, std::size_t count) {
+        using T = std::remove_reference_t<decltype(*ptr)>;
+        off = (off + 255) & ~static_cast<std::size_t>(255);
+        ptr = base != nullptr ? reinterpret_cast<T*>(base + off) : nullptr;
+        off += sizeof(T) * (count == 0 ? 1 : count);
+    };
+    RunScratch t{};
+    const std::size_t rp = a.Rp, rc = a.Rc;
+    const std::size_t groups = (ntiles + kGroup - 1) / kGroup;
+    take(t.psum, ntiles * rp);
+    take(t.tmask, ntiles * mask_words(a));
+    take(t.csum, ntiles * rc);
+    take(t.pcarry, ntiles * rp);
+    take(t.ccarry, ntiles * rc);
+    take(t.tcount, ntiles);
+    take(t.tseq, ntiles);
+    take(t.gpsum, groups * rp);
+    take(t.gcsum, groups * rc);
+    take(t.gpcarry, groups * rp);
+    take(t.gccarry, groups * rc);
+    take(t.gcount, groups);
+    take(t.gseq, groups);
+    take(t.tile_rep, ntiles);
+    take(t.desc, nsteps);
+    if (s != nullptr) {
+        *s = t;
+    }
+    return off;
+}
+
+}  // namespace
 
 namespace {
 
@@ -4218,6 +4324,9 @@ int engine_create(const engine_config& c, engine** out)
         engine_destroy(e);
         return rs;
     }
+    // set-up of the no-allocation entry point on this device (once per
+    // device; a failed lookup only disables that entry point)
+    (void)noalloc_scratch(e->device);
     *out = e;
     return HBFSIM_OK;
 }
@@ -4285,7 +4394,8 @@ int engine_synchronize(engine* e)
 
 int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                    std::uint64_t* d_comp, std::uint8_t* d_status, std::uint64_t base_ps,
-                   void* stream_ptr, hbfsim_amd_report* out, bool refresh_records);
+                   void* stream_ptr, hbfsim_amd_report* out, bool refresh_records,
+                   unsigned char* ext_scratch = nullptr);
 
 int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_t* d_comp,
                std::uint8_t* d_status, std::uint64_t base_ps, void* stream_ptr,
@@ -4302,14 +4412,65 @@ int engine_run_packed(engine* e, const hbf_record16* d_rec, std::size_t n,
     return engine_run_any(e, d_rec, true, n, d_comp, d_status, base_ps, stream_ptr, out, false);
 }
 
+int engine_run_packed_noalloc(engine* e, const hbf_record16* d_rec, std::size_t n,
+                              std::uint64_t* d_comp, std::uint8_t* d_status,
+                              std::uint64_t base_ps, void* stream_ptr, hbfsim_amd_report* out)
+{
+    if (out != nullptr) {
+        std::memset(out, 0, sizeof(*out));
+    }
+    if (hipSetDevice(e->device) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    void* ptr = noalloc_scratch(e->device);
+    if (ptr == nullptr) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    if (e->ranges_dirty) {
+        return HBFSIM_UNSUPPORTED;  // uploading a changed range table allocates
+    }
+    return engine_run_any(e, d_rec, true, n, d_comp, d_status, base_ps, stream_ptr, out, false,
+                          static_cast<unsigned char*>(ptr));
+}
+
+// Tile size of a run whose scratch comes from a fixed buffer: the engine's
+// configured tile, else the automatic one doubled (up to 16,384 records)
+// until the scratch fits; 0 when it never does.
+std::uint32_t fitting_tile(const engine* e, std::size_t n, std::size_t capacity)
+{
+    KArgs a = e->args;
+    std::uint32_t tile = e->cfg.tile != 0 ? e->cfg.tile : auto_tile(n);
+    const std::size_t nsteps = (n + kWave - 1) / kWave;
+    for (;;) {
+        const std::size_t ntiles = (n + tile - 1) / tile;
+        a.tile = tile;
+        if (carve_scratch(a, ntiles, nsteps, nullptr, nullptr) <= capacity) {
+            return tile;
+        }
+        if (e->cfg.tile != 0 || tile >= 16384) {
+            return 0;
+        }
+        tile *= 2;
+    }
+}
+
 int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                    std::uint64_t* d_comp, std::uint8_t* d_status, std::uint64_t base_ps,
-                   void* stream_ptr, hbfsim_amd_report* out, bool refresh_records)
+                   void* stream_ptr, hbfsim_amd_report* out, bool refresh_records,
+                   unsigned char* ext_scratch)
 {
     if (out != nullptr) {
         std::memset(out, 0, sizeof(*out));
     }
     if (n == 0) {
+        // a run of no records still uploads a changed range table, so that
+        // it can prepare a context for the entry point that allocates nothing
+        if (ext_scratch == nullptr && e->ranges_dirty) {
+            if (hipSetDevice(e->device) != hipSuccess) {
+                return HBFSIM_CUDA_ERROR;
+            }
+            return upload_ranges(e, static_cast<hipStream_t>(stream_ptr));
+        }
         return HBFSIM_OK;
     }
     if (d_rec == nullptr || d_comp == nullptr ||
@@ -4348,13 +4509,28 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     }
     KArgs a = e->args;
     a.tile = e->cfg.tile != 0 ? e->cfg.tile : auto_tile(n);
+    if (ext_scratch != nullptr) {
+        a.tile = fitting_tile(e, n, kNoAllocScratchBytes);
+        if (a.tile == 0) {
+            return HBFSIM_UNSUPPORTED;  // beyond the static scratch
+        }
+    }
     const std::size_t ntiles = (n + a.tile - 1) / a.tile;
     if (ntiles > 0x7fffffffull) {
         return HBFSIM_UNSUPPORTED;
     }
-    int st = ensure_scratch(e, ntiles);
-    if (st != HBFSIM_OK) {
-        return st;
+    RunScratch sc{};
+    int st = HBFSIM_OK;
+    if (ext_scratch != nullptr) {
+        (void)carve_scratch(a, ntiles, (n + kWave - 1) / kWave, ext_scratch, &sc);
+    } else {
+        st = ensure_scratch(e, ntiles);
+        if (st != HBFSIM_OK) {
+            return st;
+        }
+        sc = RunScratch{e->d_psum, e->d_tmask, e->d_csum, e->d_pcarry, e->d_ccarry,
+                        e->d_tcount, e->d_tseq, e->d_gpsum, e->d_gcsum, e->d_gpcarry,
+                        e->d_gccarry, e->d_gcount, e->d_gseq, e->d_tile_rep, nullptr};
     }
     const std::size_t lds_a = lds_summary(a), lds_c = lds_apply(a);
     if (lds_a > 65536 || lds_c > 65536) {
@@ -4379,7 +4555,9 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     }
     // step descriptors, where the apply pass replays linear steps from them
     StepDesc* desc = nullptr;
-    if (!k2 && a.slots == 1 && a.hybrid == 0) {
+    if (ext_scratch != nullptr) {
+        desc = sc.desc;  // packed runs: one page register, no sampling
+    } else if (!k2 && a.slots == 1 && a.hybrid == 0) {
         const std::size_t nsteps = (n + kWave - 1) / kWave;
         if (nsteps > e->desc_cap) {
             hfree(e->d_desc);
@@ -4397,19 +4575,19 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     const std::uint8_t* hits = d_hits;
     if (k2) {
         hipLaunchKernelGGL((k_summary<false, true>), grid, dim3(kWave), lds_a, stream, a, d_rec,
-                           n, base_ps, e->d_psum, e->d_tmask, e->d_csum, e->d_tcount,
+                           n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     } else if (refresh_records) {
         hipLaunchKernelGGL((k_summary<true, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
-                           n, base_ps, e->d_psum, e->d_tmask, e->d_csum, e->d_tcount,
+                           n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     } else if (packed) {
         hipLaunchKernelGGL((k_summary<false, false, true>), grid, dim3(kWave), lds_a, stream, a,
-                           d_rec, n, base_ps, e->d_psum, e->d_tmask, e->d_csum, e->d_tcount,
+                           d_rec, n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     } else {
         hipLaunchKernelGGL((k_summary<false, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
-                           n, base_ps, e->d_psum, e->d_tmask, e->d_csum, e->d_tcount,
+                           n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     }
     (void)hipEventRecord(e->ev[1], stream);
@@ -4418,49 +4596,49 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         const std::size_t rt = static_cast<std::size_t>(a.Rp) + a.Rc + 1;
         const unsigned wide = static_cast<unsigned>((ngroups * rt + 255) / 256);
         hipLaunchKernelGGL(k_carry_up, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
-                           e->d_psum, e->d_tmask, e->d_csum, e->d_tcount, e->d_gpsum,
-                           e->d_gcsum, e->d_gcount);
+                           sc.psum, sc.tmask, sc.csum, sc.tcount, sc.gpsum,
+                           sc.gcsum, sc.gcount);
         hipLaunchKernelGGL(k_carry_mid, dim3(a.Rp + a.Rc + 1), dim3(kMidBlock), 0, stream, a,
                            ngroups,
-                           e->d_gpsum, e->d_gcsum, e->d_gcount, e->d_gpcarry, e->d_gccarry,
-                           e->d_gseq, e->d_pbusy, e->d_ptag, e->d_cbusy, e->d_seq, e->d_ptot,
+                           sc.gpsum, sc.gcsum, sc.gcount, sc.gpcarry, sc.gccarry,
+                           sc.gseq, e->d_pbusy, e->d_ptag, e->d_cbusy, e->d_seq, e->d_ptot,
                            e->d_ctot);
         hipLaunchKernelGGL(k_carry_down, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
-                           e->d_psum, e->d_tmask, e->d_csum, e->d_tcount, e->d_gpcarry,
-                           e->d_gccarry, e->d_gseq, e->d_pcarry, e->d_ccarry, e->d_tseq);
+                           sc.psum, sc.tmask, sc.csum, sc.tcount, sc.gpcarry,
+                           sc.gccarry, sc.gseq, sc.pcarry, sc.ccarry, sc.tseq);
     }
     (void)hipEventRecord(e->ev[2], stream);
     const bool staged = desc != nullptr && staged_steps(a) != 0;
     if (k2) {
         hipLaunchKernelGGL((k_apply<false, true>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
-                           base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
-                           d_status, e->d_tile_rep, hits, desc);
+                           base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq, d_comp,
+                           d_status, sc.tile_rep, hits, desc);
     } else if (refresh_records && staged) {
         hipLaunchKernelGGL((k_apply<true, false, true>), grid, dim3(kWave), lds_c, stream, a,
-                           d_rec, n, base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq,
-                           d_comp, d_status, e->d_tile_rep, hits, desc);
+                           d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq,
+                           d_comp, d_status, sc.tile_rep, hits, desc);
     } else if (refresh_records) {
         hipLaunchKernelGGL((k_apply<true, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
-                           base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
-                           d_status, e->d_tile_rep, hits, desc);
+                           base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq, d_comp,
+                           d_status, sc.tile_rep, hits, desc);
     } else if (packed && staged) {
         hipLaunchKernelGGL((k_apply<false, false, true, true>), grid, dim3(kWave), lds_c, stream,
-                           a, d_rec, n, base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry,
-                           e->d_tseq, d_comp, d_status, e->d_tile_rep, hits, desc);
+                           a, d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry,
+                           sc.tseq, d_comp, d_status, sc.tile_rep, hits, desc);
     } else if (packed) {
         hipLaunchKernelGGL((k_apply<false, false, false, true>), grid, dim3(kWave), lds_c, stream,
-                           a, d_rec, n, base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry,
-                           e->d_tseq, d_comp, d_status, e->d_tile_rep, hits, desc);
+                           a, d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry,
+                           sc.tseq, d_comp, d_status, sc.tile_rep, hits, desc);
     } else if (staged) {
         hipLaunchKernelGGL((k_apply<false, false, true>), grid, dim3(kWave), lds_c, stream, a,
-                           d_rec, n, base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq,
-                           d_comp, d_status, e->d_tile_rep, hits, desc);
+                           d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq,
+                           d_comp, d_status, sc.tile_rep, hits, desc);
     } else {
         hipLaunchKernelGGL((k_apply<false, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
-                           base_ps, e->d_pcarry, e->d_tmask, e->d_ccarry, e->d_tseq, d_comp,
-                           d_status, e->d_tile_rep, hits, desc);
+                           base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq, d_comp,
+                           d_status, sc.tile_rep, hits, desc);
     }
-    launch_report(stream, e->d_tile_rep, ntiles, e->d_rep, e->d_rep_parts);
+    launch_report(stream, sc.tile_rep, ntiles, e->d_rep, e->d_rep_parts);
     (void)hipEventRecord(e->ev[3], stream);
     err = hipGetLastError();
     if (err == hipSuccess)

@@ -70,6 +70,14 @@ int engine_run(engine* e, const hbf_record32* d_records, std::size_t n,
 int engine_run_packed(engine* e, const hbf_record16* d_records, std::size_t n,
                       std::uint64_t* d_completion, std::uint8_t* d_status,
                       std::uint64_t base_ps, void* stream, hbfsim_amd_report* out);
+// engine_run_packed without allocating: the run's scratch comes from a
+// static per-device array of kNoAllocScratchBytes.  HBFSIM_UNSUPPORTED when
+// the run's scratch does not fit it (at the largest tile, 16,384 records), or
+// when the range table changed since the last run (uploading it allocates).
+constexpr std::size_t kNoAllocScratchBytes = std::size_t{64} << 20;
+int engine_run_packed_noalloc(engine* e, const hbf_record16* d_records, std::size_t n,
+                              std::uint64_t* d_completion, std::uint8_t* d_status,
+                              std::uint64_t base_ps, void* stream, hbfsim_amd_report* out);
 int engine_get_busy_totals(engine* e, std::uint64_t* plane_ps, std::size_t planes,
                            std::uint64_t* channel_ps, std::size_t channels);
 int engine_get_state(engine* e, std::uint64_t* plane_busy, std::uint64_t* plane_tags,

@@ -165,6 +165,28 @@ class Engine:
             ctypes.c_void_p(stream), ctypes.byref(rep)), "run (packed)")
         return rep.as_dict()
 
+    def run_packed_noalloc(self, records: Any, completion: Any, status: Any = None,
+                           base_ps: int = 0, stream: Any = None) -> dict:
+        """run_packed through hbfsim_amd_run_device_packed_noalloc, which
+        allocates nothing: its scratch is the library's static per-device
+        array.  ValueError when the run does not fit that array, when the
+        engine has not run yet or when ranges changed since its last run."""
+        n = int(records.shape[0])
+        if stream is None:
+            import torch
+            stream = torch.cuda.current_stream().cuda_stream
+        elif hasattr(stream, "cuda_stream"):
+            stream = stream.cuda_stream
+        rep = nat.Report()
+        rc = self._lib.hbfsim_amd_run_device_packed_noalloc(
+            self._ctx, _ptr(records), n, _ptr(completion), _ptr(status), base_ps,
+            ctypes.c_void_p(stream), ctypes.byref(rep))
+        if rc == nat.HBFSIM_UNSUPPORTED:
+            raise ValueError(f"{n} records do not fit the static scratch (64 MiB per device), or "
+                             "the engine has not run yet, or ranges changed since its last run")
+        nat.check(rc, "run (packed, no allocation)")
+        return rep.as_dict()
+
     def run_host(self, records: np.ndarray, base_ps: int = 0,
                  want_status: bool = True) -> tuple[np.ndarray, np.ndarray | None, dict]:
         """Copies host records in, runs on the GPU, copies completions out."""

@@ -295,6 +295,27 @@ int hbfsim_amd_run_device_packed(hbfsim_context* context,
                                  uint64_t* completion_ps, uint8_t* status,
                                  uint64_t base_ps, void* stream,
                                  hbfsim_amd_report* report);
+/* hbfsim_amd_run_device_packed for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same arguments and
+ * results; it calls no allocator: the run's scratch (per tile of T records:
+ * 64 B per plane, 24 B per channel, 16 B per 64 planes and 144 B; per group
+ * of 16 tiles the same summaries; 16 B per 64 records) comes from a static
+ * array of 64 MiB per device, held until the process ends.  T is the
+ * context's tile_records or, by default, the automatic tile doubled (up to
+ * 16,384) until the run fits: up to about 125 million records per call with
+ * 64 planes and 8 channels, 27 million with 512 planes and 16 channels and
+ * 13 million with 1,024 planes and 256 channels.  Returns
+ * HBFSIM_UNSUPPORTED, touching nothing,
+ * when the run does not fit, when the context's engine does not exist yet
+ * (make one ordinary run first) or when ranges were registered or removed
+ * since the last run (the range upload allocates).  Every call on a device
+ * shares that device's array: calls that overlap on one device race. */
+int hbfsim_amd_run_device_packed_noalloc(hbfsim_context* context,
+                                         const hbf_record16* records, size_t n,
+                                         uint64_t* completion_ps, uint8_t* status,
+                                         uint64_t base_ps, void* stream,
+                                         hbfsim_amd_report* report);
 /* Same with host buffers: copies in, runs on the default stream, copies
  * out. */
 int hbfsim_amd_run(hbfsim_context* context, const hbf_record32* records,
