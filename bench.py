@@ -1,6 +1,7 @@
 """Benchmark of the HBF access-timing engine on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c0|c4|thermal]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--config c2|c0|c4|thermal|general|hybrid]
 
 A step is one pass of the timing engine over one batch of access records
 resident in HBM (one decode step of the workload); engine state carries from
@@ -53,6 +54,9 @@ def parse() -> argparse.Namespace:
                          "32-byte ones (hbf_record32); packing runs before the timed region")
     ap.add_argument("--no-compare", action="store_true",
                     help="with packed records, skip timing the same steps from 32-byte ones")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="config c2: skip the stream-copy peak, the general-path, hybrid and "
+                         "config-4 sub-lines")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first fill and copy 2 GiB (known HBM bytes) so that counter runs "
                          "can calibrate FETCH_SIZE / WRITE_SIZE")
@@ -71,6 +75,48 @@ def copy_probe() -> None:
     torch.cuda.synchronize()
     del src, dst
     torch.cuda.empty_cache()
+
+
+def stream_copy_peak(gib: int = 4, reps: int = 5) -> dict:
+    """Measured HBM copy bandwidth on this GPU: a device-to-device copy of
+    `gib` GiB, timed with HIP events, counting the bytes read and written."""
+    import torch
+    n = (gib << 30) // 8
+    src = torch.ones(n, dtype=torch.int64, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    gbps = 2 * (gib << 30) / (ms / 1e3) / 1e9
+    return {"gbps": gbps, "bytes_per_copy": 2 * (gib << 30), "ms": ms,
+            "how": f"torch device copy of {gib} GiB (read + write), {reps} reps, HIP events"}
+
+
+def gpu_random_stream(n: int, seed: int):
+    """A config-0-shaped stream of n records generated on the GPU: uniform
+    random 128-B reads in the 1 GiB range at workloads.RANGE_BASE, issue gaps
+    exponential with a mean of 2 ns (whole ps), seeded."""
+    import torch
+    from hbfsim_amd import workloads
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    rec = torch.empty((n, 4), dtype=torch.int64, device="cuda")
+    rec[:, 0] = torch.randint(0, (1 << 30) // 128, (n,), generator=g, device="cuda") * 128 + \
+        workloads.RANGE_BASE
+    rec[:, 1] = 128
+    gaps = torch.empty(n, dtype=torch.float64, device="cuda").exponential_(1 / 2000.0, generator=g)
+    rec[:, 2] = torch.cumsum(gaps.round_().to(torch.int64), 0)
+    rec[:, 3] = 0
+    del gaps
+    torch.cuda.synchronize()
+    return rec
 
 
 def log(msg: str) -> None:
@@ -268,6 +314,7 @@ def cpu_baseline_c4(rec, ranges, budget_s: float) -> dict:
     orng, count = oracle_py.range_table(ranges, prof["page_bytes"], prof["capacity_bytes"])
     rel = oracle_py.reliability(w.C4_GRID, w.C4_RELIABILITY, params.dies)
     sample = rec[: 1_000_000].cpu().numpy().view(np.uint64)
+    oracle_py.lib().orc_set_threads(1)  # single-threaded, as `cores` states
     done, t0 = 0, time.perf_counter()
     while True:
         temp = np.full(64 * 64 * 8, w.C4_GRID["ambient_k"])
@@ -345,6 +392,88 @@ def bench_thermal(args) -> dict:
     return out
 
 
+def sub_line(engine, profile, ranges, batches, records, args, what: str, mode="fast") -> dict:
+    """One more workload timed like the main line (same step count), with
+    its own roofline for the dominant per-record kernel."""
+    value, dt, kms, streamed = time_steps(engine, profile, ranges, batches, records, args, mode)
+    names = ["k_summary", "k_carry", "k_apply"]
+    kb = kernel_bytes(records)
+    dominant = 0 if kms[0] >= kms[2] else 2
+    per_launch = streamed / args.steps
+    achieved = kb[names[dominant]] * per_launch / (kms[dominant] / 1e3) / 1e9
+    algo = RECORD_BYTES[records] + 8
+    return {"workload": what, "value": value, "unit": "accesses/s",
+            "ms_per_step": dt / args.steps * 1e3,
+            "records": "packed 16-byte records" if records == "packed" else "32-byte records",
+            "roofline": {"bound": "hbm", "kernel": names[dominant],
+                         "algorithmic": f"{kb[names[dominant]]} B per access x "
+                                        f"{int(per_launch)} accesses per launch",
+                         "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                         "frac": achieved / PEAK_HBM_GBPS,
+                         "kernel_ms": {nm: float(v) for nm, v in zip(names, kms)},
+                         "algorithmic_bytes_per_access": algo,
+                         "pipeline_frac": value * algo / 1e9 / PEAK_HBM_GBPS}}
+
+
+def bench_general(engine, args) -> dict:
+    """The general per-record path at scale: 2^28 config-0-shaped random
+    records (no linear steps: every record decodes, groups and folds on its
+    own), packed, on the config-0 profile."""
+    from hbfsim_amd import workloads
+    n = 1 << 28
+    batches = [engine.pack_records(gpu_random_stream(n, 11 + k)) for k in range(2)]
+    profile = workloads.PROFILES / "c0.json"
+    ranges = [(workloads.RANGE_BASE, 1 << 30, 3)]
+    return sub_line(engine, profile, ranges, batches, "packed", args,
+                    "config0-shaped random stream: 2^28 uniform 128-B reads in 1 GiB, exponential "
+                    "gaps mean 2 ns, 8 ch x 4 die x 2 plane, 2 distinct batches")
+
+
+def bench_hybrid(engine, batches, args) -> dict:
+    """Config 2 in hybrid mode (context mode 2): every modeled record passes
+    the reference sampler (rate 1%, 1,000 warm-up requests), which the apply
+    pass evaluates per record; 32-byte records (the packed form takes no
+    sampling)."""
+    import tempfile
+    from hbfsim_amd import workloads
+    prof = json.loads((workloads.PROFILES / "c2.json").read_text())
+    prof.update(reference_sample_rate=0.01, reference_warmup_requests=1000)
+    path = pathlib.Path(tempfile.mkdtemp(prefix="hbf-bench-")) / "c2-hybrid.json"
+    path.write_text(json.dumps(prof))
+    shape = workloads.QWEN3_30B_A3B
+    return sub_line(engine, path, workloads.moe_ranges(shape), batches, "32", args,
+                    "config2 with hybrid sampling (rate 0.01, warm-up 1,000), 32-byte records",
+                    mode="hybrid")
+
+
+def scalar_floor(budget_s: float) -> dict:
+    """The reference's own per-access fast model (the single-tail recurrence
+    of hbf_device.cu:895-910, oracle orc_fast_model_scalar) on config 0's
+    2^20 records, single-threaded: the like-for-like CPU floor."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_py
+    from hbfsim_amd import workloads
+    s = workloads.config0()
+    arrival = np.ascontiguousarray(s.records[:, 2] // 1000, np.uint64)
+    op = np.zeros(len(arrival), np.uint32)
+    nbytes = np.full(len(arrival), 16384, np.uint32)
+    target = np.zeros(len(arrival), np.uint64)
+    prof = oracle_py.load_profile(workloads.PROFILES / "c0.json")
+    L = oracle_py.lib()
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        tail = np.zeros(1, np.uint64)
+        L.orc_fast_model_scalar(arrival.ctypes.data, op.ctypes.data, nbytes.ctypes.data,
+                                len(arrival), prof["read_latency_ns"], prof["program_latency_ns"],
+                                prof["aggregate_bandwidth_bytes_per_s"], tail.ctypes.data,
+                                target.ctypes.data)
+        done += len(arrival)
+    dt = time.perf_counter() - t0
+    return {"value": done / dt, "unit": "accesses/s", "cores": 1, "kind": "port",
+            "sample": f"config 0 (2^20 records, whole-page 16 KiB transfers) through the "
+                      f"single-tail fast model, repeated {done // len(arrival)}x ({dt:.1f} s)"}
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -358,6 +487,26 @@ def main() -> None:
         copy_probe()
     if args.config in ("c4", "thermal"):
         out = bench_c4(args) if args.config == "c4" else bench_thermal(args)
+        print(json.dumps(out), flush=True)
+        return
+    if args.config in ("general", "hybrid"):
+        if args.config == "general":
+            line = bench_general(engine, args)
+        else:
+            from hbfsim_amd import workloads
+            shape = workloads.QWEN3_30B_A3B
+            sel = workloads.moe_selection(shape, 2)
+            batches = [workloads.gpu_segment_records(workloads.moe_segments(shape, sel[k]),
+                                                     shape.lines_per_expert, shape.line,
+                                                     shape.gap_ps, shape.issuers)
+                       for k in range(2)]
+            line = bench_hybrid(engine, batches, args)
+        out = {"metric": "modeled HBF accesses/sec on 1 MI355X", "value": line["value"],
+               "unit": "accesses/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+               "ms_per_step": line["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+               "vs_baseline": None, "dtype": "u64", "data": "synthetic",
+               "config": {"workload": line["workload"], "records": line["records"]},
+               "roofline": line["roofline"]}
         print(json.dumps(out), flush=True)
         return
 
@@ -420,18 +569,39 @@ def main() -> None:
     }
     if other is not None:
         out["records32"] = other
+    if args.config == "c2" and not args.no_extra:
+        log("stream copy peak")
+        peak = stream_copy_peak()
+        out["stream_copy"] = peak
+        out["roofline"]["measured_peak"] = peak["gbps"]
+        out["roofline"]["frac_of_measured_peak"] = achieved / peak["gbps"]
+        log("general path: random stream")
+        out["general"] = bench_general(engine, args)
+        log("hybrid mode")
+        out["hybrid"] = bench_hybrid(engine, batches, args)
     if not args.no_cpu:
         log("cpu baseline")
         out["cpu_baseline"] = cpu_baseline(profile, ranges, host_records, args.cpu_seconds)
+        out["cpu_baseline"]["scalar_fast_model"] = scalar_floor(min(3.0, args.cpu_seconds))
+    if args.config == "c2" and not args.no_extra:
+        del batches, timed
+        import torch
+        torch.cuda.empty_cache()
+        log("config 4")
+        c4 = bench_c4(argparse.Namespace(steps=2, warmup=1, no_cpu=args.no_cpu,
+                                         cpu_seconds=args.cpu_seconds / 2))
+        out["config4"] = {k: c4[k] for k in ("value", "unit", "ms_per_step", "steps", "warmup",
+                                              "dtype", "config", "roofline", "cpu_baseline")
+                          if k in c4}
     print(json.dumps(out), flush=True)
 
 
-def time_steps(engine, profile, ranges, batches, records, args):
+def time_steps(engine, profile, ranges, batches, records, args, mode="fast"):
     """Warm-up steps, then exactly `args.steps` timed steps of one engine
     (bracketed by device synchronisation); returns (modeled accesses/s,
     seconds, average per-kernel ms, records streamed)."""
     import torch
-    e = engine.Engine(str(profile))
+    e = engine.Engine(str(profile), mode=mode)
     for base, length, perms in ranges:
         e.register(base, length, perms)
     run = e.run_packed if records == "packed" else e.run
