@@ -437,6 +437,56 @@ int orc_coupled_run(const orc_engine_params* p, const orc_range* ranges,
                     orc_coupled_report* rep, double* hot, uint8_t* level,
                     uint8_t* refresh, uint64_t windows_cap);
 
+/* ---- UCIe Streaming / AoU link (ucie_link.c; src/ucie/link.cpp) ------ */
+typedef struct orc_link_profile {
+    uint32_t gt_per_second;        /* 8, 16 or 32 (x64 lanes, Format 6) */
+    uint32_t initial_ar_granules;  /* request-direction sender credits */
+    uint32_t initial_r_granules;   /* return-direction sender credits */
+    uint32_t max_accepted;         /* in-flight messages per direction */
+    uint64_t propagation_ns;
+} orc_link_profile;
+typedef struct orc_link_counters {
+    uint64_t flits, wire_bytes, ucie_header_bytes, crc_position_bytes;
+    uint64_t aou_header_bytes, aou_message_bytes, unused_message_bytes;
+    uint64_t credit_only_flits;
+} orc_link_counters;
+typedef struct orc_link_fragment {
+    uint64_t request_id;
+    uint32_t flit_granule, message_granule, granules;
+    uint8_t msg_start, msg_end, pad[2];
+} orc_link_fragment;
+typedef struct orc_link_flit {
+    uint32_t direction;            /* 0 request (AR), 1 return (R) */
+    uint32_t nfrag;
+    uint64_t start_ns, delivered_ns;
+    uint32_t message_granules, grant_granules, credit_only, pad;
+    orc_link_fragment frag[48];
+} orc_link_flit;
+typedef struct orc_link_delivery {
+    uint32_t direction;
+    uint32_t pad;
+    uint64_t request_id;
+    uint64_t delivered_ns;
+} orc_link_delivery;
+typedef struct orc_link orc_link;
+int orc_link_profile_valid(const orc_link_profile* p);
+uint64_t orc_link_serialization_ns(const orc_link_profile* p);
+uint32_t orc_link_legal_grant(uint32_t pending);
+orc_link* orc_link_create(const orc_link_profile* p);
+void orc_link_destroy(orc_link* l);
+int orc_link_enqueue(orc_link* l, uint32_t dir, uint64_t id, uint64_t ready_ns);
+int orc_link_consume(orc_link* l, uint32_t dir, uint64_t id, uint64_t at);
+int orc_link_next_event(const orc_link* l, uint64_t* t);
+int orc_link_step(orc_link* l, orc_link_delivery* out, size_t cap, size_t* count);
+uint64_t orc_link_now(const orc_link* l);
+uint32_t orc_link_credits(const orc_link* l, uint32_t dir);
+const orc_link_counters* orc_link_counters_of(const orc_link* l, uint32_t dir);
+size_t orc_link_flit_count(const orc_link* l);
+const orc_link_flit* orc_link_flit_at(const orc_link* l, size_t i);
+int orc_link_scenario(const orc_link_profile* p, const uint32_t* dir, const uint64_t* ready,
+                      size_t n, const uint64_t delay[2], uint64_t* delivered,
+                      orc_link_counters* counters);
+
 #ifdef __cplusplus
 }
 #endif

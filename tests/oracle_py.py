@@ -424,3 +424,163 @@ def coupled_run(params: OrcParams, ranges, count: int, rel: OrcReliability,
     trace = {"windows": windows, "dies": dies, "hot": hot.reshape(windows + 1, dies),
              "level": level[:windows], "refresh": refresh[: windows * dies].reshape(windows, dies)}
     return comp[:n], rep.as_dict(), trace, state
+
+
+# ---------------------------------------------------------------------------
+# UCIe Streaming / AoU link (oracle/ucie_link.c)
+
+
+class OrcLinkProfile(ctypes.Structure):
+    _fields_ = [("gt_per_second", _U32), ("initial_ar_granules", _U32),
+                ("initial_r_granules", _U32), ("max_accepted", _U32), ("propagation_ns", _U64)]
+
+
+LINK_COUNTER_FIELDS = ("flits", "wire_bytes", "ucie_header_bytes", "crc_position_bytes",
+                       "aou_header_bytes", "aou_message_bytes", "unused_message_bytes",
+                       "credit_only_flits")
+
+
+class OrcLinkCounters(ctypes.Structure):
+    _fields_ = [(f, _U64) for f in LINK_COUNTER_FIELDS]
+
+    def as_dict(self) -> dict:
+        return {f: int(getattr(self, f)) for f in LINK_COUNTER_FIELDS}
+
+
+class OrcLinkFragment(ctypes.Structure):
+    _fields_ = [("request_id", _U64), ("flit_granule", _U32), ("message_granule", _U32),
+                ("granules", _U32), ("msg_start", ctypes.c_uint8), ("msg_end", ctypes.c_uint8),
+                ("pad", ctypes.c_uint8 * 2)]
+
+
+class OrcLinkFlit(ctypes.Structure):
+    _fields_ = [("direction", _U32), ("nfrag", _U32), ("start_ns", _U64),
+                ("delivered_ns", _U64), ("message_granules", _U32), ("grant_granules", _U32),
+                ("credit_only", _U32), ("pad", _U32), ("frag", OrcLinkFragment * 48)]
+
+
+class OrcLinkDelivery(ctypes.Structure):
+    _fields_ = [("direction", _U32), ("pad", _U32), ("request_id", _U64),
+                ("delivered_ns", _U64)]
+
+
+REQUEST, RETURN = 0, 1
+
+
+def _link_lib() -> ctypes.CDLL:
+    L = lib()
+    if not getattr(L, "_link_bound", False):
+        sig = {
+            "orc_link_profile_valid": (ctypes.c_int, [_P]),
+            "orc_link_serialization_ns": (_U64, [_P]),
+            "orc_link_legal_grant": (_U32, [_U32]),
+            "orc_link_create": (_P, [_P]),
+            "orc_link_destroy": (None, [_P]),
+            "orc_link_enqueue": (ctypes.c_int, [_P, _U32, _U64, _U64]),
+            "orc_link_consume": (ctypes.c_int, [_P, _U32, _U64, _U64]),
+            "orc_link_next_event": (ctypes.c_int, [_P, _P]),
+            "orc_link_step": (ctypes.c_int, [_P, _P, ctypes.c_size_t, _P]),
+            "orc_link_now": (_U64, [_P]),
+            "orc_link_credits": (_U32, [_P, _U32]),
+            "orc_link_counters_of": (ctypes.POINTER(OrcLinkCounters), [_P, _U32]),
+            "orc_link_flit_count": (ctypes.c_size_t, [_P]),
+            "orc_link_flit_at": (ctypes.POINTER(OrcLinkFlit), [_P, ctypes.c_size_t]),
+            "orc_link_scenario": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t, _P, _P, _P]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        L._link_bound = True
+    return L
+
+
+def link_profile(gt=16, ar=128, r=128, max_accepted=128, propagation_ns=0) -> OrcLinkProfile:
+    return OrcLinkProfile(gt, ar, r, max_accepted, propagation_ns)
+
+
+class LinkError(Exception):
+    def __init__(self, code: int, what: str):
+        super().__init__(f"{what}: code {code}")
+        self.code = code
+
+
+class Link:
+    """The oracle's StreamingLink (object API of src/ucie/link.cpp)."""
+
+    def __init__(self, profile: OrcLinkProfile):
+        self._L = _link_lib()
+        self.profile = profile
+        self.h = self._L.orc_link_create(ctypes.byref(profile))
+        if not self.h:
+            raise ValueError("invalid link profile")
+
+    def close(self):
+        if self.h:
+            self._L.orc_link_destroy(self.h)
+            self.h = None
+
+    def enqueue(self, direction, request_id, ready_ns):
+        rc = self._L.orc_link_enqueue(self.h, direction, request_id, ready_ns)
+        if rc:
+            raise LinkError(rc, "enqueue")
+
+    def consume(self, direction, request_id, at):
+        rc = self._L.orc_link_consume(self.h, direction, request_id, at)
+        if rc:
+            raise LinkError(rc, "consume")
+
+    def next_event_ns(self):
+        t = ctypes.c_uint64()
+        return int(t.value) if self._L.orc_link_next_event(self.h, ctypes.byref(t)) else None
+
+    def step(self):
+        out = (OrcLinkDelivery * 64)()
+        k = ctypes.c_size_t()
+        rc = self._L.orc_link_step(self.h, out, 64, ctypes.byref(k))
+        if rc:
+            raise LinkError(rc, "step")
+        return [(int(out[i].direction), int(out[i].request_id), int(out[i].delivered_ns))
+                for i in range(k.value)]
+
+    def now(self):
+        return int(self._L.orc_link_now(self.h))
+
+    def credits(self, direction):
+        return int(self._L.orc_link_credits(self.h, direction))
+
+    def counters(self, direction) -> dict:
+        return self._L.orc_link_counters_of(self.h, direction).contents.as_dict()
+
+    def flits(self) -> list:
+        out = []
+        for i in range(self._L.orc_link_flit_count(self.h)):
+            f = self._L.orc_link_flit_at(self.h, i).contents
+            out.append({"direction": f.direction, "start_ns": f.start_ns,
+                        "delivered_ns": f.delivered_ns, "message_granules": f.message_granules,
+                        "grant_granules": f.grant_granules, "credit_only": bool(f.credit_only),
+                        "fragments": [dict(request_id=f.frag[k].request_id,
+                                           flit_granule=f.frag[k].flit_granule,
+                                           message_granule=f.frag[k].message_granule,
+                                           granules=f.frag[k].granules,
+                                           msg_start=bool(f.frag[k].msg_start),
+                                           msg_end=bool(f.frag[k].msg_end))
+                                      for k in range(f.nfrag)]})
+        return out
+
+
+def link_scenario(profile: OrcLinkProfile, direction, ready, delay=(0, 0)):
+    """orc_link_scenario: one link's messages (direction, ready_ns) through
+    the caller that admits in order and consumes each delivery delay[dir]
+    later.  Returns (delivered_ns[n], [request counters, return counters])."""
+    direction = np.ascontiguousarray(direction, np.uint32)
+    ready = np.ascontiguousarray(ready, np.uint64)
+    n = len(ready)
+    delivered = np.zeros(max(n, 1), np.uint64)
+    counters = (OrcLinkCounters * 2)()
+    d = (_U64 * 2)(*delay)
+    rc = _link_lib().orc_link_scenario(ctypes.byref(profile), addr(direction), addr(ready), n, d,
+                                       addr(delivered), counters)
+    if rc:
+        raise LinkError(rc, "scenario")
+    return delivered[:n], [counters[0].as_dict(), counters[1].as_dict()]
