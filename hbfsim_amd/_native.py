@@ -152,6 +152,18 @@ class CoupledReport(ctypes.Structure):
         return d
 
 
+class LinkProfile(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("gt_per_second", ctypes.c_uint32),
+                ("initial_ar_granules", ctypes.c_uint32), ("initial_r_granules", ctypes.c_uint32),
+                ("max_accepted", ctypes.c_uint32), ("reserved0", ctypes.c_uint32),
+                ("propagation_ns", ctypes.c_uint64), ("consume_delay_ns", ctypes.c_uint64 * 2)]
+
+
+LINK_COUNTER_FIELDS = ("flits", "wire_bytes", "ucie_header_bytes", "crc_position_bytes",
+                       "aou_header_bytes", "aou_message_bytes", "unused_message_bytes",
+                       "credit_only_flits")
+
+
 _P = ctypes.c_void_p
 _U32 = ctypes.c_uint32
 _U64 = ctypes.c_uint64
@@ -213,6 +225,8 @@ SIGNATURES = {
     "hbfsim_amd_coupled_last_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float), _INT]),
     "hbfsim_amd_coupled_trace": (_INT, [_P, _P, _SZ, _P, _SZ, _P, _SZ, ctypes.POINTER(_U64),
                                         ctypes.POINTER(_U32)]),
+    "hbfsim_amd_link_run": (_INT, [ctypes.POINTER(LinkProfile), _P, _U32, _P, _P, _SZ, _P, _P,
+                                   _P]),
     "hbfsim_amd_validate_profile": (_INT, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
 }
 

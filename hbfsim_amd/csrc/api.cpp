@@ -9,6 +9,7 @@
 // and registering ranges need no GPU; the engine and its device memory are
 // created on first use.
 #include "engine.hpp"
+#include "link.hpp"
 #include "thermal.hpp"
 #include "profile.hpp"
 
@@ -1040,6 +1041,22 @@ HBF_API int hbfsim_amd_calibrate(const hbfsim_amd_access_class* d_access,
                                  void* stream)
 {
     return hbfamd::calibrate(d_access, d_latency_ns, n, d_rows, max_rows, rows, stream);
+}
+
+HBF_API int hbfsim_amd_link_run(const hbfsim_amd_link_profile* profile, const uint64_t* d_first,
+                                uint32_t links, const uint64_t* d_ready_ns,
+                                const uint8_t* d_direction, size_t n, uint64_t* d_delivered_ns,
+                                hbfsim_amd_link_counters* d_counters, void* stream)
+{
+    if (profile == nullptr || profile->struct_size != sizeof(hbfsim_amd_link_profile)) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    try {
+        return hbfamd::link_run(*profile, d_first, links, d_ready_ns, d_direction, n,
+                                d_delivered_ns, d_counters, stream);
+    } catch (...) {
+        return HBFSIM_IO_ERROR;
+    }
 }
 
 HBF_API int hbfsim_amd_validate_profile(const char* path, char* error, size_t error_bytes)

@@ -584,6 +584,64 @@ int hbfsim_amd_coupled_trace(const hbfsim_amd_thermal* thermal, double* hot,
                              uint8_t* refresh, size_t refresh_count,
                              uint64_t* windows, uint32_t* dies);
 
+/* ===== 5. UCIe Streaming / AoU link ====================================
+ *
+ * The reference's StreamingLink (src/ucie/link.cpp:1-203; profile rules of
+ * src/ucie/profile.cpp:40-67) for batches of independent links, one link
+ * per GPU thread.  A link carries AR requests (3 AoU granules, direction 0)
+ * and R returns (14 granules, direction 1); each direction sends a Format 6
+ * flit of 48 granules every 32 / GT ns while it has data or a credit grant
+ * to send; a message's granules are all reserved against the sender's
+ * credits at its MsgStart; credits come back as grants of 1, 4, 8, ... 128
+ * granules riding flits of the other direction after the receiver consumes
+ * the message.
+ *
+ * The link's caller (the reference leaves it to its user,
+ * link.hpp:62-65) is fixed here: it admits each direction's messages in
+ * order while fewer than max_accepted of that direction are in flight (the
+ * reference's enqueue refuses more, link.cpp:45-46), at the later of the
+ * message's ready time and the time it finds room, and consumes every
+ * delivered message consume_delay_ns[direction] after its delivery. */
+typedef struct hbfsim_amd_link_profile {
+    uint32_t struct_size;          /* sizeof(hbfsim_amd_link_profile) */
+    uint32_t gt_per_second;        /* 8, 16 or 32 (x64 lanes) */
+    uint32_t initial_ar_granules;  /* 3..65535 */
+    uint32_t initial_r_granules;   /* 14..65535 */
+    uint32_t max_accepted;         /* 1..65535 in flight per direction */
+    uint32_t reserved0;
+    uint64_t propagation_ns;       /* at most 1e9 and (4094 flits in flight) */
+    uint64_t consume_delay_ns[2];  /* [0] AR, [1] R */
+} hbfsim_amd_link_profile;
+
+/* DirectionCounters (link.hpp:36-46) */
+typedef struct hbfsim_amd_link_counters {
+    uint64_t flits;
+    uint64_t wire_bytes;
+    uint64_t ucie_header_bytes;
+    uint64_t crc_position_bytes;
+    uint64_t aou_header_bytes;
+    uint64_t aou_message_bytes;
+    uint64_t unused_message_bytes;
+    uint64_t credit_only_flits;
+} hbfsim_amd_link_counters;
+
+/* Runs `links` links to quiescence.  Link l's messages are
+ * [d_first[l], d_first[l + 1]) of d_ready_ns / d_direction (d_first has
+ * links + 1 entries, from 0 to n); within a link each direction's ready
+ * times must not decrease.  d_delivered_ns[i] receives message i's delivery
+ * time; d_counters[2 * l + direction] the link's counters.  Device arrays;
+ * synchronises `stream`.  HBFSIM_INVALID_ARGUMENT for a profile outside the
+ * reference's rules, a direction above 1, ready times out of order or an
+ * event time beyond 2^64 - 1 ns (the reference's overflow_error), a link of
+ * 2^32 messages or more or malformed offsets; HBFSIM_UNSUPPORTED when more
+ * than 4094 flits could be in flight.  The library keeps the scratch of its
+ * largest call per device (12 B per message plus 12 B per flit slot and
+ * link) until the process ends; calls on one device run one at a time. */
+int hbfsim_amd_link_run(const hbfsim_amd_link_profile* profile, const uint64_t* d_first,
+                        uint32_t links, const uint64_t* d_ready_ns,
+                        const uint8_t* d_direction, size_t n, uint64_t* d_delivered_ns,
+                        hbfsim_amd_link_counters* d_counters, void* stream);
+
 /* Profile validation with the reference's rules and messages
  * (src/profile/profile.cpp:238-468).  Returns HBFSIM_OK or
  * HBFSIM_INVALID_ARGUMENT with the reference's message in `error`. */

@@ -1,0 +1,131 @@
+"""The UCIe Streaming / AoU link kernel (hbfsim_amd_link_run) against the CPU
+oracle's restatement of StreamingLink, link by link: every delivery time and
+every direction counter bit-exact, on the reference test's own scenarios
+(tests/cpu/ucie_link_test.cpp:50-104) and on seeded random batches of links
+across profiles, credits, capacities, propagation and consume delays."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle_py as o
+from hbfsim_amd import link as lk
+from hbfsim_amd import _native as nat
+
+pytestmark = pytest.mark.gpu
+
+FIELDS = nat.LINK_COUNTER_FIELDS
+
+
+def gpu_run(profile, links):
+    """links: list of (direction[], ready[]) per link."""
+    import torch
+    first = np.zeros(len(links) + 1, np.uint64)
+    first[1:] = np.cumsum([len(r) for _, r in links])
+    dirs = np.concatenate([np.asarray(d, np.uint8) for d, _ in links]) if links else \
+        np.zeros(0, np.uint8)
+    ready = np.concatenate([np.asarray(r, np.uint64) for _, r in links]) if links else \
+        np.zeros(0, np.uint64)
+    t_first = torch.from_numpy(first.view(np.int64)).cuda()
+    t_ready = torch.from_numpy(ready.view(np.int64).copy()).cuda()
+    t_dir = torch.from_numpy(dirs.copy()).cuda()
+    delivered, counters = lk.run(profile, t_first, t_ready, t_dir)
+    return delivered.cpu().numpy().view(np.uint64), counters, first
+
+
+def oracle_profile(p):
+    return o.link_profile(gt=p.gt_per_second, ar=p.initial_ar_granules, r=p.initial_r_granules,
+                          max_accepted=p.max_accepted, propagation_ns=p.propagation_ns)
+
+
+def check_against_oracle(profile, links):
+    delivered, counters, first = gpu_run(profile, links)
+    delay = (int(profile.consume_delay_ns[0]), int(profile.consume_delay_ns[1]))
+    for k, (d, r) in enumerate(links):
+        want, wc = o.link_scenario(oracle_profile(profile), d, r, delay)
+        got = delivered[first[k]:first[k + 1]]
+        np.testing.assert_array_equal(got, want, err_msg=f"link {k}")
+        for dirn in (0, 1):
+            assert dict(zip(FIELDS, counters[k, dirn].tolist())) == wc[dirn], (k, dirn)
+    return delivered, counters
+
+
+def test_reference_scenarios():
+    p = lk.link_profile(gt_per_second=16, initial_ar_granules=128, initial_r_granules=128,
+                        max_accepted=128)
+    links = [([0] * 16, [0] * 16), ([0] * 17, [0] * 17), ([1] * 4, [0] * 4)]
+    _, c = check_against_oracle(p, links)
+    # ucie_link_test.cpp:50-87
+    assert c[0, 0, 0] == 1 and c[0, 0, 5] == 240 and c[0, 0, 6] == 0
+    assert c[1, 0, 0] == 2 and c[1, 0, 5] == 255 and c[1, 0, 6] == 225
+    assert c[2, 1, 0] == 2 and c[2, 1, 5] == 280 and c[2, 1, 6] == 200
+    # ucie_link_test.cpp:88-104: three unit grants on the return direction
+    p3 = lk.link_profile(gt_per_second=16, initial_ar_granules=3, initial_r_granules=14,
+                         max_accepted=128)
+    _, c3 = check_against_oracle(p3, [([0], [0])])
+    assert c3[0, 1, 7] == 3 and c3[0, 1, 1] == 768 and c3[0, 1, 6] == 720
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_batches(seed):
+    """Even seeds stay within the LDS form's bounds (at most 16 messages
+    admitted per direction, at most 8 flits in flight: propagation up to 5
+    flit times); odd seeds need the HBM form (more admitted messages or a
+    longer propagation delay)."""
+    rng = np.random.default_rng(100 + seed)
+    gt = int(rng.choice([8, 16, 32]))
+    ser = 32 // gt
+    if seed % 2 == 0:
+        accepted, prop = int(rng.integers(1, 17)), int(rng.integers(0, 5 * ser + 1))
+    else:
+        accepted, prop = int(rng.integers(1, 41)), int(rng.integers(0, 60))
+        if accepted <= 16 and prop <= 5 * ser:
+            accepted = 17 + int(rng.integers(0, 24))
+    p = lk.link_profile(gt_per_second=gt, initial_ar_granules=int(rng.integers(3, 80)),
+                        initial_r_granules=int(rng.integers(14, 200)), max_accepted=accepted,
+                        propagation_ns=prop,
+                        consume_delay_ns=(int(rng.integers(0, 30)), int(rng.integers(0, 90))))
+    links = []
+    for _ in range(int(rng.integers(20, 130))):
+        m = int(rng.integers(0, 300))
+        d = rng.integers(0, 2, m).astype(np.uint8)
+        r = np.sort(rng.integers(0, int(rng.integers(1, 40)) * max(m, 1), m)).astype(np.uint64)
+        links.append((d, r))
+    check_against_oracle(p, links)
+
+
+@pytest.mark.parametrize("accepted,prop", [(4, 5), (16, 23), (17, 5), (4, 24)])
+def test_bursts_and_idle_gaps(accepted, prop):
+    """Bursts separated by idle periods longer than the pipeline, equal ready
+    times across directions, one direction only, empty links; at the edges of
+    the LDS form (16 admitted, 8 flits in flight at 8 GT/s) and just past them."""
+    p = lk.link_profile(gt_per_second=8, initial_ar_granules=12, initial_r_granules=56,
+                        max_accepted=accepted, propagation_ns=prop, consume_delay_ns=(3, 0))
+    links = [
+        ([0, 1, 0, 1, 1, 0], [0, 0, 0, 0, 1000, 1000]),
+        ([1] * 30, [0] * 10 + [500] * 10 + [501] * 10),
+        ([], []),
+        ([0] * 100, list(range(0, 1000, 10))),
+        ([0, 1] * 50, [7] * 100),
+    ]
+    check_against_oracle(p, links)
+
+
+def test_refusals():
+    import torch
+    p = lk.link_profile()
+    with pytest.raises(ValueError):  # ready times out of order within a direction
+        gpu_run(p, [([0, 0], [10, 5])])
+    with pytest.raises(ValueError):  # direction above 1
+        gpu_run(p, [([2], [0])])
+    bad = lk.link_profile(gt_per_second=64)
+    with pytest.raises(ValueError):
+        gpu_run(bad, [([0], [0])])
+    with pytest.raises(ValueError):  # an event time past 2^64 - 1 ns
+        gpu_run(p, [([0], [2**64 - 1])])
+    # malformed offsets (decreasing) are refused before anything is read
+    first = torch.tensor([0, 3, 1], dtype=torch.int64, device="cuda")
+    ready = torch.zeros(3, dtype=torch.int64, device="cuda")
+    dirs = torch.zeros(3, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):
+        lk.run(p, first, ready, dirs)
