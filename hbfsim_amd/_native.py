@@ -83,7 +83,7 @@ class EngineOptions(ctypes.Structure):
                 ("flat_geometry", ctypes.c_uint32), ("ways", ctypes.c_uint32),
                 ("xfer_quantum_ps", ctypes.c_uint64),
                 ("channel_bandwidth_bytes_per_s", ctypes.c_uint64),
-                ("tile_records", ctypes.c_uint32), ("reserved0", ctypes.c_uint32)]
+                ("tile_records", ctypes.c_uint32), ("warp_grouping", ctypes.c_uint32)]
 
 
 class Range(ctypes.Structure):
@@ -95,7 +95,7 @@ class Range(ctypes.Structure):
 
 REPORT_FIELDS = ("records", "modeled", "bypass", "unsupported", "reads", "writes", "page_hits",
                  "programs", "hybrid_sampled", "makespan_ps", "latency_sum_lo",
-                 "latency_sum_hi", "latency_max_ps", "service_sum_ps")
+                 "latency_sum_hi", "latency_max_ps", "service_sum_ps", "grouped")
 
 
 class Report(ctypes.Structure):

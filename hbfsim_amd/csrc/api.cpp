@@ -155,6 +155,7 @@ int build_config(const hbfsim_context* c, hbfamd::engine_config* cfg)
     k.xfer_den = static_cast<std::uint64_t>(den);
     k.xfer_quantum = q;
     k.tile = o.tile_records;  // 0: chosen per run from the batch size
+    k.grouping = o.warp_grouping;
     // page registers hold page + 1 in 32 bits on the device
     if ((p.capacity_bytes >> k.page_shift) >= 0xffffffffull) {
         return HBFSIM_UNSUPPORTED;
@@ -205,20 +206,22 @@ void add_report(hbfsim_amd_report& t, const hbfsim_amd_report& r)
     t.latency_sum_lo = lo;
     t.latency_max_ps = std::max(t.latency_max_ps, r.latency_max_ps);
     t.service_sum_ps += r.service_sum_ps;
+    t.grouped += r.grouped;
 }
 
 // hbfsim_stats as the reference fills it (context.cpp:1983-2004): the request
 // counters count ring requests, i.e. the requests the hybrid sampler sends to
 // the detailed model (hbf_device.cu:782-787 -> resolve_leader), so they stay 0
 // in fast mode; fast_requests counts the fast-model resolutions
-// (hbf_device.cu:951).  A sampled request is submitted and completed in the
-// same run here.
+// (hbf_device.cu:951), one per media request: lanes that joined a warp
+// group's request are not resolutions of their own.  A sampled request is
+// submitted and completed in the same run here.
 void account(hbfsim_context* c, const hbfsim_amd_report& r)
 {
     add_report(c->total, r);
     c->stats.requests_submitted += r.hybrid_sampled;
     c->stats.requests_completed += r.hybrid_sampled;
-    c->stats.fast_requests += r.modeled - r.hybrid_sampled;
+    c->stats.fast_requests += r.modeled - r.grouped - r.hybrid_sampled;
     c->stats.reference_requests += r.hybrid_sampled;
     c->stats.fast_modeled_ns += r.service_sum_ps / 1000u;
 }
@@ -242,7 +245,8 @@ void write_report(const hbfsim_context* c)
         << ",\"latency_sum_lo\":" << t.latency_sum_lo
         << ",\"latency_sum_hi\":" << t.latency_sum_hi
         << ",\"latency_max_ps\":" << t.latency_max_ps
-        << ",\"service_sum_ps\":" << t.service_sum_ps << "}\n";
+        << ",\"service_sum_ps\":" << t.service_sum_ps << ",\"grouped\":" << t.grouped
+        << "}\n";
 }
 
 }  // namespace
@@ -565,7 +569,7 @@ HBF_API int hbfsim_amd_set_engine_options(hbfsim_context* c,
         return HBFSIM_INVALID_ARGUMENT;
     }
     if (o->model > HBFSIM_AMD_MODEL_EMPIRICAL || o->page_buffers > 2 ||
-        (o->tile_records % 64) != 0) {
+        (o->tile_records % 64) != 0 || o->warp_grouping > 1) {
         return HBFSIM_INVALID_ARGUMENT;
     }
     if (o->model == HBFSIM_AMD_MODEL_EMPIRICAL && !c->prof.empirical.present) {

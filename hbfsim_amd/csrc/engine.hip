@@ -51,6 +51,8 @@ constexpr std::uint32_t kClsModeled = 0;
 constexpr std::uint32_t kClsBypass = 1;
 constexpr std::uint32_t kClsUnsupported = 2;
 constexpr std::uint32_t kClsInvalid = 3;  // lane beyond the tile
+constexpr std::uint32_t kClsFollower = 5;  // shares an earlier record's request
+constexpr std::uint8_t kStGrouped = 32;
 
 struct alignas(16) PlaneSum {
     std::uint64_t fpage1;  // page + 1 of the tile's first record (0: none)
@@ -70,7 +72,7 @@ struct alignas(16) PlaneCarry {
 struct DevReport {
     unsigned long long v[14];
 };
-static_assert(sizeof(DevReport) == sizeof(hbfsim_amd_report), "report layout");
+static_assert(offsetof(hbfsim_amd_report, grouped) == sizeof(DevReport), "report layout");
 enum {
     R_RECORDS, R_MODELED, R_BYPASS, R_UNSUPPORTED, R_READS, R_WRITES, R_HITS,
     R_PROGRAMS, R_HYBRID, R_MAKESPAN, R_LAT_LO, R_LAT_HI, R_LAT_MAX, R_SERVICE
@@ -108,6 +110,9 @@ struct KArgs {
     std::uint64_t media_pages;      // device capacity in pages
     std::uint32_t tile;
     std::uint32_t ext_hits;         // page-buffer hits given per record (K = 2)
+    // warp grouping: per record, how many records back its group's request
+    // was made (0: its own request); null when the run does not group
+    const std::uint8_t* lead;
 };
 
 // Record operations: 0 read, 1 write, and 2 refresh of media page `addr`
@@ -1503,7 +1508,8 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::s
             pipe.issue(rec, g + kSpan, end, lane);
         }
         const std::size_t gend = g + kSpan < end ? g + kSpan : end;
-        if (!kHits && a.slots == 1 && g + kSpan <= end && q.n <= kWave - kDepth) {
+        if (!kHits && a.slots == 1 && a.lead == nullptr && g + kSpan <= end &&
+            q.n <= kWave - kDepth) {
             // a whole group of linear steps joins the batch at once
             GroupLin<kDepth> gl;
             if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
@@ -1522,7 +1528,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::s
             pipe.take(st);
             const std::size_t i = s + lane;
             const bool valid = i < end;
-            if (!kHits && a.slots == 1) {
+            if (!kHits && a.slots == 1 && a.lead == nullptr) {
                 // linear steps wait in a batch; the batch is folded when full, at
                 // the tile's last step, and before any other step (order matters)
                 std::uint32_t lp, lb;
@@ -1548,7 +1554,10 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::s
             }
             uint4 x, y;
             step_records(st, lane, x, y);
-            const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
+            Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
+            if (!kPacked && a.lead != nullptr && valid && a.lead[i] != 0) {
+                d.cls = kClsFollower;
+            }
             const bool m = valid && d.cls == kClsModeled;
             const bool hbit = kHits && valid && hits[i] != 0;
             const std::uint64_t active = __ballot(m);
@@ -2484,7 +2493,7 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const void* rec, std::siz
                 pipe.take(sr);
                 const std::size_t i = s + lane;
                 const bool valid = i < end;
-                if (!kHits && a.slots == 1 && !a.hybrid) {
+                if (!kHits && a.slots == 1 && !a.hybrid && a.lead == nullptr) {
                     // batched as in the summary pass
                     std::uint32_t lp, lb;
                     std::uint64_t li;
@@ -2502,7 +2511,10 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const void* rec, std::siz
                 }
                 uint4 x, y;
                 step_records(sr, lane, x, y);
-                const Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
+                Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
+                if (!kPacked && a.lead != nullptr && valid && a.lead[i] != 0) {
+                    d.cls = kClsFollower;  // timed by k_follow from its group's request
+                }
                 const bool m = valid && d.cls == kClsModeled;
                 const bool hbit = kHits && valid && hits[i] != 0;
                 const std::uint64_t active = __ballot(m);
@@ -2762,6 +2774,156 @@ __global__ __launch_bounds__(256) void k_report(const std::uint64_t* in, std::si
 }
 
 // Folds `ntiles` tile reports into `rep` (parts: kRepParts * kRepWords words).
+// ---- warp grouping (hbf_device.cu:1223-1231) ----------------------------
+//
+// The lanes of one warp instruction are consecutive records with one nonzero
+// group id (flags bits 32-63); among them, modeled records with the same
+// (range, media page) share the media request of the first.  k_lead marks
+// every other such record with how far back that first record is; the
+// summary and apply passes then time only the requests, and k_follow gives
+// each marked record its request's completion.
+
+constexpr std::size_t kLeadSpan = 1024;  // records per wave of k_lead
+constexpr unsigned kFollowBlocks = 8192;
+
+// One wave per kLeadSpan records; the 64 records before them are decoded
+// too, as history.  Two windows of 64 records live in LDS: record i in slot
+// ((i >> 6) & 1) * 64 + (i & 63).  A group of more than 64 records or with
+// two issue times sets *err (the run is refused before anything is timed).
+__global__ __launch_bounds__(64) void k_lead(KArgs a, const hbf_record32* rec, std::size_t n,
+                                             std::uint8_t* lead, std::uint32_t* err)
+{
+    extern __shared__ std::uint64_t sm[];
+    std::uint64_t* fence = sm;
+    __shared__ std::uint64_t s_issue[2 * kWave];
+    __shared__ std::uint64_t s_page1[2 * kWave];  // media page + 1; 0: not modeled
+    __shared__ std::uint32_t s_group[2 * kWave];
+    __shared__ std::uint32_t s_range[2 * kWave];
+    const int lane = threadIdx.x;
+    const std::size_t begin = static_cast<std::size_t>(blockIdx.x) * kLeadSpan;
+    const std::size_t end = begin + kLeadSpan < n ? begin + kLeadSpan : n;
+    load_fences(a, fence, lane);
+    __syncthreads();
+    RangeCache rc = empty_cache();
+    std::uint32_t bad = 0;
+    for (std::size_t s = begin >= kWave ? begin - kWave : begin; s < end; s += kWave) {
+        const std::size_t i = s + lane;
+        const int slot = static_cast<int>(((i >> 6) & 1u) * kWave + (i & 63u));
+        std::uint32_t g = 0, rid = 0;
+        std::uint64_t issue = 0, page1 = 0;
+        if (i < end) {
+            uint4 x, y;
+            load_record(rec, i, x, y);
+            g = y.w;
+            issue = y.x | (static_cast<std::uint64_t>(y.y) << 32);
+            if (g != 0) {
+                const Dec d = decode<false>(a, fence, rc, x, y, 0);
+                if (d.cls == kClsModeled) {
+                    page1 = d.page1;
+                    rid = d.range_id;
+                }
+            }
+        }
+        s_group[slot] = g;
+        s_issue[slot] = issue;
+        s_page1[slot] = page1;
+        s_range[slot] = rid;
+        __syncthreads();
+        if (s >= begin && i < end) {
+            std::uint32_t back = 0;
+            if (g != 0) {
+                // the group's earlier records: at most 63, all in the two windows
+                for (std::size_t t = 1; t <= kWave && t <= i; ++t) {
+                    const std::size_t j = i - t;
+                    const int sj = static_cast<int>(((j >> 6) & 1u) * kWave + (j & 63u));
+                    if (s_group[sj] != g) {
+                        break;
+                    }
+                    if (t == kWave || s_issue[sj] != issue) {
+                        bad = 1;
+                        break;
+                    }
+                    if (page1 != 0 && s_page1[sj] == page1 && s_range[sj] == rid) {
+                        back = static_cast<std::uint32_t>(t);
+                    }
+                }
+            }
+            lead[i] = static_cast<std::uint8_t>(back);
+        }
+        __syncthreads();
+    }
+    if (__ballot(bad != 0) != 0 && lane == 0) {
+        atomicMax(err, 1u);
+    }
+}
+
+// Each marked record takes its request's completion (final once k_apply
+// has run: a request is never itself marked) and status kStGrouped, and is
+// counted into frep: records that joined, reads, writes, makespan, latency
+// sum (low, high words), latency maximum.
+__global__ __launch_bounds__(256) void k_follow(const hbf_record32* rec, std::size_t n,
+                                                std::uint64_t base_ps, const std::uint8_t* lead,
+                                                std::uint64_t* comp, std::uint8_t* status,
+                                                unsigned long long* frep)
+{
+    std::uint64_t cnt = 0, rd = 0, wr = 0, mk = 0, lo = 0, hi = 0, mx = 0;
+    const std::size_t stride = static_cast<std::size_t>(gridDim.x) * blockDim.x;
+    for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride) {
+        const std::uint32_t back = lead[i];
+        if (back == 0) {
+            continue;
+        }
+        const std::uint64_t done = comp[i - back];
+        comp[i] = done;
+        if (status != nullptr) {
+            status[i] = kStGrouped;
+        }
+        const uint4 y = reinterpret_cast<const uint4*>(rec + i)[1];
+        const std::uint64_t issue = base_ps + (y.x | (static_cast<std::uint64_t>(y.y) << 32));
+        const std::uint32_t op = y.z & 0xffu;
+        ++cnt;
+        rd += op == 0 ? 1u : 0u;
+        wr += op == 1 ? 1u : 0u;
+        mk = umax64(mk, done);
+        const std::uint64_t lat = done - issue;
+        const std::uint64_t l2 = lo + lat;
+        hi += l2 < lo ? 1u : 0u;
+        lo = l2;
+        mx = umax64(mx, lat);
+    }
+    const std::uint64_t total = wave_sum(cnt);
+    if (total == 0) {
+        return;  // wave-uniform
+    }
+    // 128-bit latency sum across the wave: high words, then low words with
+    // their carries
+    hi = wave_sum(hi);
+    std::uint64_t carry = 0;
+    for (int o = 32; o > 0; o >>= 1) {
+        const std::uint64_t other = shfl64(lo, threadIdx.x ^ o);
+        const std::uint64_t oc = shfl64(carry, threadIdx.x ^ o);
+        const std::uint64_t sum = lo + other;
+        carry = carry + oc + (sum < lo ? 1u : 0u);
+        lo = sum;
+    }
+    hi += carry;
+    rd = wave_sum(rd);
+    wr = wave_sum(wr);
+    mk = wave_max(mk);
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63u) == 0) {
+        atomicAdd(&frep[0], static_cast<unsigned long long>(total));
+        atomicAdd(&frep[1], static_cast<unsigned long long>(rd));
+        atomicAdd(&frep[2], static_cast<unsigned long long>(wr));
+        atomicMax(&frep[3], static_cast<unsigned long long>(mk));
+        const unsigned long long old = atomicAdd(&frep[4], static_cast<unsigned long long>(lo));
+        hi += old + lo < old ? 1u : 0u;
+        atomicAdd(&frep[5], static_cast<unsigned long long>(hi));
+        atomicMax(&frep[6], static_cast<unsigned long long>(mx));
+    }
+}
+
 void launch_report(hipStream_t stream, const DevReport* tile_rep, std::size_t ntiles,
                    DevReport* rep, std::uint64_t* parts)
 {
@@ -4042,7 +4204,7 @@ int run_empirical(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint
         }
     }
     if (out != nullptr) {
-        std::memcpy(out, e->h_rep, sizeof(*out));
+        std::memcpy(out, e->h_rep, sizeof(DevReport));
     }
     return HBFSIM_OK;
 }
@@ -4490,6 +4652,14 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     if (e->cfg.model == HBFSIM_AMD_MODEL_HBF && e->cfg.slots == 2 && refresh_records) {
         return HBFSIM_UNSUPPORTED;
     }
+    // warp grouping reads group ids from 32-byte records (packed records
+    // carry none); it runs on the main pipeline with at most one page
+    // register and no merged refresh records
+    const bool grouping = e->cfg.grouping != 0 && !packed;
+    if (grouping && (e->cfg.model != HBFSIM_AMD_MODEL_HBF || e->cfg.slots == 2 ||
+                     refresh_records || ext_scratch != nullptr)) {
+        return HBFSIM_UNSUPPORTED;
+    }
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     if (hipSetDevice(e->device) != hipSuccess) {
         return HBFSIM_CUDA_ERROR;
@@ -4537,6 +4707,43 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         return HBFSIM_UNSUPPORTED;
     }
     hipError_t err = hipSuccess;
+    // warp grouping: mark the records that join their group's request
+    // (refusing malformed groups before any state changes)
+    std::uint8_t* d_lead = nullptr;
+    std::uint32_t* d_gerr = nullptr;
+    unsigned long long* d_frep = nullptr;
+    auto free_group = [&]() {
+        hfree(d_lead);
+        hfree(d_gerr);
+        hfree(d_frep);
+    };
+    if (grouping) {
+        err = halloc(d_lead, n);
+        if (err == hipSuccess) err = halloc(d_gerr, 1);
+        if (err == hipSuccess) err = halloc(d_frep, 8);
+        if (err == hipSuccess) err = hipMemsetAsync(d_gerr, 0, 4, stream);
+        if (err == hipSuccess) err = hipMemsetAsync(d_frep, 0, 64, stream);
+        if (err == hipSuccess) {
+            const std::size_t nl = (n + kLeadSpan - 1) / kLeadSpan;
+            hipLaunchKernelGGL(k_lead, dim3(static_cast<unsigned>(nl)), dim3(kWave),
+                               static_cast<std::size_t>(a.r_nfence) * 8, stream, a,
+                               static_cast<const hbf_record32*>(d_rec), n, d_lead, d_gerr);
+            err = hipGetLastError();
+        }
+        std::uint32_t h_gerr = 0;
+        if (err == hipSuccess)
+            err = hipMemcpyAsync(&h_gerr, d_gerr, 4, hipMemcpyDeviceToHost, stream);
+        if (err == hipSuccess) err = hipStreamSynchronize(stream);
+        if (err != hipSuccess) {
+            free_group();
+            return HBFSIM_CUDA_ERROR;
+        }
+        if (h_gerr != 0) {
+            free_group();
+            return HBFSIM_INVALID_ARGUMENT;
+        }
+        a.lead = d_lead;
+    }
     // two page registers: hits first, from their own scans
     const bool k2 = e->cfg.slots == 2;
     std::uint8_t* d_hits = nullptr;
@@ -4557,13 +4764,14 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     StepDesc* desc = nullptr;
     if (ext_scratch != nullptr) {
         desc = sc.desc;  // packed runs: one page register, no sampling
-    } else if (!k2 && a.slots == 1 && a.hybrid == 0) {
+    } else if (!k2 && a.slots == 1 && a.hybrid == 0 && !grouping) {
         const std::size_t nsteps = (n + kWave - 1) / kWave;
         if (nsteps > e->desc_cap) {
             hfree(e->d_desc);
             e->desc_cap = 0;
             const std::size_t cap = nsteps + nsteps / 8;  // headroom, as for the tiles
             if (halloc(e->d_desc, cap) != hipSuccess) {
+                free_group();
                 return HBFSIM_CUDA_ERROR;
             }
             e->desc_cap = cap;
@@ -4639,15 +4847,26 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                            d_status, sc.tile_rep, hits, desc);
     }
     launch_report(stream, sc.tile_rep, ntiles, e->d_rep, e->d_rep_parts);
+    unsigned long long h_frep[8] = {};
+    if (grouping) {
+        const std::size_t nb = (n + 255) / 256;
+        hipLaunchKernelGGL(k_follow,
+                           dim3(static_cast<unsigned>(nb < kFollowBlocks ? nb : kFollowBlocks)),
+                           dim3(256), 0, stream, static_cast<const hbf_record32*>(d_rec), n,
+                           base_ps, d_lead, d_comp, d_status, d_frep);
+    }
     (void)hipEventRecord(e->ev[3], stream);
     err = hipGetLastError();
     if (err == hipSuccess)
         err = hipMemcpyAsync(e->h_rep, e->d_rep, sizeof(DevReport), hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess && grouping)
+        err = hipMemcpyAsync(h_frep, d_frep, sizeof(h_frep), hipMemcpyDeviceToHost, stream);
     if (err == hipSuccess && k2)
         err = hipMemcpyAsync(e->d_ptag, k2_tags.data(), k2_tags.size() * 8, hipMemcpyHostToDevice,
                              stream);
     if (err == hipSuccess) err = hipStreamSynchronize(stream);
     hfree(d_hits);
+    free_group();
     if (err != hipSuccess) {
         return HBFSIM_CUDA_ERROR;
     }
@@ -4658,7 +4877,19 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         }
     }
     if (out != nullptr) {
-        std::memcpy(out, e->h_rep, sizeof(*out));
+        std::memcpy(out, e->h_rep, sizeof(DevReport));
+        if (grouping) {
+            // the joined records: modeled, read or write, their latencies
+            out->grouped = h_frep[0];
+            out->modeled += h_frep[0];
+            out->reads += h_frep[1];
+            out->writes += h_frep[2];
+            out->makespan_ps = std::max<std::uint64_t>(out->makespan_ps, h_frep[3]);
+            const std::uint64_t lo = out->latency_sum_lo + h_frep[4];
+            out->latency_sum_hi += h_frep[5] + (lo < out->latency_sum_lo ? 1u : 0u);
+            out->latency_sum_lo = lo;
+            out->latency_max_ps = std::max<std::uint64_t>(out->latency_max_ps, h_frep[6]);
+        }
     }
     return HBFSIM_OK;
 }

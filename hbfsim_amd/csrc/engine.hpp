@@ -42,6 +42,7 @@ struct engine_config {
     std::uint64_t read_ps{0}, program_ps{0};
     std::uint64_t xfer_num{1}, xfer_den{1}, xfer_quantum{1};
     std::uint32_t tile{4096};
+    std::uint32_t grouping{0};         // warp grouping of records with a group id
     std::uint64_t media_pages{~0ull};  // device capacity in pages
     std::uint32_t emp_pages[6]{};
     std::uint64_t emp_cum_ns[6]{};

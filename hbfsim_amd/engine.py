@@ -23,7 +23,7 @@ _MODES = {"reference": nat.HBFSIM_MODEL_REFERENCE, "fast": nat.HBFSIM_MODEL_FAST
           "hybrid": nat.HBFSIM_MODEL_HYBRID}
 OPTION_FIELDS = ("model", "page_buffers", "plane_contention", "transfer_page",
                  "program_every_write", "flat_geometry", "ways", "xfer_quantum_ps",
-                 "channel_bandwidth_bytes_per_s", "tile_records")
+                 "channel_bandwidth_bytes_per_s", "tile_records", "warp_grouping")
 
 # The reference's single-tail fast model (hbf_device.cu:883-958): one
 # channel at the aggregate bandwidth moving whole pages in whole nanoseconds,

@@ -176,13 +176,26 @@ hbfsim_context* hbfsim_vllm_session_context(hbfsim_vllm_session* session);
 /* One access record, 32 bytes, 16-byte aligned.  Replaces one call of the
  * reference's per-access resolver __hbfsim_resolve(addr, bytes, op)
  * (hbf_device.cu:963).  issue_ps is the issue time in picoseconds relative
- * to the run's base_ps.  flags bits 0-7: operation (0 read, 1 write); other
- * bits are ignored.  Records must be ordered by issue time; a record's
- * service order on every resource is its position in the stream.  The
- * thermal-coupled run also merges refresh records into the stream it times:
- * operation 2 with flag bit 8 set, addr = media page, bytes moved on the
- * channel (read out and written back); elsewhere operation 2 is
- * unsupported like any operation above 1. */
+ * to the run's base_ps.  flags bits 0-7: operation (0 read, 1 write); bits
+ * 32-63: warp group id (0: none), read when the engine option
+ * warp_grouping is 1; other bits are ignored.  Records must be ordered by
+ * issue time; a record's service order on every resource is its position in
+ * the stream.  The thermal-coupled run also merges refresh records into the
+ * stream it times: operation 2 with flag bit 8 set, addr = media page, bytes
+ * moved on the channel (read out and written back); elsewhere operation 2
+ * is unsupported like any operation above 1.
+ *
+ * Warp grouping (hbf_device.cu:1223-1231): the reference resolves the
+ * active lanes of one warp instruction together, and lanes that passed
+ * validation and touch the same (range, page) share one media request, that
+ * of the lowest lane.  Here the lanes of one instruction are consecutive
+ * records with the same nonzero group id (at most 64, one issue time); a
+ * modeled record whose (range, page) an earlier modeled record of its group
+ * already has takes that record's completion, consumes no plane, channel or
+ * page register, takes no hybrid sequence number, and reports status
+ * HBFSIM_AMD_STATUS_GROUPED.  With warp_grouping 0 (the default) every record
+ * is its own request, which equals the reference when the caller passes one
+ * record per (warp instruction, range, page). */
 typedef struct hbf_record32 {
     uint64_t addr;
     uint64_t bytes;
@@ -205,14 +218,16 @@ typedef struct hbf_record16 {
 /* Per-record status byte: bits 0-1 class (0 modeled, 1 bypass: outside
  * every range, 2 unsupported: rejected by the resolver's checks), bit 2
  * page-buffer hit, bit 3 selected by the hybrid sampler, bit 4 write that
- * programmed the page. */
+ * programmed the page, bit 5 modeled record that shared an earlier record's
+ * media request (warp grouping). */
 enum hbfsim_amd_status_bits {
     HBFSIM_AMD_MODELED = 0,
     HBFSIM_AMD_BYPASS = 1,
     HBFSIM_AMD_UNSUPPORTED = 2,
     HBFSIM_AMD_PAGE_HIT = 4,
     HBFSIM_AMD_HYBRID_SAMPLED = 8,
-    HBFSIM_AMD_PROGRAMMED = 16
+    HBFSIM_AMD_PROGRAMMED = 16,
+    HBFSIM_AMD_STATUS_GROUPED = 32
 };
 
 enum hbfsim_amd_model {
@@ -244,7 +259,9 @@ typedef struct hbfsim_amd_engine_options {
     uint64_t channel_bandwidth_bytes_per_s; /* 0: aggregate / channels */
     uint32_t tile_records;         /* records per tile, multiple of 64;
                                       0 chooses per run (default) */
-    uint32_t reserved0;
+    uint32_t warp_grouping;        /* 1: records with a group id share media
+                                      requests (32-byte records, HBF model,
+                                      at most one page register) */
 } hbfsim_amd_engine_options;
 
 /* Result of one run (or, from hbfsim_amd_get_report, of all runs). */
@@ -263,6 +280,11 @@ typedef struct hbfsim_amd_report {
     uint64_t latency_sum_hi;
     uint64_t latency_max_ps;
     uint64_t service_sum_ps;   /* sum of uncontended service times */
+    uint64_t grouped;          /* modeled records that shared an earlier
+                                  record's media request (warp grouping);
+                                  counted in records, modeled, reads/writes
+                                  and the latencies, not in page_hits,
+                                  programs, hybrid_sampled or service_sum_ps */
 } hbfsim_amd_report;
 
 /* Defaults: HBF model (EMPIRICAL when the profile carries empirical_vmem),

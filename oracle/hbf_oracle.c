@@ -654,6 +654,30 @@ static int engine_params_ok(const orc_engine_params* p)
            p->xfer_den != 0 && p->xfer_quantum != 0;
 }
 
+static uint32_t group_of(const orc_engine_params* p, const orc_record* r)
+{
+    return p->warp_grouping ? (uint32_t)(r->flags >> 32) : 0u;
+}
+
+/* A group is a maximal run of consecutive records with one nonzero id: at
+ * most ORC_GROUP_MAX records, all with one issue time. */
+static int groups_valid(const orc_engine_params* p, const orc_record* records, size_t n)
+{
+    size_t len = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t g = group_of(p, &records[i]);
+        if (g != 0 && i > 0 && len != 0 && g == group_of(p, &records[i - 1])) {
+            if (len == ORC_GROUP_MAX || records[i].issue_ps != records[i - 1].issue_ps) {
+                return 0;
+            }
+            ++len;
+        } else {
+            len = g != 0;
+        }
+    }
+    return 1;
+}
+
 int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
                    uint32_t range_count, const orc_record* records, size_t n,
                    uint64_t base_ps, orc_engine_state* s, uint64_t* completion,
@@ -666,12 +690,54 @@ int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
         (!orc_empirical_control_valid(&p->empirical) || p->page_shift != 12)) {
         return 5;
     }
+    if (p->warp_grouping && !groups_valid(p, records, n)) {
+        return 6;
+    }
     const uint32_t slots = p->page_buffers;
+    /* the current group's requests: (range, page) and the record that made it */
+    size_t g_lead[ORC_GROUP_MAX];
+    uint64_t g_page[ORC_GROUP_MAX];
+    uint32_t g_range[ORC_GROUP_MAX];
+    uint32_t g_n = 0;
     for (size_t i = 0; i < n; ++i) {
         decoded d;
         decode(p, ranges, range_count, &records[i], base_ps, &d);
         rep->records += 1;
         uint8_t st = (uint8_t)d.cls;
+        const uint32_t g = group_of(p, &records[i]);
+        if (g == 0 || i == 0 || g != group_of(p, &records[i - 1])) {
+            g_n = 0;  /* a new group (or none) */
+        }
+        if (g != 0 && d.cls == ORC_MODELED) {
+            uint32_t k = 0;
+            while (k < g_n && !(g_range[k] == d.range_id && g_page[k] == d.page)) {
+                ++k;
+            }
+            if (k < g_n) {
+                /* a lane of the request of record g_lead[k] */
+                const uint64_t done = completion[g_lead[k]];
+                completion[i] = done;
+                rep->modeled += 1;
+                rep->grouped += 1;
+                if (d.op == 0) {
+                    rep->reads += 1;
+                } else if (d.op == 1) {
+                    rep->writes += 1;
+                }
+                rep->makespan_ps = max_u64(rep->makespan_ps, done);
+                const uint64_t lat = done - d.issue;
+                add128(rep, lat);
+                rep->latency_max_ps = max_u64(rep->latency_max_ps, lat);
+                if (status != NULL) {
+                    status[i] = (uint8_t)(ORC_MODELED | ORC_STATUS_GROUPED);
+                }
+                continue;
+            }
+            g_lead[g_n] = i;
+            g_range[g_n] = d.range_id;
+            g_page[g_n] = d.page;
+            ++g_n;
+        }
         if (d.cls == ORC_BYPASS) {
             completion[i] = d.issue;
             rep->bypass += 1;
@@ -818,6 +884,7 @@ static void merge_report(orc_engine_report* t, const orc_engine_report* r)
     t->latency_sum_lo = lo;
     t->latency_max_ps = max_u64(t->latency_max_ps, r->latency_max_ps);
     t->service_sum_ps += r->service_sum_ps;
+    t->grouped += r->grouped;
 }
 
 /* Parallel oracle, identical results to orc_engine_run for ORC_MODEL_HBF.
@@ -836,7 +903,7 @@ int orc_engine_run_parallel(const orc_engine_params* p,
                             uint64_t* completion, uint8_t* status,
                             orc_engine_report* rep, int threads)
 {
-    if (p->model != ORC_MODEL_HBF || threads <= 1) {
+    if (p->model != ORC_MODEL_HBF || threads <= 1 || p->warp_grouping) {
         return orc_engine_run(p, ranges, range_count, records, n, base_ps, s,
                               completion, status, rep);
     }

@@ -108,6 +108,8 @@ enum orc_status {
  * media_records (the coupled run's merged stream); elsewhere an operation
  * above 1 is unsupported, as the resolver has it. */
 #define ORC_OP_REFRESH 2u
+#define ORC_STATUS_GROUPED 32u
+#define ORC_GROUP_MAX 64u
 #define ORC_FLAG_MEDIA 0x100u
 uint32_t orc_classify(const orc_range* ranges, uint32_t count,
                       uint64_t address, uint64_t bytes, uint32_t operation,
@@ -199,7 +201,7 @@ typedef struct orc_engine_params {
     orc_empirical empirical;                 /* MODEL_FAST_EMPIRICAL only */
     uint64_t media_pages;                    /* device pages; 0 = no limit */
     uint32_t media_records;                  /* 1: accept refresh records */
-    uint32_t reserved;
+    uint32_t warp_grouping;                  /* 1: flags >> 32 is a group id */
 } orc_engine_params;
 
 typedef struct orc_engine_state {
@@ -219,6 +221,7 @@ typedef struct orc_engine_report {
     uint64_t latency_sum_lo, latency_sum_hi;
     uint64_t latency_max_ps;
     uint64_t service_sum_ps;
+    uint64_t grouped;         /* records that shared an earlier one's request */
 } orc_engine_report;
 
 typedef struct orc_record {
@@ -227,7 +230,16 @@ typedef struct orc_record {
 
 /* Runs records in input order.  issue = base_ps + record.issue_ps.
  * completion[i]: completion ps (bypass: issue; unsupported: UINT64_MAX).
- * status may be NULL.  Report accumulates (caller zeroes it). */
+ * status may be NULL.  Report accumulates (caller zeroes it).
+ *
+ * Warp grouping (p->warp_grouping, hbf_device.cu:1223-1231): consecutive
+ * records with the same nonzero group id (flags >> 32) are the lanes of one
+ * warp instruction; a modeled record whose (range, media page) an earlier
+ * modeled record of its group already has shares that record's request: it
+ * takes its completion and status ORC_STATUS_GROUPED and touches no
+ * resource, page register or hybrid sequence number.  Returns 6 before
+ * anything is timed when a group has more than 64 records or two issue
+ * times. */
 int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
                    uint32_t range_count, const orc_record* records, size_t n,
                    uint64_t base_ps, orc_engine_state* s, uint64_t* completion,

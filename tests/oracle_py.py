@@ -47,7 +47,7 @@ class OrcParams(ctypes.Structure):
                 ("hybrid_threshold", _U64), ("read_ps", _U64), ("program_ps", _U64),
                 ("xfer_num", _U64), ("xfer_den", _U64), ("xfer_quantum", _U64),
                 ("empirical", OrcEmpirical), ("media_pages", _U64), ("media_records", _U32),
-                ("reserved", _U32)]
+                ("warp_grouping", _U32)]
 
 
 class OrcState(ctypes.Structure):
@@ -58,7 +58,7 @@ class OrcState(ctypes.Structure):
 
 REPORT_FIELDS = ("records", "modeled", "bypass", "unsupported", "reads", "writes", "page_hits",
                  "programs", "hybrid_sampled", "makespan_ps", "latency_sum_lo",
-                 "latency_sum_hi", "latency_max_ps", "service_sum_ps")
+                 "latency_sum_hi", "latency_max_ps", "service_sum_ps", "grouped")
 
 
 class OrcReport(ctypes.Structure):
@@ -267,9 +267,11 @@ def load_profile(path) -> dict:
 
 def engine_params(profile: dict, page_buffers=1, plane_contention=1, transfer_page=0,
                   program_every_write=0, flat_geometry=0, ways=1, xfer_quantum_ps=1,
-                  channel_bandwidth_bytes_per_s=0, hybrid=False, model=0) -> OrcParams:
+                  channel_bandwidth_bytes_per_s=0, hybrid=False, model=0,
+                  warp_grouping=0) -> OrcParams:
     p = OrcParams()
     p.model = model
+    p.warp_grouping = warp_grouping
     if flat_geometry:
         p.channels = p.ways = p.dies = p.planes = 1
     else:

@@ -8,7 +8,8 @@ import oracle_py
 from hbfsim_amd import engine as eng
 
 OPTION_KEYS = ("page_buffers", "plane_contention", "transfer_page", "program_every_write",
-               "flat_geometry", "ways", "xfer_quantum_ps", "channel_bandwidth_bytes_per_s")
+               "flat_geometry", "ways", "xfer_quantum_ps", "channel_bandwidth_bytes_per_s",
+               "warp_grouping")
 
 
 def to_device(records: np.ndarray):

@@ -120,6 +120,27 @@ def test_registry_semantics(tmp_path):
     e.close()
 
 
+def test_range_capacity(tmp_path):
+    """The table holds 32,768 ranges (hbf_device.cuh:21); the next
+    registration is refused with HBFSIM_UNSUPPORTED and leaves the table as
+    it was; removing one range makes room again."""
+    e = eng.Engine(C0, str(tmp_path))
+    base, page = 0x5000_0000_0000, 16384
+    for r in range(32768):
+        e.register(base + 2 * r * page, page, nat.HBFSIM_RANGE_READ)
+    lib = nat.load()
+    o = nat.RangeOptions(nat.HBFSIM_RANGE_MODE_TIMING, nat.HBFSIM_RANGE_READ, 0, 0)
+    extra = base + 2 * 32768 * page
+    assert lib.hbfsim_register_device(e.handle, ctypes.c_void_p(extra), page,
+                                      ctypes.byref(o)) == nat.HBFSIM_UNSUPPORTED
+    assert e.lookup(extra)[0] == "outside"
+    assert e.lookup(base + 2 * 32767 * page)[0] == "matched"
+    e.unregister(base)
+    assert lib.hbfsim_register_device(e.handle, ctypes.c_void_p(extra), page,
+                                      ctypes.byref(o)) == 0
+    e.close()
+
+
 def test_map_file_and_capacity_stats(tmp_path):
     e = eng.Engine(C0, str(tmp_path))
     lib = nat.load()

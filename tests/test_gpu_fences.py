@@ -1,7 +1,7 @@
 """The range lookup's two levels at their boundaries.  The engine stages
 every stride-th range base in LDS (at most 256 of them) and searches the
 stride below in memory, so the stride steps from 1 to 2 at 257 ranges and to
-3 at 513.  Records aim at every range's first and last line, at the gaps
+3 at 513, and is 128 at the 32,768-range capacity.  Records aim at every range's first and last line, at the gaps
 before and after it (bypass), and at random lines across the whole table,
 in random order; both record forms must equal the oracle bit for bit."""
 from __future__ import annotations
@@ -35,7 +35,7 @@ def lookup_stream(ranges, seed, n_random=20_000):
 
 
 @pytest.mark.parametrize("profile", [C0, C2], ids=["c0", "c2"])
-@pytest.mark.parametrize("count", [255, 256, 257, 511, 512, 513, 1000])
+@pytest.mark.parametrize("count", [255, 256, 257, 511, 512, 513, 1000, 16384, 32767, 32768])
 def test_range_lookup_stride_boundaries(profile, count):
     ranges = ranges_for(count=count - 1, pages=2)  # count - 1 readable + 1 write-only
     assert len(ranges) == count
