@@ -54,9 +54,22 @@ CLI_SOURCES = [CSRC / "trace_timing.cpp", CSRC / "profile.cpp"]
 
 
 def cli_command(output: pathlib.Path = CLI) -> list[str]:
-    """The hbf_trace_timing drop-in: host C++ only."""
-    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
-    return [cxx, "-O2", "-std=c++17", "-Wall", "-o", str(output), *[str(s) for s in CLI_SOURCES]]
+    """The hbf_trace_timing drop-in: host code, linked against the library
+    (its GPU sampler serves hybrid mode), found next to the executable."""
+    return [hipcc(), "-O2", "-std=c++17", "-Wall", "-o", str(output),
+            *[str(s) for s in CLI_SOURCES], "-L", str(HERE), "-lhbfsim_amd",
+            "-Wl,-rpath,$ORIGIN"]
+
+
+MEDIA_BENCH = HERE / "hbf_media_bench"
+MEDIA_BENCH_SOURCES = [CSRC / "media_bench.cpp", CSRC / "profile.cpp"]
+
+
+def media_bench_command(output: pathlib.Path = MEDIA_BENCH) -> list[str]:
+    """hbf_media_bench: host code timing through the library."""
+    return [hipcc(), "-O2", "-std=c++17", "-Wall", "-o", str(output),
+            *[str(s) for s in MEDIA_BENCH_SOURCES], "-L", str(HERE), "-lhbfsim_amd",
+            "-Wl,-rpath,$ORIGIN"]
 
 
 def build_cli(verbose: bool = False) -> pathlib.Path:
@@ -69,6 +82,9 @@ def build_cli(verbose: bool = False) -> pathlib.Path:
         sys.stderr.write(proc.stdout + proc.stderr)
         raise RuntimeError(f"c++ failed with status {proc.returncode}")
     os.replace(tmp, CLI)
+    tmp = MEDIA_BENCH.with_suffix(".tmp")
+    _run(media_bench_command(tmp), verbose)
+    os.replace(tmp, MEDIA_BENCH)
     return CLI
 
 

@@ -9,15 +9,23 @@
 // reads, tPROG for writes; transfer = ceil(page * 1e9 / aggregate)).  All
 // pages of one event have the same cost, so an event contributes
 // pages * cost in one saturating step -- the replay is parse-bound, and this
-// is host code.  hybrid and mqsim modes need the MQSim reference (hybrid
-// sends the first request of every access class to it,
-// calibrator.cpp:83-96), which is not part of this build: they exit 2.
+// is host code.  In hybrid mode the library's GPU HybridSampler
+// (hbfsim_amd_sampler_reference, calibrator.cpp:83-96) picks the requests
+// the reference would send to MQSim (hbf_trace_timing.cpp:196-206); MQSim is
+// not part of this build, so those requests are counted as reference
+// requests and timed by the fast model, and the report says so in
+// "reference_timing".  mqsim mode needs MQSim for every request: it exits 2.
 //
 // Output: the reference's JSON report, keys sorted and two-space indented as
 // nlohmann::json::dump(2) prints it.  Exit 64 on invalid arguments or
 // events (std::invalid_argument in the reference), 2 on other errors.
+#include "cli_json.hpp"
 #include "json_min.hpp"
 #include "profile.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/hbfsim_amd.h"
 
 #include <charconv>
 #include <chrono>
@@ -30,6 +38,7 @@
 #include <stdexcept>
 #include <string>
 #include <string_view>
+#include <vector>
 
 namespace {
 
@@ -153,43 +162,54 @@ event parse_event(const json_min::value& e, std::uint64_t input_sequence)
     return {address, bytes, static_cast<std::uint32_t>(page), operation == "write"};
 }
 
-std::string quote(const std::string& s)
-{
-    std::string out = "\"";
-    for (const char ch : s) {
-        const auto c = static_cast<unsigned char>(ch);
-        switch (c) {
-        case '"': out += "\\\""; break;
-        case '\\': out += "\\\\"; break;
-        case '\b': out += "\\b"; break;
-        case '\f': out += "\\f"; break;
-        case '\n': out += "\\n"; break;
-        case '\r': out += "\\r"; break;
-        case '\t': out += "\\t"; break;
-        default:
-            if (c < 0x20) {
-                char buf[8];
-                std::snprintf(buf, sizeof buf, "\\u%04x", c);
-                out += buf;
-            } else {
-                out += ch;
-            }
-        }
-    }
-    return out + "\"";
-}
+using cli_json::quote;
+using cli_json::real;
 
-// A double as nlohmann::json prints it: the shortest round-trip form, with
-// ".0" appended when that reads as an integer.
-std::string real(double v)
+// HybridSampler(warmup, rate, 0).reference(sequence - 1, access) for every
+// page request in order (hbf_trace_timing.cpp:154-155, 181-206), on the GPU.
+std::vector<std::uint8_t> sample_requests(const hbfamd::profile& prof, const std::vector<event>& evs)
 {
-    char buf[64];
-    const auto r = std::to_chars(buf, buf + sizeof buf, v);
-    std::string s(buf, r.ptr);
-    if (s.find_first_of(".eEn") == std::string::npos) {
-        s += ".0";
+    std::vector<hbfsim_amd_access_class> access;
+    for (const event& ev : evs) {
+        const hbfsim_amd_access_class a{ev.write ? 1u : 0u,
+                                        static_cast<std::uint32_t>(ev.page_bytes), 0u, 0u};
+        access.insert(access.end(), ev.bytes / ev.page_bytes, a);
     }
-    return s;
+    std::vector<std::uint8_t> flags(access.size(), 0);
+    if (access.empty()) {
+        return flags;
+    }
+    if (access.size() >= (std::size_t{1} << 32)) {
+        throw std::runtime_error("hybrid mode takes fewer than 2^32 page requests");
+    }
+    hbfsim_amd_sampler* sampler = nullptr;
+    if (hbfsim_amd_sampler_create(prof.reference_warmup_requests, prof.reference_sample_rate, 0,
+                                  &sampler) != HBFSIM_OK) {
+        throw std::invalid_argument("sample_rate must be in [0, 1]");
+    }
+    hbfsim_amd_access_class* d_access = nullptr;
+    std::uint8_t* d_flags = nullptr;
+    hipError_t err = hipMalloc(reinterpret_cast<void**>(&d_access), access.size() * sizeof(access[0]));
+    if (err == hipSuccess) err = hipMalloc(reinterpret_cast<void**>(&d_flags), flags.size());
+    if (err == hipSuccess)
+        err = hipMemcpy(d_access, access.data(), access.size() * sizeof(access[0]),
+                        hipMemcpyHostToDevice);
+    int st = err == hipSuccess ? HBFSIM_OK : HBFSIM_CUDA_ERROR;
+    if (st == HBFSIM_OK) {
+        st = hbfsim_amd_sampler_reference(sampler, d_access, nullptr, 0, access.size(), d_flags,
+                                          nullptr, nullptr);
+    }
+    if (st == HBFSIM_OK && hipMemcpy(flags.data(), d_flags, flags.size(), hipMemcpyDeviceToHost) !=
+                               hipSuccess) {
+        st = HBFSIM_CUDA_ERROR;
+    }
+    (void)hipFree(d_access);
+    (void)hipFree(d_flags);
+    hbfsim_amd_sampler_destroy(sampler);
+    if (st != HBFSIM_OK) {
+        throw std::runtime_error("the GPU sampler failed (hybrid mode needs a GPU)");
+    }
+    return flags;
 }
 
 }  // namespace
@@ -203,12 +223,12 @@ int main(int argc, char** argv)
         if (!in) {
             throw std::runtime_error("failed to open timing event JSONL");
         }
-        if (o.mode != "fast") {
-            throw std::runtime_error(
-                "MQSim reference timing is not part of this engine (mode " + o.mode + ")");
+        if (o.mode == "mqsim") {
+            throw std::runtime_error("MQSim reference timing is not part of this engine");
         }
         std::uint64_t input_events = 0, sequence = 0, clock_ns = 0, service_ns = 0;
-        std::uint64_t fast_requests = 0;
+        std::uint64_t fast_requests = 0, reference_requests = 0;
+        std::vector<event> evs;
         std::string line;
         const auto t0 = std::chrono::steady_clock::now();
         while (std::getline(in, line)) {
@@ -221,6 +241,14 @@ int main(int argc, char** argv)
                 throw std::invalid_argument(
                     "event page size or range differs from the frozen profile");
             }
+            evs.push_back(ev);
+        }
+        std::vector<std::uint8_t> sampled;
+        if (o.mode == "hybrid") {
+            sampled = sample_requests(prof, evs);
+        }
+        std::size_t k = 0;
+        for (const event& ev : evs) {
             const std::uint64_t pages = ev.bytes / ev.page_bytes;
             const std::uint64_t base = ev.write ? prof.program_latency_ns : prof.read_latency_ns;
             const std::uint64_t service =
@@ -233,7 +261,15 @@ int main(int argc, char** argv)
             service_ns = sat_add_n(service_ns, pages, service);
             clock_ns = sat_add_n(clock_ns, pages, exposed);
             sequence += pages;
-            fast_requests += pages;
+            std::uint64_t ref = 0;
+            if (!sampled.empty()) {
+                for (std::uint64_t p = 0; p < pages; ++p) {
+                    ref += sampled[k + p];
+                }
+                k += pages;
+            }
+            reference_requests += ref;
+            fast_requests += pages - ref;
         }
         const auto wall = static_cast<std::uint64_t>(
             std::chrono::duration_cast<std::chrono::nanoseconds>(
@@ -243,15 +279,18 @@ int main(int argc, char** argv)
         os << "{\n"
            << "  \"demand_exposed_stall_ns\": " << clock_ns << ",\n"
            << "  \"emulator_dispatcher_wall_time_ns\": " << wall << ",\n"
-           << "  \"engine\": \"hbf-fast\",\n"
+           << "  \"engine\": \"" << (o.mode == "hybrid" ? "hbf-hybrid" : "hbf-fast") << "\",\n"
            << "  \"modeled_device_service_ns\": " << service_ns << ",\n"
            << "  \"profile\": " << quote(prof.name) << ",\n"
            << "  \"reference_sample_rate\": " << real(prof.reference_sample_rate) << ",\n"
+           << (o.mode == "hybrid"
+                   ? "  \"reference_timing\": \"hbf-fast (MQSim is not part of this engine)\",\n"
+                   : "")
            << "  \"reference_warmup_requests\": " << prof.reference_warmup_requests << ",\n"
            << "  \"requests\": {\n"
            << "    \"fast\": " << fast_requests << ",\n"
            << "    \"input_expert_misses\": " << input_events << ",\n"
-           << "    \"reference\": 0,\n"
+           << "    \"reference\": " << reference_requests << ",\n"
            << "    \"submitted\": " << sequence << "\n"
            << "  },\n"
            << "  \"scheduling_semantics\": \"ordered blocking demand misses with no compute "

@@ -1,0 +1,53 @@
+"""hbf_trace_timing --mode hybrid: the page requests the reference's replay
+would send to MQSim (hbf_trace_timing.cpp:196-206: HybridSampler(warmup,
+rate, 0).reference(sequence - 1, access)) are picked by the library's GPU
+sampler and counted as reference requests; the count must equal the CPU
+oracle's sampler over the same request sequence, and the clocks the fast
+mode's (MQSim is absent, so the sampled requests are timed by the fast model
+and the report's reference_timing says so)."""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+import oracle_py
+from test_cli import PROFILES, cli, run, write_events  # noqa: F401  (fixture)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("name", ["nominal", "aggressive", "conservative"])
+def test_hybrid_mode_counts_sampled_requests(cli, tmp_path, name):  # noqa: F811
+    path = PROFILES / f"{name}.json"
+    prof = json.loads(path.read_text())
+    page = prof["page_bytes"]
+    rng = np.random.default_rng(3 + len(name))
+    events = []
+    for _ in range(2000):
+        pages = int(rng.integers(1, 30))
+        addr = int(rng.integers(0, prof["capacity_bytes"] // page - pages)) * page
+        events.append((addr, pages * page, page, "write" if rng.random() < 0.3 else "read"))
+    ev_path = tmp_path / "events.jsonl"
+    write_events(ev_path, events)
+    fast = run(cli, "--profile", path, "--events", ev_path, "--mode", "fast")
+    hyb = run(cli, "--profile", path, "--events", ev_path, "--mode", "hybrid")
+    assert fast.returncode == 0 and hyb.returncode == 0, hyb.stderr
+    f, h = json.loads(fast.stdout), json.loads(hyb.stdout)
+    access = []
+    for _, nbytes, pg, op in events:
+        access += [(1 if op == "write" else 0, pg, 0, 0)] * (nbytes // pg)
+    flags = oracle_py.sampler_run(prof["reference_warmup_requests"],
+                                  prof["reference_sample_rate"], 0, np.array(access),
+                                  np.arange(len(access), dtype=np.uint64))
+    ref = int(flags.sum())
+    assert 0 < ref < len(access)
+    assert h["engine"] == "hbf-hybrid" and h["status"] == "PASS"
+    assert h["requests"] == {"input_expert_misses": len(events), "submitted": len(access),
+                             "fast": len(access) - ref, "reference": ref}
+    assert h["reference_timing"].startswith("hbf-fast")
+    for k in ("demand_exposed_stall_ns", "modeled_device_service_ns", "profile",
+              "reference_sample_rate", "reference_warmup_requests", "scheduling_semantics"):
+        assert h[k] == f[k], k
+    assert list(h) == sorted(h)
