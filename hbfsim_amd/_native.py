@@ -225,6 +225,7 @@ SIGNATURES = {
     "hbfsim_amd_coupled_last_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float), _INT]),
     "hbfsim_amd_coupled_trace": (_INT, [_P, _P, _SZ, _P, _SZ, _P, _SZ, ctypes.POINTER(_U64),
                                         ctypes.POINTER(_U32)]),
+    "hbfsim_amd_mqsim_admission": (_INT, [_P, _P, _SZ, _U32, _U64, _U64, _P, _P, _P]),
     "hbfsim_amd_link_run": (_INT, [ctypes.POINTER(LinkProfile), _P, _U32, _P, _P, _SZ, _P, _P,
                                    _P]),
     "hbfsim_amd_validate_profile": (_INT, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),

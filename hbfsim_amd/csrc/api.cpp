@@ -994,6 +994,15 @@ HBF_API int hbfsim_amd_media_servers(const uint64_t* d_now_ns, size_t n, uint32_
     return hbfamd::media_servers(d_now_ns, n, servers, latency_ns, d_completion_ns, stream);
 }
 
+HBF_API int hbfsim_amd_mqsim_admission(const uint64_t* d_arrival_ns, const uint64_t* d_bytes,
+                                       size_t n, uint32_t queue_depth, uint64_t latency_ns,
+                                       uint64_t bandwidth_bytes_per_s, uint64_t* d_admission_ns,
+                                       uint64_t* d_completion_ns, void* stream)
+{
+    return hbfamd::mqsim_admission(d_arrival_ns, d_bytes, n, queue_depth, latency_ns,
+                                   bandwidth_bytes_per_s, d_admission_ns, d_completion_ns, stream);
+}
+
 struct hbfsim_amd_sampler {
     hbfamd::sampler_state* state;
 };

@@ -112,6 +112,12 @@ int gen_spans(hbf_record32* d_records, std::size_t capacity, const std::uint64_t
 int media_servers(const std::uint64_t* d_now, std::size_t n, std::uint32_t servers,
                   std::uint64_t latency_ns, std::uint64_t* d_completion, void* stream);
 
+// hbfsim_amd_mqsim_admission (admission.hip).  Synchronises `stream`.
+int mqsim_admission(const std::uint64_t* d_arrival, const std::uint64_t* d_bytes, std::size_t n,
+                    std::uint32_t queue_depth, std::uint64_t latency_ns,
+                    std::uint64_t bandwidth, std::uint64_t* d_admission,
+                    std::uint64_t* d_completion, void* stream);
+
 // Hybrid model's sampler and calibrator (hybrid.hip).
 struct sampler_state;
 int sampler_create(std::uint32_t warmup, double sample_rate, std::uint64_t seed,

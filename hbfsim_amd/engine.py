@@ -378,6 +378,25 @@ def pack_records(records: Any) -> Any:
     return torch.stack([addr | (nbytes << 48), issue | (flags << 56)], dim=1).contiguous()
 
 
+def mqsim_admission(arrival_ns: Any, nbytes: Any, queue_depth: int, latency_ns: int,
+                    bandwidth_bytes_per_s: int, stream: Any = None) -> tuple[Any, Any]:
+    """hbfsim_amd_mqsim_admission: the MQSim adapter's queue-depth admission
+    and bandwidth cursor over a media port of one latency (int64 tensors on
+    the GPU, arrivals non-decreasing).  Returns (admission_ns,
+    completion_ns); ValueError for what the library refuses."""
+    import torch
+    n = int(arrival_ns.shape[0])
+    adm = torch.empty(max(n, 1), dtype=torch.int64, device=arrival_ns.device)
+    done = torch.empty(max(n, 1), dtype=torch.int64, device=arrival_ns.device)
+    rc = nat.load().hbfsim_amd_mqsim_admission(
+        _ptr(arrival_ns), _ptr(nbytes), n, queue_depth, latency_ns, bandwidth_bytes_per_s,
+        _ptr(adm), _ptr(done), ctypes.c_void_p(_stream_handle(stream)))
+    if rc == nat.HBFSIM_INVALID_ARGUMENT:
+        raise ValueError("arrivals out of order, bandwidth 0 or times from 2^63 ns")
+    nat.check(rc, "mqsim admission")
+    return adm[:n], done[:n]
+
+
 def media_servers(now_ns: Any, servers: int, latency_ns: int, stream: Any = None) -> Any:
     """MediaServers::issue (prefetch_model.cpp:22-50) over a batch of reads
     issued at non-decreasing times `now_ns` (torch int64 on the GPU): returns

@@ -428,6 +428,24 @@ int hbfsim_amd_gen_spans(hbf_record32* d_records, size_t capacity,
 int hbfsim_amd_media_servers(const uint64_t* d_now_ns, size_t n, uint32_t servers,
                              uint64_t latency_ns, uint64_t* d_completion_ns, void* stream);
 
+/* The MQSim adapter's queue-depth admission and bandwidth cursor
+ * (mqsim_online.cpp:291-376: submit_to_device, dispatch_to_device, the
+ * completion callback, release_admission_slots) over a media port that
+ * completes every request latency_ns after it is handed over (the role of
+ * MQSim, which is not part of this engine).  Requests in submission order
+ * with non-decreasing d_arrival_ns; at most max(1, queue_depth) are in the
+ * device at a time, the rest wait in arrival order; each completion applies
+ * cursor = max(cursor, arrival) + ceil(bytes * 1e9 / bandwidth).
+ * d_admission_ns[i] (may be NULL): when request i was handed over;
+ * d_completion_ns[i]: max(admission + latency, cursor), the adapter's
+ * bounded completion.  Device arrays; synchronises `stream`.
+ * HBFSIM_INVALID_ARGUMENT for bandwidth 0, arrivals out of order or times
+ * from 2^63 ns. */
+int hbfsim_amd_mqsim_admission(const uint64_t* d_arrival_ns, const uint64_t* d_bytes, size_t n,
+                               uint32_t queue_depth, uint64_t latency_ns,
+                               uint64_t bandwidth_bytes_per_s, uint64_t* d_admission_ns,
+                               uint64_t* d_completion_ns, void* stream);
+
 /* ----- Hybrid model: request sampler and calibrator -------------------
  * The host-side HybridSampler and Calibrator of src/hybrid/calibrator.cpp
  * (include/hbfsim/hybrid_model.hpp:13-60) for batches of requests held in

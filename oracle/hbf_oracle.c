@@ -1150,6 +1150,122 @@ uint64_t orc_bandwidth_cursor(uint64_t* cursor_ns, uint64_t arrival_ns,
     return max_u64(media_completion_ns, *cursor_ns);
 }
 
+/* MQSim-style event queue: (time, registration order) min-heap. */
+typedef struct adm_event {
+    uint64_t time, order;
+    uint32_t kind;  /* 0 arrival, 1 completion */
+    uint32_t request;
+} adm_event;
+
+static int adm_before(const adm_event* a, const adm_event* b)
+{
+    return a->time != b->time ? a->time < b->time : a->order < b->order;
+}
+
+static void adm_push(adm_event* h, size_t* size, adm_event e)
+{
+    size_t i = (*size)++;
+    h[i] = e;
+    while (i > 0 && adm_before(&h[i], &h[(i - 1) / 2])) {
+        const adm_event t = h[i];
+        h[i] = h[(i - 1) / 2];
+        h[(i - 1) / 2] = t;
+        i = (i - 1) / 2;
+    }
+}
+
+static adm_event adm_pop(adm_event* h, size_t* size)
+{
+    const adm_event top = h[0];
+    h[0] = h[--(*size)];
+    size_t i = 0;
+    for (;;) {
+        const size_t l = 2 * i + 1, r = l + 1;
+        size_t m = i;
+        if (l < *size && adm_before(&h[l], &h[m])) m = l;
+        if (r < *size && adm_before(&h[r], &h[m])) m = r;
+        if (m == i) break;
+        const adm_event t = h[i];
+        h[i] = h[m];
+        h[m] = t;
+        i = m;
+    }
+    return top;
+}
+
+static const uint64_t* adm_sort_key;
+static int adm_cmp(const void* pa, const void* pb)
+{
+    const uint32_t a = *(const uint32_t*)pa, b = *(const uint32_t*)pb;
+    if (adm_sort_key[a] != adm_sort_key[b]) {
+        return adm_sort_key[a] < adm_sort_key[b] ? -1 : 1;
+    }
+    return a < b ? -1 : (a > b);
+}
+
+int orc_mqsim_admission(const uint64_t* arrival_ns, const uint64_t* bytes,
+                        const uint64_t* latency_ns, size_t n, uint32_t queue_depth,
+                        uint64_t bandwidth, uint64_t* admission_ns, uint64_t* device_ns,
+                        uint64_t* completion_ns)
+{
+    if (bandwidth == 0 || n >= ((size_t)1 << 32)) {
+        return 1;
+    }
+    if (n == 0) {
+        return 0;
+    }
+    const uint64_t depth = queue_depth == 0 ? 1 : queue_depth;  /* max(1, queue_depth) */
+    uint32_t* staged = malloc(n * sizeof(uint32_t));
+    uint32_t* fifo = malloc(n * sizeof(uint32_t));
+    uint8_t* readmitted = calloc(n, 1);
+    adm_event* heap = malloc(3 * n * sizeof(adm_event));  /* arrivals, completions, re-registrations */
+    size_t size = 0, fhead = 0, ftail = 0;
+    uint64_t order = 0, in_device = 0, cursor = 0;
+    for (size_t i = 0; i < n; ++i) {
+        staged[i] = (uint32_t)i;
+    }
+    adm_sort_key = arrival_ns;
+    qsort(staged, n, sizeof(uint32_t), adm_cmp);  /* flush_staged */
+    for (size_t i = 0; i < n; ++i) {
+        const adm_event e = {arrival_ns[staged[i]], order++, 0, staged[i]};
+        adm_push(heap, &size, e);
+    }
+    while (size != 0) {
+        const adm_event e = adm_pop(heap, &size);
+        const uint32_t k = e.request;
+        if (e.kind == 0) {  /* submit_to_device */
+            if (!readmitted[k]) {
+                if (in_device >= depth) {
+                    fifo[ftail++] = k;
+                    continue;
+                }
+                ++in_device;
+            }
+            readmitted[k] = 0;
+            admission_ns[k] = e.time;  /* dispatch_to_device */
+            device_ns[k] = e.time + latency_ns[k];
+            const adm_event c = {device_ns[k], order++, 1, k};
+            adm_push(heap, &size, c);
+        } else {  /* the completion callback */
+            completion_ns[k] = orc_bandwidth_cursor(&cursor, arrival_ns[k], bytes[k],
+                                                    bandwidth, e.time);
+            --in_device;
+            while (in_device < depth && fhead != ftail) {  /* release_admission_slots */
+                const uint32_t j = fifo[fhead++];
+                readmitted[j] = 1;
+                ++in_device;
+                const adm_event a = {e.time, order++, 0, j};
+                adm_push(heap, &size, a);
+            }
+        }
+    }
+    free(staged);
+    free(fifo);
+    free(readmitted);
+    free(heap);
+    return 0;
+}
+
 /* prefetch_model.cpp:22-50: k identical servers; a read issued at `now`
  * takes the server that frees first and finishes one latency later. */
 /* MediaServers::issue (prefetch_model.cpp:37-46): the server that frees

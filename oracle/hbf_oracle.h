@@ -287,6 +287,24 @@ uint64_t orc_bandwidth_cursor(uint64_t* cursor_ns, uint64_t arrival_ns,
 void orc_pagebuf_sequence(const uint64_t* pages, size_t n, uint32_t slots,
                           uint8_t* hits);
 
+/* ---- MQSim adapter admission (mqsim_online.cpp:266-376) --------------
+ * The adapter over a fake media port (in the style of the reference's
+ * FakeMedia, ucie_device_frontend_fake_test.cpp:14-66) that completes
+ * request i latency_ns[i] after it is handed over.  Requests are staged and
+ * their arrival events registered in (arrival, index) order (flush_staged);
+ * an arrival finding queue_depth requests in the device waits in a FIFO
+ * (submit_to_device); a completion applies the bandwidth cursor
+ * (orc_bandwidth_cursor, in completion order), frees its slot and
+ * re-registers waiting requests at the current time
+ * (release_admission_slots).  Events at one time fire in the order they
+ * were registered, as MQSim's event queue fires them.  Outputs per request:
+ * the time it was handed to the media port, the port's completion and the
+ * bounded completion.  Returns 0, or 1 for bandwidth 0 or n >= 2^32. */
+int orc_mqsim_admission(const uint64_t* arrival_ns, const uint64_t* bytes,
+                        const uint64_t* latency_ns, size_t n, uint32_t queue_depth,
+                        uint64_t bandwidth, uint64_t* admission_ns, uint64_t* device_ns,
+                        uint64_t* completion_ns);
+
 /* ---- k-server busy-until (prefetch_model.cpp:22-50) ------------------ */
 void orc_media_servers(const uint64_t* now_ns, size_t n, uint32_t servers,
                        uint64_t latency_ns, uint64_t* completion_ns);

@@ -168,6 +168,8 @@ def lib() -> ctypes.CDLL:
             "orc_bandwidth_cursor": (_U64, [_P, _U64, _U64, _U64, _U64]),
             "orc_pagebuf_sequence": (None, [_P, ctypes.c_size_t, _U32, _P]),
             "orc_media_servers": (None, [_P, ctypes.c_size_t, _U32, _U64, _P]),
+            "orc_mqsim_admission": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t, _U32, _U64,
+                                                   _P, _P, _P]),
             "orc_simulate_prefetch": (ctypes.c_int, [_P, ctypes.c_size_t, _U32, _U32, _U32,
                                                      _U32, _U64, _U64, _P]),
             "orc_sampler_run": (ctypes.c_int, [_U32, ctypes.c_double, _U64, _P, _P,
@@ -230,6 +232,22 @@ CALIBRATION_DTYPE = np.dtype([("operation", "<u4"), ("bytes", "<u4"), ("queue_bu
                               ("locality_bucket", "<u4"), ("count", "<u8"), ("mean_ns", "<u8"),
                               ("p50_ns", "<u8"), ("p95_ns", "<u8"), ("p99_ns", "<u8"),
                               ("log_mean", "<f8"), ("log_sigma", "<f8")])
+
+
+def mqsim_admission(arrival, nbytes, latency, queue_depth: int, bandwidth: int):
+    """orc_mqsim_admission: (admission, media completion, bounded completion)
+    per request, in ns."""
+    arrival = np.ascontiguousarray(arrival, np.uint64)
+    nbytes = np.ascontiguousarray(nbytes, np.uint64)
+    latency = np.ascontiguousarray(np.broadcast_to(np.asarray(latency, np.uint64),
+                                                   arrival.shape))
+    n = len(arrival)
+    out = [np.zeros(max(n, 1), np.uint64) for _ in range(3)]
+    rc = lib().orc_mqsim_admission(addr(arrival), addr(nbytes), addr(latency), n, queue_depth,
+                                   bandwidth, addr(out[0]), addr(out[1]), addr(out[2]))
+    if rc != 0:
+        raise ValueError("bandwidth 0 or too many requests")
+    return tuple(o[:n] for o in out)
 
 
 def sampler_run(warmup, rate, seed, access, sequence) -> np.ndarray:
