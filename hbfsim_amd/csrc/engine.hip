@@ -194,6 +194,40 @@ __device__ __forceinline__ void group_scan(std::uint64_t& A, std::uint64_t& B, i
     }
 }
 
+// Two independent group scans of 32-bit (A, B) maps, interleaved: pointer
+// jumping along pred1 and pred2 (previous lane of the same group, or -1).
+__device__ __forceinline__ void group_scan32x2(std::uint32_t& A1, std::uint32_t& B1, int pred1,
+                                               std::uint32_t& A2, std::uint32_t& B2, int pred2,
+                                               int lane)
+{
+    int p1 = pred1, p2 = pred2;
+    for (int s = 0; s < 6; ++s) {
+        if (__ballot(p1 >= 0 || p2 >= 0) == 0) {
+            break;
+        }
+        const int s1 = p1 < 0 ? lane : p1;
+        const int s2 = p2 < 0 ? lane : p2;
+        const std::uint32_t a1 = static_cast<std::uint32_t>(__shfl(static_cast<int>(A1), s1));
+        const std::uint32_t b1 = static_cast<std::uint32_t>(__shfl(static_cast<int>(B1), s1));
+        const int q1 = __shfl(p1, s1);
+        const std::uint32_t a2 = static_cast<std::uint32_t>(__shfl(static_cast<int>(A2), s2));
+        const std::uint32_t b2 = static_cast<std::uint32_t>(__shfl(static_cast<int>(B2), s2));
+        const int q2 = __shfl(p2, s2);
+        if (p1 >= 0) {
+            const std::uint32_t nb = b1 + A1;
+            B1 = nb > B1 ? nb : B1;
+            A1 = a1 + A1;
+            p1 = q1;
+        }
+        if (p2 >= 0) {
+            const std::uint32_t nb = b2 + A2;
+            B2 = nb > B2 ? nb : B2;
+            A2 = a2 + A2;
+            p2 = q2;
+        }
+    }
+}
+
 // Whole-wave inclusive scan of (A, B) maps in lane order, for steps where
 // every active lane belongs to one group (inactive lanes hold the identity
 // (0, 0)).  DPP row shifts build 16-lane scans, then row broadcasts join the
@@ -441,6 +475,12 @@ constexpr std::size_t kGroupSpan = static_cast<std::size_t>(kPipe) * kWave;
 // The summary pass, whose occupancy its per-plane LDS state limits (not its
 // registers), keeps twice as many steps in flight per wave.
 constexpr int kSumPipe = 8;
+// Linear-step detection on streams that show none: after kLinGiveUp steps in
+// a row fail it, a wave probes only every kLinProbe-th step until one
+// passes (every step is exact on the general path too; random streams stop
+// paying for the check).
+constexpr std::uint32_t kLinGiveUp = 8;
+constexpr std::size_t kLinProbe = 32;
 
 // A step in the registers of one lane: the coalesced halves of 32-byte
 // records, or one packed 16-byte record.
@@ -1232,28 +1272,31 @@ __device__ __forceinline__ void scan_group(const Group& g, std::uint64_t& A, std
     }
 }
 
-// Scans a step's plane maps and channel maps.  When both are single-key
-// steps and the narrow check passes, both run as interleaved 32-bit DPP scans
-// relative to the time origin; otherwise each runs exactly in 64 bits.
+// Scans a step's plane maps and channel maps.  When the narrow check passes
+// both run in 32 bits relative to the step's time origin: as interleaved DPP
+// scans when both are single-key steps, else as interleaved pointer-jumping
+// group scans.  Otherwise each runs exactly in 64 bits.
 __device__ __forceinline__ void scan_pair(const Group& gp, std::uint64_t& Ap, std::uint64_t& Bp,
                                           const Group& gc, std::uint64_t& Ac, std::uint64_t& Bc,
                                           const Dec& d, bool m, std::uint64_t active,
                                           std::uint64_t svc, std::uint64_t xfer, int lane)
 {
-    if (gp.uniform && gc.uniform) {
-        const Narrow nw = narrow_check(d, m, active, svc, xfer);
-        if (nw.ok) {
-            std::uint32_t ap = static_cast<std::uint32_t>(Ap);
-            std::uint32_t bp = Bp == 0 ? 0u : static_cast<std::uint32_t>(Bp - nw.origin);
-            std::uint32_t ac = static_cast<std::uint32_t>(Ac);
-            std::uint32_t bc = Bc == 0 ? 0u : static_cast<std::uint32_t>(Bc - nw.origin);
+    const Narrow nw = narrow_check(d, m, active, svc, xfer);
+    if (nw.ok) {
+        std::uint32_t ap = static_cast<std::uint32_t>(Ap);
+        std::uint32_t bp = Bp == 0 ? 0u : static_cast<std::uint32_t>(Bp - nw.origin);
+        std::uint32_t ac = static_cast<std::uint32_t>(Ac);
+        std::uint32_t bc = Bc == 0 ? 0u : static_cast<std::uint32_t>(Bc - nw.origin);
+        if (gp.uniform && gc.uniform) {
             wave_scan32x2(ap, bp, ac, bc);
-            Ap = ap;
-            Bp = nw.origin + bp;
-            Ac = ac;
-            Bc = nw.origin + bc;
-            return;
+        } else {
+            group_scan32x2(ap, bp, gp.pred, ac, bc, gc.pred, lane);
         }
+        Ap = ap;
+        Bp = nw.origin + bp;
+        Ac = ac;
+        Bc = nw.origin + bc;
+        return;
     }
     scan_group(gp, Ap, Bp, lane);
     scan_group(gc, Ac, Bc, lane);
@@ -1501,6 +1544,17 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::s
     LinBatch q = empty_batch();
     LinBatch dq = empty_batch();  // a folded batch whose descriptors are not written yet
     std::uint64_t modeled = 0;
+    std::uint32_t lin_miss = 0;  // steps in a row that were not linear (wave-uniform)
+    // descriptors of steps replayed from their records are zeroed up to 64
+    // at a time, one lane per step: steps zbase + l for the bits l of zmask
+    std::size_t zbase = 0;
+    std::uint64_t zmask = 0;
+    const auto flush_zero = [&]() {
+        if (((zmask >> lane) & 1u) != 0) {
+            desc[zbase + lane] = StepDesc{0, 0, 0};
+        }
+        zmask = 0;
+    };
     for (std::size_t g = begin; g < end; g += kSpan) {
         pipe.promote();
         write_descs(desc, dq, lane);
@@ -1509,7 +1563,7 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::s
         }
         const std::size_t gend = g + kSpan < end ? g + kSpan : end;
         if (!kHits && a.slots == 1 && a.lead == nullptr && g + kSpan <= end &&
-            q.n <= kWave - kDepth) {
+            q.n <= kWave - kDepth && lin_miss < kLinGiveUp) {
             // a whole group of linear steps joins the batch at once
             GroupLin<kDepth> gl;
             if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
@@ -1533,8 +1587,12 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::s
                 // the tile's last step, and before any other step (order matters)
                 std::uint32_t lp, lb;
                 std::uint64_t li;
-                const bool lin = linear_detect<kRefresh>(a, fence, rcu, st, base_ps,
-                                                         s + kWave <= end, lane, lp, li, lb);
+                bool lin = false;
+                if (lin_miss < kLinGiveUp || (s / kWave) % kLinProbe == 0) {
+                    lin = linear_detect<kRefresh>(a, fence, rcu, st, base_ps, s + kWave <= end,
+                                                  lane, lp, li, lb);
+                    lin_miss = lin ? 0u : lin_miss + 1u;
+                }
                 if (lin) {
                     q.push(lp, li, lb, s);
                 }
@@ -1548,8 +1606,15 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::s
                 if (lin) {
                     continue;
                 }
-                if (desc != nullptr && lane == 0) {
-                    desc[s / kWave] = StepDesc{0, 0, 0};  // replayed from its records
+                if (desc != nullptr) {  // replayed from its records
+                    const std::size_t step = s / kWave;
+                    if (zmask != 0 && step - zbase >= static_cast<std::size_t>(kWave)) {
+                        flush_zero();
+                    }
+                    if (zmask == 0) {
+                        zbase = step;
+                    }
+                    zmask |= 1ull << (step - zbase);
                 }
             }
             uint4 x, y;
@@ -1650,6 +1715,9 @@ __global__ __launch_bounds__(64) void k_summary(KArgs a, const void* rec, std::s
         }
     }
     write_descs(desc, dq, lane);
+    if (desc != nullptr) {
+        flush_zero();
+    }
     __syncthreads();
     // Only planes the tile touched get a summary, packed in plane order; the
     // tile's mask words say which (the others are identities, and the carry
@@ -2380,15 +2448,15 @@ __device__ __forceinline__ void load_chan_carry(const KArgs& a, const std::uint6
     }
 }
 
+// Three waves per SIMD (at most 168 registers): the general steps' chains of
+// ballots, shuffles and LDS updates need the latency hiding, and the
+// streamed linear steps lose nothing.
 template <bool kRefresh, bool kHits, bool kStaged = false, bool kPacked = false>
-__global__ __launch_bounds__(64) void k_apply(KArgs a, const void* rec, std::size_t n,
-                                              std::uint64_t base_ps, const PlaneCarry* pcarry,
-                                              const MaskWord* tmask,
-                                              const std::uint64_t* ccarry,
-                                              const std::uint64_t* tile_seq,
-                                              std::uint64_t* completion, std::uint8_t* status,
-                                              DevReport* tile_rep, const std::uint8_t* hits,
-                                              const StepDesc* desc)
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_apply(
+    KArgs a, const void* rec, std::size_t n, std::uint64_t base_ps, const PlaneCarry* pcarry,
+    const MaskWord* tmask, const std::uint64_t* ccarry, const std::uint64_t* tile_seq,
+    std::uint64_t* completion, std::uint8_t* status, DevReport* tile_rep,
+    const std::uint8_t* hits, const StepDesc* desc)
 {
     extern __shared__ std::uint64_t sm[];
     std::uint64_t* fence = sm;
@@ -2441,6 +2509,7 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const void* rec, std::siz
     RangeCache rc = empty_cache();
     RangeCache rcu = empty_cache();  // wave-uniform copy for linear steps
     LinBatch q = empty_batch();
+    std::uint32_t lin_miss = 0;  // steps in a row that were not linear (wave-uniform)
     const auto fold = [&]() {
         ApplySums t{n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq};
         fold_apply(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t);
@@ -2497,8 +2566,12 @@ __global__ __launch_bounds__(64) void k_apply(KArgs a, const void* rec, std::siz
                     // batched as in the summary pass
                     std::uint32_t lp, lb;
                     std::uint64_t li;
-                    const bool lin = linear_detect<kRefresh>(a, fence, rcu, sr, base_ps,
-                                                             s + kWave <= end, lane, lp, li, lb);
+                    bool lin = false;
+                    if (lin_miss < kLinGiveUp || (s / kWave) % kLinProbe == 0) {
+                        lin = linear_detect<kRefresh>(a, fence, rcu, sr, base_ps,
+                                                      s + kWave <= end, lane, lp, li, lb);
+                        lin_miss = lin ? 0u : lin_miss + 1u;
+                    }
                     if (lin) {
                         q.push(lp, li, lb, s);
                     }
