@@ -1493,7 +1493,7 @@ __device__ __forceinline__ int slot(const MaskWord* tmask, std::uint32_t words, 
 // channel the map of all its records.  Pages are stored as page + 1 in 32
 // bits (capacity / page_bytes < 2^32 is checked on the host).
 template <bool kRefresh, bool kHits, bool kPacked = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_summary(KArgs a, const void* rec, std::size_t n,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 : 1))) void k_summary(KArgs a, const void* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
                                                 MaskWord* tmask, ChanSum* csum,
                                                 std::uint64_t* tile_count,
@@ -2450,11 +2450,12 @@ __device__ __forceinline__ void load_chan_carry(const KArgs& a, const std::uint6
     }
 }
 
-// Three waves per SIMD (at most 168 registers): the general steps' chains of
-// ballots, shuffles and LDS updates need the latency hiding, and the
-// streamed linear steps lose nothing.
+// Packed records: three waves per SIMD (at most 168 registers), since the
+// general steps' chains of ballots, shuffles and LDS updates need the
+// latency hiding and the streamed linear steps lose nothing.  32-byte
+// records hold twice the bytes per step in registers and would spill.
 template <bool kRefresh, bool kHits, bool kStaged = false, bool kPacked = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_apply(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 : 1))) void k_apply(
     KArgs a, const void* rec, std::size_t n, std::uint64_t base_ps, const PlaneCarry* pcarry,
     const MaskWord* tmask, const std::uint64_t* ccarry, const std::uint64_t* tile_seq,
     std::uint64_t* completion, std::uint8_t* status, DevReport* tile_rep,
