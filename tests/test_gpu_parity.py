@@ -205,16 +205,28 @@ def test_many_ranges_two_level_search():
         p.close()
 
 
-@pytest.mark.parametrize("scheme", ["CWDP", "PDWC", "DCPW", "WPCD"])
-def test_allocation_orders(tmp_path, scheme):
+SCHEMES = ["".join(o) for o in __import__("itertools").permutations("CWDP")]
+
+
+@pytest.mark.parametrize("geometry", ["pow2", "mixed"])
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_allocation_orders(tmp_path, scheme, geometry):
+    """All 24 channel/way/die/plane orders, with two ways per channel so
+    that every axis has extent: power-of-two axes (shift and mask striping)
+    and mixed-radix ones (division striping)."""
     prof = json.loads(C0.read_text())
     prof["plane_allocation_scheme"] = scheme
-    path = tmp_path / f"c0-{scheme}.json"
+    ways = 2
+    if geometry == "mixed":
+        prof.update(channels=6, dies_per_channel=3, planes_per_die=2,
+                    capacity_bytes=6 * 3 * 2 * 3 * 16384 * prof["pages_per_block"] * 64)
+        ways = 3
+    path = tmp_path / f"c0-{scheme}-{geometry}.json"
     path.write_text(json.dumps(prof))
     s = workloads.config0(n=30_000, seed=2)
-    p = parity.Pair(path, s.ranges, ways=2 if scheme == "WPCD" else 1)
+    p = parity.Pair(path, s.ranges, ways=ways)
     try:
-        check(p, s.records, scheme)
+        check(p, s.records, f"{scheme} {geometry}")
         p.check_state()
     finally:
         p.close()
