@@ -35,6 +35,13 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kCellsPerThread = 8;
 constexpr std::uint32_t kMaxRegion = kThreads * kCellsPerThread;
+// Wide workgroups for big uncoupled grids: 512 threads stage regions of up
+// to 4,096 cells (65.5 KB of LDS for the two sweep buffers, two workgroups
+// per CU), so that a tile's halo re-reads fewer cells per owned cell (14 x 14
+// interiors in 22 x 22 regions at 8 layers: 2.5x, against 4x for 8 x 8
+// interiors in 16 x 16 regions).
+constexpr int kWideBlock = 512;
+constexpr std::uint32_t kMaxWideRegion = kWideBlock * kCellsPerThread;
 constexpr std::uint32_t kAfBins = 4096;
 constexpr double kAfT0 = 200.0;
 constexpr double kAfStepsPerK = 16.0;
@@ -52,6 +59,7 @@ struct TArgs {
     std::uint32_t nx, ny, nz, sweeps;
     std::uint32_t tx, ty, rx, ry;  // tile interior and staged region
     std::uint32_t tiles_x;
+    std::uint32_t block;           // threads per workgroup (kThreads or kWideBlock)
     std::uint32_t cells;           // rx * ry * nz
     std::uint32_t step_x, step_y, step_z;  // 256 in the region's mixed radix
     double cdt, gx, gy, gz, gb, tb;
@@ -95,8 +103,8 @@ enum : std::uint32_t {
     kZm = 1u << 9, kZp = 1u << 10, kTop = 1u << 11, kInterior = 1u << 12
 };
 
-template <bool kCoupled, int kCells>
-__global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const double* tin,
+template <bool kCoupled, int kCells, int kBlock = kThreads>
+__global__ __launch_bounds__(kBlock) void k_thermal_window(TArgs a, const double* tin,
                                                              double* tout, std::uint64_t w)
 {
     // LDS: cur[cells + 1] and nxt[cells + 1]; slot `cells` of both holds
@@ -149,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
         }
 #pragma unroll
         for (int k = 0; k < kCells; ++k) {
-            const std::uint32_t c = tid + k * kThreads;
+            const std::uint32_t c = tid + k * kBlock;
             const int gxx = x0 + static_cast<int>(xi);
             const int gyy = y0 + static_cast<int>(yi);
             std::uint32_t f = 0, g = 0, d = safe_die;
@@ -196,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
     // 1b. Neighbour slots, 1 / den and the ambient term.
 #pragma unroll
     for (int k = 0; k < kCells; ++k) {
-        const std::uint32_t c = tid + k * kThreads;
+        const std::uint32_t c = tid + k * kBlock;
         const std::uint32_t xi = cx[k], yi = cy[k], zi = cz[k];
         const int gxx = x0 + static_cast<int>(xi);
         const int gyy = y0 + static_cast<int>(yi);
@@ -225,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
         // this window's retention and refresh decisions for every die (all
         // blocks; block 0 stores them)
         const double* hrow = reinterpret_cast<const double*>(a.hot + w * a.ndie);
-        for (std::uint32_t d = tid; d < a.ndie; d += kThreads) {
+        for (std::uint32_t d = tid; d < a.ndie; d += kBlock) {
             std::uint64_t age = a.age_in[d];
             if (w > 0) {
                 age = sat_add(age, a.af[af_bin(hrow[d])]);
@@ -250,7 +258,7 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
     double rhs[kCells];
 #pragma unroll
     for (int k = 0; k < kCells; ++k) {
-        const std::uint32_t c = tid + k * kThreads;
+        const std::uint32_t c = tid + k * kBlock;
         double p;
         if (kCoupled) {
             p = (a.static_w + static_cast<double>(cnt[k]) * a.pa) +
@@ -289,7 +297,7 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
         }
 #pragma unroll
         for (int k = 0; k < kCells; ++k) {
-            const std::uint32_t c = tid + k * kThreads;
+            const std::uint32_t c = tid + k * kBlock;
             if (c < cells) {
                 nxt[c] = out[k];
             }
@@ -304,7 +312,7 @@ __global__ __launch_bounds__(kThreads) void k_thermal_window(TArgs a, const doub
 #pragma unroll
     for (int k = 0; k < kCells; ++k) {
         if (fl[k] & kInterior) {
-            const double val = cur[tid + k * kThreads];
+            const double val = cur[tid + k * kBlock];
             tout[gidx[k]] = val;
             if (kCoupled) {
                 atomicMax(&s_hot[die[k] - safe_die],
@@ -324,6 +332,11 @@ template <bool kCoupled>
 void launch_window(const TArgs& a, std::uint32_t blocks, std::size_t lds, hipStream_t stream,
                    const double* tin, double* tout, std::uint64_t w)
 {
+    if (!kCoupled && a.block == kWideBlock) {  // regions of up to 8,192 cells
+        hipLaunchKernelGGL((k_thermal_window<false, kCellsPerThread, kWideBlock>), dim3(blocks),
+                           dim3(kWideBlock), lds, stream, a, tin, tout, w);
+        return;
+    }
     const std::uint32_t per = (a.cells + kThreads - 1) / kThreads;
     if (per <= 2) {
         hipLaunchKernelGGL((k_thermal_window<kCoupled, 2>), dim3(blocks), dim3(kThreads), lds,
@@ -633,6 +646,31 @@ void choose_tile(std::uint32_t nx, std::uint32_t ny, std::uint32_t nz, std::uint
     }
 }
 
+// Uncoupled steps: the largest square interior whose region fits a wide
+// workgroup (when the device gives a workgroup that much LDS) and that still
+// gives every CU a tile, if it re-reads fewer cells than choose_tile's tile;
+// else choose_tile's.  Returns the workgroup size.
+std::uint32_t choose_step_tile(const hbfsim_amd_thermal_grid& g, std::size_t lds_per_block,
+                               std::uint32_t& tx, std::uint32_t& ty)
+{
+    choose_tile(g.nx, g.ny, g.nz, g.sweeps, 16, 16, tx, ty);
+    if (tx == 0) {
+        return kThreads;
+    }
+    for (std::uint32_t t = 64; t > tx; --t) {
+        const std::uint64_t r = t + 2ull * g.sweeps;
+        const std::uint64_t cells = r * r * g.nz;
+        const std::uint64_t tiles =
+            static_cast<std::uint64_t>((g.nx + t - 1) / t) * ((g.ny + t - 1) / t);
+        if (cells <= kMaxWideRegion && 2 * (cells + 1) * sizeof(double) <= lds_per_block &&
+            tiles >= 256 && t <= g.nx && t <= g.ny) {
+            tx = ty = t;
+            return kWideBlock;
+        }
+    }
+    return kThreads;
+}
+
 std::uint64_t host_sat_add(std::uint64_t a, std::uint64_t b)
 {
     return a > ~0ull - b ? ~0ull : a + b;
@@ -688,6 +726,8 @@ struct thermal {
     hipEvent_t cev[8] = {};        // coupled-run phase boundaries
     float last_ms = 0.0f;
     float phase_ms[5] = {};        // counts, thermal chain, admission, engine, gather
+    std::size_t lds_per_block = 0;  // the device's LDS limit per workgroup
+    bool wide_ready = false;        // the wide kernel may take that much LDS
     // last coupled run
     std::uint64_t windows = 0;
     std::uint32_t ndie = 0;
@@ -715,6 +755,11 @@ int thermal_create(const hbfsim_amd_thermal_grid& g, thermal** out)
     }
     th->grid = g;
     hipError_t err = hipGetDevice(&th->device);
+    int lds_max = 0;
+    if (err == hipSuccess)
+        err = hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock,
+                                    th->device);
+    th->lds_per_block = lds_max > 0 ? static_cast<std::size_t>(lds_max) : 0;
     if (err == hipSuccess)
         err = halloc(th->d_scratch, static_cast<std::size_t>(g.nx) * g.ny * g.nz);
     for (int i = 0; i < 2 && err == hipSuccess; ++i) {
@@ -767,7 +812,8 @@ int coupled_last_ms(const thermal* th, float* ms, int max)
 
 namespace {
 
-TArgs base_args(const hbfsim_amd_thermal_grid& g, std::uint32_t tx, std::uint32_t ty)
+TArgs base_args(const hbfsim_amd_thermal_grid& g, std::uint32_t tx, std::uint32_t ty,
+                std::uint32_t block = kThreads)
 {
     TArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -781,9 +827,10 @@ TArgs base_args(const hbfsim_amd_thermal_grid& g, std::uint32_t tx, std::uint32_
     a.ry = ty + 2 * g.sweeps;
     a.tiles_x = (g.nx + tx - 1) / tx;
     a.cells = a.rx * a.ry * g.nz;
-    a.step_x = kThreads % a.rx;
-    a.step_y = (kThreads / a.rx) % a.ry;
-    a.step_z = kThreads / (a.rx * a.ry);
+    a.block = block;
+    a.step_x = block % a.rx;
+    a.step_y = (block / a.rx) % a.ry;
+    a.step_z = block / (a.rx * a.ry);
     a.cdt = g.capacity_j_per_k / g.dt_s;
     a.gx = g.gx_w_per_k;
     a.gy = g.gy_w_per_k;
@@ -816,10 +863,20 @@ int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     const auto& g = th->grid;
     std::uint32_t tx, ty;
-    choose_tile(g.nx, g.ny, g.nz, g.sweeps, 16, 16, tx, ty);
-    TArgs a = base_args(g, tx, ty);
+    const std::uint32_t block = choose_step_tile(g, th->lds_per_block, tx, ty);
+    TArgs a = base_args(g, tx, ty, block);
     a.power = d_power;
     const std::size_t lds = 2ull * (a.cells + 1) * sizeof(double);
+    if (block == kWideBlock && !th->wide_ready) {
+        if (hipFuncSetAttribute(
+                reinterpret_cast<const void*>(
+                    k_thermal_window<false, kCellsPerThread, kWideBlock>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
+            hipSuccess) {
+            return HBFSIM_CUDA_ERROR;
+        }
+        th->wide_ready = true;
+    }
     const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
     double* buf[2] = {d_temp, th->d_scratch};
     (void)hipEventRecord(th->ev[0], stream);

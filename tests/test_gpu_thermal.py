@@ -26,7 +26,11 @@ def grid_kw(**kw):
 
 @pytest.mark.parametrize("shape,sweeps,steps", [
     ((64, 64, 8), 4, 3), ((7, 5, 3), 1, 2), ((7, 5, 3), 3, 1), ((33, 17, 1), 2, 4),
-    ((1, 1, 4), 4, 2), ((40, 24, 16), 2, 1), ((130, 3, 2), 8, 1)])
+    ((1, 1, 4), 4, 2), ((40, 24, 16), 2, 1), ((130, 3, 2), 8, 1),
+    # big enough for the 1,024-thread tiles (interiors of 24-50 cells, ragged
+    # last tiles at every edge)
+    ((400, 400, 8), 4, 3), ((390, 410, 6), 3, 2), ((512, 300, 4), 8, 1),
+    ((1000, 700, 2), 1, 2)])
 def test_thermal_step_bit_exact(oracle, shape, sweeps, steps):
     import torch
     nx, ny, nz = shape
