@@ -113,6 +113,9 @@ struct KArgs {
     // warp grouping: per record, how many records back its group's request
     // was made (0: its own request); null when the run does not group
     const std::uint8_t* lead;
+    // hybrid runs: the range id of each linear step beside its descriptor
+    // (the sampler's key needs it); null otherwise
+    std::uint32_t* desc_rid;
 };
 
 // Record operations: 0 read, 1 write, and 2 refresh of media page `addr`
@@ -1151,11 +1154,12 @@ struct LinBatch {
     std::uint32_t page1;
     std::uint32_t bytes;
     std::uint64_t issue;
+    std::uint32_t rid;  // range id (kept by the apply pass, for hybrid sampling)
     std::size_t first;
     int n;
 
     __device__ __forceinline__ void push(std::uint32_t p1, std::uint64_t i0, std::uint32_t b0,
-                                         std::size_t s)
+                                         std::size_t s, std::uint32_t r = 0)
     {
         if (n == 0) {
             first = s;
@@ -1164,12 +1168,14 @@ struct LinBatch {
             page1 = p1;
             bytes = b0;
             issue = i0;
+            rid = r;
         }
         ++n;
     }
     // Appends a linear group's D steps (needs n <= 64 - D).
     template <int D>
-    __device__ __forceinline__ void push_group(const GroupLin<D>& gl, std::size_t s)
+    __device__ __forceinline__ void push_group(const GroupLin<D>& gl, std::size_t s,
+                                               std::uint32_t r = 0)
     {
         if (n == 0) {
             first = s;
@@ -1186,6 +1192,7 @@ struct LinBatch {
             page1 = p1;
             issue = i0;
             bytes = gl.bytes;
+            rid = r;
         }
         n += D;
     }
@@ -1197,6 +1204,7 @@ __device__ __forceinline__ LinBatch empty_batch()
     b.page1 = 0;
     b.bytes = 0;
     b.issue = 0;
+    b.rid = 0;
     b.first = 0;
     b.n = 0;
     return b;
@@ -1449,7 +1457,8 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
 // before issuing a group's loads: vector memory operations complete in
 // issue order, so a store placed after a group's loads would hold up the
 // wait for that group.
-__device__ __forceinline__ void write_descs(StepDesc* desc, LinBatch& dq, int lane)
+__device__ __forceinline__ void write_descs(StepDesc* desc, std::uint32_t* rid, LinBatch& dq,
+                                            int lane)
 {
     if (dq.n != 0 && desc != nullptr && lane < dq.n) {
         StepDesc sd;
@@ -1457,6 +1466,9 @@ __device__ __forceinline__ void write_descs(StepDesc* desc, LinBatch& dq, int la
         sd.bytes = dq.bytes;
         sd.issue = dq.issue;
         desc[dq.first / kWave + lane] = sd;
+        if (rid != nullptr) {
+            rid[dq.first / kWave + lane] = dq.rid;
+        }
     }
     dq.n = 0;
 }
@@ -1559,7 +1571,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     };
     for (std::size_t g = begin; g < end; g += kSpan) {
         pipe.promote();
-        write_descs(desc, dq, lane);
+        write_descs(desc, a.desc_rid, dq, lane);
         if (g + kSpan < end) {
             pipe.issue(rec, g + kSpan, end, lane);
         }
@@ -1569,7 +1581,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
             // a whole group of linear steps joins the batch at once
             GroupLin<kDepth> gl;
             if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
-                q.push_group(gl, g);
+                q.push_group(gl, g, rcu.id);
                 if (q.n == kWave || gend >= end) {
                     fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
@@ -1596,12 +1608,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                     lin_miss = lin ? 0u : lin_miss + 1u;
                 }
                 if (lin) {
-                    q.push(lp, li, lb, s);
+                    q.push(lp, li, lb, s, rcu.id);
                 }
                 if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= end)) {
                     fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
-                    write_descs(desc, dq, lane);  // at most one batch waits
+                    write_descs(desc, a.desc_rid, dq, lane);  // at most one batch waits
                     dq = q;
                     q.n = 0;
                 }
@@ -1716,7 +1728,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
             }
         }
     }
-    write_descs(desc, dq, lane);
+    write_descs(desc, a.desc_rid, dq, lane);
     if (desc != nullptr) {
         flush_zero();
     }
@@ -2186,7 +2198,7 @@ __device__ __forceinline__ std::uint64_t wave_max(std::uint64_t v)
 //          contention); lanes 1..63: lead with contention, else issue;
 //   channel lane j: top - x (63 - j), top = max(busy, issue) + 64 x.
 struct ApplySums {
-    std::uint64_t n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq;
+    std::uint64_t n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq, n_hyb;
 };
 
 __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* xp,
@@ -2246,6 +2258,7 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
     const std::uint64_t sx = wave_sum(v.x);                        // lanes 1..63: service x
     const std::uint64_t s0 = wave_sum(m ? umax64(ls, v.x) : 0ull);  // lane 0: max(sense, x)
     t.svc_sum += lane == 0 ? s0 : sx;
+    const std::uint64_t seq0 = t.seq;  // sequence number of the batch's first record
     t.seq += 64 * nq;
     // Per-step totals of the 64 records, in closed form (lane k: step k).
     // Record j completes at done_j = max(pd_j, top - x (63 - j)), with pd_0 =
@@ -2341,22 +2354,51 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
         }
     }
     // Status bytes four steps at a time: 4 for a page-register hit (every
-    // record but a sensing lane 0), 0 otherwise.
-    if (status != nullptr) {
-        const bool words = (reinterpret_cast<std::uintptr_t>(status) & 3u) == 0;
+    // record but a sensing lane 0), 0 otherwise; with hybrid sampling, 8 more
+    // for each record the sampler picks (record j of step k has sequence
+    // number seq0 + 64 k + j and key (page, range, read), as in the general
+    // path).  Lane l takes records 4 (l & 15) .. + 3 of step k + (l >> 4).
+    if (status != nullptr || a.hybrid) {
+        const bool words = status != nullptr && (reinterpret_cast<std::uintptr_t>(status) & 3u) == 0;
         for (int k = 0; k < q.n; k += 4) {
             const int ks = k + (lane >> 4);
+            // every lane takes part in the shuffles
+            const std::uint32_t kp = static_cast<std::uint32_t>(
+                __shfl(static_cast<int>(q.page1), ks < q.n ? ks : 0));
+            const std::uint32_t kr = static_cast<std::uint32_t>(
+                __shfl(static_cast<int>(q.rid), ks < q.n ? ks : 0));
             if (ks < q.n) {
                 const std::uint32_t r0 = 4u * static_cast<std::uint32_t>(lane & 15);
                 const bool sense = r0 == 0 && ((hits >> ks) & 1u) == 0;
-                std::uint8_t* out = status + q.first + static_cast<std::size_t>(ks) * kWave + r0;
-                if (words) {
-                    *reinterpret_cast<std::uint32_t*>(out) = sense ? 0x04040400u : 0x04040404u;
-                } else {
-                    out[0] = sense ? 0u : 4u;
-                    out[1] = 4u;
-                    out[2] = 4u;
-                    out[3] = 4u;
+                std::uint32_t word = sense ? 0x04040400u : 0x04040404u;
+                if (a.hybrid) {
+                    const std::uint64_t key =
+                        ((static_cast<std::uint64_t>(kp) - 1) << a.page_shift) ^
+                        (static_cast<std::uint64_t>(kr) << 32);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const std::uint64_t qn =
+                            seq0 + static_cast<std::uint64_t>(ks) * kWave + r0 + u;
+                        const bool sampled =
+                            qn < a.hybrid_warmup ||
+                            (a.hybrid_threshold != 0 && mix64(qn ^ key) <= a.hybrid_threshold);
+                        if (sampled) {
+                            word |= 8u << (8 * u);
+                            ++t.n_hyb;
+                        }
+                    }
+                }
+                if (status != nullptr) {
+                    std::uint8_t* out =
+                        status + q.first + static_cast<std::size_t>(ks) * kWave + r0;
+                    if (words) {
+                        *reinterpret_cast<std::uint32_t*>(out) = word;
+                    } else {
+                        out[0] = static_cast<std::uint8_t>(word);
+                        out[1] = static_cast<std::uint8_t>(word >> 8);
+                        out[2] = static_cast<std::uint8_t>(word >> 16);
+                        out[3] = static_cast<std::uint8_t>(word >> 24);
+                    }
                 }
             }
         }
@@ -2514,8 +2556,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     LinBatch q = empty_batch();
     std::uint32_t lin_miss = 0;  // steps in a row that were not linear (wave-uniform)
     const auto fold = [&]() {
-        ApplySums t{n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq};
+        ApplySums t{n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq, n_hyb};
         fold_apply(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t);
+        n_hyb = t.n_hyb;
         n_rec = t.n_rec;
         n_mod = t.n_mod;
         n_rd = t.n_rd;
@@ -2548,6 +2591,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                 q.page1 = sd.page1;
                 q.bytes = sd.bytes;
                 q.issue = sd.issue;
+                q.rid = a.desc_rid != nullptr && lane < nst ? a.desc_rid[w0 / kWave + lane] : 0u;
                 q.first = w0;
                 q.n = nst;
                 fold();
@@ -2565,7 +2609,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                 pipe.take(sr);
                 const std::size_t i = s + lane;
                 const bool valid = i < end;
-                if (!kHits && a.slots == 1 && !a.hybrid && a.lead == nullptr) {
+                if (!kHits && a.slots == 1 && a.lead == nullptr) {
                     // batched as in the summary pass
                     std::uint32_t lp, lb;
                     std::uint64_t li;
@@ -2576,7 +2620,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                         lin_miss = lin ? 0u : lin_miss + 1u;
                     }
                     if (lin) {
-                        q.push(lp, li, lb, s);
+                        q.push(lp, li, lb, s, rcu.id);
                     }
                     if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= wend)) {
                         fold();
@@ -3103,6 +3147,7 @@ struct engine {
     std::uint64_t* d_gseq{nullptr};
     DevReport* d_tile_rep{nullptr};
     StepDesc* d_desc{nullptr};  // per-step descriptors (records / 64)
+    std::uint32_t* d_desc_rid{nullptr};  // and their range ids (hybrid runs)
     std::size_t desc_cap{0};
     hipEvent_t ev[4]{};
     float last_ms[3]{0, 0, 0};
@@ -3229,6 +3274,7 @@ void free_scratch(engine* e)
     hfree(e->d_gseq);
     hfree(e->d_tile_rep);
     hfree(e->d_desc);
+    hfree(e->d_desc_rid);
     e->desc_cap = 0;
     e->tile_cap = 0;
 }
@@ -4716,10 +4762,12 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         (reinterpret_cast<std::uintptr_t>(d_comp) & 7u) != 0) {
         return HBFSIM_INVALID_ARGUMENT;
     }
-    // packed records take the main pipeline only: one page register, no
-    // hybrid sampling, the HBF model (no refresh records: they need flags)
+    // packed records take the main pipeline only: one page register, the
+    // HBF model (no refresh records: they need flags); hybrid sampling needs
+    // the linear steps' range ids beside their descriptors, for which the
+    // run without allocation has no room
     if (packed && (e->cfg.model != HBFSIM_AMD_MODEL_HBF || e->cfg.slots != 1 ||
-                   e->cfg.hybrid != 0)) {
+                   (e->cfg.hybrid != 0 && ext_scratch != nullptr))) {
         return HBFSIM_UNSUPPORTED;
     }
     if (e->cfg.model != HBFSIM_AMD_MODEL_HBF && e->cfg.model != HBFSIM_AMD_MODEL_EMPIRICAL) {
@@ -4840,19 +4888,23 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     StepDesc* desc = nullptr;
     if (ext_scratch != nullptr) {
         desc = sc.desc;  // packed runs: one page register, no sampling
-    } else if (!k2 && a.slots == 1 && a.hybrid == 0 && !grouping) {
+    } else if (!k2 && a.slots == 1 && !grouping) {
         const std::size_t nsteps = (n + kWave - 1) / kWave;
         if (nsteps > e->desc_cap) {
             hfree(e->d_desc);
+            hfree(e->d_desc_rid);
             e->desc_cap = 0;
             const std::size_t cap = nsteps + nsteps / 8;  // headroom, as for the tiles
-            if (halloc(e->d_desc, cap) != hipSuccess) {
+            if (halloc(e->d_desc, cap) != hipSuccess || halloc(e->d_desc_rid, cap) != hipSuccess) {
                 free_group();
                 return HBFSIM_CUDA_ERROR;
             }
             e->desc_cap = cap;
         }
         desc = e->d_desc;
+        if (a.hybrid != 0) {
+            a.desc_rid = e->d_desc_rid;
+        }
     }
     const dim3 grid(static_cast<unsigned>(ntiles));
     (void)hipEventRecord(e->ev[0], stream);

@@ -310,8 +310,8 @@ int hbfsim_amd_run_device(hbfsim_context* context,
                           uint64_t base_ps, void* stream,
                           hbfsim_amd_report* report);
 /* hbfsim_amd_run_device for packed records: the same results as the
- * 32-byte records they pack.  Contexts with two page registers, hybrid
- * sampling or the empirical model return HBFSIM_UNSUPPORTED. */
+ * 32-byte records they pack.  Contexts with two page registers or the
+ * empirical model return HBFSIM_UNSUPPORTED. */
 int hbfsim_amd_run_device_packed(hbfsim_context* context,
                                  const hbf_record16* records, size_t n,
                                  uint64_t* completion_ps, uint8_t* status,
@@ -330,8 +330,8 @@ int hbfsim_amd_run_device_packed(hbfsim_context* context,
  * 13 million with 1,024 planes and 256 channels.  Returns
  * HBFSIM_UNSUPPORTED, touching nothing,
  * when the run does not fit, when the context's engine does not exist yet
- * (make one ordinary run first) or when ranges were registered or removed
- * since the last run (the range upload allocates).  Every call on a device
+ * (make one ordinary run first), when ranges were registered or removed
+ * since the last run (the range upload allocates) or in hybrid mode.  Every call on a device
  * shares that device's array: calls that overlap on one device race. */
 int hbfsim_amd_run_device_packed_noalloc(hbfsim_context* context,
                                          const hbf_record16* records, size_t n,

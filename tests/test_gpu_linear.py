@@ -97,6 +97,32 @@ def test_linear_batches_bit_exact(profile, options):
         p.close()
 
 
+@pytest.mark.parametrize("rate,warmup", [(0.02, 100), (0.0, 70_000), (1.0, 0), (0.3, 5)])
+@pytest.mark.parametrize("options", [dict(), dict(tile_records=64 * 70),
+                                     dict(plane_contention=0)])
+def test_linear_batches_hybrid(tmp_path, rate, warmup, options):
+    """Hybrid mode on streams of linear steps across several ranges: the apply
+    pass folds linear steps and samples each of their records (sequence
+    number, media page, range id), as the general path does record by record;
+    a warm-up reaching past the stream, a rate of 0 and of 1."""
+    prof = json.loads(C0.read_text())
+    prof.update(reference_sample_rate=rate, reference_warmup_requests=warmup)
+    path = tmp_path / "c0-hybrid-linear.json"
+    path.write_text(json.dumps(prof))
+    ranges = ranges_for()
+    rec = linear_stream(13, 1200, ranges)
+    p = parity.Pair(path, ranges, mode="hybrid", **options)
+    try:
+        for k in range(2):  # the second run's sequence numbers continue
+            (_, _, grep), _ = check(p, rec, f"hybrid linear {rate} {warmup} {options} run {k}")
+            assert grep["hybrid_sampled"] > 0 or (rate == 0.0 and k == 1 and warmup < 2 * len(rec))
+            rec = rec.copy()
+            rec[:, 2] += np.uint64(int(rec[-1, 2]) + 1)
+        p.check_state()
+    finally:
+        p.close()
+
+
 @pytest.mark.parametrize("n_linear", [1, 2, 63, 64, 65, 127, 128, 129, 4095, 4097])
 def test_linear_batch_lengths(n_linear):
     """Runs of exactly n linear steps, then a breaking step, a tail of fewer

@@ -6,6 +6,8 @@ and both profiles; a whole config-2 step must equal the 32-byte run of the
 same step; modes the packed path does not take are refused."""
 from __future__ import annotations
 
+import json
+
 import numpy as np
 import pytest
 
@@ -104,7 +106,31 @@ def test_packed_full_config2_step_equals_32_byte_run():
         b.close()
 
 
-@pytest.mark.parametrize("options", [dict(page_buffers=2), dict(mode="hybrid")])
+@pytest.mark.parametrize("profile", [C0, C2], ids=["c0", "c2"])
+@pytest.mark.parametrize("options", [dict(), dict(tile_records=64 * 24)])
+def test_packed_hybrid(tmp_path, profile, options):
+    """Hybrid sampling on packed records: linear steps folded in the apply
+    pass with each record sampled, general steps record by record; equal to
+    the oracle on the 32-byte records they pack, over two runs."""
+    prof = json.loads(profile.read_text())
+    prof.update(reference_sample_rate=0.05, reference_warmup_requests=300)
+    path = tmp_path / "hybrid.json"
+    path.write_text(json.dumps(prof))
+    ranges = ranges_for()
+    rec = np.concatenate([linear_stream(5, 600, ranges), contiguous_stream(6, 150, ranges)])
+    p = parity.Pair(path, ranges, mode="hybrid", **options)
+    try:
+        (_, _, g1), _ = check_packed(p, rec, f"packed hybrid {profile.name} {options}")
+        rec2 = rec.copy()
+        rec2[:, 2] += np.uint64(int(rec[-1, 2]) + 1)
+        (_, _, g2), _ = check_packed(p, rec2, f"packed hybrid second run {options}")
+        assert g1["hybrid_sampled"] > 300 and g2["hybrid_sampled"] > 0
+        p.check_state()
+    finally:
+        p.close()
+
+
+@pytest.mark.parametrize("options", [dict(page_buffers=2)])
 def test_packed_refuses_other_pipelines(options):
     import torch
     from hbfsim_amd import _native as nat

@@ -134,3 +134,22 @@ def test_noalloc_refusals_leave_the_context_alone():
         e.run_packed_noalloc(d, comp)
     finally:
         e.close()
+
+
+def test_noalloc_refuses_hybrid_mode():
+    """Hybrid sampling reads the records again in the apply pass, which the
+    run without allocation does not do: refused, while the ordinary packed
+    run samples."""
+    import torch
+    s, rec = mixed_c0(20_000, 4)
+    e = eng.Engine(str(s.profile), mode="hybrid")
+    try:
+        for base, length, perms in s.ranges:
+            e.register(base, length, perms)
+        d = pack_records(torch.from_numpy(rec.view(np.int64)).cuda())
+        comp = torch.zeros(len(rec), dtype=torch.int64, device="cuda")
+        e.run_packed(d, comp)
+        with pytest.raises(ValueError):
+            e.run_packed_noalloc(d, comp)
+    finally:
+        e.close()
