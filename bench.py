@@ -448,6 +448,83 @@ def bench_hybrid(engine, batches, args) -> dict:
                     mode="hybrid")
 
 
+def link_workload(links: int, per_link: int, seed: int = 5):
+    """Synthetic UCIe traffic: per link, `per_link` reads, each an AR request
+    (exponential gaps, mean 3 ns) and its R return 300 ns later, merged in
+    ready order.  Returns host arrays (first, ready_ns, direction)."""
+    rng = np.random.default_rng(seed)
+    gaps = rng.exponential(3.0, (links, per_link)).astype(np.uint64) + 1
+    ar = np.cumsum(gaps, axis=1, dtype=np.uint64)
+    ready = np.concatenate([ar, ar + 300], axis=1)
+    direction = np.concatenate([np.zeros_like(ar, np.uint8), np.ones_like(ar, np.uint8)], axis=1)
+    order = np.argsort(ready, axis=1, kind="stable")
+    ready = np.take_along_axis(ready, order, axis=1).reshape(-1)
+    direction = np.take_along_axis(direction, order, axis=1).reshape(-1)
+    first = np.arange(links + 1, dtype=np.uint64) * np.uint64(2 * per_link)
+    return first, ready, direction
+
+
+def bench_link(args, links: int = 1 << 15, per_link: int = 256) -> dict:
+    """The UCIe Streaming / AoU link stage (hbfsim_amd_link_run): `links`
+    independent links, each carrying `per_link` reads through the reference
+    LinkProfile defaults; one step is one run of every link to quiescence.
+    The kernel runs one link per lane, an event loop whose steps depend on
+    each other, so it is bound by load latency rather than HBM bandwidth;
+    the roofline prices its algorithmic bytes (ready 8 + direction 1 in,
+    delivery 8 out = 17 B per message) against HBM all the same."""
+    import torch
+    from hbfsim_amd import link as lk
+    first, ready, direction = link_workload(links, per_link)
+    n = len(ready)
+    t_first = torch.from_numpy(first.view(np.int64)).cuda()
+    t_ready = torch.from_numpy(ready.view(np.int64)).cuda()
+    t_dir = torch.from_numpy(direction).cuda()
+    prof = lk.link_profile()
+    stream = torch.cuda.current_stream()
+    for _ in range(max(1, args.warmup)):
+        lk.run(prof, t_first, t_ready, t_dir, stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        delivered, counters = lk.run(prof, t_first, t_ready, t_dir, stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    achieved = 17 * n / (ms / 1e3) / 1e9
+    out = {"workload": f"{links} links x {per_link} reads (AR + R each, AR gaps exp mean 3 ns, "
+                       f"R 300 ns later), reference LinkProfile defaults (16 GT/s, AR 12 / R 56 "
+                       f"granule credits, 4 accepted per direction)",
+           "value": n * args.steps / dt, "unit": "messages/s", "ms_per_step": dt / args.steps * 1e3,
+           "roofline": {"bound": "latency (priced against hbm)", "kernel": "k_link",
+                        "algorithmic": f"17 B per message x {n} messages per launch",
+                        "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                        "frac": achieved / PEAK_HBM_GBPS, "event_ms": ms},
+           "flits": int(counters[:, :, 0].sum())}
+    if not args.no_cpu:
+        sys.path.insert(0, str(ROOT / "tests"))
+        import oracle_py
+        op = oracle_py.link_profile(gt=16, ar=12, r=56, max_accepted=4)
+        budget = min(5.0, args.cpu_seconds)
+        done, k, c0 = 0, 0, time.perf_counter()
+        while time.perf_counter() - c0 < budget and k < links:
+            b, e = int(first[k]), int(first[k + 1])
+            got, _ = oracle_py.link_scenario(op, direction[b:e], ready[b:e])
+            if k < 64:
+                assert np.array_equal(got, delivered[b:e].cpu().numpy().view(np.uint64)), k
+            done += e - b
+            k += 1
+        cdt = time.perf_counter() - c0
+        out["cpu_baseline"] = {"value": done / cdt, "unit": "messages/s", "cores": 1,
+                               "kind": "port",
+                               "sample": f"the first {k} links of the same workload through the "
+                                         f"oracle's StreamingLink restatement ({cdt:.1f} s); the "
+                                         f"first 64 checked equal to the GPU's deliveries"}
+    return out
+
+
 def scalar_floor(budget_s: float) -> dict:
     """The reference's own per-access fast model (the single-tail recurrence
     of hbf_device.cu:895-910, oracle orc_fast_model_scalar) on config 0's
