@@ -152,3 +152,32 @@ def test_exit_codes(cli, tmp_path):
     blank.write_text(blank.read_text().replace("\n", "\n\n", 1))
     p = run(cli, "--profile", nominal, "--events", blank, "--mode", "fast")
     assert p.returncode == 0 and json.loads(p.stdout)["requests"]["submitted"] == 2
+
+
+def test_reference_known_answers(cli, tmp_path):
+    """Known answers of the reference's own CLI tests on the nominal profile:
+    one 32,768-byte read event over 16,384-byte pages is two page requests,
+    each max(10,000 ns first-byte latency, 32 ns transfer)
+    (tests/integration/test_trace_timing.py:14-68); three one-page misses cost
+    30,000 ns (tests/integration/test_trace_replay_timing.py:131-134)."""
+    nominal = PROFILES / "nominal.json"
+    one = tmp_path / "one.jsonl"
+    one.write_text(json.dumps({"schema_version": 1, "sequence": 1, "logical_address": 0,
+                               "bytes": 32_768, "page_bytes": 16_384,
+                               "operation": "read"}) + "\n")
+    p = run(cli, "--profile", nominal, "--events", one, "--mode", "fast")
+    assert p.returncode == 0, p.stderr
+    out = json.loads(p.stdout)
+    assert out["status"] == "PASS" and out["engine"] == "hbf-fast"
+    assert out["requests"] == {"input_expert_misses": 1, "submitted": 2, "fast": 2,
+                               "reference": 0}
+    assert out["modeled_device_service_ns"] == 20_000
+    assert out["demand_exposed_stall_ns"] == 20_000
+    assert out["emulator_dispatcher_wall_time_ns"] > 0
+    three = tmp_path / "three.jsonl"
+    write_events(three, [(e * 16_384, 16_384, 16_384, "read") for e in (0, 1, 0)])
+    p = run(cli, "--profile", nominal, "--events", three, "--mode", "fast")
+    assert p.returncode == 0, p.stderr
+    out = json.loads(p.stdout)
+    assert out["requests"]["submitted"] == 3
+    assert out["modeled_device_service_ns"] == 30_000

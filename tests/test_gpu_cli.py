@@ -51,3 +51,19 @@ def test_hybrid_mode_counts_sampled_requests(cli, tmp_path, name):  # noqa: F811
               "reference_sample_rate", "reference_warmup_requests", "scheduling_semantics"):
         assert h[k] == f[k], k
     assert list(h) == sorted(h)
+
+
+def test_hybrid_reference_known_answer(cli, tmp_path):  # noqa: F811
+    """tests/integration/test_trace_timing.py:69-77 of the reference: in hybrid
+    mode the two page requests of one event fall inside the sampler's warm-up,
+    so both are reference requests and none is fast."""
+    one = tmp_path / "one.jsonl"
+    write_events(one, [(0, 32_768, 16_384, "read")])
+    p = run(cli, "--profile", PROFILES / "nominal.json", "--events", one, "--mode", "hybrid")
+    assert p.returncode == 0, p.stderr
+    h = json.loads(p.stdout)
+    assert h["status"] == "PASS" and h["engine"] == "hbf-hybrid"
+    assert h["requests"] == {"input_expert_misses": 1, "submitted": 2, "fast": 0,
+                             "reference": 2}
+    assert h["modeled_device_service_ns"] > 0 and h["demand_exposed_stall_ns"] > 0
+    assert h["emulator_dispatcher_wall_time_ns"] > 0
