@@ -25,6 +25,7 @@
 #include <cmath>
 #include <cstring>
 #include <new>
+#include <type_traits>
 #include <vector>
 
 #pragma clang fp contract(off)
@@ -350,6 +351,284 @@ void launch_window(const TArgs& a, std::uint32_t blocks, std::size_t lds, hipStr
     } else {
         hipLaunchKernelGGL((k_thermal_window<kCoupled, 8>), dim3(blocks), dim3(kThreads), lds,
                            stream, a, tin, tout, w);
+    }
+}
+
+// ---- marching stencil for large uncoupled grids ----------------------------
+// A workgroup owns a strip of 64 x columns (one wave per z layer, lane = x
+// offset) over a segment of rows, and walks it along y.  Each row that
+// enters (level 0: T and P from memory) is swept S times on the way through:
+// at step t, level k (1..S) updates row t - 2k from level k - 1's rows
+// t - 2k - 1 .. t - 2k + 1, all of which earlier steps wrote, so one barrier
+// per step separates every writer from its readers.  Each level keeps a ring
+// of 4 rows in LDS (written at step s, read at s + 1 .. s + 3); the right-hand
+// side of a row stays in the owning thread's registers until its last sweep.
+// Halo: S columns on each side of the W = 64 - 2S written columns, and S rows
+// at each end of a segment, against S on every side of a square tile; the
+// lanes and rows next to the staged edge read a stand-in (0.0 for the lane
+// beyond the wave, a zero row before the segment) and only feed cells that
+// are not written.
+// Cells outside the grid hold 0.0 at every level, so a missing x or y
+// neighbour adds g * 0.0 = +0.0 exactly as the per-tile kernel's zero slot
+// does; a missing z neighbour is read from the cell itself with conductance
+// 0.0, which adds the same +0.0.
+constexpr int kMarchLanes = 64;
+constexpr int kMarchAhead = 4;  // rows of T and P loaded ahead of their use (= ring length)
+
+struct MArgs {
+    std::uint32_t nx, ny, nz;
+    std::uint32_t strips, seg_len, total, per_xcd;
+    double cdt, gx, gy, gz, gb, tb;
+    const double* power;
+};
+
+// Per-thread constants of the marching kernel.
+struct MCtx {
+    std::size_t col;     // this thread's cell in row 0 of its layer (x clamped into the grid)
+    std::uint32_t nx;
+    int ny, ys, ye, tload;
+    bool xin, own;
+    double cdt, gx, gy, gzm, gzp, top;
+    double rden0, rden1, rden2, rden3;
+    double* me;          // this thread's LDS slot of level 0, ring slot 0
+    const double* pzm;   // the same for the z - 1 and z + 1 neighbours (the
+    const double* pzp;   // thread itself in the bottom and top layers)
+};
+
+template <int S>
+struct MRows {
+    double pt[kMarchAhead], pp[kMarchAhead];  // T and P of rows loaded ahead
+    double rh[2 * S + 1];                     // rh[i]: right-hand side of row t - i
+    double h[S][4];                           // h[k][r & 3]: this cell's level k at row r
+};
+
+__device__ __forceinline__ bool march_enters(const MCtx& c, int r)
+{
+    return c.xin && r >= 0 && r < c.tload;
+}
+
+// Rows outside [0, tload) and lanes outside the grid load the lane's row-0
+// cell (in bounds) and use 0.0 instead.
+__device__ __forceinline__ std::size_t march_at(const MCtx& c, int r)
+{
+    return c.col + (march_enters(c, r) ? static_cast<std::size_t>(r) * c.nx : std::size_t{0});
+}
+
+// The value of the lane one below (kCtrl = wave_shr:1, 0x138) or one above
+// (wave_shl:1, 0x130) in the wave; lanes 0 and 63 get 0.0 for the missing one.
+template <int kCtrl>
+__device__ __forceinline__ double wave_shift(double v)
+{
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(b), kCtrl, 0xF, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), kCtrl, 0xF, 0xF, true);
+    return __longlong_as_double((static_cast<long long>(hi) << 32) |
+                                static_cast<long long>(static_cast<unsigned>(lo)));
+}
+
+// Step t, in ring slot J = t & 3.  kInner: rows t - 2S .. t - 2 lie in
+// 1 .. ny - 2 and row t enters, so no row checks are needed.  A thread keeps
+// its own cell's values of every level in registers: those give the y - 1
+// and y + 1 terms, and the neighbouring lanes' copies (a one-lane wave shift)
+// the x - 1 and x + 1 terms; only the z neighbours, held by other waves, are
+// read from LDS.
+template <int S, bool kInner, int J>
+__device__ __forceinline__ void march_step(const MCtx& c, MRows<S>& m, int t, const double* tin,
+                                           const double* power, double* tout)
+{
+    constexpr int kRing = 4 * kMarchLanes;
+    const bool ent = kInner ? c.xin : march_enters(c, t);
+    const double tv = ent ? m.pt[J] : 0.0, pv = ent ? m.pp[J] : 0.0;
+    // the next load into pt[J] / pp[J] is issued after row t's values are
+    // taken (the empty asm orders them), so both rows share the registers and
+    // the loop carries no copies of pending loads
+    std::size_t nxt = march_at(c, t + kMarchAhead);
+    asm volatile("" : "+v"(nxt) : "v"(tv), "v"(pv));
+    m.pt[J] = tin[nxt];
+    m.pp[J] = power[nxt];
+#pragma unroll
+    for (int i = 2 * S; i > 0; --i) {
+        m.rh[i] = m.rh[i - 1];
+    }
+    m.rh[0] = c.cdt * tv + pv;
+    m.h[0][J] = tv;
+    c.me[J * kMarchLanes] = tv;  // level 0
+#pragma unroll
+    for (int k = 1; k <= S; ++k) {
+        const int r = t - 2 * k;
+        const int qr = (J - 2 * k) & 3;
+        const double cr = m.h[k - 1][qr];
+        const int sr = (k - 1) * kRing + qr * kMarchLanes;
+        double num = m.rh[2 * k];
+        num += c.gx * wave_shift<0x138>(cr);
+        num += c.gx * wave_shift<0x130>(cr);
+        num += c.gy * m.h[k - 1][(J - 2 * k - 1) & 3];
+        num += c.gy * m.h[k - 1][(J - 2 * k + 1) & 3];
+        num += c.gzm * c.pzm[sr];
+        num += c.gzp * c.pzp[sr];
+        num += c.top;
+        double v;
+        if (kInner) {
+            v = num * c.rden3;
+        } else {
+            // (values made opaque first, so the choice stays a register select
+            // rather than a load from a chosen address of the context)
+            double d0 = c.rden0, d1 = c.rden1, d2 = c.rden2, d3 = c.rden3;
+            asm volatile("" : "+v"(d0), "+v"(d1), "+v"(d2), "+v"(d3));
+            const double rd = r > 0 ? (r + 1 < c.ny ? d3 : d1) : (r + 1 < c.ny ? d2 : d0);
+            v = (r >= 0 && r < c.ny) ? num * rd : 0.0;
+        }
+        if (k < S) {
+            m.h[k][qr] = v;
+            c.me[k * kRing + qr * kMarchLanes] = v;
+        } else if (c.own && r >= c.ys && r < c.ye) {
+            tout[c.col + static_cast<std::size_t>(r) * c.nx] = v;
+        }
+    }
+}
+
+template <int S, int J>
+__device__ __forceinline__ void march_sub(const MCtx& c, MRows<S>& m, int t, const double* tin,
+                                          const double* power, double* tout)
+{
+    if (t >= 2 * S + 1 && t < c.tload) {
+        march_step<S, true, J>(c, m, t, tin, power, tout);
+    } else {
+        march_step<S, false, J>(c, m, t, tin, power, tout);
+    }
+    __syncthreads();
+}
+
+template <int S>
+__global__ __launch_bounds__(1024) void k_thermal_march(MArgs a, const double* tin, double* tout)
+{
+    // LDS: [z][level 0..S-1][ring slot 0..3][64 lanes], read only by the
+    // layers above and below; every offset from a thread's base is a
+    // compile-time constant once steps are unrolled by 4
+    extern __shared__ double lds[];
+    constexpr int W = kMarchLanes - 2 * S;
+    constexpr int kLayer = S * 4 * kMarchLanes;
+    // consecutive workgroups go to different XCDs: give each XCD a run of
+    // neighbouring strips, so the halo columns they share hit one L2
+    const std::uint32_t b = blockIdx.x;
+    const std::uint32_t id = (b % 8u) * a.per_xcd + b / 8u;
+    if (id >= a.total) {
+        return;  // the whole workgroup
+    }
+    const int lane = static_cast<int>(threadIdx.x) & (kMarchLanes - 1);
+    const int z = static_cast<int>(threadIdx.x) / kMarchLanes;
+    const int nx = static_cast<int>(a.nx), ny = static_cast<int>(a.ny), nz = static_cast<int>(a.nz);
+    const int strip = static_cast<int>(id % a.strips);
+    MCtx c;
+    c.nx = a.nx;
+    c.ny = ny;
+    c.ys = static_cast<int>((id / a.strips) * a.seg_len);
+    c.ye = c.ys + static_cast<int>(a.seg_len) < ny ? c.ys + static_cast<int>(a.seg_len) : ny;
+    c.tload = c.ye + S < ny ? c.ye + S : ny;
+    const int x = strip * W - S + lane;
+    c.xin = x >= 0 && x < nx;
+    c.own = c.xin && lane >= S && lane < kMarchLanes - S;
+    c.cdt = a.cdt;
+    c.gx = a.gx;
+    c.gy = a.gy;
+    // 1 / den for the four y cases (bit 0: row above exists, bit 1: row
+    // below), den summed in the CPU restatement's order: x-, x+, y-, y+, z-,
+    // then z+ or the ambient link.  0.0 for lanes outside the grid, whose
+    // updates (finite num times 0.0) are then 0.0.
+    double rden[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        double den = a.cdt;
+        if (x > 0) den += a.gx;
+        if (x + 1 < nx) den += a.gx;
+        if (k & 1) den += a.gy;
+        if (k & 2) den += a.gy;
+        if (z > 0) den += a.gz;
+        if (z + 1 < nz) {
+            den += a.gz;
+        } else {
+            den += a.gb;
+        }
+        rden[k] = c.xin ? 1.0 / den : 0.0;
+    }
+    c.rden0 = rden[0];
+    c.rden1 = rden[1];
+    c.rden2 = rden[2];
+    c.rden3 = rden[3];
+    c.top = z + 1 < nz ? 0.0 : a.gb * a.tb;
+    c.gzm = z > 0 ? a.gz : 0.0;
+    c.gzp = z + 1 < nz ? a.gz : 0.0;
+    c.me = lds + z * kLayer + lane;
+    c.pzm = c.me - (z > 0 ? kLayer : 0);
+    c.pzp = c.me + (z + 1 < nz ? kLayer : 0);
+    c.col = static_cast<std::size_t>(z) * a.nx * a.ny + (c.xin ? x : 0);
+#pragma unroll
+    for (int k = 0; k < 4 * S; ++k) {
+        c.me[k * kMarchLanes] = 0.0;
+    }
+    // Rows [ys - S, ye + S) enter (those inside the grid from memory).  Steps
+    // start at a multiple of 4 at or before ys - S, so that row t sits in
+    // ring slot t & 3 = its index in the unrolled body, and run in whole
+    // rounds of 4; the extra steps only sweep rows that are not written.
+    const int t0 = (c.ys - S) & ~3;
+    const int t1 = t0 + ((c.ye + 2 * S - t0 + 3) & ~3);
+    MRows<S> m;
+#pragma unroll
+    for (int j = 0; j < kMarchAhead; ++j) {
+        m.pt[j] = tin[march_at(c, t0 + j)];
+        m.pp[j] = a.power[march_at(c, t0 + j)];
+    }
+#pragma unroll
+    for (int i = 0; i <= 2 * S; ++i) {
+        m.rh[i] = 0.0;
+    }
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            m.h[k][q] = 0.0;
+        }
+    }
+    __syncthreads();
+    for (int t = t0; t < t1; t += kMarchAhead) {
+        march_sub<S, 0>(c, m, t, tin, a.power, tout);
+        march_sub<S, 1>(c, m, t + 1, tin, a.power, tout);
+        march_sub<S, 2>(c, m, t + 2, tin, a.power, tout);
+        march_sub<S, 3>(c, m, t + 3, tin, a.power, tout);
+    }
+}
+
+template <int S>
+hipError_t launch_march_s(const MArgs& m, std::uint32_t blocks, std::uint32_t threads,
+                          std::size_t lds, hipStream_t stream, const double* tin, double* tout)
+{
+    hipLaunchKernelGGL((k_thermal_march<S>), dim3(blocks), dim3(threads), lds, stream, m, tin,
+                       tout);
+    return hipGetLastError();
+}
+
+using MarchLaunch = hipError_t (*)(const MArgs&, std::uint32_t, std::uint32_t, std::size_t,
+                                   hipStream_t, const double*, double*);
+
+const void* march_kernel(std::uint32_t s)
+{
+    switch (s) {
+    case 1: return reinterpret_cast<const void*>(k_thermal_march<1>);
+    case 2: return reinterpret_cast<const void*>(k_thermal_march<2>);
+    case 3: return reinterpret_cast<const void*>(k_thermal_march<3>);
+    case 4: return reinterpret_cast<const void*>(k_thermal_march<4>);
+    default: return nullptr;
+    }
+}
+
+MarchLaunch march_launcher(std::uint32_t s)
+{
+    switch (s) {
+    case 1: return launch_march_s<1>;
+    case 2: return launch_march_s<2>;
+    case 3: return launch_march_s<3>;
+    case 4: return launch_march_s<4>;
+    default: return nullptr;
     }
 }
 
@@ -728,6 +1007,13 @@ struct thermal {
     float phase_ms[5] = {};        // counts, thermal chain, admission, engine, gather
     std::size_t lds_per_block = 0;  // the device's LDS limit per workgroup
     bool wide_ready = false;        // the wide kernel may take that much LDS
+    int cus = 0;                    // compute units
+    // marching stencil (uncoupled steps on large grids), set up at the first step
+    bool march_checked = false;
+    bool march = false;
+    MArgs m{};
+    std::uint32_t m_blocks = 0, m_threads = 0;
+    std::size_t m_lds = 0;
     // last coupled run
     std::uint64_t windows = 0;
     std::uint32_t ndie = 0;
@@ -760,6 +1046,8 @@ int thermal_create(const hbfsim_amd_thermal_grid& g, thermal** out)
         err = hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock,
                                     th->device);
     th->lds_per_block = lds_max > 0 ? static_cast<std::size_t>(lds_max) : 0;
+    if (err == hipSuccess)
+        err = hipDeviceGetAttribute(&th->cus, hipDeviceAttributeMultiprocessorCount, th->device);
     if (err == hipSuccess)
         err = halloc(th->d_scratch, static_cast<std::size_t>(g.nx) * g.ny * g.nz);
     for (int i = 0; i < 2 && err == hipSuccess; ++i) {
@@ -846,6 +1134,64 @@ std::uint32_t tile_blocks(const TArgs& a)
     return a.tiles_x * ((a.ny + a.ty - 1) / a.ty);
 }
 
+// The marching stencil takes grids of at least kMarchMinCells cells with up
+// to 16 layers and 1..4 sweeps per step.  Segments are sized so that one
+// round of resident workgroups covers the grid (or every strip is one
+// segment when strips alone exceed a round).
+constexpr std::size_t kMarchMinCells = std::size_t{1} << 21;
+
+hipError_t setup_march(thermal* th)
+{
+    th->march_checked = true;
+    const auto& g = th->grid;
+    const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
+    const void* fn = march_kernel(g.sweeps);
+    if (fn == nullptr || g.nz > 16 || cells < kMarchMinCells || th->cus <= 0) {
+        return hipSuccess;
+    }
+    const std::uint32_t W = kMarchLanes - 2 * g.sweeps;
+    const std::uint32_t threads = kMarchLanes * g.nz;
+    const std::size_t lds = static_cast<std::size_t>(g.sweeps) * 4 * threads * sizeof(double);
+    if (lds > th->lds_per_block || g.nx < 2 * W || g.ny < 8 * g.sweeps) {
+        return hipSuccess;
+    }
+    hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         static_cast<int>(lds));
+    int per_cu = 0;
+    if (err == hipSuccess)
+        err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, static_cast<int>(threads),
+                                                           lds);
+    if (err != hipSuccess || per_cu <= 0) {
+        return err;
+    }
+    const std::uint32_t strips = (g.nx + W - 1) / W;
+    const std::uint64_t round = static_cast<std::uint64_t>(per_cu) * th->cus;
+    std::uint64_t segs = round / strips;
+    const std::uint64_t max_segs = g.ny / (8ull * g.sweeps);  // segments of >= 8 S rows
+    segs = std::max<std::uint64_t>(1, std::min(segs, max_segs));
+    const std::uint32_t seg_len = static_cast<std::uint32_t>((g.ny + segs - 1) / segs);
+    segs = (g.ny + seg_len - 1) / seg_len;
+    MArgs& m = th->m;
+    m.nx = g.nx;
+    m.ny = g.ny;
+    m.nz = g.nz;
+    m.strips = strips;
+    m.seg_len = seg_len;
+    m.total = static_cast<std::uint32_t>(strips * segs);
+    m.per_xcd = (m.total + 7) / 8;
+    m.cdt = g.capacity_j_per_k / g.dt_s;
+    m.gx = g.gx_w_per_k;
+    m.gy = g.gy_w_per_k;
+    m.gz = g.gz_w_per_k;
+    m.gb = g.top_g_w_per_k;
+    m.tb = g.ambient_k;
+    th->m_blocks = m.per_xcd * 8;
+    th->m_threads = threads;
+    th->m_lds = lds;
+    th->march = true;
+    return hipSuccess;
+}
+
 }  // namespace
 
 int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64_t steps,
@@ -862,6 +1208,9 @@ int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64
     }
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     const auto& g = th->grid;
+    if (!th->march_checked && setup_march(th) != hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
     std::uint32_t tx, ty;
     const std::uint32_t block = choose_step_tile(g, th->lds_per_block, tx, ty);
     TArgs a = base_args(g, tx, ty, block);
@@ -880,11 +1229,23 @@ int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64
     const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
     double* buf[2] = {d_temp, th->d_scratch};
     (void)hipEventRecord(th->ev[0], stream);
-    for (std::uint64_t s = 0; s < steps; ++s) {
-        launch_window<false>(a, tile_blocks(a), lds, stream, buf[s & 1], buf[(s + 1) & 1], 0ull);
+    hipError_t err = hipSuccess;
+    if (th->march) {
+        MArgs m = th->m;
+        m.power = d_power;
+        const MarchLaunch launch = march_launcher(g.sweeps);
+        for (std::uint64_t s = 0; s < steps && err == hipSuccess; ++s) {
+            err = launch(m, th->m_blocks, th->m_threads, th->m_lds, stream, buf[s & 1],
+                         buf[(s + 1) & 1]);
+        }
+    } else {
+        for (std::uint64_t s = 0; s < steps; ++s) {
+            launch_window<false>(a, tile_blocks(a), lds, stream, buf[s & 1], buf[(s + 1) & 1],
+                                 0ull);
+        }
     }
     (void)hipEventRecord(th->ev[1], stream);
-    hipError_t err = hipGetLastError();
+    if (err == hipSuccess) err = hipGetLastError();
     if (err == hipSuccess && (steps & 1)) {
         err = hipMemcpyAsync(d_temp, th->d_scratch, cells * sizeof(double),
                              hipMemcpyDeviceToDevice, stream);

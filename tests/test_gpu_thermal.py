@@ -30,7 +30,13 @@ def grid_kw(**kw):
     # big enough for the 1,024-thread tiles (interiors of 24-50 cells, ragged
     # last tiles at every edge)
     ((400, 400, 8), 4, 3), ((390, 410, 6), 3, 2), ((512, 300, 4), 8, 1),
-    ((1000, 700, 2), 1, 2)])
+    ((1000, 700, 2), 1, 2),
+    # at least 2^21 cells with 1-4 sweeps: the marching stencil (64-column
+    # strips walked along y in segments; ragged last strips and segments,
+    # 1 to 16 layers)
+    ((1030, 260, 8), 4, 3), ((2048, 128, 8), 3, 2), ((700, 3000, 1), 2, 2),
+    ((520, 260, 16), 4, 2), ((300, 1200, 6), 1, 3), ((129, 2100, 8), 4, 1),
+    ((1100, 1000, 2), 4, 2)])
 def test_thermal_step_bit_exact(oracle, shape, sweeps, steps):
     import torch
     nx, ny, nz = shape
