@@ -44,8 +44,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="c2")
-    ap.add_argument("--batches", type=int, default=6,
-                    help="distinct decode-step batches generated for config c2")
+    ap.add_argument("--batches", type=int, default=None,
+                    help="distinct decode-step batches generated for config c2 (default: one "
+                         "per warm-up and timed step, at most 12; steps beyond reuse them "
+                         "in turn)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="budget for the CPU-oracle baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -432,7 +434,7 @@ def bench_general(engine, args) -> dict:
                     "gaps mean 2 ns, 8 ch x 4 die x 2 plane, 2 distinct batches")
 
 
-def bench_hybrid(engine, batches, args) -> dict:
+def bench_hybrid(engine, batches, args, packed=None) -> dict:
     """Config 2 in hybrid mode (context mode 2): every modeled record passes
     the reference sampler (rate 1%, 1,000 warm-up requests); the apply pass
     folds linear steps and samples each of their records (the range id the
@@ -445,7 +447,8 @@ def bench_hybrid(engine, batches, args) -> dict:
     path = pathlib.Path(tempfile.mkdtemp(prefix="hbf-bench-")) / "c2-hybrid.json"
     path.write_text(json.dumps(prof))
     shape = workloads.QWEN3_30B_A3B
-    packed = [engine.pack_records(b) for b in batches]
+    if packed is None:
+        packed = [engine.pack_records(b) for b in batches]
     return sub_line(engine, path, workloads.moe_ranges(shape), packed, "packed", args,
                     "config2 with hybrid sampling (rate 0.01, warm-up 1,000), packed records",
                     mode="hybrid")
@@ -595,6 +598,8 @@ def main() -> None:
         print(json.dumps(out), flush=True)
         return
 
+    if args.batches is None:
+        args.batches = max(1, min(args.steps + args.warmup, 12))
     profile, ranges, batches, desc, host_records = build_workload(args.config, args.steps,
                                                                   args.batches)
     records = args.records
@@ -663,7 +668,8 @@ def main() -> None:
         log("general path: random stream")
         out["general"] = bench_general(engine, args)
         log("hybrid mode")
-        out["hybrid"] = bench_hybrid(engine, batches, args)
+        out["hybrid"] = bench_hybrid(engine, batches, args,
+                                     packed=timed if records == "packed" else None)
         log("ucie link")
         out["link"] = bench_link(args)
     if not args.no_cpu:
