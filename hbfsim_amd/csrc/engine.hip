@@ -110,6 +110,10 @@ struct KArgs {
     std::uint64_t media_pages;      // device capacity in pages
     std::uint32_t tile;
     std::uint32_t ext_hits;         // page-buffer hits given per record (K = 2)
+    // the per-record passes match lane keys through per-wave LDS tables (one
+    // 64-bit lane mask per plane and per channel) instead of one ballot per
+    // key bit; set where the tables cost the passes no occupancy
+    std::uint32_t match_lds;
     // warp grouping: per record, how many records back its group's request
     // was made (0: its own request); null when the run does not group
     const std::uint8_t* lead;
@@ -1219,8 +1223,31 @@ struct Group {
     bool uniform;  // every active lane has the same key (wave-uniform)
 };
 
+// Lanes whose key equals this lane's key, through a per-wave LDS table of
+// lane masks (tab[key] is 0 between calls): every lane ORs its bit into its
+// key's slot, reads the slot back, and clears it.  A wave's LDS operations
+// complete in issue order, so each read sees every lane's bit and each clear
+// follows every read.  Every lane of the wave must call it.
+__device__ __forceinline__ std::uint64_t match_lds(std::uint64_t* tab, std::uint32_t key, bool m,
+                                                   int lane)
+{
+    std::uint64_t peers = 0;
+    if (m) {
+        __hip_atomic_fetch_or(&tab[key], 1ull << lane, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (m) {
+        peers = __hip_atomic_load(&tab[key], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (m) {
+        __hip_atomic_store(&tab[key], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    return peers;
+}
+
 __device__ __forceinline__ Group group_by(std::uint32_t key, std::uint32_t bits, bool m,
-                                          std::uint64_t active, int lane)
+                                          std::uint64_t active, int lane,
+                                          std::uint64_t* tab = nullptr)
 {
     const int first = __ffsll(static_cast<long long>(active)) - 1;
     const std::uint32_t key0 = static_cast<std::uint32_t>(__shfl(static_cast<int>(key), first));
@@ -1229,6 +1256,8 @@ __device__ __forceinline__ Group group_by(std::uint32_t key, std::uint32_t bits,
     g.uniform = __ballot(m && key == key0) == active;
     if (g.uniform) {
         peers = active;
+    } else if (tab != nullptr) {
+        peers = match_lds(tab, key, m, lane);
     } else {
         peers = match_key(key, bits, active);
     }
@@ -1247,7 +1276,8 @@ __device__ __forceinline__ Group group_by(std::uint32_t key, std::uint32_t bits,
 // two ballots instead of a ballot per key bit.  Otherwise, by key.
 __device__ __forceinline__ Group group_plane_runs(const KArgs& a, std::uint32_t page1,
                                                   std::uint32_t key, bool m,
-                                                  std::uint64_t active, int lane)
+                                                  std::uint64_t active, int lane,
+                                                  std::uint64_t* tab)
 {
     const std::uint32_t prev =
         static_cast<std::uint32_t>(__shfl(static_cast<int>(page1), lane > 0 ? lane - 1 : 0));
@@ -1256,7 +1286,7 @@ __device__ __forceinline__ Group group_plane_runs(const KArgs& a, std::uint32_t 
     const std::uint32_t pl = rl32(page1, last_lane);
     const bool falls = m && lane > 0 && prev > page1;
     if (__ballot(falls) != 0 || pl - p0 >= a.Rp) {
-        return group_by(key, a.pbits, m, active, lane);
+        return group_by(key, a.pbits, m, active, lane, tab);
     }
     const bool head = m && (lane == 0 || prev != page1);
     const std::uint64_t heads = __ballot(head);
@@ -1403,14 +1433,15 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
                                              std::uint64_t* p_rA, std::uint64_t* p_rB,
                                              std::uint64_t* c_A, std::uint64_t* c_B,
                                              std::uint32_t* p_f1, std::uint32_t* p_l1,
-                                             std::uint8_t* p_fc)
+                                             std::uint8_t* p_fc, std::uint64_t* mt_p,
+                                             std::uint64_t* mt_c)
 {
     const StepView v = step_view(a, xp, q, lane);
     const bool m = v.m;
     const std::uint32_t pkey = m ? v.d.plane : 0u;
     const std::uint32_t ckey = m ? v.d.chan : 0u;
-    const Group gp = group_plane_runs(a, q.page1, pkey, m, v.active, lane);
-    const Group gc = group_by(ckey, a.cbits, m, v.active, lane);
+    const Group gp = group_plane_runs(a, q.page1, pkey, m, v.active, lane, mt_p);
+    const Group gc = group_by(ckey, a.cbits, m, v.active, lane, mt_c);
     const std::uint32_t f1 = m ? p_f1[pkey] : 0u;
     const std::uint32_t last_page = m ? p_l1[pkey] : 0u;
     const bool has = f1 != 0;
@@ -1504,6 +1535,14 @@ __device__ __forceinline__ int slot(const MaskWord* tmask, std::uint32_t words, 
 // class), the (max,+) map of the records after it, and the last page; per
 // channel the map of all its records.  Pages are stored as page + 1 in 32
 // bits (capacity / page_bytes < 2^32 is checked on the host).
+// Byte offset of the summary pass's lane-matching tables (plane table, then
+// channel table) after its state: fences, three 64-bit and two 32-bit plane
+// arrays, two 64-bit channel arrays and the plane class bytes; 8-byte aligned.
+__host__ __device__ __forceinline__ std::size_t summary_match_offset(const KArgs& a)
+{
+    return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 8ull * a.Rp + ((a.Rp + 7ull) & ~7ull);
+}
+
 template <bool kRefresh, bool kHits, bool kPacked = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 : 1))) void k_summary(KArgs a, const void* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
@@ -1521,6 +1560,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     std::uint32_t* p_f1 = reinterpret_cast<std::uint32_t*>(c_B + a.Rc);
     std::uint32_t* p_l1 = p_f1 + a.Rp;
     std::uint8_t* p_fc = reinterpret_cast<std::uint8_t*>(p_l1 + a.Rp);  // class bits < 16
+    std::uint64_t* mt_p = a.match_lds ? reinterpret_cast<std::uint64_t*>(
+                                            reinterpret_cast<unsigned char*>(sm) +
+                                            summary_match_offset(a))
+                                      : nullptr;
+    std::uint64_t* mt_c = a.match_lds ? mt_p + a.Rp : nullptr;
     __shared__ std::uint64_t xp[33];
     const int lane = threadIdx.x;
     const std::size_t tile = blockIdx.x;
@@ -1551,6 +1595,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     for (std::uint32_t r = lane; r < a.Rc; r += kWave) {
         c_A[r] = 0;
         c_B[r] = 0;
+    }
+    if (a.match_lds) {
+        for (std::uint32_t r = lane; r < a.Rp + a.Rc; r += kWave) {
+            mt_p[r] = 0;
+        }
     }
     __syncthreads();
     RangeCache rc = empty_cache();
@@ -1583,7 +1632,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
             if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
                 q.push_group(gl, g, rcu.id);
                 if (q.n == kWave || gend >= end) {
-                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc);
+                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc, mt_p, mt_c);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
                     dq = q;
                     q.n = 0;
@@ -1611,7 +1660,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                     q.push(lp, li, lb, s, rcu.id);
                 }
                 if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= end)) {
-                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc);
+                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc, mt_p, mt_c);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
                     write_descs(desc, a.desc_rid, dq, lane);  // at most one batch waits
                     dq = q;
@@ -1679,8 +1728,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
             const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
             const std::uint32_t pkey = m ? d.plane : 0u;
             const std::uint32_t ckey = m ? d.chan : 0u;
-            const Group gp = group_by(pkey, a.pbits, m, active, lane);
-            const Group gc = group_by(ckey, a.cbits, m, active, lane);
+            const Group gp = group_by(pkey, a.pbits, m, active, lane, mt_p);
+            const Group gc = group_by(ckey, a.cbits, m, active, lane, mt_c);
             // state reads come before this step's writes
             const std::uint32_t f1 = m ? p_f1[pkey] : 0u;
             const std::uint32_t last_page = m ? p_l1[pkey] : 0u;
@@ -2205,14 +2254,15 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
                                            const LinBatch& q, int lane, std::uint64_t* p_busy,
                                            std::uint64_t* c_busy, std::uint32_t* p_tag,
                                            std::uint64_t* completion, std::uint8_t* status,
-                                           ApplySums& t)
+                                           ApplySums& t, std::uint64_t* mt_p,
+                                           std::uint64_t* mt_c)
 {
     const StepView v = step_view(a, xp, q, lane);
     const bool m = v.m;
     const std::uint32_t pkey = m ? v.d.plane : 0u;
     const std::uint32_t ckey = m ? v.d.chan : 0u;
-    const Group gp = group_plane_runs(a, q.page1, pkey, m, v.active, lane);
-    const Group gc = group_by(ckey, a.cbits, m, v.active, lane);
+    const Group gp = group_plane_runs(a, q.page1, pkey, m, v.active, lane, mt_p);
+    const Group gc = group_by(ckey, a.cbits, m, v.active, lane, mt_c);
     const std::uint32_t tag = m ? p_tag[pkey] : 0u;
     const std::uint64_t pbusy = m ? p_busy[pkey] : 0ull;
     const std::uint64_t cbusy = m ? c_busy[ckey] : 0ull;
@@ -2423,6 +2473,13 @@ __host__ __device__ __forceinline__ std::size_t apply_desc_offset(const KArgs& a
     return (8ull * (a.r_nfence + a.Rp + a.Rc) + 4ull * a.Rp + 15ull) & ~15ull;
 }
 
+// Byte offset of the apply pass's lane-matching tables (plane table, then
+// channel table) after its state; 16-byte aligned.
+__host__ __device__ __forceinline__ std::size_t apply_match_offset(const KArgs& a)
+{
+    return apply_desc_offset(a) + 16ull * staged_steps(a);
+}
+
 // A tile's plane carry-ins are packed like its summaries: word w of the
 // mask covers planes [64 w, 64 w + 64), so lane l reads bit l of each word.
 // Eight words' carries are in flight before any is written.
@@ -2520,6 +2577,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     constexpr bool stage = kStaged;
     StepDesc* sdesc = reinterpret_cast<StepDesc*>(reinterpret_cast<unsigned char*>(sm) +
                                                   apply_desc_offset(a));
+    std::uint64_t* mt_p = a.match_lds ? reinterpret_cast<std::uint64_t*>(
+                                            reinterpret_cast<unsigned char*>(sm) +
+                                            apply_match_offset(a))
+                                      : nullptr;
+    std::uint64_t* mt_c = a.match_lds ? mt_p + a.Rp : nullptr;
     const std::size_t tsteps = (end - begin + kWave - 1) / kWave;
     const FenceRegs fr = fetch_fences(a, lane);
     const std::uint64_t xv = fetch_xfer(a, lane);
@@ -2537,6 +2599,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     load_chan_carry(a, ccarry, tile, c_busy, lane);
     store_fences(a, fr, fence, lane);
     store_xfer(xp, xv, lane);
+    if (a.match_lds) {
+        for (std::uint32_t r = lane; r < a.Rp + a.Rc; r += kWave) {
+            mt_p[r] = 0;
+        }
+    }
     if (stage) {
 #pragma unroll
         for (int k = 0; k < kDescPerLane; ++k) {
@@ -2557,7 +2624,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     std::uint32_t lin_miss = 0;  // steps in a row that were not linear (wave-uniform)
     const auto fold = [&]() {
         ApplySums t{n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq, n_hyb};
-        fold_apply(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t);
+        fold_apply(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t, mt_p, mt_c);
         n_hyb = t.n_hyb;
         n_rec = t.n_rec;
         n_mod = t.n_mod;
@@ -2700,8 +2767,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                     const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
                     const std::uint32_t pkey = m ? d.plane : 0u;
                     const std::uint32_t ckey = m ? d.chan : 0u;
-                    const Group gp = group_by(pkey, a.pbits, m, active, lane);
-                    const Group gc = group_by(ckey, a.cbits, m, active, lane);
+                    const Group gp = group_by(pkey, a.pbits, m, active, lane, mt_p);
+                    const Group gc = group_by(ckey, a.cbits, m, active, lane, mt_c);
                     // state reads come before this step's writes
                     const std::uint32_t tag = m ? p_tag[pkey] : 0u;
                     const std::uint64_t pbusy = m ? p_busy[pkey] : 0ull;
@@ -4110,12 +4177,31 @@ __global__ __launch_bounds__(64) void k_k2_hits(KArgs a, const hbf_record32* rec
 
 std::size_t lds_summary(const KArgs& a)
 {
-    return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 8ull * a.Rp + ((a.Rp + 7ull) & ~7ull);
+    return summary_match_offset(a) + (a.match_lds ? 8ull * (a.Rp + a.Rc) : 0ull);
 }
 
 std::size_t lds_apply(const KArgs& a)
 {
-    return apply_desc_offset(a) + 16ull * staged_steps(a);
+    return apply_match_offset(a) + (a.match_lds ? 8ull * (a.Rp + a.Rc) : 0ull);
+}
+
+// The lane-matching tables go where they cost neither per-record pass any
+// waves per CU (gfx950: 160 KB of LDS per CU; both passes run at most three
+// waves per SIMD).
+void choose_match(KArgs& a)
+{
+    constexpr std::size_t kLdsPerCu = 160 * 1024;
+    constexpr std::size_t kMaxWaves = 12;
+    const auto waves = [&](std::size_t bytes) {
+        const std::size_t w = bytes == 0 ? kMaxWaves : kLdsPerCu / bytes;
+        return w < kMaxWaves ? w : kMaxWaves;
+    };
+    a.match_lds = 0;
+    const std::size_t s0 = lds_summary(a), p0 = lds_apply(a);
+    a.match_lds = 1;
+    if (waves(lds_summary(a)) < waves(s0) || waves(lds_apply(a)) < waves(p0)) {
+        a.match_lds = 0;
+    }
 }
 
 // Records per tile when the configuration leaves it open: the largest power
@@ -4826,6 +4912,7 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                         e->d_tcount, e->d_tseq, e->d_gpsum, e->d_gcsum, e->d_gpcarry,
                         e->d_gccarry, e->d_gcount, e->d_gseq, e->d_tile_rep, nullptr};
     }
+    choose_match(a);
     const std::size_t lds_a = lds_summary(a), lds_c = lds_apply(a);
     if (lds_a > 65536 || lds_c > 65536) {
         return HBFSIM_UNSUPPORTED;
