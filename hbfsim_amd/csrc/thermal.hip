@@ -33,16 +33,21 @@
 namespace hbfamd {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;  // workgroups of the admission-gate and gather kernels
 constexpr int kCellsPerThread = 8;
-constexpr std::uint32_t kMaxRegion = kThreads * kCellsPerThread;
-// Wide workgroups for big uncoupled grids: 512 threads stage regions of up
-// to 4,096 cells (65.5 KB of LDS for the two sweep buffers, two workgroups
-// per CU), so that a tile's halo re-reads fewer cells per owned cell (14 x 14
-// interiors in 22 x 22 regions at 8 layers: 2.5x, against 4x for 8 x 8
-// interiors in 16 x 16 regions).
-constexpr int kWideBlock = 512;
-constexpr std::uint32_t kMaxWideRegion = kWideBlock * kCellsPerThread;
+// Staged tile regions: up to kMaxRegion cells, or kMaxWideRegion for the
+// wide tiles of big uncoupled grids (65.5 KB of LDS for the two sweep
+// buffers, two workgroups per CU), whose halo re-reads fewer cells per owned
+// cell (14 x 14 interiors in 22 x 22 regions at 8 layers: 2.5x, against 4x
+// for 8 x 8 interiors in 16 x 16 regions).
+constexpr std::uint32_t kMaxRegion = 2048;
+constexpr std::uint32_t kMaxWideRegion = 4096;
+// Tiles are swept by 512-thread workgroups: 2-4 cells per thread, 8 for wide
+// regions.  Against 256 threads with up to 8 cells each, the extra waves
+// hide the sweeps' LDS latency (the coupled 64 x 64 x 8 grid: 8.2 -> 6.6 us
+// per window).
+constexpr int kTileBlock = 512;
+static_assert(kMaxWideRegion == kTileBlock * kCellsPerThread, "wide region");
 constexpr std::uint32_t kAfBins = 4096;
 constexpr double kAfT0 = 200.0;
 constexpr double kAfStepsPerK = 16.0;
@@ -60,7 +65,7 @@ struct TArgs {
     std::uint32_t nx, ny, nz, sweeps;
     std::uint32_t tx, ty, rx, ry;  // tile interior and staged region
     std::uint32_t tiles_x;
-    std::uint32_t block;           // threads per workgroup (kThreads or kWideBlock)
+    std::uint32_t block;           // threads per workgroup (kTileBlock)
     std::uint32_t cells;           // rx * ry * nz
     std::uint32_t step_x, step_y, step_z;  // 256 in the region's mixed radix
     double cdt, gx, gy, gz, gb, tb;
@@ -104,7 +109,7 @@ enum : std::uint32_t {
     kZm = 1u << 9, kZp = 1u << 10, kTop = 1u << 11, kInterior = 1u << 12
 };
 
-template <bool kCoupled, int kCells, int kBlock = kThreads>
+template <bool kCoupled, int kCells, int kBlock = kTileBlock>
 __global__ __launch_bounds__(kBlock) void k_thermal_window(TArgs a, const double* tin,
                                                              double* tout, std::uint64_t w)
 {
@@ -329,28 +334,24 @@ __global__ __launch_bounds__(kBlock) void k_thermal_window(TArgs a, const double
     }
 }
 
+// Every tile launch uses kTileBlock threads (TArgs built with that block).
 template <bool kCoupled>
 void launch_window(const TArgs& a, std::uint32_t blocks, std::size_t lds, hipStream_t stream,
                    const double* tin, double* tout, std::uint64_t w)
 {
-    if (!kCoupled && a.block == kWideBlock) {  // regions of up to 8,192 cells
-        hipLaunchKernelGGL((k_thermal_window<false, kCellsPerThread, kWideBlock>), dim3(blocks),
-                           dim3(kWideBlock), lds, stream, a, tin, tout, w);
-        return;
-    }
-    const std::uint32_t per = (a.cells + kThreads - 1) / kThreads;
-    if (per <= 2) {
-        hipLaunchKernelGGL((k_thermal_window<kCoupled, 2>), dim3(blocks), dim3(kThreads), lds,
-                           stream, a, tin, tout, w);
-    } else if (per <= 4) {
-        hipLaunchKernelGGL((k_thermal_window<kCoupled, 4>), dim3(blocks), dim3(kThreads), lds,
-                           stream, a, tin, tout, w);
-    } else if (per <= 5) {
-        hipLaunchKernelGGL((k_thermal_window<kCoupled, 5>), dim3(blocks), dim3(kThreads), lds,
-                           stream, a, tin, tout, w);
+    const std::uint32_t per = (a.cells + kTileBlock - 1) / kTileBlock;
+    if (!kCoupled && per > 4) {  // wide regions of up to kMaxWideRegion cells
+        hipLaunchKernelGGL((k_thermal_window<false, kCellsPerThread, kTileBlock>), dim3(blocks),
+                           dim3(kTileBlock), lds, stream, a, tin, tout, w);
+    } else if (per <= 2) {
+        hipLaunchKernelGGL((k_thermal_window<kCoupled, 2, kTileBlock>), dim3(blocks),
+                           dim3(kTileBlock), lds, stream, a, tin, tout, w);
+    } else if (per <= 3) {
+        hipLaunchKernelGGL((k_thermal_window<kCoupled, 3, kTileBlock>), dim3(blocks),
+                           dim3(kTileBlock), lds, stream, a, tin, tout, w);
     } else {
-        hipLaunchKernelGGL((k_thermal_window<kCoupled, 8>), dim3(blocks), dim3(kThreads), lds,
-                           stream, a, tin, tout, w);
+        hipLaunchKernelGGL((k_thermal_window<kCoupled, 4, kTileBlock>), dim3(blocks),
+                           dim3(kTileBlock), lds, stream, a, tin, tout, w);
     }
 }
 
@@ -928,13 +929,13 @@ void choose_tile(std::uint32_t nx, std::uint32_t ny, std::uint32_t nz, std::uint
 // Uncoupled steps: the largest square interior whose region fits a wide
 // workgroup (when the device gives a workgroup that much LDS) and that still
 // gives every CU a tile, if it re-reads fewer cells than choose_tile's tile;
-// else choose_tile's.  Returns the workgroup size.
-std::uint32_t choose_step_tile(const hbfsim_amd_thermal_grid& g, std::size_t lds_per_block,
-                               std::uint32_t& tx, std::uint32_t& ty)
+// else choose_tile's.  Returns whether the tile is a wide one.
+bool choose_step_tile(const hbfsim_amd_thermal_grid& g, std::size_t lds_per_block,
+                      std::uint32_t& tx, std::uint32_t& ty)
 {
     choose_tile(g.nx, g.ny, g.nz, g.sweeps, 16, 16, tx, ty);
     if (tx == 0) {
-        return kThreads;
+        return false;
     }
     for (std::uint32_t t = 64; t > tx; --t) {
         const std::uint64_t r = t + 2ull * g.sweeps;
@@ -944,10 +945,10 @@ std::uint32_t choose_step_tile(const hbfsim_amd_thermal_grid& g, std::size_t lds
         if (cells <= kMaxWideRegion && 2 * (cells + 1) * sizeof(double) <= lds_per_block &&
             tiles >= 256 && t <= g.nx && t <= g.ny) {
             tx = ty = t;
-            return kWideBlock;
+            return true;
         }
     }
-    return kThreads;
+    return false;
 }
 
 std::uint64_t host_sat_add(std::uint64_t a, std::uint64_t b)
@@ -1101,7 +1102,7 @@ int coupled_last_ms(const thermal* th, float* ms, int max)
 namespace {
 
 TArgs base_args(const hbfsim_amd_thermal_grid& g, std::uint32_t tx, std::uint32_t ty,
-                std::uint32_t block = kThreads)
+                std::uint32_t block = kTileBlock)
 {
     TArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -1212,14 +1213,14 @@ int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64
         return HBFSIM_CUDA_ERROR;
     }
     std::uint32_t tx, ty;
-    const std::uint32_t block = choose_step_tile(g, th->lds_per_block, tx, ty);
-    TArgs a = base_args(g, tx, ty, block);
+    const bool wide = choose_step_tile(g, th->lds_per_block, tx, ty);
+    TArgs a = base_args(g, tx, ty, kTileBlock);
     a.power = d_power;
     const std::size_t lds = 2ull * (a.cells + 1) * sizeof(double);
-    if (block == kWideBlock && !th->wide_ready) {
+    if (wide && !th->wide_ready) {
         if (hipFuncSetAttribute(
                 reinterpret_cast<const void*>(
-                    k_thermal_window<false, kCellsPerThread, kWideBlock>),
+                    k_thermal_window<false, kCellsPerThread, kTileBlock>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
             hipSuccess) {
             return HBFSIM_CUDA_ERROR;
@@ -1368,7 +1369,7 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     err = hipMemcpyAsync(d_af, table.data(), kAfBins * 8, hipMemcpyHostToDevice, stream);
     if (err == hipSuccess)
         err = hipMemcpyAsync(d_age, age, ndie * 8ull, hipMemcpyHostToDevice, stream);
-    TArgs a = base_args(g, tx, ty);
+    TArgs a = base_args(g, tx, ty, kTileBlock);
     a.coupled = 1;
     a.ndie = ndie;
     a.regions_x = o.regions_x;
