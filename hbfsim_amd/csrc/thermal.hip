@@ -500,8 +500,16 @@ __device__ __forceinline__ void march_sub(const MCtx& c, MRows<S>& m, int t, con
     __syncthreads();
 }
 
+// Threads per workgroup the marching kernel is built for: up to 16 layers
+// with 1-4 sweeps, up to 8 with 5-8 (whose registers exceed 128 per lane).
+__host__ __device__ constexpr int march_max_threads(int s)
+{
+    return s <= 4 ? 16 * kMarchLanes : 8 * kMarchLanes;
+}
+
 template <int S>
-__global__ __launch_bounds__(1024) void k_thermal_march(MArgs a, const double* tin, double* tout)
+__global__ __launch_bounds__(march_max_threads(S)) void k_thermal_march(MArgs a, const double* tin,
+                                                                        double* tout)
 {
     // LDS: [z][level 0..S-1][ring slot 0..3][64 lanes], read only by the
     // layers above and below; every offset from a thread's base is a
@@ -618,6 +626,10 @@ const void* march_kernel(std::uint32_t s)
     case 2: return reinterpret_cast<const void*>(k_thermal_march<2>);
     case 3: return reinterpret_cast<const void*>(k_thermal_march<3>);
     case 4: return reinterpret_cast<const void*>(k_thermal_march<4>);
+    case 5: return reinterpret_cast<const void*>(k_thermal_march<5>);
+    case 6: return reinterpret_cast<const void*>(k_thermal_march<6>);
+    case 7: return reinterpret_cast<const void*>(k_thermal_march<7>);
+    case 8: return reinterpret_cast<const void*>(k_thermal_march<8>);
     default: return nullptr;
     }
 }
@@ -629,8 +641,36 @@ MarchLaunch march_launcher(std::uint32_t s)
     case 2: return launch_march_s<2>;
     case 3: return launch_march_s<3>;
     case 4: return launch_march_s<4>;
+    case 5: return launch_march_s<5>;
+    case 6: return launch_march_s<6>;
+    case 7: return launch_march_s<7>;
+    case 8: return launch_march_s<8>;
     default: return nullptr;
     }
+}
+
+// The marching stencil takes grids of at least kMarchMinCells cells with up
+// to 16 layers at 1-4 sweeps per step, up to 8 layers at 5-8 sweeps, at
+// least two strips wide and eight rows per sweep long, whose rings fit the
+// workgroup's LDS limit.  Returns the LDS bytes, 0 when it does not apply.
+constexpr std::size_t kMarchMinCells = std::size_t{1} << 21;
+
+std::size_t march_lds(const hbfsim_amd_thermal_grid& g, std::size_t lds_limit)
+{
+    const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
+    if (march_kernel(g.sweeps) == nullptr || g.nz > 16 || cells < kMarchMinCells) {
+        return 0;
+    }
+    const std::uint32_t W = kMarchLanes - 2 * g.sweeps;
+    const std::uint32_t threads = kMarchLanes * g.nz;
+    if (threads > static_cast<std::uint32_t>(march_max_threads(static_cast<int>(g.sweeps)))) {
+        return 0;
+    }
+    const std::size_t lds = static_cast<std::size_t>(g.sweeps) * 4 * threads * sizeof(double);
+    if (lds > lds_limit || g.nx < 2 * W || g.ny < 8 * g.sweeps) {
+        return 0;
+    }
+    return lds;
 }
 
 // Row 0 of the hotspot trace: every die's hottest cell of the initial grid.
@@ -1031,9 +1071,17 @@ int thermal_create(const hbfsim_amd_thermal_grid& g, thermal** out)
         !std::isfinite(g.ambient_k)) {
         return HBFSIM_INVALID_ARGUMENT;
     }
+    int device = 0, lds_max = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=
+            hipSuccess) {
+        return HBFSIM_CUDA_ERROR;
+    }
+    const std::size_t lds_limit = lds_max > 0 ? static_cast<std::size_t>(lds_max) : 0;
+    // steps take LDS tiles or, on large grids, the marching kernel
     std::uint32_t tx, ty;
     choose_tile(g.nx, g.ny, g.nz, g.sweeps, 16, 16, tx, ty);
-    if (tx == 0) {
+    if (tx == 0 && march_lds(g, lds_limit) == 0) {
         return HBFSIM_UNSUPPORTED;
     }
     auto* th = new (std::nothrow) thermal;
@@ -1041,12 +1089,9 @@ int thermal_create(const hbfsim_amd_thermal_grid& g, thermal** out)
         return HBFSIM_IO_ERROR;
     }
     th->grid = g;
-    hipError_t err = hipGetDevice(&th->device);
-    int lds_max = 0;
-    if (err == hipSuccess)
-        err = hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock,
-                                    th->device);
-    th->lds_per_block = lds_max > 0 ? static_cast<std::size_t>(lds_max) : 0;
+    th->device = device;
+    th->lds_per_block = lds_limit;
+    hipError_t err = hipSuccess;
     if (err == hipSuccess)
         err = hipDeviceGetAttribute(&th->cus, hipDeviceAttributeMultiprocessorCount, th->device);
     if (err == hipSuccess)
@@ -1135,27 +1180,20 @@ std::uint32_t tile_blocks(const TArgs& a)
     return a.tiles_x * ((a.ny + a.ty - 1) / a.ty);
 }
 
-// The marching stencil takes grids of at least kMarchMinCells cells with up
-// to 16 layers and 1..4 sweeps per step.  Segments are sized so that one
-// round of resident workgroups covers the grid (or every strip is one
-// segment when strips alone exceed a round).
-constexpr std::size_t kMarchMinCells = std::size_t{1} << 21;
+// Segments are sized so that one round of resident workgroups covers the
+// grid (or every strip is one segment when strips alone exceed a round).
 
 hipError_t setup_march(thermal* th)
 {
     th->march_checked = true;
     const auto& g = th->grid;
-    const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
-    const void* fn = march_kernel(g.sweeps);
-    if (fn == nullptr || g.nz > 16 || cells < kMarchMinCells || th->cus <= 0) {
+    const std::size_t lds = march_lds(g, th->lds_per_block);
+    if (lds == 0 || th->cus <= 0) {
         return hipSuccess;
     }
+    const void* fn = march_kernel(g.sweeps);
     const std::uint32_t W = kMarchLanes - 2 * g.sweeps;
     const std::uint32_t threads = kMarchLanes * g.nz;
-    const std::size_t lds = static_cast<std::size_t>(g.sweeps) * 4 * threads * sizeof(double);
-    if (lds > th->lds_per_block || g.nx < 2 * W || g.ny < 8 * g.sweeps) {
-        return hipSuccess;
-    }
     hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                          static_cast<int>(lds));
     int per_cu = 0;
@@ -1212,20 +1250,27 @@ int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64
     if (!th->march_checked && setup_march(th) != hipSuccess) {
         return HBFSIM_CUDA_ERROR;
     }
-    std::uint32_t tx, ty;
-    const bool wide = choose_step_tile(g, th->lds_per_block, tx, ty);
-    TArgs a = base_args(g, tx, ty, kTileBlock);
-    a.power = d_power;
-    const std::size_t lds = 2ull * (a.cells + 1) * sizeof(double);
-    if (wide && !th->wide_ready) {
-        if (hipFuncSetAttribute(
-                reinterpret_cast<const void*>(
-                    k_thermal_window<false, kCellsPerThread, kTileBlock>),
-                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
-            hipSuccess) {
-            return HBFSIM_CUDA_ERROR;
+    TArgs a{};
+    std::size_t lds = 0;
+    if (!th->march) {
+        std::uint32_t tx, ty;
+        const bool wide = choose_step_tile(g, th->lds_per_block, tx, ty);
+        if (tx == 0) {
+            return HBFSIM_UNSUPPORTED;  // no tile fits and the marching kernel does not apply
         }
-        th->wide_ready = true;
+        a = base_args(g, tx, ty, kTileBlock);
+        a.power = d_power;
+        lds = 2ull * (a.cells + 1) * sizeof(double);
+        if (wide && !th->wide_ready) {
+            if (hipFuncSetAttribute(
+                    reinterpret_cast<const void*>(
+                        k_thermal_window<false, kCellsPerThread, kTileBlock>),
+                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) !=
+                hipSuccess) {
+                return HBFSIM_CUDA_ERROR;
+            }
+            th->wide_ready = true;
+        }
     }
     const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
     double* buf[2] = {d_temp, th->d_scratch};

@@ -36,7 +36,10 @@ def grid_kw(**kw):
     # 1 to 16 layers)
     ((1030, 260, 8), 4, 3), ((2048, 128, 8), 3, 2), ((700, 3000, 1), 2, 2),
     ((520, 260, 16), 4, 2), ((300, 1200, 6), 1, 3), ((129, 2100, 8), 4, 1),
-    ((1100, 1000, 2), 4, 2)])
+    ((1100, 1000, 2), 4, 2),
+    # 5-8 sweeps march with up to 8 layers (48-54 written columns per strip)
+    ((600, 900, 4), 5, 1), ((700, 3000, 1), 6, 2), ((520, 520, 8), 7, 1),
+    ((1030, 260, 8), 8, 2)])
 def test_thermal_step_bit_exact(oracle, shape, sweeps, steps):
     import torch
     nx, ny, nz = shape
@@ -245,3 +248,7 @@ def test_thermal_rejects_bad_shapes():
         eng.Thermal(**grid_kw(sweeps=9))
     with pytest.raises(eng.nat.HbfSimError):
         eng.Thermal(**grid_kw(nz=64, sweeps=8))
+    # no tile holds 12 layers at 8 sweeps, and the marching kernel takes at
+    # most 8 layers at 5-8 sweeps
+    with pytest.raises(eng.nat.HbfSimError):
+        eng.Thermal(**grid_kw(nx=1024, ny=1024, nz=12, sweeps=8))
