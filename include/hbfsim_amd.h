@@ -530,7 +530,12 @@ typedef struct hbfsim_amd_thermal_grid {
 typedef struct hbfsim_amd_thermal hbfsim_amd_thermal;
 
 /* Replaces ThermalModel's constructor for a grid network
- * (thermal.cpp:242-311).  Owns device scratch on the current device. */
+ * (thermal.cpp:242-311).  Owns device scratch on the current device.
+ * HBFSIM_UNSUPPORTED for a grid that no kernel takes: steps run on staged
+ * tiles of at most 2,048 cells ((t + 2 sweeps)^2 nz for some tile edge t),
+ * or, on grids of at least 2^21 cells, on the marching kernel (at most 16
+ * layers with 1-4 sweeps, at most 8 with 5-8; nx >= 2 (64 - 2 sweeps),
+ * ny >= 8 sweeps). */
 int hbfsim_amd_thermal_create(const hbfsim_amd_thermal_grid* grid,
                               hbfsim_amd_thermal** out);
 /* ThermalModel::advance_to (thermal.cpp:127-160) with constant power:
