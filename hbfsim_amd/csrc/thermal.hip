@@ -704,17 +704,31 @@ __global__ void k_fill_u64(unsigned long long* p, std::size_t n, unsigned long l
 struct GArgs {
     const hbf_record32* rec;
     std::size_t n;
-    std::uint32_t tile;            // records per block (kThreads * per)
-    std::uint32_t per;             // records per thread
     std::uint64_t window_ps, windows, light_gap_ps;
     const std::uint8_t* level;     // [windows]
     const std::uint32_t* ok2;      // [windows + 1]: first window >= w with level < 2
 };
 
-__device__ __forceinline__ void gate_record(const GArgs& g, std::size_t i, std::uint64_t& e,
+// A block takes kGateTile records, kGatePer consecutive ones per thread.  The
+// block first stages their issue times in LDS with coalesced loads, thread
+// t's records in row t (rows padded by one word against bank conflicts);
+// the admission times go back out the same way.
+constexpr std::uint32_t kGatePer = 16;
+constexpr std::uint32_t kGateTile = kThreads * kGatePer;
+constexpr std::uint32_t kGateRow = kGatePer + 1;
+
+__device__ __forceinline__ void stage_issue(const GArgs& g, std::size_t base, std::uint64_t* s)
+{
+    for (std::uint32_t k = threadIdx.x; k < kGateTile; k += kThreads) {
+        const std::size_t i = base + k;
+        s[(k / kGatePer) * kGateRow + k % kGatePer] = i < g.n ? g.rec[i].issue_ps : 0ull;
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ void gate_record(const GArgs& g, std::uint64_t t, std::uint64_t& e,
                                             std::uint64_t& gap)
 {
-    const std::uint64_t t = g.rec[i].issue_ps;
     const std::uint64_t w = t / g.window_ps;
     e = t;
     if (w < g.windows && g.level[w] >= 2) {
@@ -735,15 +749,23 @@ __device__ __forceinline__ MaxPlus compose(MaxPlus f, MaxPlus s)
     return MaxPlus{f.A + s.A, b > s.B ? b : s.B};
 }
 
-__device__ MaxPlus thread_map(const GArgs& g, std::size_t begin, std::size_t end)
+// The map of a thread's `count` records (issue times in its LDS row).
+__device__ MaxPlus thread_map(const GArgs& g, const std::uint64_t* row, std::uint32_t count)
 {
     MaxPlus m{0, 0};
-    for (std::size_t i = begin; i < end; ++i) {
+    for (std::uint32_t j = 0; j < count; ++j) {
         std::uint64_t e, gap;
-        gate_record(g, i, e, gap);
+        gate_record(g, row[j], e, gap);
         m = compose(m, MaxPlus{gap, e + gap});
     }
     return m;
+}
+
+// Records of this thread in the block's tile starting at `base`.
+__device__ __forceinline__ std::uint32_t gate_count(const GArgs& g, std::size_t base)
+{
+    const std::size_t b = base + static_cast<std::size_t>(threadIdx.x) * kGatePer;
+    return b < g.n ? static_cast<std::uint32_t>(std::min<std::size_t>(kGatePer, g.n - b)) : 0u;
 }
 
 // Inclusive scan of per-thread maps in thread order (Hillis-Steele).
@@ -767,10 +789,12 @@ __device__ MaxPlus block_scan(MaxPlus m, MaxPlus* sA)
 __global__ __launch_bounds__(kThreads) void k_gate_summary(GArgs g, MaxPlus* tiles)
 {
     __shared__ MaxPlus sA[kThreads];
-    const std::size_t base = static_cast<std::size_t>(blockIdx.x) * g.tile;
-    const std::size_t b = base + static_cast<std::size_t>(threadIdx.x) * g.per;
-    const std::size_t e = std::min(b + g.per, g.n);
-    const MaxPlus m = block_scan(b < g.n ? thread_map(g, b, e) : MaxPlus{0, 0}, sA);
+    __shared__ std::uint64_t s_t[kThreads * kGateRow];
+    const std::size_t base = static_cast<std::size_t>(blockIdx.x) * kGateTile;
+    stage_issue(g, base, s_t);
+    const std::uint32_t cnt = gate_count(g, base);
+    const MaxPlus m =
+        block_scan(thread_map(g, s_t + static_cast<std::size_t>(threadIdx.x) * kGateRow, cnt), sA);
     if (threadIdx.x == kThreads - 1) {
         tiles[blockIdx.x] = m;
     }
@@ -806,10 +830,12 @@ __global__ __launch_bounds__(kThreads) void k_gate_apply(GArgs g, const std::uin
                                                          std::uint64_t* admit)
 {
     __shared__ MaxPlus sA[kThreads];
-    const std::size_t base = static_cast<std::size_t>(blockIdx.x) * g.tile;
-    const std::size_t b = base + static_cast<std::size_t>(threadIdx.x) * g.per;
-    const std::size_t e = std::min(b + g.per, g.n);
-    const MaxPlus mine = b < g.n ? thread_map(g, b, e) : MaxPlus{0, 0};
+    __shared__ std::uint64_t s_t[kThreads * kGateRow];
+    const std::size_t base = static_cast<std::size_t>(blockIdx.x) * kGateTile;
+    stage_issue(g, base, s_t);
+    const std::uint32_t cnt = gate_count(g, base);
+    std::uint64_t* row = s_t + static_cast<std::size_t>(threadIdx.x) * kGateRow;
+    const MaxPlus mine = thread_map(g, row, cnt);
     block_scan(mine, sA);
     std::uint64_t gate = carry[blockIdx.x];
     if (threadIdx.x > 0) {
@@ -817,12 +843,19 @@ __global__ __launch_bounds__(kThreads) void k_gate_apply(GArgs g, const std::uin
         const std::uint64_t x = gate + ex.A;
         gate = x > ex.B ? x : ex.B;
     }
-    for (std::size_t i = b; i < e; ++i) {
+    for (std::uint32_t j = 0; j < cnt; ++j) {  // admission times replace the issue times
         std::uint64_t ei, gap;
-        gate_record(g, i, ei, gap);
+        gate_record(g, row[j], ei, gap);
         const std::uint64_t ai = ei > gate ? ei : gate;
-        admit[i] = ai;
+        row[j] = ai;
         gate = ai + gap;
+    }
+    __syncthreads();
+    for (std::uint32_t k = threadIdx.x; k < kGateTile; k += kThreads) {
+        const std::size_t i = base + k;
+        if (i < g.n) {
+            admit[i] = s_t[(k / kGatePer) * kGateRow + k % kGatePer];
+        }
     }
 }
 
@@ -1526,9 +1559,7 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     const std::size_t nref = refs.size();
     rep.refreshes = nref;
     const std::size_t total = n + nref;
-    const std::uint32_t per = 16;
-    const std::uint32_t gtile = kThreads * per;
-    const std::size_t gtiles = (n + gtile - 1) / gtile;
+    const std::size_t gtiles = (n + kGateTile - 1) / kGateTile;
     err = halloc(d_ok2, windows + 1);
     if (err == hipSuccess) err = halloc(d_gtiles, gtiles);
     if (err == hipSuccess) err = halloc(d_gcarry, gtiles);
@@ -1559,8 +1590,6 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
         GArgs ga;
         ga.rec = d_rec;
         ga.n = n;
-        ga.tile = gtile;
-        ga.per = per;
         ga.window_ps = o.window_ps;
         ga.windows = windows;
         ga.light_gap_ps = o.light_gap_ps;
