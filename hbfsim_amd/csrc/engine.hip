@@ -1531,10 +1531,6 @@ __device__ __forceinline__ int slot(const MaskWord* tmask, std::uint32_t words, 
     return static_cast<int>(m.base) + __popcll(m.bits & ((1ull << bit) - 1));
 }
 
-// Summary pass.  Per plane the tile keeps: the first record (page, issue,
-// class), the (max,+) map of the records after it, and the last page; per
-// channel the map of all its records.  Pages are stored as page + 1 in 32
-// bits (capacity / page_bytes < 2^32 is checked on the host).
 // Byte offset of the summary pass's lane-matching tables (plane table, then
 // channel table) after its state: fences, three 64-bit and two 32-bit plane
 // arrays, two 64-bit channel arrays and the plane class bytes; 8-byte aligned.
@@ -1543,6 +1539,10 @@ __host__ __device__ __forceinline__ std::size_t summary_match_offset(const KArgs
     return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 8ull * a.Rp + ((a.Rp + 7ull) & ~7ull);
 }
 
+// Summary pass.  Per plane the tile keeps: the first record (page, issue,
+// class), the (max,+) map of the records after it, and the last page; per
+// channel the map of all its records.  Pages are stored as page + 1 in 32
+// bits (capacity / page_bytes < 2^32 is checked on the host).
 template <bool kRefresh, bool kHits, bool kPacked = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 : 1))) void k_summary(KArgs a, const void* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
@@ -1632,7 +1632,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
             if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
                 q.push_group(gl, g, rcu.id);
                 if (q.n == kWave || gend >= end) {
-                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc, mt_p, mt_c);
+                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
+                                 mt_p, mt_c);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
                     dq = q;
                     q.n = 0;
@@ -1660,7 +1661,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                     q.push(lp, li, lb, s, rcu.id);
                 }
                 if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= end)) {
-                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc, mt_p, mt_c);
+                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
+                                 mt_p, mt_c);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
                     write_descs(desc, a.desc_rid, dq, lane);  // at most one batch waits
                     dq = q;
