@@ -361,14 +361,16 @@ void launch_window(const TArgs& a, std::uint32_t blocks, std::size_t lds, hipStr
 // enters (level 0: T and P from memory) is swept S times on the way through:
 // at step t, level k (1..S) updates row t - 2k from level k - 1's rows
 // t - 2k - 1 .. t - 2k + 1, all of which earlier steps wrote, so one barrier
-// per step separates every writer from its readers.  Each level keeps a ring
-// of 4 rows in LDS (written at step s, read at s + 1 .. s + 3); the right-hand
+// per step separates every writer from its readers.  A thread keeps its own
+// cell's last 4 rows of every level in registers (written at step s, read at
+// s + 1 .. s + 3); the level's rows also go to an LDS ring of 4 for the
+// layers above and below, which read them 2 steps later.  The right-hand
 // side of a row stays in the owning thread's registers until its last sweep.
 // Halo: S columns on each side of the W = 64 - 2S written columns, and S rows
 // at each end of a segment, against S on every side of a square tile; the
 // lanes and rows next to the staged edge read a stand-in (0.0 for the lane
 // beyond the wave, a zero row before the segment) and only feed cells that
-// are not written.
+// are not written.  Workgroups run 64 x nz threads, so up to 16 layers.
 // Cells outside the grid hold 0.0 at every level, so a missing x or y
 // neighbour adds g * 0.0 = +0.0 exactly as the per-tile kernel's zero slot
 // does; a missing z neighbour is read from the cell itself with conductance
