@@ -65,6 +65,35 @@ def test_thermal_step_bit_exact(oracle, shape, sweeps, steps):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("shape,sweeps", [((1030, 260, 8), 4), ((400, 400, 8), 4)])
+def test_thermal_steps_across_calls(oracle, shape, sweeps):
+    """One grid object stepped by two calls with different power arrays and
+    odd and even step counts (the marching kernel keeps its launch geometry
+    from the first call; the tiles rebuild theirs), against the oracle."""
+    import torch
+    nx, ny, nz = shape
+    n = nx * ny * nz
+    g = grid_kw(nx=nx, ny=ny, nz=nz, sweeps=sweeps)
+    rng = np.random.default_rng(nx + ny)
+    t0 = rng.uniform(318.0, 340.0, n)
+    powers = [rng.uniform(0.0, 0.05, n), rng.uniform(0.0, 0.02, n)]
+    th = eng.Thermal(**g)
+    try:
+        t = torch.from_numpy(t0.copy()).cuda()
+        for p, steps in zip(powers, (3, 2)):
+            th.step(torch.from_numpy(p).cuda(), t, steps)
+        got = t.cpu().numpy()
+    finally:
+        th.close()
+    want = t0.copy()
+    for p, steps in zip(powers, (3, 2)):
+        for _ in range(steps):
+            oracle.orc_thermal_grid_step(nx, ny, nz, g["capacity_j_per_k"], g["gx_w_per_k"],
+                                         g["gy_w_per_k"], g["gz_w_per_k"], g["top_g_w_per_k"],
+                                         g["ambient_k"], g["dt_s"], f(p), f(want), -1.0, sweeps)
+    np.testing.assert_array_equal(got, want)
+
+
 def test_thermal_step_is_the_implicit_solve(oracle):
     """Six sweeps at the config-4 stiffness reach the dense backward-Euler
     solution (pinned to the compiled reference thermal.cpp) to 1e-12."""
