@@ -373,7 +373,14 @@ def bench_thermal(args) -> dict:
                                                   "k_thermal_march", cells)[0],
                      "traffic_source": "profiles/thermal_traffic_grid2048.txt", "kernel_ms": kms,
                      "algorithmic": "24 B per cell per step (T and P read, T written; "
-                                    "the 4 sweeps stay on chip)"},
+                                    "the 4 sweeps stay on chip)",
+                     # the per-sweep model (8 B read + 8 B written per cell and sweep): a
+                     # kernel that kept no sweep on chip would need these bytes, so a
+                     # blocked one can pass 1.0 on it
+                     "per_sweep_model": {"bytes_per_cell_sweep": 16,
+                                         "achieved": 16 * sweeps / (kms / 1e3) / 1e9,
+                                         "frac": 16 * sweeps / (kms / 1e3) / 1e9
+                                         / PEAK_HBM_GBPS}},
     }
     if not args.no_cpu:
         sys.path.insert(0, str(ROOT / "tests"))
@@ -674,8 +681,13 @@ def main() -> None:
         out["link"] = bench_link(args)
     if not args.no_cpu:
         log("cpu baseline")
-        out["cpu_baseline"] = cpu_baseline(profile, ranges, host_records, args.cpu_seconds)
-        out["cpu_baseline"]["scalar_fast_model"] = scalar_floor(min(3.0, args.cpu_seconds))
+        cb = cpu_baseline(profile, ranges, host_records, args.cpu_seconds)
+        cb["scalar_fast_model"] = scalar_floor(min(3.0, args.cpu_seconds))
+        # the speedup over the CPU oracle, on the host's single core and on its cores together
+        cb["speedup"] = {"vs_1_core": value / cb["value"],
+                         "vs_all_cores": value / cb["parallel"]["value"]
+                         if cb.get("parallel") else None}
+        out["cpu_baseline"] = cb
     if args.config == "c2" and not args.no_extra:
         del batches, timed
         import torch
