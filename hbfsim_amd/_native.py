@@ -218,6 +218,7 @@ SIGNATURES = {
     "hbfsim_amd_thermal_create": (_INT, [ctypes.POINTER(ThermalGrid), ctypes.POINTER(_P)]),
     "hbfsim_amd_thermal_step": (_INT, [_P, _P, _P, _U64, _P]),
     "hbfsim_amd_thermal_last_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float)]),
+    "hbfsim_amd_thermal_last_launches": (_INT, [_P, ctypes.POINTER(ctypes.c_uint64)]),
     "hbfsim_amd_thermal_destroy": (None, [_P]),
     "hbfsim_amd_run_coupled": (_INT, [_P, _P, ctypes.POINTER(ReliabilityOptions), _P, _SZ, _P,
                                       _P, _P, _P, ctypes.POINTER(CoupledReport),

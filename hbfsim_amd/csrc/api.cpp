@@ -757,6 +757,15 @@ HBF_API int hbfsim_amd_thermal_last_ms(const hbfsim_amd_thermal* t, float* ms)
     return HBFSIM_OK;
 }
 
+HBF_API int hbfsim_amd_thermal_last_launches(const hbfsim_amd_thermal* t, uint64_t* launches)
+{
+    if (t == nullptr || launches == nullptr) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    *launches = hbfamd::thermal_last_launches(t->impl);
+    return HBFSIM_OK;
+}
+
 HBF_API void hbfsim_amd_thermal_destroy(hbfsim_amd_thermal* t)
 {
     if (t == nullptr) {

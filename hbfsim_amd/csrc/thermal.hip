@@ -357,20 +357,24 @@ void launch_window(const TArgs& a, std::uint32_t blocks, std::size_t lds, hipStr
 
 // ---- marching stencil for large uncoupled grids ----------------------------
 // A workgroup owns a strip of 64 x columns (one wave per z layer, lane = x
-// offset) over a segment of rows, and walks it along y.  Each row that
-// enters (level 0: T and P from memory) is swept S times on the way through:
-// at step t, level k (1..S) updates row t - 2k from level k - 1's rows
-// t - 2k - 1 .. t - 2k + 1, all of which earlier steps wrote, so one barrier
-// per step separates every writer from its readers.  A thread keeps its own
-// cell's last 4 rows of every level in registers (written at step s, read at
-// s + 1 .. s + 3); the level's rows also go to an LDS ring of 4 for the
-// layers above and below, which read them 2 steps later.  The right-hand
-// side of a row stays in the owning thread's registers until its last sweep.
-// Halo: S columns on each side of the W = 64 - 2S written columns, and S rows
-// at each end of a segment, against S on every side of a square tile; the
-// lanes and rows next to the staged edge read a stand-in (0.0 for the lane
-// beyond the wave, a zero row before the segment) and only feed cells that
-// are not written.  Workgroups run 64 x nz threads, so up to 16 layers.
+// offset) over a segment of rows, and walks it along y.  Each row that enters
+// (level 0: T and P from memory) is swept L times on the way through: S
+// sweeps of one step, or 2 S when a pass makes two steps with the same
+// power (the first step's result, at level S, becomes the second step's
+// start and right-hand side without leaving the chip).  At step t, level k
+// (1..L) updates row t - 2k from level k - 1's rows t - 2k - 1 .. t - 2k + 1,
+// all of which earlier steps wrote; the z neighbours' values come from step
+// t - 2, so one barrier per two steps separates every writer from its
+// readers.  A thread keeps its own cell's last 4 rows of every level in
+// registers (written at step s, read at s + 1 .. s + 3); the level's rows
+// also go to an LDS ring of 4 for the layers above and below, which read
+// them 2 steps later.  The right-hand side of a row stays in the owning
+// thread's registers until its last sweep.
+// Halo: L columns on each side of the W = 64 - 2L written columns, and L
+// rows at each end of a segment, against L on every side of a square tile;
+// the lanes and rows next to the staged edge read a stand-in (0.0 for the
+// lane beyond the wave, a zero row before the segment) and only feed cells
+// that are not written.  Workgroups run 64 x nz threads, so up to 16 layers.
 // Cells outside the grid hold 0.0 at every level, so a missing x or y
 // neighbour adds g * 0.0 = +0.0 exactly as the per-tile kernel's zero slot
 // does; a missing z neighbour is read from the cell itself with conductance
@@ -398,11 +402,16 @@ struct MCtx {
     const double* pzp;   // thread itself in the bottom and top layers)
 };
 
-template <int S>
+// S sweeps per step, F steps per pass (1 or 2, the same power in both): the
+// pass sweeps L = F S levels.
+template <int S, int F>
 struct MRows {
+    static constexpr int L = S * F;
     double pt[kMarchAhead], pp[kMarchAhead];  // T and P of rows loaded ahead
     double rh[2 * S + 1];                     // rh[i]: right-hand side of row t - i
-    double h[S][4];                           // h[k][r & 3]: this cell's level k at row r
+    double ph[F == 2 ? 2 * S + 1 : 1];        // ph[i]: power of row t - i (second step)
+    double rh1[F == 2 ? 2 * S + 1 : 1];       // rh1[i]: second step's right-hand side of row t - 2S - i
+    double h[L][4];                           // h[k][r & 3]: this cell's level k at row r
 };
 
 __device__ __forceinline__ bool march_enters(const MCtx& c, int r)
@@ -435,34 +444,34 @@ __device__ __forceinline__ double wave_shift(double v)
 // and y + 1 terms, and the neighbouring lanes' copies (a one-lane wave shift)
 // the x - 1 and x + 1 terms; only the z neighbours, held by other waves, are
 // read from LDS.
-template <int S, bool kInner, int J>
-__device__ __forceinline__ void march_step(const MCtx& c, MRows<S>& m, int t, const double* tin,
-                                           const double* power, double* tout)
+template <int S, int F, bool kInner, int J>
+__device__ __forceinline__ void march_step(const MCtx& c, MRows<S, F>& m, int t, double tv,
+                                           double pv, double* tout)
 {
     constexpr int kRing = 4 * kMarchLanes;
-    const bool ent = kInner ? c.xin : march_enters(c, t);
-    const double tv = ent ? m.pt[J] : 0.0, pv = ent ? m.pp[J] : 0.0;
-    // the next load into pt[J] / pp[J] is issued after row t's values are
-    // taken (the empty asm orders them), so both rows share the registers and
-    // the loop carries no copies of pending loads
-    std::size_t nxt = march_at(c, t + kMarchAhead);
-    asm volatile("" : "+v"(nxt) : "v"(tv), "v"(pv));
-    m.pt[J] = tin[nxt];
-    m.pp[J] = power[nxt];
+    constexpr int L = S * F;
 #pragma unroll
     for (int i = 2 * S; i > 0; --i) {
         m.rh[i] = m.rh[i - 1];
     }
     m.rh[0] = c.cdt * tv + pv;
+    if constexpr (F == 2) {
+#pragma unroll
+        for (int i = 2 * S; i > 0; --i) {
+            m.ph[i] = m.ph[i - 1];
+            m.rh1[i] = m.rh1[i - 1];
+        }
+        m.ph[0] = pv;
+    }
     m.h[0][J] = tv;
     c.me[J * kMarchLanes] = tv;  // level 0
 #pragma unroll
-    for (int k = 1; k <= S; ++k) {
+    for (int k = 1; k <= L; ++k) {
         const int r = t - 2 * k;
         const int qr = (J - 2 * k) & 3;
         const double cr = m.h[k - 1][qr];
         const int sr = (k - 1) * kRing + qr * kMarchLanes;
-        double num = m.rh[2 * k];
+        double num = k <= S ? m.rh[2 * k] : m.rh1[2 * (k - S)];
         num += c.gx * wave_shift<0x138>(cr);
         num += c.gx * wave_shift<0x130>(cr);
         num += c.gy * m.h[k - 1][(J - 2 * k - 1) & 3];
@@ -481,7 +490,12 @@ __device__ __forceinline__ void march_step(const MCtx& c, MRows<S>& m, int t, co
             const double rd = r > 0 ? (r + 1 < c.ny ? d3 : d1) : (r + 1 < c.ny ? d2 : d0);
             v = (r >= 0 && r < c.ny) ? num * rd : 0.0;
         }
-        if (k < S) {
+        if constexpr (F == 2) {
+            if (k == S) {  // the first step's result: the second step's T and start
+                m.rh1[0] = c.cdt * v + m.ph[2 * S];
+            }
+        }
+        if (k < L) {
             m.h[k][qr] = v;
             c.me[k * kRing + qr * kMarchLanes] = v;
         } else if (c.own && r >= c.ys && r < c.ye) {
@@ -490,16 +504,36 @@ __device__ __forceinline__ void march_step(const MCtx& c, MRows<S>& m, int t, co
     }
 }
 
-template <int S, int J>
-__device__ __forceinline__ void march_sub(const MCtx& c, MRows<S>& m, int t, const double* tin,
+template <int S, int F, int J>
+__device__ __forceinline__ void march_sub(const MCtx& c, MRows<S, F>& m, int t, const double* tin,
                                           const double* power, double* tout)
 {
-    if (t >= 2 * S + 1 && t < c.tload) {
-        march_step<S, true, J>(c, m, t, tin, power, tout);
+    const bool ent = march_enters(c, t);
+    const double tv = ent ? m.pt[J] : 0.0, pv = ent ? m.pp[J] : 0.0;
+    // the next load into pt[J] / pp[J] is issued after row t's values are
+    // taken (the empty asm orders them), so both rows share the registers and
+    // the loop carries no copies of pending loads; it sits before the branch
+    // so that both paths keep the loaded rows in the same registers (a
+    // pending load in other registers on one path would make the wait
+    // analysis drain every prefetched row on the other)
+    std::size_t nxt = march_at(c, t + kMarchAhead);
+    asm volatile("" : "+v"(nxt) : "v"(tv), "v"(pv));
+    m.pt[J] = tin[nxt];
+    m.pp[J] = power[nxt];
+    if (t >= 2 * S * F + 1 && t < c.tload) {
+        march_step<S, F, true, J>(c, m, t, tv, pv, tout);
     } else {
-        march_step<S, false, J>(c, m, t, tin, power, tout);
+        march_step<S, F, false, J>(c, m, t, tv, pv, tout);
     }
-    __syncthreads();
+    // One barrier per two steps.  Step t reads the z neighbours' level k - 1
+    // of row t - 2k, written at step t - 2, so steps t and t + 1 (t even) read
+    // only what the previous pair wrote; the pair reads ring slots t - 2k and
+    // t - 2k + 1 of level k - 1 while writing slots t - 2k + 2 and t - 2k + 3,
+    // disjoint in the 4-slot ring, and the next pair's writes to the slots
+    // read here come after the barrier.
+    if constexpr ((J & 1) != 0) {
+        __syncthreads();
+    }
 }
 
 // Threads per workgroup the marching kernel is built for: up to 16 layers
@@ -509,18 +543,21 @@ __host__ __device__ constexpr int march_max_threads(int s)
     return s <= 4 ? 16 * kMarchLanes : 8 * kMarchLanes;
 }
 
-template <int S>
-__global__ __launch_bounds__(march_max_threads(S)) void k_thermal_march(MArgs a, const double* tin,
-                                                                        double* tout)
+template <int S, int F = 1>
+__global__ __launch_bounds__(march_max_threads(S * F)) void k_thermal_march(MArgs a,
+                                                                            const double* tin,
+                                                                            double* tout)
 {
-    // LDS: [z][level 0..S-1][ring slot 0..3][64 lanes], read only by the
+    // LDS: [z][level 0..L-1][ring slot 0..3][64 lanes], read only by the
     // layers above and below; every offset from a thread's base is a
     // compile-time constant once steps are unrolled by 4
     extern __shared__ double lds[];
-    constexpr int W = kMarchLanes - 2 * S;
-    constexpr int kLayer = S * 4 * kMarchLanes;
+    constexpr int L = S * F;  // levels: F steps of S sweeps
+    constexpr int W = kMarchLanes - 2 * L;
+    constexpr int kLayer = L * 4 * kMarchLanes;
     // consecutive workgroups go to different XCDs: give each XCD a run of
-    // neighbouring strips, so the halo columns they share hit one L2
+    // neighbouring strips, so the halo columns they share hit one L2 (and the
+    // strips of a segment, walking the same rows together, read whole rows)
     const std::uint32_t b = blockIdx.x;
     const std::uint32_t id = (b % 8u) * a.per_xcd + b / 8u;
     if (id >= a.total) {
@@ -535,10 +572,10 @@ __global__ __launch_bounds__(march_max_threads(S)) void k_thermal_march(MArgs a,
     c.ny = ny;
     c.ys = static_cast<int>((id / a.strips) * a.seg_len);
     c.ye = c.ys + static_cast<int>(a.seg_len) < ny ? c.ys + static_cast<int>(a.seg_len) : ny;
-    c.tload = c.ye + S < ny ? c.ye + S : ny;
-    const int x = strip * W - S + lane;
+    c.tload = c.ye + L < ny ? c.ye + L : ny;
+    const int x = strip * W - L + lane;
     c.xin = x >= 0 && x < nx;
-    c.own = c.xin && lane >= S && lane < kMarchLanes - S;
+    c.own = c.xin && lane >= L && lane < kMarchLanes - L;
     c.cdt = a.cdt;
     c.gx = a.gx;
     c.gy = a.gy;
@@ -574,16 +611,16 @@ __global__ __launch_bounds__(march_max_threads(S)) void k_thermal_march(MArgs a,
     c.pzp = c.me + (z + 1 < nz ? kLayer : 0);
     c.col = static_cast<std::size_t>(z) * a.nx * a.ny + (c.xin ? x : 0);
 #pragma unroll
-    for (int k = 0; k < 4 * S; ++k) {
+    for (int k = 0; k < 4 * L; ++k) {
         c.me[k * kMarchLanes] = 0.0;
     }
-    // Rows [ys - S, ye + S) enter (those inside the grid from memory).  Steps
-    // start at a multiple of 4 at or before ys - S, so that row t sits in
+    // Rows [ys - L, ye + L) enter (those inside the grid from memory).  Steps
+    // start at a multiple of 4 at or before ys - L, so that row t sits in
     // ring slot t & 3 = its index in the unrolled body, and run in whole
     // rounds of 4; the extra steps only sweep rows that are not written.
-    const int t0 = (c.ys - S) & ~3;
-    const int t1 = t0 + ((c.ye + 2 * S - t0 + 3) & ~3);
-    MRows<S> m;
+    const int t0 = (c.ys - L) & ~3;
+    const int t1 = t0 + ((c.ye + 2 * L - t0 + 3) & ~3);
+    MRows<S, F> m;
 #pragma unroll
     for (int j = 0; j < kMarchAhead; ++j) {
         m.pt[j] = tin[march_at(c, t0 + j)];
@@ -592,9 +629,13 @@ __global__ __launch_bounds__(march_max_threads(S)) void k_thermal_march(MArgs a,
 #pragma unroll
     for (int i = 0; i <= 2 * S; ++i) {
         m.rh[i] = 0.0;
+        if constexpr (F == 2) {
+            m.ph[i] = 0.0;
+            m.rh1[i] = 0.0;
+        }
     }
 #pragma unroll
-    for (int k = 0; k < S; ++k) {
+    for (int k = 0; k < L; ++k) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             m.h[k][q] = 0.0;
@@ -602,18 +643,18 @@ __global__ __launch_bounds__(march_max_threads(S)) void k_thermal_march(MArgs a,
     }
     __syncthreads();
     for (int t = t0; t < t1; t += kMarchAhead) {
-        march_sub<S, 0>(c, m, t, tin, a.power, tout);
-        march_sub<S, 1>(c, m, t + 1, tin, a.power, tout);
-        march_sub<S, 2>(c, m, t + 2, tin, a.power, tout);
-        march_sub<S, 3>(c, m, t + 3, tin, a.power, tout);
+        march_sub<S, F, 0>(c, m, t, tin, a.power, tout);
+        march_sub<S, F, 1>(c, m, t + 1, tin, a.power, tout);
+        march_sub<S, F, 2>(c, m, t + 2, tin, a.power, tout);
+        march_sub<S, F, 3>(c, m, t + 3, tin, a.power, tout);
     }
 }
 
-template <int S>
+template <int S, int F>
 hipError_t launch_march_s(const MArgs& m, std::uint32_t blocks, std::uint32_t threads,
                           std::size_t lds, hipStream_t stream, const double* tin, double* tout)
 {
-    hipLaunchKernelGGL((k_thermal_march<S>), dim3(blocks), dim3(threads), lds, stream, m, tin,
+    hipLaunchKernelGGL((k_thermal_march<S, F>), dim3(blocks), dim3(threads), lds, stream, m, tin,
                        tout);
     return hipGetLastError();
 }
@@ -621,8 +662,18 @@ hipError_t launch_march_s(const MArgs& m, std::uint32_t blocks, std::uint32_t th
 using MarchLaunch = hipError_t (*)(const MArgs&, std::uint32_t, std::uint32_t, std::size_t,
                                    hipStream_t, const double*, double*);
 
-const void* march_kernel(std::uint32_t s)
+// Fused passes (F = 2) exist for 1-4 sweeps per step (up to 8 levels).
+const void* march_kernel(std::uint32_t s, int f = 1)
 {
+    if (f == 2) {
+        switch (s) {
+        case 1: return reinterpret_cast<const void*>(k_thermal_march<1, 2>);
+        case 2: return reinterpret_cast<const void*>(k_thermal_march<2, 2>);
+        case 3: return reinterpret_cast<const void*>(k_thermal_march<3, 2>);
+        case 4: return reinterpret_cast<const void*>(k_thermal_march<4, 2>);
+        default: return nullptr;
+        }
+    }
     switch (s) {
     case 1: return reinterpret_cast<const void*>(k_thermal_march<1>);
     case 2: return reinterpret_cast<const void*>(k_thermal_march<2>);
@@ -636,17 +687,26 @@ const void* march_kernel(std::uint32_t s)
     }
 }
 
-MarchLaunch march_launcher(std::uint32_t s)
+MarchLaunch march_launcher(std::uint32_t s, int f = 1)
 {
+    if (f == 2) {
+        switch (s) {
+        case 1: return launch_march_s<1, 2>;
+        case 2: return launch_march_s<2, 2>;
+        case 3: return launch_march_s<3, 2>;
+        case 4: return launch_march_s<4, 2>;
+        default: return nullptr;
+        }
+    }
     switch (s) {
-    case 1: return launch_march_s<1>;
-    case 2: return launch_march_s<2>;
-    case 3: return launch_march_s<3>;
-    case 4: return launch_march_s<4>;
-    case 5: return launch_march_s<5>;
-    case 6: return launch_march_s<6>;
-    case 7: return launch_march_s<7>;
-    case 8: return launch_march_s<8>;
+    case 1: return launch_march_s<1, 1>;
+    case 2: return launch_march_s<2, 1>;
+    case 3: return launch_march_s<3, 1>;
+    case 4: return launch_march_s<4, 1>;
+    case 5: return launch_march_s<5, 1>;
+    case 6: return launch_march_s<6, 1>;
+    case 7: return launch_march_s<7, 1>;
+    case 8: return launch_march_s<8, 1>;
     default: return nullptr;
     }
 }
@@ -657,19 +717,21 @@ MarchLaunch march_launcher(std::uint32_t s)
 // workgroup's LDS limit.  Returns the LDS bytes, 0 when it does not apply.
 constexpr std::size_t kMarchMinCells = std::size_t{1} << 21;
 
-std::size_t march_lds(const hbfsim_amd_thermal_grid& g, std::size_t lds_limit)
+// f = 2: the fused pass of two steps (2 sweeps levels), under the same rules.
+std::size_t march_lds(const hbfsim_amd_thermal_grid& g, std::size_t lds_limit, int f = 1)
 {
     const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
-    if (march_kernel(g.sweeps) == nullptr || g.nz > 16 || cells < kMarchMinCells) {
+    if (march_kernel(g.sweeps, f) == nullptr || g.nz > 16 || cells < kMarchMinCells) {
         return 0;
     }
-    const std::uint32_t W = kMarchLanes - 2 * g.sweeps;
+    const std::uint32_t levels = g.sweeps * static_cast<std::uint32_t>(f);
+    const std::uint32_t W = kMarchLanes - 2 * levels;
     const std::uint32_t threads = kMarchLanes * g.nz;
-    if (threads > static_cast<std::uint32_t>(march_max_threads(static_cast<int>(g.sweeps)))) {
+    if (threads > static_cast<std::uint32_t>(march_max_threads(static_cast<int>(levels)))) {
         return 0;
     }
-    const std::size_t lds = static_cast<std::size_t>(g.sweeps) * 4 * threads * sizeof(double);
-    if (lds > lds_limit || g.nx < 2 * W || g.ny < 8 * g.sweeps) {
+    const std::size_t lds = static_cast<std::size_t>(levels) * 4 * threads * sizeof(double);
+    if (lds > lds_limit || g.nx < 2 * W || g.ny < 8 * levels) {
         return 0;
     }
     return lds;
@@ -1077,9 +1139,11 @@ struct thermal {
     hbfsim_amd_thermal_grid grid{};
     int device = 0;
     double* d_scratch = nullptr;   // second temperature buffer
+    double* d_scratch2 = nullptr;  // third, made when an odd pass count first needs it
     hipEvent_t ev[2] = {nullptr, nullptr};
     hipEvent_t cev[8] = {};        // coupled-run phase boundaries
     float last_ms = 0.0f;
+    std::uint64_t last_launches = 0;  // kernel passes of the last thermal_step
     float phase_ms[5] = {};        // counts, thermal chain, admission, engine, gather
     std::size_t lds_per_block = 0;  // the device's LDS limit per workgroup
     bool wide_ready = false;        // the wide kernel may take that much LDS
@@ -1087,9 +1151,9 @@ struct thermal {
     // marching stencil (uncoupled steps on large grids), set up at the first step
     bool march_checked = false;
     bool march = false;
-    MArgs m{};
-    std::uint32_t m_blocks = 0, m_threads = 0;
-    std::size_t m_lds = 0;
+    MArgs m[2] = {};               // [0] one step per pass, [1] two (m_lds[1] == 0: none)
+    std::uint32_t m_blocks[2] = {}, m_threads[2] = {};
+    std::size_t m_lds[2] = {};
     // last coupled run
     std::uint64_t windows = 0;
     std::uint32_t ndie = 0;
@@ -1153,6 +1217,7 @@ void thermal_destroy(thermal* th)
     (void)hipSetDevice(th->device);
     (void)hipDeviceSynchronize();
     hfree(th->d_scratch);
+    hfree(th->d_scratch2);
     for (auto& e : th->ev) {
         if (e != nullptr) {
             (void)hipEventDestroy(e);
@@ -1169,6 +1234,8 @@ void thermal_destroy(thermal* th)
 const hbfsim_amd_thermal_grid& thermal_get_grid(const thermal* th) { return th->grid; }
 
 float thermal_last_step_ms(const thermal* th) { return th->last_ms; }
+
+std::uint64_t thermal_last_launches(const thermal* th) { return th->last_launches; }
 
 int coupled_last_ms(const thermal* th, float* ms, int max)
 {
@@ -1217,17 +1284,21 @@ std::uint32_t tile_blocks(const TArgs& a)
 
 // Segments are sized so that one round of resident workgroups covers the
 // grid (or every strip is one segment when strips alone exceed a round).
+// Rows are not balanced across strips: the strips of a segment walk the
+// same rows at the same time, so HBM sees whole 16 KB rows rather than
+// scattered pieces of them, which measured faster than equal row counts.
 
-hipError_t setup_march(thermal* th)
+// One pass form (f steps per pass): its launch geometry.
+hipError_t setup_march_form(thermal* th, int f)
 {
-    th->march_checked = true;
     const auto& g = th->grid;
-    const std::size_t lds = march_lds(g, th->lds_per_block);
-    if (lds == 0 || th->cus <= 0) {
+    const std::size_t lds = march_lds(g, th->lds_per_block, f);
+    if (lds == 0) {
         return hipSuccess;
     }
-    const void* fn = march_kernel(g.sweeps);
-    const std::uint32_t W = kMarchLanes - 2 * g.sweeps;
+    const void* fn = march_kernel(g.sweeps, f);
+    const std::uint32_t levels = g.sweeps * static_cast<std::uint32_t>(f);
+    const std::uint32_t W = kMarchLanes - 2 * levels;
     const std::uint32_t threads = kMarchLanes * g.nz;
     hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                          static_cast<int>(lds));
@@ -1241,11 +1312,11 @@ hipError_t setup_march(thermal* th)
     const std::uint32_t strips = (g.nx + W - 1) / W;
     const std::uint64_t round = static_cast<std::uint64_t>(per_cu) * th->cus;
     std::uint64_t segs = round / strips;
-    const std::uint64_t max_segs = g.ny / (8ull * g.sweeps);  // segments of >= 8 S rows
+    const std::uint64_t max_segs = g.ny / (8ull * levels);  // segments of >= 8 L rows
     segs = std::max<std::uint64_t>(1, std::min(segs, max_segs));
     const std::uint32_t seg_len = static_cast<std::uint32_t>((g.ny + segs - 1) / segs);
     segs = (g.ny + seg_len - 1) / seg_len;
-    MArgs& m = th->m;
+    MArgs& m = th->m[f - 1];
     m.nx = g.nx;
     m.ny = g.ny;
     m.nz = g.nz;
@@ -1259,11 +1330,24 @@ hipError_t setup_march(thermal* th)
     m.gz = g.gz_w_per_k;
     m.gb = g.top_g_w_per_k;
     m.tb = g.ambient_k;
-    th->m_blocks = m.per_xcd * 8;
-    th->m_threads = threads;
-    th->m_lds = lds;
-    th->march = true;
+    th->m_blocks[f - 1] = m.per_xcd * 8;
+    th->m_threads[f - 1] = threads;
+    th->m_lds[f - 1] = lds;
     return hipSuccess;
+}
+
+hipError_t setup_march(thermal* th)
+{
+    th->march_checked = true;
+    if (th->cus <= 0) {
+        return hipSuccess;
+    }
+    hipError_t err = setup_march_form(th, 1);
+    if (err == hipSuccess && th->m_lds[0] != 0) {
+        err = setup_march_form(th, 2);
+        th->march = err == hipSuccess;
+    }
+    return err;
 }
 
 }  // namespace
@@ -1308,27 +1392,48 @@ int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64
         }
     }
     const std::size_t cells = static_cast<std::size_t>(g.nx) * g.ny * g.nz;
-    double* buf[2] = {d_temp, th->d_scratch};
-    (void)hipEventRecord(th->ev[0], stream);
+    // Passes: on the marching kernel pairs of steps in fused passes (the
+    // power is the same in both) and the odd step in a single-step one.
+    const std::uint64_t pairs = th->march && th->m_lds[1] != 0 ? steps / 2 : 0;
+    const std::uint64_t launches = steps - pairs;
+    // Each pass reads one buffer and writes another.  An even count
+    // alternates d_temp and the scratch and ends in d_temp; an odd count of 3
+    // or more goes d_temp -> scratch, then between the two scratch buffers,
+    // and its last pass writes d_temp; a single pass leaves the result in the
+    // scratch, copied back below.
     hipError_t err = hipSuccess;
-    if (th->march) {
-        MArgs m = th->m;
-        m.power = d_power;
-        const MarchLaunch launch = march_launcher(g.sweeps);
-        for (std::uint64_t s = 0; s < steps && err == hipSuccess; ++s) {
-            err = launch(m, th->m_blocks, th->m_threads, th->m_lds, stream, buf[s & 1],
-                         buf[(s + 1) & 1]);
+    const bool three = (launches & 1) != 0 && launches >= 3;
+    if (three && th->d_scratch2 == nullptr) {
+        err = halloc(th->d_scratch2, cells);
+        if (err != hipSuccess) {
+            return HBFSIM_CUDA_ERROR;
         }
-    } else {
-        for (std::uint64_t s = 0; s < steps; ++s) {
-            launch_window<false>(a, tile_blocks(a), lds, stream, buf[s & 1], buf[(s + 1) & 1],
-                                 0ull);
+    }
+    double* cur = d_temp;
+    const auto target = [&](std::uint64_t i) {
+        if (!three) {
+            return cur == d_temp ? th->d_scratch : d_temp;
         }
+        return i + 1 == launches ? d_temp : (cur == th->d_scratch ? th->d_scratch2 : th->d_scratch);
+    };
+    (void)hipEventRecord(th->ev[0], stream);
+    for (std::uint64_t i = 0; i < launches && err == hipSuccess; ++i) {
+        double* dst = target(i);
+        if (th->march) {
+            const int f = i < pairs ? 2 : 1;
+            MArgs m = th->m[f - 1];
+            m.power = d_power;
+            err = march_launcher(g.sweeps, f)(m, th->m_blocks[f - 1], th->m_threads[f - 1],
+                                              th->m_lds[f - 1], stream, cur, dst);
+        } else {
+            launch_window<false>(a, tile_blocks(a), lds, stream, cur, dst, 0ull);
+        }
+        cur = dst;
     }
     (void)hipEventRecord(th->ev[1], stream);
     if (err == hipSuccess) err = hipGetLastError();
-    if (err == hipSuccess && (steps & 1)) {
-        err = hipMemcpyAsync(d_temp, th->d_scratch, cells * sizeof(double),
+    if (err == hipSuccess && cur != d_temp) {
+        err = hipMemcpyAsync(d_temp, cur, cells * sizeof(double),
                              hipMemcpyDeviceToDevice, stream);
     }
     if (err == hipSuccess) err = hipStreamSynchronize(stream);
@@ -1339,6 +1444,7 @@ int thermal_step(thermal* th, const double* d_power, double* d_temp, std::uint64
     if (hipEventElapsedTime(&ms, th->ev[0], th->ev[1]) == hipSuccess) {
         th->last_ms = ms / static_cast<float>(steps);
     }
+    th->last_launches = launches;
     return HBFSIM_OK;
 }
 

@@ -20,6 +20,9 @@ int thermal_step(thermal* th, const double* d_power, double* d_temperature,
                  std::uint64_t steps, void* stream);
 // Average device time of one step's kernel in the last thermal_step call.
 float thermal_last_step_ms(const thermal* th);
+// Kernel passes the last thermal_step call launched (a pass makes one step,
+// or two on the marching kernel's fused form).
+std::uint64_t thermal_last_launches(const thermal* th);
 
 // The coupled run on engine `e` (whose geometry `cfg` describes):
 // per-window access counts -> thermal / retention / throttle chain ->

@@ -331,6 +331,13 @@ class Thermal:
                   "thermal time")
         return float(ms.value)
 
+    def last_launches(self) -> int:
+        """Kernel passes of the last step() call (a fused pass makes two steps)."""
+        n = ctypes.c_uint64()
+        nat.check(self._lib.hbfsim_amd_thermal_last_launches(self.handle, ctypes.byref(n)),
+                  "thermal launches")
+        return int(n.value)
+
     def coupled_ms(self) -> dict:
         """Device time of the last coupled run's phases."""
         ms = (ctypes.c_float * 5)()

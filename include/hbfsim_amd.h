@@ -547,6 +547,11 @@ int hbfsim_amd_thermal_step(hbfsim_amd_thermal* thermal, const double* d_power,
 /* Average device time (ms) of one step in the last hbfsim_amd_thermal_step
  * call, from HIP events on its stream. */
 int hbfsim_amd_thermal_last_ms(const hbfsim_amd_thermal* thermal, float* ms);
+/* Kernel passes the last hbfsim_amd_thermal_step call launched: one per step,
+ * except that on the marching kernel with 1-4 sweeps one pass makes two steps
+ * (the power is the same in both).  A diagnostic with no counterpart in the
+ * reference: it turns last_ms into a per-pass time. */
+int hbfsim_amd_thermal_last_launches(const hbfsim_amd_thermal* thermal, uint64_t* launches);
 void hbfsim_amd_thermal_destroy(hbfsim_amd_thermal* thermal);
 
 /* Thermal-coupled refresh and throttling.  The grid is stepped once per

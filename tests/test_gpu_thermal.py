@@ -37,6 +37,10 @@ def grid_kw(**kw):
     ((1030, 260, 8), 4, 3), ((2048, 128, 8), 3, 2), ((700, 3000, 1), 2, 2),
     ((520, 260, 16), 4, 2), ((300, 1200, 6), 1, 3), ((129, 2100, 8), 4, 1),
     ((1100, 1000, 2), 4, 2),
+    # odd pass counts of 3 (three two-step passes; two and a single step):
+    # the passes route through a second scratch buffer and the last writes
+    # the caller's array
+    ((1030, 260, 8), 4, 6), ((700, 3000, 1), 2, 5),
     # 5-8 sweeps march with up to 8 layers (48-54 written columns per strip)
     ((600, 900, 4), 5, 1), ((700, 3000, 1), 6, 2), ((520, 520, 8), 7, 1),
     ((1030, 260, 8), 8, 2)])
