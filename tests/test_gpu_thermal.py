@@ -208,16 +208,19 @@ def test_coupled_run_matches_oracle():
     assert_coupled_equal(got, want)
 
 
-def test_coupled_run_full_grid_prefix():
-    """The config-4 grid and parameters on the first 300 windows of the
-    config-4 trace."""
-    n = 300 * 4000  # 4 lines per ns issued -> 300 windows of 1 us
+@pytest.mark.parametrize("windows", [300, 1301])
+def test_coupled_run_full_grid_prefix(windows):
+    """The config-4 grid and parameters on the first 300 (one launch per
+    window) or 1,301 windows of the config-4 trace (five replays of the
+    chain's 256-window captured chunk, then 21 windows launched one by one,
+    an odd count that ends in the scratch buffer)."""
+    n = windows * 4000  # 4 lines per ns issued -> one window per 1 us
     rec, ranges = c4_case(n, layers=3)
     opts = dict(w.C4_RELIABILITY)
     age0 = w.staggered_ages(64, opts["retention_ps"])
     t0 = np.full(64 * 64 * 8, 318.15)
     got, want = run_pair(rec, ranges, dict(w.C4_GRID), opts, age0, t0)
-    assert want["rep"]["windows"] == 300
+    assert want["rep"]["windows"] == windows
     assert want["rep"]["refreshes"] > 0
     assert_coupled_equal(got, want)
 
