@@ -2372,6 +2372,57 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
     const std::uint64_t back = static_cast<std::uint64_t>(63 - lane);
     const std::uint64_t P = a.contention ? lead : q.issue;
     const std::uint64_t D0 = umax64(lead, top - 63 * v.x);
+    // Status bytes four steps at a time: 4 for a page-register hit (every
+    // record but a sensing lane 0), 0 otherwise; with hybrid sampling, 8 more
+    // for each record the sampler picks (record j of step k has sequence
+    // number seq0 + 64 k + j and key (page, range, read), as in the general
+    // path).  Lane l takes records 4 (l & 15) .. + 3 of step k + (l >> 4).
+    // They are made next to the completion stores of the same four steps, so
+    // that the sampler's hashes run while those stores drain.
+    const bool stat = status != nullptr || a.hybrid;
+    const bool words = status != nullptr && (reinterpret_cast<std::uintptr_t>(status) & 3u) == 0;
+    const auto status4 = [&](int k) {
+        const int ks = k + (lane >> 4);
+        // every lane takes part in the shuffles
+        const std::uint32_t kp = static_cast<std::uint32_t>(
+            __shfl(static_cast<int>(q.page1), ks < q.n ? ks : 0));
+        const std::uint32_t kr = static_cast<std::uint32_t>(
+            __shfl(static_cast<int>(q.rid), ks < q.n ? ks : 0));
+        if (ks < q.n) {
+            const std::uint32_t r0 = 4u * static_cast<std::uint32_t>(lane & 15);
+            const bool sense = r0 == 0 && ((hits >> ks) & 1u) == 0;
+            std::uint32_t word = sense ? 0x04040400u : 0x04040404u;
+            if (a.hybrid) {
+                const std::uint64_t key =
+                    ((static_cast<std::uint64_t>(kp) - 1) << a.page_shift) ^
+                    (static_cast<std::uint64_t>(kr) << 32);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const std::uint64_t qn =
+                        seq0 + static_cast<std::uint64_t>(ks) * kWave + r0 + u;
+                    const bool sampled =
+                        qn < a.hybrid_warmup ||
+                        (a.hybrid_threshold != 0 && mix64(qn ^ key) <= a.hybrid_threshold);
+                    if (sampled) {
+                        word |= 8u << (8 * u);
+                        ++t.n_hyb;
+                    }
+                }
+            }
+            if (status != nullptr) {
+                std::uint8_t* out =
+                    status + q.first + static_cast<std::size_t>(ks) * kWave + r0;
+                if (words) {
+                    *reinterpret_cast<std::uint32_t*>(out) = word;
+                } else {
+                    out[0] = static_cast<std::uint8_t>(word);
+                    out[1] = static_cast<std::uint8_t>(word >> 8);
+                    out[2] = static_cast<std::uint8_t>(word >> 16);
+                    out[3] = static_cast<std::uint8_t>(word >> 24);
+                }
+            }
+        }
+    };
     std::uint64_t* out = completion + q.first + lane;
     wait_vector_loads();
     const bool z = lane == 0;
@@ -2391,11 +2442,18 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
                 const std::uint64_t done = umax64(pk[u], tk[u] - xm);
                 out[static_cast<std::size_t>(k + u) * kWave] = z ? dk[u] : done;
             }
+            if (stat) {
+                status4(k);
+            }
         }
+        const int kt = k;
         for (; k < q.n; ++k) {
             const std::uint64_t done = umax64(shfl64(P, k), shfl64(top, k) - xm);
             const std::uint64_t d = shfl64(D0, k);
             out[static_cast<std::size_t>(k) * kWave] = z ? d : done;
+        }
+        if (stat && kt < q.n) {
+            status4(kt);
         }
     } else {
         for (int k = 0; k < q.n; ++k) {
@@ -2404,54 +2462,9 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
             const std::uint64_t d = shfl64(D0, k);
             out[static_cast<std::size_t>(k) * kWave] = z ? d : done;
         }
-    }
-    // Status bytes four steps at a time: 4 for a page-register hit (every
-    // record but a sensing lane 0), 0 otherwise; with hybrid sampling, 8 more
-    // for each record the sampler picks (record j of step k has sequence
-    // number seq0 + 64 k + j and key (page, range, read), as in the general
-    // path).  Lane l takes records 4 (l & 15) .. + 3 of step k + (l >> 4).
-    if (status != nullptr || a.hybrid) {
-        const bool words = status != nullptr && (reinterpret_cast<std::uintptr_t>(status) & 3u) == 0;
-        for (int k = 0; k < q.n; k += 4) {
-            const int ks = k + (lane >> 4);
-            // every lane takes part in the shuffles
-            const std::uint32_t kp = static_cast<std::uint32_t>(
-                __shfl(static_cast<int>(q.page1), ks < q.n ? ks : 0));
-            const std::uint32_t kr = static_cast<std::uint32_t>(
-                __shfl(static_cast<int>(q.rid), ks < q.n ? ks : 0));
-            if (ks < q.n) {
-                const std::uint32_t r0 = 4u * static_cast<std::uint32_t>(lane & 15);
-                const bool sense = r0 == 0 && ((hits >> ks) & 1u) == 0;
-                std::uint32_t word = sense ? 0x04040400u : 0x04040404u;
-                if (a.hybrid) {
-                    const std::uint64_t key =
-                        ((static_cast<std::uint64_t>(kp) - 1) << a.page_shift) ^
-                        (static_cast<std::uint64_t>(kr) << 32);
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const std::uint64_t qn =
-                            seq0 + static_cast<std::uint64_t>(ks) * kWave + r0 + u;
-                        const bool sampled =
-                            qn < a.hybrid_warmup ||
-                            (a.hybrid_threshold != 0 && mix64(qn ^ key) <= a.hybrid_threshold);
-                        if (sampled) {
-                            word |= 8u << (8 * u);
-                            ++t.n_hyb;
-                        }
-                    }
-                }
-                if (status != nullptr) {
-                    std::uint8_t* out =
-                        status + q.first + static_cast<std::size_t>(ks) * kWave + r0;
-                    if (words) {
-                        *reinterpret_cast<std::uint32_t*>(out) = word;
-                    } else {
-                        out[0] = static_cast<std::uint8_t>(word);
-                        out[1] = static_cast<std::uint8_t>(word >> 8);
-                        out[2] = static_cast<std::uint8_t>(word >> 16);
-                        out[3] = static_cast<std::uint8_t>(word >> 24);
-                    }
-                }
+        if (stat) {
+            for (int k = 0; k < q.n; k += 4) {
+                status4(k);
             }
         }
     }
