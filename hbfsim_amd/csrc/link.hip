@@ -1,8 +1,8 @@
 // link.hip -- the UCIe Streaming / AoU link (src/ucie/link.cpp:1-203) for
 // batches of independent links on gfx950 (MI355X).
 //
-// One thread runs one link's event loop: AR requests (3 AoU granules) and R
-// returns (14) queue per direction; a direction sends a Format 6 flit of 48
+// Two lanes run one link's event loop, one per direction: AR requests (3
+// AoU granules) and R returns (14) queue per direction; a direction sends a Format 6 flit of 48
 // granules every 32 / GT ns while it has work; a message's granules are all
 // reserved against the sender's credits at its MsgStart; a delivered message
 // is consumed a fixed delay later by the link's caller, which releases its
@@ -138,247 +138,257 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_link_split(LinkArgs a)
 constexpr std::uint32_t kLdsMsgSlots = 16;
 constexpr std::uint32_t kLdsFlitSlots = 8;
 
+// The partner lane's value (lane ^ 1: the same link's other direction), by
+// DPP quad_perm [1, 0, 3, 2].  Both lanes of a link run the loop in step.
+__device__ __forceinline__ std::uint32_t pair32(std::uint32_t v)
+{
+    return static_cast<std::uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xB1, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ std::uint64_t pair64(std::uint64_t v)
+{
+    return (static_cast<std::uint64_t>(pair32(static_cast<std::uint32_t>(v >> 32))) << 32) |
+           pair32(static_cast<std::uint32_t>(v));
+}
+
+// Two lanes per link, one per direction (lane & 1: 0 AR, 1 R).  The
+// directions meet only through the event time, the grants a delivered flit
+// carries to the other direction's credits, the consumes that fill the
+// other direction's pending grant, and errors: those cross between the two
+// lanes once per step, at the points where the reference's step() would
+// read them, and everything else is the lane's own direction.
 template <bool kLds>
 __global__ __launch_bounds__(kLinkThreads) void k_link(LinkArgs a)
 {
-    __shared__ std::uint64_t s_msg_t[kLds ? 2 * kLdsMsgSlots * kLinkThreads : 1];
-    __shared__ std::uint32_t s_msg_i[kLds ? 2 * kLdsMsgSlots * kLinkThreads : 1];
-    __shared__ std::uint64_t s_fl_t[kLds ? 2 * kLdsFlitSlots * kLinkThreads : 1];
-    __shared__ std::uint32_t s_fl_i[kLds ? 2 * kLdsFlitSlots * kLinkThreads : 1];
+    __shared__ std::uint64_t s_msg_t[kLds ? kLdsMsgSlots * kLinkThreads : 1];
+    __shared__ std::uint32_t s_msg_i[kLds ? kLdsMsgSlots * kLinkThreads : 1];
+    __shared__ std::uint64_t s_fl_t[kLds ? kLdsFlitSlots * kLinkThreads : 1];
+    __shared__ std::uint32_t s_fl_i[kLds ? kLdsFlitSlots * kLinkThreads : 1];
     const std::uint32_t lane = threadIdx.x;
-    const std::uint32_t l = blockIdx.x * kLinkThreads + lane;
+    const std::uint32_t d = lane & 1u;
+    const std::uint32_t l = blockIdx.x * (kLinkThreads / 2) + (lane >> 1);
     if (l >= a.links) {
-        return;
+        return;  // both lanes of the link
     }
     const std::uint64_t ar = a.n_ar[l];
     if (ar == kBadLink) {
         return;  // refused by the split pass
     }
     const std::uint64_t b = a.first[l], e = a.first[l + 1];
-    const std::uint64_t base[2] = {b, b + ar};     // each direction's list
+    const std::uint64_t base = d == 0 ? b : b + ar;  // this direction's list
     // the split pass refuses links of 2^32 messages or more
-    const std::uint32_t count[2] = {static_cast<std::uint32_t>(ar),
-                                    static_cast<std::uint32_t>(e - b - ar)};
-    const std::uint32_t size[2] = {3u, 14u};
+    const std::uint32_t count = static_cast<std::uint32_t>(d == 0 ? ar : e - b - ar);
+    const std::uint32_t size = d == 0 ? 3u : 14u;    // granules of this direction's messages
+    const std::uint32_t osize = d == 0 ? 14u : 3u;   // and of the other's
+    const std::uint64_t delay = a.delay[d];
+    const std::uint32_t credit0 = a.credit0[d];
     const std::uint32_t M = a.max_accepted;
-    // flit slot s of direction d: LDS lane-minor (conflict-free), HBM link-major
-    auto fl_t = [&](std::uint32_t d, std::uint32_t s) -> std::uint64_t& {
+    // flit slot s: LDS lane-minor (conflict-free), HBM link-major
+    auto fl_t = [&](std::uint32_t s) -> std::uint64_t& {
         if constexpr (kLds) {
-            return s_fl_t[(d * kLdsFlitSlots + s) * kLinkThreads + lane];
+            return s_fl_t[s * kLinkThreads + lane];
         } else {
             return a.ring_time[(2ull * l + d) * a.ring + s];
         }
     };
-    auto fl_i = [&](std::uint32_t d, std::uint32_t s) -> std::uint32_t& {
+    auto fl_i = [&](std::uint32_t s) -> std::uint32_t& {
         if constexpr (kLds) {
-            return s_fl_i[(d * kLdsFlitSlots + s) * kLinkThreads + lane];
+            return s_fl_i[s * kLinkThreads + lane];
         } else {
             return a.ring_info[(2ull * l + d) * a.ring + s];
         }
     };
-    // message k of direction d (LDS slot s = k mod max_accepted)
-    auto msg_t = [&](std::uint32_t d, std::uint32_t k, std::uint32_t s) -> std::uint64_t& {
+    // message k (LDS slot s = k mod max_accepted)
+    auto msg_t = [&](std::uint32_t k, std::uint32_t s) -> std::uint64_t& {
         if constexpr (kLds) {
-            return s_msg_t[(d * kLdsMsgSlots + s) * kLinkThreads + lane];
+            return s_msg_t[s * kLinkThreads + lane];
         } else {
-            return a.part_time[base[d] + k];
+            return a.part_time[base + k];
         }
     };
-    auto msg_i = [&](std::uint32_t d, std::uint32_t k, std::uint32_t s) -> std::uint32_t {
+    auto msg_i = [&](std::uint32_t k, std::uint32_t s) -> std::uint32_t {
         if constexpr (kLds) {
-            return s_msg_i[(d * kLdsMsgSlots + s) * kLinkThreads + lane];
+            return s_msg_i[s * kLinkThreads + lane];
         } else {
-            return a.part_index[base[d] + k];
+            return a.part_index[base + k];
         }
     };
     auto wrap = [&](std::uint32_t s) -> std::uint32_t { return s + 1 == M ? 0u : s + 1; };
-    // per direction: messages admitted, arrived, sent, delivered, consumed,
-    // with their LDS slots; the next admission's ready time and index
-    std::uint32_t n_adm[2] = {0, 0}, n_arr[2] = {0, 0}, n_done[2] = {0, 0};
-    std::uint32_t n_dlv[2] = {0, 0}, n_con[2] = {0, 0};
-    std::uint32_t s_adm[2] = {0, 0}, s_arr[2] = {0, 0}, s_dlv[2] = {0, 0}, s_con[2] = {0, 0};
-    std::uint64_t next_ready[2] = {0, 0};
-    std::uint32_t next_index[2] = {0, 0};
-    std::uint64_t last_ready[2] = {0, 0};
-    std::uint32_t h_rem[2], h_started[2] = {0, 0};
-    std::uint64_t cursor[2] = {0, 0};
-    std::uint32_t credits[2] = {a.credit0[0], a.credit0[1]};
-    std::uint32_t gp[2] = {0, 0};  // credits to grant back on direction d's flits
-    std::uint32_t rh[2] = {0, 0}, rn[2] = {0, 0};  // flit ring head, entries
-    std::uint64_t flits[2] = {0, 0}, gran[2] = {0, 0}, credit_only[2] = {0, 0};
-    for (std::uint32_t d = 0; d < 2; ++d) {
-        h_rem[d] = size[d];
-        if (count[d] != 0) {
-            next_ready[d] = a.part_time[base[d]];
-            next_index[d] = kLds ? a.part_index[base[d]] : 0u;
-        }
+    // messages admitted, arrived, sent, delivered, consumed, with their LDS
+    // slots; the next admission's ready time and index
+    std::uint32_t n_adm = 0, n_arr = 0, n_done = 0, n_dlv = 0, n_con = 0;
+    std::uint32_t s_adm = 0, s_arr = 0, s_dlv = 0, s_con = 0;
+    std::uint64_t next_ready = 0, last_ready = 0;
+    std::uint32_t next_index = 0;
+    std::uint32_t h_rem = size, h_started = 0;
+    std::uint64_t cursor = 0;
+    std::uint32_t credits = credit0;
+    std::uint32_t gp = 0;  // credits to grant back on this direction's flits
+    std::uint32_t rh = 0, rn = 0;  // flit ring head, entries
+    std::uint64_t flits = 0, gran = 0, credit_only = 0;
+    if (count != 0) {
+        next_ready = a.part_time[base];
+        next_index = kLds ? a.part_index[base] : 0u;
     }
     std::uint64_t now = 0;
     std::uint32_t err = 0;
     const std::uint64_t cap = 64ull * (e - b) + 4096;
-    for (std::uint64_t it = 0; err == 0; ++it) {
+    for (std::uint64_t it = 0;; ++it) {
         if (it >= cap) {
             err = 2;
             break;
         }
-        // the caller admits waiting messages while a direction has room
-        for (std::uint32_t d = 0; d < 2; ++d) {
-            while (n_adm[d] < count[d] && n_adm[d] - n_con[d] < M) {
-                const std::uint64_t r = next_ready[d];
-                if (r < last_ready[d]) {
-                    err = 1;  // a direction's ready times must not decrease
-                }
-                last_ready[d] = r;
-                msg_t(d, n_adm[d], s_adm[d]) = r > now ? r : now;
+        // the caller admits waiting messages while the direction has room
+        while (n_adm < count && n_adm - n_con < M) {
+            const std::uint64_t r = next_ready;
+            if (r < last_ready) {
+                err = 1;  // a direction's ready times must not decrease
+            }
+            last_ready = r;
+            msg_t(n_adm, s_adm) = r > now ? r : now;
+            if constexpr (kLds) {
+                s_msg_i[s_adm * kLinkThreads + lane] = next_index;
+                s_adm = wrap(s_adm);
+            }
+            ++n_adm;
+            if (n_adm < count) {  // fetch the next admission ahead of its use
+                next_ready = a.part_time[base + n_adm];
                 if constexpr (kLds) {
-                    s_msg_i[(d * kLdsMsgSlots + s_adm[d]) * kLinkThreads + lane] = next_index[d];
-                    s_adm[d] = wrap(s_adm[d]);
-                }
-                ++n_adm[d];
-                if (n_adm[d] < count[d]) {  // fetch the next admission ahead of its use
-                    next_ready[d] = a.part_time[base[d] + n_adm[d]];
-                    if constexpr (kLds) {
-                        next_index[d] = a.part_index[base[d] + n_adm[d]];
-                    }
+                    next_index = a.part_index[base + n_adm];
                 }
             }
         }
-        if (err != 0) {
+        if ((err | pair32(err)) != 0) {
             break;
         }
-        // the next event
+        // the next event: the least over both directions
         bool any = false;
         std::uint64_t t = ~0ull;
-        for (std::uint32_t d = 0; d < 2; ++d) {
-            if (n_arr[d] < n_adm[d]) {
-                const std::uint64_t x = msg_t(d, n_arr[d], s_arr[d]);
-                t = x < t ? x : t;
-                any = true;
-            }
-            if (rn[d] != 0) {
-                const std::uint64_t x = fl_t(d, rh[d]);
-                t = x < t ? x : t;
-                any = true;
-            }
-            if (n_con[d] < n_dlv[d]) {
-                const std::uint64_t dv = msg_t(d, n_con[d], s_con[d]);
-                if (dv > ~0ull - a.delay[d]) {
-                    err = 1;
-                }
-                const std::uint64_t x = dv + a.delay[d];
-                t = x < t ? x : t;
-                any = true;
-            }
-            if (cursor[d] > now && (n_arr[d] > n_done[d] || gp[d] != 0)) {
-                t = cursor[d] < t ? cursor[d] : t;
-                any = true;
-            }
+        if (n_arr < n_adm) {
+            const std::uint64_t x = msg_t(n_arr, s_arr);
+            t = x < t ? x : t;
+            any = true;
         }
-        if (err != 0 || !any) {
+        if (rn != 0) {
+            const std::uint64_t x = fl_t(rh);
+            t = x < t ? x : t;
+            any = true;
+        }
+        if (n_con < n_dlv) {
+            const std::uint64_t dv = msg_t(n_con, s_con);
+            if (dv > ~0ull - delay) {
+                err = 1;
+            }
+            const std::uint64_t x = dv + delay;
+            t = x < t ? x : t;
+            any = true;
+        }
+        if (cursor > now && (n_arr > n_done || gp != 0)) {
+            t = cursor < t ? cursor : t;
+            any = true;
+        }
+        const std::uint64_t tp = pair64(t);
+        const std::uint32_t anyp = pair32(any ? 1u : 0u);
+        if ((err | pair32(err)) != 0 || (!any && anyp == 0)) {
             break;
         }
-        now = t;
+        now = t < tp ? t : tp;
         // every arrival, delivery and consume scheduled at `now`; consumes
         // of messages this step delivers wait for the next step
-        const std::uint32_t dlv_before[2] = {n_dlv[0], n_dlv[1]};
-        for (std::uint32_t d = 0; d < 2; ++d) {
-            while (n_arr[d] < n_adm[d] && msg_t(d, n_arr[d], s_arr[d]) == now) {
-                ++n_arr[d];
-                s_arr[d] = wrap(s_arr[d]);
-            }
+        const std::uint32_t dlv_before = n_dlv;
+        while (n_arr < n_adm && msg_t(n_arr, s_arr) == now) {
+            ++n_arr;
+            s_arr = wrap(s_arr);
         }
-        for (std::uint32_t d = 0; d < 2; ++d) {
-            if (rn[d] != 0 && fl_t(d, rh[d]) == now) {
-                const std::uint32_t info = fl_i(d, rh[d]);
-                const std::uint32_t grant = info >> 16, done = info & 0xffffu;
-                const std::uint32_t o = d ^ 1u;  // the grant is for the other direction
-                if (grant > a.credit0[o] - credits[o]) {
-                    err = 1;
-                }
-                credits[o] += grant;
-                for (std::uint32_t k = 0; k < done; ++k) {
-                    msg_t(d, n_dlv[d], s_dlv[d]) = now;
-                    a.delivered[b + msg_i(d, n_dlv[d], s_dlv[d])] = now;
-                    ++n_dlv[d];
-                    s_dlv[d] = wrap(s_dlv[d]);
-                }
-                rh[d] = rh[d] + 1 == a.ring ? 0u : rh[d] + 1;
-                --rn[d];
+        std::uint32_t g_out = 0;  // the grant this direction's flit brings the other
+        if (rn != 0 && fl_t(rh) == now) {
+            const std::uint32_t info = fl_i(rh);
+            const std::uint32_t done = info & 0xffffu;
+            g_out = info >> 16;
+            for (std::uint32_t k = 0; k < done; ++k) {
+                msg_t(n_dlv, s_dlv) = now;
+                a.delivered[b + msg_i(n_dlv, s_dlv)] = now;
+                ++n_dlv;
+                s_dlv = wrap(s_dlv);
             }
+            rh = rh + 1 == a.ring ? 0u : rh + 1;
+            --rn;
         }
-        for (std::uint32_t d = 0; d < 2; ++d) {
-            while (n_con[d] < dlv_before[d] && msg_t(d, n_con[d], s_con[d]) + a.delay[d] == now) {
-                const std::uint32_t o = d ^ 1u;
-                if (gp[o] > 65535u - size[d]) {
-                    err = 1;
-                    break;
-                }
-                gp[o] += size[d];
-                ++n_con[d];
-                s_con[d] = wrap(s_con[d]);
-            }
+        std::uint32_t c_out = 0;  // consumes, each a grant of `size` for the other
+        while (n_con < dlv_before && msg_t(n_con, s_con) + delay == now) {
+            ++c_out;
+            ++n_con;
+            s_con = wrap(s_con);
         }
-        if (err != 0) {
+        const std::uint32_t g_in = pair32(g_out);
+        const std::uint32_t c_in = pair32(c_out);
+        if (g_in > credit0 - credits) {
+            err = 1;
+        }
+        credits += g_in;
+        if (static_cast<std::uint64_t>(gp) + static_cast<std::uint64_t>(c_in) * osize > 65535u) {
+            err = 1;
+        } else {
+            gp += c_in * osize;
+        }
+        if ((err | pair32(err)) != 0) {
             break;
         }
-        // both directions send (link.cpp send_ready)
-        for (std::uint32_t d = 0; d < 2; ++d) {
-            if (cursor[d] > now) {
-                continue;
-            }
+        // this direction sends (link.cpp send_ready)
+        if (cursor <= now) {
             std::uint32_t used = 0, done = 0;
-            while (n_arr[d] > n_done[d] && used < 48) {
-                if (!h_started[d]) {
-                    if (credits[d] < size[d]) {
+            while (n_arr > n_done && used < 48) {
+                if (!h_started) {
+                    if (credits < size) {
                         break;
                     }
-                    credits[d] -= size[d];
-                    h_started[d] = 1;
+                    credits -= size;
+                    h_started = 1;
                 }
-                const std::uint32_t frag = 48 - used < h_rem[d] ? 48 - used : h_rem[d];
+                const std::uint32_t frag = 48 - used < h_rem ? 48 - used : h_rem;
                 used += frag;
-                h_rem[d] -= frag;
-                if (h_rem[d] == 0) {
+                h_rem -= frag;
+                if (h_rem == 0) {
                     ++done;
-                    ++n_done[d];
-                    h_rem[d] = size[d];
-                    h_started[d] = 0;
+                    ++n_done;
+                    h_rem = size;
+                    h_started = 0;
                 }
             }
-            const std::uint32_t grant = legal_grant(gp[d]);
-            if (used == 0 && grant == 0) {
-                continue;
+            const std::uint32_t grant = legal_grant(gp);
+            if (used != 0 || grant != 0) {
+                gp -= grant;
+                if (now > ~0ull - a.ser || now + a.ser > ~0ull - a.prop || rn == a.ring) {
+                    err = 1;
+                } else {
+                    cursor = now + a.ser;
+                    const std::uint32_t slot = rh + rn < a.ring ? rh + rn : rh + rn - a.ring;
+                    fl_t(slot) = cursor + a.prop;
+                    fl_i(slot) = (grant << 16) | done;
+                    ++rn;
+                    ++flits;
+                    gran += used;
+                    credit_only += used == 0 ? 1u : 0u;
+                }
             }
-            gp[d] -= grant;
-            if (now > ~0ull - a.ser || now + a.ser > ~0ull - a.prop || rn[d] == a.ring) {
-                err = 1;
-                break;
-            }
-            cursor[d] = now + a.ser;
-            const std::uint32_t slot = rh[d] + rn[d] < a.ring ? rh[d] + rn[d]
-                                                               : rh[d] + rn[d] - a.ring;
-            fl_t(d, slot) = cursor[d] + a.prop;
-            fl_i(d, slot) = (grant << 16) | done;
-            ++rn[d];
-            ++flits[d];
-            gran[d] += used;
-            credit_only[d] += used == 0 ? 1u : 0u;
+        }
+        if ((err | pair32(err)) != 0) {
+            break;
         }
     }
     if (err != 0) {
         atomicMax(a.error, err);
     }
-    for (std::uint32_t d = 0; d < 2; ++d) {
-        std::uint64_t* c = a.counters + (2ull * l + d) * 8;
-        c[0] = flits[d];
-        c[1] = 256 * flits[d];
-        c[2] = 2 * flits[d];
-        c[3] = 4 * flits[d];
-        c[4] = 10 * flits[d];
-        c[5] = 5 * gran[d];
-        c[6] = 5 * (48 * flits[d] - gran[d]);
-        c[7] = credit_only[d];
-    }
+    std::uint64_t* c = a.counters + (2ull * l + d) * 8;
+    c[0] = flits;
+    c[1] = 256 * flits;
+    c[2] = 2 * flits;
+    c[3] = 4 * flits;
+    c[4] = 10 * flits;
+    c[5] = 5 * gran;
+    c[6] = 5 * (48 * flits - gran);
+    c[7] = credit_only;
 }
 
 // The split lists and flit rings of the last, largest call, kept per device
@@ -484,7 +494,7 @@ int link_run(const hbfsim_amd_link_profile& p, const std::uint64_t* d_first, std
         hipLaunchKernelGGL(k_link_split, dim3((links + kSplitWaves - 1) / kSplitWaves),
                            dim3(kSplitWaves * 64), 0, stream, a);
         err = hipGetLastError();
-        const dim3 grid((links + kLinkThreads - 1) / kLinkThreads);
+        const dim3 grid((links + kLinkThreads / 2 - 1) / (kLinkThreads / 2));  // two lanes a link
         if (err == hipSuccess) {
             if (lds) {
                 hipLaunchKernelGGL(k_link<true>, grid, dim3(kLinkThreads), 0, stream, a);
