@@ -1562,8 +1562,8 @@ __host__ __device__ __forceinline__ std::size_t summary_match_offset(const KArgs
 // class), the (max,+) map of the records after it, and the last page; per
 // channel the map of all its records.  Pages are stored as page + 1 in 32
 // bits (capacity / page_bytes < 2^32 is checked on the host).
-template <bool kRefresh, bool kHits, bool kPacked = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 : 1))) void k_summary(KArgs a, const void* rec, std::size_t n,
+template <bool kRefresh, bool kHits, bool kPacked = false, bool kDeep = false>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (kDeep ? 2 : 3) : 1))) void k_summary(KArgs a, const void* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
                                                 MaskWord* tmask, ChanSum* csum,
                                                 std::uint64_t* tile_count,
@@ -1596,7 +1596,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     // packed records keep kSumPipe steps too, which leaves registers for a
     // third wave per SIMD: as fast on streamed steps, a quarter faster on
     // general ones than twice as deep at two waves)
-    constexpr int kDepth = kHits ? kPipe : kSumPipe;
+    // (kDeep: packed records where LDS already holds the pass at two waves
+    // per SIMD, whose registers then allow twice the steps in flight)
+    constexpr int kDepth = kHits ? kPipe : (kDeep ? 2 * kSumPipe : kSumPipe);
     constexpr std::size_t kSpan = static_cast<std::size_t>(kDepth) * kWave;
     using Pipe = std::conditional_t<kPacked, PackedPipeT<kDepth>, RecordPipeT<kDepth>>;
     Pipe pipe;
@@ -4222,9 +4224,11 @@ std::size_t lds_apply(const KArgs& a)
 // The lane-matching tables go where they cost neither per-record pass any
 // waves per CU (gfx950: 160 KB of LDS per CU; both passes run at most three
 // waves per SIMD).
+constexpr std::size_t kLdsPerCuBytes = 160 * 1024;  // gfx950
+
 void choose_match(KArgs& a)
 {
-    constexpr std::size_t kLdsPerCu = 160 * 1024;
+    constexpr std::size_t kLdsPerCu = kLdsPerCuBytes;
     constexpr std::size_t kMaxWaves = 12;
     const auto waves = [&](std::size_t bytes) {
         const std::size_t w = bytes == 0 ? kMaxWaves : kLdsPerCu / bytes;
@@ -5037,6 +5041,10 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     } else if (refresh_records) {
         hipLaunchKernelGGL((k_summary<true, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
                            n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
+                           hits, desc);
+    } else if (packed && kLdsPerCuBytes / lds_a <= 8) {  // LDS allows at most 8 waves per CU
+        hipLaunchKernelGGL((k_summary<false, false, true, true>), grid, dim3(kWave), lds_a, stream,
+                           a, d_rec, n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     } else if (packed) {
         hipLaunchKernelGGL((k_summary<false, false, true>), grid, dim3(kWave), lds_a, stream, a,
