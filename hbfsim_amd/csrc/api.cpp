@@ -661,9 +661,7 @@ HBF_API int hbfsim_amd_run_device_packed_noalloc(hbfsim_context* c, const hbf_re
                                                  uint8_t* status, uint64_t base_ps, void* stream,
                                                  hbfsim_amd_report* report)
 {
-    if (report != nullptr) {
-        std::memset(report, 0, sizeof(*report));
-    }
+    // a refused call leaves the caller's report, like the context, untouched
     if (c == nullptr || (n != 0 && (records == nullptr || completion_ps == nullptr))) {
         return HBFSIM_INVALID_ARGUMENT;
     }

@@ -120,6 +120,11 @@ struct KArgs {
     // hybrid runs: the range id of each linear step beside its descriptor
     // (the sampler's key needs it); null otherwise
     std::uint32_t* desc_rid;
+    // set to 1 by the summary pass when some record's issue time is below its
+    // predecessor's; the carry chain then leaves the engine state untouched
+    // and the engine times the stream again from a sorted copy (null: the
+    // stream is known to be in issue order)
+    std::uint32_t* disorder;
 };
 
 // Record operations: 0 read, 1 write, and 2 refresh of media page `addr`
@@ -1440,6 +1445,17 @@ __device__ __forceinline__ StepView step_view(const KArgs& a, const std::uint64_
     return v;
 }
 
+// Issue order across a batch of linear steps (one issue time per step):
+// every step's time must be at least the one before it, the first step's at
+// least `last` (the last issue time the wave saw before the batch).
+__device__ __forceinline__ void batch_order(const LinBatch& q, int lane, std::uint64_t& last,
+                                            bool& back)
+{
+    const std::uint64_t prev = shfl64(q.issue, lane == 0 ? 0 : lane - 1);
+    back = back || __ballot(lane < q.n && q.issue < (lane == 0 ? last : prev)) != 0;
+    last = readlane64(q.issue, q.n - 1);
+}
+
 // Folds a batch of linear steps into the tile summary: the per-record fold
 // of the general path applied to whole steps.  A step after another record of
 // its plane has plane map (sense, issue + sense) -- lane 0 senses unless its
@@ -1592,6 +1608,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
     // set-up loads and the first group of records are in flight together
     const FenceRegs fr = fetch_fences(a, lane);
     const std::uint64_t xv = fetch_xfer(a, lane);
+    // The record before the tile: every record's issue time must be at least
+    // its predecessor's for stream position to be the service order.  Steps
+    // check their records against the last issue time seen (wave-uniform);
+    // any that goes back sets a.disorder.
+    std::uint64_t last_issue = 0;
+    if (begin > 0) {
+        last_issue = base_ps + (kPacked ? (static_cast<const hbf_record16*>(rec)[begin - 1].issue_op &
+                                           ((1ull << 56) - 1))
+                                        : static_cast<const hbf_record32*>(rec)[begin - 1].issue_ps);
+    }
+    bool disorder = false;
     // (the page-register variant takes no linear groups and keeps 4 deep;
     // packed records keep kSumPipe steps too, which leaves registers for a
     // third wave per SIMD: as fast on streamed steps, a quarter faster on
@@ -1653,6 +1680,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
                 q.push_group(gl, g, rcu.id);
                 if (q.n == kWave || gend >= end) {
+                    batch_order(q, lane, last_issue, disorder);
                     fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
                                  mt_p, mt_c);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
@@ -1682,6 +1710,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
                     q.push(lp, li, lb, s, rcu.id);
                 }
                 if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= end)) {
+                    batch_order(q, lane, last_issue, disorder);
                     fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
                                  mt_p, mt_c);
                     modeled += static_cast<std::uint64_t>(q.n) * kWave;
@@ -1706,6 +1735,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             uint4 x, y;
             step_records(st, lane, x, y);
             Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
+            {
+                const std::uint64_t prev = shfl64(d.issue, lane == 0 ? 0 : lane - 1);
+                const bool back = valid && d.issue < (lane == 0 ? last_issue : prev);
+                disorder = disorder || __ballot(back) != 0;
+                const std::uint64_t vmask = __ballot(valid);  // lanes 0 .. k
+                last_issue = readlane64(d.issue, 63 - __clzll(static_cast<long long>(vmask)));
+            }
             if (!kPacked && a.lead != nullptr && valid && a.lead[i] != 0) {
                 d.cls = kClsFollower;
             }
@@ -1803,6 +1839,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
     write_descs(desc, a.desc_rid, dq, lane);
     if (desc != nullptr) {
         flush_zero();
+    }
+    if (disorder && a.disorder != nullptr && lane == 0) {
+        *a.disorder = 1u;
     }
     __syncthreads();
     // Only planes the tile touched get a summary, packed in plane order; the
@@ -2073,6 +2112,9 @@ __global__ __launch_bounds__(kMidBlock) void k_carry_mid(
     __shared__ std::uint64_t next[2];
     const std::uint32_t r = blockIdx.x;
     const int tid = threadIdx.x;
+    // a stream whose issue time goes back is timed again from a sorted copy:
+    // this run then leaves the engine state as it found it
+    const bool commit = a.disorder == nullptr || *a.disorder == 0u;
     if (r < a.Rp) {
         std::uint64_t busy = st_pbusy[r];
         std::uint64_t tag1 = st_ptag[static_cast<std::size_t>(r) * 2];
@@ -2112,7 +2154,7 @@ __global__ __launch_bounds__(kMidBlock) void k_carry_mid(
             tag1 = next[1];
             __syncthreads();
         }
-        if (tid == 0) {
+        if (tid == 0 && commit) {
             st_pbusy[r] = busy;
             st_ptag[static_cast<std::size_t>(r) * 2] = tag1;
             ptotal[r] += total;
@@ -2144,7 +2186,7 @@ __global__ __launch_bounds__(kMidBlock) void k_carry_mid(
             busy = next[0];
             __syncthreads();
         }
-        if (tid == 0) {
+        if (tid == 0 && commit) {
             st_cbusy[c] = busy;
             ctotal[c] += total;
         }
@@ -2166,7 +2208,7 @@ __global__ __launch_bounds__(kMidBlock) void k_carry_mid(
             seq = next[0];
             __syncthreads();
         }
-        if (tid == 0) {
+        if (tid == 0 && commit) {
             *st_seq = seq;
         }
     }
@@ -2949,7 +2991,8 @@ __device__ __forceinline__ void rep_join(int f, std::uint64_t& acc, std::uint64_
 // kRepWords partial per block.
 template <int kIn, bool kFinal>
 __global__ __launch_bounds__(256) void k_report(const std::uint64_t* in, std::size_t count,
-                                                std::size_t per, std::uint64_t* out)
+                                                std::size_t per, std::uint64_t* out,
+                                                std::uint32_t* disorder)
 {
     __shared__ std::uint64_t acc_sh[16][kRepWords];
     __shared__ std::uint64_t carry_sh[16];
@@ -2988,6 +3031,13 @@ __global__ __launch_bounds__(256) void k_report(const std::uint64_t* in, std::si
         if (kFinal) {
             if (f < 14) {
                 out[f] = f == R_LAT_HI ? acc_sh[0][f] + carry_sh[0] : acc_sh[0][f];
+            } else if (f == 14) {
+                // the run's disorder flag travels with the report, and is
+                // cleared for the next run
+                out[14] = disorder != nullptr ? *disorder : 0u;
+                if (disorder != nullptr) {
+                    *disorder = 0u;
+                }
             }
         } else {
             out[static_cast<std::size_t>(blockIdx.x) * kRepWords + f] =
@@ -3147,21 +3197,24 @@ __global__ __launch_bounds__(256) void k_follow(const hbf_record32* rec, std::si
     }
 }
 
+// The report's word 14 receives *disorder, which is then cleared (both skipped
+// when disorder is null); `rep` holds two DevReports.
 void launch_report(hipStream_t stream, const DevReport* tile_rep, std::size_t ntiles,
-                   DevReport* rep, std::uint64_t* parts)
+                   DevReport* rep, std::uint64_t* parts, std::uint32_t* disorder)
 {
     const std::size_t per = (ntiles + kRepParts - 1) / kRepParts;
     const std::size_t nparts = per == 0 ? 0 : (ntiles + per - 1) / per;
     if (nparts == 0) {
         hipLaunchKernelGGL((k_report<kRepWords, true>), dim3(1), dim3(256), 0, stream, parts,
-                           std::size_t{0}, std::size_t{1}, reinterpret_cast<std::uint64_t*>(rep));
+                           std::size_t{0}, std::size_t{1}, reinterpret_cast<std::uint64_t*>(rep),
+                           disorder);
         return;
     }
     hipLaunchKernelGGL((k_report<14, false>), dim3(static_cast<unsigned>(nparts)), dim3(256), 0,
                        stream, reinterpret_cast<const std::uint64_t*>(tile_rep), ntiles, per,
-                       parts);
+                       parts, static_cast<std::uint32_t*>(nullptr));
     hipLaunchKernelGGL((k_report<kRepWords, true>), dim3(1), dim3(256), 0, stream, parts, nparts,
-                       nparts, reinterpret_cast<std::uint64_t*>(rep));
+                       nparts, reinterpret_cast<std::uint64_t*>(rep), disorder);
 }
 
 }  // namespace
@@ -3230,9 +3283,10 @@ struct engine {
     std::uint64_t* d_ptot{nullptr};
     std::uint64_t* d_ctot{nullptr};
     std::uint64_t* d_seq{nullptr};
-    DevReport* d_rep{nullptr};
-    DevReport* h_rep{nullptr};  // pinned
+    DevReport* d_rep{nullptr};  // two: the report, then the disorder word
+    DevReport* h_rep{nullptr};  // pinned, the same two
     std::uint64_t* d_rep_parts{nullptr};  // report partials
+    std::uint32_t* d_disorder{nullptr};  // a run's records went back in time
     // scratch
     std::size_t tile_cap{0};
     PlaneSum* d_psum{nullptr};
@@ -4339,7 +4393,7 @@ std::vector<std::uint64_t> emp_service_table(const engine_config& c)
 
 int run_empirical(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_t* d_comp,
                   std::uint8_t* d_status, std::uint64_t base_ps, hipStream_t stream,
-                  hbfsim_amd_report* out)
+                  hbfsim_amd_report* out, bool in_order)
 {
     const engine_config& c = e->cfg;
     if (c.page_shift != 12 || !emp_control_valid(c)) {
@@ -4371,16 +4425,38 @@ int run_empirical(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint
     if (err == hipSuccess) err = halloc(d_final, 1);
     if (err == hipSuccess) err = halloc(d_fin, 2);
     std::uint64_t seq0 = 0, tail0 = 0;
+    std::uint32_t back = 0;
+    const std::uint32_t zero = 0;
+    if (err == hipSuccess && !in_order &&
+        order_check(d_rec, false, n, e->d_disorder, stream) != HBFSIM_OK) {
+        err = hipErrorLaunchFailure;
+    }
     if (err == hipSuccess)
         err = hipMemcpyAsync(d_svc, table.data(), table.size() * 8, hipMemcpyHostToDevice, stream);
     if (err == hipSuccess)
         err = hipMemcpyAsync(&seq0, e->d_seq, 8, hipMemcpyDeviceToHost, stream);
     if (err == hipSuccess)
         err = hipMemcpyAsync(&tail0, e->d_cbusy, 8, hipMemcpyDeviceToHost, stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(&back, e->d_disorder, 4, hipMemcpyDeviceToHost, stream);
     if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    if (err == hipSuccess && back != 0) {
+        err = hipMemcpyAsync(e->d_disorder, &zero, 4, hipMemcpyHostToDevice, stream);
+        if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    }
     if (err != hipSuccess) {
         release();
         return HBFSIM_CUDA_ERROR;
+    }
+    if (back != 0) {
+        // a record's issue time goes back: served in (issue, position) order
+        release();
+        return run_in_issue_order(
+            d_rec, false, n, d_comp, d_status, stream,
+            [&](const void* sorted, std::uint64_t* comp, std::uint8_t* status) {
+                return run_empirical(e, static_cast<const hbf_record32*>(sorted), n, comp, status,
+                                     base_ps, stream, out, true);
+            });
     }
     BState init{};
     {
@@ -4412,7 +4488,7 @@ int run_empirical(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint
                        static_cast<const std::uint64_t*>(d_svc), c.emp_program_ns * 1000ull,
                        d_comp, d_status, d_trep);
     launch_report(stream, static_cast<const DevReport*>(d_trep), ntiles, e->d_rep,
-                  e->d_rep_parts);
+                  e->d_rep_parts, nullptr);
     (void)hipEventRecord(e->ev[3], stream);
     BState fin{};
     std::uint64_t fin2[2] = {0, 0};
@@ -4716,10 +4792,11 @@ int engine_create(const engine_config& c, engine** out)
     if (err == hipSuccess) err = halloc(e->d_ptot, rp);
     if (err == hipSuccess) err = halloc(e->d_ctot, rc);
     if (err == hipSuccess) err = halloc(e->d_seq, 1);
-    if (err == hipSuccess) err = halloc(e->d_rep, 1);
+    if (err == hipSuccess) err = halloc(e->d_rep, 2);
     if (err == hipSuccess) err = halloc(e->d_rep_parts, kRepParts * kRepWords);
+    if (err == hipSuccess) err = halloc(e->d_disorder, 1);
     if (err == hipSuccess)
-        err = hipHostMalloc(reinterpret_cast<void**>(&e->h_rep), sizeof(DevReport));
+        err = hipHostMalloc(reinterpret_cast<void**>(&e->h_rep), 2 * sizeof(DevReport));
     for (int i = 0; i < 4 && err == hipSuccess; ++i) {
         err = hipEventCreate(&e->ev[i]);
     }
@@ -4760,6 +4837,7 @@ void engine_destroy(engine* e)
     hfree(e->d_seq);
     hfree(e->d_rep);
     hfree(e->d_rep_parts);
+    hfree(e->d_disorder);
     if (e->h_rep != nullptr) {
         (void)hipHostFree(e->h_rep);
     }
@@ -4789,6 +4867,7 @@ int engine_reset(engine* e)
     if (err == hipSuccess) err = hipMemset(e->d_ptot, 0, rp * 8);
     if (err == hipSuccess) err = hipMemset(e->d_ctot, 0, rc * 8);
     if (err == hipSuccess) err = hipMemset(e->d_seq, 0, 8);
+    if (err == hipSuccess) err = hipMemset(e->d_disorder, 0, 4);
     if (err == hipSuccess) err = hipDeviceSynchronize();
     e->burst = 0;
     return hip_status(err);
@@ -4800,10 +4879,12 @@ int engine_synchronize(engine* e)
     return hip_status(hipDeviceSynchronize());
 }
 
+// in_order: the records are known to be in issue order (a sorted copy), so
+// the summary pass does not watch for records that go back in time.
 int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                    std::uint64_t* d_comp, std::uint8_t* d_status, std::uint64_t base_ps,
                    void* stream_ptr, hbfsim_amd_report* out, bool refresh_records,
-                   unsigned char* ext_scratch = nullptr);
+                   unsigned char* ext_scratch = nullptr, bool in_order = false);
 
 int engine_run(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint64_t* d_comp,
                std::uint8_t* d_status, std::uint64_t base_ps, void* stream_ptr,
@@ -4824,15 +4905,12 @@ int engine_run_packed_noalloc(engine* e, const hbf_record16* d_rec, std::size_t 
                               std::uint64_t* d_comp, std::uint8_t* d_status,
                               std::uint64_t base_ps, void* stream_ptr, hbfsim_amd_report* out)
 {
-    if (out != nullptr) {
-        std::memset(out, 0, sizeof(*out));
-    }
     if (hipSetDevice(e->device) != hipSuccess) {
         return HBFSIM_CUDA_ERROR;
     }
     void* ptr = noalloc_scratch(e->device);
     if (ptr == nullptr) {
-        return HBFSIM_CUDA_ERROR;
+        return HBFSIM_UNSUPPORTED;  // the static scratch's address lookup failed
     }
     if (e->ranges_dirty) {
         return HBFSIM_UNSUPPORTED;  // uploading a changed range table allocates
@@ -4865,7 +4943,7 @@ std::uint32_t fitting_tile(const engine* e, std::size_t n, std::size_t capacity)
 int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                    std::uint64_t* d_comp, std::uint8_t* d_status, std::uint64_t base_ps,
                    void* stream_ptr, hbfsim_amd_report* out, bool refresh_records,
-                   unsigned char* ext_scratch)
+                   unsigned char* ext_scratch, bool in_order)
 {
     if (out != nullptr) {
         std::memset(out, 0, sizeof(*out));
@@ -4923,9 +5001,10 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
             return HBFSIM_UNSUPPORTED;
         }
         return run_empirical(e, static_cast<const hbf_record32*>(d_rec), n, d_comp, d_status,
-                             base_ps, stream, out);
+                             base_ps, stream, out, in_order);
     }
     KArgs a = e->args;
+    a.disorder = in_order ? nullptr : e->d_disorder;
     a.tile = e->cfg.tile != 0 ? e->cfg.tile : auto_tile(n);
     if (ext_scratch != nullptr) {
         a.tile = fitting_tile(e, n, kNoAllocScratchBytes);
@@ -5103,7 +5182,7 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                            base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq, d_comp,
                            d_status, sc.tile_rep, hits, desc);
     }
-    launch_report(stream, sc.tile_rep, ntiles, e->d_rep, e->d_rep_parts);
+    launch_report(stream, sc.tile_rep, ntiles, e->d_rep, e->d_rep_parts, e->d_disorder);
     unsigned long long h_frep[8] = {};
     if (grouping) {
         const std::size_t nb = (n + 255) / 256;
@@ -5115,17 +5194,37 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     (void)hipEventRecord(e->ev[3], stream);
     err = hipGetLastError();
     if (err == hipSuccess)
-        err = hipMemcpyAsync(e->h_rep, e->d_rep, sizeof(DevReport), hipMemcpyDeviceToHost, stream);
+        err = hipMemcpyAsync(e->h_rep, e->d_rep, sizeof(DevReport) + 8, hipMemcpyDeviceToHost,
+                             stream);
     if (err == hipSuccess && grouping)
         err = hipMemcpyAsync(h_frep, d_frep, sizeof(h_frep), hipMemcpyDeviceToHost, stream);
-    if (err == hipSuccess && k2)
+    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    const bool went_back = err == hipSuccess && e->h_rep[1].v[0] != 0;
+    // two page registers: the tags the run leaves, unless it is timed again
+    if (err == hipSuccess && k2 && !went_back) {
         err = hipMemcpyAsync(e->d_ptag, k2_tags.data(), k2_tags.size() * 8, hipMemcpyHostToDevice,
                              stream);
-    if (err == hipSuccess) err = hipStreamSynchronize(stream);
+        if (err == hipSuccess) err = hipStreamSynchronize(stream);
+    }
     hfree(d_hits);
     free_group();
     if (err != hipSuccess) {
         return HBFSIM_CUDA_ERROR;
+    }
+    if (went_back) {
+        // Some record's issue time went back: the engine state is as the run
+        // found it.  The stream is served in (issue time, position) order,
+        // from a sorted copy, which the entry point without allocation
+        // cannot make.
+        if (ext_scratch != nullptr) {
+            return HBFSIM_INVALID_ARGUMENT;
+        }
+        return run_in_issue_order(
+            d_rec, packed, n, d_comp, d_status, stream_ptr,
+            [&](const void* sorted, std::uint64_t* comp, std::uint8_t* status) {
+                return engine_run_any(e, sorted, packed, n, comp, status, base_ps, stream_ptr,
+                                      out, refresh_records, nullptr, true);
+            });
     }
     for (int k = 0; k < 3; ++k) {
         float ms = 0.0f;

@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <vector>
 
 namespace hbfamd {
@@ -94,6 +95,21 @@ int engine_last_kernel_ms(const engine* e, float* ms, int max_kernels);
 int engine_run_host(engine* e, const hbf_record32* records, std::size_t n,
                     std::uint64_t* completion, std::uint8_t* status,
                     std::uint64_t base_ps, hbfsim_amd_report* out);
+
+// Issue order (order.hip).  order_check sets *d_flag (device) to 1 when some
+// record's issue time is below its predecessor's; asynchronous on `stream`.
+int order_check(const void* d_records, bool packed, std::size_t n, std::uint32_t* d_flag,
+                void* stream);
+// Times a stream in (issue time, position) order: sorts a copy of the
+// records stably by issue time, calls run(sorted records, completions,
+// status) with device buffers in that order (status NULL when d_status is),
+// then scatters completions and status bytes back to stream positions and
+// synchronises `stream`.  HBFSIM_UNSUPPORTED from 2^32 records.
+using sorted_runner =
+    std::function<int(const void* d_sorted, std::uint64_t* d_comp, std::uint8_t* d_status)>;
+int run_in_issue_order(const void* d_records, bool packed, std::size_t n,
+                       std::uint64_t* d_completion, std::uint8_t* d_status, void* stream,
+                       const sorted_runner& run);
 
 // Workload compiler (gen.hip).
 int gen_segment_lines(hbf_record32* d_records, std::size_t capacity,

@@ -1549,6 +1549,12 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
         cfg.dies > 64 || ndie > kMaxDies || cfg.model != HBFSIM_AMD_MODEL_HBF) {
         return HBFSIM_UNSUPPORTED;
     }
+    // The merged stream carries refresh records, which the engine times only
+    // with at most one page register and without warp grouping: refused here,
+    // before anything is allocated or written.
+    if (cfg.grouping != 0 || cfg.slots == 2) {
+        return HBFSIM_UNSUPPORTED;
+    }
     const std::uint32_t rw = g.nx / o.regions_x, rh = g.ny / o.regions_y;
     std::uint32_t tx, ty;
     choose_tile(g.nx, g.ny, g.nz, g.sweeps, rw, rh, tx, ty);
@@ -1561,11 +1567,27 @@ int coupled_run(engine* e, const engine_config& cfg, thermal* th,
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
     std::uint64_t windows = 0;
     if (n != 0) {
+        // demand records in issue order (the windows, admission gate and
+        // merge follow it): any that goes back refuses the run before the
+        // grid, the ages or the engine change
+        std::uint32_t* d_back = nullptr;
+        std::uint32_t back = 0;
         std::uint64_t last = 0;
-        if (hipMemcpyAsync(&last, &d_rec[n - 1].issue_ps, 8, hipMemcpyDeviceToHost, stream) !=
-                hipSuccess ||
-            hipStreamSynchronize(stream) != hipSuccess) {
+        hipError_t e0 = halloc(d_back, 1);
+        if (e0 == hipSuccess) e0 = hipMemcpyAsync(d_back, &back, 4, hipMemcpyHostToDevice, stream);
+        if (e0 == hipSuccess && order_check(d_rec, false, n, d_back, stream_ptr) != HBFSIM_OK) {
+            e0 = hipErrorLaunchFailure;
+        }
+        if (e0 == hipSuccess) e0 = hipMemcpyAsync(&back, d_back, 4, hipMemcpyDeviceToHost, stream);
+        if (e0 == hipSuccess)
+            e0 = hipMemcpyAsync(&last, &d_rec[n - 1].issue_ps, 8, hipMemcpyDeviceToHost, stream);
+        if (e0 == hipSuccess) e0 = hipStreamSynchronize(stream);
+        hfree(d_back);
+        if (e0 != hipSuccess) {
             return HBFSIM_CUDA_ERROR;
+        }
+        if (back != 0) {
+            return HBFSIM_INVALID_ARGUMENT;
         }
         windows = last / o.window_ps + 1;
     }

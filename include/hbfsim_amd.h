@@ -178,9 +178,11 @@ hbfsim_context* hbfsim_vllm_session_context(hbfsim_vllm_session* session);
  * (hbf_device.cu:963).  issue_ps is the issue time in picoseconds relative
  * to the run's base_ps.  flags bits 0-7: operation (0 read, 1 write); bits
  * 32-63: warp group id (0: none), read when the engine option
- * warp_grouping is 1; other bits are ignored.  Records must be ordered by
- * issue time; a record's service order on every resource is its position in
- * the stream.  The thermal-coupled run also merges refresh records into the
+ * warp_grouping is 1; other bits are ignored.  A record's service order on
+ * every resource is its place in (issue time, stream position) order: its
+ * stream position when records are ordered by issue time (the fast case),
+ * else its position in the stably sorted stream (see hbfsim_amd_run_device).
+ * The thermal-coupled run also merges refresh records into the
  * stream it times: operation 2 with flag bit 8 set, addr = media page, bytes
  * moved on the channel (read out and written back); elsewhere operation 2
  * is unsupported like any operation above 1.
@@ -303,7 +305,17 @@ int hbfsim_amd_get_engine_options(const hbfsim_context* context,
  * base_ps is added to every issue_ps.  Engine state (per-plane busy and
  * page-buffer tags, per-channel cursors) carries over from the previous run
  * on the context.  `report` (host) may be NULL.  The call returns when the
- * run has completed on `stream`. */
+ * run has completed on `stream`.
+ *
+ * Order: every resource serves its records in (issue time, position) order,
+ * as the reference's MQSim adapter serves staged arrivals sorted by
+ * (arrival, sequence) (mqsim_online.cpp:269-289).  An issue-ordered stream
+ * is timed as it lies; when some record's issue time is below its
+ * predecessor's, the run leaves the engine state untouched, times a copy of
+ * the records sorted stably by issue time (allocating about 40 bytes per
+ * record more) and writes completions and status bytes back to the records'
+ * positions; the hybrid sampler's sequence numbers follow the sorted order.
+ * Up to 2^32 - 1 records per run in that case (HBFSIM_UNSUPPORTED beyond). */
 int hbfsim_amd_run_device(hbfsim_context* context,
                           const hbf_record32* records, size_t n,
                           uint64_t* completion_ps, uint8_t* status,
@@ -328,11 +340,15 @@ int hbfsim_amd_run_device_packed(hbfsim_context* context,
  * 16,384) until the run fits: up to about 125 million records per call with
  * 64 planes and 8 channels, 27 million with 512 planes and 16 channels and
  * 13 million with 1,024 planes and 256 channels.  Returns
- * HBFSIM_UNSUPPORTED, touching nothing,
+ * HBFSIM_UNSUPPORTED, touching neither the context nor *report,
  * when the run does not fit, when the context's engine does not exist yet
  * (make one ordinary run first), when ranges were registered or removed
- * since the last run (the range upload allocates) or in hybrid mode.  Every call on a device
- * shares that device's array: calls that overlap on one device race. */
+ * since the last run (the range upload allocates), in hybrid mode, or when
+ * the static array's device address cannot be looked up.  It cannot sort:
+ * records whose issue time goes back return HBFSIM_INVALID_ARGUMENT with the
+ * context and *report untouched (completion_ps and status then hold no
+ * result).  Every call on a device shares that device's array: calls that
+ * overlap on one device race. */
 int hbfsim_amd_run_device_packed_noalloc(hbfsim_context* context,
                                          const hbf_record16* records, size_t n,
                                          uint64_t* completion_ps, uint8_t* status,
@@ -611,7 +627,12 @@ typedef struct hbfsim_amd_coupled_report {
  * temperature and receives the final one; age_ps (host, channels * ways *
  * dies entries) holds each die's equivalent age and is updated.  Engine
  * state carries over as for hbfsim_amd_run_device.  Either report may be
- * NULL; engine_report covers the merged stream. */
+ * NULL; engine_report covers the merged stream.  Refused before anything
+ * changes (temperature, ages, engine state): demand records whose issue time
+ * goes back (HBFSIM_INVALID_ARGUMENT: the windows, the admission gate and
+ * the merge follow issue order), and contexts with warp grouping or two
+ * page registers (HBFSIM_UNSUPPORTED: the engine times the merged refresh
+ * records only without them). */
 int hbfsim_amd_run_coupled(hbfsim_context* context, hbfsim_amd_thermal* thermal,
                            const hbfsim_amd_reliability_options* options,
                            const hbf_record32* d_records, size_t n,

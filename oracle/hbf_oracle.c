@@ -678,10 +678,12 @@ static int groups_valid(const orc_engine_params* p, const orc_record* records, s
     return 1;
 }
 
-int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
-                   uint32_t range_count, const orc_record* records, size_t n,
-                   uint64_t base_ps, orc_engine_state* s, uint64_t* completion,
-                   uint8_t* status, orc_engine_report* rep)
+/* The engine over a stream whose records are served in stream position
+ * order (orc_engine_run sorts any other stream first). */
+static int engine_run_in_order(const orc_engine_params* p, const orc_range* ranges,
+                               uint32_t range_count, const orc_record* records, size_t n,
+                               uint64_t base_ps, orc_engine_state* s, uint64_t* completion,
+                               uint8_t* status, orc_engine_report* rep)
 {
     if (!engine_params_ok(p)) {
         return 1;
@@ -896,16 +898,16 @@ static void merge_report(orc_engine_report* t, const orc_engine_report* r)
  * status, report and the hybrid sequence in parallel over parts of the
  * chunk, each part's sequence numbers offset by the modeled records before
  * it. */
-int orc_engine_run_parallel(const orc_engine_params* p,
-                            const orc_range* ranges, uint32_t range_count,
-                            const orc_record* records, size_t n,
-                            uint64_t base_ps, orc_engine_state* s,
-                            uint64_t* completion, uint8_t* status,
-                            orc_engine_report* rep, int threads)
+static int engine_run_parallel_in_order(const orc_engine_params* p,
+                                        const orc_range* ranges, uint32_t range_count,
+                                        const orc_record* records, size_t n,
+                                        uint64_t base_ps, orc_engine_state* s,
+                                        uint64_t* completion, uint8_t* status,
+                                        orc_engine_report* rep, int threads)
 {
     if (p->model != ORC_MODEL_HBF || threads <= 1 || p->warp_grouping) {
-        return orc_engine_run(p, ranges, range_count, records, n, base_ps, s,
-                              completion, status, rep);
+        return engine_run_in_order(p, ranges, range_count, records, n, base_ps, s,
+                                   completion, status, rep);
     }
     if (!engine_params_ok(p)) {
         return 1;
@@ -1074,6 +1076,118 @@ int orc_engine_run_parallel(const orc_engine_params* p,
     free(part_modeled);
     free(part);
     return 0;
+}
+
+/* ---- issue order ----------------------------------------------------
+ * Every resource serves its records in (issue time, stream position)
+ * order: the order in which the reference's MQSim adapter serves staged
+ * arrivals, sorted by (arrival, sequence) (mqsim_online.cpp:269-289).  A
+ * stream already in issue order is run as it lies.  Any other stream is run
+ * from a copy sorted by (issue_ps, position), and its completions and
+ * statuses are written back to stream positions.  Warp groups are checked
+ * on the stream as given, then again on the sorted copy. */
+static int issue_ordered(const orc_record* r, size_t n)
+{
+    for (size_t i = 1; i < n; ++i) {
+        if (r[i].issue_ps < r[i - 1].issue_ps) {
+            return 0;
+        }
+    }
+    return 1;
+}
+
+/* pos[] = 0..n-1 stably merge-sorted by issue_ps (tmp: n entries). */
+static void issue_sort(const orc_record* r, size_t n, size_t* pos, size_t* tmp)
+{
+    for (size_t i = 0; i < n; ++i) {
+        pos[i] = i;
+    }
+    size_t* a = pos;
+    size_t* b = tmp;
+    for (size_t w = 1; w < n; w *= 2) {
+        for (size_t lo = 0; lo < n; lo += 2 * w) {
+            const size_t mid = lo + w < n ? lo + w : n;
+            const size_t hi = lo + 2 * w < n ? lo + 2 * w : n;
+            size_t i = lo, j = mid, k = lo;
+            while (i < mid && j < hi) {
+                /* ties take the left run first: stream order is kept */
+                b[k++] = r[a[j]].issue_ps < r[a[i]].issue_ps ? a[j++] : a[i++];
+            }
+            while (i < mid) b[k++] = a[i++];
+            while (j < hi) b[k++] = a[j++];
+        }
+        size_t* t = a;
+        a = b;
+        b = t;
+    }
+    if (a != pos) {
+        memcpy(pos, a, n * sizeof(size_t));
+    }
+}
+
+static int engine_run_ordered(const orc_engine_params* p, const orc_range* ranges,
+                              uint32_t range_count, const orc_record* records, size_t n,
+                              uint64_t base_ps, orc_engine_state* s, uint64_t* completion,
+                              uint8_t* status, orc_engine_report* rep, int threads)
+{
+    if (issue_ordered(records, n)) {
+        return engine_run_parallel_in_order(p, ranges, range_count, records, n, base_ps, s,
+                                            completion, status, rep, threads);
+    }
+    if (!engine_params_ok(p)) {
+        return 1;
+    }
+    if (p->warp_grouping && !groups_valid(p, records, n)) {
+        return 6;
+    }
+    size_t* pos = (size_t*)malloc(n * sizeof(size_t));
+    size_t* tmp = (size_t*)malloc(n * sizeof(size_t));
+    orc_record* sorted = (orc_record*)malloc(n * sizeof(orc_record));
+    uint64_t* comp = (uint64_t*)malloc(n * sizeof(uint64_t));
+    uint8_t* st = (uint8_t*)malloc(n);
+    int rc = 2;
+    if (pos && tmp && sorted && comp && st) {
+        issue_sort(records, n, pos, tmp);
+        for (size_t j = 0; j < n; ++j) {
+            sorted[j] = records[pos[j]];
+        }
+        rc = engine_run_parallel_in_order(p, ranges, range_count, sorted, n, base_ps, s, comp,
+                                          st, rep, threads);
+        if (rc == 0) {
+            for (size_t j = 0; j < n; ++j) {
+                completion[pos[j]] = comp[j];
+                if (status != NULL) {
+                    status[pos[j]] = st[j];
+                }
+            }
+        }
+    }
+    free(pos);
+    free(tmp);
+    free(sorted);
+    free(comp);
+    free(st);
+    return rc;
+}
+
+int orc_engine_run(const orc_engine_params* p, const orc_range* ranges,
+                   uint32_t range_count, const orc_record* records, size_t n,
+                   uint64_t base_ps, orc_engine_state* s, uint64_t* completion,
+                   uint8_t* status, orc_engine_report* rep)
+{
+    return engine_run_ordered(p, ranges, range_count, records, n, base_ps, s, completion,
+                              status, rep, 1);
+}
+
+int orc_engine_run_parallel(const orc_engine_params* p,
+                            const orc_range* ranges, uint32_t range_count,
+                            const orc_record* records, size_t n,
+                            uint64_t base_ps, orc_engine_state* s,
+                            uint64_t* completion, uint8_t* status,
+                            orc_engine_report* rep, int threads)
+{
+    return engine_run_ordered(p, ranges, range_count, records, n, base_ps, s, completion,
+                              status, rep, threads);
 }
 
 /* hbf_device.cu:883-958, time_scale 1: one global tail; the latency bound
@@ -1860,12 +1974,10 @@ int orc_coupled_run(const orc_engine_params* p, const orc_range* ranges,
         r->dies != p->dies || p->model != ORC_MODEL_HBF) {
         return 1;
     }
-    uint64_t last = 0;
-    for (size_t i = 0; i < n; ++i) {
-        if (rec[i].issue_ps > last) {
-            last = rec[i].issue_ps;
-        }
+    if (!issue_ordered(rec, n)) {
+        return 1;  /* the windows, the admission gate and the merge follow issue order */
     }
+    const uint64_t last = n ? rec[n - 1].issue_ps : 0;
     const uint64_t windows = n ? last / r->window_ps + 1 : 0;
     rep->windows = windows;
     if (windows > windows_cap) {

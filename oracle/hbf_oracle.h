@@ -228,7 +228,11 @@ typedef struct orc_record {
     uint64_t addr, bytes, issue_ps, flags;
 } orc_record;
 
-/* Runs records in input order.  issue = base_ps + record.issue_ps.
+/* Runs records in (issue time, position) order: in input order when the
+ * stream is issue-ordered, else from a copy sorted stably by issue_ps (the
+ * order in which the reference's MQSim adapter serves staged arrivals,
+ * mqsim_online.cpp:269-289), results written back to input positions.
+ * issue = base_ps + record.issue_ps.
  * completion[i]: completion ps (bypass: issue; unsupported: UINT64_MAX).
  * status may be NULL.  Report accumulates (caller zeroes it).
  *
@@ -459,7 +463,8 @@ void orc_set_threads(int threads);
 int orc_get_threads(void);
 /* The whole coupled run: counts -> chain -> admission -> refresh records ->
  * merge -> engine; completion[n] of the demand records.  hot, level and
- * refresh are sized for windows_cap windows. */
+ * refresh are sized for windows_cap windows.  Demand records must be in
+ * issue order (1 otherwise, before anything changes). */
 int orc_coupled_run(const orc_engine_params* p, const orc_range* ranges,
                     uint32_t range_count, const orc_reliability* r,
                     const orc_record* rec, size_t n, double* temperature,

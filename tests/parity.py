@@ -134,7 +134,9 @@ def compare_whole(pair: "Pair", d_rec, d_comp, d_st, base_ps: int, what: str,
     """Every completion and status byte of a GPU run of the 32-byte records
     d_rec (int64 [n, 4] on the GPU) against the OpenMP oracle run over the
     same records, taken in chunks with the oracle's state carried (the same
-    as one run).  Returns the oracle's report of the whole run."""
+    as one run; the records must be in issue order, since the oracle serves a
+    stream that goes back in time from its sorted copy, per run).  Returns the
+    oracle's report of the whole run."""
     n = int(d_rec.shape[0])
     rep = None
     for a in range(0, n, chunk):

@@ -2,11 +2,14 @@
 Config 1 (TinyLlama-1.1B weight streaming, 17.2M records a step): two whole
 decode steps.  Config 2 (the benchmarked Qwen3-30B-A3B MoE decode, 2.7e8
 records a step): the bench's first two steps, chained with the makespan
-carried as the next base as bench.py does, in both record forms.  Config 3
-(paged KV cache): every step of a reduced shape, and one whole full-size step
-(1.17e9 records over 150 GB of KV).  The oracle runs over each whole step in
-chunks with its state carried.  The GPU record compiler is checked against
-its host mirror on the way."""
+carried as the next base as bench.py does, in both record forms; the same
+two steps in hybrid mode (the bench's hybrid line), one hybrid step whose
+sampler sequence crosses 2^32, and one step with two page registers per
+plane.  Config 3 (paged KV cache): every step of a reduced shape, and one
+whole full-size step (1.17e9 records over 150 GB of KV).  The oracle runs
+over each whole step in chunks with its state carried (the steps are in issue
+order, so chunks are the same as one run).  The GPU record compiler is
+checked against its host mirror on the way."""
 from __future__ import annotations
 
 import numpy as np
@@ -214,3 +217,105 @@ def test_config2_bench_steps_whole():
         pair.close()
         wide.close()
         split.close()
+
+
+def hybrid_c2_profile(tmp_path):
+    """Config 2's profile with the bench's hybrid sampling: rate 1%, 1,000
+    warm-up requests."""
+    import json
+    prof = json.loads((w.PROFILES / "c2.json").read_text())
+    prof.update(reference_sample_rate=0.01, reference_warmup_requests=1000)
+    path = tmp_path / "c2-hybrid.json"
+    path.write_text(json.dumps(prof))
+    return path
+
+
+def c2_step(shape, sel, k):
+    return w.gpu_segment_records(w.moe_segments(shape, sel[k]), shape.lines_per_expert,
+                                 shape.line, shape.gap_ps, shape.issuers)
+
+
+def test_config2_hybrid_two_steps_whole(tmp_path):
+    """The bench's hybrid line: two chained whole config-2 steps in hybrid
+    mode (context mode 2) from packed records, every completion and status
+    byte (sampled flag included), both reports, busy totals and the engine
+    state (sequence included) equal to the oracle's."""
+    import torch
+    shape = w.QWEN3_30B_A3B
+    sel = w.moe_selection(shape, 2)
+    pair = parity.Pair(hybrid_c2_profile(tmp_path), w.moe_ranges(shape), mode="hybrid")
+    try:
+        base = 0
+        for k in range(2):
+            d_rec = c2_step(shape, sel, k)
+            n = int(d_rec.shape[0])
+            d_pk = pack_records(d_rec)
+            d_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+            d_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+            rep = pair.engine.run_packed(d_pk, d_comp, d_st, base_ps=base)
+            torch.cuda.synchronize()
+            del d_pk
+            assert rep["modeled"] == n and rep["hybrid_sampled"] > n // 200
+            orep = parity.compare_whole(pair, d_rec, d_comp, d_st, base,
+                                        f"config-2 hybrid step {k}")
+            assert orep == rep
+            base = rep["makespan_ps"]
+            del d_rec, d_comp, d_st
+        pair.check_state()
+    finally:
+        pair.close()
+
+
+def test_config2_hybrid_sequence_past_2_32(tmp_path):
+    """One whole config-2 step in hybrid mode with the engine's and the
+    oracle's modeled-request sequence set just below 2^32: the sampler's
+    hash takes sequence ^ key in 64 bits all through the step, which
+    carries the sequence past 2^32."""
+    import torch
+    shape = w.QWEN3_30B_A3B
+    sel = w.moe_selection(shape, 1)
+    pair = parity.Pair(hybrid_c2_profile(tmp_path), w.moe_ranges(shape), mode="hybrid")
+    try:
+        seq0 = (1 << 32) - 3_000_000
+        st = pair.engine.state()
+        st["sequence"] = seq0
+        pair.engine.set_state(st)
+        pair.ostate.s.modeled_sequence = seq0
+        d_rec = c2_step(shape, sel, 0)
+        n = int(d_rec.shape[0])
+        d_pk = pack_records(d_rec)
+        d_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+        d_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+        rep = pair.engine.run_packed(d_pk, d_comp, d_st)
+        torch.cuda.synchronize()
+        del d_pk
+        orep = parity.compare_whole(pair, d_rec, d_comp, d_st, 0, "config-2 hybrid near 2^32")
+        assert orep == rep and rep["hybrid_sampled"] > 0
+        assert pair.engine.state()["sequence"] == seq0 + n > 1 << 32
+        pair.check_state()
+    finally:
+        pair.close()
+
+
+def test_config2_two_page_registers_whole_step():
+    """One whole config-2 step with two page registers per plane
+    (device_coalescer.cpp:134-168), from 32-byte records: every completion
+    and status byte, the report, busy totals and both tags of every plane
+    equal to the oracle's."""
+    import torch
+    shape = w.QWEN3_30B_A3B
+    sel = w.moe_selection(shape, 1)
+    pair = parity.Pair(w.PROFILES / "c2.json", w.moe_ranges(shape), page_buffers=2)
+    try:
+        d_rec = c2_step(shape, sel, 0)
+        n = int(d_rec.shape[0])
+        d_comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+        d_st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+        rep = pair.engine.run(d_rec, d_comp, d_st)
+        torch.cuda.synchronize()
+        assert rep["modeled"] == n and rep["page_hits"] > n // 2
+        orep = parity.compare_whole(pair, d_rec, d_comp, d_st, 0, "config-2 K=2 step")
+        assert orep == rep
+        pair.check_state()
+    finally:
+        pair.close()

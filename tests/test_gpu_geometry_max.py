@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import parity
-from test_gpu_linear import contiguous_stream, linear_stream, ranges_for
+from test_gpu_linear import chain_clocks, contiguous_stream, linear_stream, ranges_for
 from test_gpu_parity import C0
 from hbfsim_amd import _native as nat
 from hbfsim_amd import workloads
@@ -34,7 +34,7 @@ def test_maximum_geometry(tmp_path, channels, dies, planes):
     path = geometry_profile(tmp_path, channels, dies, planes)
     s = workloads.config0(n=100_000, seed=5, write_fraction_per_mille=50)
     ranges = ranges_for()
-    lin = np.concatenate([linear_stream(8, 700, ranges), contiguous_stream(9, 150, ranges)])
+    lin = chain_clocks(linear_stream(8, 700, ranges), contiguous_stream(9, 150, ranges))
     for rng_set, rec, what in [(s.ranges, s.records, "config0"), (ranges, lin, "linear")]:
         a = parity.Pair(path, rng_set)
         b = parity.Pair(path, rng_set)

@@ -2,10 +2,11 @@
 page) take a batched path on the GPU: they wait in a batch of up to 64 steps
 that is folded with one lane per step.  These streams mix such steps with
 steps that end a batch early (writes, page crossings, bypass and unreadable
-ranges, short or out-of-order steps), revisit planes and pages inside one
-batch, jump between ranges (the uniform range cache refills) and let issue
-times fall back, under every plane/transfer option; results must match the
-CPU oracle bit for bit."""
+ranges, short steps, steps with two issue times), revisit planes and pages inside one
+batch and jump between ranges (the uniform range cache refills), under every
+plane/transfer option; results must match the CPU oracle bit for bit.  The
+streams are in issue order (streams that leave it are tested in
+test_gpu_order.py)."""
 from __future__ import annotations
 
 import json
@@ -29,13 +30,27 @@ def ranges_for(count=6, pages=96):
     return out
 
 
+def chain_clocks(*parts):
+    """Concatenates record streams, each shifted in time to start no earlier
+    than the previous one ends, so that the whole stream is in issue order."""
+    out, t = [], 0
+    for part in parts:
+        part = part.copy()
+        if len(part):
+            first = int(part[:, 2].min())
+            part[:, 2] += np.uint64(max(0, t - first))
+            t = int(part[:, 2].max())
+        out.append(part)
+    return np.concatenate(out)
+
+
 def linear_stream(seed, steps, ranges, kinds=None):
     """One step at a time: mostly linear steps on a few hot pages (so later
     steps of a batch hit pages earlier ones opened, on the same and other
     planes), with breaking steps in between."""
     rng = np.random.default_rng(seed)
     kinds = kinds or {"lin": 0.80, "write": 0.03, "cross": 0.03, "bypass": 0.03,
-                      "wo": 0.02, "ragged": 0.03, "late": 0.03, "mixed_issue": 0.03}
+                      "wo": 0.02, "ragged": 0.03, "mixed_issue": 0.03}
     names = list(kinds)
     probs = np.array([kinds[k] for k in names], float)
     probs /= probs.sum()
@@ -72,10 +87,11 @@ def linear_stream(seed, steps, ranges, kinds=None):
             step[:, 0] = np.uint64(wb + pg * PAGE) + lanes * np.uint64(b)
         elif kind == "ragged":  # one lane's byte count differs
             step[int(rng.integers(0, 64)), 1] = b // 2
-        elif kind == "late":  # issue time falls back far
+        elif kind == "late":  # issue time falls back far (the stream leaves issue order)
             step[:, 2] = max(0, issue - 9_000_000)
         elif kind == "mixed_issue":
             step[int(rng.integers(1, 64)):, 2] = issue + 1
+            t += 1
         out.append(step)
     return np.concatenate(out)
 
@@ -219,7 +235,8 @@ def contiguous_stream(seed, runs, ranges):
             if r < 0.02:
                 step[int(rng.integers(0, 64)), 3] = 1        # a write
             elif r < 0.04:
-                step[int(rng.integers(0, 64)), 2] += 1       # one late record
+                step[int(rng.integers(1, 64)):, 2] += 1      # the step's later records later
+                t += 1
             elif r < 0.05:
                 step[int(rng.integers(0, 64)), 0] += 1       # one address off the line
             out.append(step)

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import parity
-from test_gpu_linear import contiguous_stream, linear_stream, ranges_for, striding_stream
+from test_gpu_linear import chain_clocks, contiguous_stream, linear_stream, ranges_for, striding_stream
 from test_gpu_parity import C0, C2
 from hbfsim_amd import workloads
 
@@ -30,7 +30,7 @@ def check_packed(pair, rec, what, base_ps=0):
                                      dict(tile_records=64 * 24), dict(tile_records=64 * 300)])
 def test_packed_linear_and_general_paths(profile, options):
     ranges = ranges_for()
-    rec = np.concatenate([linear_stream(3, 800, ranges), contiguous_stream(4, 200, ranges)])
+    rec = chain_clocks(linear_stream(3, 800, ranges), contiguous_stream(4, 200, ranges))
     p = parity.Pair(profile, ranges, **options)
     try:
         (_, _, grep), _ = check_packed(p, rec, f"packed {profile.name} {options}")
@@ -117,7 +117,7 @@ def test_packed_hybrid(tmp_path, profile, options):
     path = tmp_path / "hybrid.json"
     path.write_text(json.dumps(prof))
     ranges = ranges_for()
-    rec = np.concatenate([linear_stream(5, 600, ranges), contiguous_stream(6, 150, ranges)])
+    rec = chain_clocks(linear_stream(5, 600, ranges), contiguous_stream(6, 150, ranges))
     p = parity.Pair(path, ranges, mode="hybrid", **options)
     try:
         (_, _, g1), _ = check_packed(p, rec, f"packed hybrid {profile.name} {options}")

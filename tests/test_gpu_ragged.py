@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import parity
-from test_gpu_linear import contiguous_stream, linear_stream, ranges_for
+from test_gpu_linear import chain_clocks, contiguous_stream, linear_stream, ranges_for
 from test_gpu_parity import C0, C2
 
 pytestmark = pytest.mark.gpu
@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 @pytest.mark.parametrize("form", ["32", "packed"])
 def test_empty_single_and_ragged_runs(profile, form):
     ranges = ranges_for()
-    rec = np.concatenate([linear_stream(11, 60, ranges), contiguous_stream(12, 12, ranges)])
+    rec = chain_clocks(linear_stream(11, 60, ranges), contiguous_stream(12, 12, ranges))
     p = parity.Pair(profile, ranges)
     run = p.run if form == "32" else p.run_packed
     cuts = [(0, 0), (0, 1), (1, 1), (1, 64), (64, 129), (129, 129), (129, len(rec)),

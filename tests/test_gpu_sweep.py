@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import parity
-from test_gpu_linear import contiguous_stream, linear_stream, ranges_for
+from test_gpu_linear import chain_clocks, contiguous_stream, linear_stream, ranges_for
 from test_gpu_parity import C0, C2
 from hbfsim_amd import workloads
 
@@ -41,8 +41,9 @@ def mixed_stream(seed):
             off = (rec[:, 0] - np.uint64(workloads.RANGE_BASE)) % np.uint64(r[1])
             rec[:, 0] = np.uint64(r[0]) + off
             parts.append(rec)
-    # parts keep their own issue clocks: issue times fall back between parts
-    return ranges, np.concatenate(parts)
+    # each part continues the clock of the one before: the stream is in issue
+    # order (streams that leave it are tested in test_gpu_order.py)
+    return ranges, chain_clocks(*parts)
 
 
 @pytest.mark.parametrize("seed", range(32))
