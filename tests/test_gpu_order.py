@@ -130,16 +130,34 @@ def test_unordered_two_page_registers():
 
 
 def test_unordered_warp_grouping():
+    """Warp groups in a stream that falls back: groups are checked on the
+    stream as given and again once sorted, where records of equal issue time
+    from the two halves meet.  With distinct group ids the sorted groups are
+    valid and timed; with the ids reused, two groups of one id and two issue
+    times end up side by side and both sides refuse the run."""
     from test_oracle_grouping import grouping_ranges, warp_stream
     ranges = grouping_ranges()
     a = warp_stream(21, 300, ranges)
     b = warp_stream(22, 300, ranges)  # its own clock from 0: falls back
-    rec = np.concatenate([a, b])
+    gid = b[:, 3] >> np.uint64(32)
+    moved = b.copy()
+    moved[:, 3] += np.where(gid != 0, np.uint64(10_000 << 32), np.uint64(0))
     p = parity.Pair(C0, ranges, warp_grouping=1)
     try:
-        g, c = p.run(rec)
+        g, c = p.run(np.concatenate([a, moved]))
         parity.assert_same(g, c, "grouping unordered")
         assert g[2]["grouped"] > 0
+        p.check_state()
+        before = p.engine.state()
+        with pytest.raises(nat.HbfSimError) as err:
+            p.engine.run(parity.to_device(np.concatenate([a, b])),
+                         parity.to_device(np.zeros((len(a) + len(b), 1), np.uint64)))
+        assert err.value.code == nat.HBFSIM_INVALID_ARGUMENT
+        with pytest.raises(RuntimeError, match="failed: 6"):
+            oracle_py.run(p.params, p.ranges, p.count, np.concatenate([a, b]), 0, p.ostate)
+        after = p.engine.state()
+        for k in ("plane_busy", "plane_tags", "channel_cursor"):
+            np.testing.assert_array_equal(after[k], before[k], k)
         p.check_state()
     finally:
         p.close()
