@@ -149,9 +149,10 @@ def test_unordered_warp_grouping():
         assert g[2]["grouped"] > 0
         p.check_state()
         before = p.engine.state()
+        import torch
         with pytest.raises(nat.HbfSimError) as err:
             p.engine.run(parity.to_device(np.concatenate([a, b])),
-                         parity.to_device(np.zeros((len(a) + len(b), 1), np.uint64)))
+                         torch.zeros(len(a) + len(b), dtype=torch.int64, device="cuda"))
         assert err.value.code == nat.HBFSIM_INVALID_ARGUMENT
         with pytest.raises(RuntimeError, match="failed: 6"):
             oracle_py.run(p.params, p.ranges, p.count, np.concatenate([a, b]), 0, p.ostate)
