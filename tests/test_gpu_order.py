@@ -244,7 +244,8 @@ def test_coupled_refusals_leave_everything(case):
     try:
         if case == "unordered":
             rec = rec.copy()
-            rec[[500, 501], 2] = rec[[501, 500], 2]
+            rec[[500, 9000], 2] = rec[[9000, 500], 2]  # records share issue times in fours
+            assert np.any(rec[1:, 2] < rec[:-1, 2])
             want = nat.HBFSIM_INVALID_ARGUMENT
         elif case == "grouping":
             e.set_options(warp_grouping=1)

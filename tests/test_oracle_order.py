@@ -133,7 +133,8 @@ def test_coupled_run_refuses_unsorted_demand():
     rel = oracle_py.reliability(dict(w.C4_GRID, nx=8, ny=8, nz=8), dict(
         w.C4_RELIABILITY, regions_x=4, regions_y=2), params.dies)
     rec = w.config0(n=500, seed=2).records.copy()
-    rec[[10, 11], 2] = rec[[11, 10], 2]
+    rec[[10, 400], 2] = rec[[400, 10], 2]
+    assert np.any(rec[1:, 2] < rec[:-1, 2])
     temp = np.full(8 * 8 * 8, 318.15)
     age = np.zeros(params.channels * params.dies, np.uint64)
     t0, a0 = temp.copy(), age.copy()
