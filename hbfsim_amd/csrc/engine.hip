@@ -1445,6 +1445,21 @@ __device__ __forceinline__ StepView step_view(const KArgs& a, const std::uint64_
     return v;
 }
 
+// The summary pass keeps its per-plane LDS state at slot pslot(plane) =
+// plane ^ ((plane >> 5) & 31), a permutation within each aligned block of 32
+// planes (the arrays are padded to whole blocks, plane_slots).  A batch of
+// linear steps walks the striping's fastest axis: its planes lie 32 apart on
+// the 16 x 8 x 4 geometry (8 apart on 8 x 4 x 2), so plain indexing puts every
+// lane of a fold on one LDS bank; the swizzle spreads them over distinct ones.
+__host__ __device__ __forceinline__ std::uint32_t plane_slots(const KArgs& a)
+{
+    return (a.Rp + 31u) & ~31u;
+}
+__device__ __forceinline__ std::uint32_t pslot(std::uint32_t plane)
+{
+    return plane ^ ((plane >> 5) & 31u);
+}
+
 // Issue order across a batch of linear steps (one issue time per step):
 // every step's time must be at least the one before it, the first step's at
 // least `last` (the last issue time the wave saw before the batch).
@@ -1477,8 +1492,9 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
     const std::uint32_t ckey = m ? v.d.chan : 0u;
     const Group gp = group_plane_runs(a, q.page1, pkey, m, v.active, lane, mt_p);
     const Group gc = group_by(ckey, a.cbits, m, v.active, lane, mt_c);
-    const std::uint32_t f1 = m ? p_f1[pkey] : 0u;
-    const std::uint32_t last_page = m ? p_l1[pkey] : 0u;
+    const std::uint32_t pk = pslot(pkey);
+    const std::uint32_t f1 = m ? p_f1[pk] : 0u;
+    const std::uint32_t last_page = m ? p_l1[pk] : 0u;
     const bool has = f1 != 0;
     const bool tfirst = m && gp.pred < 0 && !has;
     std::uint32_t prev1 = static_cast<std::uint32_t>(
@@ -1501,15 +1517,15 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
     const std::uint64_t li = shfl64(q.issue, gp.leader);
     if (m && lane == gp.last) {
         if (!has) {
-            p_f1[pkey] = l1;
-            p_fi[pkey] = li;
-            p_fc[pkey] = 0;  // a read
+            p_f1[pk] = l1;
+            p_fi[pk] = li;
+            p_fc[pk] = 0;  // a read
         }
-        const std::uint64_t sA = p_rA[pkey];
-        const std::uint64_t sB = p_rB[pkey];
-        p_rB[pkey] = umax64(sB + Ap, Bp);
-        p_rA[pkey] = sA + Ap;
-        p_l1[pkey] = q.page1;
+        const std::uint64_t sA = p_rA[pk];
+        const std::uint64_t sB = p_rB[pk];
+        p_rB[pk] = umax64(sB + Ap, Bp);
+        p_rA[pk] = sA + Ap;
+        p_l1[pk] = q.page1;
     }
     if (m && lane == gc.last) {
         const std::uint64_t sA = c_A[ckey];
@@ -1571,7 +1587,8 @@ __device__ __forceinline__ int slot(const MaskWord* tmask, std::uint32_t words, 
 // arrays, two 64-bit channel arrays and the plane class bytes; 8-byte aligned.
 __host__ __device__ __forceinline__ std::size_t summary_match_offset(const KArgs& a)
 {
-    return 8ull * (a.r_nfence + 3ull * a.Rp + 2ull * a.Rc) + 8ull * a.Rp + ((a.Rp + 7ull) & ~7ull);
+    const std::uint64_t rp = plane_slots(a);
+    return 8ull * (a.r_nfence + 3ull * rp + 2ull * a.Rc) + 8ull * rp + ((rp + 7ull) & ~7ull);
 }
 
 // Summary pass.  Per plane the tile keeps: the first record (page, issue,
@@ -1586,15 +1603,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
                                                 const std::uint8_t* hits, StepDesc* desc)
 {
     extern __shared__ std::uint64_t sm[];
+    // per-plane state at slot pslot(plane) of plane_slots(a) entries
+    const std::uint32_t rpp = plane_slots(a);
     std::uint64_t* fence = sm;
     std::uint64_t* p_fi = fence + a.r_nfence;
-    std::uint64_t* p_rA = p_fi + a.Rp;
-    std::uint64_t* p_rB = p_rA + a.Rp;
-    std::uint64_t* c_A = p_rB + a.Rp;
+    std::uint64_t* p_rA = p_fi + rpp;
+    std::uint64_t* p_rB = p_rA + rpp;
+    std::uint64_t* c_A = p_rB + rpp;
     std::uint64_t* c_B = c_A + a.Rc;
     std::uint32_t* p_f1 = reinterpret_cast<std::uint32_t*>(c_B + a.Rc);
-    std::uint32_t* p_l1 = p_f1 + a.Rp;
-    std::uint8_t* p_fc = reinterpret_cast<std::uint8_t*>(p_l1 + a.Rp);  // class bits < 16
+    std::uint32_t* p_l1 = p_f1 + rpp;
+    std::uint8_t* p_fc = reinterpret_cast<std::uint8_t*>(p_l1 + rpp);  // class bits < 16
     std::uint64_t* mt_p = a.match_lds ? reinterpret_cast<std::uint64_t*>(
                                             reinterpret_cast<unsigned char*>(sm) +
                                             summary_match_offset(a))
@@ -1632,7 +1651,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
     pipe.issue(rec, begin, end, lane);
     store_fences(a, fr, fence, lane);
     store_xfer(xp, xv, lane);
-    for (std::uint32_t r = lane; r < a.Rp; r += kWave) {
+    for (std::uint32_t r = lane; r < rpp; r += kWave) {
         p_fi[r] = 0;
         p_rA[r] = 0;
         p_rB[r] = 0;
@@ -1756,7 +1775,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             if (!kHits && run_step(a, d, active, lane)) {
                 const std::uint64_t W = run_channel_max(d, xfer, lane);
                 if (lane == 63) {
-                    const std::uint32_t pkey = d.plane;
+                    const std::uint32_t pkey = pslot(d.plane);
                     const std::uint32_t ckey = d.chan;
                     const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
                     const std::uint64_t i0 = readlane64(d.issue, 0);
@@ -1790,8 +1809,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             const Group gp = group_by(pkey, a.pbits, m, active, lane, mt_p);
             const Group gc = group_by(ckey, a.cbits, m, active, lane, mt_c);
             // state reads come before this step's writes
-            const std::uint32_t f1 = m ? p_f1[pkey] : 0u;
-            const std::uint32_t last_page = m ? p_l1[pkey] : 0u;
+            const std::uint32_t pk = pslot(pkey);
+            const std::uint32_t f1 = m ? p_f1[pk] : 0u;
+            const std::uint32_t last_page = m ? p_l1[pk] : 0u;
             const bool has = f1 != 0;
             const bool tfirst = m && gp.pred < 0 && !has;
             std::uint32_t prev1 = static_cast<std::uint32_t>(
@@ -1818,15 +1838,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
                 static_cast<std::uint32_t>(__shfl(static_cast<int>(lbits), gp.leader));
             if (m && lane == gp.last) {
                 if (!has) {
-                    p_f1[pkey] = l1;
-                    p_fi[pkey] = li;
-                    p_fc[pkey] = static_cast<std::uint8_t>(lc);
+                    p_f1[pk] = l1;
+                    p_fi[pk] = li;
+                    p_fc[pk] = static_cast<std::uint8_t>(lc);
                 }
-                const std::uint64_t sA = p_rA[pkey];
-                const std::uint64_t sB = p_rB[pkey];
-                p_rB[pkey] = umax64(sB + Ap, Bp);
-                p_rA[pkey] = sA + Ap;
-                p_l1[pkey] = page1;
+                const std::uint64_t sA = p_rA[pk];
+                const std::uint64_t sB = p_rB[pk];
+                p_rB[pk] = umax64(sB + Ap, Bp);
+                p_rA[pk] = sA + Ap;
+                p_l1[pk] = page1;
             }
             if (m && lane == gc.last) {
                 const std::uint64_t sA = c_A[ckey];
@@ -1852,7 +1872,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
     std::uint32_t count = 0;
     for (std::uint32_t r0 = 0; r0 < a.Rp; r0 += kWave) {
         const std::uint32_t r = r0 + lane;
-        const bool touched = r < a.Rp && p_f1[r] != 0;
+        const std::uint32_t k = pslot(r);
+        const bool touched = r < a.Rp && p_f1[k] != 0;
         const std::uint64_t bits = __ballot(touched);
         if (lane == 0) {
             MaskWord m;
@@ -1863,12 +1884,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
         }
         if (touched) {
             PlaneSum v;
-            v.fpage1 = p_f1[r];
-            v.fissue = p_fi[r];
-            v.rA = p_rA[r];
-            v.rB = p_rB[r];
-            v.lpage1 = p_l1[r];
-            v.fcls = p_fc[r];
+            v.fpage1 = p_f1[k];
+            v.fissue = p_fi[k];
+            v.rA = p_rA[k];
+            v.rB = p_rB[k];
+            v.lpage1 = p_l1[k];
+            v.fcls = p_fc[k];
             v.pad = 0;
             ps[count + __popcll(bits & lanemask_lt(lane))] = v;
         }
