@@ -1,7 +1,7 @@
 """Benchmark of the HBF access-timing engine on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--config c2|c0|c4|thermal|general|hybrid|link]
+                    [--config c2|c0|c1|c3|c4|thermal|general|hybrid|link]
 
 A step is one pass of the timing engine over one batch of access records
 resident in HBM (one decode step of the workload); engine state carries from
@@ -25,6 +25,11 @@ ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_FP64_TFLOPS = 78.6  # MI355X dense FP64 (vector / matrix)
+# EQ3 Jacobi update per cell and sweep: 6 neighbour products, 7 additions
+# (the six terms and the ambient term onto the right-hand side) and the
+# product with 1 / den
+THERMAL_FLOPS_PER_CELL_SWEEP = 14
 # Algorithmic bytes per access: the record in + the 8-B completion out, 40 B
 # with 32-byte records and 24 B with packed 16-byte ones (the roofline of
 # each form is its own; the two are never mixed).  The same bytes split over
@@ -34,8 +39,40 @@ PEAK_HBM_GBPS = 8000.0
 RECORD_BYTES = {"packed": 16, "32": 32}
 
 
-def kernel_bytes(records: str) -> dict:
-    return {"k_summary": RECORD_BYTES[records], "k_apply": 8}
+def kernel_bytes(records: str, apply_rereads: bool = False) -> dict:
+    """Algorithmic bytes per access of the two per-record kernels.  The apply
+    pass writes the 8-B completion; it re-reads the record too where steps
+    are replayed from their records (streams without linear steps, such as
+    random ones), and replays linear steps from the summary pass's step
+    descriptors otherwise."""
+    return {"k_summary": RECORD_BYTES[records],
+            "k_apply": 8 + (RECORD_BYTES[records] if apply_rereads else 0)}
+
+
+def profile_kernel_us(summary: str, kernel: str) -> float | None:
+    """Average duration (us) of `kernel` in a committed kernel-trace summary
+    under profiles/ (rocprofv3 --kernel-trace --stats, one line per kernel)."""
+    import re
+    path = ROOT / "profiles" / summary
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        m = re.match(r"(\S+?(?:<[^>]*>)?)\s+(\d+)\s+([\d.]+)\s", line)
+        if m and not line.startswith("#") and (m.group(1) == kernel or
+                                               m.group(1).startswith(kernel + "<")):
+            return float(m.group(3))
+    return None
+
+
+def roofline_from_profile(summary: str, kernel: str, bytes_per_launch: float) -> dict | None:
+    """The same roofline recomputed from a committed kernel summary: the
+    algorithmic bytes of one launch over the profile's average duration."""
+    us = profile_kernel_us(summary, kernel)
+    if us is None:
+        return None
+    gbps = bytes_per_launch / (us / 1e6) / 1e9
+    return {"source": f"profiles/{summary}", "kernel_avg_us": us, "achieved": gbps,
+            "frac": gbps / PEAK_HBM_GBPS}
 
 
 def parse() -> argparse.Namespace:
@@ -57,8 +94,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-compare", action="store_true",
                     help="with packed records, skip timing the same steps from 32-byte ones")
     ap.add_argument("--no-extra", action="store_true",
-                    help="config c2: skip the stream-copy peak, the general-path, hybrid, "
-                         "UCIe-link and config-4 sub-lines")
+                    help="config c2: skip the read/write ceilings and the general-path, "
+                         "hybrid, UCIe-link, config-4, EQ3-stencil and config 0/1/3 sub-lines")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first fill and copy 2 GiB (known HBM bytes) so that counter runs "
                          "can calibrate FETCH_SIZE / WRITE_SIZE")
@@ -77,29 +114,6 @@ def copy_probe() -> None:
     torch.cuda.synchronize()
     del src, dst
     torch.cuda.empty_cache()
-
-
-def stream_copy_peak(gib: int = 4, reps: int = 5) -> dict:
-    """Measured HBM copy bandwidth on this GPU: a device-to-device copy of
-    `gib` GiB, timed with HIP events, counting the bytes read and written."""
-    import torch
-    n = (gib << 30) // 8
-    src = torch.ones(n, dtype=torch.int64, device="cuda")
-    dst = torch.empty_like(src)
-    dst.copy_(src)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / reps
-    del src, dst
-    torch.cuda.empty_cache()
-    gbps = 2 * (gib << 30) / (ms / 1e3) / 1e9
-    return {"gbps": gbps, "bytes_per_copy": 2 * (gib << 30), "ms": ms,
-            "how": f"torch device copy of {gib} GiB (read + write), {reps} reps, HIP events"}
 
 
 def gpu_random_stream(n: int, seed: int):
@@ -143,9 +157,8 @@ def committed_traffic(summary: str, kernel: str, units: int) -> tuple[float | No
 
 def build_workload(name: str, steps: int, batches: int = 6):
     """Returns (profile, ranges, list of per-step record arrays on the GPU,
-    description, host sample).  Config c2 generates `batches` distinct decode
-    steps on the GPU (step k of the run uses batch k mod batches); config 0
-    is a single stream replayed step after step."""
+    description, host sample) of config 2: `batches` distinct decode steps
+    generated on the GPU (step k of the run uses batch k mod batches)."""
     import torch
     from hbfsim_amd import workloads
 
@@ -168,12 +181,6 @@ def build_workload(name: str, steps: int, batches: int = 6):
                 "ranges": len(workloads.moe_ranges(shape))}
         return (workloads.PROFILES / "c2.json", workloads.moe_ranges(shape), out, desc, sample)
 
-    if name == "c0":
-        s = workloads.config0()
-        rec = torch.from_numpy(s.records.view(np.int64)).cuda()
-        desc = {"workload": "config0: 2^20 uniform 128-B reads, 1 GiB range, Poisson 2 ns",
-                "records_per_step": int(len(s.records)), "profile": s.profile.name}
-        return s.profile, s.ranges, [rec], desc, s.records
     raise SystemExit(f"unknown config {name}")
 
 
@@ -268,16 +275,22 @@ def bench_c4(args) -> dict:
     dt = time.perf_counter() - t0
     windows = rep["windows"]
     per_window_ms = phases["thermal_chain"] / max(1, windows)
-    cell_sweeps = cells * w.C4_GRID["sweeps"]
-    thermal_gbps = 16 * cell_sweeps / (per_window_ms / 1e3) / 1e9
+    # one window moves each cell's temperature in and out (8 + 8 B; the power
+    # map comes from the per-die counts on chip): 16 B per cell per launch
+    thermal_gbps = 16 * cells / (per_window_ms / 1e3) / 1e9
     n = int(rec.shape[0])
     engine_gbps = (RECORD_BYTES["32"] + 8) * (n + rep["refreshes"]) / (phases["engine"] / 1e3) / 1e9
     dominant = max(("thermal_chain", "engine"), key=lambda k: phases[k])
-    roof = ({"bound": "hbm", "kernel": "k_thermal_window", "achieved": thermal_gbps,
+    traffic = committed_traffic("coupled_traffic_config4.txt", "k_thermal_window", cells)[0]
+    roof = ({"bound": "latency (a chain of dependent one-window launches; priced against hbm)",
+             "kernel": "k_thermal_window", "achieved": thermal_gbps,
              "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": thermal_gbps / PEAK_HBM_GBPS,
-             "traffic": None, "algorithmic": "16 B per cell-sweep, 32768 cells x 4 sweeps "
-                                             "per launch (one launch per window)",
-             "kernel_ms": per_window_ms}
+             "traffic": traffic, "traffic_source": "profiles/coupled_traffic_config4.txt",
+             "algorithmic": f"16 B per cell per window (temperature read and written) x {cells} "
+                            f"cells per launch, one launch per window",
+             "kernel_ms": per_window_ms,
+             "from_profile": roofline_from_profile("coupled_kernels_config4.txt",
+                                                   "k_thermal_window", 16 * cells)}
             if dominant == "thermal_chain" else
             {"bound": "hbm", "kernel": "engine (k_summary + k_carry + k_apply)",
              "achieved": engine_gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
@@ -361,9 +374,15 @@ def bench_thermal(args) -> dict:
     launch_ms = kms * per_launch
     sweeps = cells * g["sweeps"]
     value = sweeps * steps_per_call * args.steps / dt
-    # algorithmic bytes of one backward-Euler step: T and P read once, T
-    # written once (24 B per cell, however many sweeps the step makes)
-    achieved = 24 * per_launch * cells / (launch_ms / 1e3) / 1e9
+    # HBM bytes one launch must move, however many steps it fuses: T and P
+    # read once, T written once (24 B per cell); the sweeps and the fused
+    # steps stay on chip
+    achieved = 24 * cells / (launch_ms / 1e3) / 1e9
+    # FP64: per cell and sweep six neighbour products and their sums, the
+    # ambient and right-hand-side terms and the scaling by 1 / den
+    flops = THERMAL_FLOPS_PER_CELL_SWEEP * sweeps * per_launch
+    tflops = flops / (launch_ms / 1e3) / 1e12
+    traffic = committed_traffic("thermal_traffic_grid2048.txt", "k_thermal_march", cells)[0]
     out = {
         "metric": "EQ3 thermal grid cell-sweeps/sec on 1 MI355X", "value": value,
         "unit": "cell-sweeps/s", "n_gpus": 1, "steps": args.steps * steps_per_call,
@@ -372,24 +391,23 @@ def bench_thermal(args) -> dict:
         "data": "synthetic",
         "config": {"workload": "EQ3 grid 2048 x 2048 x 8 cells, 4 Jacobi sweeps per backward-"
                                "Euler step, config-4 conductances, random power"},
-        "roofline": {"bound": "hbm", "kernel": "k_thermal_march", "achieved": achieved,
-                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBPS,
-                     "traffic": committed_traffic("thermal_traffic_grid2048.txt",
-                                                  "k_thermal_march", cells)[0],
-                     "traffic_source": "profiles/thermal_traffic_grid2048.txt",
+        "roofline": {"bound": "lds (LDS-staged sweeps; below both the HBM and the FP64 peak)",
+                     "kernel": "k_thermal_march",
+                     "algorithmic": f"24 B per cell per launch (T and P read once, T written "
+                                    f"once; {per_launch:g} steps of {g['sweeps']} sweeps fused "
+                                    f"on chip) x {cells} cells",
+                     "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBPS,
+                     "traffic": traffic, "traffic_source": "profiles/thermal_traffic_grid2048.txt",
+                     "traffic_gbps": traffic / (launch_ms / 1e3) / 1e9 if traffic else None,
+                     "traffic_frac": traffic / (launch_ms / 1e3) / 1e9 / PEAK_HBM_GBPS
+                     if traffic else None,
+                     "fp64": {"flops_per_cell_sweep": THERMAL_FLOPS_PER_CELL_SWEEP,
+                              "achieved_tflops": tflops, "peak_tflops": PEAK_FP64_TFLOPS,
+                              "frac": tflops / PEAK_FP64_TFLOPS},
                      "kernel_ms": launch_ms, "steps_per_launch": per_launch, "step_ms": kms,
-                     "algorithmic": "24 B per cell per step (T and P read, T written; "
-                                    "the 4 sweeps stay on chip) x steps per launch",
-                     "note": "a two-step launch keeps the first step's result on chip, so "
-                             "its HBM traffic is about half its algorithmic bytes; its time "
-                             "is set by the FP64 stencil arithmetic, not by HBM",
-                     # the per-sweep model (8 B read + 8 B written per cell and sweep): a
-                     # kernel that kept no sweep on chip would need these bytes, so a
-                     # blocked one can pass 1.0 on it
-                     "per_sweep_model": {"bytes_per_cell_sweep": 16,
-                                         "achieved": 16 * sweeps / (kms / 1e3) / 1e9,
-                                         "frac": 16 * sweeps / (kms / 1e3) / 1e9
-                                         / PEAK_HBM_GBPS}},
+                     "from_profile": roofline_from_profile("thermal_kernel_grid2048.txt",
+                                                           "k_thermal_march", 24 * cells)},
     }
     if not args.no_cpu:
         sys.path.insert(0, str(ROOT / "tests"))
@@ -413,27 +431,114 @@ def bench_thermal(args) -> dict:
     return out
 
 
-def sub_line(engine, profile, ranges, batches, records, args, what: str, mode="fast") -> dict:
+def sub_line(engine, profile, ranges, batches, records, args, what: str, mode="fast",
+             apply_rereads: bool = False, kernels_summary: str | None = None,
+             traffic_summary: str | None = None) -> dict:
     """One more workload timed like the main line (same step count), with
-    its own roofline for the dominant per-record kernel."""
+    its own roofline for the dominant per-record kernel, the same roofline
+    recomputed from the committed kernel summary it cites, and the HBM
+    traffic of that summary's counter companion."""
     value, dt, kms, streamed = time_steps(engine, profile, ranges, batches, records, args, mode)
     names = ["k_summary", "k_carry", "k_apply"]
-    kb = kernel_bytes(records)
+    kb = kernel_bytes(records, apply_rereads)
     dominant = 0 if kms[0] >= kms[2] else 2
     per_launch = streamed / args.steps
     achieved = kb[names[dominant]] * per_launch / (kms[dominant] / 1e3) / 1e9
     algo = RECORD_BYTES[records] + 8
+    roof = {"bound": "hbm", "kernel": names[dominant],
+            "algorithmic": f"{kb[names[dominant]]} B per access x {int(per_launch)} accesses "
+                           f"per launch",
+            "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": achieved / PEAK_HBM_GBPS,
+            "kernel_ms": {nm: float(v) for nm, v in zip(names, kms)},
+            "apply_bytes_per_access": kb["k_apply"],
+            "algorithmic_bytes_per_access": algo,
+            "pipeline_frac": value * algo / 1e9 / PEAK_HBM_GBPS}
+    if kernels_summary is not None:
+        roof["from_profile"] = roofline_from_profile(kernels_summary, names[dominant],
+                                                     kb[names[dominant]] * per_launch)
+    if traffic_summary is not None:
+        traffic, src = committed_traffic(traffic_summary, names[dominant], int(per_launch))
+        roof["traffic"], roof["traffic_source"] = traffic, src
     return {"workload": what, "value": value, "unit": "accesses/s",
             "ms_per_step": dt / args.steps * 1e3,
             "records": "packed 16-byte records" if records == "packed" else "32-byte records",
-            "roofline": {"bound": "hbm", "kernel": names[dominant],
-                         "algorithmic": f"{kb[names[dominant]]} B per access x "
-                                        f"{int(per_launch)} accesses per launch",
-                         "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                         "frac": achieved / PEAK_HBM_GBPS,
-                         "kernel_ms": {nm: float(v) for nm, v in zip(names, kms)},
-                         "algorithmic_bytes_per_access": algo,
-                         "pipeline_frac": value * algo / 1e9 / PEAK_HBM_GBPS}}
+            "roofline": roof}
+
+
+def config_workload(name: str, batches: int = 2):
+    """Configs 0, 1 and 3 as the engine times them (packed records on the
+    GPU): (profile, ranges, packed batches, description, host sample of the
+    first step for the CPU baseline, whether the apply pass re-reads records).
+    Config 0: the 2^20-record stream (random: every step replayed from its
+    records).  Config 1: TinyLlama-1.1B decode steps (17.2M records each).
+    Config 3: full-size paged-KV decode steps (1.17e9 records each)."""
+    import torch
+    from hbfsim_amd import engine, workloads as w
+    if name == "c0":
+        s = w.config0()
+        rec = torch.from_numpy(s.records.view(np.int64)).cuda()
+        desc = {"workload": "config0: 2^20 uniform 128-B reads in one 1 GiB range, Poisson "
+                            "issue gaps of mean 2 ns, seed 0; the same stream each step",
+                "records_per_step": len(s.records), "profile": "c0.json (8 ch x 4 die x 2 plane)"}
+        return (s.profile, s.ranges, [engine.pack_records(rec)], desc, s.records, True)
+    if name == "c1":
+        shape = w.TINYLLAMA
+        spans = w.dense_spans(shape)
+        rec = w.gpu_span_records(*spans, shape.line, shape.gap_ps, shape.issuers)
+        sample = rec[: 1 << 22].cpu().numpy().view(np.uint64)
+        desc = {"workload": "config1: TinyLlama-1.1B decode, 22 layers, every matrix and norm "
+                            "read in 128-B lines by 256 wavefronts; the same step each time",
+                "records_per_step": int(rec.shape[0]), "profile": "c0.json",
+                "ranges": len(w.dense_ranges(shape))}
+        out = [engine.pack_records(rec)]
+        del rec
+        torch.cuda.empty_cache()
+        return (w.PROFILES / "c0.json", w.dense_ranges(shape), out, desc, sample, False)
+    if name == "c3":
+        shape = w.PAGED_KV
+        tables = shape.tables()
+        out, sample, n = [], None, 0
+        for step in range(batches):
+            spans = w.kv_spans(shape, step, tables)
+            rec = w.gpu_span_records(*spans, shape.line, shape.gap_ps, shape.issuers)
+            if sample is None:
+                sample = rec[: 1 << 22].cpu().numpy().view(np.uint64)
+            n = int(rec.shape[0])
+            out.append(engine.pack_records(rec))
+            del rec
+            torch.cuda.empty_cache()
+            log(f"config 3 step {step}: {n} records")
+        desc = {"workload": "config3: paged KV cache on HBF, 32 layers x 8 KV heads x 128 dim "
+                            "bf16, 16-token pages, 64 sequences of 1,024-32,768 tokens (seed 2); "
+                            "each step reads every page and appends one token per sequence and "
+                            "layer (page-fill programs at tPROG 200 us)",
+                "records_per_step": n, "distinct_steps": batches, "profile": "c3.json",
+                "ranges": len(w.kv_ranges(shape))}
+        return (w.PROFILES / "c3.json", w.kv_ranges(shape), out, desc, sample, False)
+    raise SystemExit(f"unknown config {name}")
+
+
+def bench_config(engine_mod, name: str, args, cpu_seconds: float) -> dict:
+    """A config line: whole steps of config 0, 1 or 3 with the dominant
+    kernel's roofline (and the same recomputed from the committed summary it
+    cites) and the CPU oracle on a bounded sample of the same stream."""
+    import torch
+    profile, ranges, batches, desc, sample, rereads = config_workload(name)
+    line = sub_line(engine_mod, profile, ranges, batches, "packed", args, desc["workload"],
+                    apply_rereads=rereads,
+                    kernels_summary=f"engine_kernels_config{name[1:]}_packed.txt",
+                    traffic_summary=f"engine_traffic_config{name[1:]}_packed.txt")
+    line["config"] = desc
+    del batches
+    torch.cuda.empty_cache()
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(profile, ranges, sample, cpu_seconds)
+        line["cpu_baseline"]["speedup"] = {
+            "vs_1_core": line["value"] / line["cpu_baseline"]["value"],
+            "vs_all_cores": line["value"] / line["cpu_baseline"]["parallel"]["value"]
+            if line["cpu_baseline"].get("parallel") else None}
+    return line
 
 
 def bench_general(engine, args) -> dict:
@@ -447,7 +552,9 @@ def bench_general(engine, args) -> dict:
     ranges = [(workloads.RANGE_BASE, 1 << 30, 3)]
     return sub_line(engine, profile, ranges, batches, "packed", args,
                     "config0-shaped random stream: 2^28 uniform 128-B reads in 1 GiB, exponential "
-                    "gaps mean 2 ns, 8 ch x 4 die x 2 plane, 2 distinct batches")
+                    "gaps mean 2 ns, 8 ch x 4 die x 2 plane, 2 distinct batches",
+                    apply_rereads=True, kernels_summary="engine_kernels_general.txt",
+                    traffic_summary="engine_traffic_general.txt")
 
 
 def bench_hybrid(engine, batches, args, packed=None) -> dict:
@@ -467,7 +574,7 @@ def bench_hybrid(engine, batches, args, packed=None) -> dict:
         packed = [engine.pack_records(b) for b in batches]
     return sub_line(engine, path, workloads.moe_ranges(shape), packed, "packed", args,
                     "config2 with hybrid sampling (rate 0.01, warm-up 1,000), packed records",
-                    mode="hybrid")
+                    mode="hybrid", kernels_summary="engine_kernels_config2_hybrid.txt")
 
 
 def link_workload(links: int, per_link: int, seed: int = 5):
@@ -486,7 +593,7 @@ def link_workload(links: int, per_link: int, seed: int = 5):
     return first, ready, direction
 
 
-def bench_link(args, links: int = 1 << 15, per_link: int = 256) -> dict:
+def bench_link(args, links: int = 1 << 17, per_link: int = 256) -> dict:
     """The UCIe Streaming / AoU link stage (hbfsim_amd_link_run): `links`
     independent links, each carrying `per_link` reads through the reference
     LinkProfile defaults; one step is one run of every link to quiescence.
@@ -516,14 +623,24 @@ def bench_link(args, links: int = 1 << 15, per_link: int = 256) -> dict:
     dt = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
     achieved = 17 * n / (ms / 1e3) / 1e9
+    # two lanes per link, 64-lane waves; the small LDS form (4 admitted
+    # messages and 4 flit slots per direction, 6 KiB per wave) leaves room
+    # for 7 waves per SIMD (71 VGPRs), so all of them are resident at once
+    simds = 4 * torch.cuda.get_device_properties(0).multi_processor_count
+    waves = (2 * links + 63) // 64
     out = {"workload": f"{links} links x {per_link} reads (AR + R each, AR gaps exp mean 3 ns, "
                        f"R 300 ns later), reference LinkProfile defaults (16 GT/s, AR 12 / R 56 "
                        f"granule credits, 4 accepted per direction)",
            "value": n * args.steps / dt, "unit": "messages/s", "ms_per_step": dt / args.steps * 1e3,
-           "roofline": {"bound": "latency (priced against hbm)", "kernel": "k_link",
+           "occupancy": {"waves": waves, "simds": simds, "waves_per_simd": waves / simds,
+                         "kernel_form": "k_link<4, 4> (LDS rings, 6 KiB per wave)",
+                         "resident_waves_per_simd_max": 7},
+           "roofline": {"bound": "latency (dependent event loop per link direction; priced "
+                                 "against hbm)", "kernel": "k_link (with k_link_split)",
                         "algorithmic": f"17 B per message x {n} messages per launch",
                         "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                        "frac": achieved / PEAK_HBM_GBPS, "event_ms": ms},
+                        "frac": achieved / PEAK_HBM_GBPS, "call_ms": ms,
+                        "messages_per_s_per_call": n / (ms / 1e3)},
            "flits": int(counters[:, :, 0].sum())}
     if not args.no_cpu:
         sys.path.insert(0, str(ROOT / "tests"))
@@ -613,6 +730,18 @@ def main() -> None:
                "roofline": line["roofline"]}
         print(json.dumps(out), flush=True)
         return
+    if args.config in ("c0", "c1", "c3"):
+        line = bench_config(engine, args.config, args, args.cpu_seconds)
+        out = {"metric": "modeled HBF accesses/sec on 1 MI355X", "value": line["value"],
+               "unit": "accesses/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+               "ms_per_step": line["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+               "vs_baseline": None, "dtype": "u64", "data": "synthetic",
+               "config": dict(line["config"], records=line["records"]),
+               "roofline": line["roofline"]}
+        if "cpu_baseline" in line:
+            out["cpu_baseline"] = line["cpu_baseline"]
+        print(json.dumps(out), flush=True)
+        return
 
     if args.batches is None:
         args.batches = max(1, min(args.steps + args.warmup, 12))
@@ -647,8 +776,9 @@ def main() -> None:
     achieved = kb[names[dominant]] * per_launch / (avg_ms[dominant] / 1e3) / 1e9
     summary = ("engine_traffic_config2_packed.txt" if records == "packed"
                else "engine_traffic_config2.txt")
-    traffic, traffic_src = (committed_traffic(summary, names[dominant], int(per_launch))
-                            if args.config == "c2" else (None, None))
+    kernels_summary = ("engine_kernels_config2_packed.txt" if records == "packed"
+                       else "engine_kernels_config2.txt")
+    traffic, traffic_src = committed_traffic(summary, names[dominant], int(per_launch))
     out = {
         "metric": "modeled HBF accesses/sec on 1 MI355X",
         "value": value,
@@ -671,16 +801,24 @@ def main() -> None:
                      "traffic_source": traffic_src,
                      "kernel_ms": {nm: float(v) for nm, v in zip(names, avg_ms)},
                      "algorithmic_bytes_per_access": algo,
-                     "pipeline_frac": value * algo / 1e9 / PEAK_HBM_GBPS},
+                     "pipeline_frac": value * algo / 1e9 / PEAK_HBM_GBPS,
+                     "from_profile": roofline_from_profile(
+                         kernels_summary, names[dominant], kb[names[dominant]] * per_launch)},
     }
     if other is not None:
         out["records32"] = other
     if args.config == "c2" and not args.no_extra:
-        log("stream copy peak")
-        peak = stream_copy_peak()
-        out["stream_copy"] = peak
-        out["roofline"]["measured_peak"] = peak["gbps"]
-        out["roofline"]["frac_of_measured_peak"] = achieved / peak["gbps"]
+        log("read / write ceilings")
+        probe = engine.probe_bandwidth()
+        out["stream_probe"] = probe
+        # k_summary only reads (its records), k_apply only writes (completions):
+        # each against the ceiling of its own access pattern
+        out["roofline"]["measured_read_gbps"] = probe["read_gbps"]
+        out["roofline"]["frac_of_measured_read"] = (
+            kb["k_summary"] * per_launch / (avg_ms[0] / 1e3) / 1e9 / probe["read_gbps"])
+        out["roofline"]["measured_write_gbps"] = probe["write_gbps"]
+        out["roofline"]["k_apply_frac_of_measured_write"] = (
+            kb["k_apply"] * per_launch / (avg_ms[2] / 1e3) / 1e9 / probe["write_gbps"])
         log("general path: random stream")
         out["general"] = bench_general(engine, args)
         log("hybrid mode")
@@ -713,6 +851,15 @@ def main() -> None:
         out["thermal"] = {k: th[k] for k in ("metric", "value", "unit", "ms_per_step", "steps",
                                              "warmup", "dtype", "config", "roofline",
                                              "cpu_baseline") if k in th}
+        # configs 0, 1 and 3 at their own sizes, each with its own roofline and
+        # CPU baseline
+        for name in ("c0", "c1", "c3"):
+            log(f"config {name[1:]}")
+            out[f"config{name[1:]}"] = bench_config(
+                engine, name, argparse.Namespace(steps=args.steps, warmup=args.warmup,
+                                                 no_cpu=args.no_cpu),
+                min(3.0, args.cpu_seconds / 2))
+            torch.cuda.empty_cache()
     print(json.dumps(out), flush=True)
 
 

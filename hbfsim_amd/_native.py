@@ -230,6 +230,9 @@ SIGNATURES = {
     "hbfsim_amd_link_run": (_INT, [ctypes.POINTER(LinkProfile), _P, _U32, _P, _P, _SZ, _P, _P,
                                    _P]),
     "hbfsim_amd_validate_profile": (_INT, [ctypes.c_char_p, ctypes.c_char_p, _SZ]),
+    "hbfsim_amd_probe_bandwidth": (_INT, [_P, _SZ, ctypes.c_uint, _P,
+                                          ctypes.POINTER(ctypes.c_float),
+                                          ctypes.POINTER(ctypes.c_float)]),
 }
 
 _lib = None

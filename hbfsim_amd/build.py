@@ -18,7 +18,7 @@ LIB = HERE / "libhbfsim_amd.so"
 
 SOURCES = [CSRC / "engine.hip", CSRC / "gen.hip", CSRC / "thermal.hip", CSRC / "servers.hip",
            CSRC / "hybrid.hip", CSRC / "link.hip", CSRC / "admission.hip", CSRC / "order.hip",
-           CSRC / "api.cpp",
+           CSRC / "probe.hip", CSRC / "api.cpp",
            CSRC / "profile.cpp"]
 HEADERS = [CSRC / "engine.hpp", CSRC / "thermal.hpp", CSRC / "link.hpp", CSRC / "profile.hpp",
            CSRC / "json_min.hpp", ROOT / "include" / "hbfsim_amd.h"]

@@ -130,13 +130,15 @@ __global__ __launch_bounds__(kSplitWaves * 64) void k_link_split(LinkArgs a)
 }
 
 // The message FIFOs and in-flight flit rings of a link live either in LDS
-// (the fast form: at most kLdsMsgSlots messages admitted per direction and
-// kLdsFlitSlots flits in flight, which the reference defaults and every
-// propagation delay up to 5 flit times meet) or in HBM: the message times
-// in place of their ready times in the split lists, the flit rings in a
-// scratch buffer.
-constexpr std::uint32_t kLdsMsgSlots = 16;
-constexpr std::uint32_t kLdsFlitSlots = 8;
+// (the fast forms: at most kMsg messages admitted per direction and kFlit
+// flits in flight) or in HBM: the message times in place of their ready
+// times in the split lists, the flit rings in a scratch buffer.  The small
+// form (4 + 4 slots, 6 KiB per 64-lane workgroup) serves the reference's
+// default of 4 admitted messages without propagation delay and leaves room
+// for 6 waves per SIMD; the large one (16 + 8, 18 KiB: 2 waves per SIMD)
+// serves up to 16 admitted messages and propagation up to 5 flit times.
+constexpr std::uint32_t kSmallMsg = 4, kSmallFlit = 4;
+constexpr std::uint32_t kLargeMsg = 16, kLargeFlit = 8;
 
 // The partner lane's value (lane ^ 1: the same link's other direction), by
 // DPP quad_perm [1, 0, 3, 2].  Both lanes of a link run the loop in step.
@@ -158,13 +160,14 @@ __device__ __forceinline__ std::uint64_t pair64(std::uint64_t v)
 // other direction's pending grant, and errors: those cross between the two
 // lanes once per step, at the points where the reference's step() would
 // read them, and everything else is the lane's own direction.
-template <bool kLds>
+template <std::uint32_t kMsg, std::uint32_t kFlit>
 __global__ __launch_bounds__(kLinkThreads) void k_link(LinkArgs a)
 {
-    __shared__ std::uint64_t s_msg_t[kLds ? kLdsMsgSlots * kLinkThreads : 1];
-    __shared__ std::uint32_t s_msg_i[kLds ? kLdsMsgSlots * kLinkThreads : 1];
-    __shared__ std::uint64_t s_fl_t[kLds ? kLdsFlitSlots * kLinkThreads : 1];
-    __shared__ std::uint32_t s_fl_i[kLds ? kLdsFlitSlots * kLinkThreads : 1];
+    constexpr bool kLds = kMsg != 0;  // else the HBM form
+    __shared__ std::uint64_t s_msg_t[kLds ? kMsg * kLinkThreads : 1];
+    __shared__ std::uint32_t s_msg_i[kLds ? kMsg * kLinkThreads : 1];
+    __shared__ std::uint64_t s_fl_t[kLds ? kFlit * kLinkThreads : 1];
+    __shared__ std::uint32_t s_fl_i[kLds ? kFlit * kLinkThreads : 1];
     const std::uint32_t lane = threadIdx.x;
     const std::uint32_t d = lane & 1u;
     const std::uint32_t l = blockIdx.x * (kLinkThreads / 2) + (lane >> 1);
@@ -431,7 +434,8 @@ int link_run(const hbfsim_amd_link_profile& p, const std::uint64_t* d_first, std
         return HBFSIM_UNSUPPORTED;
     }
     hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-    const bool lds = p.max_accepted <= kLdsMsgSlots && ring <= kLdsFlitSlots;
+    const bool small = p.max_accepted <= kSmallMsg && ring <= kSmallFlit;
+    const bool lds = small || (p.max_accepted <= kLargeMsg && ring <= kLargeFlit);
     // one allocation: the split lists, the AR counts, the flit rings (HBM
     // form) and the error flag, each piece 256-byte aligned
     auto up = [](std::size_t x) { return (x + 255) & ~std::size_t{255}; };
@@ -496,10 +500,14 @@ int link_run(const hbfsim_amd_link_profile& p, const std::uint64_t* d_first, std
         err = hipGetLastError();
         const dim3 grid((links + kLinkThreads / 2 - 1) / (kLinkThreads / 2));  // two lanes a link
         if (err == hipSuccess) {
-            if (lds) {
-                hipLaunchKernelGGL(k_link<true>, grid, dim3(kLinkThreads), 0, stream, a);
+            if (small) {
+                hipLaunchKernelGGL((k_link<kSmallMsg, kSmallFlit>), grid, dim3(kLinkThreads), 0,
+                                   stream, a);
+            } else if (lds) {
+                hipLaunchKernelGGL((k_link<kLargeMsg, kLargeFlit>), grid, dim3(kLinkThreads), 0,
+                                   stream, a);
             } else {
-                hipLaunchKernelGGL(k_link<false>, grid, dim3(kLinkThreads), 0, stream, a);
+                hipLaunchKernelGGL((k_link<0, 0>), grid, dim3(kLinkThreads), 0, stream, a);
             }
             err = hipGetLastError();
         }

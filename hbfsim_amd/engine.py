@@ -427,3 +427,24 @@ def validate_profile(path: str) -> str | None:
     buf = ctypes.create_string_buffer(512)
     code = nat.load().hbfsim_amd_validate_profile(os.fsencode(path), buf, len(buf))
     return None if code == nat.HBFSIM_OK else buf.value.decode()
+
+
+def probe_bandwidth(gib: int = 4, reps: int = 5, stream: Any = None) -> dict:
+    """HBM ceilings of the per-record passes' access patterns on this GPU
+    (hbfsim_amd_probe_bandwidth): `gib` GiB streamed with 16-byte
+    non-temporal loads, then written with 16-byte non-temporal stores of
+    whole 1 KiB rows; GB/s of each, averaged over `reps` passes."""
+    import torch
+    nbytes = gib << 30
+    buf = torch.empty(nbytes // 8, dtype=torch.int64, device="cuda")
+    rms, wms = ctypes.c_float(), ctypes.c_float()
+    nat.check(nat.load().hbfsim_amd_probe_bandwidth(
+        _ptr(buf), nbytes, reps, ctypes.c_void_p(_stream_handle(stream)), ctypes.byref(rms),
+        ctypes.byref(wms)), "bandwidth probe")
+    del buf
+    return {"read_gbps": nbytes / (rms.value / 1e3) / 1e9,
+            "write_gbps": nbytes / (wms.value / 1e3) / 1e9,
+            "read_ms": rms.value, "write_ms": wms.value, "bytes": nbytes, "reps": reps,
+            "how": "hbfsim_amd_probe_bandwidth: 16-B non-temporal loads (one wave per 256 KiB, "
+                   "16 in flight per lane), then 16-B non-temporal stores of 1 KiB rows (one "
+                   "wave per 128 KiB), HIP events"}

@@ -719,6 +719,20 @@ int hbfsim_amd_link_run(const hbfsim_amd_link_profile* profile, const uint64_t* 
 int hbfsim_amd_validate_profile(const char* path, char* error,
                                 size_t error_bytes);
 
+/* ===== 6. Measurement ==================================================
+ *
+ * No counterpart in the reference: the HBM ceilings the benchmark prices
+ * its per-record passes against, measured with their access patterns.
+ * Streams `bytes` of d_buffer (device, 16-byte aligned, at least 256 KiB)
+ * `reps` times with 16-byte non-temporal loads, one wave per 256 KiB and 16
+ * loads in flight per lane (the summary pass's record stream), then `reps`
+ * times with 16-byte non-temporal stores of whole 1 KiB rows, one wave per
+ * 128 KiB (the apply pass's completion stream); *read_ms and *write_ms
+ * receive the average time of one pass (HIP events on `stream`).  The
+ * buffer's contents are overwritten.  Synchronises `stream`. */
+int hbfsim_amd_probe_bandwidth(void* d_buffer, size_t bytes, unsigned reps, void* stream,
+                               float* read_ms, float* write_ms);
+
 #ifdef __cplusplus
 }
 #endif

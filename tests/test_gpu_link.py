@@ -68,15 +68,20 @@ def test_reference_scenarios():
 
 @pytest.mark.parametrize("seed", range(12))
 def test_random_batches(seed):
-    """Even seeds stay within the LDS form's bounds (at most 16 messages
-    admitted per direction, at most 8 flits in flight: propagation up to 5
-    flit times); odd seeds need the HBM form (more admitted messages or a
-    longer propagation delay)."""
+    """Seeds 0, 3, 6, 9 fit the small LDS form (at most 4 messages admitted
+    per direction, at most 4 flits in flight: propagation below 2 flit
+    times); seeds 2, 5, 8, 11 the large one (at most 16 admitted, at most 8
+    flits: propagation up to 5 flit times); the others need the HBM form
+    (more admitted messages or a longer propagation delay)."""
     rng = np.random.default_rng(100 + seed)
     gt = int(rng.choice([8, 16, 32]))
     ser = 32 // gt
-    if seed % 2 == 0:
+    if seed % 3 == 0:
+        accepted, prop = int(rng.integers(1, 5)), int(rng.integers(0, 2 * ser))
+    elif seed % 3 == 2:
         accepted, prop = int(rng.integers(1, 17)), int(rng.integers(0, 5 * ser + 1))
+        if accepted <= 4 and prop < 2 * ser:
+            accepted = 5 + int(rng.integers(0, 12))
     else:
         accepted, prop = int(rng.integers(1, 41)), int(rng.integers(0, 60))
         if accepted <= 16 and prop <= 5 * ser:
@@ -94,11 +99,13 @@ def test_random_batches(seed):
     check_against_oracle(p, links)
 
 
-@pytest.mark.parametrize("accepted,prop", [(4, 5), (16, 23), (17, 5), (4, 24)])
+@pytest.mark.parametrize("accepted,prop", [(4, 7), (5, 7), (4, 8), (4, 5), (16, 23), (17, 5),
+                                           (4, 24)])
 def test_bursts_and_idle_gaps(accepted, prop):
     """Bursts separated by idle periods longer than the pipeline, equal ready
     times across directions, one direction only, empty links; at the edges of
-    the LDS form (16 admitted, 8 flits in flight at 8 GT/s) and just past them."""
+    the small LDS form (4 admitted, 4 flits in flight at 8 GT/s), of the large
+    one (16 admitted, 8 flits) and just past them."""
     p = lk.link_profile(gt_per_second=8, initial_ar_granules=12, initial_r_granules=56,
                         max_accepted=accepted, propagation_ns=prop, consume_delay_ns=(3, 0))
     links = [
