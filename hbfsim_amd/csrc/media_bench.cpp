@@ -12,19 +12,28 @@
 //
 // Every request is split at page boundaries into records of one range that
 // covers the benchmark capacity; the GPU engine (HBF model, profile
-// geometry, engine defaults) times them, and a request completes with its
-// last page.  Latencies are completion - arrival in ns (ceiling of the
-// engine's picoseconds).  The engine's device accepts every request at its
-// arrival: the MQSim adapter's queue-depth admission (mqsim_online.cpp:
-// 291-376) couples each request to earlier completions and is not applied,
-// which the report states in "queue_depth_applied".  Exit 64 on invalid
-// arguments, 70 on other errors, as the reference.
+// geometry, engine defaults) is the media port of the MQSim adapter's
+// admission (mqsim_online.cpp:291-376): at most the profile's queue_depth
+// requests are in the device, a request that arrives while it is full waits
+// in arrival order and enters when a completion frees a slot, and the engine
+// times its pages issued at that admission time; a request's device
+// completion is the ceiling in ns of its last page's.  Completions then pass
+// the adapter's bandwidth cursor in completion order (ties in dispatch
+// order).  Admission couples each request to earlier completions, which
+// depend on the engine state the earlier requests left: the requests are
+// taken in chunks of queue_depth, and a chunk's admission times are iterated
+// to their fixed point, the engine state restored before each retry (device
+// completions grow with admission times, so the iteration rises from
+// admission = arrival to the event loop's times, one request at least per
+// pass).  Latencies are bounded completion - arrival in ns.  Exit 64 on
+// invalid arguments, 70 on other errors, as the reference.
 #include "cli_json.hpp"
 #include "profile.hpp"
 
 #include "../../include/hbfsim_amd.h"
 
 #include <algorithm>
+#include <queue>
 #include <charconv>
 #include <chrono>
 #include <cstdint>
@@ -172,6 +181,106 @@ void check(int status, const char* what)
     }
 }
 
+// Admission times of requests [c, e): a request enters at its arrival while
+// fewer than `depth` requests are in the device, else at the later of its
+// arrival and the earliest device completion among those in it (FIFO, one
+// slot per completion).  `held` holds the device completions of the requests
+// in the device before c; dev[c..e) the current estimates (an admission time
+// stands for a completion not yet known: completions are never earlier).
+std::vector<std::uint64_t> chunk_admissions(
+    const std::priority_queue<std::uint64_t, std::vector<std::uint64_t>,
+                              std::greater<std::uint64_t>>& held,
+    std::uint64_t depth, const std::vector<std::uint64_t>& arrival, std::uint64_t c,
+    std::uint64_t e, const std::vector<std::uint64_t>* dev)
+{
+    auto h = held;
+    std::vector<std::uint64_t> adm(e - c);
+    for (std::uint64_t i = c; i < e; ++i) {
+        std::uint64_t a = arrival[i];
+        if (h.size() >= depth) {
+            a = std::max(a, h.top());
+            h.pop();
+        }
+        adm[i - c] = a;
+        h.push(dev != nullptr ? std::max((*dev)[i - c], a) : a);
+    }
+    return adm;
+}
+
+// Times the requests through the engine under queue-depth admission (see the
+// file comment): per chunk of `depth` requests, admission times and device
+// completions iterated to their fixed point, the engine state restored
+// before every retry.  completion/status per record; device_ns per request.
+int admit_and_time(hbfsim_context* ctx, std::uint64_t requests, std::uint64_t depth,
+                   const std::vector<std::uint64_t>& arrival,
+                   const std::vector<std::uint64_t>& last, std::vector<hbf_record32>& records,
+                   std::vector<std::uint64_t>& completion, std::vector<std::uint8_t>& status,
+                   std::vector<std::uint64_t>& device_ns)
+{
+    std::uint32_t channels = 0, planes = 0;
+    int st = hbfsim_amd_get_geometry(ctx, &channels, &planes);
+    if (st != HBFSIM_OK) {
+        return st;
+    }
+    std::vector<std::uint64_t> busy(planes), tags(2ull * planes), cursor(channels);
+    std::priority_queue<std::uint64_t, std::vector<std::uint64_t>, std::greater<std::uint64_t>>
+        held;
+    for (std::uint64_t c = 0; c < requests; c += depth) {
+        const std::uint64_t e = std::min(requests, c + depth);
+        const std::uint64_t r0 = c == 0 ? 0 : last[c - 1] + 1, r1 = last[e - 1] + 1;
+        std::uint64_t seq = 0, burst = 0;
+        st = hbfsim_amd_get_state(ctx, busy.data(), tags.data(), cursor.data(), &seq, &burst);
+        if (st != HBFSIM_OK) {
+            return st;
+        }
+        std::vector<std::uint64_t> adm = chunk_admissions(held, depth, arrival, c, e, nullptr);
+        std::vector<std::uint64_t> dev(e - c);
+        for (std::uint64_t pass = 0;; ++pass) {
+            if (pass > 0) {
+                st = hbfsim_amd_set_state(ctx, busy.data(), tags.data(), cursor.data(), seq, burst);
+                if (st != HBFSIM_OK) {
+                    return st;
+                }
+            }
+            std::uint64_t r = r0;
+            for (std::uint64_t i = c; i < e; ++i) {
+                for (; r <= last[i]; ++r) {
+                    records[r].issue_ps = adm[i - c] * 1000u;
+                }
+            }
+            st = hbfsim_amd_run(ctx, records.data() + r0, r1 - r0, completion.data() + r0,
+                                status.data() + r0, 0, nullptr);
+            if (st != HBFSIM_OK) {
+                return st;
+            }
+            r = r0;
+            for (std::uint64_t i = c; i < e; ++i) {
+                std::uint64_t done_ps = adm[i - c] * 1000u;
+                for (; r <= last[i]; ++r) {
+                    done_ps = std::max(done_ps, completion[r]);
+                }
+                dev[i - c] = (done_ps + 999) / 1000;
+            }
+            std::vector<std::uint64_t> next = chunk_admissions(held, depth, arrival, c, e, &dev);
+            if (next == adm) {
+                break;  // the times the engine ran with are the fixed point
+            }
+            if (pass > e - c) {
+                return HBFSIM_INVALID_ARGUMENT;  // cannot happen: one request settles per pass
+            }
+            adm = std::move(next);
+        }
+        for (std::uint64_t i = c; i < e; ++i) {
+            if (held.size() >= depth) {
+                held.pop();
+            }
+            held.push(dev[i - c]);
+            device_ns[i] = dev[i - c];
+        }
+    }
+    return HBFSIM_OK;
+}
+
 }  // namespace
 
 int main(int argc, char** argv)
@@ -197,6 +306,7 @@ int main(int argc, char** argv)
         const std::uint64_t page = prof.page_bytes;
         std::vector<hbf_record32> records;
         std::vector<std::uint64_t> last;  // each request's last record
+        std::vector<std::uint64_t> arrival_ns;
         std::uint64_t state = o.seed;
         for (std::uint64_t i = 0; i < o.requests; ++i) {
             const std::uint64_t slot = o.pattern == "random" ? splitmix64(state) % slots
@@ -212,9 +322,12 @@ int main(int argc, char** argv)
                 left -= piece;
             }
             last.push_back(records.size() - 1);
+            arrival_ns.push_back(arrival_ps / 1000);
         }
+        const std::uint64_t depth = std::max<std::uint64_t>(1, prof.queue_depth);
         std::vector<std::uint64_t> completion(records.size());
         std::vector<std::uint8_t> status(records.size());
+        std::vector<std::uint64_t> device_ns(o.requests);
         const std::filesystem::path dir = std::filesystem::temp_directory_path() /
                                           ("hbf-media-bench-" + std::to_string(::getpid()));
         std::filesystem::create_directories(dir);
@@ -230,8 +343,8 @@ int main(int argc, char** argv)
             int st = hbfsim_register_device(ctx, reinterpret_cast<void*>(kRangeBase),
                                             prof.capacity_bytes, &ro);
             if (st == HBFSIM_OK) {
-                st = hbfsim_amd_run(ctx, records.data(), records.size(), completion.data(),
-                                    status.data(), 0, nullptr);
+                st = admit_and_time(ctx, o.requests, depth, arrival_ns, last, records,
+                                    completion, status, device_ns);
             }
             hbfsim_context_destroy(ctx);
             check(st, "engine run");
@@ -243,24 +356,36 @@ int main(int argc, char** argv)
         std::error_code ec;
         std::filesystem::remove_all(dir, ec);
 
+        for (const std::uint8_t b : status) {
+            if ((b & 3u) != HBFSIM_AMD_MODELED) {
+                throw std::runtime_error("the engine did not model a benchmark request");
+            }
+        }
+        // the adapter's completion callbacks, in completion order (ties in
+        // dispatch order, which is request order): the bandwidth cursor
+        std::vector<std::uint64_t> order(o.requests);
+        for (std::uint64_t i = 0; i < o.requests; ++i) order[i] = i;
+        std::sort(order.begin(), order.end(), [&](std::uint64_t a, std::uint64_t b) {
+            return device_ns[a] != device_ns[b] ? device_ns[a] < device_ns[b] : a < b;
+        });
+        const std::uint64_t xfer_ns = static_cast<std::uint64_t>(
+            (static_cast<unsigned __int128>(o.bytes) * 1000000000u +
+             prof.aggregate_bandwidth_bytes_per_s - 1) /
+            prof.aggregate_bandwidth_bytes_per_s);
+        std::vector<std::uint64_t> bounded(o.requests);
+        std::uint64_t cursor = 0;
+        for (const std::uint64_t k : order) {
+            cursor = std::max(cursor, arrival_ns[k]) + xfer_ns;
+            bounded[k] = std::max(device_ns[k], cursor);
+        }
         std::vector<std::uint64_t> latencies;
         latencies.reserve(o.requests);
         std::uint64_t modeled_end_ns = 0;
         unsigned __int128 latency_sum = 0;
-        std::size_t r = 0;
         for (std::uint64_t i = 0; i < o.requests; ++i) {
-            std::uint64_t done_ps = 0;
-            for (; r <= last[i]; ++r) {
-                if ((status[r] & 3u) != HBFSIM_AMD_MODELED) {
-                    throw std::runtime_error("the engine did not model a benchmark request");
-                }
-                done_ps = std::max(done_ps, completion[r]);
-            }
-            const std::uint64_t done_ns = (done_ps + 999) / 1000;
-            const std::uint64_t arrival_ns = i * o.arrival_gap_ns;
-            latencies.push_back(done_ns - arrival_ns);
-            latency_sum += done_ns - arrival_ns;
-            modeled_end_ns = std::max(modeled_end_ns, done_ns);
+            latencies.push_back(bounded[i] - arrival_ns[i]);
+            latency_sum += bounded[i] - arrival_ns[i];
+            modeled_end_ns = std::max(modeled_end_ns, bounded[i]);
         }
         std::sort(latencies.begin(), latencies.end());
         const long double total_bytes =
@@ -293,7 +418,8 @@ int main(int argc, char** argv)
            << "  },\n"
            << "  \"modeled_bandwidth_bytes_per_s\": " << real(bandwidth) << ",\n"
            << "  \"profile\": " << quote(prof.name) << ",\n"
-           << "  \"queue_depth_applied\": false,\n"
+           << "  \"queue_depth\": " << depth << ",\n"
+           << "  \"queue_depth_applied\": true,\n"
            << "  \"requests\": {\n"
            << "    \"completed\": " << o.requests << ",\n"
            << "    \"submitted\": " << o.requests << "\n"

@@ -1380,6 +1380,109 @@ int orc_mqsim_admission(const uint64_t* arrival_ns, const uint64_t* bytes,
     return 0;
 }
 
+/* The adapter's admission and bandwidth cursor (mqsim_online.cpp:269-376)
+ * with this engine as the media port, as one event loop: request k's pages
+ * are records[first[k] .. first[k + 1]); when the loop dispatches it (at its
+ * arrival, or at the completion that frees its slot) the engine times its
+ * pages issued at that time, with the engine state carried from the requests
+ * dispatched before it, and its device completion (ns, the ceiling of the
+ * engine's latest page completion) is an event like MQSim's completion
+ * callback.  Times in ns as the adapter's; issue_ps = dispatch ns * 1000. */
+int orc_engine_admission(const orc_engine_params* p, const orc_range* ranges,
+                         uint32_t range_count, const orc_record* records,
+                         const uint64_t* first, size_t n, const uint64_t* arrival_ns,
+                         const uint64_t* bytes, uint32_t queue_depth, uint64_t bandwidth,
+                         orc_engine_state* s, uint64_t* admission_ns, uint64_t* device_ns,
+                         uint64_t* completion_ns)
+{
+    if (bandwidth == 0 || n >= ((size_t)1 << 32)) {
+        return 1;
+    }
+    if (n == 0) {
+        return 0;
+    }
+    const uint64_t depth = queue_depth == 0 ? 1 : queue_depth;
+    size_t most = 1;
+    for (size_t k = 0; k < n; ++k) {
+        const size_t m = (size_t)(first[k + 1] - first[k]);
+        most = m > most ? m : most;
+    }
+    uint32_t* staged = malloc(n * sizeof(uint32_t));
+    uint32_t* fifo = malloc(n * sizeof(uint32_t));
+    uint8_t* readmitted = calloc(n, 1);
+    adm_event* heap = malloc(3 * n * sizeof(adm_event));
+    orc_record* pages = malloc(most * sizeof(orc_record));
+    uint64_t* done = malloc(most * sizeof(uint64_t));
+    int rc = 0;
+    if (!staged || !fifo || !readmitted || !heap || !pages || !done) {
+        rc = 2;
+        goto out;
+    }
+    size_t size = 0, fhead = 0, ftail = 0;
+    uint64_t order = 0, in_device = 0, cursor = 0;
+    for (size_t i = 0; i < n; ++i) {
+        staged[i] = (uint32_t)i;
+    }
+    adm_sort_key = arrival_ns;
+    qsort(staged, n, sizeof(uint32_t), adm_cmp);  /* flush_staged */
+    for (size_t i = 0; i < n; ++i) {
+        const adm_event e = {arrival_ns[staged[i]], order++, 0, staged[i]};
+        adm_push(heap, &size, e);
+    }
+    while (size != 0) {
+        const adm_event e = adm_pop(heap, &size);
+        const uint32_t k = e.request;
+        if (e.kind == 0) {  /* submit_to_device */
+            if (!readmitted[k]) {
+                if (in_device >= depth) {
+                    fifo[ftail++] = k;
+                    continue;
+                }
+                ++in_device;
+            }
+            readmitted[k] = 0;
+            admission_ns[k] = e.time;  /* dispatch_to_device: the engine times the pages */
+            const size_t b = (size_t)first[k], m = (size_t)(first[k + 1] - first[k]);
+            for (size_t j = 0; j < m; ++j) {
+                pages[j] = records[b + j];
+                pages[j].issue_ps = e.time * 1000u;
+            }
+            orc_engine_report rep;
+            memset(&rep, 0, sizeof(rep));
+            rc = orc_engine_run(p, ranges, range_count, pages, m, 0, s, done, NULL, &rep);
+            if (rc != 0) {
+                goto out;
+            }
+            uint64_t last = e.time * 1000u;
+            for (size_t j = 0; j < m; ++j) {
+                last = done[j] > last ? done[j] : last;
+            }
+            device_ns[k] = (last + 999) / 1000;
+            const adm_event c = {device_ns[k], order++, 1, k};
+            adm_push(heap, &size, c);
+        } else {  /* the completion callback */
+            completion_ns[k] = orc_bandwidth_cursor(&cursor, arrival_ns[k], bytes[k],
+                                                    bandwidth, e.time);
+            --in_device;
+            while (in_device < depth && fhead != ftail) {  /* release_admission_slots */
+                const uint32_t j = fifo[fhead++];
+                readmitted[j] = 1;
+                ++in_device;
+                const adm_event a = {e.time, order++, 0, j};
+                adm_push(heap, &size, a);
+            }
+        }
+    }
+out:
+    free(staged);
+    free(fifo);
+    free(readmitted);
+    free(heap);
+    free(pages);
+    free(done);
+    return rc;
+}
+
 /* prefetch_model.cpp:22-50: k identical servers; a read issued at `now`
  * takes the server that frees first and finishes one latency later. */
 /* MediaServers::issue (prefetch_model.cpp:37-46): the server that frees

@@ -310,6 +310,18 @@ int orc_mqsim_admission(const uint64_t* arrival_ns, const uint64_t* bytes,
                         uint64_t* completion_ns);
 
 /* ---- k-server busy-until (prefetch_model.cpp:22-50) ------------------ */
+/* orc_mqsim_admission with this engine as the media port: request k's
+ * pages are records[first[k] .. first[k + 1]) (first: n + 1 entries), timed
+ * by orc_engine_run (state s carried) when the loop dispatches the request,
+ * issued at that time (ns * 1000 ps); the device completion is the ceiling
+ * in ns of their latest completion.  admission_ns, device_ns and
+ * completion_ns (bounded by the cursor) per request. */
+int orc_engine_admission(const orc_engine_params* p, const orc_range* ranges,
+                         uint32_t range_count, const orc_record* records,
+                         const uint64_t* first, size_t n, const uint64_t* arrival_ns,
+                         const uint64_t* bytes, uint32_t queue_depth, uint64_t bandwidth,
+                         orc_engine_state* s, uint64_t* admission_ns, uint64_t* device_ns,
+                         uint64_t* completion_ns);
 void orc_media_servers(const uint64_t* now_ns, size_t n, uint32_t servers,
                        uint64_t latency_ns, uint64_t* completion_ns);
 

@@ -170,6 +170,8 @@ def lib() -> ctypes.CDLL:
             "orc_media_servers": (None, [_P, ctypes.c_size_t, _U32, _U64, _P]),
             "orc_mqsim_admission": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t, _U32, _U64,
                                                    _P, _P, _P]),
+            "orc_engine_admission": (ctypes.c_int, [_P, _P, _U32, _P, _P, ctypes.c_size_t, _P,
+                                                    _P, _U32, _U64, _P, _P, _P, _P]),
             "orc_simulate_prefetch": (ctypes.c_int, [_P, ctypes.c_size_t, _U32, _U32, _U32,
                                                      _U32, _U64, _U64, _P]),
             "orc_sampler_run": (ctypes.c_int, [_U32, ctypes.c_double, _U64, _P, _P,
@@ -247,6 +249,30 @@ def mqsim_admission(arrival, nbytes, latency, queue_depth: int, bandwidth: int):
                                    bandwidth, addr(out[0]), addr(out[1]), addr(out[2]))
     if rc != 0:
         raise ValueError("bandwidth 0 or too many requests")
+    return tuple(o[:n] for o in out)
+
+
+def engine_admission(params: OrcParams, ranges, count: int, records: np.ndarray,
+                     first: np.ndarray, arrival_ns, nbytes, queue_depth: int, bandwidth: int,
+                     state: "OracleState | None" = None):
+    """orc_engine_admission: the adapter's admission and cursor with the engine
+    as the media port.  records: every request's pages (32-byte records),
+    request k = records[first[k]:first[k + 1]].  Returns (admission, device
+    completion, bounded completion) per request, in ns."""
+    rec = np.ascontiguousarray(records, dtype=np.uint64).reshape(-1, 4)
+    first = np.ascontiguousarray(first, np.uint64)
+    arrival = np.ascontiguousarray(arrival_ns, np.uint64)
+    nbytes = np.ascontiguousarray(nbytes, np.uint64)
+    n = len(arrival)
+    if state is None:
+        state = OracleState(params)
+    out = [np.zeros(max(n, 1), np.uint64) for _ in range(3)]
+    rc = lib().orc_engine_admission(ctypes.byref(params), ranges, count, addr(rec), addr(first),
+                                    n, addr(arrival), addr(nbytes), queue_depth, bandwidth,
+                                    ctypes.byref(state.s), addr(out[0]), addr(out[1]),
+                                    addr(out[2]))
+    if rc != 0:
+        raise RuntimeError(f"oracle admission failed: {rc}")
     return tuple(o[:n] for o in out)
 
 

@@ -82,50 +82,73 @@ def workload(prof, requests, nbytes, operation, gap, pattern, seed, capacity):
     return np.array(rec, np.uint64), last
 
 
+def oracle_report(raw, prof, args, capacity, depth):
+    """The report's timing from the oracle's event loop (orc_engine_admission:
+    the adapter's queue-depth admission and bandwidth cursor with the engine
+    as the media port) over the regenerated workload."""
+    rec, last = workload(raw, args["requests"], args["nbytes"], args["operation"], args["gap"],
+                         args["pattern"], args["seed"], capacity)
+    first = np.concatenate([[0], np.array(last, np.uint64) + 1]).astype(np.uint64)
+    params = oracle_py.engine_params(prof)
+    table, count = oracle_py.range_table([(RANGE_BASE, capacity, 3)], prof["page_bytes"],
+                                         prof["capacity_bytes"])
+    n = args["requests"]
+    arrival = np.arange(n, dtype=np.uint64) * np.uint64(args["gap"])
+    adm, dev, bounded = oracle_py.engine_admission(
+        params, table, count, rec, first, arrival, np.full(n, args["nbytes"], np.uint64), depth,
+        prof["aggregate_bandwidth_bytes_per_s"])
+    lat = sorted(int(b) - int(a) for a, b in zip(arrival, bounded))
+    pct = lambda q: lat[max(1, (q * len(lat) + 99) // 100) - 1]  # noqa: E731
+    return adm, dev, bounded, lat, pct, int(bounded.max())
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("args", [
     dict(requests=1024, nbytes=16384, operation="read", gap=0, pattern="sequential", seed=0),
     dict(requests=3000, nbytes=4096, operation="mixed", gap=50, pattern="random", seed=7),
     dict(requests=500, nbytes=65536, operation="read", gap=200, pattern="random", seed=3),
-    dict(requests=2000, nbytes=1536, operation="write", gap=10, pattern="sequential", seed=0)])
-def test_report_matches_oracle(bench, args):
-    prof = oracle_py.load_profile(NOMINAL)
+    dict(requests=2000, nbytes=1536, operation="write", gap=10, pattern="sequential", seed=0),
+    dict(requests=700, nbytes=16384, operation="read", gap=0, pattern="random", seed=5, depth=4),
+    dict(requests=300, nbytes=8192, operation="mixed", gap=700, pattern="random", seed=9,
+         depth=1),
+    dict(requests=1200, nbytes=32768, operation="read", gap=40, pattern="sequential", seed=0,
+         depth=16)])
+def test_report_matches_oracle(bench, args, tmp_path):
+    """Every latency statistic, the modeled time and bandwidth equal the
+    oracle's event loop; the nominal profile's queue depth (128) and smaller
+    ones (16, 4 and 1) that make requests wait for earlier completions."""
     raw = json.loads(NOMINAL.read_text())
+    path = NOMINAL
+    if "depth" in args:
+        raw["queue_depth"] = args["depth"]
+        path = tmp_path / "nominal-qd.json"
+        path.write_text(json.dumps(raw))
+    prof = oracle_py.load_profile(path)
+    depth = raw["queue_depth"]
     blocks16 = raw["page_bytes"] * raw["pages_per_block"] * raw["planes_per_die"] * \
         raw["dies_per_channel"] * raw["channels"] * 16
     capacity = min(raw["capacity_bytes"], blocks16)
-    p = run(bench, "--profile", NOMINAL, "--requests", args["requests"], "--bytes",
+    p = run(bench, "--profile", path, "--requests", args["requests"], "--bytes",
             args["nbytes"], "--operation", args["operation"], "--arrival-gap-ns", args["gap"],
             "--pattern", args["pattern"], "--seed", args["seed"])
     assert p.returncode == 0, p.stderr
     out = json.loads(p.stdout)
     assert list(out) == sorted(out)
     assert set(out) == {"effective_profile", "engine", "latency_ns",
-                        "modeled_bandwidth_bytes_per_s", "profile", "queue_depth_applied",
-                        "requests", "schema_version", "simulator_requests_per_s", "timing_ns",
-                        "workload"}
-    assert out["engine"] == "hbf-amd-media-only" and out["queue_depth_applied"] is False
+                        "modeled_bandwidth_bytes_per_s", "profile", "queue_depth",
+                        "queue_depth_applied", "requests", "schema_version",
+                        "simulator_requests_per_s", "timing_ns", "workload"}
+    assert out["engine"] == "hbf-amd-media-only" and out["queue_depth_applied"] is True
+    assert out["queue_depth"] == depth
     assert out["effective_profile"]["capacity_bytes"] == capacity
     assert out["requests"] == {"submitted": args["requests"], "completed": args["requests"]}
     assert out["workload"] == {"operation": args["operation"], "pattern": args["pattern"],
                                "seed": args["seed"], "requests": args["requests"],
                                "bytes_per_request": args["nbytes"],
                                "arrival_gap_ns": args["gap"]}
-    rec, last = workload(raw, args["requests"], args["nbytes"], args["operation"], args["gap"],
-                         args["pattern"], args["seed"], capacity)
-    params = oracle_py.engine_params(prof)
-    table, count = oracle_py.range_table([(RANGE_BASE, capacity, 3)], prof["page_bytes"],
-                                         prof["capacity_bytes"])
-    comp, st, _, _ = oracle_py.run(params, table, count, rec)
-    assert ((st & 3) == 0).all()
-    lat, end, first = [], 0, 0
-    for i, j in enumerate(last):
-        done_ns = -(-int(comp[first:j + 1].max()) // 1000)
-        lat.append(done_ns - i * args["gap"])
-        end = max(end, done_ns)
-        first = j + 1
-    lat.sort()
-    pct = lambda q: lat[max(1, (q * len(lat) + 99) // 100) - 1]  # noqa: E731
+    adm, dev, bounded, lat, pct, end = oracle_report(raw, prof, args, capacity, depth)
+    if depth < args["requests"] and args["gap"] == 0:
+        assert adm.max() > 0  # requests waited for slots
     assert out["timing_ns"]["modeled"] == end
     assert out["latency_ns"] == {"average": sum(lat) // len(lat), "p50": pct(50), "p99": pct(99)}
     expect = args["requests"] * args["nbytes"] * 1e9 / end

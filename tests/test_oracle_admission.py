@@ -91,3 +91,87 @@ def test_closed_forms():
     np.testing.assert_array_equal(again[2], done)
     with pytest.raises(ValueError):
         oracle_py.mqsim_admission(arrival, nbytes, latency, 1, 0)
+
+
+# ---- the same loop with the engine as the media port (orc_engine_admission)
+
+def _media_case(n, nbytes, gap, seed, flat=False):
+    """The media bench's workload on the nominal profile: n requests of
+    nbytes at random 16 KiB-aligned slots, arrivals i * gap ns, split at
+    pages; returns (profile, params, table, count, records, first, arrival)."""
+    from test_media_bench import NOMINAL, RANGE_BASE
+    prof = oracle_py.load_profile(NOMINAL)
+    opts = dict(flat_geometry=1, page_buffers=0, plane_contention=0,
+                channel_bandwidth_bytes_per_s=1 << 60) if flat else {}
+    params = oracle_py.engine_params(prof, **opts)
+    cap = 1 << 30
+    table, count = oracle_py.range_table([(RANGE_BASE, cap, 3)], prof["page_bytes"],
+                                         prof["capacity_bytes"])
+    rng = np.random.default_rng(seed)
+    page = prof["page_bytes"]
+    rec, first = [], [0]
+    for i in range(n):
+        addr = int(rng.integers(0, cap // nbytes)) * nbytes
+        left = nbytes
+        while left:
+            piece = min(left, page - addr % page)
+            rec.append((RANGE_BASE + addr, piece, 0, 0))
+            addr += piece
+            left -= piece
+        first.append(len(rec))
+    arrival = np.arange(n, dtype=np.uint64) * np.uint64(gap)
+    return prof, params, table, count, np.array(rec, np.uint64), np.array(first, np.uint64), \
+        arrival
+
+
+def test_engine_port_unbounded_queue_is_one_engine_run():
+    """Queue depth beyond the request count: every request dispatched at its
+    arrival, so the device completions are one engine run of all pages
+    issued at their arrivals."""
+    prof, params, table, count, rec, first, arrival = _media_case(400, 32768, 30, 1)
+    adm, dev, _ = oracle_py.engine_admission(params, table, count, rec, first, arrival,
+                                             np.full(400, 32768, np.uint64), 1000,
+                                             prof["aggregate_bandwidth_bytes_per_s"])
+    np.testing.assert_array_equal(adm, arrival)
+    issued = rec.copy()
+    for k in range(400):
+        issued[first[k]:first[k + 1], 2] = arrival[k] * np.uint64(1000)
+    comp, _, _, _ = oracle_py.run(params, table, count, issued)
+    want = [-(-int(comp[first[k]:first[k + 1]].max()) // 1000) for k in range(400)]
+    np.testing.assert_array_equal(dev, np.array(want, np.uint64))
+
+
+@pytest.mark.parametrize("depth", [1, 3, 32])
+def test_engine_port_fixed_latency_is_the_fake_port_loop(depth):
+    """A single plane without page register or contention, with a channel
+    so fast that transfers never bind: every request's device time is its
+    admission + tR, the fake media port of orc_mqsim_admission, whose loop the
+    results must then equal exactly."""
+    n = 300
+    prof, params, table, count, rec, first, arrival = _media_case(n, 16384, 2000, 2, flat=True)
+    nb = np.full(n, 16384, np.uint64)
+    bw = prof["aggregate_bandwidth_bytes_per_s"]
+    got = oracle_py.engine_admission(params, table, count, rec, first, arrival, nb, depth, bw)
+    want = oracle_py.mqsim_admission(arrival, nb, prof["read_latency_ns"], depth, bw)
+    for g, w_ in zip(got, want):
+        np.testing.assert_array_equal(g, w_)
+
+
+def test_engine_port_one_slot_chains_requests():
+    """One slot: request k dispatches at max(arrival_k, device_{k-1}) and the
+    engine times the requests one after another with its state carried."""
+    n = 200
+    prof, params, table, count, rec, first, arrival = _media_case(n, 16384, 500, 3)
+    adm, dev, _ = oracle_py.engine_admission(params, table, count, rec, first, arrival,
+                                             np.full(n, 16384, np.uint64), 1,
+                                             prof["aggregate_bandwidth_bytes_per_s"])
+    state = oracle_py.OracleState(params)
+    prev = 0
+    for k in range(n):
+        t = max(int(arrival[k]), prev)
+        assert int(adm[k]) == t
+        pages = rec[first[k]:first[k + 1]].copy()
+        pages[:, 2] = t * 1000
+        comp, _, _, _ = oracle_py.run(params, table, count, pages, 0, state)
+        prev = -(-int(comp.max()) // 1000)
+        assert int(dev[k]) == prev
