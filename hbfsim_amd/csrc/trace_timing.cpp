@@ -9,12 +9,17 @@
 // reads, tPROG for writes; transfer = ceil(page * 1e9 / aggregate)).  All
 // pages of one event have the same cost, so an event contributes
 // pages * cost in one saturating step -- the replay is parse-bound, and this
-// is host code.  In hybrid mode the library's GPU HybridSampler
-// (hbfsim_amd_sampler_reference, calibrator.cpp:83-96) picks the requests
-// the reference would send to MQSim (hbf_trace_timing.cpp:196-206); MQSim is
-// not part of this build, so those requests are counted as reference
-// requests and timed by the fast model, and the report says so in
-// "reference_timing".  mqsim mode needs MQSim for every request: it exits 2.
+// is host code that streams the events.  In hybrid mode the library's GPU
+// HybridSampler (hbfsim_amd_sampler_reference, calibrator.cpp:83-96) picks
+// the requests the reference sends to its detailed engine, MQSim
+// (hbf_trace_timing.cpp:196-213).  MQSim is not part of this build; the
+// library's engine stands in for it: a picked page request arrives at the
+// demand clock, the engine times it on the GPU (per-plane tR / tPROG with
+// the page register, the channel cursor, its state carried from one picked
+// request to the next), and, as after an MQSim completion, the clock moves to
+// its completion (ns, rounded up) and the modeled service grows by
+// completion - arrival.  The report names that engine in "reference_timing".
+// mqsim mode needs MQSim for every request: it exits 2.
 //
 // Output: the reference's JSON report, keys sorted and two-space indented as
 // nlohmann::json::dump(2) prints it.  Exit 64 on invalid arguments or
@@ -31,6 +36,7 @@
 #include <chrono>
 #include <cstdint>
 #include <cstdio>
+#include <filesystem>
 #include <fstream>
 #include <iostream>
 #include <limits>
@@ -214,6 +220,53 @@ std::vector<std::uint8_t> sample_requests(const hbfamd::profile& prof, const std
 
 }  // namespace
 
+// The library's engine as the detailed model of hybrid mode: one range over
+// the profile's capacity, so a request's media page is its logical address
+// divided by the page size; each picked page request is one record.
+class detailed_engine {
+public:
+    detailed_engine(const options& o, const hbfamd::profile& prof)
+    {
+        const std::string dir = std::filesystem::temp_directory_path().string();
+        const hbfsim_options co{o.profile_path.c_str(), dir.c_str(), HBFSIM_MODEL_FAST, 64,
+                                1000000000ull};
+        if (hbfsim_context_create(&co, &ctx_) != HBFSIM_OK) {
+            throw std::runtime_error("the detailed engine failed to start (it needs a GPU)");
+        }
+        const hbfsim_range_options ro{HBFSIM_RANGE_MODE_TIMING, HBFSIM_RANGE_READ_WRITE,
+                                      HBFSIM_CACHE_POLICY_NONE, 0};
+        if (hbfsim_register_device(ctx_, reinterpret_cast<void*>(kBase), prof.capacity_bytes,
+                                   &ro) != HBFSIM_OK) {
+            hbfsim_context_destroy(ctx_);
+            throw std::runtime_error("the detailed engine refused the profile's capacity");
+        }
+    }
+    ~detailed_engine() { hbfsim_context_destroy(ctx_); }
+    detailed_engine(const detailed_engine&) = delete;
+    detailed_engine& operator=(const detailed_engine&) = delete;
+
+    // Completion (ns, rounded up) of one page request arriving at arrival_ns.
+    std::uint64_t complete(std::uint64_t logical, std::uint32_t page_bytes, bool write,
+                           std::uint64_t arrival_ns)
+    {
+        if (arrival_ns > std::numeric_limits<std::uint64_t>::max() / 1000) {
+            throw std::overflow_error("demand clock beyond the engine's picosecond range");
+        }
+        const hbf_record32 r{kBase + logical, page_bytes, arrival_ns * 1000u, write ? 1u : 0u};
+        std::uint64_t done_ps = 0;
+        std::uint8_t status = 0;
+        if (hbfsim_amd_run(ctx_, &r, 1, &done_ps, &status, 0, nullptr) != HBFSIM_OK ||
+            (status & 3u) != HBFSIM_AMD_MODELED) {
+            throw std::runtime_error("the detailed engine did not time a page request");
+        }
+        return done_ps / 1000 + (done_ps % 1000 != 0 ? 1u : 0u);
+    }
+
+private:
+    static constexpr std::uint64_t kBase = 0x4000'0000'0000ull;
+    hbfsim_context* ctx_ = nullptr;
+};
+
 int main(int argc, char** argv)
 {
     try {
@@ -228,28 +281,11 @@ int main(int argc, char** argv)
         }
         std::uint64_t input_events = 0, sequence = 0, clock_ns = 0, service_ns = 0;
         std::uint64_t fast_requests = 0, reference_requests = 0;
-        std::vector<event> evs;
+        std::vector<event> evs;  // hybrid mode: the sampler takes every request at once
         std::string line;
         const auto t0 = std::chrono::steady_clock::now();
-        while (std::getline(in, line)) {
-            if (line.empty()) {
-                continue;
-            }
-            ++input_events;
-            const event ev = parse_event(json_min::parse(line), input_events);
-            if (ev.page_bytes != prof.page_bytes || ev.logical_address + ev.bytes > prof.capacity_bytes) {
-                throw std::invalid_argument(
-                    "event page size or range differs from the frozen profile");
-            }
-            evs.push_back(ev);
-        }
-        std::vector<std::uint8_t> sampled;
-        if (o.mode == "hybrid") {
-            sampled = sample_requests(prof, evs);
-        }
-        std::size_t k = 0;
-        for (const event& ev : evs) {
-            const std::uint64_t pages = ev.bytes / ev.page_bytes;
+        // the fast model of one event's pages (hbf_trace_timing.cpp:214-231)
+        const auto fast = [&](const event& ev, std::uint64_t pages) {
             const std::uint64_t base = ev.write ? prof.program_latency_ns : prof.read_latency_ns;
             const std::uint64_t service =
                 fast_service(base, ev.page_bytes, prof.aggregate_bandwidth_bytes_per_s);
@@ -260,16 +296,52 @@ int main(int argc, char** argv)
             }
             service_ns = sat_add_n(service_ns, pages, service);
             clock_ns = sat_add_n(clock_ns, pages, exposed);
-            sequence += pages;
-            std::uint64_t ref = 0;
-            if (!sampled.empty()) {
-                for (std::uint64_t p = 0; p < pages; ++p) {
-                    ref += sampled[k + p];
-                }
-                k += pages;
+            fast_requests += pages;
+        };
+        while (std::getline(in, line)) {
+            if (line.empty()) {
+                continue;
             }
-            reference_requests += ref;
-            fast_requests += pages - ref;
+            ++input_events;
+            const event ev = parse_event(json_min::parse(line), input_events);
+            if (ev.page_bytes != prof.page_bytes || ev.logical_address + ev.bytes > prof.capacity_bytes) {
+                throw std::invalid_argument(
+                    "event page size or range differs from the frozen profile");
+            }
+            const std::uint64_t pages = ev.bytes / ev.page_bytes;
+            sequence += pages;
+            if (o.mode == "hybrid") {
+                evs.push_back(ev);
+            } else {
+                fast(ev, pages);
+            }
+        }
+        if (o.mode == "hybrid") {
+            const std::vector<std::uint8_t> sampled = sample_requests(prof, evs);
+            detailed_engine detail(o, prof);
+            std::size_t k = 0;
+            for (const event& ev : evs) {
+                const std::uint64_t pages = ev.bytes / ev.page_bytes;
+                std::uint64_t run = 0;  // pending fast pages, in order
+                for (std::uint64_t p = 0; p < pages; ++p, ++k) {
+                    if (!sampled[k]) {
+                        ++run;
+                        continue;
+                    }
+                    fast(ev, run);
+                    run = 0;
+                    // hbf_trace_timing.cpp:203-208: the detailed engine's
+                    // completion becomes the demand clock
+                    const std::uint64_t arrival = clock_ns;
+                    const std::uint64_t done =
+                        detail.complete(ev.logical_address + p * ev.page_bytes, ev.page_bytes,
+                                        ev.write, arrival);
+                    clock_ns = done;
+                    service_ns = sat_add_n(service_ns, 1, done - arrival);
+                    ++reference_requests;
+                }
+                fast(ev, run);
+            }
         }
         const auto wall = static_cast<std::uint64_t>(
             std::chrono::duration_cast<std::chrono::nanoseconds>(
@@ -284,7 +356,8 @@ int main(int argc, char** argv)
            << "  \"profile\": " << quote(prof.name) << ",\n"
            << "  \"reference_sample_rate\": " << real(prof.reference_sample_rate) << ",\n"
            << (o.mode == "hybrid"
-                   ? "  \"reference_timing\": \"hbf-fast (MQSim is not part of this engine)\",\n"
+                   ? "  \"reference_timing\": \"hbf-amd-engine (per-plane tR/tPROG, page "
+                     "register and channel cursor on the GPU, in place of MQSim)\",\n"
                    : "")
            << "  \"reference_warmup_requests\": " << prof.reference_warmup_requests << ",\n"
            << "  \"requests\": {\n"

@@ -1,10 +1,12 @@
 """hbf_trace_timing --mode hybrid: the page requests the reference's replay
-would send to MQSim (hbf_trace_timing.cpp:196-206: HybridSampler(warmup,
-rate, 0).reference(sequence - 1, access)) are picked by the library's GPU
-sampler and counted as reference requests; the count must equal the CPU
-oracle's sampler over the same request sequence, and the clocks the fast
-mode's (MQSim is absent, so the sampled requests are timed by the fast model
-and the report's reference_timing says so)."""
+sends to MQSim (hbf_trace_timing.cpp:196-213: HybridSampler(warmup, rate,
+0).reference(sequence - 1, access)) are picked by the library's GPU sampler
+and timed by the library's engine in MQSim's place: the request arrives at
+the demand clock, and its completion becomes the clock.  The count must equal
+the CPU oracle's sampler over the same request sequence, and both clocks the
+replay recomputed here with the oracle's engine (state carried from one
+picked request to the next) for the picked requests and the fast model's
+arithmetic for the others."""
 from __future__ import annotations
 
 import json
@@ -46,11 +48,45 @@ def test_hybrid_mode_counts_sampled_requests(cli, tmp_path, name):  # noqa: F811
     assert h["engine"] == "hbf-hybrid" and h["status"] == "PASS"
     assert h["requests"] == {"input_expert_misses": len(events), "submitted": len(access),
                              "fast": len(access) - ref, "reference": ref}
-    assert h["reference_timing"].startswith("hbf-fast")
-    for k in ("demand_exposed_stall_ns", "modeled_device_service_ns", "profile",
-              "reference_sample_rate", "reference_warmup_requests", "scheduling_semantics"):
+    assert h["reference_timing"].startswith("hbf-amd-engine")
+    for k in ("profile", "reference_sample_rate", "reference_warmup_requests",
+              "scheduling_semantics"):
         assert h[k] == f[k], k
+    clock, service = replay(prof, path, events, flags)
+    assert h["demand_exposed_stall_ns"] == clock
+    assert h["modeled_device_service_ns"] == service
     assert list(h) == sorted(h)
+
+
+def replay(prof, path, events, flags):
+    """The hybrid replay (hbf_trace_timing.cpp:181-233) with the oracle's
+    engine standing in for MQSim on the picked requests."""
+    o = oracle_py.load_profile(path)
+    params = oracle_py.engine_params(o)
+    base = 0x4000_0000_0000
+    table, count = oracle_py.range_table([(base, o["capacity_bytes"], 3)], o["page_bytes"],
+                                         o["capacity_bytes"])
+    state = oracle_py.OracleState(params)
+    bw = o["aggregate_bandwidth_bytes_per_s"]
+    clock = service = 0
+    k = 0
+    for addr, nbytes, pg, op in events:
+        write = op == "write"
+        lat = o["program_latency_ns"] if write else o["read_latency_ns"]
+        xfer = -(-pg * 10**9 // bw)
+        for p in range(nbytes // pg):
+            if flags[k]:
+                rec = np.array([[base + addr + p * pg, pg, clock * 1000, int(write)]], np.uint64)
+                comp, st, _, _ = oracle_py.run(params, table, count, rec, 0, state)
+                assert st[0] & 3 == 0
+                done = -(-int(comp[0]) // 1000)
+                service += done - clock
+                clock = done
+            else:
+                service += max(lat, xfer)
+                clock += max(lat, xfer)
+            k += 1
+    return clock, service
 
 
 def test_hybrid_reference_known_answer(cli, tmp_path):  # noqa: F811
