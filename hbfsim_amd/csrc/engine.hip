@@ -45,7 +45,9 @@ constexpr int kWave = 64;
 // every per-record kernel.  256 fences (2 KiB) rather than 512 let the
 // summary pass hold 8 waves per CU instead of 7 at 512 planes.
 constexpr std::uint32_t kMaxFences = 256;
-constexpr std::uint32_t kMaxPlanes = 1024;
+// Planes: the summary pass keeps 33 B of state per plane in LDS, which at
+// 4,096 planes (135 KB) still fits gfx950's 160 KB per workgroup.
+constexpr std::uint32_t kMaxPlanes = 4096;
 constexpr std::uint32_t kMaxChannels = 256;
 constexpr std::uint32_t kClsModeled = 0;
 constexpr std::uint32_t kClsBypass = 1;
@@ -4300,6 +4302,22 @@ std::size_t lds_apply(const KArgs& a)
 // waves per CU (gfx950: 160 KB of LDS per CU; both passes run at most three
 // waves per SIMD).
 constexpr std::size_t kLdsPerCuBytes = 160 * 1024;  // gfx950
+// A workgroup may hold all of it; beyond 64 KB of dynamic LDS a kernel has
+// to be allowed the size first (allow_lds).
+constexpr std::size_t kLdsPerBlockBytes = 160 * 1024;
+
+// Raises a kernel's dynamic-LDS limit where a launch needs more than the
+// default 64 KB (geometries of more than about 1,900 planes).
+template <typename F>
+hipError_t allow_lds(F* kernel, std::size_t bytes)
+{
+    if (bytes <= 65536) {
+        return hipSuccess;
+    }
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               static_cast<int>(bytes));
+}
 
 void choose_match(KArgs& a)
 {
@@ -5052,7 +5070,7 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     }
     choose_match(a);
     const std::size_t lds_a = lds_summary(a), lds_c = lds_apply(a);
-    if (lds_a > 65536 || lds_c > 65536) {
+    if (lds_a > kLdsPerBlockBytes || lds_c > kLdsPerBlockBytes) {
         return HBFSIM_UNSUPPORTED;
     }
     hipError_t err = hipSuccess;
@@ -5135,22 +5153,27 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     (void)hipEventRecord(e->ev[0], stream);
     const std::uint8_t* hits = d_hits;
     if (k2) {
+        (void)allow_lds(k_summary<false, true>, lds_a);
         hipLaunchKernelGGL((k_summary<false, true>), grid, dim3(kWave), lds_a, stream, a, d_rec,
                            n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     } else if (refresh_records) {
+        (void)allow_lds(k_summary<true, false>, lds_a);
         hipLaunchKernelGGL((k_summary<true, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
                            n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     } else if (packed && kLdsPerCuBytes / lds_a <= 8) {  // LDS allows at most 8 waves per CU
+        (void)allow_lds(k_summary<false, false, true, true>, lds_a);
         hipLaunchKernelGGL((k_summary<false, false, true, true>), grid, dim3(kWave), lds_a, stream,
                            a, d_rec, n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     } else if (packed) {
+        (void)allow_lds(k_summary<false, false, true>, lds_a);
         hipLaunchKernelGGL((k_summary<false, false, true>), grid, dim3(kWave), lds_a, stream, a,
                            d_rec, n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     } else {
+        (void)allow_lds(k_summary<false, false>, lds_a);
         hipLaunchKernelGGL((k_summary<false, false>), grid, dim3(kWave), lds_a, stream, a, d_rec,
                            n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
@@ -5175,30 +5198,37 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     (void)hipEventRecord(e->ev[2], stream);
     const bool staged = desc != nullptr && staged_steps(a) != 0;
     if (k2) {
+        (void)allow_lds(k_apply<false, true>, lds_c);
         hipLaunchKernelGGL((k_apply<false, true>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
                            base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq, d_comp,
                            d_status, sc.tile_rep, hits, desc);
     } else if (refresh_records && staged) {
+        (void)allow_lds(k_apply<true, false, true>, lds_c);
         hipLaunchKernelGGL((k_apply<true, false, true>), grid, dim3(kWave), lds_c, stream, a,
                            d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq,
                            d_comp, d_status, sc.tile_rep, hits, desc);
     } else if (refresh_records) {
+        (void)allow_lds(k_apply<true, false>, lds_c);
         hipLaunchKernelGGL((k_apply<true, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
                            base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq, d_comp,
                            d_status, sc.tile_rep, hits, desc);
     } else if (packed && staged) {
+        (void)allow_lds(k_apply<false, false, true, true>, lds_c);
         hipLaunchKernelGGL((k_apply<false, false, true, true>), grid, dim3(kWave), lds_c, stream,
                            a, d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry,
                            sc.tseq, d_comp, d_status, sc.tile_rep, hits, desc);
     } else if (packed) {
+        (void)allow_lds(k_apply<false, false, false, true>, lds_c);
         hipLaunchKernelGGL((k_apply<false, false, false, true>), grid, dim3(kWave), lds_c, stream,
                            a, d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry,
                            sc.tseq, d_comp, d_status, sc.tile_rep, hits, desc);
     } else if (staged) {
+        (void)allow_lds(k_apply<false, false, true>, lds_c);
         hipLaunchKernelGGL((k_apply<false, false, true>), grid, dim3(kWave), lds_c, stream, a,
                            d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq,
                            d_comp, d_status, sc.tile_rep, hits, desc);
     } else {
+        (void)allow_lds(k_apply<false, false>, lds_c);
         hipLaunchKernelGGL((k_apply<false, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
                            base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq, d_comp,
                            d_status, sc.tile_rep, hits, desc);

@@ -1,8 +1,11 @@
-"""Geometry at the engine's maxima: 1,024 planes (with 16 channels, and with
-256 channels, the channel maximum too).  Random config-0 records and
-linear/contiguous streams must equal the oracle bit for bit in both record
-forms; a geometry beyond 1,024 planes is refused with HBFSIM_UNSUPPORTED
-when the first run builds the engine."""
+"""Large geometries: 1,024 planes (16 channels, and 256 channels, the channel
+maximum); 2,048 planes as the reference's aggressive profile has them (64
+channels x 8 dies x 4 planes: the summary pass's per-plane LDS state passes
+64 KB); 4,096 planes, the engine's maximum (256 channels; 135 KB of LDS per
+summary wave).  Random config-0 records and linear/contiguous streams must
+equal the oracle bit for bit in both record forms; a geometry beyond 4,096
+planes is refused with HBFSIM_UNSUPPORTED when the first run builds the
+engine."""
 from __future__ import annotations
 
 import json
@@ -28,8 +31,9 @@ def geometry_profile(tmp_path, channels, dies, planes):
     return path
 
 
-@pytest.mark.parametrize("channels,dies,planes", [(16, 16, 4), (256, 1, 4)],
-                         ids=["1024p-16ch", "1024p-256ch"])
+@pytest.mark.parametrize("channels,dies,planes", [(16, 16, 4), (256, 1, 4), (64, 8, 4),
+                                                  (256, 4, 4)],
+                         ids=["1024p-16ch", "1024p-256ch", "2048p-64ch", "4096p-256ch"])
 def test_maximum_geometry(tmp_path, channels, dies, planes):
     path = geometry_profile(tmp_path, channels, dies, planes)
     s = workloads.config0(n=100_000, seed=5, write_fraction_per_mille=50)
@@ -53,7 +57,7 @@ def test_maximum_geometry(tmp_path, channels, dies, planes):
 def test_geometry_beyond_maximum_is_refused(tmp_path):
     import torch
     from hbfsim_amd.engine import Engine
-    path = geometry_profile(tmp_path, 256, 2, 4)  # 2,048 planes
+    path = geometry_profile(tmp_path, 256, 4, 8)  # 8,192 planes
     rec = linear_stream(1, 4, ranges_for())
     e = Engine(str(path))
     try:
