@@ -80,6 +80,17 @@ enum {
     R_PROGRAMS, R_HYBRID, R_MAKESPAN, R_LAT_LO, R_LAT_HI, R_LAT_MAX, R_SERVICE
 };
 
+// A split step's second run (its media page + 1, the lane it starts at and
+// its range id), beside the step's descriptor, whose byte count then carries
+// kSplitFlag.
+struct alignas(16) SplitDesc {
+    std::uint32_t page1b;
+    std::uint32_t k;
+    std::uint32_t ridb;
+    std::uint32_t pad;
+};
+constexpr std::uint32_t kSplitFlag = 0x80000000u;
+
 // Kernel arguments, passed by value.
 struct KArgs {
     // ranges (structure of arrays, sorted by base)
@@ -122,6 +133,8 @@ struct KArgs {
     // hybrid runs: the range id of each linear step beside its descriptor
     // (the sampler's key needs it); null otherwise
     std::uint32_t* desc_rid;
+    // split steps' second runs beside their descriptors (with the descriptors)
+    SplitDesc* desc_split;
     // set to 1 by the summary pass when some record's issue time is below its
     // predecessor's; the carry chain then leaves the engine state untouched
     // and the engine times the stream again from a sorted copy (null: the
@@ -1034,6 +1047,137 @@ __device__ __forceinline__ bool linear_tail(const KArgs& a, const std::uint64_t*
     return true;
 }
 
+// A linear step (k = 0: one run of 64) or a split step (two linear runs,
+// lanes 0 .. k-1 and k .. 63, with one issue time and byte count).
+struct LinStep {
+    std::uint32_t page1, page1b, k, bytes, rid, ridb;
+    std::uint64_t issue;
+};
+
+// Packed steps: a step whose records all share record 0's byte count, issue
+// time and read operation, and whose addresses continue record 0's (one run,
+// split where a page boundary falls inside it) or continue record 0's up to
+// a lane k and lane k's after it (two spans joined).  Each run must lie in
+// one page of a range that admits reads (access_supported,
+// hbf_device.cuh:843-860, for the run's records at once); a run whose first
+// address lies outside the wave-uniform range cache refills it through the
+// full classification (one call site for both runs).
+template <bool kRefresh>
+__device__ __forceinline__ bool linear_detect_split(const KArgs& a, const std::uint64_t* fence,
+                                                    RangeCache& rcu, const Step16& st,
+                                                    std::uint64_t base_ps, bool full, int lane,
+                                                    LinStep& ls)
+{
+    if (!full) {
+        return false;
+    }
+    const uint4& R = st.R;
+    const uint4 r0 = make_uint4(rfl32(R.x), rfl32(R.y), rfl32(R.z), rfl32(R.w));
+    uint4 xu, yu;
+    unpack16(r0, xu, yu);
+    if (yu.z != 0 || xu.z == 0) {
+        return false;  // reads of at least one byte only
+    }
+    const std::uint32_t b0 = xu.z;
+    if (__ballot((R.y >> 16) != b0 || R.z != r0.z || R.w != r0.w) != 0) {
+        return false;
+    }
+    const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
+    const std::uint64_t addr = R.x | (static_cast<std::uint64_t>(R.y & 0xffffu) << 32);
+    const std::uint64_t breaks = __ballot(addr != a0 + static_cast<std::uint64_t>(lane) * b0);
+    std::uint32_t k = 0;  // the split lane (0: none)
+    std::uint64_t a1 = 0;
+    if (breaks != 0) {
+        k = static_cast<std::uint32_t>(__ffsll(static_cast<long long>(breaks)) - 1);
+        a1 = readlane64(addr, static_cast<int>(k));
+        const std::uint64_t own =
+            a1 + static_cast<std::uint64_t>(lane - static_cast<int>(k)) * b0;
+        if (__ballot(lane >= static_cast<int>(k) && addr != own) != 0) {
+            return false;
+        }
+    }
+    ls.issue = base_ps + (yu.x | (static_cast<std::uint64_t>(yu.y) << 32));
+    ls.bytes = b0;
+    ls.page1b = 0;
+    ls.ridb = 0;
+    const std::uint64_t page_mask = (1ull << a.page_shift) - 1;
+    std::uint64_t at = a0;
+    std::uint32_t cnt = k != 0 ? k : static_cast<std::uint32_t>(kWave);
+    for (int part = 0; part < 2; ++part) {
+        if (!(at >= rcu.base && at < rcu.end)) {
+            const uint4 xa = make_uint4(static_cast<std::uint32_t>(at),
+                                        static_cast<std::uint32_t>(at >> 32), b0, 0u);
+            const Dec d = decode<kRefresh, true>(a, fence, rcu, xa, yu, base_ps);
+            if (d.cls != kClsModeled) {
+                return false;
+            }
+        }
+        const std::uint32_t mode = rcu.meta & 0xffu;
+        if ((mode != 1 && mode != 2) || (rcu.meta & (1u << 8)) == 0) {
+            return false;
+        }
+        const std::uint64_t off = at - rcu.base;
+        std::uint64_t span = static_cast<std::uint64_t>(cnt) * b0;
+        if ((off >> a.page_shift) != ((off + span - 1) >> a.page_shift)) {
+            // one run crossing a page boundary: split it there when the
+            // boundary falls between two records
+            const std::uint64_t room = (off | page_mask) + 1 - off;
+            if (part != 0 || k != 0 || room % b0 != 0) {
+                return false;
+            }
+            k = static_cast<std::uint32_t>(room / b0);
+            a1 = a0 + room;
+            cnt = k;
+            span = room;
+        }
+        if (span > rcu.end - at || (off & ~page_mask) > ~0ull - rcu.file_offset) {
+            return false;
+        }
+        const std::uint32_t page1 =
+            static_cast<std::uint32_t>(((rcu.file_offset + off) >> a.page_shift) + 1);
+        if (part == 0) {
+            ls.page1 = page1;
+            ls.rid = rcu.id;
+            if (k == 0) {
+                break;  // a whole linear step
+            }
+        } else {
+            ls.page1b = page1;
+            ls.ridb = rcu.id;
+        }
+        at = a1;
+        cnt = static_cast<std::uint32_t>(kWave) - k;
+    }
+    ls.k = k;
+    return true;
+}
+
+// The step detection of a record form: packed steps may be split; 32-byte
+// steps are whole linear steps or none.
+template <bool kRefresh>
+__device__ __forceinline__ bool detect_step(const KArgs& a, const std::uint64_t* fence,
+                                            RangeCache& rcu, const Step16& st,
+                                            std::uint64_t base_ps, bool full, int lane,
+                                            LinStep& ls)
+{
+    return linear_detect_split<kRefresh>(a, fence, rcu, st, base_ps, full, lane, ls);
+}
+
+template <bool kRefresh>
+__device__ __forceinline__ bool detect_step(const KArgs& a, const std::uint64_t* fence,
+                                            RangeCache& rcu, const Step32& st,
+                                            std::uint64_t base_ps, bool full, int lane,
+                                            LinStep& ls)
+{
+    ls.k = 0;
+    ls.page1b = 0;
+    ls.ridb = 0;
+    const bool lin = linear_detect<kRefresh>(a, fence, rcu, st, base_ps, full, lane, ls.page1,
+                                             ls.issue, ls.bytes);
+    ls.rid = rcu.id;
+    return lin;
+}
+
 // A linear group: D consecutive linear steps continuing one another
 // (record r of the group at address a0 + r * bytes0), each step with its own
 // issue time, all inside the cached range.  Checked at once on the group's
@@ -1177,16 +1321,28 @@ struct alignas(16) StepDesc {
     std::uint64_t issue;
 };
 
-// Linear steps waiting to be folded: lane k holds step k (k < n) -- its media
-// page + 1, issue time and byte count.  Pending steps are always consecutive
-// steps of the tile, the first starting at record `first`.
-struct LinBatch {
+// Linear steps waiting to be folded, as runs: lane r (r < n) holds run r --
+// m consecutive records of one step, issued together and reading one page
+// (its media page + 1, byte count and issue time), starting at lane lo of
+// that step.  A whole linear step is one run (m = 64, lo = 0); a split step
+// (two linear runs, split at lane k: a page boundary inside the step, or two
+// spans joined) is two, (m = k, lo = 0) and (m = 64 - k, lo = k).  Pending
+// steps are always consecutive steps of the tile, `rows` of them, the first
+// starting at record `first`; `split` says whether any is a split step.
+// Only packed records form split steps (kRuns); in a batch of 32-byte
+// records every run is a whole step, which len() and at() give as constants.
+template <bool kRuns>
+struct LinBatchT {
     std::uint32_t page1;
     std::uint32_t bytes;
     std::uint64_t issue;
     std::uint32_t rid;  // range id (kept by the apply pass, for hybrid sampling)
+    std::uint32_t m;    // records of the run
+    std::uint32_t lo;   // lane of its first record in its step
     std::size_t first;
     int n;
+    int rows;
+    bool split;
 
     __device__ __forceinline__ void push(std::uint32_t p1, std::uint64_t i0, std::uint32_t b0,
                                          std::size_t s, std::uint32_t r = 0)
@@ -1199,8 +1355,34 @@ struct LinBatch {
             bytes = b0;
             issue = i0;
             rid = r;
+            m = kWave;
+            lo = 0;
         }
         ++n;
+        ++rows;
+    }
+    // A split step: lanes 0 .. k-1 read page pa - 1, lanes k .. 63 page pb - 1
+    // (needs n <= 62).
+    __device__ __forceinline__ void push_split(std::uint32_t pa, std::uint32_t pb, std::uint32_t k,
+                                               std::uint64_t i0, std::uint32_t b0, std::size_t s,
+                                               std::uint32_t ra, std::uint32_t rb)
+    {
+        if (n == 0) {
+            first = s;
+        }
+        const int l = static_cast<int>(threadIdx.x);
+        if (l == n || l == n + 1) {
+            const bool second = l == n + 1;
+            page1 = second ? pb : pa;
+            bytes = b0;
+            issue = i0;
+            rid = second ? rb : ra;
+            m = second ? kWave - k : k;
+            lo = second ? k : 0u;
+        }
+        n += 2;
+        ++rows;
+        split = true;
     }
     // Appends a linear group's D steps (needs n <= 64 - D).
     template <int D>
@@ -1223,20 +1405,37 @@ struct LinBatch {
             issue = i0;
             bytes = gl.bytes;
             rid = r;
+            m = kWave;
+            lo = 0;
         }
         n += D;
+        rows += D;
     }
+    __device__ __forceinline__ void clear()
+    {
+        n = 0;
+        rows = 0;
+        split = false;
+    }
+    __device__ __forceinline__ std::uint32_t len() const { return kRuns ? m : kWave; }
+    __device__ __forceinline__ std::uint32_t at() const { return kRuns ? lo : 0u; }
+    __device__ __forceinline__ bool any_split() const { return kRuns && split; }
 };
 
-__device__ __forceinline__ LinBatch empty_batch()
+template <bool kRuns>
+__device__ __forceinline__ LinBatchT<kRuns> empty_batch()
 {
-    LinBatch b;
+    LinBatchT<kRuns> b;
     b.page1 = 0;
     b.bytes = 0;
     b.issue = 0;
     b.rid = 0;
+    b.m = kWave;
+    b.lo = 0;
     b.first = 0;
     b.n = 0;
+    b.rows = 0;
+    b.split = false;
     return b;
 }
 
@@ -1425,8 +1624,9 @@ struct StepView {
     std::uint64_t x;  // transfer of one record
 };
 
+template <bool kR>
 __device__ __forceinline__ StepView step_view(const KArgs& a, const std::uint64_t* xp,
-                                              const LinBatch& q, int lane)
+                                              const LinBatchT<kR>& q, int lane)
 {
     StepView v;
     v.m = lane < q.n;
@@ -1465,7 +1665,8 @@ __device__ __forceinline__ std::uint32_t pslot(std::uint32_t plane)
 // Issue order across a batch of linear steps (one issue time per step):
 // every step's time must be at least the one before it, the first step's at
 // least `last` (the last issue time the wave saw before the batch).
-__device__ __forceinline__ void batch_order(const LinBatch& q, int lane, std::uint64_t& last,
+template <bool kR>
+__device__ __forceinline__ void batch_order(const LinBatchT<kR>& q, int lane, std::uint64_t& last,
                                             bool& back)
 {
     const std::uint64_t prev = shfl64(q.issue, lane == 0 ? 0 : lane - 1);
@@ -1473,15 +1674,16 @@ __device__ __forceinline__ void batch_order(const LinBatch& q, int lane, std::ui
     last = readlane64(q.issue, q.n - 1);
 }
 
-// Folds a batch of linear steps into the tile summary: the per-record fold
-// of the general path applied to whole steps.  A step after another record of
-// its plane has plane map (sense, issue + sense) -- lane 0 senses unless its
-// page is the one the plane last read, lanes 1..63 hit; a step that is the
-// tile's first record on its plane records lane 0 as that first record and
-// folds the 63 hits after it, map (0, issue).  The channel map of a step is
-// (64 x, issue + 64 x).
+// Folds a batch of linear runs into the tile summary: the per-record fold of
+// the general path applied to whole runs.  A run of m records after another
+// record of its plane has plane map (sense, issue + sense) -- its first record
+// senses unless its page is the one the plane last read, the others hit; a
+// run that holds the tile's first record on its plane records that record
+// and folds the m - 1 hits after it, map (0, issue) (the identity for m = 1).
+// The channel map of a run is (m x, issue + m x).
+template <bool kR>
 __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t* xp,
-                                             const LinBatch& q, int lane, std::uint64_t* p_fi,
+                                             const LinBatchT<kR>& q, int lane, std::uint64_t* p_fi,
                                              std::uint64_t* p_rA, std::uint64_t* p_rB,
                                              std::uint64_t* c_A, std::uint64_t* c_B,
                                              std::uint32_t* p_f1, std::uint32_t* p_l1,
@@ -1505,11 +1707,14 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
         prev1 = last_page;
     }
     const std::uint64_t ls = prev1 == q.page1 ? 0ull : a.read_ps;
-    const std::uint64_t cx = 64 * v.x;
+    const std::uint64_t cx = q.len() * v.x;
     std::uint64_t Ap = 0, Bp = 0, Ac = 0, Bc = 0;
     if (m) {
+        // a run that holds the tile's first record on its plane records that
+        // one apart; the map of the run's others is (0, issue), the identity
+        // when it has none
         Ap = tfirst ? 0ull : ls;
-        Bp = q.issue + Ap;
+        Bp = tfirst ? (q.len() >= 2 ? q.issue : 0ull) : q.issue + ls;
         Ac = cx;
         Bc = q.issue + cx;
     }
@@ -1541,20 +1746,43 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
 // before issuing a group's loads: vector memory operations complete in
 // issue order, so a store placed after a group's loads would hold up the
 // wait for that group.
-__device__ __forceinline__ void write_descs(StepDesc* desc, std::uint32_t* rid, LinBatch& dq,
-                                            int lane)
+template <bool kR>
+__device__ __forceinline__ void write_descs(StepDesc* desc, SplitDesc* split, std::uint32_t* rid,
+                                            LinBatchT<kR>& dq, int lane)
 {
-    if (dq.n != 0 && desc != nullptr && lane < dq.n) {
-        StepDesc sd;
-        sd.page1 = dq.page1;
-        sd.bytes = dq.bytes;
-        sd.issue = dq.issue;
-        desc[dq.first / kWave + lane] = sd;
-        if (rid != nullptr) {
-            rid[dq.first / kWave + lane] = dq.rid;
+    if (dq.n != 0 && desc != nullptr) {
+        // one descriptor per step, written by its first run's lane; a split
+        // step's second run is the next lane
+        // (32-byte batches hold whole steps only: row = lane, no second runs)
+        const bool head = lane < dq.n && dq.at() == 0;
+        const int row = kR ? __popcll(__ballot(head) & lanemask_lt(lane)) : lane;
+        const int nx = lane + 1 < kWave ? lane + 1 : lane;
+        std::uint32_t nlo = 0, np1 = 0, nrid = 0;
+        if constexpr (kR) {
+            nlo = static_cast<std::uint32_t>(__shfl(static_cast<int>(dq.at()), nx));
+            np1 = static_cast<std::uint32_t>(__shfl(static_cast<int>(dq.page1), nx));
+            nrid = static_cast<std::uint32_t>(__shfl(static_cast<int>(dq.rid), nx));
+        }
+        const bool second = kR && head && lane + 1 < dq.n && nlo != 0;
+        if (head) {
+            const std::size_t at = dq.first / kWave + static_cast<std::size_t>(row);
+            StepDesc sd;
+            sd.page1 = dq.page1;
+            sd.bytes = dq.bytes | (second ? kSplitFlag : 0u);
+            sd.issue = dq.issue;
+            if (second && split == nullptr) {
+                sd = StepDesc{0, 0, 0};  // no side array: replayed from its records
+            }
+            desc[at] = sd;
+            if (second && split != nullptr) {
+                split[at] = SplitDesc{np1, nlo, nrid, 0u};
+            }
+            if (rid != nullptr) {
+                rid[at] = dq.rid;
+            }
         }
     }
-    dq.n = 0;
+    dq.clear();
 }
 
 // 64-bit words of a tile's touched-plane mask.
@@ -1673,8 +1901,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
     __syncthreads();
     RangeCache rc = empty_cache();
     RangeCache rcu = empty_cache();  // wave-uniform copy for linear steps
-    LinBatch q = empty_batch();
-    LinBatch dq = empty_batch();  // a folded batch whose descriptors are not written yet
+    LinBatchT<kPacked> q = empty_batch<kPacked>();
+    LinBatchT<kPacked> dq = empty_batch<kPacked>();  // folded, descriptors not written yet
+    // a batch is folded once it holds kFull runs: packed batches keep two
+    // lanes free for a split step's runs
+    constexpr int kFull = kPacked ? kWave - 1 : kWave;
     std::uint64_t modeled = 0;
     std::uint32_t lin_miss = 0;  // steps in a row that were not linear (wave-uniform)
     // descriptors of steps replayed from their records are zeroed up to 64
@@ -1689,7 +1920,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
     };
     for (std::size_t g = begin; g < end; g += kSpan) {
         pipe.promote();
-        write_descs(desc, a.desc_rid, dq, lane);
+        write_descs(desc, a.desc_split, a.desc_rid, dq, lane);
         if (g + kSpan < end) {
             pipe.issue(rec, g + kSpan, end, lane);
         }
@@ -1700,13 +1931,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             GroupLin<kDepth> gl;
             if (group_linear<kRefresh>(a, fence, rcu, pipe, base_ps, lane, gl)) {
                 q.push_group(gl, g, rcu.id);
-                if (q.n == kWave || gend >= end) {
+                if (q.n >= kFull || gend >= end) {
                     batch_order(q, lane, last_issue, disorder);
                     fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
                                  mt_p, mt_c);
-                    modeled += static_cast<std::uint64_t>(q.n) * kWave;
-                    dq = q;
-                    q.n = 0;
+                    modeled += static_cast<std::uint64_t>(q.rows) * kWave;
+                    dq = q;  // (its descriptors wait for the next group's loads)
+                    q.clear();
                 }
                 continue;
             }
@@ -1719,25 +1950,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             if (!kHits && a.slots == 1 && a.lead == nullptr) {
                 // linear steps wait in a batch; the batch is folded when full, at
                 // the tile's last step, and before any other step (order matters)
-                std::uint32_t lp, lb;
-                std::uint64_t li;
+                LinStep ls;
                 bool lin = false;
                 if (lin_miss < kLinGiveUp || (s / kWave) % kLinProbe == 0) {
-                    lin = linear_detect<kRefresh>(a, fence, rcu, st, base_ps, s + kWave <= end,
-                                                  lane, lp, li, lb);
+                    lin = detect_step<kRefresh>(a, fence, rcu, st, base_ps, s + kWave <= end,
+                                                lane, ls);
                     lin_miss = lin ? 0u : lin_miss + 1u;
                 }
                 if (lin) {
-                    q.push(lp, li, lb, s, rcu.id);
+                    if (ls.k == 0) {
+                        q.push(ls.page1, ls.issue, ls.bytes, s, ls.rid);
+                    } else {
+                        q.push_split(ls.page1, ls.page1b, ls.k, ls.issue, ls.bytes, s, ls.rid,
+                                     ls.ridb);
+                    }
                 }
-                if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= end)) {
+                if (q.n != 0 && (!lin || q.n >= kFull || s + kWave >= end)) {
                     batch_order(q, lane, last_issue, disorder);
                     fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
                                  mt_p, mt_c);
-                    modeled += static_cast<std::uint64_t>(q.n) * kWave;
-                    write_descs(desc, a.desc_rid, dq, lane);  // at most one batch waits
+                    modeled += static_cast<std::uint64_t>(q.rows) * kWave;
+                    write_descs(desc, a.desc_split, a.desc_rid, dq, lane);  // at most one waits
                     dq = q;
-                    q.n = 0;
+                    q.clear();
                 }
                 if (lin) {
                     continue;
@@ -1858,7 +2093,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             }
         }
     }
-    write_descs(desc, a.desc_rid, dq, lane);
+    write_descs(desc, a.desc_split, a.desc_rid, dq, lane);
     if (desc != nullptr) {
         flush_zero();
     }
@@ -2338,8 +2573,9 @@ struct ApplySums {
     std::uint64_t n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq, n_hyb;
 };
 
+template <bool kR>
 __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* xp,
-                                           const LinBatch& q, int lane, std::uint64_t* p_busy,
+                                           const LinBatchT<kR>& q, int lane, std::uint64_t* p_busy,
                                            std::uint64_t* c_busy, std::uint32_t* p_tag,
                                            std::uint64_t* completion, std::uint8_t* status,
                                            ApplySums& t, std::uint64_t* mt_p,
@@ -2556,6 +2792,168 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
     }
 }
 
+// fold_apply for a batch that holds split steps: lane r is run r, m records
+// from lane lo of its step, all issued together and reading one page.  The
+// run-level maps scan as in fold_apply with the channel moving m records;
+// with e = lo + m - 1 the run's records complete at
+//   record lo:           max(lead, top - x (m - 1))
+//   record j > lo:       max(P, top - x (e - j))
+// (P = lead with contention, else the issue time).  Rows are stored whole:
+// lane j of a row takes the run its record belongs to, found by walking the
+// runs row by row (a row's second run starts at a nonzero lane).
+__device__ __forceinline__ void fold_apply_runs(const KArgs& a, const std::uint64_t* xp,
+                                                const LinBatchT<true>& q, int lane,
+                                                std::uint64_t* p_busy, std::uint64_t* c_busy,
+                                                std::uint32_t* p_tag, std::uint64_t* completion,
+                                                std::uint8_t* status, ApplySums& t,
+                                                std::uint64_t* mt_p, std::uint64_t* mt_c)
+{
+    const StepView v = step_view(a, xp, q, lane);
+    const bool m = v.m;
+    const std::uint32_t pkey = m ? v.d.plane : 0u;
+    const std::uint32_t ckey = m ? v.d.chan : 0u;
+    const Group gp = group_plane_runs(a, q.page1, pkey, m, v.active, lane, mt_p);
+    const Group gc = group_by(ckey, a.cbits, m, v.active, lane, mt_c);
+    const std::uint32_t tag = m ? p_tag[pkey] : 0u;
+    const std::uint64_t pbusy = m ? p_busy[pkey] : 0ull;
+    const std::uint64_t cbusy = m ? c_busy[ckey] : 0ull;
+    std::uint32_t prev1 = static_cast<std::uint32_t>(
+        __shfl(static_cast<int>(q.page1), gp.pred < 0 ? lane : gp.pred));
+    if (gp.pred < 0) {
+        prev1 = tag;
+    }
+    const bool lhit = m && prev1 == q.page1;
+    const std::uint64_t ls = lhit ? 0ull : a.read_ps;
+    const std::uint64_t rm = m ? q.m : 1u;
+    const std::uint64_t x = v.x;
+    const std::uint64_t cx = rm * x;
+    std::uint64_t Ap = 0, Bp = 0, Ac = 0, Bc = 0;
+    if (m) {
+        Ap = ls;
+        Bp = q.issue + ls;
+        Ac = cx;
+        Bc = q.issue + cx;
+    }
+    if (a.contention) {
+        scan_pair(gp, Ap, Bp, gc, Ac, Bc, v.d, m, v.active, ls, cx, lane);
+    } else {
+        scan_group(gc, Ac, Bc, lane);
+    }
+    const std::uint64_t lead = a.contention ? umax64(pbusy + Ap, Bp) : q.issue + ls;
+    const std::uint64_t top = umax64(cbusy + Ac, Bc);
+    if (m && lane == gp.last) {
+        if (a.contention) {
+            p_busy[pkey] = lead;
+        }
+        p_tag[pkey] = q.page1;
+    }
+    if (m && lane == gc.last) {
+        c_busy[ckey] = top;
+    }
+    const std::uint64_t P = a.contention ? lead : q.issue;
+    const std::uint64_t D0 = umax64(lead, top - (rm - 1) * x);
+    // accounting: all modeled reads; every record after a run's first hits,
+    // the first when its page was buffered
+    const std::uint64_t recs = static_cast<std::uint64_t>(q.rows) * kWave;
+    if (lane == 0) {
+        t.n_rec += recs;
+        t.n_mod += recs;
+        t.n_rd += recs;
+    }
+    if (m) {
+        t.n_hit += rm - 1 + (lhit ? 1u : 0u);
+        t.svc_sum += umax64(ls, x) + (rm - 1) * x;
+        // sum of the run's completions - m issue, exactly in 128 bits: among
+        // records lo + 1 .. e the last cnt follow the channel, the others P
+        std::uint64_t cnt = 0;
+        if (rm >= 2 && top >= P) {
+            const std::uint64_t D = top - P;
+            std::uint64_t tmax = 0;  // largest t <= m - 2 with x t <= D
+            for (std::uint64_t stp = 32; stp != 0; stp >>= 1) {
+                if (tmax + stp <= rm - 2 && x * (tmax + stp) <= D) {
+                    tmax += stp;
+                }
+            }
+            cnt = tmax + 1;
+        }
+        std::uint64_t lo = D0, hi = 0;
+        const auto add = [&](std::uint64_t f, std::uint64_t w) {  // += f * w
+            const std::uint64_t pl = f * w;
+            const std::uint64_t ph = __umul64hi(f, w);
+            const std::uint64_t n2 = lo + pl;
+            hi += ph + (n2 < lo ? 1u : 0u);
+            lo = n2;
+        };
+        const auto sub = [&](std::uint64_t f, std::uint64_t w) {  // -= f * w
+            const std::uint64_t pl = f * w;
+            const std::uint64_t ph = __umul64hi(f, w);
+            hi -= ph + (lo < pl ? 1u : 0u);
+            lo -= pl;
+        };
+        add(rm - 1 - cnt, P);
+        add(cnt, top);
+        sub(x, cnt * (cnt - (cnt != 0 ? 1 : 0)) / 2);
+        sub(rm, q.issue);
+        const std::uint64_t n2 = t.lat_lo + lo;
+        t.lat_hi += hi + (n2 < t.lat_lo ? 1u : 0u);
+        t.lat_lo = n2;
+        const std::uint64_t most = umax64(lead, top);
+        t.mk = umax64(t.mk, most);
+        t.lat_max = umax64(t.lat_max, most - q.issue);
+    }
+    const std::uint64_t seq0 = t.seq;
+    t.seq += recs;
+    const std::uint32_t e = m ? q.lo + q.m - 1 : 0u;
+    const std::uint32_t hit1 = lhit ? 1u : 0u;
+    wait_vector_loads();
+    int ra = 0;  // the row's first run (wave-uniform)
+    for (int r = 0; r < q.rows; ++r) {
+        const bool two = ra + 1 < q.n && rl32(q.lo, ra + 1) != 0;
+        const int rb = two ? ra + 1 : ra;
+        const std::uint32_t kb = two ? rl32(q.lo, rb) : 0u;
+        const bool second = two && static_cast<std::uint32_t>(lane) >= kb;
+        const auto pick64 = [&](std::uint64_t val) {
+            const std::uint64_t va = readlane64(val, ra);
+            const std::uint64_t vb = readlane64(val, rb);
+            return second ? vb : va;
+        };
+        const auto pick32 = [&](std::uint32_t val) {
+            const std::uint32_t va = rl32(val, ra);
+            const std::uint32_t vb = rl32(val, rb);
+            return second ? vb : va;
+        };
+        const std::uint64_t rP = pick64(P);
+        const std::uint64_t rtop = pick64(top);
+        const std::uint64_t rD0 = pick64(D0);
+        const std::uint64_t rx = pick64(x);
+        const std::uint32_t re = pick32(e);
+        const std::uint32_t j = static_cast<std::uint32_t>(lane);
+        const bool first = j == (second ? kb : 0u);
+        const std::uint64_t done =
+            first ? rD0 : umax64(rP, rtop - rx * static_cast<std::uint64_t>(re - j));
+        const std::size_t at = q.first + static_cast<std::size_t>(r) * kWave + lane;
+        put_done(&completion[at], done);
+        if (status != nullptr || a.hybrid) {
+            std::uint8_t st = first && pick32(hit1) == 0 ? 0u : 4u;
+            if (a.hybrid) {
+                const std::uint64_t key =
+                    ((static_cast<std::uint64_t>(pick32(q.page1)) - 1) << a.page_shift) ^
+                    (static_cast<std::uint64_t>(pick32(q.rid)) << 32);
+                const std::uint64_t qn = seq0 + static_cast<std::uint64_t>(r) * kWave + j;
+                if (qn < a.hybrid_warmup ||
+                    (a.hybrid_threshold != 0 && mix64(qn ^ key) <= a.hybrid_threshold)) {
+                    st |= 8u;
+                    ++t.n_hyb;
+                }
+            }
+            if (status != nullptr) {
+                status[at] = st;
+            }
+        }
+        ra = rb + 1;
+    }
+}
+
 // The apply pass copies a tile's step descriptors into LDS with its other
 // set-up loads (tiles of up to kStageSteps steps, 4 KiB): read per window
 // from memory instead, each read would wait for the previous window's
@@ -2650,6 +3048,69 @@ __device__ __forceinline__ void load_chan_carry(const KArgs& a, const std::uint6
     }
 }
 
+// Runs of descriptor rows r0 .. r1 - 1 of a window (lane r holding row r's
+// descriptor sd, its split side entry sp and range id; smask: the split
+// rows) laid out one run per lane, at most 64: row r's first run sits at
+// lane (r - r0) + the split rows in [r0, r), its second run after it.
+__device__ __forceinline__ void expand_rows(LinBatchT<true>& q, const StepDesc& sd,
+                                            const SplitDesc& sp,
+                                            std::uint32_t rid, std::uint64_t smask, int r0,
+                                            int r1, std::size_t w0, int lane)
+{
+    const std::uint64_t below0 = lanemask_lt(r0);
+    const auto before = [&](int r) {  // runs of rows r0 .. r - 1
+        return (r - r0) + __popcll(smask & lanemask_lt(r) & ~below0);
+    };
+    int r = r0;  // the last row whose first run is at or before this lane
+    for (int stp = 32; stp != 0; stp >>= 1) {
+        if (r + stp < r1 && before(r + stp) <= lane) {
+            r += stp;
+        }
+    }
+    const int nruns = before(r1 - 1) + 1 + static_cast<int>((smask >> (r1 - 1)) & 1ull);
+    const bool second = lane > before(r);
+    const bool two = ((smask >> r) & 1ull) != 0;
+    const std::uint32_t p1 = static_cast<std::uint32_t>(__shfl(static_cast<int>(sd.page1), r));
+    const std::uint32_t by = static_cast<std::uint32_t>(__shfl(static_cast<int>(sd.bytes), r));
+    const std::uint64_t is = shfl64(sd.issue, r);
+    const std::uint32_t ra = static_cast<std::uint32_t>(__shfl(static_cast<int>(rid), r));
+    const std::uint32_t pb = static_cast<std::uint32_t>(__shfl(static_cast<int>(sp.page1b), r));
+    const std::uint32_t k = static_cast<std::uint32_t>(__shfl(static_cast<int>(sp.k), r));
+    const std::uint32_t rb = static_cast<std::uint32_t>(__shfl(static_cast<int>(sp.ridb), r));
+    const bool in = lane < nruns;
+    q.page1 = in ? (second ? pb : p1) : 0u;
+    q.bytes = by & ~kSplitFlag;
+    q.issue = is;
+    q.rid = second ? rb : ra;
+    q.m = two ? (second ? kWave - k : k) : kWave;
+    q.lo = second ? k : 0u;
+    q.first = w0 + static_cast<std::size_t>(r0) * kWave;
+    q.n = nruns;
+    q.rows = r1 - r0;
+    q.split = (smask & lanemask_lt(r1) & ~below0) != 0;
+}
+
+// Folds the apply pass's pending batch (fold_apply_runs when it holds a
+// split step) and empties it.
+template <bool kR>
+__device__ __forceinline__ void fold_batch(const KArgs& a, const std::uint64_t* xp,
+                                           LinBatchT<kR>& q, int lane, std::uint64_t* p_busy,
+                                           std::uint64_t* c_busy, std::uint32_t* p_tag,
+                                           std::uint64_t* completion, std::uint8_t* status,
+                                           ApplySums& t, std::uint64_t* mt_p, std::uint64_t* mt_c)
+{
+    if constexpr (kR) {
+        if (q.any_split()) {
+            fold_apply_runs(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t, mt_p,
+                            mt_c);
+            q.clear();
+            return;
+        }
+    }
+    fold_apply(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t, mt_p, mt_c);
+    q.clear();
+}
+
 // Packed records: three waves per SIMD (at most 168 registers), since the
 // general steps' chains of ballots, shuffles and LDS updates need the
 // latency hiding and the streamed linear steps lose nothing.  32-byte
@@ -2715,30 +3176,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
         }
     }
     __syncthreads();
-    std::uint64_t seq = tile_seq[tile];
-    std::uint64_t n_rec = 0, n_mod = 0, n_byp = 0, n_uns = 0, n_rd = 0, n_wr = 0;
-    std::uint64_t n_hit = 0, n_prog = 0, n_hyb = 0, mk = 0, lat_lo = 0, lat_hi = 0;
-    std::uint64_t lat_max = 0, svc_sum = 0;
+    // the batch folds' accumulators, and the ones only the general path adds to
+    ApplySums t{0, 0, 0, 0, 0, 0, 0, 0, 0, tile_seq[tile], 0};
+    std::uint64_t n_byp = 0, n_uns = 0, n_wr = 0, n_prog = 0;
     RangeCache rc = empty_cache();
     RangeCache rcu = empty_cache();  // wave-uniform copy for linear steps
-    LinBatch q = empty_batch();
+    LinBatchT<kPacked> q = empty_batch<kPacked>();
+    constexpr int kFull = kPacked ? kWave - 1 : kWave;  // as in the summary pass
     std::uint32_t lin_miss = 0;  // steps in a row that were not linear (wave-uniform)
-    const auto fold = [&]() {
-        ApplySums t{n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq, n_hyb};
-        fold_apply(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t, mt_p, mt_c);
-        n_hyb = t.n_hyb;
-        n_rec = t.n_rec;
-        n_mod = t.n_mod;
-        n_rd = t.n_rd;
-        n_hit = t.n_hit;
-        mk = t.mk;
-        lat_lo = t.lat_lo;
-        lat_hi = t.lat_hi;
-        lat_max = t.lat_max;
-        svc_sum = t.svc_sum;
-        seq = t.seq;
-        q.n = 0;
-    };
     // Windows of 64 steps.  A window whose steps the summary pass found all
     // linear is replayed from their descriptors alone, without reading its
     // records; any other window streams its records through the pipeline.
@@ -2756,13 +3201,42 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
             }
             const std::uint64_t all = nst == kWave ? ~0ull : ((1ull << nst) - 1);
             if (__ballot(lane < nst && sd.bytes != 0) == all) {
-                q.page1 = sd.page1;
-                q.bytes = sd.bytes;
-                q.issue = sd.issue;
-                q.rid = a.desc_rid != nullptr && lane < nst ? a.desc_rid[w0 / kWave + lane] : 0u;
-                q.first = w0;
-                q.n = nst;
-                fold();
+                const std::uint32_t rid =
+                    a.desc_rid != nullptr && lane < nst ? a.desc_rid[w0 / kWave + lane] : 0u;
+                // (split steps come from packed records only)
+                const std::uint64_t smask =
+                    kPacked ? __ballot(lane < nst && (sd.bytes & kSplitFlag) != 0) : 0ull;
+                // split steps (packed records only) have their second runs in
+                // the side array; the window's runs fold in one batch, or in
+                // two when they exceed 64
+                SplitDesc sp{0, 0, 0, 0};
+                if (kPacked && ((smask >> lane) & 1ull) != 0) {
+                    sp = a.desc_split[w0 / kWave + lane];
+                }
+                const int runs = nst + __popcll(smask);
+                const int half = runs <= kWave ? nst : nst / 2;
+                for (int r0 = 0; r0 < nst;) {
+                    const int r1 = r0 == 0 ? half : nst;
+                    if constexpr (kPacked) {
+                        if (smask != 0) {
+                            expand_rows(q, sd, sp, rid, smask, r0, r1, w0, lane);
+                        }
+                    }
+                    if (smask == 0) {
+                        q.page1 = sd.page1;
+                        q.bytes = sd.bytes;
+                        q.issue = sd.issue;
+                        q.rid = rid;
+                        q.m = kWave;
+                        q.lo = 0;
+                        q.first = w0;
+                        q.n = nst;
+                        q.rows = nst;
+                    }
+                    fold_batch(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t,
+                               mt_p, mt_c);
+                    r0 = r1;
+                }
                 continue;
             }
         }
@@ -2779,19 +3253,24 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                 const bool valid = i < end;
                 if (!kHits && a.slots == 1 && a.lead == nullptr) {
                     // batched as in the summary pass
-                    std::uint32_t lp, lb;
-                    std::uint64_t li;
+                    LinStep ls;
                     bool lin = false;
                     if (lin_miss < kLinGiveUp || (s / kWave) % kLinProbe == 0) {
-                        lin = linear_detect<kRefresh>(a, fence, rcu, sr, base_ps,
-                                                      s + kWave <= end, lane, lp, li, lb);
+                        lin = detect_step<kRefresh>(a, fence, rcu, sr, base_ps, s + kWave <= end,
+                                                    lane, ls);
                         lin_miss = lin ? 0u : lin_miss + 1u;
                     }
                     if (lin) {
-                        q.push(lp, li, lb, s, rcu.id);
+                        if (ls.k == 0) {
+                            q.push(ls.page1, ls.issue, ls.bytes, s, ls.rid);
+                        } else {
+                            q.push_split(ls.page1, ls.page1b, ls.k, ls.issue, ls.bytes, s,
+                                         ls.rid, ls.ridb);
+                        }
                     }
-                    if (q.n != 0 && (!lin || q.n == kWave || s + kWave >= wend)) {
-                        fold();
+                    if (q.n != 0 && (!lin || q.n >= kFull || s + kWave >= wend)) {
+                        fold_batch(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t,
+                               mt_p, mt_c);
                     }
                     if (lin) {
                         continue;
@@ -2842,27 +3321,27 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                     const bool hit = lane == 0 ? lhit : true;
                     const std::uint64_t svc = lane == 0 ? ls : 0ull;
                     if (a.hybrid) {
-                        const std::uint64_t qn = seq + static_cast<std::uint64_t>(lane);
+                        const std::uint64_t qn = t.seq + static_cast<std::uint64_t>(lane);
                         const std::uint64_t key = ((d.page1 - 1) << a.page_shift) ^
                                                   (static_cast<std::uint64_t>(d.range_id) << 32);
                         if (qn < a.hybrid_warmup ||
                             (a.hybrid_threshold != 0 && mix64(qn ^ key) <= a.hybrid_threshold)) {
                             st |= 8u;
-                            ++n_hyb;
+                            ++t.n_hyb;
                         }
                     }
-                    ++n_mod;
-                    ++n_rd;
+                    ++t.n_mod;
+                    ++t.n_rd;
                     if (hit) {
                         st |= 4u;
-                        ++n_hit;
+                        ++t.n_hit;
                     }
-                    mk = umax64(mk, done);
+                    t.mk = umax64(t.mk, done);
                     const std::uint64_t lat = done - d.issue;
-                    add128(lat_lo, lat_hi, lat);
-                    lat_max = umax64(lat_max, lat);
-                    svc_sum += umax64(svc, xfer);
-                    seq += 64;
+                    add128(t.lat_lo, t.lat_hi, lat);
+                    t.lat_max = umax64(t.lat_max, lat);
+                    t.svc_sum += umax64(svc, xfer);
+                    t.seq += 64;
                 } else if (active != 0) {
                     const std::uint64_t xfer = lane_xfer(a, xp, d, m, active);
                     const std::uint32_t page1 = static_cast<std::uint32_t>(d.page1);
@@ -2905,7 +3384,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                     if (m) {
                         done = umax64(pd, cd);
                         const std::uint64_t rank = __popcll(active & lanemask_lt(lane));
-                        const std::uint64_t qn = seq + rank;
+                        const std::uint64_t qn = t.seq + rank;
                         if (a.hybrid) {
                             const std::uint64_t key =
                                 ((d.page1 - 1) << a.page_shift) ^
@@ -2915,15 +3394,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                                 (a.hybrid_threshold != 0 && mix64(qn ^ key) <= a.hybrid_threshold);
                             if (sampled) {
                                 st |= 8u;
-                                ++n_hyb;
+                                ++t.n_hyb;
                             }
                         }
-                        ++n_mod;
+                        ++t.n_mod;
                         if ((d.bits & 1u) == 0) {
-                            ++n_rd;
+                            ++t.n_rd;
                             if (hit) {
                                 st |= 4u;
-                                ++n_hit;
+                                ++t.n_hit;
                             }
                         } else {
                             n_wr += (d.bits & 4u) ? 0u : 1u;
@@ -2932,16 +3411,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                                 ++n_prog;
                             }
                         }
-                        mk = umax64(mk, done);
+                        t.mk = umax64(t.mk, done);
                         const std::uint64_t lat = done - d.issue;
-                        add128(lat_lo, lat_hi, lat);
-                        lat_max = umax64(lat_max, lat);
-                        svc_sum += umax64(svc, xfer);
+                        add128(t.lat_lo, t.lat_hi, lat);
+                        t.lat_max = umax64(t.lat_max, lat);
+                        t.svc_sum += umax64(svc, xfer);
                     }
-                    seq += __popcll(active);
+                    t.seq += __popcll(active);
                 }
                 if (valid) {
-                    ++n_rec;
+                    ++t.n_rec;
                     if (d.cls == kClsBypass) {
                         done = d.issue;
                         ++n_byp;
@@ -2959,9 +3438,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     }
     // 128-bit latency sum: reduce the high words, then the low words with
     // their carries.
-    std::uint64_t hi = wave_sum(lat_hi);
+    std::uint64_t hi = wave_sum(t.lat_hi);
     std::uint64_t carry = 0;
-    std::uint64_t v = lat_lo;
+    std::uint64_t v = t.lat_lo;
     for (int o = 32; o > 0; o >>= 1) {
         const std::uint64_t other = shfl64(v, threadIdx.x ^ o);
         const std::uint64_t oc = shfl64(carry, threadIdx.x ^ o);
@@ -2971,9 +3450,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     }
     hi += carry;
     const std::uint64_t vals[14] = {
-        wave_sum(n_rec), wave_sum(n_mod), wave_sum(n_byp), wave_sum(n_uns), wave_sum(n_rd),
-        wave_sum(n_wr),  wave_sum(n_hit), wave_sum(n_prog), wave_sum(n_hyb), wave_max(mk),
-        v,               hi,              wave_max(lat_max), wave_sum(svc_sum)};
+        wave_sum(t.n_rec), wave_sum(t.n_mod), wave_sum(n_byp), wave_sum(n_uns), wave_sum(t.n_rd),
+        wave_sum(n_wr),  wave_sum(t.n_hit), wave_sum(n_prog), wave_sum(t.n_hyb), wave_max(t.mk),
+        v,               hi,              wave_max(t.lat_max), wave_sum(t.svc_sum)};
     if (lane < 14) {
         unsigned long long out = 0;
 #pragma unroll
@@ -3328,6 +3807,7 @@ struct engine {
     DevReport* d_tile_rep{nullptr};
     StepDesc* d_desc{nullptr};  // per-step descriptors (records / 64)
     std::uint32_t* d_desc_rid{nullptr};  // and their range ids (hybrid runs)
+    SplitDesc* d_desc_split{nullptr};    // and split steps' second runs
     std::size_t desc_cap{0};
     hipEvent_t ev[4]{};
     float last_ms[3]{0, 0, 0};
@@ -3455,6 +3935,7 @@ void free_scratch(engine* e)
     hfree(e->d_tile_rep);
     hfree(e->d_desc);
     hfree(e->d_desc_rid);
+    hfree(e->d_desc_split);
     e->desc_cap = 0;
     e->tile_cap = 0;
 }
@@ -5130,21 +5611,25 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     // step descriptors, where the apply pass replays linear steps from them
     StepDesc* desc = nullptr;
     if (ext_scratch != nullptr) {
-        desc = sc.desc;  // packed runs: one page register, no sampling
+        desc = sc.desc;  // packed runs: one page register, no sampling; split
+                         // steps go without descriptors (no side array)
     } else if (!k2 && a.slots == 1 && !grouping) {
         const std::size_t nsteps = (n + kWave - 1) / kWave;
         if (nsteps > e->desc_cap) {
             hfree(e->d_desc);
             hfree(e->d_desc_rid);
+            hfree(e->d_desc_split);
             e->desc_cap = 0;
             const std::size_t cap = nsteps + nsteps / 8;  // headroom, as for the tiles
-            if (halloc(e->d_desc, cap) != hipSuccess || halloc(e->d_desc_rid, cap) != hipSuccess) {
+            if (halloc(e->d_desc, cap) != hipSuccess || halloc(e->d_desc_rid, cap) != hipSuccess ||
+                halloc(e->d_desc_split, cap) != hipSuccess) {
                 free_group();
                 return HBFSIM_CUDA_ERROR;
             }
             e->desc_cap = cap;
         }
         desc = e->d_desc;
+        a.desc_split = e->d_desc_split;
         if (a.hybrid != 0) {
             a.desc_rid = e->d_desc_rid;
         }
