@@ -140,6 +140,10 @@ struct KArgs {
     // and the engine times the stream again from a sorted copy (null: the
     // stream is known to be in issue order)
     std::uint32_t* disorder;
+    // per tile, written by the summary pass of packed records: 1 when the
+    // tile holds a split step (the apply pass then takes its split-capable
+    // body), else 0; null when the run takes no linear batches
+    std::uint8_t* tile_split;
 };
 
 // Record operations: 0 read, 1 write, and 2 refresh of media page `addr`
@@ -1152,18 +1156,27 @@ __device__ __forceinline__ bool linear_detect_split(const KArgs& a, const std::u
     return true;
 }
 
-// The step detection of a record form: packed steps may be split; 32-byte
-// steps are whole linear steps or none.
-template <bool kRefresh>
+// The step detection of a record form: packed steps may be split (kSplit);
+// otherwise, and for 32-byte records, steps are whole linear steps or none.
+template <bool kRefresh, bool kSplit>
 __device__ __forceinline__ bool detect_step(const KArgs& a, const std::uint64_t* fence,
                                             RangeCache& rcu, const Step16& st,
                                             std::uint64_t base_ps, bool full, int lane,
                                             LinStep& ls)
 {
-    return linear_detect_split<kRefresh>(a, fence, rcu, st, base_ps, full, lane, ls);
+    if constexpr (kSplit) {
+        return linear_detect_split<kRefresh>(a, fence, rcu, st, base_ps, full, lane, ls);
+    }
+    ls.k = 0;
+    ls.page1b = 0;
+    ls.ridb = 0;
+    const bool lin = linear_detect<kRefresh>(a, fence, rcu, st, base_ps, full, lane, ls.page1,
+                                             ls.issue, ls.bytes);
+    ls.rid = rcu.id;
+    return lin;
 }
 
-template <bool kRefresh>
+template <bool kRefresh, bool kSplit>
 __device__ __forceinline__ bool detect_step(const KArgs& a, const std::uint64_t* fence,
                                             RangeCache& rcu, const Step32& st,
                                             std::uint64_t base_ps, bool full, int lane,
@@ -1868,6 +1881,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
                                         : static_cast<const hbf_record32*>(rec)[begin - 1].issue_ps);
     }
     bool disorder = false;
+    bool any_split = false;  // some step of the tile was split (wave-uniform)
     // (the page-register variant takes no linear groups and keeps 4 deep;
     // packed records keep kSumPipe steps too, which leaves registers for a
     // third wave per SIMD: as fast on streamed steps, a quarter faster on
@@ -1953,7 +1967,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
                 LinStep ls;
                 bool lin = false;
                 if (lin_miss < kLinGiveUp || (s / kWave) % kLinProbe == 0) {
-                    lin = detect_step<kRefresh>(a, fence, rcu, st, base_ps, s + kWave <= end,
+                    lin = detect_step<kRefresh, kPacked>(a, fence, rcu, st, base_ps, s + kWave <= end,
                                                 lane, ls);
                     lin_miss = lin ? 0u : lin_miss + 1u;
                 }
@@ -1963,6 +1977,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
                     } else {
                         q.push_split(ls.page1, ls.page1b, ls.k, ls.issue, ls.bytes, s, ls.rid,
                                      ls.ridb);
+                        any_split = true;
                     }
                 }
                 if (q.n != 0 && (!lin || q.n >= kFull || s + kWave >= end)) {
@@ -2099,6 +2114,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
     }
     if (disorder && a.disorder != nullptr && lane == 0) {
         *a.disorder = 1u;
+    }
+    if (kPacked && a.tile_split != nullptr && lane == 0) {
+        a.tile_split[tile] = any_split ? 1u : 0u;
     }
     __syncthreads();
     // Only planes the tile touched get a summary, packed in plane order; the
@@ -3111,23 +3129,23 @@ __device__ __forceinline__ void fold_batch(const KArgs& a, const std::uint64_t* 
     q.clear();
 }
 
-// Packed records: three waves per SIMD (at most 168 registers), since the
-// general steps' chains of ballots, shuffles and LDS updates need the
-// latency hiding and the streamed linear steps lose nothing.  32-byte
-// records hold twice the bytes per step in registers and would spill.
-template <bool kRefresh, bool kHits, bool kStaged = false, bool kPacked = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 : 1))) void k_apply(
-    KArgs a, const void* rec, std::size_t n, std::uint64_t base_ps, const PlaneCarry* pcarry,
-    const MaskWord* tmask, const std::uint64_t* ccarry, const std::uint64_t* tile_seq,
-    std::uint64_t* completion, std::uint8_t* status, DevReport* tile_rep,
-    const std::uint8_t* hits, const StepDesc* desc)
+// The apply pass over one tile.  kSplit: the tile holds split steps (packed
+// records; the summary pass says so per tile), which its batches take as
+// runs; without it the body is the whole-step one, whose folds and stores
+// then keep every register the pass has (the split-capable body needs more:
+// compiled into the same code path it would make the whole-step folds spill).
+template <bool kRefresh, bool kHits, bool kStaged, bool kPacked, bool kSplit>
+__device__ __forceinline__ void apply_tile(
+    const KArgs& a, const void* rec, std::size_t n, std::uint64_t base_ps,
+    const PlaneCarry* pcarry, const MaskWord* tmask, const std::uint64_t* ccarry,
+    const std::uint64_t* tile_seq, std::uint64_t* completion, std::uint8_t* status,
+    DevReport* tile_rep, const std::uint8_t* hits, const StepDesc* desc, std::uint64_t* sm,
+    std::uint64_t* xp)
 {
-    extern __shared__ std::uint64_t sm[];
     std::uint64_t* fence = sm;
     std::uint64_t* p_busy = fence + a.r_nfence;
     std::uint64_t* c_busy = p_busy + a.Rp;
     std::uint32_t* p_tag = reinterpret_cast<std::uint32_t*>(c_busy + a.Rc);
-    __shared__ std::uint64_t xp[33];
     const int lane = threadIdx.x;
     const std::size_t tile = blockIdx.x;
     // set-up loads in flight together: the fences, then the carry-ins, which
@@ -3181,8 +3199,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     std::uint64_t n_byp = 0, n_uns = 0, n_wr = 0, n_prog = 0;
     RangeCache rc = empty_cache();
     RangeCache rcu = empty_cache();  // wave-uniform copy for linear steps
-    LinBatchT<kPacked> q = empty_batch<kPacked>();
-    constexpr int kFull = kPacked ? kWave - 1 : kWave;  // as in the summary pass
+    LinBatchT<kSplit> q = empty_batch<kSplit>();
+    constexpr int kFull = kSplit ? kWave - 1 : kWave;  // room for a split step's runs
     std::uint32_t lin_miss = 0;  // steps in a row that were not linear (wave-uniform)
     // Windows of 64 steps.  A window whose steps the summary pass found all
     // linear is replayed from their descriptors alone, without reading its
@@ -3200,42 +3218,52 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                 }
             }
             const std::uint64_t all = nst == kWave ? ~0ull : ((1ull << nst) - 1);
-            if (__ballot(lane < nst && sd.bytes != 0) == all) {
+            // (a split step's descriptor in a tile not marked split: the
+            // window is streamed, where such a step takes the general path)
+            const bool ok = sd.bytes != 0 && (kSplit || (sd.bytes & kSplitFlag) == 0);
+            if (__ballot(lane < nst && ok) == all) {
                 const std::uint32_t rid =
                     a.desc_rid != nullptr && lane < nst ? a.desc_rid[w0 / kWave + lane] : 0u;
-                // (split steps come from packed records only)
                 const std::uint64_t smask =
-                    kPacked ? __ballot(lane < nst && (sd.bytes & kSplitFlag) != 0) : 0ull;
-                // split steps (packed records only) have their second runs in
-                // the side array; the window's runs fold in one batch, or in
-                // two when they exceed 64
+                    kSplit ? __ballot(lane < nst && (sd.bytes & kSplitFlag) != 0) : 0ull;
+                // split steps have their second runs in the side array; the
+                // window's runs fold in one batch, or in two when they exceed 64
                 SplitDesc sp{0, 0, 0, 0};
-                if (kPacked && ((smask >> lane) & 1ull) != 0) {
+                if (kSplit && ((smask >> lane) & 1ull) != 0) {
                     sp = a.desc_split[w0 / kWave + lane];
                 }
-                const int runs = nst + __popcll(smask);
-                const int half = runs <= kWave ? nst : nst / 2;
-                for (int r0 = 0; r0 < nst;) {
-                    const int r1 = r0 == 0 ? half : nst;
-                    if constexpr (kPacked) {
-                        if (smask != 0) {
-                            expand_rows(q, sd, sp, rid, smask, r0, r1, w0, lane);
-                        }
-                    }
-                    if (smask == 0) {
-                        q.page1 = sd.page1;
-                        q.bytes = sd.bytes;
-                        q.issue = sd.issue;
-                        q.rid = rid;
-                        q.m = kWave;
-                        q.lo = 0;
-                        q.first = w0;
-                        q.n = nst;
-                        q.rows = nst;
-                    }
+                if constexpr (!kSplit) {
+                    q.page1 = sd.page1;
+                    q.bytes = sd.bytes;
+                    q.issue = sd.issue;
+                    q.rid = rid;
+                    q.first = w0;
+                    q.n = nst;
+                    q.rows = nst;
                     fold_batch(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t,
                                mt_p, mt_c);
-                    r0 = r1;
+                } else {
+                    const int runs = nst + __popcll(smask);
+                    const int half = runs <= kWave ? nst : nst / 2;
+                    for (int r0 = 0; r0 < nst;) {
+                        const int r1 = r0 == 0 ? half : nst;
+                        if (smask != 0) {
+                            expand_rows(q, sd, sp, rid, smask, r0, r1, w0, lane);
+                        } else {
+                            q.page1 = sd.page1;
+                            q.bytes = sd.bytes;
+                            q.issue = sd.issue;
+                            q.rid = rid;
+                            q.m = kWave;
+                            q.lo = 0;
+                            q.first = w0;
+                            q.n = nst;
+                            q.rows = nst;
+                        }
+                        fold_batch(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t,
+                                   mt_p, mt_c);
+                        r0 = r1;
+                    }
                 }
                 continue;
             }
@@ -3256,8 +3284,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
                     LinStep ls;
                     bool lin = false;
                     if (lin_miss < kLinGiveUp || (s / kWave) % kLinProbe == 0) {
-                        lin = detect_step<kRefresh>(a, fence, rcu, sr, base_ps, s + kWave <= end,
-                                                    lane, ls);
+                        lin = detect_step<kRefresh, kSplit>(a, fence, rcu, sr, base_ps,
+                                                            s + kWave <= end, lane, ls);
                         lin_miss = lin ? 0u : lin_miss + 1u;
                     }
                     if (lin) {
@@ -3461,6 +3489,33 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
         }
         tile_rep[tile].v[lane] = out;
     }
+}
+
+// Packed records: three waves per SIMD (at most 168 registers), since the
+// general steps' chains of ballots, shuffles and LDS updates need the
+// latency hiding and the streamed linear steps lose nothing.  32-byte
+// records hold twice the bytes per step in registers and would spill.
+template <bool kRefresh, bool kHits, bool kStaged = false, bool kPacked = false>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 : 1))) void k_apply(
+    KArgs a, const void* rec, std::size_t n, std::uint64_t base_ps, const PlaneCarry* pcarry,
+    const MaskWord* tmask, const std::uint64_t* ccarry, const std::uint64_t* tile_seq,
+    std::uint64_t* completion, std::uint8_t* status, DevReport* tile_rep,
+    const std::uint8_t* hits, const StepDesc* desc)
+{
+    extern __shared__ std::uint64_t sm[];
+    __shared__ std::uint64_t xp[33];
+    if constexpr (kPacked) {
+        if (a.tile_split != nullptr && a.tile_split[blockIdx.x] != 0) {
+            apply_tile<kRefresh, kHits, kStaged, kPacked, true>(a, rec, n, base_ps, pcarry, tmask,
+                                                                ccarry, tile_seq, completion,
+                                                                status, tile_rep, hits, desc, sm,
+                                                                xp);
+            return;
+        }
+    }
+    apply_tile<kRefresh, kHits, kStaged, kPacked, false>(a, rec, n, base_ps, pcarry, tmask,
+                                                         ccarry, tile_seq, completion, status,
+                                                         tile_rep, hits, desc, sm, xp);
 }
 
 // Folds the per-tile report partials into one report (sums, maxima and the
@@ -3805,6 +3860,7 @@ struct engine {
     std::uint64_t* d_gcount{nullptr};
     std::uint64_t* d_gseq{nullptr};
     DevReport* d_tile_rep{nullptr};
+    std::uint8_t* d_tsplit{nullptr};  // per tile: holds a split step
     StepDesc* d_desc{nullptr};  // per-step descriptors (records / 64)
     std::uint32_t* d_desc_rid{nullptr};  // and their range ids (hybrid runs)
     SplitDesc* d_desc_split{nullptr};    // and split steps' second runs
@@ -3832,6 +3888,7 @@ struct RunScratch {
     std::uint64_t* gseq;
     DevReport* tile_rep;
     StepDesc* desc;
+    std::uint8_t* tsplit;
 };
 
 namespace {
@@ -3839,7 +3896,8 @@ namespace {
 // Lays a run's scratch out in one buffer from `base`, each piece 256-byte
 // aligned: per tile the plane summaries and carries (64 B per plane), the
 // mask words (16 B per 64 planes), the channel summaries and carries (24 B
-// per channel), two counters and a tile report (128 B); per group of kGroup
+// per channel), two counters, a tile report (128 B) and a split flag (1 B);
+// per group of kGroup
 // tiles the same summaries and carries; and 16 B of step descriptor per 64
 // records.  Returns the bytes needed; with base == nullptr it only counts.
 std::size_t carve_scratch(const KArgs& a, std::size_t ntiles, std::size_t nsteps,
@@ -3870,6 +3928,7 @@ std::size_t carve_scratch(const KArgs& a, std::size_t ntiles, std::size_t nsteps
     take(t.gseq, groups);
     take(t.tile_rep, ntiles);
     take(t.desc, nsteps);
+    take(t.tsplit, ntiles);
     if (s != nullptr) {
         *s = t;
     }
@@ -3933,6 +3992,7 @@ void free_scratch(engine* e)
     hfree(e->d_gcount);
     hfree(e->d_gseq);
     hfree(e->d_tile_rep);
+    hfree(e->d_tsplit);
     hfree(e->d_desc);
     hfree(e->d_desc_rid);
     hfree(e->d_desc_split);
@@ -3963,7 +4023,8 @@ int ensure_scratch(engine* e, std::size_t ntiles)
     if (halloc(e->d_gpsum, gcap * rp) != hipSuccess || halloc(e->d_gcsum, gcap * rc) != hipSuccess ||
         halloc(e->d_gpcarry, gcap * rp) != hipSuccess ||
         halloc(e->d_gccarry, gcap * rc) != hipSuccess || halloc(e->d_gcount, gcap) != hipSuccess ||
-        halloc(e->d_gseq, gcap) != hipSuccess || halloc(e->d_tile_rep, cap) != hipSuccess) {
+        halloc(e->d_gseq, gcap) != hipSuccess || halloc(e->d_tile_rep, cap) != hipSuccess ||
+        halloc(e->d_tsplit, cap) != hipSuccess) {
         free_scratch(e);
         return HBFSIM_CUDA_ERROR;
     }
@@ -5547,7 +5608,11 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         }
         sc = RunScratch{e->d_psum, e->d_tmask, e->d_csum, e->d_pcarry, e->d_ccarry,
                         e->d_tcount, e->d_tseq, e->d_gpsum, e->d_gcsum, e->d_gpcarry,
-                        e->d_gccarry, e->d_gcount, e->d_gseq, e->d_tile_rep, nullptr};
+                        e->d_gccarry, e->d_gcount, e->d_gseq, e->d_tile_rep, nullptr,
+                        e->d_tsplit};
+    }
+    if (packed) {
+        a.tile_split = sc.tsplit;  // the summary pass marks tiles with split steps
     }
     choose_match(a);
     const std::size_t lds_a = lds_summary(a), lds_c = lds_apply(a);
