@@ -333,7 +333,7 @@ int hbfsim_amd_run_device_packed(hbfsim_context* context,
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference.  Same arguments and
  * results; it calls no allocator: the run's scratch (per tile of T records:
- * 64 B per plane, 24 B per channel, 16 B per 64 planes and 144 B; per group
+ * 64 B per plane, 24 B per channel, 16 B per 64 planes and 145 B; per group
  * of 16 tiles the same summaries; 16 B per 64 records) comes from a static
  * array of 64 MiB per device, held until the process ends.  T is the
  * context's tile_records or, by default, the automatic tile doubled (up to
