@@ -1079,6 +1079,26 @@ HBF_API int hbfsim_amd_link_run(const hbfsim_amd_link_profile* profile, const ui
     }
 }
 
+HBF_API int hbfsim_amd_link_run_traced(const hbfsim_amd_link_profile* profile,
+                                       const uint64_t* d_first, uint32_t links,
+                                       const uint64_t* d_ready_ns, const uint8_t* d_direction,
+                                       size_t n, uint64_t* d_delivered_ns,
+                                       hbfsim_amd_link_counters* d_counters,
+                                       hbfsim_amd_link_flit* d_flits, uint32_t flit_limit,
+                                       void* stream)
+{
+    if (profile == nullptr || profile->struct_size != sizeof(hbfsim_amd_link_profile) ||
+        d_flits == nullptr || flit_limit == 0) {
+        return HBFSIM_INVALID_ARGUMENT;
+    }
+    try {
+        return hbfamd::link_run(*profile, d_first, links, d_ready_ns, d_direction, n,
+                                d_delivered_ns, d_counters, stream, d_flits, flit_limit);
+    } catch (...) {
+        return HBFSIM_IO_ERROR;
+    }
+}
+
 HBF_API int hbfsim_amd_validate_profile(const char* path, char* error, size_t error_bytes)
 {
     if (error != nullptr && error_bytes != 0) {

@@ -496,6 +496,7 @@ typedef struct orc_link_counters {
     uint64_t flits, wire_bytes, ucie_header_bytes, crc_position_bytes;
     uint64_t aou_header_bytes, aou_message_bytes, unused_message_bytes;
     uint64_t credit_only_flits;
+    uint64_t accounting_saturated;  /* 1 once any count reached 2^64 - 1 */
 } orc_link_counters;
 typedef struct orc_link_fragment {
     uint64_t request_id;
@@ -533,6 +534,14 @@ const orc_link_flit* orc_link_flit_at(const orc_link* l, size_t i);
 int orc_link_scenario(const orc_link_profile* p, const uint32_t* dir, const uint64_t* ready,
                       size_t n, const uint64_t delay[2], uint64_t* delivered,
                       orc_link_counters* counters);
+/* the same, also copying the link's flit records (the first 4096 in
+ * emission order) to flits[0 .. min(count, flits_cap)) and the number not
+ * recorded to *dropped */
+int orc_link_scenario_traced(const orc_link_profile* p, const uint32_t* dir,
+                             const uint64_t* ready, size_t n, const uint64_t delay[2],
+                             uint64_t* delivered, orc_link_counters* counters,
+                             orc_link_flit* flits, size_t flits_cap, size_t* nflits,
+                             uint64_t* dropped);
 
 #ifdef __cplusplus
 }

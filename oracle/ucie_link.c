@@ -253,9 +253,15 @@ const orc_link_counters* orc_link_counters_of(const orc_link* l, uint32_t dir)
 size_t orc_link_flit_count(const orc_link* l) { return l->nflits; }
 const orc_link_flit* orc_link_flit_at(const orc_link* l, size_t i) { return &l->flits[i]; }
 
-static void add_sat(uint64_t* target, uint64_t amount)
+/* link.cpp:15-23: bounded at 2^64 - 1; the direction's flag records it */
+static void add_sat(orc_link_counters* c, uint64_t* target, uint64_t amount)
 {
-    *target = amount > UINT64_MAX - *target ? UINT64_MAX : *target + amount;
+    if (amount > UINT64_MAX - *target) {
+        *target = UINT64_MAX;
+        c->accounting_saturated = 1;
+    } else {
+        *target += amount;
+    }
 }
 
 /* link.cpp:112-177 for one direction; 0 ok, 2 time overflow, 3 no memory */
@@ -331,14 +337,14 @@ static int send_ready(orc_link* l, uint32_t dir)
         e.dir = dir;
         if (!push_event(l, e)) return 3;
     }
-    add_sat(&c->flits, 1);
-    add_sat(&c->wire_bytes, 256);
-    add_sat(&c->ucie_header_bytes, 2);
-    add_sat(&c->crc_position_bytes, 4);
-    add_sat(&c->aou_header_bytes, 10);
-    add_sat(&c->aou_message_bytes, (uint64_t)used * 5);
-    add_sat(&c->unused_message_bytes, (uint64_t)(48 - used) * 5);
-    if (used == 0) add_sat(&c->credit_only_flits, 1);
+    add_sat(c, &c->flits, 1);
+    add_sat(c, &c->wire_bytes, 256);
+    add_sat(c, &c->ucie_header_bytes, 2);
+    add_sat(c, &c->crc_position_bytes, 4);
+    add_sat(c, &c->aou_header_bytes, 10);
+    add_sat(c, &c->aou_message_bytes, (uint64_t)used * 5);
+    add_sat(c, &c->unused_message_bytes, (uint64_t)(48 - used) * 5);
+    if (used == 0) add_sat(c, &c->credit_only_flits, 1);
     if (l->nflits < FLIT_TRACE_LIMIT) {
         rec.direction = dir;
         rec.start_ns = start;
@@ -416,9 +422,11 @@ int orc_link_step(orc_link* l, orc_link_delivery* out, size_t cap, size_t* count
  * ready time and the time the caller finds room (after each step).
  * delivered[i] receives message i's delivery time.  0 ok, else the first
  * error a link call returned. */
-int orc_link_scenario(const orc_link_profile* p, const uint32_t* dir, const uint64_t* ready,
-                      size_t n, const uint64_t delay[2], uint64_t* delivered,
-                      orc_link_counters* counters)
+int orc_link_scenario_traced(const orc_link_profile* p, const uint32_t* dir,
+                             const uint64_t* ready, size_t n, const uint64_t delay[2],
+                             uint64_t* delivered, orc_link_counters* counters,
+                             orc_link_flit* flits, size_t flits_cap, size_t* nflits,
+                             uint64_t* dropped)
 {
     orc_link* l = orc_link_create(p);
     if (!l) return 1;
@@ -474,10 +482,24 @@ int orc_link_scenario(const orc_link_profile* p, const uint32_t* dir, const uint
         counters[0] = l->counters[0];
         counters[1] = l->counters[1];
     }
+    if (flits) {
+        const size_t k = l->nflits < flits_cap ? l->nflits : flits_cap;
+        memcpy(flits, l->flits, k * sizeof(orc_link_flit));
+        if (nflits) *nflits = k;
+    }
+    if (dropped) *dropped = l->flits_dropped;
 done:
     free(order[0]);
     free(order[1]);
     free(out);
     orc_link_destroy(l);
     return rc;
+}
+
+int orc_link_scenario(const orc_link_profile* p, const uint32_t* dir, const uint64_t* ready,
+                      size_t n, const uint64_t delay[2], uint64_t* delivered,
+                      orc_link_counters* counters)
+{
+    return orc_link_scenario_traced(p, dir, ready, n, delay, delivered, counters, NULL, 0, NULL,
+                                    NULL);
 }

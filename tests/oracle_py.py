@@ -483,7 +483,7 @@ class OrcLinkProfile(ctypes.Structure):
 
 LINK_COUNTER_FIELDS = ("flits", "wire_bytes", "ucie_header_bytes", "crc_position_bytes",
                        "aou_header_bytes", "aou_message_bytes", "unused_message_bytes",
-                       "credit_only_flits")
+                       "credit_only_flits", "accounting_saturated")
 
 
 class OrcLinkCounters(ctypes.Structure):
@@ -532,6 +532,8 @@ def _link_lib() -> ctypes.CDLL:
             "orc_link_flit_count": (ctypes.c_size_t, [_P]),
             "orc_link_flit_at": (ctypes.POINTER(OrcLinkFlit), [_P, ctypes.c_size_t]),
             "orc_link_scenario": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t, _P, _P, _P]),
+            "orc_link_scenario_traced": (ctypes.c_int, [_P, _P, _P, ctypes.c_size_t, _P, _P, _P,
+                                                        _P, ctypes.c_size_t, _P, _P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -599,20 +601,22 @@ class Link:
         return self._L.orc_link_counters_of(self.h, direction).contents.as_dict()
 
     def flits(self) -> list:
-        out = []
-        for i in range(self._L.orc_link_flit_count(self.h)):
-            f = self._L.orc_link_flit_at(self.h, i).contents
-            out.append({"direction": f.direction, "start_ns": f.start_ns,
-                        "delivered_ns": f.delivered_ns, "message_granules": f.message_granules,
-                        "grant_granules": f.grant_granules, "credit_only": bool(f.credit_only),
-                        "fragments": [dict(request_id=f.frag[k].request_id,
-                                           flit_granule=f.frag[k].flit_granule,
-                                           message_granule=f.frag[k].message_granule,
-                                           granules=f.frag[k].granules,
-                                           msg_start=bool(f.frag[k].msg_start),
-                                           msg_end=bool(f.frag[k].msg_end))
-                                      for k in range(f.nfrag)]})
-        return out
+        return [flit_dict(self._L.orc_link_flit_at(self.h, i).contents)
+                for i in range(self._L.orc_link_flit_count(self.h))]
+
+
+def flit_dict(f) -> dict:
+    """An orc_link_flit as a dict (FlitRecord's fields, link.hpp:22-38)."""
+    return {"direction": f.direction, "start_ns": f.start_ns,
+            "delivered_ns": f.delivered_ns, "message_granules": f.message_granules,
+            "grant_granules": f.grant_granules, "credit_only": bool(f.credit_only),
+            "fragments": [dict(request_id=f.frag[k].request_id,
+                               flit_granule=f.frag[k].flit_granule,
+                               message_granule=f.frag[k].message_granule,
+                               granules=f.frag[k].granules,
+                               msg_start=bool(f.frag[k].msg_start),
+                               msg_end=bool(f.frag[k].msg_end))
+                          for k in range(f.nfrag)]}
 
 
 def link_scenario(profile: OrcLinkProfile, direction, ready, delay=(0, 0)):
@@ -630,3 +634,24 @@ def link_scenario(profile: OrcLinkProfile, direction, ready, delay=(0, 0)):
     if rc:
         raise LinkError(rc, "scenario")
     return delivered[:n], [counters[0].as_dict(), counters[1].as_dict()]
+
+
+def link_scenario_traced(profile: OrcLinkProfile, direction, ready, delay=(0, 0), cap=4096):
+    """link_scenario that also returns the link's flit records (the first
+    4096, in emission order) and how many were not recorded."""
+    direction = np.ascontiguousarray(direction, np.uint32)
+    ready = np.ascontiguousarray(ready, np.uint64)
+    n = len(ready)
+    delivered = np.zeros(max(n, 1), np.uint64)
+    counters = (OrcLinkCounters * 2)()
+    flits = (OrcLinkFlit * cap)()
+    nflits = ctypes.c_size_t(0)
+    dropped = _U64(0)
+    d = (_U64 * 2)(*delay)
+    rc = _link_lib().orc_link_scenario_traced(ctypes.byref(profile), addr(direction), addr(ready),
+                                              n, d, addr(delivered), counters, flits, cap,
+                                              ctypes.byref(nflits), ctypes.byref(dropped))
+    if rc:
+        raise LinkError(rc, "scenario")
+    return (delivered[:n], [counters[0].as_dict(), counters[1].as_dict()],
+            [flit_dict(flits[i]) for i in range(nflits.value)], int(dropped.value))
