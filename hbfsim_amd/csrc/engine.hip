@@ -1693,16 +1693,22 @@ __device__ __forceinline__ void batch_order(const LinBatchT<kR>& q, int lane, st
 // senses unless its page is the one the plane last read, the others hit; a
 // run that holds the tile's first record on its plane records that record
 // and folds the m - 1 hits after it, map (0, issue) (the identity for m = 1).
-// The channel map of a run is (m x, issue + m x).
-template <bool kR>
+// The channel map of a run is (m x, issue + m x).  kGiven: page-register
+// hits come per record from `hits` (two page registers, whole steps only):
+// a step's first record hits as hits[] says, and a step that is the tile's
+// first record on its plane records that hit in its class (bit 3), as the
+// per-record path does.
+template <bool kR, bool kGiven = false>
 __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t* xp,
                                              const LinBatchT<kR>& q, int lane, std::uint64_t* p_fi,
                                              std::uint64_t* p_rA, std::uint64_t* p_rB,
                                              std::uint64_t* c_A, std::uint64_t* c_B,
                                              std::uint32_t* p_f1, std::uint32_t* p_l1,
                                              std::uint8_t* p_fc, std::uint64_t* mt_p,
-                                             std::uint64_t* mt_c)
+                                             std::uint64_t* mt_c,
+                                             const std::uint8_t* hits = nullptr)
 {
+    static_assert(!(kR && kGiven), "given hits take whole steps only");
     const StepView v = step_view(a, xp, q, lane);
     const bool m = v.m;
     const std::uint32_t pkey = m ? v.d.plane : 0u;
@@ -1719,7 +1725,11 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
     if (gp.pred < 0) {
         prev1 = last_page;
     }
-    const std::uint64_t ls = prev1 == q.page1 ? 0ull : a.read_ps;
+    bool hit0 = prev1 == q.page1;
+    if constexpr (kGiven) {
+        hit0 = m && hits[q.first + static_cast<std::size_t>(lane) * kWave] != 0;
+    }
+    const std::uint64_t ls = hit0 ? 0ull : a.read_ps;
     const std::uint64_t cx = q.len() * v.x;
     std::uint64_t Ap = 0, Bp = 0, Ac = 0, Bc = 0;
     if (m) {
@@ -1735,11 +1745,15 @@ __device__ __forceinline__ void fold_summary(const KArgs& a, const std::uint64_t
     const std::uint32_t l1 =
         static_cast<std::uint32_t>(__shfl(static_cast<int>(q.page1), gp.leader));
     const std::uint64_t li = shfl64(q.issue, gp.leader);
+    std::uint32_t lc = 0;  // the leader's class: a read (bit 3: its given hit)
+    if constexpr (kGiven) {
+        lc = static_cast<std::uint32_t>(__shfl(hit0 ? 8 : 0, gp.leader));
+    }
     if (m && lane == gp.last) {
         if (!has) {
             p_f1[pk] = l1;
             p_fi[pk] = li;
-            p_fc[pk] = 0;  // a read
+            p_fc[pk] = static_cast<std::uint8_t>(lc);
         }
         const std::uint64_t sA = p_rA[pk];
         const std::uint64_t sB = p_rB[pk];
@@ -1939,7 +1953,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             pipe.issue(rec, g + kSpan, end, lane);
         }
         const std::size_t gend = g + kSpan < end ? g + kSpan : end;
-        if (!kHits && a.slots == 1 && a.lead == nullptr && g + kSpan <= end &&
+        if ((kHits || a.slots == 1) && a.lead == nullptr && g + kSpan <= end &&
             q.n <= kWave - kDepth && lin_miss < kLinGiveUp) {
             // a whole group of linear steps joins the batch at once
             GroupLin<kDepth> gl;
@@ -1947,8 +1961,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
                 q.push_group(gl, g, rcu.id);
                 if (q.n >= kFull || gend >= end) {
                     batch_order(q, lane, last_issue, disorder);
-                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
-                                 mt_p, mt_c);
+                    fold_summary<kPacked, kHits>(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B,
+                                                 p_f1, p_l1, p_fc, mt_p, mt_c, hits);
                     modeled += static_cast<std::uint64_t>(q.rows) * kWave;
                     dq = q;  // (its descriptors wait for the next group's loads)
                     q.clear();
@@ -1961,7 +1975,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             pipe.take(st);
             const std::size_t i = s + lane;
             const bool valid = i < end;
-            if (!kHits && a.slots == 1 && a.lead == nullptr) {
+            if ((kHits || a.slots == 1) && a.lead == nullptr) {
                 // linear steps wait in a batch; the batch is folded when full, at
                 // the tile's last step, and before any other step (order matters)
                 LinStep ls;
@@ -1982,8 +1996,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
                 }
                 if (q.n != 0 && (!lin || q.n >= kFull || s + kWave >= end)) {
                     batch_order(q, lane, last_issue, disorder);
-                    fold_summary(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B, p_f1, p_l1, p_fc,
-                                 mt_p, mt_c);
+                    fold_summary<kPacked, kHits>(a, xp, q, lane, p_fi, p_rA, p_rB, c_A, c_B,
+                                                 p_f1, p_l1, p_fc, mt_p, mt_c, hits);
                     modeled += static_cast<std::uint64_t>(q.rows) * kWave;
                     write_descs(desc, a.desc_split, a.desc_rid, dq, lane);  // at most one waits
                     dq = q;
@@ -2591,13 +2605,15 @@ struct ApplySums {
     std::uint64_t n_rec, n_mod, n_rd, n_hit, mk, lat_lo, lat_hi, lat_max, svc_sum, seq, n_hyb;
 };
 
-template <bool kR>
+// kGiven: page-register hits per record from `given` (two page registers):
+// a step's first record hits as given[] says.
+template <bool kR, bool kGiven = false>
 __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* xp,
                                            const LinBatchT<kR>& q, int lane, std::uint64_t* p_busy,
                                            std::uint64_t* c_busy, std::uint32_t* p_tag,
                                            std::uint64_t* completion, std::uint8_t* status,
                                            ApplySums& t, std::uint64_t* mt_p,
-                                           std::uint64_t* mt_c)
+                                           std::uint64_t* mt_c, const std::uint8_t* given = nullptr)
 {
     const StepView v = step_view(a, xp, q, lane);
     const bool m = v.m;
@@ -2613,7 +2629,10 @@ __device__ __forceinline__ void fold_apply(const KArgs& a, const std::uint64_t* 
     if (gp.pred < 0) {
         prev1 = tag;
     }
-    const bool lhit = m && prev1 == q.page1;
+    bool lhit = m && prev1 == q.page1;
+    if constexpr (kGiven) {
+        lhit = m && given[q.first + static_cast<std::size_t>(lane) * kWave] != 0;
+    }
     const std::uint64_t ls = lhit ? 0ull : a.read_ps;
     const std::uint64_t cx = 64 * v.x;
     std::uint64_t Ap = 0, Bp = 0, Ac = 0, Bc = 0;
@@ -3109,13 +3128,14 @@ __device__ __forceinline__ void expand_rows(LinBatchT<true>& q, const StepDesc& 
 }
 
 // Folds the apply pass's pending batch (fold_apply_runs when it holds a
-// split step) and empties it.
-template <bool kR>
+// split step; kGiven: page-register hits from `hits`) and empties it.
+template <bool kR, bool kGiven>
 __device__ __forceinline__ void fold_batch(const KArgs& a, const std::uint64_t* xp,
                                            LinBatchT<kR>& q, int lane, std::uint64_t* p_busy,
                                            std::uint64_t* c_busy, std::uint32_t* p_tag,
                                            std::uint64_t* completion, std::uint8_t* status,
-                                           ApplySums& t, std::uint64_t* mt_p, std::uint64_t* mt_c)
+                                           ApplySums& t, std::uint64_t* mt_p, std::uint64_t* mt_c,
+                                           const std::uint8_t* hits)
 {
     if constexpr (kR) {
         if (q.any_split()) {
@@ -3125,7 +3145,8 @@ __device__ __forceinline__ void fold_batch(const KArgs& a, const std::uint64_t* 
             return;
         }
     }
-    fold_apply(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t, mt_p, mt_c);
+    fold_apply<kR, kGiven>(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t, mt_p,
+                           mt_c, hits);
     q.clear();
 }
 
@@ -3240,8 +3261,8 @@ __device__ __forceinline__ void apply_tile(
                     q.first = w0;
                     q.n = nst;
                     q.rows = nst;
-                    fold_batch(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t,
-                               mt_p, mt_c);
+                    fold_batch<kSplit, kHits>(a, xp, q, lane, p_busy, c_busy, p_tag, completion,
+                               status, t, mt_p, mt_c, hits);
                 } else {
                     const int runs = nst + __popcll(smask);
                     const int half = runs <= kWave ? nst : nst / 2;
@@ -3260,8 +3281,8 @@ __device__ __forceinline__ void apply_tile(
                             q.n = nst;
                             q.rows = nst;
                         }
-                        fold_batch(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t,
-                                   mt_p, mt_c);
+                        fold_batch<kSplit, kHits>(a, xp, q, lane, p_busy, c_busy, p_tag, completion,
+                                   status, t, mt_p, mt_c, hits);
                         r0 = r1;
                     }
                 }
@@ -3279,7 +3300,7 @@ __device__ __forceinline__ void apply_tile(
                 pipe.take(sr);
                 const std::size_t i = s + lane;
                 const bool valid = i < end;
-                if (!kHits && a.slots == 1 && a.lead == nullptr) {
+                if ((kHits || a.slots == 1) && a.lead == nullptr) {
                     // batched as in the summary pass
                     LinStep ls;
                     bool lin = false;
@@ -3297,8 +3318,8 @@ __device__ __forceinline__ void apply_tile(
                         }
                     }
                     if (q.n != 0 && (!lin || q.n >= kFull || s + kWave >= wend)) {
-                        fold_batch(a, xp, q, lane, p_busy, c_busy, p_tag, completion, status, t,
-                               mt_p, mt_c);
+                        fold_batch<kSplit, kHits>(a, xp, q, lane, p_busy, c_busy, p_tag, completion,
+                               status, t, mt_p, mt_c, hits);
                     }
                     if (lin) {
                         continue;
@@ -5678,7 +5699,7 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     if (ext_scratch != nullptr) {
         desc = sc.desc;  // packed runs: one page register, no sampling; split
                          // steps go without descriptors (no side array)
-    } else if (!k2 && a.slots == 1 && !grouping) {
+    } else if ((k2 || a.slots == 1) && !grouping) {
         const std::size_t nsteps = (n + kWave - 1) / kWave;
         if (nsteps > e->desc_cap) {
             hfree(e->d_desc);
