@@ -96,6 +96,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-extra", action="store_true",
                     help="config c2: skip the read/write ceilings and the general-path, "
                          "hybrid, UCIe-link, config-4, EQ3-stencil and config 0/1/3 sub-lines")
+    ap.add_argument("--c4-records", type=int, default=None,
+                    help="config c4: time only this prefix of the trace (fewer windows; "
+                         "below 512 windows the chain launches window by window, which "
+                         "counter runs need)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first fill and copy 2 GiB (known HBM bytes) so that counter runs "
                          "can calibrate FETCH_SIZE / WRITE_SIZE")
@@ -242,8 +246,9 @@ def bench_c4(args) -> dict:
 
     shape = w.OLMOE
     seg = w.c4_segments(shape, 2)
+    limit = getattr(args, "c4_records", None) or w.C4_ACCESSES
     rec = w.gpu_segment_records(seg, shape.lines_per_expert, shape.line, shape.gap_ps,
-                                shape.issuers)[: w.C4_ACCESSES]
+                                shape.issuers)[: min(limit, w.C4_ACCESSES)]
     ranges = w.moe_ranges(shape)
     e = engine.Engine(str(w.PROFILES / "c4.json"))
     for base, length, perms in ranges:
