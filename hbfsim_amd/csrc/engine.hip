@@ -5089,9 +5089,9 @@ int run_empirical(engine* e, const hbf_record32* d_rec, std::size_t n, std::uint
                        static_cast<const std::uint64_t*>(d_tail),
                        static_cast<const std::uint64_t*>(d_svc), c.emp_program_ns * 1000ull,
                        d_comp, d_status, d_trep);
+    (void)hipEventRecord(e->ev[3], stream);
     launch_report(stream, static_cast<const DevReport*>(d_trep), ntiles, e->d_rep,
                   e->d_rep_parts, nullptr);
-    (void)hipEventRecord(e->ev[3], stream);
     BState fin{};
     std::uint64_t fin2[2] = {0, 0};
     err = hipGetLastError();
@@ -5804,6 +5804,9 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                            base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq, d_comp,
                            d_status, sc.tile_rep, hits, desc);
     }
+    // (the apply pass's interval ends with it: the report reduction's two
+    // small launches are no part of it)
+    (void)hipEventRecord(e->ev[3], stream);
     launch_report(stream, sc.tile_rep, ntiles, e->d_rep, e->d_rep_parts, e->d_disorder);
     unsigned long long h_frep[8] = {};
     if (grouping) {
@@ -5813,7 +5816,6 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                            dim3(256), 0, stream, static_cast<const hbf_record32*>(d_rec), n,
                            base_ps, d_lead, d_comp, d_status, d_frep);
     }
-    (void)hipEventRecord(e->ev[3], stream);
     err = hipGetLastError();
     if (err == hipSuccess)
         err = hipMemcpyAsync(e->h_rep, e->d_rep, sizeof(DevReport) + 8, hipMemcpyDeviceToHost,

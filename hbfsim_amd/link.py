@@ -82,6 +82,25 @@ def flit_dict(r) -> dict:
                           for f in r["fragment"][:int(r["fragments"])]]}
 
 
+def run_into(profile: nat.LinkProfile, first: Any, ready_ns: Any, direction: Any,
+             delivered: Any, counters: Any, stream: Any = None) -> None:
+    """hbfsim_amd_link_run into caller-owned device tensors (delivered int64
+    [n], counters int64 [links, 2, 9]); nothing is copied to the host."""
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    elif hasattr(stream, "cuda_stream"):
+        stream = stream.cuda_stream
+    rc = nat.load().hbfsim_amd_link_run(ctypes.byref(profile), first.data_ptr(),
+                                        int(first.shape[0]) - 1, ready_ns.data_ptr(),
+                                        direction.data_ptr(), int(ready_ns.shape[0]),
+                                        delivered.data_ptr(), counters.data_ptr(),
+                                        ctypes.c_void_p(stream))
+    if rc in (nat.HBFSIM_INVALID_ARGUMENT, nat.HBFSIM_UNSUPPORTED):
+        raise ValueError(f"link run refused: {nat.status_name(rc)} ({rc})")
+    nat.check(rc, "link run")
+
+
 def _run(profile, first, ready_ns, direction, stream, limit):
     import torch
     links = int(first.shape[0]) - 1
