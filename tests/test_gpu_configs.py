@@ -61,7 +61,24 @@ def run_pair(pair, d_rec, n, base_ps, threads=8):
     return gpu, (ocomp, ost, orep)
 
 
+def packed_equals(packed, d_rec, n, base_ps, gpu, what):
+    """The same step through packed records on a second engine with the same
+    history (where steps crossing a page fold as split steps): completions,
+    status bytes and report equal to the 32-byte run's."""
+    import torch
+    d_pk = pack_records(d_rec)
+    comp = torch.zeros(n, dtype=torch.int64, device="cuda")
+    st = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    rep = packed.engine.run_packed(d_pk, comp, st, base_ps=base_ps)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(comp.cpu().numpy().view(np.uint64), gpu[0], err_msg=what)
+    np.testing.assert_array_equal(st.cpu().numpy(), gpu[1], err_msg=what)
+    assert rep == gpu[2], what
+
+
 def test_tinyllama_two_decode_steps_bit_exact():
+    """Both record forms: the packed one folds the steps that cross a page
+    as split steps."""
     shape = w.TINYLLAMA
     spans = w.dense_spans(shape)
     d_rec = gpu_records(spans, shape)
@@ -70,22 +87,28 @@ def test_tinyllama_two_decode_steps_bit_exact():
     np.testing.assert_array_equal(d_rec[:1 << 20].cpu().numpy().view(np.uint64),
                                   host_records(spans, shape, 0, 1 << 20))
     pair = parity.Pair(C0, w.dense_ranges(shape))
+    packed = parity.Pair(C0, w.dense_ranges(shape))
     try:
         base = 0
         for step in range(2):
             gpu, cpu = run_pair(pair, d_rec, n, base)
             parity.assert_same(gpu, cpu, f"TinyLlama step {step}")
             assert gpu[2]["modeled"] == n and gpu[2]["page_hits"] > 0
+            packed_equals(packed, d_rec, n, base, gpu, f"TinyLlama step {step} packed")
             base = gpu[2]["makespan_ps"]
         pair.check_state()
+        for k in ("plane_busy", "plane_tags", "channel_cursor"):
+            np.testing.assert_array_equal(packed.engine.state()[k], pair.engine.state()[k], k)
     finally:
         pair.close()
+        packed.close()
 
 
 def test_kv_reduced_all_steps_bit_exact():
     shape = w.PagedKvShape(layers=3, seqs=9, min_len=40, max_len=700, steps=5)
     tables = shape.tables()
     pair = parity.Pair(C3, w.kv_ranges(shape))
+    packed = parity.Pair(C3, w.kv_ranges(shape))
     try:
         base, programs = 0, 0
         for step in range(shape.steps):
@@ -95,12 +118,15 @@ def test_kv_reduced_all_steps_bit_exact():
             gpu, cpu = run_pair(pair, d_rec, n, base, threads=1)
             parity.assert_same(gpu, cpu, f"paged KV step {step}")
             assert gpu[2]["writes"] == 2 * shape.layers * shape.seqs * 16
+            # token blocks joined inside a step fold as split steps when packed
+            packed_equals(packed, d_rec, n, base, gpu, f"paged KV step {step} packed")
             programs += gpu[2]["programs"]
             base = gpu[2]["makespan_ps"]
         assert programs > 0  # appends that fill a page program it
         pair.check_state()
     finally:
         pair.close()
+        packed.close()
 
 
 def test_kv_full_size_step():
