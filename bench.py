@@ -188,12 +188,13 @@ def build_workload(name: str, steps: int, batches: int = 6):
     raise SystemExit(f"unknown config {name}")
 
 
-def cpu_baseline(profile, ranges, host_records: np.ndarray, budget_s: float) -> dict:
+def cpu_baseline(profile, ranges, host_records: np.ndarray, budget_s: float,
+                 **options) -> dict:
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle_py
 
     prof = oracle_py.load_profile(profile)
-    params = oracle_py.engine_params(prof)
+    params = oracle_py.engine_params(prof, **options)
     orng, count = oracle_py.range_table(ranges, prof["page_bytes"], prof["capacity_bytes"])
 
     def timed(threads: int, seconds: float) -> tuple[float, int, float]:
@@ -552,14 +553,34 @@ def bench_general(engine, args) -> dict:
     own), packed, on the config-0 profile."""
     from hbfsim_amd import workloads
     n = 1 << 28
-    batches = [engine.pack_records(gpu_random_stream(n, 11 + k)) for k in range(2)]
+    batches, sample = [], None
+    for k in range(2):
+        b = gpu_random_stream(n, 11 + k)
+        if k == 0:
+            sample = b[: 1 << 22].cpu().numpy().view(np.uint64)
+        batches.append(engine.pack_records(b))
+        del b
     profile = workloads.PROFILES / "c0.json"
     ranges = [(workloads.RANGE_BASE, 1 << 30, 3)]
-    return sub_line(engine, profile, ranges, batches, "packed", args,
+    line = sub_line(engine, profile, ranges, batches, "packed", args,
                     "config0-shaped random stream: 2^28 uniform 128-B reads in 1 GiB, exponential "
                     "gaps mean 2 ns, 8 ch x 4 die x 2 plane, 2 distinct batches",
                     apply_rereads=True, kernels_summary="engine_kernels_general.txt",
                     traffic_summary="engine_traffic_general.txt")
+    del batches
+    if not getattr(args, "no_cpu", True):
+        line["cpu_baseline"] = sub_cpu_baseline(line, profile, ranges, sample, args)
+    return line
+
+
+def sub_cpu_baseline(line: dict, profile, ranges, sample: np.ndarray, args, **options) -> dict:
+    """The CPU oracle on a bounded sample of a sub-line's stream (a few
+    seconds), with the line's speedup over it."""
+    cb = cpu_baseline(profile, ranges, sample, min(3.0, args.cpu_seconds / 2), **options)
+    cb["speedup"] = {"vs_1_core": line["value"] / cb["value"],
+                     "vs_all_cores": line["value"] / cb["parallel"]["value"]
+                     if cb.get("parallel") else None}
+    return cb
 
 
 def bench_hybrid(engine, batches, args, packed=None) -> dict:
@@ -577,9 +598,14 @@ def bench_hybrid(engine, batches, args, packed=None) -> dict:
     shape = workloads.QWEN3_30B_A3B
     if packed is None:
         packed = [engine.pack_records(b) for b in batches]
-    return sub_line(engine, path, workloads.moe_ranges(shape), packed, "packed", args,
+    line = sub_line(engine, path, workloads.moe_ranges(shape), packed, "packed", args,
                     "config2 with hybrid sampling (rate 0.01, warm-up 1,000), packed records",
                     mode="hybrid", kernels_summary="engine_kernels_config2_hybrid.txt")
+    if not getattr(args, "no_cpu", True):
+        sample = batches[0][: 1 << 22].cpu().numpy().view(np.uint64)
+        line["cpu_baseline"] = sub_cpu_baseline(line, path, workloads.moe_ranges(shape), sample,
+                                                args, hybrid=True)
+    return line
 
 
 def link_workload(links: int, per_link: int, seed: int = 5):
@@ -748,6 +774,8 @@ def main() -> None:
                "vs_baseline": None, "dtype": "u64", "data": "synthetic",
                "config": {"workload": line["workload"], "records": line["records"]},
                "roofline": line["roofline"]}
+        if "cpu_baseline" in line:
+            out["cpu_baseline"] = line["cpu_baseline"]
         print(json.dumps(out), flush=True)
         return
     if args.config in ("c0", "c1", "c3"):
