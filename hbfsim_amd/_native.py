@@ -218,6 +218,7 @@ SIGNATURES = {
     "hbfsim_amd_set_state": (_INT, [_P, _P, _P, _P, _U64, _U64]),
     "hbfsim_amd_reset": (_INT, [_P]),
     "hbfsim_amd_last_kernel_ms": (_INT, [_P, ctypes.POINTER(ctypes.c_float), _INT]),
+    "hbfsim_amd_last_apply_waves": (_INT, [_P]),
     "hbfsim_amd_lookup_range": (_INT, [_P, _U64, _U32, ctypes.POINTER(_U32),
                                         ctypes.POINTER(Range), ctypes.POINTER(_U32)]),
     "hbfsim_amd_gen_segment_lines": (_INT, [_P, _SZ, _P, _SZ, _U64, _U32, _U64, _U32, _U64,

@@ -927,6 +927,14 @@ HBF_API int hbfsim_amd_last_kernel_ms(const hbfsim_context* c, float* ms, int ma
     return hbfamd::engine_last_kernel_ms(c->eng, ms, max_kernels);
 }
 
+HBF_API int hbfsim_amd_last_apply_waves(const hbfsim_context* c)
+{
+    if (c == nullptr || c->eng == nullptr) {
+        return 0;
+    }
+    return hbfamd::engine_last_apply_waves(c->eng);
+}
+
 HBF_API int hbfsim_amd_lookup_range(hbfsim_context* c, uint64_t address, uint32_t bytes,
                                     uint32_t* kind, hbfsim_amd_range* out, uint32_t* count)
 {

@@ -512,9 +512,16 @@ __device__ __forceinline__ void load_record(const hbf_record32* rec, std::size_t
 // index would put the group in scratch memory).
 constexpr int kPipe = 4;
 constexpr std::size_t kGroupSpan = static_cast<std::size_t>(kPipe) * kWave;
-// The summary pass, whose occupancy its per-plane LDS state limits (not its
-// registers), keeps twice as many steps in flight per wave.
+// The summary pass of 32-byte records, whose occupancy its per-plane LDS
+// state limits (not its registers), keeps twice as many steps in flight per
+// wave.
 constexpr int kSumPipe = 8;
+// Packed records in the summary pass: four waves per SIMD with three steps in
+// flight each.  Measured against three waves with eight steps: general
+// streams +8% per step (k_summary 4.15 -> 3.57 ms at 2^28 records) and the
+// paged-KV step +15%, the TinyLlama step 2% slower; the LDS-bound variant
+// (kDeep) keeps 2 * kSumPipe at two waves.
+constexpr int kPackedSumPipe = 3;
 // Linear-step detection on streams that show none: after kLinGiveUp steps in
 // a row fail it, a wave probes only every kLinProbe-th step until one
 // passes (every step is exact on the general path too; random streams stop
@@ -1853,7 +1860,7 @@ __host__ __device__ __forceinline__ std::size_t summary_match_offset(const KArgs
 // channel the map of all its records.  Pages are stored as page + 1 in 32
 // bits (capacity / page_bytes < 2^32 is checked on the host).
 template <bool kRefresh, bool kHits, bool kPacked = false, bool kDeep = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (kDeep ? 2 : 3) : 1))) void k_summary(KArgs a, const void* rec, std::size_t n,
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (kDeep ? 2 : 4) : 1))) void k_summary(KArgs a, const void* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
                                                 MaskWord* tmask, ChanSum* csum,
                                                 std::uint64_t* tile_count,
@@ -1897,12 +1904,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
     bool disorder = false;
     bool any_split = false;  // some step of the tile was split (wave-uniform)
     // (the page-register variant takes no linear groups and keeps 4 deep;
-    // packed records keep kSumPipe steps too, which leaves registers for a
-    // third wave per SIMD: as fast on streamed steps, a quarter faster on
-    // general ones than twice as deep at two waves)
+    // packed records keep kPackedSumPipe steps at four waves per SIMD)
     // (kDeep: packed records where LDS already holds the pass at two waves
-    // per SIMD, whose registers then allow twice the steps in flight)
-    constexpr int kDepth = kHits ? kPipe : (kDeep ? 2 * kSumPipe : kSumPipe);
+    // per SIMD, whose registers then allow 2 * kSumPipe steps in flight)
+    constexpr int kDepth =
+        kHits ? kPipe : (kDeep ? 2 * kSumPipe : (kPacked ? kPackedSumPipe : kSumPipe));
     constexpr std::size_t kSpan = static_cast<std::size_t>(kDepth) * kWave;
     using Pipe = std::conditional_t<kPacked, PackedPipeT<kDepth>, RecordPipeT<kDepth>>;
     Pipe pipe;
@@ -3155,7 +3161,7 @@ __device__ __forceinline__ void fold_batch(const KArgs& a, const std::uint64_t* 
 // runs; without it the body is the whole-step one, whose folds and stores
 // then keep every register the pass has (the split-capable body needs more:
 // compiled into the same code path it would make the whole-step folds spill).
-template <bool kRefresh, bool kHits, bool kStaged, bool kPacked, bool kSplit>
+template <bool kRefresh, bool kHits, bool kStaged, bool kPacked, bool kSplit, bool kWide = false>
 __device__ __forceinline__ void apply_tile(
     const KArgs& a, const void* rec, std::size_t n, std::uint64_t base_ps,
     const PlaneCarry* pcarry, const MaskWord* tmask, const std::uint64_t* ccarry,
@@ -3289,12 +3295,16 @@ __device__ __forceinline__ void apply_tile(
                 continue;
             }
         }
-        using Pipe = std::conditional_t<kPacked, PackedPipeT<kPipe>, RecordPipe>;
+        // (the four-wave form keeps two steps in flight)
+        constexpr int kDepth = kPacked && kWide ? 2 : kPipe;
+        constexpr std::size_t kSpan = static_cast<std::size_t>(kDepth) * kWave;
+        using Pipe = std::conditional_t<kPacked, PackedPipeT<kDepth>, RecordPipe>;
+        static_assert(kPacked || kDepth == kPipe, "32-byte records keep kPipe steps");
         Pipe pipe;
         pipe.issue(rec, w0, wend, lane);
-        for (std::size_t g = w0; g < wend; g += kGroupSpan) {
-            pipe.advance(rec, g + kGroupSpan, wend, lane);
-            const std::size_t gend = g + kGroupSpan < wend ? g + kGroupSpan : wend;
+        for (std::size_t g = w0; g < wend; g += kSpan) {
+            pipe.advance(rec, g + kSpan, wend, lane);
+            const std::size_t gend = g + kSpan < wend ? g + kSpan : wend;
             for (std::size_t s = g; s < gend; s += kWave) {
                 typename Pipe::Step sr;
                 pipe.take(sr);
@@ -3516,8 +3526,12 @@ __device__ __forceinline__ void apply_tile(
 // general steps' chains of ballots, shuffles and LDS updates need the
 // latency hiding and the streamed linear steps lose nothing.  32-byte
 // records hold twice the bytes per step in registers and would spill.
-template <bool kRefresh, bool kHits, bool kStaged = false, bool kPacked = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 : 1))) void k_apply(
+// kWide: four waves per SIMD with two steps in flight, for large streams of
+// general steps (k_apply 4.15 -> 3.59 ms at 2^28 random records); on streams
+// of linear steps its spilled registers cost 7-15% of the pass.
+template <bool kRefresh, bool kHits, bool kStaged = false, bool kPacked = false,
+          bool kWide = false>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kWide ? 4 : (kPacked ? 3 : 1)))) void k_apply(
     KArgs a, const void* rec, std::size_t n, std::uint64_t base_ps, const PlaneCarry* pcarry,
     const MaskWord* tmask, const std::uint64_t* ccarry, const std::uint64_t* tile_seq,
     std::uint64_t* completion, std::uint8_t* status, DevReport* tile_rep,
@@ -3527,16 +3541,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? 3 
     __shared__ std::uint64_t xp[33];
     if constexpr (kPacked) {
         if (a.tile_split != nullptr && a.tile_split[blockIdx.x] != 0) {
-            apply_tile<kRefresh, kHits, kStaged, kPacked, true>(a, rec, n, base_ps, pcarry, tmask,
-                                                                ccarry, tile_seq, completion,
-                                                                status, tile_rep, hits, desc, sm,
-                                                                xp);
+            apply_tile<kRefresh, kHits, kStaged, kPacked, true, kWide>(
+                a, rec, n, base_ps, pcarry, tmask, ccarry, tile_seq, completion, status, tile_rep,
+                hits, desc, sm, xp);
             return;
         }
     }
-    apply_tile<kRefresh, kHits, kStaged, kPacked, false>(a, rec, n, base_ps, pcarry, tmask,
-                                                         ccarry, tile_seq, completion, status,
-                                                         tile_rep, hits, desc, sm, xp);
+    apply_tile<kRefresh, kHits, kStaged, kPacked, false, kWide>(a, rec, n, base_ps, pcarry, tmask,
+                                                                ccarry, tile_seq, completion,
+                                                                status, tile_rep, hits, desc, sm,
+                                                                xp);
 }
 
 // Folds the per-tile report partials into one report (sums, maxima and the
@@ -3889,6 +3903,12 @@ struct engine {
     hipEvent_t ev[4]{};
     float last_ms[3]{0, 0, 0};
     std::uint64_t burst{0};
+    // the last completed run's modeled records and page-register hits: a
+    // large stream with few hits is mostly general steps, and its next run
+    // takes the four-wave apply pass (results are the same either way)
+    std::uint64_t last_modeled{0};
+    std::uint64_t last_hits{0};
+    int last_apply_waves{0};  // waves per SIMD the last run's apply pass was built for
 };
 
 // Where one run of the main pipeline keeps its per-tile and per-group
@@ -4862,9 +4882,12 @@ std::size_t lds_apply(const KArgs& a)
 }
 
 // The lane-matching tables go where they cost neither per-record pass any
-// waves per CU (gfx950: 160 KB of LDS per CU; both passes run at most three
-// waves per SIMD).
+// waves per CU (gfx950: 160 KB of LDS per CU, four SIMDs; both passes run at
+// most four waves per SIMD).
 constexpr std::size_t kLdsPerCuBytes = 160 * 1024;  // gfx950
+constexpr std::size_t kSimdsPerCu = 4;
+// the four-wave apply pass is considered from this many records
+constexpr std::size_t kWideApplyRecords = std::size_t{1} << 24;
 // A workgroup may hold all of it; beyond 64 KB of dynamic LDS a kernel has
 // to be allowed the size first (allow_lds).
 constexpr std::size_t kLdsPerBlockBytes = 160 * 1024;
@@ -4885,7 +4908,7 @@ hipError_t allow_lds(F* kernel, std::size_t bytes)
 void choose_match(KArgs& a)
 {
     constexpr std::size_t kLdsPerCu = kLdsPerCuBytes;
-    constexpr std::size_t kMaxWaves = 12;
+    constexpr std::size_t kMaxWaves = 4 * kSimdsPerCu;
     const auto waves = [&](std::size_t bytes) {
         const std::size_t w = bytes == 0 ? kMaxWaves : kLdsPerCu / bytes;
         return w < kMaxWaves ? w : kMaxWaves;
@@ -5768,6 +5791,13 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
     }
     (void)hipEventRecord(e->ev[2], stream);
     const bool staged = desc != nullptr && staged_steps(a) != 0;
+    // the four-wave apply pass: a large stream whose last run on this engine
+    // had few page-register hits (mostly general steps), where LDS leaves
+    // room for four waves per SIMD
+    const bool wide_apply = packed && n >= kWideApplyRecords &&
+                            kLdsPerCuBytes / lds_c >= 4 * kSimdsPerCu && e->last_modeled != 0 &&
+                            e->last_hits * 8 < e->last_modeled;
+    e->last_apply_waves = packed && !k2 && !refresh_records ? (wide_apply ? 4 : 3) : 1;
     if (k2) {
         (void)allow_lds(k_apply<false, true>, lds_c);
         hipLaunchKernelGGL((k_apply<false, true>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
@@ -5783,10 +5813,20 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         hipLaunchKernelGGL((k_apply<true, false>), grid, dim3(kWave), lds_c, stream, a, d_rec, n,
                            base_ps, sc.pcarry, sc.tmask, sc.ccarry, sc.tseq, d_comp,
                            d_status, sc.tile_rep, hits, desc);
+    } else if (packed && staged && wide_apply) {
+        (void)allow_lds(k_apply<false, false, true, true, true>, lds_c);
+        hipLaunchKernelGGL((k_apply<false, false, true, true, true>), grid, dim3(kWave), lds_c,
+                           stream, a, d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry,
+                           sc.tseq, d_comp, d_status, sc.tile_rep, hits, desc);
     } else if (packed && staged) {
         (void)allow_lds(k_apply<false, false, true, true>, lds_c);
         hipLaunchKernelGGL((k_apply<false, false, true, true>), grid, dim3(kWave), lds_c, stream,
                            a, d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry,
+                           sc.tseq, d_comp, d_status, sc.tile_rep, hits, desc);
+    } else if (packed && wide_apply) {
+        (void)allow_lds(k_apply<false, false, false, true, true>, lds_c);
+        hipLaunchKernelGGL((k_apply<false, false, false, true, true>), grid, dim3(kWave), lds_c,
+                           stream, a, d_rec, n, base_ps, sc.pcarry, sc.tmask, sc.ccarry,
                            sc.tseq, d_comp, d_status, sc.tile_rep, hits, desc);
     } else if (packed) {
         (void)allow_lds(k_apply<false, false, false, true>, lds_c);
@@ -5850,6 +5890,8 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
                                       out, refresh_records, nullptr, true);
             });
     }
+    e->last_modeled = e->h_rep[0].v[R_MODELED];
+    e->last_hits = e->h_rep[0].v[R_HITS];
     for (int k = 0; k < 3; ++k) {
         float ms = 0.0f;
         if (hipEventElapsedTime(&ms, e->ev[k], e->ev[k + 1]) == hipSuccess) {
@@ -5979,6 +6021,11 @@ int engine_last_kernel_ms(const engine* e, float* ms, int max_kernels)
         ms[i] = e->last_ms[i];
     }
     return k;
+}
+
+int engine_last_apply_waves(const engine* e)
+{
+    return e->last_apply_waves;
 }
 
 

@@ -91,6 +91,7 @@ int engine_set_state(engine* e, const std::uint64_t* plane_busy,
 int engine_reset(engine* e);
 int engine_synchronize(engine* e);
 int engine_last_kernel_ms(const engine* e, float* ms, int max_kernels);
+int engine_last_apply_waves(const engine* e);
 // Host <-> device staging helpers for the host-pointer entry point.
 int engine_run_host(engine* e, const hbf_record32* records, std::size_t n,
                     std::uint64_t* completion, std::uint8_t* status,

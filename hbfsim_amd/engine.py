@@ -250,6 +250,11 @@ class Engine:
         k = self._lib.hbfsim_amd_last_kernel_ms(self._ctx, ms, 8)
         return [float(ms[i]) for i in range(k)]
 
+    def apply_waves(self) -> int:
+        """Waves per SIMD the last run's apply kernel was built for (4: the
+        form for large streams of general steps; results do not depend on it)."""
+        return int(self._lib.hbfsim_amd_last_apply_waves(self._ctx))
+
     def run_coupled(self, thermal: "Thermal", options: dict, records: Any, completion: Any,
                     temperature: Any, age_ps: np.ndarray, stream: Any = None) -> tuple[dict, dict]:
         """Thermal-coupled run (hbfsim_amd_run_coupled): returns the coupled

@@ -387,6 +387,13 @@ int hbfsim_amd_reset(hbfsim_context* context);
  * chain, [2] apply.  Returns the number of kernels written. */
 int hbfsim_amd_last_kernel_ms(const hbfsim_context* context, float* ms,
                               int max_kernels);
+/* Diagnostics, no counterpart in the reference: the waves per SIMD the last
+ * run's apply kernel was built for (4: the form for large streams of general
+ * steps, taken when the engine's previous run of at least 2^24 records had
+ * fewer page-register hits than an eighth of its modeled records; 3: packed
+ * records otherwise; 1: 32-byte records, two page registers or refresh
+ * records), 0 before any run.  Results do not depend on the form. */
+int hbfsim_amd_last_apply_waves(const hbfsim_context* context);
 
 /* One registered range as the registry holds it (SharedRangeRecord,
  * hbf_device.cuh:105-117). */
