@@ -51,17 +51,21 @@ def kernel_bytes(records: str, apply_rereads: bool = False) -> dict:
 
 def profile_kernel_us(summary: str, kernel: str) -> float | None:
     """Average duration (us) of `kernel` in a committed kernel-trace summary
-    under profiles/ (rocprofv3 --kernel-trace --stats, one line per kernel)."""
+    under profiles/ (rocprofv3 --kernel-trace --stats, one line per kernel);
+    of several instantiations, the one launched most often (the timed steps'
+    form: a warm-up run may take another)."""
     import re
     path = ROOT / "profiles" / summary
     if not path.exists():
         return None
+    best = None
     for line in path.read_text().splitlines():
         m = re.match(r"(\S+?(?:<[^>]*>)?)\s+(\d+)\s+([\d.]+)\s", line)
         if m and not line.startswith("#") and (m.group(1) == kernel or
                                                m.group(1).startswith(kernel + "<")):
-            return float(m.group(3))
-    return None
+            if best is None or int(m.group(2)) > best[0]:
+                best = (int(m.group(2)), float(m.group(3)))
+    return None if best is None else best[1]
 
 
 def roofline_from_profile(summary: str, kernel: str, bytes_per_launch: float) -> dict | None:
@@ -444,7 +448,8 @@ def sub_line(engine, profile, ranges, batches, records, args, what: str, mode="f
     its own roofline for the dominant per-record kernel, the same roofline
     recomputed from the committed kernel summary it cites, and the HBM
     traffic of that summary's counter companion."""
-    value, dt, kms, streamed = time_steps(engine, profile, ranges, batches, records, args, mode)
+    value, dt, kms, streamed, apply_waves = time_steps(engine, profile, ranges, batches, records,
+                                                       args, mode)
     names = ["k_summary", "k_carry", "k_apply"]
     kb = kernel_bytes(records, apply_rereads)
     dominant = 0 if kms[0] >= kms[2] else 2
@@ -458,6 +463,7 @@ def sub_line(engine, profile, ranges, batches, records, args, what: str, mode="f
             "frac": achieved / PEAK_HBM_GBPS,
             "kernel_ms": {nm: float(v) for nm, v in zip(names, kms)},
             "apply_bytes_per_access": kb["k_apply"],
+            "apply_waves_per_simd": apply_waves,
             "algorithmic_bytes_per_access": algo,
             "pipeline_frac": value * algo / 1e9 / PEAK_HBM_GBPS}
     if kernels_summary is not None:
@@ -805,11 +811,11 @@ def main() -> None:
             records = "32"
     desc = dict(desc, records=("packed 16-byte records (hbf_record16)" if records == "packed"
                                else "32-byte records (hbf_record32)"))
-    value, dt, avg_ms, accesses = time_steps(engine, profile, ranges, timed, records, args)
+    value, dt, avg_ms, accesses, _ = time_steps(engine, profile, ranges, timed, records, args)
     other = None
     if records == "packed" and not args.no_compare:
         # the same steps from 32-byte records, for comparison (its own roofline)
-        v32, dt32, ms32, _ = time_steps(engine, profile, ranges, batches, "32", args)
+        v32, dt32, ms32, _, _ = time_steps(engine, profile, ranges, batches, "32", args)
         other = {"records": "32-byte records (hbf_record32)", "value": v32,
                  "ms_per_step": dt32 / args.steps * 1e3, "algorithmic_bytes_per_access": 40,
                  "pipeline_frac": v32 * 40 / 1e9 / PEAK_HBM_GBPS,
@@ -914,7 +920,8 @@ def main() -> None:
 def time_steps(engine, profile, ranges, batches, records, args, mode="fast"):
     """Warm-up steps, then exactly `args.steps` timed steps of one engine
     (bracketed by device synchronisation); returns (modeled accesses/s,
-    seconds, average per-kernel ms, records streamed)."""
+    seconds, average per-kernel ms, records streamed, waves per SIMD of the
+    last step's apply kernel)."""
     import torch
     e = engine.Engine(str(profile), mode=mode)
     for base, length, perms in ranges:
@@ -941,9 +948,11 @@ def time_steps(engine, profile, ranges, batches, records, args, mode="fast"):
         kernel_ms += np.array(e.kernel_ms()[:3])
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    # the apply kernel's form in the last timed step (waves per SIMD it was built for)
+    apply_waves = e.apply_waves()
     e.close()
     # the metric counts modeled accesses; the kernels stream every record
-    return modeled / dt, dt, kernel_ms / args.steps, records_seen
+    return modeled / dt, dt, kernel_ms / args.steps, records_seen, apply_waves
 
 
 if __name__ == "__main__":
