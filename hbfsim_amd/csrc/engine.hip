@@ -2355,30 +2355,65 @@ __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, s
 // and the service total.
 constexpr int kMidBlock = 512;
 
+// one entry per wave of the block: the waves' inclusive totals
 union MidShared {
-    PlaneSum p[kMidBlock];
-    ChanSum c[kMidBlock];
-    std::uint64_t s[kMidBlock];
+    PlaneSum p[kMidBlock / kWave];
+    ChanSum c[kMidBlock / kWave];
+    std::uint64_t s[kMidBlock / kWave];
 };
 
-// Inclusive scan of x over the block (Hillis-Steele, earlier elements first).
+// Lane `src`'s value of a scanned type.
+__device__ __forceinline__ std::uint64_t lane_value(std::uint64_t v, int src)
+{
+    return shfl64(v, src);
+}
+
+__device__ __forceinline__ ChanSum lane_value(const ChanSum& v, int src)
+{
+    return ChanSum{shfl64(v.A, src), shfl64(v.B, src)};
+}
+
+__device__ __forceinline__ PlaneSum lane_value(const PlaneSum& v, int src)
+{
+    PlaneSum r;
+    r.fpage1 = shfl64(v.fpage1, src);
+    r.fissue = shfl64(v.fissue, src);
+    r.rA = shfl64(v.rA, src);
+    r.rB = shfl64(v.rB, src);
+    r.lpage1 = shfl64(v.lpage1, src);
+    r.fcls = static_cast<std::uint32_t>(__shfl(static_cast<int>(v.fcls), src));
+    r.pad = 0;
+    return r;
+}
+
+// Inclusive scan of x over the block, earlier elements first: each wave
+// scans its lanes through shuffles (Hillis-Steele), then every thread
+// composes the totals of the waves before its own from LDS; two barriers in
+// all.  `excl` receives the exclusive prefix (identity for thread 0).
 template <typename T, typename F>
-__device__ __forceinline__ T block_scan(T x, T* sh, T identity, F compose)
+__device__ __forceinline__ T block_scan(T x, T* wsh, T identity, F compose, T& excl)
 {
     const int tid = threadIdx.x;
-    sh[tid] = x;
-    __syncthreads();
-    for (int off = 1; off < kMidBlock; off <<= 1) {
-        T y = identity;
-        if (tid >= off) {
-            y = sh[tid - off];
+    const int lane = tid & (kWave - 1);
+    const int w = tid / kWave;
+    for (int off = 1; off < kWave; off <<= 1) {
+        const T y = lane_value(x, lane >= off ? lane - off : lane);
+        if (lane >= off) {
+            x = compose(y, x);
         }
-        __syncthreads();
-        x = compose(y, x);
-        sh[tid] = x;
-        __syncthreads();
     }
-    return x;
+    T before_lane = lane_value(x, lane > 0 ? lane - 1 : 0);
+    if (lane == kWave - 1) {
+        wsh[w] = x;
+    }
+    __syncthreads();
+    T before = identity;
+    for (int k = 0; k < w; ++k) {
+        before = compose(before, wsh[k]);
+    }
+    __syncthreads();  // (wsh may be written again after the return)
+    excl = lane > 0 ? compose(before, before_lane) : before;
+    return compose(before, x);
 }
 
 __device__ __forceinline__ std::uint64_t block_sum(std::uint64_t v, std::uint64_t* sh)
@@ -2425,11 +2460,8 @@ __global__ __launch_bounds__(kMidBlock) void k_carry_mid(
             if (g < ngroups) {
                 own = gpsum[g * a.Rp + r];
             }
-            (void)block_scan(own, sh.p, id, compose);
-            PlaneSum before = id;
-            if (tid > 0) {
-                before = sh.p[tid - 1];
-            }
+            PlaneSum before;
+            (void)block_scan(own, sh.p, id, compose, before);
             std::uint64_t b = busy, t1 = tag1;
             (void)plane_apply(a, before, b, t1);  // the state this group starts from
             std::uint64_t svc = 0;
@@ -2466,11 +2498,8 @@ __global__ __launch_bounds__(kMidBlock) void k_carry_mid(
             if (g < ngroups) {
                 own = gcsum[g * a.Rc + c];
             }
-            const ChanSum inc = block_scan(own, sh.c, id, chan_compose);
-            ChanSum before = id;
-            if (tid > 0) {
-                before = sh.c[tid - 1];
-            }
+            ChanSum before;
+            const ChanSum inc = block_scan(own, sh.c, id, chan_compose, before);
             if (g < ngroups) {
                 gccarry[g * a.Rc + c] = umax64(busy + before.A, before.B);
             }
@@ -2492,9 +2521,10 @@ __global__ __launch_bounds__(kMidBlock) void k_carry_mid(
         for (std::size_t g0 = 0; g0 < ngroups; g0 += kMidBlock) {
             const std::size_t g = g0 + tid;
             const std::uint64_t own = g < ngroups ? gcount[g] : 0ull;
-            const std::uint64_t inc = block_scan(own, sh.s, std::uint64_t{0}, add);
+            std::uint64_t before;
+            const std::uint64_t inc = block_scan(own, sh.s, std::uint64_t{0}, add, before);
             if (g < ngroups) {
-                gseq[g] = seq + inc - own;
+                gseq[g] = seq + before;
             }
             const std::size_t last = (ngroups - g0 < kMidBlock ? ngroups - g0 : kMidBlock) - 1;
             if (static_cast<std::size_t>(tid) == last) {
