@@ -511,7 +511,6 @@ __device__ __forceinline__ void load_record(const hbf_record32* rec, std::size_t
 // with constant indices that wait on nothing in flight (a selection by step
 // index would put the group in scratch memory).
 constexpr int kPipe = 4;
-constexpr std::size_t kGroupSpan = static_cast<std::size_t>(kPipe) * kWave;
 // The summary pass of 32-byte records, whose occupancy its per-plane LDS
 // state limits (not its registers), keeps twice as many steps in flight per
 // wave.

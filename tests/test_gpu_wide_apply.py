@@ -7,7 +7,8 @@ equal the oracle's either way, with linear, grouped and split steps mixed
 into the general ones."""
 from __future__ import annotations
 
-import numpy as np
+import json
+
 import pytest
 
 import parity
@@ -46,6 +47,29 @@ def test_wide_apply_takes_over_on_general_streams():
         g, c = p.run_packed(linear, base_ps=int(g[2]["makespan_ps"]))
         parity.assert_same(g, c, "small linear run")
         assert p.engine.apply_waves() == 3
+        p.check_state()
+    finally:
+        p.close()
+
+
+def test_wide_apply_hybrid_sampling(tmp_path):
+    """Hybrid mode (every modeled record through the reference sampler, rate
+    1%, 1,000 warm-up requests) in both forms of the apply pass: sequence
+    numbers carry across the runs."""
+    prof = json.loads(C0.read_text())
+    prof.update(reference_sample_rate=0.01, reference_warmup_requests=1000)
+    path = tmp_path / "c0-hybrid-wide.json"
+    path.write_text(json.dumps(prof))
+    first = workloads.config0(n=BIG, seed=31)
+    second = workloads.config0(n=BIG, seed=32, write_fraction_per_mille=30)
+    p = parity.Pair(path, first.ranges, mode="hybrid")
+    try:
+        g, c = p.run_packed(first.records)
+        parity.assert_same(g, c, "hybrid, three-wave apply")
+        assert p.engine.apply_waves() == 3 and g[2]["hybrid_sampled"] > 0
+        g, c = p.run_packed(second.records, base_ps=int(g[2]["makespan_ps"]))
+        parity.assert_same(g, c, "hybrid, four-wave apply")
+        assert p.engine.apply_waves() == 4
         p.check_state()
     finally:
         p.close()
