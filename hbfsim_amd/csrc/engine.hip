@@ -3623,12 +3623,23 @@ __global__ __launch_bounds__(256) void k_report(const std::uint64_t* in, std::si
     const std::size_t lo = static_cast<std::size_t>(blockIdx.x) * per;
     const std::size_t hi = lo + per < count ? lo + per : count;
     std::uint64_t acc = 0, carry = 0;
-    for (std::size_t i = lo + stream; i < hi; i += 16) {
-        const std::uint64_t v = f < kIn ? in[i * kIn + f] : 0ull;
-        // a partial's carry word travels with its latency word
-        const std::uint64_t vc = (kIn == kRepWords && f == R_LAT_LO) ? in[i * kIn + kRepCarry]
-                                                                       : 0ull;
-        rep_join(f, acc, carry, f == kRepCarry ? 0ull : v, vc);
+    // kBatch entries per stream are loaded before any is joined (one memory
+    // round trip per batch, not per entry); entries past `hi` read as 0,
+    // which every field's join leaves unchanged
+    constexpr int kBatch = 8;
+    for (std::size_t i0 = lo + stream; i0 < hi; i0 += 16 * kBatch) {
+        std::uint64_t v[kBatch], vc[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const std::size_t i = i0 + 16 * static_cast<std::size_t>(k);
+            v[k] = i < hi && f < kIn ? in[i * kIn + f] : 0ull;
+            // a partial's carry word travels with its latency word
+            vc[k] = i < hi && kIn == kRepWords && f == R_LAT_LO ? in[i * kIn + kRepCarry] : 0ull;
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            rep_join(f, acc, carry, f == kRepCarry ? 0ull : v[k], vc[k]);
+        }
     }
     acc_sh[stream][f] = acc;
     if (f == R_LAT_LO) {
