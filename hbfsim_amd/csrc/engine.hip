@@ -519,8 +519,11 @@ constexpr int kSumPipe = 8;
 // flight each.  Measured against three waves with eight steps: general
 // streams +8% per step (k_summary 4.15 -> 3.57 ms at 2^28 records) and the
 // paged-KV step +15%, the TinyLlama step 2% slower; the LDS-bound variant
-// (kDeep) keeps 2 * kSumPipe at two waves.
+// (kDeep) keeps 2 * kSumPipe at two waves.  A run whose tiles all fit in one
+// round of three-wave slots (kFewTiles) leaves SIMDs without a fourth wave
+// anyway: it keeps three waves with kSumPipe steps in flight (kFew).
 constexpr int kPackedSumPipe = 3;
+constexpr std::size_t kFewTiles = 3 * 4 * 256;  // waves per SIMD x SIMDs per CU x CUs
 // Linear-step detection on streams that show none: after kLinGiveUp steps in
 // a row fail it, a wave probes only every kLinProbe-th step until one
 // passes (every step is exact on the general path too; random streams stop
@@ -1858,8 +1861,8 @@ __host__ __device__ __forceinline__ std::size_t summary_match_offset(const KArgs
 // class), the (max,+) map of the records after it, and the last page; per
 // channel the map of all its records.  Pages are stored as page + 1 in 32
 // bits (capacity / page_bytes < 2^32 is checked on the host).
-template <bool kRefresh, bool kHits, bool kPacked = false, bool kDeep = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (kDeep ? 2 : 4) : 1))) void k_summary(KArgs a, const void* rec, std::size_t n,
+template <bool kRefresh, bool kHits, bool kPacked = false, bool kDeep = false, bool kFew = false>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (kDeep ? 2 : (kFew ? 3 : 4)) : 1))) void k_summary(KArgs a, const void* rec, std::size_t n,
                                                 std::uint64_t base_ps, PlaneSum* psum,
                                                 MaskWord* tmask, ChanSum* csum,
                                                 std::uint64_t* tile_count,
@@ -1907,7 +1910,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
     // (kDeep: packed records where LDS already holds the pass at two waves
     // per SIMD, whose registers then allow 2 * kSumPipe steps in flight)
     constexpr int kDepth =
-        kHits ? kPipe : (kDeep ? 2 * kSumPipe : (kPacked ? kPackedSumPipe : kSumPipe));
+        kHits ? kPipe
+              : (kDeep ? 2 * kSumPipe : (kPacked && !kFew ? kPackedSumPipe : kSumPipe));
     constexpr std::size_t kSpan = static_cast<std::size_t>(kDepth) * kWave;
     using Pipe = std::conditional_t<kPacked, PackedPipeT<kDepth>, RecordPipeT<kDepth>>;
     Pipe pipe;
@@ -5800,6 +5804,11 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         (void)allow_lds(k_summary<false, false, true, true>, lds_a);
         hipLaunchKernelGGL((k_summary<false, false, true, true>), grid, dim3(kWave), lds_a, stream,
                            a, d_rec, n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
+                           hits, desc);
+    } else if (packed && ntiles <= kFewTiles) {
+        (void)allow_lds(k_summary<false, false, true, false, true>, lds_a);
+        hipLaunchKernelGGL((k_summary<false, false, true, false, true>), grid, dim3(kWave), lds_a,
+                           stream, a, d_rec, n, base_ps, sc.psum, sc.tmask, sc.csum, sc.tcount,
                            hits, desc);
     } else if (packed) {
         (void)allow_lds(k_summary<false, false, true>, lds_a);

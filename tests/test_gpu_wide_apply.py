@@ -31,7 +31,9 @@ def test_wide_apply_takes_over_on_general_streams():
                          contiguous_stream(6, 400, side), split_stream(7, 2000, side),
                          second.records[BIG // 2:])
     linear = chain_clocks(linear_stream(8, 4000, side), contiguous_stream(9, 400, side))
-    p = parity.Pair(C0, first.ranges + side)
+    # tiles of 4,096 records: the large runs have more tiles than one round of
+    # three-wave slots, so their summary pass is the four-wave form too
+    p = parity.Pair(C0, first.ranges + side, tile_records=4096)
     try:
         # no earlier run: the three-wave form
         g, c = p.run_packed(first.records)
