@@ -5669,6 +5669,7 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         if (refresh_records) {
             return HBFSIM_UNSUPPORTED;
         }
+        e->last_apply_waves = 0;  // (the empirical model's own kernels, no apply pass)
         return run_empirical(e, static_cast<const hbf_record32*>(d_rec), n, d_comp, d_status,
                              base_ps, stream, out, in_order);
     }

@@ -392,7 +392,8 @@ int hbfsim_amd_last_kernel_ms(const hbfsim_context* context, float* ms,
  * steps, taken when the engine's previous run of at least 2^24 records had
  * fewer page-register hits than an eighth of its modeled records; 3: packed
  * records otherwise; 1: 32-byte records, two page registers or refresh
- * records), 0 before any run.  Results do not depend on the form. */
+ * records), 0 before any run and after an empirical-model run (no apply
+ * pass).  Results do not depend on the form. */
 int hbfsim_amd_last_apply_waves(const hbfsim_context* context);
 
 /* One registered range as the registry holds it (SharedRangeRecord,
