@@ -1204,20 +1204,23 @@ __device__ __forceinline__ bool detect_step(const KArgs& a, const std::uint64_t*
 // (record r of the group at address a0 + r * bytes0), each step with its own
 // issue time, all inside the cached range.  Checked at once on the group's
 // registers: lane l looks at word pair l & 1 of records 64 j + 32 h + (l >> 1)
-// for every step j and half h.
+// for every step j and half h.  The step values live one step per lane
+// (lane j < D: step j), not in D wave-uniform registers each: per-step
+// scalar arrays would hold about 3 D scalar registers across the group's
+// checks, more than the wave has beside the kernel's own, and the overflow
+// goes to VGPR lanes one write and one read at a time.
 template <int D>
 struct GroupLin {
-    std::uint32_t page1[D];
-    std::uint64_t issue[D];
+    std::uint32_t page1;  // lane j < D: step j's media page + 1
+    std::uint64_t issue;  // lane j < D: step j's issue time
     std::uint32_t bytes;
 };
 
 template <bool kRefresh, int D>
 __device__ __forceinline__ bool group_tail(const KArgs& a, const std::uint64_t* fence,
                                            RangeCache& rcu, std::uint64_t base_ps,
-                                           const uint4& xu, std::uint32_t op0,
-                                           const std::uint32_t (&ilo)[D],
-                                           const std::uint32_t (&ihi)[D], GroupLin<D>& gl);
+                                           const uint4& xu, std::uint32_t op0, std::uint32_t vlo,
+                                           std::uint32_t vhi, int lane, GroupLin<D>& gl);
 
 template <bool kRefresh, int D>
 __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t* fence,
@@ -1235,12 +1238,14 @@ __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t
     const std::uint64_t half = 32ull * b0;  // bytes between the two halves of a step
     const std::uint64_t mine = a0 + static_cast<std::uint64_t>(lane >> 1) * b0;
     const bool odd = (lane & 1) != 0;
-    std::uint32_t ilo[D], ihi[D];
+    std::uint32_t vlo = 0, vhi = 0;  // lane j < D: step j's issue time
     bool ok = true;
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-        ilo[j] = rl32(pipe.ca[j].x, 1);
-        ihi[j] = rl32(pipe.ca[j].y, 1);
+        const std::uint32_t ilo = rl32(pipe.ca[j].x, 1);
+        const std::uint32_t ihi = rl32(pipe.ca[j].y, 1);
+        vlo = lane == j ? ilo : vlo;
+        vhi = lane == j ? ihi : vhi;
         const uint4& A = pipe.ca[j];
         const uint4& B = pipe.cb[j];
         const std::uint64_t ea = mine + static_cast<std::uint64_t>(2 * j) * half;
@@ -1249,14 +1254,14 @@ __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t
         const std::uint64_t wb = B.x | (static_cast<std::uint64_t>(B.y) << 32);
         const bool ev = wa == ea && A.z == xu.z && A.w == 0 && wb == eb && B.z == xu.z &&
                         B.w == 0;
-        const bool od = A.x == ilo[j] && A.y == ihi[j] && A.z == op0 && B.x == ilo[j] &&
-                        B.y == ihi[j] && B.z == op0;
+        const bool od = A.x == ilo && A.y == ihi && A.z == op0 && B.x == ilo && B.y == ihi &&
+                        B.z == op0;
         ok = ok && (odd ? od : ev);
     }
     if (__ballot(!ok) != 0) {
         return false;
     }
-    return group_tail<kRefresh, D>(a, fence, rcu, base_ps, xu, op0, ilo, ihi, gl);
+    return group_tail<kRefresh, D>(a, fence, rcu, base_ps, xu, op0, vlo, vhi, lane, gl);
 }
 
 // A packed group: lane l checks its own record of every step.
@@ -1275,38 +1280,40 @@ __device__ __forceinline__ bool group_linear(const KArgs& a, const std::uint64_t
     const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
     const std::uint64_t b0 = xu.z;
     const std::uint64_t mine = a0 + static_cast<std::uint64_t>(lane) * b0;
-    std::uint32_t ilo[D], ihi[D];
+    std::uint32_t vlo = 0, vhi = 0;  // lane j < D: step j's issue time
     bool ok = true;
 #pragma unroll
     for (int j = 0; j < D; ++j) {
         const uint4& R = pipe.c[j];
         const std::uint32_t w = rfl32(R.w);  // record 0 of step j: issue high, operation
-        ilo[j] = rfl32(R.z);
-        ihi[j] = w & 0xffffffu;
+        const std::uint32_t ilo = rfl32(R.z);
+        vlo = lane == j ? ilo : vlo;
+        vhi = lane == j ? (w & 0xffffffu) : vhi;
         const std::uint64_t e = mine + static_cast<std::uint64_t>(j) * 64ull * b0;
         ok = ok && (w >> 24) == 0 && R.x == static_cast<std::uint32_t>(e) &&
-             (R.y & 0xffffu) == (e >> 32) && (R.y >> 16) == b0 && R.z == ilo[j] && R.w == w;
+             (R.y & 0xffffu) == (e >> 32) && (R.y >> 16) == b0 && R.z == ilo && R.w == w;
     }
     if (__ballot(!ok) != 0) {
         return false;
     }
-    return group_tail<kRefresh, D>(a, fence, rcu, base_ps, xu, 0u, ilo, ihi, gl);
+    return group_tail<kRefresh, D>(a, fence, rcu, base_ps, xu, 0u, vlo, vhi, lane, gl);
 }
 
 // The range and page checks of a group whose records already continue one
-// another from record 0 (xu: its address and bytes; op0, ilo, ihi: its
-// operation and every step's issue time), and the group's step values.
+// another from record 0 (xu: its address and bytes; op0: its operation;
+// vlo, vhi: lane j < D holds step j's issue time), and the group's step
+// values, lane j checking and holding step j.
 template <bool kRefresh, int D>
 __device__ __forceinline__ bool group_tail(const KArgs& a, const std::uint64_t* fence,
                                            RangeCache& rcu, std::uint64_t base_ps,
-                                           const uint4& xu, std::uint32_t op0,
-                                           const std::uint32_t (&ilo)[D],
-                                           const std::uint32_t (&ihi)[D], GroupLin<D>& gl)
+                                           const uint4& xu, std::uint32_t op0, std::uint32_t vlo,
+                                           std::uint32_t vhi, int lane, GroupLin<D>& gl)
 {
+    static_assert(D <= kWave, "one lane per step");
     const std::uint64_t a0 = xu.x | (static_cast<std::uint64_t>(xu.y) << 32);
     const std::uint64_t b0 = xu.z;
     if (!(a0 >= rcu.base && a0 < rcu.end)) {
-        const uint4 yu = make_uint4(ilo[0], ihi[0], op0, 0);
+        const uint4 yu = make_uint4(rl32(vlo, 0), rl32(vhi, 0), op0, 0);
         const Dec d = decode<kRefresh, true>(a, fence, rcu, xu, yu, base_ps);
         if (d.cls != kClsModeled) {
             return false;
@@ -1319,17 +1326,15 @@ __device__ __forceinline__ bool group_tail(const KArgs& a, const std::uint64_t* 
         return false;
     }
     const std::uint64_t page_mask = (1ull << a.page_shift) - 1;
-    const std::uint64_t off0 = a0 - rcu.base;
-#pragma unroll
-    for (int j = 0; j < D; ++j) {
-        const std::uint64_t off = off0 + static_cast<std::uint64_t>(j) * step;
-        if ((off >> a.page_shift) != ((off + step - 1) >> a.page_shift) ||
-            (off & ~page_mask) > ~0ull - rcu.file_offset) {
-            return false;
-        }
-        gl.page1[j] = static_cast<std::uint32_t>(((rcu.file_offset + off) >> a.page_shift) + 1);
-        gl.issue[j] = base_ps + (ilo[j] | (static_cast<std::uint64_t>(ihi[j]) << 32));
+    const std::uint64_t off = a0 - rcu.base + static_cast<std::uint64_t>(lane) * step;
+    // a step crossing a page, or a page whose file offset overflows
+    const bool bad = lane < D && ((off >> a.page_shift) != ((off + step - 1) >> a.page_shift) ||
+                                  (off & ~page_mask) > ~0ull - rcu.file_offset);
+    if (__ballot(bad) != 0) {
+        return false;
     }
+    gl.page1 = static_cast<std::uint32_t>(((rcu.file_offset + off) >> a.page_shift) + 1);
+    gl.issue = base_ps + (vlo | (static_cast<std::uint64_t>(vhi) << 32));
     gl.bytes = xu.z;
     return true;
 }
@@ -1415,14 +1420,13 @@ struct LinBatchT {
             first = s;
         }
         const int j = static_cast<int>(threadIdx.x) - n;
+        // batch lane n + j takes step j from the group's lane j (every lane
+        // takes part in the shuffles)
+        const int src = j >= 0 && j < D ? j : 0;
+        const std::uint32_t p1 =
+            static_cast<std::uint32_t>(__shfl(static_cast<int>(gl.page1), src));
+        const std::uint64_t i0 = shfl64(gl.issue, src);
         if (j >= 0 && j < D) {
-            std::uint32_t p1 = gl.page1[0];
-            std::uint64_t i0 = gl.issue[0];
-#pragma unroll
-            for (int k = 1; k < D; ++k) {
-                p1 = j == k ? gl.page1[k] : p1;
-                i0 = j == k ? gl.issue[k] : i0;
-            }
             page1 = p1;
             issue = i0;
             bytes = gl.bytes;
