@@ -766,13 +766,9 @@ def main() -> None:
         if args.config == "general":
             line = bench_general(engine, args)
         else:
-            from hbfsim_amd import workloads
-            shape = workloads.QWEN3_30B_A3B
-            sel = workloads.moe_selection(shape, 2)
-            batches = [workloads.gpu_segment_records(workloads.moe_segments(shape, sel[k]),
-                                                     shape.lines_per_expert, shape.line,
-                                                     shape.gap_ps, shape.issuers)
-                       for k in range(2)]
+            # the same decode steps as the default run's hybrid sub-line
+            nb = args.batches or max(1, min(args.steps + args.warmup, 12))
+            batches = build_workload("c2", args.steps, nb)[2]
             line = bench_hybrid(engine, batches, args)
         out = {"metric": "modeled HBF accesses/sec on 1 MI355X", "value": line["value"],
                "unit": "accesses/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
