@@ -127,6 +127,11 @@ struct KArgs {
     // 64-bit lane mask per plane and per channel) instead of one ballot per
     // key bit; set where the tables cost the passes no occupancy
     std::uint32_t match_lds;
+    // the per-record passes' general steps look a media page's plane and
+    // channel up in a per-wave LDS table of Rp entries (power-of-two axes:
+    // both depend on the page modulo Rp only) instead of striping it; set
+    // where the table costs the passes no occupancy
+    std::uint32_t stripe_lds;
     // warp grouping: per record, how many records back its group's request
     // was made (0: its own request); null when the run does not group
     const std::uint8_t* lead;
@@ -735,6 +740,20 @@ __device__ __forceinline__ void stripe(const KArgs& a, std::uint64_t page, Dec& 
     d.plane = ((c[0] * a.W + c[1]) * a.D + c[2]) * a.P + c[3];
 }
 
+// A wave's stripe table: entry r = plane | channel << 20 of media page r,
+// r < Rp.  With power-of-two axes every axis digit is a bit field of the
+// page's low log2(Rp) bits, so page p stripes as p mod Rp does.
+__device__ __forceinline__ void fill_stripe_table(const KArgs& a, std::uint32_t* stab, int lane)
+{
+    for (std::uint32_t r = static_cast<std::uint32_t>(lane); r < a.Rp; r += kWave) {
+        Dec d;
+        d.plane = 0;
+        d.chan = 0;
+        stripe(a, r, d);
+        stab[r] = d.plane | (d.chan << 20);
+    }
+}
+
 // The operation a decoded record carries (hybrid sampler key).
 __device__ __forceinline__ std::uint32_t dec_op(std::uint32_t bits)
 {
@@ -744,10 +763,12 @@ __device__ __forceinline__ std::uint32_t dec_op(std::uint32_t bits)
 // Classification in the resolver's order (hbf_device.cu:1081-1165) followed
 // by striping of the media page.  Refresh records are recognised only in
 // the kRefresh instantiation (streams the thermal-coupled run merged them
-// into); the other streams keep the branch out of the hot loop.
+// into); the other streams keep the branch out of the hot loop.  `stab`:
+// the wave's stripe table (fill_stripe_table), when the run keeps one.
 template <bool kRefresh, bool kUniform = false>
 __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence, RangeCache& rc,
-                                      const uint4& x, const uint4& y, std::uint64_t base_ps)
+                                      const uint4& x, const uint4& y, std::uint64_t base_ps,
+                                      const std::uint32_t* stab = nullptr)
 {
     const std::uint64_t addr = x.x | (static_cast<std::uint64_t>(x.y) << 32);
     const std::uint64_t bytes = x.z | (static_cast<std::uint64_t>(x.w) << 32);
@@ -831,7 +852,12 @@ __device__ __forceinline__ Dec decode(const KArgs& a, const std::uint64_t* fence
     d.xbytes = a.transfer_page ? page_bytes : bytes;
     // (striping written out here rather than through stripe(): the helper
     // costs the summary kernel a quarter of its speed)
-    if (!a.flat) {
+    if (!a.flat && stab != nullptr) {
+        // plane | channel << 20 of the page modulo Rp (a power of two)
+        const std::uint32_t e = stab[static_cast<std::uint32_t>(page) & (a.Rp - 1)];
+        d.chan = e >> 20;
+        d.plane = e & 0xfffffu;
+    } else if (!a.flat) {
         std::uint32_t c[4];
         if (a.pow2) {
 #pragma unroll
@@ -1861,6 +1887,13 @@ __host__ __device__ __forceinline__ std::size_t summary_match_offset(const KArgs
     return 8ull * (a.r_nfence + 3ull * rp + 2ull * a.Rc) + 8ull * rp + ((rp + 7ull) & ~7ull);
 }
 
+// Byte offset of the summary pass's stripe table (Rp words), after the
+// lane-matching tables when the run keeps them.
+__host__ __device__ __forceinline__ std::size_t summary_stripe_offset(const KArgs& a)
+{
+    return summary_match_offset(a) + (a.match_lds ? 8ull * (a.Rp + a.Rc) : 0ull);
+}
+
 // Summary pass.  Per plane the tile keeps: the first record (page, issue,
 // class), the (max,+) map of the records after it, and the last page; per
 // channel the map of all its records.  Pages are stored as page + 1 in 32
@@ -1938,6 +1971,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
         for (std::uint32_t r = lane; r < a.Rp + a.Rc; r += kWave) {
             mt_p[r] = 0;
         }
+    }
+    std::uint32_t* stab = nullptr;
+    if (a.stripe_lds) {
+        stab = reinterpret_cast<std::uint32_t*>(reinterpret_cast<unsigned char*>(sm) +
+                                                summary_stripe_offset(a));
+        fill_stripe_table(a, stab, lane);
     }
     __syncthreads();
     RangeCache rc = empty_cache();
@@ -2032,7 +2071,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPacked ? (k
             }
             uint4 x, y;
             step_records(st, lane, x, y);
-            Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
+            Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps, stab) : invalid_dec();
             {
                 const std::uint64_t prev = shfl64(d.issue, lane == 0 ? 0 : lane - 1);
                 const bool back = valid && d.issue < (lane == 0 ? last_issue : prev);
@@ -3059,6 +3098,13 @@ __host__ __device__ __forceinline__ std::size_t apply_match_offset(const KArgs& 
     return apply_desc_offset(a) + 16ull * staged_steps(a);
 }
 
+// Byte offset of the apply pass's stripe table (Rp words), after the
+// lane-matching tables when the run keeps them.
+__host__ __device__ __forceinline__ std::size_t apply_stripe_offset(const KArgs& a)
+{
+    return apply_match_offset(a) + (a.match_lds ? 8ull * (a.Rp + a.Rc) : 0ull);
+}
+
 // A tile's plane carry-ins are packed like its summaries: word w of the
 // mask covers planes [64 w, 64 w + 64), so lane l reads bit l of each word.
 // Eight words' carries are in flight before any is written.
@@ -3248,6 +3294,12 @@ __device__ __forceinline__ void apply_tile(
             mt_p[r] = 0;
         }
     }
+    std::uint32_t* stab = nullptr;
+    if (a.stripe_lds) {
+        stab = reinterpret_cast<std::uint32_t*>(reinterpret_cast<unsigned char*>(sm) +
+                                                apply_stripe_offset(a));
+        fill_stripe_table(a, stab, lane);
+    }
     if (stage) {
 #pragma unroll
         for (int k = 0; k < kDescPerLane; ++k) {
@@ -3374,7 +3426,8 @@ __device__ __forceinline__ void apply_tile(
                 }
                 uint4 x, y;
                 step_records(sr, lane, x, y);
-                Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps) : invalid_dec();
+                Dec d = valid ? decode<kRefresh>(a, fence, rc, x, y, base_ps, stab)
+                              : invalid_dec();
                 if (!kPacked && a.lead != nullptr && valid && a.lead[i] != 0) {
                     d.cls = kClsFollower;  // timed by k_follow from its group's request
                 }
@@ -4921,12 +4974,12 @@ __global__ __launch_bounds__(64) void k_k2_hits(KArgs a, const hbf_record32* rec
 
 std::size_t lds_summary(const KArgs& a)
 {
-    return summary_match_offset(a) + (a.match_lds ? 8ull * (a.Rp + a.Rc) : 0ull);
+    return summary_stripe_offset(a) + (a.stripe_lds ? 4ull * a.Rp : 0ull);
 }
 
 std::size_t lds_apply(const KArgs& a)
 {
-    return apply_match_offset(a) + (a.match_lds ? 8ull * (a.Rp + a.Rc) : 0ull);
+    return apply_stripe_offset(a) + (a.stripe_lds ? 4ull * a.Rp : 0ull);
 }
 
 // The lane-matching tables go where they cost neither per-record pass any
@@ -4962,10 +5015,20 @@ void choose_match(KArgs& a)
         return w < kMaxWaves ? w : kMaxWaves;
     };
     a.match_lds = 0;
+    a.stripe_lds = 0;
     const std::size_t s0 = lds_summary(a), p0 = lds_apply(a);
     a.match_lds = 1;
     if (waves(lds_summary(a)) < waves(s0) || waves(lds_apply(a)) < waves(p0)) {
         a.match_lds = 0;
+    }
+    // the stripe table likewise, for power-of-two axes (plane ids below
+    // 2^20 and channel ids below 2^12 pack into one word)
+    if (!a.flat && a.pow2 && a.Rp <= (1u << 20) && a.Rc <= (1u << 12)) {
+        const std::size_t s1 = lds_summary(a), p1 = lds_apply(a);
+        a.stripe_lds = 1;
+        if (waves(lds_summary(a)) < waves(s1) || waves(lds_apply(a)) < waves(p1)) {
+            a.stripe_lds = 0;
+        }
     }
 }
 
