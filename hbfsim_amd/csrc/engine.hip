@@ -5700,11 +5700,11 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         (reinterpret_cast<std::uintptr_t>(d_comp) & 7u) != 0) {
         return HBFSIM_INVALID_ARGUMENT;
     }
-    // packed records take the main pipeline only: one page register, the
-    // HBF model (no refresh records: they need flags); hybrid sampling needs
-    // the linear steps' range ids beside their descriptors, for which the
-    // run without allocation has no room
-    if (packed && (e->cfg.model != HBFSIM_AMD_MODEL_HBF || e->cfg.slots != 1 ||
+    // packed records take the main pipeline only: at most one page register,
+    // the HBF model (no refresh records: they need flags); hybrid sampling
+    // needs the linear steps' range ids beside their descriptors, for which
+    // the run without allocation has no room
+    if (packed && (e->cfg.model != HBFSIM_AMD_MODEL_HBF || e->cfg.slots > 1 ||
                    (e->cfg.hybrid != 0 && ext_scratch != nullptr))) {
         return HBFSIM_UNSUPPORTED;
     }

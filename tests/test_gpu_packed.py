@@ -130,6 +130,23 @@ def test_packed_hybrid(tmp_path, profile, options):
         p.close()
 
 
+@pytest.mark.parametrize("profile", [C0, C2], ids=["c0", "c2"])
+def test_packed_without_page_register(profile):
+    """page_buffers 0: no step is batched (the linear-step path needs the
+    page register), every record takes the general path, none hits."""
+    ranges = ranges_for()
+    rec = chain_clocks(linear_stream(7, 600, ranges), contiguous_stream(8, 100, ranges))
+    p = parity.Pair(profile, ranges, page_buffers=0)
+    try:
+        (_, _, grep), _ = check_packed(p, rec, f"packed {profile.name}, no page register")
+        assert grep["page_hits"] == 0 and grep["modeled"] > 0
+        check_packed(p, rec, f"packed {profile.name}, no page register, second run",
+                     base_ps=int(grep["makespan_ps"]))
+        p.check_state()
+    finally:
+        p.close()
+
+
 @pytest.mark.parametrize("options", [dict(page_buffers=2)])
 def test_packed_refuses_other_pipelines(options):
     import torch
