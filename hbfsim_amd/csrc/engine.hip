@@ -12,7 +12,8 @@
 //              its page-buffer hit resolved later, from the carry.
 //   k_carry_*  a three-level scan over the tile summaries gives the exact
 //              busy-until / tag state at the start of every tile (and the
-//              final state, kept for the next run).
+//              final state, kept for the next run); one launch for runs of
+//              at most 4,096 tiles, three for larger ones.
 //   k_apply    re-reads each tile, replays it from its carry-in state and
 //              writes completion times, status bytes and accounting.
 //
@@ -2327,6 +2328,75 @@ __device__ __forceinline__ void chunk_slots(const MaskWord* tmask, std::uint32_t
     }
 }
 
+// Level-1 work of thread (g, r): the composition of group g's tile
+// summaries of plane r, of channel c, and its tiles' modeled-record count.
+// Loads go out kChunk at a time ahead of the (serial) composition, so a
+// thread waits once per chunk rather than once per tile.
+__device__ __forceinline__ PlaneSum plane_fold(const KArgs& a, const PlaneSum* psum,
+                                               const MaskWord* tmask, std::size_t ntiles,
+                                               std::size_t g, std::uint32_t r)
+{
+    const std::size_t t0 = g * kGroup;
+    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
+    const std::uint32_t words = mask_words(a);
+    PlaneSum acc{};  // the identity: no first record
+#pragma unroll
+    for (std::uint32_t c = 0; c < kGroup / kChunk; ++c) {
+        const std::size_t t = t0 + static_cast<std::size_t>(c) * kChunk;
+        if (t >= t1) {
+            break;
+        }
+        int at[kChunk];
+        PlaneSum buf[kChunk];
+        chunk_slots(tmask, words, t, t1, r, at);
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            if (at[k] >= 0) {
+                buf[k] = psum[(t + k) * a.Rp + at[k]];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            if (at[k] >= 0) {
+                acc = plane_compose(a, acc, buf[k]);
+            }
+        }
+    }
+    return acc;
+}
+
+__device__ __forceinline__ ChanSum chan_fold(const KArgs& a, const ChanSum* csum,
+                                             std::size_t ntiles, std::size_t g, std::uint32_t c)
+{
+    const std::size_t t0 = g * kGroup;
+    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
+    ChanSum acc{0, 0};  // the identity
+    for (std::size_t t = t0; t < t1; t += kChunk) {
+        ChanSum buf[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            buf[k] = t + k < t1 ? csum[(t + k) * a.Rc + c] : ChanSum{0, 0};
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            acc = chan_compose(acc, buf[k]);
+        }
+    }
+    return acc;
+}
+
+__device__ __forceinline__ std::uint64_t count_fold(const std::uint64_t* tile_count,
+                                                    std::size_t ntiles, std::size_t g)
+{
+    const std::size_t t0 = g * kGroup;
+    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
+    std::uint64_t sum = 0;
+    for (std::size_t t = t0; t < t1; ++t) {
+        sum += tile_count[t];
+    }
+    return sum;
+}
+
 __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, std::size_t ngroups,
                                                   const PlaneSum* psum,
                                                   const MaskWord* tmask, const ChanSum* csum,
@@ -2341,57 +2411,13 @@ __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, s
     }
     const std::size_t g = id / rt;
     const std::uint32_t r = static_cast<std::uint32_t>(id - g * rt);
-    const std::size_t t0 = g * kGroup;
-    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
-    // Loads go out kChunk at a time ahead of the (serial) composition, so a
-    // thread waits once per chunk rather than once per tile.
     if (r < a.Rp) {
-        const std::uint32_t words = mask_words(a);
-        PlaneSum acc{};  // the identity: no first record
-#pragma unroll
-        for (std::uint32_t c = 0; c < kGroup / kChunk; ++c) {
-            const std::size_t t = t0 + static_cast<std::size_t>(c) * kChunk;
-            if (t >= t1) {
-                break;
-            }
-            int at[kChunk];
-            PlaneSum buf[kChunk];
-            chunk_slots(tmask, words, t, t1, r, at);
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if (at[k] >= 0) {
-                    buf[k] = psum[(t + k) * a.Rp + at[k]];
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if (at[k] >= 0) {
-                    acc = plane_compose(a, acc, buf[k]);
-                }
-            }
-        }
-        gpsum[g * a.Rp + r] = acc;
+        gpsum[g * a.Rp + r] = plane_fold(a, psum, tmask, ntiles, g, r);
     } else if (r < a.Rp + a.Rc) {
         const std::uint32_t c = r - a.Rp;
-        ChanSum acc{0, 0};  // the identity
-        for (std::size_t t = t0; t < t1; t += kChunk) {
-            ChanSum buf[kChunk];
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                buf[k] = t + k < t1 ? csum[(t + k) * a.Rc + c] : ChanSum{0, 0};
-            }
-#pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                acc = chan_compose(acc, buf[k]);
-            }
-        }
-        gcsum[g * a.Rc + c] = acc;
+        gcsum[g * a.Rc + c] = chan_fold(a, csum, ntiles, g, c);
     } else {
-        std::uint64_t sum = 0;
-        for (std::size_t t = t0; t < t1; ++t) {
-            sum += tile_count[t];
-        }
-        gcount[g] = sum;
+        gcount[g] = count_fold(tile_count, ntiles, g);
     }
 }
 
@@ -2400,6 +2426,8 @@ __global__ __launch_bounds__(256) void k_carry_up(KArgs a, std::size_t ntiles, s
 // each prefix to the engine state: every group's carry-in, the final state,
 // and the service total.
 constexpr int kMidBlock = 512;
+// runs of at most this many tiles take the one-launch chain (k_carry_one)
+constexpr std::size_t kOneCarryTiles = static_cast<std::size_t>(kMidBlock) * kChunk;
 
 // one entry per wave of the block: the waves' inclusive totals
 union MidShared {
@@ -2586,8 +2614,80 @@ __global__ __launch_bounds__(kMidBlock) void k_carry_mid(
     }
 }
 
-// Level 3: thread (g, r) walks group g's tiles from the group carry-in and
-// writes every tile's carry-in.
+// Level-3 work of thread (g, r): walks group g's tiles from the group's
+// carry-in and writes every tile's carry-in.
+__device__ __forceinline__ void plane_walk(const KArgs& a, const PlaneSum* psum,
+                                           const MaskWord* tmask, std::size_t ntiles,
+                                           std::size_t g, std::uint32_t r, PlaneCarry c0,
+                                           PlaneCarry* pcarry)
+{
+    const std::size_t t0 = g * kGroup;
+    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
+    const std::uint32_t words = mask_words(a);
+    std::uint64_t busy = c0.busy, tag1 = c0.tag1;
+#pragma unroll
+    for (std::uint32_t c = 0; c < kGroup / kChunk; ++c) {
+        const std::size_t t = t0 + static_cast<std::size_t>(c) * kChunk;
+        if (t >= t1) {
+            break;
+        }
+        int at[kChunk];
+        PlaneSum buf[kChunk];
+        chunk_slots(tmask, words, t, t1, r, at);
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            if (at[k] >= 0) {
+                buf[k] = psum[(t + k) * a.Rp + at[k]];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            // an untouched tile neither reads nor changes this plane
+            if (at[k] >= 0) {
+                PlaneCarry c;
+                c.busy = busy;
+                c.tag1 = tag1;
+                pcarry[(t + k) * a.Rp + at[k]] = c;  // packed like the summaries
+                (void)plane_apply(a, buf[k], busy, tag1);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void chan_walk(const KArgs& a, const ChanSum* csum, std::size_t ntiles,
+                                          std::size_t g, std::uint32_t c, std::uint64_t busy,
+                                          std::uint64_t* ccarry)
+{
+    const std::size_t t0 = g * kGroup;
+    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
+    for (std::size_t t = t0; t < t1; t += kChunk) {
+        ChanSum buf[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            buf[k] = t + k < t1 ? csum[(t + k) * a.Rc + c] : ChanSum{0, 0};
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            if (t + k < t1) {
+                ccarry[(t + k) * a.Rc + c] = busy;
+                busy = umax64(busy + buf[k].A, buf[k].B);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ void seq_walk(const std::uint64_t* tile_count, std::size_t ntiles,
+                                         std::size_t g, std::uint64_t s, std::uint64_t* tile_seq)
+{
+    const std::size_t t0 = g * kGroup;
+    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
+    for (std::size_t t = t0; t < t1; ++t) {
+        tile_seq[t] = s;
+        s += tile_count[t];
+    }
+}
+
+// Level 3: thread (g, r) walks group g's tiles from the group carry-in.
 __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
                                                     std::size_t ngroups, const PlaneSum* psum,
                                                     const MaskWord* tmask,
@@ -2605,61 +2705,141 @@ __global__ __launch_bounds__(256) void k_carry_down(KArgs a, std::size_t ntiles,
     }
     const std::size_t g = id / rt;
     const std::uint32_t r = static_cast<std::uint32_t>(id - g * rt);
-    const std::size_t t0 = g * kGroup;
-    const std::size_t t1 = t0 + kGroup < ntiles ? t0 + kGroup : ntiles;
     if (r < a.Rp) {
-        const PlaneCarry c0 = gpcarry[g * a.Rp + r];
-        const std::uint32_t words = mask_words(a);
-        std::uint64_t busy = c0.busy, tag1 = c0.tag1;
+        plane_walk(a, psum, tmask, ntiles, g, r, gpcarry[g * a.Rp + r], pcarry);
+    } else if (r < a.Rp + a.Rc) {
+        const std::uint32_t c = r - a.Rp;
+        chan_walk(a, csum, ntiles, g, c, gccarry[g * a.Rc + c], ccarry);
+    } else {
+        seq_walk(tile_count, ntiles, g, gseq[g], tile_seq);
+    }
+}
+
+// The whole chain in one launch, for runs of at most kMidBlock * kChunk
+// tiles.  Thread g of block r owns tiles [g span, g span + span) (span <=
+// kChunk): it loads their summaries of resource r in one round, folds them,
+// the block scans the folds from the engine state, and the thread walks its
+// tiles from its carry-in with the summaries still in registers.  Two
+// rounds of dependent loads in all, where the three kernels above take
+// eight; the compositions, and so the results, are the same.
+__global__ __launch_bounds__(kMidBlock) void k_carry_one(
+    KArgs a, std::size_t ntiles, std::uint32_t span, const PlaneSum* psum,
+    const MaskWord* tmask, const ChanSum* csum, const std::uint64_t* tile_count,
+    PlaneCarry* pcarry, std::uint64_t* ccarry, std::uint64_t* tile_seq,
+    std::uint64_t* st_pbusy, std::uint64_t* st_ptag, std::uint64_t* st_cbusy,
+    std::uint64_t* st_seq, std::uint64_t* ptotal, std::uint64_t* ctotal)
+{
+    __shared__ MidShared sh;
+    __shared__ std::uint64_t red[kMidBlock / kWave];
+    const std::uint32_t r = blockIdx.x;
+    const std::size_t t0 = static_cast<std::size_t>(threadIdx.x) * span;
+    const std::size_t t1 = t0 + span < ntiles ? t0 + span : ntiles;
+    const bool in = t0 < ntiles;
+    const bool last = in && t1 == ntiles;
+    const bool commit = a.disorder == nullptr || *a.disorder == 0u;
+    if (r < a.Rp) {
+        std::uint64_t busy = st_pbusy[r];
+        std::uint64_t tag1 = st_ptag[static_cast<std::size_t>(r) * 2];
+        const auto compose = [&](const PlaneSum& s1, const PlaneSum& s2) {
+            return plane_compose(a, s1, s2);
+        };
+        int at[kChunk];
+        PlaneSum buf[kChunk];
+        chunk_slots(tmask, mask_words(a), t0, in ? t1 : t0, r, at);
 #pragma unroll
-        for (std::uint32_t c = 0; c < kGroup / kChunk; ++c) {
-            const std::size_t t = t0 + static_cast<std::size_t>(c) * kChunk;
-            if (t >= t1) {
-                break;
+        for (int k = 0; k < kChunk; ++k) {
+            if (at[k] >= 0) {
+                buf[k] = psum[(t0 + k) * a.Rp + at[k]];
             }
-            int at[kChunk];
-            PlaneSum buf[kChunk];
-            chunk_slots(tmask, words, t, t1, r, at);
+        }
+        PlaneSum own{};
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if (at[k] >= 0) {
-                    buf[k] = psum[(t + k) * a.Rp + at[k]];
-                }
+        for (int k = 0; k < kChunk; ++k) {
+            if (at[k] >= 0) {
+                own = compose(own, buf[k]);
             }
+        }
+        PlaneSum before;
+        (void)block_scan(own, sh.p, PlaneSum{}, compose, before);
+        (void)plane_apply(a, before, busy, tag1);  // the state this thread's tiles start from
+        std::uint64_t svc = 0;
+        {
+            std::uint64_t b = busy, t = tag1;
+            svc = plane_apply(a, own, b, t);
+        }
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                // an untouched tile neither reads nor changes this plane
-                if (at[k] >= 0) {
-                    PlaneCarry c;
-                    c.busy = busy;
-                    c.tag1 = tag1;
-                    pcarry[(t + k) * a.Rp + at[k]] = c;  // packed like the summaries
-                    (void)plane_apply(a, buf[k], busy, tag1);
-                }
+        for (int k = 0; k < kChunk; ++k) {
+            // an untouched tile neither reads nor changes this plane
+            if (at[k] >= 0) {
+                pcarry[(t0 + k) * a.Rp + at[k]] = PlaneCarry{busy, tag1};
+                (void)plane_apply(a, buf[k], busy, tag1);
             }
+        }
+        const std::uint64_t total = block_sum(svc, red);
+        if (last && commit) {
+            st_pbusy[r] = busy;
+            st_ptag[static_cast<std::size_t>(r) * 2] = tag1;
+        }
+        if (threadIdx.x == 0 && commit) {
+            ptotal[r] += total;
         }
     } else if (r < a.Rp + a.Rc) {
         const std::uint32_t c = r - a.Rp;
-        std::uint64_t busy = gccarry[g * a.Rc + c];
-        for (std::size_t t = t0; t < t1; t += kChunk) {
-            ChanSum buf[kChunk];
+        std::uint64_t busy = st_cbusy[c];
+        ChanSum buf[kChunk];
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                buf[k] = t + k < t1 ? csum[(t + k) * a.Rc + c] : ChanSum{0, 0};
-            }
+        for (int k = 0; k < kChunk; ++k) {
+            buf[k] = t0 + k < t1 ? csum[(t0 + k) * a.Rc + c] : ChanSum{0, 0};
+        }
+        ChanSum own{0, 0};
 #pragma unroll
-            for (int k = 0; k < kChunk; ++k) {
-                if (t + k < t1) {
-                    ccarry[(t + k) * a.Rc + c] = busy;
-                    busy = umax64(busy + buf[k].A, buf[k].B);
-                }
+        for (int k = 0; k < kChunk; ++k) {
+            own = chan_compose(own, buf[k]);
+        }
+        ChanSum before;
+        const ChanSum inc = block_scan(own, sh.c, ChanSum{0, 0}, chan_compose, before);
+        const std::uint64_t fin = umax64(busy + inc.A, inc.B);
+        busy = umax64(busy + before.A, before.B);
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            if (t0 + k < t1) {
+                ccarry[(t0 + k) * a.Rc + c] = busy;
+                busy = umax64(busy + buf[k].A, buf[k].B);
             }
         }
-    } else {
-        std::uint64_t s = gseq[g];
-        for (std::size_t t = t0; t < t1; ++t) {
-            tile_seq[t] = s;
-            s += tile_count[t];
+        const std::uint64_t total = block_sum(own.A, red);
+        if (last && commit) {
+            st_cbusy[c] = fin;
+        }
+        if (threadIdx.x == 0 && commit) {
+            ctotal[c] += total;
+        }
+    } else if (r == a.Rp + a.Rc) {
+        const std::uint64_t seq = *st_seq;
+        std::uint64_t cnt[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            cnt[k] = t0 + k < t1 ? tile_count[t0 + k] : 0ull;
+        }
+        std::uint64_t own = 0;
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            own += cnt[k];
+        }
+        std::uint64_t before;
+        const std::uint64_t inc = block_scan(
+            own, sh.s, std::uint64_t{0}, [](std::uint64_t x, std::uint64_t y) { return x + y; },
+            before);
+        std::uint64_t q = seq + before;
+#pragma unroll
+        for (int k = 0; k < kChunk; ++k) {
+            if (t0 + k < t1) {
+                tile_seq[t0 + k] = q;
+                q += cnt[k];
+            }
+        }
+        if (last && commit) {
+            *st_seq = seq + inc;
         }
     }
 }
@@ -5894,17 +6074,25 @@ int engine_run_any(engine* e, const void* d_rec, bool packed, std::size_t n,
         const std::size_t ngroups = (ntiles + kGroup - 1) / kGroup;
         const std::size_t rt = static_cast<std::size_t>(a.Rp) + a.Rc + 1;
         const unsigned wide = static_cast<unsigned>((ngroups * rt + 255) / 256);
-        hipLaunchKernelGGL(k_carry_up, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
-                           sc.psum, sc.tmask, sc.csum, sc.tcount, sc.gpsum,
-                           sc.gcsum, sc.gcount);
-        hipLaunchKernelGGL(k_carry_mid, dim3(a.Rp + a.Rc + 1), dim3(kMidBlock), 0, stream, a,
-                           ngroups,
-                           sc.gpsum, sc.gcsum, sc.gcount, sc.gpcarry, sc.gccarry,
-                           sc.gseq, e->d_pbusy, e->d_ptag, e->d_cbusy, e->d_seq, e->d_ptot,
-                           e->d_ctot);
-        hipLaunchKernelGGL(k_carry_down, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
-                           sc.psum, sc.tmask, sc.csum, sc.tcount, sc.gpcarry,
-                           sc.gccarry, sc.gseq, sc.pcarry, sc.ccarry, sc.tseq);
+        if (ntiles <= kOneCarryTiles) {
+            const auto span = static_cast<std::uint32_t>((ntiles + kMidBlock - 1) / kMidBlock);
+            hipLaunchKernelGGL(k_carry_one, dim3(static_cast<unsigned>(rt)), dim3(kMidBlock), 0,
+                               stream, a, ntiles, span, sc.psum, sc.tmask, sc.csum,
+                               sc.tcount, sc.pcarry, sc.ccarry, sc.tseq, e->d_pbusy, e->d_ptag,
+                               e->d_cbusy, e->d_seq, e->d_ptot, e->d_ctot);
+        } else {
+            hipLaunchKernelGGL(k_carry_up, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
+                               sc.psum, sc.tmask, sc.csum, sc.tcount, sc.gpsum,
+                               sc.gcsum, sc.gcount);
+            hipLaunchKernelGGL(k_carry_mid, dim3(a.Rp + a.Rc + 1), dim3(kMidBlock), 0, stream, a,
+                               ngroups,
+                               sc.gpsum, sc.gcsum, sc.gcount, sc.gpcarry, sc.gccarry,
+                               sc.gseq, e->d_pbusy, e->d_ptag, e->d_cbusy, e->d_seq, e->d_ptot,
+                               e->d_ctot);
+            hipLaunchKernelGGL(k_carry_down, dim3(wide), dim3(256), 0, stream, a, ntiles, ngroups,
+                               sc.psum, sc.tmask, sc.csum, sc.tcount, sc.gpcarry,
+                               sc.gccarry, sc.gseq, sc.pcarry, sc.ccarry, sc.tseq);
+        }
     }
     (void)hipEventRecord(e->ev[2], stream);
     const bool staged = desc != nullptr && staged_steps(a) != 0;
