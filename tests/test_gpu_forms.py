@@ -5,7 +5,9 @@ three-wave slots (at most 3,072 tiles: three waves, eight steps), and the
 four-wave form (three steps) for the rest; general steps look their plane and
 channel up in an LDS stripe table where it costs no occupancy.  The forms
 differ in speed only: runs on either side of the 3,072-tile boundary, and on
-both geometries, must equal the oracle bit for bit."""
+both geometries, must equal the oracle bit for bit.  So must runs on either
+side of the carry chain's 4,096-tile boundary (one launch up to it, three
+above)."""
 from __future__ import annotations
 
 import pytest
@@ -61,6 +63,29 @@ def test_summary_lds_bound_form_with_general_steps():
     try:
         g, c = p.run_packed(rec)
         parity.assert_same(g, c, "config 2 geometry, mixed stream")
+        p.check_state()
+    finally:
+        p.close()
+
+
+ONE_CARRY = 4096  # tiles up to which the carry chain is one launch
+
+
+@pytest.mark.parametrize("profile", [C0, C2], ids=["c0", "c2"])
+@pytest.mark.parametrize("tiles", [ONE_CARRY, ONE_CARRY + 1],
+                         ids=["one-launch carry", "three-launch carry"])
+def test_carry_forms_at_the_tile_boundary(profile, tiles):
+    side = ranges_for()
+    ranges = [(workloads.RANGE_BASE, 1 << 30, 3)] + side
+    rec = mixed(tiles * 64, 60 + tiles % 2, side)
+    assert len(rec) == tiles * 64
+    p = parity.Pair(profile, ranges, tile_records=64)
+    try:
+        base = 0
+        for k in range(2):  # the second run starts from the first one's state
+            g, c = p.run_packed(rec, base_ps=base)
+            parity.assert_same(g, c, f"{profile.name}, {tiles} tiles, run {k}")
+            base = int(g[2]["makespan_ps"])
         p.check_state()
     finally:
         p.close()
