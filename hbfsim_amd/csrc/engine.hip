@@ -5213,10 +5213,17 @@ void choose_match(KArgs& a)
 }
 
 // Records per tile when the configuration leaves it open: the largest power
-// of two up to 16384 that still gives every CU eight tiles, at least 256.
+// of two up to 16384 that gives every CU sixteen tiles, down to 1024 records;
+// below that, the largest that gives every CU eight tiles, at least 256.
+// (Mid-sized runs of 2^22 to 2^25 records take twice the tiles they would at
+// eight per CU: more waves to cover the per-record passes' latency, at the
+// price of a carry chain of twice the tiles.)
 std::uint32_t auto_tile(std::size_t n)
 {
     std::uint32_t t = 16384;
+    while (t > 1024 && (n + t - 1) / t < 4096) {
+        t >>= 1;
+    }
     while (t > 256 && (n + t - 1) / t < 2048) {
         t >>= 1;
     }
