@@ -469,6 +469,10 @@ def sub_line(engine, profile, ranges, batches, records, args, what: str, mode="f
     if kernels_summary is not None:
         roof["from_profile"] = roofline_from_profile(kernels_summary, names[dominant],
                                                      kb[names[dominant]] * per_launch)
+        if kms[dominant] < 0.1:
+            roof["timing_note"] = ("a kernel of tens of microseconds: the HIP-event interval "
+                                   "around it holds its dispatch too (2.5-5 us more than the "
+                                   "kernel trace's duration on config 0)")
     if traffic_summary is not None:
         traffic, src = committed_traffic(traffic_summary, names[dominant], int(per_launch))
         roof["traffic"], roof["traffic_source"] = traffic, src
